@@ -1,0 +1,144 @@
+/*
+ * nncpu_hip.h — the C-ABI of libnncpu_hip.so, the MI355X (gfx950) quantized
+ * matmul that sits behind nncpu's matmul dispatch.
+ *
+ * The reference (ZacWalk/nncpu, Rust) dispatches every weight matmul through
+ * two functions that read a `Tensor`'s dtype and call its CPU kernels:
+ *
+ *   model_gemv  crates/nncpu/src/model/mod.rs:417-444      (one vector)
+ *   gemv_batch  crates/nncpu/src/model/forward.rs:15-58    (n_tok vectors, one weight pass)
+ *
+ * and greedy decoding reads the lm_head through model_argmax
+ * (model/forward.rs:989-1011). This header replaces those three for the
+ * Q8_0 and Q4 ("Q4S") split layouts (crates/nncpu/src/runtime.rs:52-63,
+ * 136-164). Weights are uploaded once after load (model/load.rs:1266-1287)
+ * and freed when the model drops (model/mod.rs:342-348).
+ *
+ * Plain C types only. Every function returns NNH_OK or an NNH_E_* code;
+ * nnh_last_error() gives the calling thread's last message. All entry points
+ * are thread-safe. Host-buffer calls are synchronous: y is ready on return,
+ * as the reference's kernels are.
+ */
+#ifndef NNCPU_HIP_H
+#define NNCPU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The Rust wrapper maps NNH_E_INVALID to a panic, as the
+ * reference panics on violated kernel preconditions (kernels/mod.rs:12-14,
+ * 412-415); NNH_E_OOM to ErrorKind::OutOfMemory (error.rs:8-23); and
+ * NNH_E_DEVICE to an Io-like error. */
+enum {
+    NNH_OK = 0,
+    NNH_E_INVALID = 1,
+    NNH_E_OOM = 2,
+    NNH_E_DEVICE = 3,
+    NNH_E_STATE = 4
+};
+
+/* Weight formats: nncpu's DType::Q8_0 and DType::Q4S (runtime.rs:52-63). */
+enum {
+    NNH_Q8_0 = 1,
+    NNH_Q4S = 2
+};
+
+/* Activation modes of a matmul call.
+ *   NNH_ACT_F32: f32 activations, as the reference. Every output is
+ *     bit-identical to nncpu's CPU kernels (kernels/scalar.rs:626-742,
+ *     kernels/avx2.rs:1256-1521), and a batched call gives each vector the
+ *     bits of a single-vector call.
+ *   NNH_ACT_I8: each activation vector is quantized on the device with
+ *     nncpu's own Q8_0 encoder (kernels/quant.rs:31-60) to int8 blocks of 32
+ *     with a BF16 scale; the kernels form the exact int32 block dot products
+ *     and scale them in f64. The result is the f32 rounding of the exact
+ *     product of the dequantized weights and activations. */
+enum {
+    NNH_ACT_F32 = 0,
+    NNH_ACT_I8 = 1
+};
+
+typedef struct nnh_weight nnh_weight;
+
+/* Select and initialise `device` for this process. Idempotent; a second call
+ * with another device fails with NNH_E_STATE. */
+int nnh_init(int device);
+
+/* The calling thread's last error message ("" when none). */
+const char* nnh_last_error(void);
+
+/* Upload a matrix of `rows` x `cols` (cols % 32 == 0), one row per output,
+ * from the split layout the reference's Tensor::q8()/q4() views
+ * (runtime.rs:136-164). The host copy is not retained.
+ *   nnh_upload_q8_0: qs[rows*cols], scales[rows*cols/32] (BF16 bits).
+ *   nnh_upload_q4:   qs[rows*cols/2] (byte i of a block: element i low
+ *                    nibble, element i+16 high), scales and biases
+ *                    [rows*cols/32] (BF16 bits).
+ *   nnh_upload:      one buffer as Tensor.data points at it. */
+int nnh_upload_q8_0(const int8_t* qs, const uint16_t* scales, size_t rows, size_t cols, nnh_weight** out);
+int nnh_upload_q4(const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, size_t rows, size_t cols,
+                  nnh_weight** out);
+int nnh_upload(int dtype, const void* data, size_t rows, size_t cols, nnh_weight** out);
+
+/* Release a weight (NULL is a no-op). */
+void nnh_free(nnh_weight* w);
+
+/* Shape and format of an uploaded weight. */
+int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols);
+
+/* model_gemv (model/mod.rs:417-444): y[0..rows) = W x[0..cols).
+ * Host buffers; synchronous. */
+int nnh_model_gemv(const nnh_weight* w, const float* x, float* y, int act);
+
+/* gemv_batch (model/forward.rs:15-58) and kernels::gemv_*_batch
+ * (kernels/mod.rs:858-902): n_tok vectors x_stride floats apart into n_tok
+ * outputs y_stride floats apart (y_stride >= rows when n_tok > 1). The Q4
+ * block sums of x are formed on the device. Host buffers; synchronous. */
+int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok,
+                   int act);
+
+/* model_argmax (model/forward.rs:989-1011) for a Q8_0/Q4 lm_head: the row of
+ * the first largest logit of W x (ties to the lower row; NaN never wins, and
+ * a NaN in row 0 keeps row 0). Host x; synchronous. */
+int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int act);
+
+/* Device-resident form of nnh_gemv_batch: x and y are device pointers, the
+ * call is asynchronous on `stream` (a hipStream_t; NULL = the null stream).
+ * Uses a library-owned scratch buffer for the Q4 block sums / quantized
+ * activations: calls on different streams must not overlap. */
+int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
+                       size_t n_tok, int act, void* stream);
+
+/* ---- int8 activation blocks (device memory, caller-owned) ----
+ * An activation buffer holds n_tok vectors of `cols` values quantized with
+ * nncpu's Q8_0 encoder, laid out as:
+ *   int8_t   q[n_tok][cols]          the quants
+ *   uint16_t s[n_tok][cols/32]       the BF16 block scales
+ *   float    sx[n_tok][cols/32][2]   {bf16(s) as f32, s * sum(q of block)}
+ * at the offsets nnh_act_layout() reports. */
+int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes);
+
+/* Quantize n_tok f32 vectors (device, x_stride apart) into `act`. */
+int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream);
+
+/* y (device, y_stride apart) = W x for activations already in `act`: the
+ * int8 path without the quantization step. */
+int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream);
+
+/* Diagnostics: the exact int32 block dot products P[n][r][b] =
+ * sum_k q_w[r, 32b+k] * q_x[n, 32b+k] (device output, rows*cols/32 per
+ * vector), as the int8 path forms them. */
+int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32_t* P, void* stream);
+
+/* Block until all work the library queued on `stream` is done. */
+int nnh_sync(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNCPU_HIP_H */

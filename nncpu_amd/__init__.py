@@ -1,0 +1,174 @@
+"""nncpu_amd: nncpu's quantized matmul on MI355X (gfx950), behind nncpu's own dispatch.
+
+The host-side mirror of the reference's matmul dispatch
+(crates/nncpu/src/model/mod.rs:417-444 ``model_gemv``,
+crates/nncpu/src/model/forward.rs:15-58 ``gemv_batch``,
+crates/nncpu/src/model/forward.rs:989-1011 ``model_argmax``), calling the C-ABI
+of ``lib/libnncpu_hip.so`` (``include/nncpu_hip.h``). Same names and argument
+meaning as the reference; a violated precondition raises ``InvalidArgument``
+where the reference panics (kernels/mod.rs:12-14). Every call runs on the GPU;
+there is no CPU fallback, and importing fails if the library is not built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import (NNH_ACT_F32, NNH_ACT_I8, NNH_Q4S, NNH_Q8_0, DeviceOutOfMemory, InvalidArgument, NnhError,
+                   build, check, declared_functions, lib)
+
+Q8_0 = NNH_Q8_0
+Q4S = NNH_Q4S
+ACT_F32 = NNH_ACT_F32
+ACT_I8 = NNH_ACT_I8
+
+__all__ = [
+    "Q8_0", "Q4S", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
+    "gemv_batch_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
+    "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
+]
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def init(device: int = 0) -> None:
+    check(lib().nnh_init(device))
+
+
+class Weight:
+    """One uploaded Q8_0 / Q4 matrix: the device side of a reference ``Tensor``
+    (runtime.rs:69-75) whose ``dtype`` is ``DType::Q8_0`` or ``DType::Q4S``."""
+
+    def __init__(self, handle: C.c_void_p, dtype: int, rows: int, cols: int):
+        self._h = handle
+        self.dtype, self._rows, self._cols = dtype, rows, cols
+
+    @classmethod
+    def from_split(cls, dtype: int, data: np.ndarray, rows: int, cols: int) -> "Weight":
+        """Upload from one buffer in the split layout Tensor.data points at."""
+        data = np.ascontiguousarray(data).view(np.uint8)
+        n = rows * cols
+        need = (n + n // 16) if dtype == Q8_0 else (n // 2 + n // 8)
+        if cols % 32 == 0 and data.size < need:
+            raise InvalidArgument(1, "split buffer too short")
+        h = C.c_void_p()
+        check(lib().nnh_upload(dtype, _ptr(data), rows, cols, C.byref(h)))
+        return cls(h, dtype, rows, cols)
+
+    @classmethod
+    def q8_0(cls, qs: np.ndarray, scales: np.ndarray, rows: int, cols: int) -> "Weight":
+        qs = np.ascontiguousarray(qs).view(np.int8)
+        scales = np.ascontiguousarray(scales).view(np.uint16)
+        if cols % 32 == 0 and (qs.size < rows * cols or scales.size < rows * cols // 32):
+            raise InvalidArgument(1, "q8_0 parts too short")
+        h = C.c_void_p()
+        check(lib().nnh_upload_q8_0(_ptr(qs), _ptr(scales), rows, cols, C.byref(h)))
+        return cls(h, Q8_0, rows, cols)
+
+    @classmethod
+    def q4(cls, qs: np.ndarray, scales: np.ndarray, biases: np.ndarray, rows: int, cols: int) -> "Weight":
+        qs = np.ascontiguousarray(qs).view(np.uint8)
+        scales = np.ascontiguousarray(scales).view(np.uint16)
+        biases = np.ascontiguousarray(biases).view(np.uint16)
+        nb = rows * cols // 32
+        if cols % 32 == 0 and (qs.size < rows * cols // 2 or scales.size < nb or biases.size < nb):
+            raise InvalidArgument(1, "q4 parts too short")
+        h = C.c_void_p()
+        check(lib().nnh_upload_q4(_ptr(qs), _ptr(scales), _ptr(biases), rows, cols, C.byref(h)))
+        return cls(h, Q4S, rows, cols)
+
+    def rows(self) -> int:
+        """Rows: the output length of a gemv over this matrix (runtime.rs:103-107)."""
+        return self._rows
+
+    def cols(self) -> int:
+        """Columns: the input length of a gemv (runtime.rs:97-101)."""
+        return self._cols
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise InvalidArgument(1, "weight was freed")
+        return self._h
+
+    def free(self) -> None:
+        if self._h is not None:
+            lib().nnh_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def model_gemv(w: Weight, x: np.ndarray, y: np.ndarray | None = None, act: int = ACT_F32) -> np.ndarray:
+    """y[..rows] = W x[..cols] for one vector (model/mod.rs:417-444)."""
+    x = np.ascontiguousarray(x, np.float32)
+    if x.size < w.cols():
+        raise InvalidArgument(1, "x shorter than cols")
+    out = np.empty(w.rows(), np.float32) if y is None else y
+    if out.dtype != np.float32 or not out.flags.c_contiguous or out.size < w.rows():
+        raise InvalidArgument(1, "y must be a contiguous f32 array of at least rows values")
+    check(lib().nnh_model_gemv(w.handle, _ptr(x), _ptr(out), act))
+    return out
+
+
+def gemv_batch(t: Weight, x: np.ndarray, x_stride: int, y: np.ndarray, y_stride: int, n_tok: int,
+               act: int = ACT_F32) -> None:
+    """``n_tok`` vectors of x (``x_stride`` apart) against one pass over the
+    weights, into ``n_tok`` outputs of y (``y_stride`` apart), in place
+    (model/forward.rs:15-58). The Q4 block sums are formed on the device, so
+    the reference's ``xsum`` scratch argument has no counterpart here."""
+    if n_tok == 0:
+        return
+    x = np.ascontiguousarray(x, np.float32)
+    if x.size < (n_tok - 1) * x_stride + t.cols():
+        raise InvalidArgument(1, "x too short for n_tok vectors at x_stride")
+    if y.dtype != np.float32 or not y.flags.c_contiguous or y.size < (n_tok - 1) * y_stride + t.rows():
+        raise InvalidArgument(1, "y must be a contiguous f32 array covering n_tok vectors at y_stride")
+    check(lib().nnh_gemv_batch(t.handle, _ptr(x), x_stride, _ptr(y), y_stride, n_tok, act))
+
+
+def model_argmax(w: Weight, x: np.ndarray, act: int = ACT_F32) -> int:
+    """Row of the first largest logit of W x (model/forward.rs:989-1011)."""
+    x = np.ascontiguousarray(x, np.float32)
+    if x.size < w.cols():
+        raise InvalidArgument(1, "x shorter than cols")
+    out = C.c_size_t(0)
+    check(lib().nnh_model_argmax(w.handle, _ptr(x), C.byref(out), act))
+    return int(out.value)
+
+
+# ---- device-resident entry points (device pointers as ints) -----------------------
+
+def gemv_batch_dev(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,
+                   act: int = ACT_F32, stream: int = 0) -> None:
+    check(lib().nnh_gemv_batch_dev(w.handle, x_ptr, x_stride, y_ptr, y_stride, n_tok, act, stream or None))
+
+
+def act_layout(cols: int, n_tok: int) -> tuple[int, int, int]:
+    """(offset of the BF16 scales, offset of the f64 pairs, total bytes)."""
+    a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    check(lib().nnh_act_layout(cols, n_tok, C.byref(a), C.byref(b), C.byref(c)))
+    return a.value, b.value, c.value
+
+
+def quantize_act_dev(x_ptr: int, x_stride: int, cols: int, n_tok: int, act_ptr: int, stream: int = 0) -> None:
+    check(lib().nnh_quantize_act_dev(x_ptr, x_stride, cols, n_tok, act_ptr, stream or None))
+
+
+def gemv_i8_dev(w: Weight, act_ptr: int, n_tok: int, y_ptr: int, y_stride: int, stream: int = 0) -> None:
+    check(lib().nnh_gemv_i8_dev(w.handle, act_ptr, n_tok, y_ptr, y_stride, stream or None))
+
+
+def block_dots_dev(w: Weight, act_ptr: int, n_tok: int, P_ptr: int, stream: int = 0) -> None:
+    check(lib().nnh_block_dots_dev(w.handle, act_ptr, n_tok, P_ptr, stream or None))
+
+
+def sync(stream: int = 0) -> None:
+    check(lib().nnh_sync(stream or None))

@@ -1,0 +1,390 @@
+// The C-ABI of libnncpu_hip.so (include/nncpu_hip.h): weight upload, the
+// model_gemv / gemv_batch / model_argmax dispatch on the uploaded weight's
+// format (crates/nncpu/src/model/mod.rs:417-444, model/forward.rs:15-58,
+// 989-1011), and the device-resident entry points.
+//
+// One process-wide context (device, one non-blocking stream at default
+// priority, a growable device scratch buffer and pinned staging) guarded by
+// a mutex, as the reference's pool serialises dispatch (pool.rs:7-9,253).
+
+#include <mutex>
+#include <string>
+
+#include "common.h"
+#include "nncpu_hip.h"
+
+struct nnh_weight {
+    int dtype;
+    int device;
+    size_t rows, cols, nb, nbp;
+    uint8_t* raw;         // device: nncpu's split layout, as uploaded
+    const uint8_t* qs;    // views into raw
+    const uint16_t* sc;
+    const uint16_t* bi;   // Q4 only
+    uint8_t* fq;          // device: per-lane quant groups for the f32 path
+    uint16_t* fs;         // device: scales padded to nbp per row
+};
+
+namespace {
+
+thread_local std::string t_err;
+std::mutex g_mu;
+int g_device = -1;
+hipStream_t g_stream = nullptr;
+uint8_t* g_scratch = nullptr;
+size_t g_scratch_bytes = 0;
+
+int fail(int code, const std::string& msg) {
+    t_err = msg;
+    return code;
+}
+
+#define NNH_HIP(expr)                                                                              \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return fail(e_ == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,                      \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));                        \
+    } while (0)
+
+constexpr size_t ALIGN = 256;
+inline size_t align_up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
+
+// Caller holds g_mu.
+int init_locked(int device) {
+    if (g_device >= 0) {
+        if (device != g_device) return fail(NNH_E_STATE, "nnh_init: already initialised on another device");
+        NNH_HIP(hipSetDevice(g_device));
+        return NNH_OK;
+    }
+    int count = 0;
+    NNH_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(NNH_E_STATE, "nnh_init: no such device");
+    NNH_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    NNH_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
+        return fail(NNH_E_STATE, std::string("nnh_init: built for gfx950, device is ") + prop.gcnArchName);
+    NNH_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    g_device = device;
+    return NNH_OK;
+}
+
+int ensure_locked() { return init_locked(g_device >= 0 ? g_device : 0); }
+
+// Grow the scratch to `bytes`; caller holds g_mu. The old buffer may still
+// be read by queued work, so the device is drained first.
+int scratch_locked(size_t bytes, uint8_t** out) {
+    if (bytes > g_scratch_bytes) {
+        if (g_scratch) {
+            NNH_HIP(hipDeviceSynchronize());
+            NNH_HIP(hipFree(g_scratch));
+            g_scratch = nullptr;
+            g_scratch_bytes = 0;
+        }
+        size_t want = align_up(bytes + bytes / 4);
+        NNH_HIP(hipMalloc((void**)&g_scratch, want));
+        g_scratch_bytes = want;
+    }
+    *out = g_scratch;
+    return NNH_OK;
+}
+
+struct ActLayout {
+    size_t off_s, off_sx, bytes;
+};
+
+ActLayout act_layout(size_t cols, size_t n_tok) {
+    size_t nb = cols / 32;
+    ActLayout l;
+    l.off_s = align_up(n_tok * cols);
+    l.off_sx = l.off_s + align_up(n_tok * nb * 2);
+    l.bytes = l.off_sx + align_up(n_tok * nb * 16);
+    return l;
+}
+
+int check_weight(const nnh_weight* w) {
+    if (!w) return fail(NNH_E_INVALID, "null weight");
+    if (w->device != g_device) return fail(NNH_E_STATE, "weight belongs to another device");
+    return NNH_OK;
+}
+
+// Queue the matmul for device x / y; `scratch` holds xsum or the act buffer.
+int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok, int act,
+             uint8_t* scratch, hipStream_t st) {
+    const int rows = (int)w->rows, nb = (int)w->nb;
+    if (act == NNH_ACT_F32) {
+        float* xsum = nullptr;
+        if (w->dtype == NNH_Q4S) {
+            xsum = (float*)scratch;
+            nnh::launch_block_sums(x, x_stride, nb, (int)n_tok, xsum, st);
+        }
+        nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
+                             y, y_stride, st);
+    } else {
+        ActLayout l = act_layout(w->cols, n_tok);
+        int8_t* q = (int8_t*)scratch;
+        uint16_t* s = (uint16_t*)(scratch + l.off_s);
+        double* sx = (double*)(scratch + l.off_sx);
+        nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, q, s, sx, st);
+        nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, q, sx, rows, nb, (int)n_tok, y, y_stride, st);
+    }
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+size_t gemv_scratch_bytes(const nnh_weight* w, size_t n_tok, int act) {
+    if (act == NNH_ACT_F32) return w->dtype == NNH_Q4S ? align_up(n_tok * w->nb * 4) : 0;
+    return act_layout(w->cols, n_tok).bytes;
+}
+
+int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_tok, int act) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    if (act != NNH_ACT_F32 && act != NNH_ACT_I8) return fail(NNH_E_INVALID, "unknown activation mode");
+    if (n_tok > 1 && y_stride < w->rows) return fail(NNH_E_INVALID, "gemv batch: y_stride < rows");
+    if (n_tok > (size_t)1 << 20) return fail(NNH_E_INVALID, "gemv batch: too many vectors");
+    (void)x_stride;
+    return NNH_OK;
+}
+
+int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size_t rows, size_t cols,
+                 nnh_weight** out) {
+    if (!out) return fail(NNH_E_INVALID, "nnh_upload: null out");
+    *out = nullptr;
+    if (dtype != NNH_Q8_0 && dtype != NNH_Q4S) return fail(NNH_E_INVALID, "nnh_upload: unknown dtype");
+    if (!qs || !sc || (dtype == NNH_Q4S && !bi)) return fail(NNH_E_INVALID, "nnh_upload: null data");
+    if (rows == 0 || cols == 0) return fail(NNH_E_INVALID, "nnh_upload: empty matrix");
+    if (cols % 32 != 0) return fail(NNH_E_INVALID, "nnh_upload: cols is not a multiple of 32");
+    if (rows >= ((size_t)1 << 31) || cols >= ((size_t)1 << 31) || rows > ((size_t)1 << 62) / cols)
+        return fail(NNH_E_INVALID, "nnh_upload: matrix too large");
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    const size_t n = rows * cols, nb = cols / 32;
+    const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2;
+    const size_t tbytes = (n / 32) * 2;
+    const size_t raw_bytes = qbytes + tbytes * (dtype == NNH_Q8_0 ? 1 : 2);
+    const size_t group = dtype == NNH_Q8_0 ? 8 : 16;
+    const size_t nbp = (nb + group - 1) / group * group;
+
+    nnh_weight* w = new nnh_weight();
+    w->dtype = dtype;
+    w->device = g_device;
+    w->rows = rows;
+    w->cols = cols;
+    w->nb = nb;
+    w->nbp = nbp;
+    auto cleanup = [&](int code) {
+        if (w->raw) (void)hipFree(w->raw);
+        if (w->fq) (void)hipFree(w->fq);
+        if (w->fs) (void)hipFree(w->fs);
+        delete w;
+        return code;
+    };
+    hipError_t e;
+    if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes))) != hipSuccess ||
+        (e = hipMalloc((void**)&w->fq, align_up(qbytes))) != hipSuccess ||
+        (e = hipMalloc((void**)&w->fs, align_up(rows * nbp * 2))) != hipSuccess) {
+        return cleanup(fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
+                            std::string("nnh_upload: ") + hipGetErrorString(e)));
+    }
+    w->qs = w->raw;
+    w->sc = (const uint16_t*)(w->raw + qbytes);
+    w->bi = dtype == NNH_Q4S ? (const uint16_t*)(w->raw + qbytes + tbytes) : nullptr;
+    if ((e = hipMemcpyAsync(w->raw, qs, qbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
+        (e = hipMemcpyAsync(w->raw + qbytes, sc, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
+        (dtype == NNH_Q4S &&
+         (e = hipMemcpyAsync(w->raw + qbytes + tbytes, bi, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess))
+        return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: copy: ") + hipGetErrorString(e)));
+    nnh::launch_relayout_f32(dtype, w->qs, w->sc, w->fq, w->fs, (int)rows, (int)nb, (int)nbp, g_stream);
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
+        return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: relayout: ") + hipGetErrorString(e)));
+    *out = w;
+    return NNH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nnh_init(int device) {
+    std::lock_guard<std::mutex> g(g_mu);
+    return init_locked(device);
+}
+
+const char* nnh_last_error(void) { return t_err.c_str(); }
+
+int nnh_upload_q8_0(const int8_t* qs, const uint16_t* scales, size_t rows, size_t cols, nnh_weight** out) {
+    return upload_parts(NNH_Q8_0, qs, scales, nullptr, rows, cols, out);
+}
+
+int nnh_upload_q4(const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, size_t rows, size_t cols,
+                  nnh_weight** out) {
+    return upload_parts(NNH_Q4S, qs, scales, biases, rows, cols, out);
+}
+
+int nnh_upload(int dtype, const void* data, size_t rows, size_t cols, nnh_weight** out) {
+    if (!data) return fail(NNH_E_INVALID, "nnh_upload: null data");
+    const uint8_t* p = (const uint8_t*)data;
+    size_t n = rows * cols;
+    if (dtype == NNH_Q8_0) return upload_parts(dtype, p, p + n, nullptr, rows, cols, out);
+    if (dtype == NNH_Q4S) return upload_parts(dtype, p, p + n / 2, p + n / 2 + n / 16, rows, cols, out);
+    return fail(NNH_E_INVALID, "nnh_upload: unknown dtype");
+}
+
+void nnh_free(nnh_weight* w) {
+    if (!w) return;
+    std::lock_guard<std::mutex> g(g_mu);
+    (void)hipSetDevice(w->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(w->raw);
+    (void)hipFree(w->fq);
+    (void)hipFree(w->fs);
+    delete w;
+}
+
+int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols) {
+    if (!w) return fail(NNH_E_INVALID, "null weight");
+    if (dtype) *dtype = w->dtype;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    return NNH_OK;
+}
+
+int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok,
+                   int act) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, x_stride, y_stride, n_tok, act))) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!x || !y) return fail(NNH_E_INVALID, "gemv: null x or y");
+    const size_t xs = n_tok > 1 ? x_stride : w->cols;
+    const size_t ys = n_tok > 1 ? y_stride : w->rows;
+    const size_t x_elems = (n_tok - 1) * xs + w->cols;
+    const size_t y_elems = (n_tok - 1) * ys + w->rows;
+    const size_t off_y = align_up(x_elems * 4);
+    const size_t off_s = off_y + align_up(y_elems * 4);
+    uint8_t* s;
+    if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, n_tok, act), &s))) return rc;
+    float* dx = (float*)s;
+    float* dy = (float*)(s + off_y);
+    NNH_HIP(hipMemcpyAsync(dx, x, x_elems * 4, hipMemcpyHostToDevice, g_stream));
+    if ((rc = run_gemv(w, dx, xs, dy, ys, n_tok, act, s + off_s, g_stream))) return rc;
+    // Only each vector's rows: the reference leaves the stride gaps alone.
+    NNH_HIP(hipMemcpy2DAsync(y, ys * 4, dy, ys * 4, w->rows * 4, n_tok, hipMemcpyDeviceToHost, g_stream));
+    NNH_HIP(hipStreamSynchronize(g_stream));
+    return NNH_OK;
+}
+
+int nnh_model_gemv(const nnh_weight* w, const float* x, float* y, int act) {
+    return nnh_gemv_batch(w, x, w ? w->cols : 0, y, w ? w->rows : 0, 1, act);
+}
+
+int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int act) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, 0, 0, 1, act))) return rc;
+    if (!x || !out_row) return fail(NNH_E_INVALID, "argmax: null x or out");
+    if (w->rows >= ((size_t)1 << 32)) return fail(NNH_E_INVALID, "argmax: too many rows");
+    const size_t off_y = align_up(w->cols * 4);
+    const size_t off_p = off_y + align_up(w->rows * 4);
+    const size_t off_o = off_p + align_up(nnh::argmax_partial_words(w->rows) * 8);
+    const size_t off_s = off_o + ALIGN;
+    uint8_t* s;
+    if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, 1, act), &s))) return rc;
+    float* dx = (float*)s;
+    float* dy = (float*)(s + off_y);
+    uint64_t* dout = (uint64_t*)(s + off_o);
+    NNH_HIP(hipMemcpyAsync(dx, x, w->cols * 4, hipMemcpyHostToDevice, g_stream));
+    if ((rc = run_gemv(w, dx, w->cols, dy, w->rows, 1, act, s + off_s, g_stream))) return rc;
+    nnh::launch_argmax(dy, w->rows, (uint64_t*)(s + off_p), dout, g_stream);
+    NNH_HIP(hipGetLastError());
+    uint64_t idx = 0;
+    NNH_HIP(hipMemcpyAsync(&idx, dout, 8, hipMemcpyDeviceToHost, g_stream));
+    NNH_HIP(hipStreamSynchronize(g_stream));
+    *out_row = (size_t)idx;
+    return NNH_OK;
+}
+
+int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
+                       size_t n_tok, int act, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, x_stride, y_stride, n_tok, act))) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!x || !y) return fail(NNH_E_INVALID, "gemv: null x or y");
+    uint8_t* s = nullptr;
+    size_t need = gemv_scratch_bytes(w, n_tok, act);
+    if (need && (rc = scratch_locked(need, &s))) return rc;
+    const size_t xs = n_tok > 1 ? x_stride : w->cols;
+    const size_t ys = n_tok > 1 ? y_stride : w->rows;
+    return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
+}
+
+int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes) {
+    if (cols % 32 != 0) return fail(NNH_E_INVALID, "act layout: cols is not a multiple of 32");
+    ActLayout l = act_layout(cols, n_tok);
+    if (off_s) *off_s = l.off_s;
+    if (off_sx) *off_sx = l.off_sx;
+    if (bytes) *bytes = l.bytes;
+    return NNH_OK;
+}
+
+int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if (cols == 0 || cols % 32 != 0) return fail(NNH_E_INVALID, "quantize: cols is not a positive multiple of 32");
+    if (n_tok == 0) return NNH_OK;
+    if (!x || !act) return fail(NNH_E_INVALID, "quantize: null pointer");
+    if (cols >= ((size_t)1 << 31) || n_tok * (cols / 32) >= ((size_t)1 << 31))
+        return fail(NNH_E_INVALID, "quantize: too large");
+    ActLayout l = act_layout(cols, n_tok);
+    uint8_t* a = (uint8_t*)act;
+    nnh::launch_quantize_act(x, n_tok > 1 ? x_stride : cols, (int)cols, (int)n_tok, (int8_t*)a,
+                             (uint16_t*)(a + l.off_s), (double*)(a + l.off_sx), (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, 0, y_stride, n_tok, NNH_ACT_I8))) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
+    ActLayout l = act_layout(w->cols, n_tok);
+    const uint8_t* a = (const uint8_t*)act;
+    nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, (const int8_t*)a, (const double*)(a + l.off_sx), (int)w->rows,
+                        (int)w->nb, (int)n_tok, y, n_tok > 1 ? y_stride : w->rows, (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32_t* P, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_weight(w))) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!act || !P) return fail(NNH_E_INVALID, "block_dots: null pointer");
+    nnh::launch_block_dots(w->dtype, w->qs, (const int8_t*)act, (int)w->rows, (int)w->nb, (int)n_tok, P,
+                           (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_sync(void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    NNH_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return NNH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,257 @@
+// The int8-activation path: activations quantized on the device with nncpu's
+// own Q8_0 encoder (crates/nncpu/src/kernels/quant.rs:31-60), exact int32
+// block dot products against the weights' integer quants, and the block
+// terms scaled and summed in f64.
+//
+// For a row r and activation vector x' = q_x * s_x (exact in f32), nncpu's
+// gemv computes sum_b s_w[r,b] * sum_k q_w[r,32b+k] * x'[32b+k] (+ for Q4
+// sum_b bias[r,b] * xsum[b], kernels/mod.rs:848-856). With
+// P_b = sum_k q_w * q_x (an exact int32, |P_b| < 2^20) that is
+//     y_r = sum_b s_w s_x P_b  (+ bias s_x sum_k q_x),
+// each term exact in f64 (at most 8+8+20 significant bits). Summing those in
+// f64 and rounding once gives the f32 nearest the exact product of the
+// dequantized operands, to within f64 rounding.
+
+#include "common.h"
+
+namespace nnh {
+namespace {
+
+// ---- activation quantizer: quant.rs:31-60 on the device ----------------------
+
+// Round half to even, then Rust's saturating `as i32` (quant.rs:18-29).
+__device__ __forceinline__ int rint_sat(float v) {
+    float r = __builtin_rintf(v);
+    if (!(r == r)) return 0;
+    if (r >= 2147483648.0f) return 2147483647;
+    if (r <= -2147483648.0f) return (int)0x80000000;
+    return (int)r;
+}
+
+// One 32-lane half-wave per block of 32 values.
+__global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, size_t x_stride, int cols,
+                                                           int n_tok, int8_t* __restrict__ q,
+                                                           uint16_t* __restrict__ s, double* __restrict__ sx) {
+    const int nb = cols >> 5;
+    const int k = threadIdx.x & 31;
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const bool valid = blk < nb * n_tok;
+    const int bb = valid ? blk : 0;
+    const int t = bb / nb, b = bb - t * nb;
+    float v = x[(size_t)t * x_stride + 32 * (size_t)b + k];
+    // amax: the reference skips NaNs (`v.abs() > amax` is false for them);
+    // fmaxf does too, and max is order-free over the rest.
+    float a = fabsf(v);
+    a = (a == a) ? a : 0.0f;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
+    // Times the reciprocal of 127, rounded to BF16 (quant.rs:49-53).
+    uint32_t sbits = f32_to_bf16(__fmul_rn(a, 1.0f / 127.0f));
+    float scale = bf16f(sbits);
+    float inv = scale > 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+    int qi = rint_sat(__fmul_rn(v, inv));
+    qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+    int qsum = qi;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) qsum += __shfl_xor(qsum, m, 32);
+    if (!valid) return;
+    q[(size_t)t * cols + 32 * (size_t)b + k] = (int8_t)qi;
+    if (k == 0) {
+        s[(size_t)t * nb + b] = (uint16_t)sbits;
+        sx[2 * ((size_t)t * nb + b)] = (double)scale;
+        sx[2 * ((size_t)t * nb + b) + 1] = (double)scale * (double)qsum;  // exact: s_x * sum(q_x)
+    }
+}
+
+// ---- exact block dots ----------------------------------------------------------
+
+// Q8_0: 32 signed weight bytes against 32 activation bytes.
+__device__ __forceinline__ int dot_q8(const int4& w0, const int4& w1, const int4& x0, const int4& x1) {
+    int p = 0;
+    p = __builtin_amdgcn_sdot4(w0.x, x0.x, p, false);
+    p = __builtin_amdgcn_sdot4(w0.y, x0.y, p, false);
+    p = __builtin_amdgcn_sdot4(w0.z, x0.z, p, false);
+    p = __builtin_amdgcn_sdot4(w0.w, x0.w, p, false);
+    p = __builtin_amdgcn_sdot4(w1.x, x1.x, p, false);
+    p = __builtin_amdgcn_sdot4(w1.y, x1.y, p, false);
+    p = __builtin_amdgcn_sdot4(w1.z, x1.z, p, false);
+    p = __builtin_amdgcn_sdot4(w1.w, x1.w, p, false);
+    return p;
+}
+
+// Q4: byte i of the 16 holds element i (low nibble) and i+16 (high). The
+// nibbles are 0..15, so as bytes they are valid non-negative int8 lanes.
+__device__ __forceinline__ int dot_q4(const int4& w, const int4& x0, const int4& x1) {
+    const int m = 0x0f0f0f0f;
+    int p = 0;
+    p = __builtin_amdgcn_sdot4(w.x & m, x0.x, p, false);
+    p = __builtin_amdgcn_sdot4(w.y & m, x0.y, p, false);
+    p = __builtin_amdgcn_sdot4(w.z & m, x0.z, p, false);
+    p = __builtin_amdgcn_sdot4(w.w & m, x0.w, p, false);
+    p = __builtin_amdgcn_sdot4((int)((unsigned)w.x >> 4) & m, x1.x, p, false);
+    p = __builtin_amdgcn_sdot4((int)((unsigned)w.y >> 4) & m, x1.y, p, false);
+    p = __builtin_amdgcn_sdot4((int)((unsigned)w.z >> 4) & m, x1.z, p, false);
+    p = __builtin_amdgcn_sdot4((int)((unsigned)w.w >> 4) & m, x1.w, p, false);
+    return p;
+}
+
+// ---- int8 GEMV -----------------------------------------------------------------
+//
+// A workgroup of 256 lanes = 4 waves; each wave is 64/LPR groups of LPR lanes,
+// a group owns R consecutive rows and its lanes take the blocks cyclically
+// (lane l: blocks l, l+LPR, ...), so one wave-wide 128-bit load reads
+// contiguous weight bytes. Per block and row: the int32 dot, then
+// acc += (s_w * s_x) * P (+ bias * s_x * sum q_x) in f64. The group's lanes
+// are summed with an xor tree in f64 and rounded once.
+template <int DT, int M, int R, int LPR>
+__global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ sc,
+                                                      const uint16_t* __restrict__ bi, const int8_t* __restrict__ aq,
+                                                      const double* __restrict__ asx, int rows, int nb,
+                                                      float* __restrict__ y, size_t y_stride) {
+    constexpr int G = 64 / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int grp = threadIdx.x / LPR;  // 0 .. 4*G-1
+    const int row0 = (blockIdx.x * (4 * G) + grp) * R;
+    const size_t cols = (size_t)nb * 32;
+    const size_t qrow_bytes = DT == 1 ? cols : cols / 2;
+
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rr[r] = row0 + r < rows ? row0 + r : rows - 1;
+
+    double acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = 0.0;
+
+    for (int b = lane; b < nb; b += LPR) {
+        int4 x0[M], x1[M];
+        double sxv[M], sxq[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * (size_t)b);
+            x0[m] = xp[0];
+            x1[m] = xp[1];
+            sxv[m] = asx[2 * ((size_t)m * nb + b)];
+            sxq[m] = asx[2 * ((size_t)m * nb + b) + 1];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t rb = (size_t)rr[r] * nb + b;
+            const double sw = (double)bf16f(sc[rb]);
+            int P[M];
+            if (DT == 1) {
+                const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + 32 * (size_t)b);
+                int4 w0 = wp[0], w1 = wp[1];
+#pragma unroll
+                for (int m = 0; m < M; ++m) P[m] = dot_q8(w0, w1, x0[m], x1[m]);
+            } else {
+                int4 w = *(const int4*)(qs + (size_t)rr[r] * qrow_bytes + 16 * (size_t)b);
+#pragma unroll
+                for (int m = 0; m < M; ++m) P[m] = dot_q4(w, x0[m], x1[m]);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(sw * sxv[m], (double)P[m], acc[r][m]);
+            if (DT == 2) {
+                const double bw = (double)bf16f(bi[rb]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sxq[m], acc[r][m]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            double v = acc[r][m];
+#pragma unroll
+            for (int k = LPR / 2; k >= 1; k >>= 1) v += xor_get(v, k);
+            acc[r][m] = v;
+        }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < rows)
+#pragma unroll
+                for (int m = 0; m < M; ++m) y[(size_t)m * y_stride + row0 + r] = (float)acc[r][m];
+    }
+}
+
+// P[t][r][b], one thread per (t, r, b), with the path's dot routines.
+template <int DT>
+__global__ void block_dots_kernel(const uint8_t* __restrict__ qs, const int8_t* __restrict__ aq, int rows, int nb,
+                                  int n_tok, int32_t* __restrict__ P) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t per = (size_t)rows * nb;
+    if (idx >= per * n_tok) return;
+    size_t t = idx / per, rb = idx - t * per;
+    size_t r = rb / nb, b = rb - r * nb;
+    const size_t cols = (size_t)nb * 32;
+    const int4* xp = (const int4*)(aq + t * cols + 32 * b);
+    int4 x0 = xp[0], x1 = xp[1];
+    if (DT == 1) {
+        const int4* wp = (const int4*)(qs + r * cols + 32 * b);
+        P[idx] = dot_q8(wp[0], wp[1], x0, x1);
+    } else {
+        P[idx] = dot_q4(*(const int4*)(qs + r * cols / 2 + 16 * b), x0, x1);
+    }
+}
+
+template <int DT, int M, int R, int LPR>
+void launch_cfg(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const int8_t* aq, const double* asx,
+                int rows, int nb, float* y, size_t ys, hipStream_t st) {
+    constexpr int rows_per_wg = 4 * (64 / LPR) * R;
+    gemv_i8_kernel<DT, M, R, LPR><<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, bi, aq, asx, rows, nb, y, ys);
+}
+
+template <int DT, int M>
+void launch_m(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const int8_t* aq, const double* asx,
+              int rows, int nb, float* y, size_t ys, hipStream_t st) {
+    // Lanes per row: enough blocks per lane to amortise the reduction.
+    if (nb >= 256)
+        launch_cfg<DT, M, 2, 64>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+    else if (nb >= 64)
+        launch_cfg<DT, M, 2, 32>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+    else
+        launch_cfg<DT, M, 2, 16>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+}
+
+}  // namespace
+
+void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
+                         hipStream_t st) {
+    int blocks = (cols / 32) * n_tok;
+    quantize_act_kernel<<<ceil_div(blocks, 8), 256, 0, st>>>(x, x_stride, cols, n_tok, q, s, sx);
+}
+
+void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
+                    const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st) {
+    const size_t cols = (size_t)nb * 32;
+    for (int t0 = 0; t0 < n_tok; t0 += 4) {
+        int m = n_tok - t0 < 4 ? n_tok - t0 : 4;
+        const int8_t* a = aq + (size_t)t0 * cols;
+        const double* s = asx + 2 * (size_t)t0 * nb;
+        float* yt = y + (size_t)t0 * y_stride;
+#define NNH_L(DT, M) launch_m<DT, M>(qs, scales, biases, a, s, rows, nb, yt, y_stride, st)
+        if (dtype == 1) {
+            if (m == 1) NNH_L(1, 1); else if (m == 2) NNH_L(1, 2); else if (m == 3) NNH_L(1, 3); else NNH_L(1, 4);
+        } else {
+            if (m == 1) NNH_L(2, 1); else if (m == 2) NNH_L(2, 2); else if (m == 3) NNH_L(2, 3); else NNH_L(2, 4);
+        }
+#undef NNH_L
+    }
+}
+
+void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
+                       hipStream_t st) {
+    size_t n = (size_t)rows * nb * n_tok;
+    int blocks = (int)((n + 255) / 256);
+    if (dtype == 1)
+        block_dots_kernel<1><<<blocks, 256, 0, st>>>(qs, aq, rows, nb, n_tok, P);
+    else
+        block_dots_kernel<2><<<blocks, 256, 0, st>>>(qs, aq, rows, nb, n_tok, P);
+}
+
+}  // namespace nnh

@@ -1,0 +1,249 @@
+"""ctypes front end of the CPU oracle (oracle.cpp, avx2.cpp).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+bench.py's cpu_baseline leg, never by the product package ``nncpu_amd``.
+
+Array helpers build nncpu's split weight layouts (crates/nncpu/src/runtime.rs:52-63,
+136-164) from f32 matrices with the restated re-encoder (kernels/quant.rs:31-95),
+and run the restated kernels on them.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+Q8_0 = 1
+Q4S = 2
+
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so with its Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _declare(L):
+    vp, sz, f32, i32 = C.c_void_p, C.c_size_t, C.c_float, C.c_int
+    L.or_bf16_to_f32.argtypes, L.or_bf16_to_f32.restype = [C.c_uint16], f32
+    L.or_f32_to_bf16.argtypes, L.or_f32_to_bf16.restype = [f32], C.c_uint16
+    L.or_rint.argtypes, L.or_rint.restype = [f32], C.c_int32
+    L.or_quantize_q8_0.argtypes = [vp, sz, vp, vp]
+    L.or_quantize_q4.argtypes = [vp, sz, vp, vp, vp]
+    L.or_block_sums.argtypes = [vp, sz, vp]
+    L.or_dot_bf16_f32.argtypes, L.or_dot_bf16_f32.restype = [vp, vp, sz], f32
+    L.or_gemv_q8_0_batch.argtypes, L.or_gemv_q8_0_batch.restype = [vp, vp, vp, sz, vp, sz, sz, sz, sz], i32
+    L.or_gemv_q4_batch.argtypes, L.or_gemv_q4_batch.restype = [vp, vp, vp, vp, sz, vp, sz, vp, sz, sz, sz, sz], i32
+    L.or_gemv_batch.argtypes, L.or_gemv_batch.restype = [i32, vp, sz, sz, vp, sz, vp, sz, sz], i32
+    L.or_argmax.argtypes, L.or_argmax.restype = [vp, sz], sz
+    L.or_block_dots.argtypes = [i32, vp, sz, sz, vp, vp]
+    L.or_dequant_act.argtypes = [vp, vp, sz, vp]
+    L.or_gemv_i8_exact.argtypes = [i32, vp, sz, sz, vp, vp, vp]
+    L.or_rng_init.argtypes = [C.POINTER(C.c_uint64), C.c_uint64]
+    L.or_rng_next.argtypes, L.or_rng_next.restype = [C.POINTER(C.c_uint64)], C.c_uint64
+    L.or_rng_uniform.argtypes = [C.POINTER(C.c_uint64), sz, f32, f32, vp]
+    L.or_rng_normals.argtypes = [C.POINTER(C.c_uint64), sz, f32, vp]
+    L.avx_available.restype = i32
+    L.avx_set_threads.argtypes = [i32]
+    L.avx_threads.restype = i32
+    L.avx_gemv_batch.argtypes, L.avx_gemv_batch.restype = [i32, vp, sz, sz, vp, sz, vp, sz, sz], i32
+    L.avx_stream_gbs.argtypes, L.avx_stream_gbs.restype = [sz, i32], C.c_double
+
+
+# ---- scalars ---------------------------------------------------------------------
+
+def bf16_to_f32(v: int) -> float:
+    return lib().or_bf16_to_f32(v)
+
+
+def f32_to_bf16(v: float) -> int:
+    return lib().or_f32_to_bf16(v)
+
+
+def rint(v: float) -> int:
+    return lib().or_rint(v)
+
+
+def bf16_array_to_f32(a: np.ndarray) -> np.ndarray:
+    """Exact BF16 -> F32 (runtime.rs:10-13), vectorised."""
+    return (a.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- deterministic data: kernels/tests.rs:9-50 ----------------------------------
+
+class Rng:
+    """xorshift64* with Box-Muller normals, as the reference's test Rng."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(0)
+        lib().or_rng_init(C.byref(self.state), C.c_uint64(seed & (2**64 - 1)))
+
+    def next_u64(self) -> int:
+        return lib().or_rng_next(C.byref(self.state))
+
+    def vec(self, n: int, lo: float, hi: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        lib().or_rng_uniform(C.byref(self.state), n, lo, hi, _p(out))
+        return out
+
+    def normals(self, n: int, sd: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        lib().or_rng_normals(C.byref(self.state), n, sd, _p(out))
+        return out
+
+
+# ---- re-encoder (quant.rs:31-95) and split layouts ------------------------------
+
+def quantize_q8_0(src: np.ndarray):
+    src = np.ascontiguousarray(src, np.float32).ravel()
+    n = src.size
+    assert n % 32 == 0
+    qs = np.empty(n, np.int8)
+    sc = np.empty(n // 32, np.uint16)
+    lib().or_quantize_q8_0(_p(src), n, _p(qs), _p(sc))
+    return qs, sc
+
+
+def quantize_q4(src: np.ndarray):
+    src = np.ascontiguousarray(src, np.float32).ravel()
+    n = src.size
+    assert n % 32 == 0
+    qs = np.empty(n // 2, np.uint8)
+    sc = np.empty(n // 32, np.uint16)
+    bi = np.empty(n // 32, np.uint16)
+    lib().or_quantize_q4(_p(src), n, _p(qs), _p(sc), _p(bi))
+    return qs, sc, bi
+
+
+def pack_q8(qs: np.ndarray, sc: np.ndarray) -> np.ndarray:
+    """One buffer in the Q8_0 split layout: i8 qs[n], then bf16 scales[n/32]."""
+    return np.concatenate([qs.view(np.uint8).ravel(), sc.view(np.uint8).ravel()])
+
+
+def pack_q4(qs: np.ndarray, sc: np.ndarray, bi: np.ndarray) -> np.ndarray:
+    """One buffer in the Q4 split layout: u8 qs[n/2], bf16 scales[n/32], bf16 biases[n/32]."""
+    return np.concatenate([qs.ravel(), sc.view(np.uint8).ravel(), bi.view(np.uint8).ravel()])
+
+
+class QMatrix:
+    """A matrix re-encoded by the restated nncpu encoder, in one split-layout buffer."""
+
+    def __init__(self, dtype: int, rows: int, cols: int, parts):
+        self.dtype, self.rows, self.cols = dtype, rows, cols
+        self.parts = parts
+        self.buf = pack_q8(*parts) if dtype == Q8_0 else pack_q4(*parts)
+
+    @staticmethod
+    def from_f32(dtype: int, w: np.ndarray) -> "QMatrix":
+        rows, cols = w.shape
+        parts = quantize_q8_0(w) if dtype == Q8_0 else quantize_q4(w)
+        return QMatrix(dtype, rows, cols, parts)
+
+    def dequant(self) -> np.ndarray:
+        """f32 weights the kernels multiply by (kernels/tests.rs:380-397)."""
+        if self.dtype == Q8_0:
+            qs, sc = self.parts
+            s = bf16_array_to_f32(sc).repeat(32)
+            return (qs.astype(np.float32) * s).reshape(self.rows, self.cols)
+        qs, sc, bi = self.parts
+        s = bf16_array_to_f32(sc)
+        b = bf16_array_to_f32(bi)
+        blk = qs.reshape(-1, 16)
+        q = np.concatenate([blk & 15, blk >> 4], axis=1).astype(np.float32)  # elements 0..15, 16..31
+        return (q * s[:, None] + b[:, None]).reshape(self.rows, self.cols)
+
+
+# ---- kernels -----------------------------------------------------------------------
+
+def block_sums(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size // 32, np.float32)
+    lib().or_block_sums(_p(x), x.size, _p(out))
+    return out
+
+
+def dot_bf16_f32(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().or_dot_bf16_f32(_p(a), _p(b), a.size)
+
+
+def gemv_batch(m: QMatrix, x: np.ndarray, n_tok: int = 1, x_stride: int | None = None,
+               y_stride: int | None = None, backend: str = "scalar") -> np.ndarray:
+    """model/forward.rs:15-58 on the scalar (oracle.cpp) or AVX2 (avx2.cpp) restatement."""
+    x = np.ascontiguousarray(x, np.float32)
+    xs = m.cols if x_stride is None else x_stride
+    ys = m.rows if y_stride is None else y_stride
+    assert x.size >= (n_tok - 1) * xs + m.cols
+    y = np.zeros((n_tok - 1) * ys + m.rows, np.float32)
+    fn = lib().or_gemv_batch if backend == "scalar" else lib().avx_gemv_batch
+    rc = fn(m.dtype, _p(m.buf), m.rows, m.cols, _p(x), xs, _p(y), ys, n_tok)
+    if rc != 0:
+        raise ValueError("gemv precondition violated")
+    return y
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return lib().or_argmax(_p(v), v.size)
+
+
+def quantize_act(x: np.ndarray):
+    """The int8-block activation quantizer: nncpu's own Q8_0 encoder on x."""
+    return quantize_q8_0(x)
+
+
+def dequant_act(qx: np.ndarray, sx: np.ndarray) -> np.ndarray:
+    out = np.empty(qx.size, np.float32)
+    lib().or_dequant_act(_p(np.ascontiguousarray(qx)), _p(np.ascontiguousarray(sx)), qx.size, _p(out))
+    return out
+
+
+def block_dots(m: QMatrix, qx: np.ndarray) -> np.ndarray:
+    P = np.empty(m.rows * (m.cols // 32), np.int32)
+    qs = m.parts[0]
+    lib().or_block_dots(m.dtype, _p(qs), m.rows, m.cols, _p(np.ascontiguousarray(qx)), _p(P))
+    return P.reshape(m.rows, m.cols // 32)
+
+
+def gemv_i8_exact(m: QMatrix, qx: np.ndarray, sx: np.ndarray) -> np.ndarray:
+    y = np.empty(m.rows, np.float32)
+    lib().or_gemv_i8_exact(m.dtype, _p(m.buf), m.rows, m.cols, _p(np.ascontiguousarray(qx)),
+                           _p(np.ascontiguousarray(sx)), _p(y))
+    return y
+
+
+def avx_available() -> bool:
+    return bool(lib().avx_available())
+
+
+def avx_set_threads(n: int) -> None:
+    lib().avx_set_threads(n)
+
+
+def avx_threads() -> int:
+    return lib().avx_threads()
+
+
+def avx_stream_gbs(nbytes: int = 512 << 20, reps: int = 3) -> float:
+    return lib().avx_stream_gbs(nbytes, reps)

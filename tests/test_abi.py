@@ -1,0 +1,55 @@
+"""The C-ABI library, without a GPU: it loads, exports exactly what
+include/nncpu_hip.h declares, and its host-side checks work."""
+import ctypes as C
+import subprocess
+
+import pytest
+
+import nncpu_amd as N
+from nncpu_amd import _lib
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    names = N.declared_functions()
+    assert len(names) >= 15
+    L = N.lib()
+    for name in names:
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T nnh_" in line}
+    assert exported == set(names)
+
+
+def test_library_targets_gfx950_only():
+    # The offload bundle names its targets in the clear: gfx950 and nothing else.
+    import re
+    data = open(_lib.LIB_PATH, "rb").read()
+    targets = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx[0-9a-z]+)", data))
+    assert targets == {b"gfx950"}
+
+
+def test_null_arguments_are_rejected_without_a_device():
+    L = N.lib()
+    assert L.nnh_weight_info(None, None, None, None) == _lib.NNH_E_INVALID
+    assert b"null" in L.nnh_last_error()
+    h = C.c_void_p()
+    assert L.nnh_upload(7, None, 1, 32, C.byref(h)) == _lib.NNH_E_INVALID
+    L.nnh_free(None)
+
+
+def test_act_layout_is_aligned():
+    off_s, off_sx, total = N.act_layout(4096, 3)
+    assert off_s >= 3 * 4096 and off_s % 256 == 0
+    assert off_sx >= off_s + 3 * 128 * 2 and off_sx % 256 == 0
+    assert total >= off_sx + 3 * 128 * 16
+    with pytest.raises(N.InvalidArgument):
+        N.act_layout(100, 1)
+
+
+def test_init_without_gpu_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    rc = N.lib().nnh_init(0)
+    assert rc in (_lib.NNH_E_DEVICE, _lib.NNH_E_STATE)
+    assert N.lib().nnh_last_error()

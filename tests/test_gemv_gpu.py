@@ -1,0 +1,271 @@
+"""Parity of the HIP path with the oracle, through the C-ABI (needs an MI355X).
+
+f32 path: bit-exact against the oracle (nncpu's kernels restated) on the
+golden vectors, the reference's own test shapes and the BASELINE shapes.
+int8 path: the device quantizer bit-exact against nncpu's Q8_0 encoder, the
+int32 block dots bit-exact, and the outputs within the north-star tolerance
+(1e-3 relative L2, 1e-5 absolute) of the reference kernel fed the
+dequantized activations; also within one f32 ulp of the exact sum.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import bits, close
+from golden_io import cases, load_case
+
+pytestmark = pytest.mark.gpu
+
+N = pytest.importorskip("nncpu_amd")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    N.init(0)
+
+
+def upload(m):
+    if m.dtype == 1:
+        return N.Weight.q8_0(m.parts[0], m.parts[1], m.rows, m.cols)
+    return N.Weight.q4(m.parts[0], m.parts[1], m.parts[2], m.rows, m.cols)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ---- f32 path: bit-exact ----------------------------------------------------------
+
+@pytest.mark.parametrize("case", [c for c in cases() if c["kind"] == "gemv_f32"], ids=lambda c: c["name"])
+def test_f32_golden_bit_exact(oracle, case):
+    say("case", case["name"])
+    m, x, y, _ = load_case(oracle, case)
+    w = upload(m)
+    n, xs, ys = case["n_tok"], case["x_stride"], case["y_stride"]
+    got = np.full_like(y, 7.0)  # stride gaps must stay untouched
+    N.gemv_batch(w, x, xs, got, ys, n, N.ACT_F32)
+    for t in range(n):
+        assert np.array_equal(bits(got[t * ys:t * ys + m.rows]), bits(y[t * ys:t * ys + m.rows])), t
+        gap = got[t * ys + m.rows:(t + 1) * ys] if t + 1 < n else []
+        assert np.all(np.asarray(gap) == 7.0)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_f32_reference_shapes(oracle, dtype):
+    # kernels/tests.rs:555-576 and 616-639: U(-1,1) weights and x, against f64
+    # brute force at 1e-3, and bit-exact against the oracle.
+    rng = oracle.Rng(0xC8E2 if dtype == 1 else 0x40E5)
+    shapes = [(1, 32), (8, 64), (64, 128), (256, 256), (512, 512), (2048, 2048)] if dtype == 1 else \
+        [(1, 32), (8, 64), (64, 128), (256, 256), (512, 512), (1024, 2048), (300, 640)]
+    for rows, cols in shapes:
+        say("shape", dtype, rows, cols)
+        m = oracle.QMatrix.from_f32(dtype, rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols))
+        x = rng.vec(cols, -1.0, 1.0)
+        w = upload(m)
+        y = N.model_gemv(w, x)
+        want = m.dequant().astype(np.float64) @ x.astype(np.float64)
+        assert close(y, want, 1e-3).all()
+        assert np.array_equal(bits(y), bits(oracle.gemv_batch(m, x)))
+
+
+BASELINE_SHAPES = [
+    # Gemma-3-1B decode (config 1): q, k/v, o, gate/up, down.
+    (1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912),
+    # Llama-3-8B projections (config 2).
+    (4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336),
+    # Gemma-4-E2B-like verify shapes (config 4).
+    (6144, 1536), (1536, 6144),
+]
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols", BASELINE_SHAPES)
+def test_f32_baseline_shapes_bit_exact(oracle, dtype, rows, cols):
+    say("baseline", dtype, rows, cols)
+    rng = oracle.Rng(0x5EED00 + rows + cols + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = rng.normals(cols, 1.0)
+    assert np.array_equal(bits(N.model_gemv(w, x)), bits(oracle.gemv_batch(m, x)))
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_f32_batch_equals_single(oracle, dtype):
+    # kernels/tests.rs:641-691: every vector of a batch gets the single-vector bits.
+    rng = oracle.Rng(0xBA7C + dtype)
+    for n_batch in (2, 3, 4, 7, 16):
+        for rows, cols in [(64, 256), (512, 2048), (68, 96), (6, 64)]:
+            m = oracle.QMatrix.from_f32(dtype, rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols))
+            w = upload(m)
+            xs, ys = cols + 32, rows + 3
+            x = rng.vec(n_batch * xs, -1.0, 1.0)
+            yb = np.zeros(n_batch * ys, np.float32)
+            N.gemv_batch(w, x, xs, yb, ys, n_batch)
+            for t in range(n_batch):
+                y1 = N.model_gemv(w, x[t * xs:t * xs + cols])
+                assert np.array_equal(bits(y1), bits(yb[t * ys:t * ys + rows])), (n_batch, rows, cols, t)
+                assert np.array_equal(bits(y1), bits(oracle.gemv_batch(m, x[t * xs:t * xs + cols])))
+
+
+def test_f32_lm_head_gemma_vocab(oracle):
+    # The largest decode gemv: the tied Gemma-3 lm_head, 262144 x 1152, Q8_0.
+    rows, cols = 262144, 1152
+    rng = oracle.Rng(0x5EED03)
+    m = oracle.QMatrix.from_f32(1, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = rng.normals(cols, 1.0)
+    y = N.model_gemv(w, x)
+    ref = oracle.gemv_batch(m, x)
+    assert np.array_equal(bits(y), bits(ref))
+    assert N.model_argmax(w, x) == oracle.argmax(ref)
+
+
+def test_wide_q4_exact():
+    # model/tests.rs:404-423: every weight 1.5, x = 1 -> y = 1.5 * cols exactly.
+    cols, rows = 32 * 1025, 2
+    n = cols * rows
+    w = N.Weight.q4(np.full(n // 2, 0x11, np.uint8), np.full(n // 32, 0x3F80, np.uint16),
+                    np.full(n // 32, 0x3F00, np.uint16), rows, cols)
+    for act in (N.ACT_F32, N.ACT_I8):
+        y = N.model_gemv(w, np.ones(cols, np.float32), act=act)
+        assert np.array_equal(y, np.full(2, 1.5 * cols, np.float32)), act
+
+
+def test_argmax_ties_and_nan(oracle):
+    rows, cols = 4096, 64
+    rng = oracle.Rng(0xA4)
+    m = oracle.QMatrix.from_f32(1, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    qs, sc = m.parts[0].copy(), m.parts[1].copy()
+    x = rng.normals(cols, 1.0)
+    # Rows 3000 and 1000 identical and dominant: the lower row wins.
+    qs.reshape(rows, cols)[1000] = 127 * np.sign(x).astype(np.int8)
+    qs.reshape(rows, cols)[3000] = qs.reshape(rows, cols)[1000]
+    sc.reshape(rows, 2)[[1000, 3000]] = 0x3F80
+    w = N.Weight.q8_0(qs, sc, rows, cols)
+    assert N.model_argmax(w, x) == 1000
+    # A NaN in row 0 keeps row 0 (every `v > NaN` is false).
+    sc.reshape(rows, 2)[0] = 0x7FC0
+    w = N.Weight.q8_0(qs, sc, rows, cols)
+    assert N.model_argmax(w, x) == 0
+    # A NaN elsewhere never wins.
+    sc.reshape(rows, 2)[0] = 0x3F80
+    sc.reshape(rows, 2)[2000] = 0x7FC0
+    w = N.Weight.q8_0(qs, sc, rows, cols)
+    assert np.isnan(N.model_gemv(w, x)[2000])
+    assert N.model_argmax(w, x) == 1000
+
+
+def test_preconditions():
+    w = N.Weight.q8_0(np.zeros(64, np.int8), np.zeros(2, np.uint16), 2, 32)
+    with pytest.raises(N.InvalidArgument):
+        N.gemv_batch(w, np.zeros(64, np.float32), 32, np.zeros(64, np.float32), 1, 2)
+    with pytest.raises(N.InvalidArgument):
+        N.Weight.q8_0(np.zeros(40, np.int8), np.zeros(2, np.uint16), 1, 40)
+    y = np.full(2, 3.0, np.float32)
+    N.gemv_batch(w, np.zeros(32, np.float32), 32, y, 2, 0)  # empty batch: a no-op
+    assert np.all(y == 3.0)
+
+
+# ---- int8 path ---------------------------------------------------------------------
+
+def torch_dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def quantize_on_device(x, cols, n_tok, x_stride=None):
+    import torch
+    xs = cols if x_stride is None else x_stride
+    dx = torch_dev(x)
+    off_s, off_sx, nbytes = N.act_layout(cols, n_tok)
+    act = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    N.quantize_act_dev(dx.data_ptr(), xs, cols, n_tok, act.data_ptr())
+    N.sync()
+    a = act.cpu().numpy()
+    nb = cols // 32
+    q = a[:n_tok * cols].view(np.int8).reshape(n_tok, cols)
+    s = a[off_s:off_s + n_tok * nb * 2].view(np.uint16).reshape(n_tok, nb)
+    return act, q, s
+
+
+@pytest.mark.parametrize("cols", [32, 1152, 4096, 18944])
+def test_act_quantizer_matches_nncpu_encoder(oracle, cols):
+    rng = oracle.Rng(0xAC7 + cols)
+    n_tok = 3
+    x = rng.normals(n_tok * cols, 1.0)
+    x[5] = 0.0
+    if cols >= 96:
+        x[64:96] = 0.0  # an all-zero block
+    _, q, s = quantize_on_device(x, cols, n_tok)
+    for t in range(n_tok):
+        qo, so = oracle.quantize_act(x[t * cols:(t + 1) * cols])
+        assert np.array_equal(q[t], qo) and np.array_equal(s[t], so), t
+
+
+def test_act_quantizer_reciprocal_tie():
+    # An input where amax*(1/127) and amax/127 round to different BF16 scales.
+    from oracle import oracle as O
+    x = np.zeros(64, np.float32)
+    x[3] = np.array([0x3FFEFE01], np.uint32).view(np.float32)[0]
+    x[40] = -1.25
+    _, q, s = quantize_on_device(x, 64, 1)
+    qo, so = O.quantize_act(x)
+    assert np.array_equal(s[0], so) and np.array_equal(q[0], qo)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols", [(32, 256), (16, 1152), (300, 640), (1024, 4096)])
+def test_block_dots_bit_exact(oracle, dtype, rows, cols):
+    import torch
+    rng = oracle.Rng(0xB0 + rows + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    n_tok = 2
+    x = rng.normals(n_tok * cols, 1.0)
+    act, q, _ = quantize_on_device(x, cols, n_tok)
+    P = torch.zeros(n_tok * rows * (cols // 32), dtype=torch.int32, device="cuda")
+    N.block_dots_dev(w, act.data_ptr(), n_tok, P.data_ptr())
+    N.sync()
+    P = P.cpu().numpy().reshape(n_tok, rows, cols // 32)
+    for t in range(n_tok):
+        assert np.array_equal(P[t], oracle.block_dots(m, q[t]))
+
+
+@pytest.mark.parametrize("case", [c for c in cases() if c["kind"] == "gemv_i8"], ids=lambda c: c["name"])
+def test_i8_golden(oracle, case):
+    m, x, y, extra = load_case(oracle, case)
+    w = upload(m)
+    got = N.model_gemv(w, x, act=N.ACT_I8)
+    ulp = np.spacing(np.abs(y))
+    assert np.all(np.abs(got - y) <= ulp)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols,n_tok", [
+    (4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1), (4096, 14336, 1),
+    (6144, 1536, 2), (1536, 6144, 4), (6144, 1536, 8), (1536, 6144, 16),
+    (512, 3584, 3), (3584, 18944, 1),
+])
+def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
+    say("i8", dtype, rows, cols, n_tok)
+    rng = oracle.Rng(0x5EED00 + 7 * rows + cols + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = rng.normals(n_tok * cols, 1.0)
+    y = np.zeros(n_tok * rows, np.float32)
+    N.gemv_batch(w, x, cols, y, rows, n_tok, N.ACT_I8)
+    for t in range(n_tok):
+        qx, sx = oracle.quantize_act(x[t * cols:(t + 1) * cols])
+        ref = oracle.gemv_batch(m, oracle.dequant_act(qx, sx))
+        got = y[t * rows:(t + 1) * rows]
+        # north-star tolerances against nncpu's kernel on the same (dequantized) inputs
+        assert np.abs(got - ref).max() <= 1e-5
+        assert np.linalg.norm(got - ref) <= 1e-3 * np.linalg.norm(ref)
+        if rows * cols <= 4096 * 4096:
+            exact = oracle.gemv_i8_exact(m, qx, sx)
+            assert np.all(np.abs(got - exact) <= np.spacing(np.abs(exact)))

@@ -1,0 +1,320 @@
+"""Pins the CPU oracle (oracle/oracle.cpp, oracle/avx2.cpp) before it is trusted.
+
+Each check comes from the reference's own tests or from what the mathematics
+fixes, chosen so a plausible restatement mistake fails one of them:
+  * known answers from crates/nncpu/src/kernels/tests.rs, runtime.rs and
+    model/tests.rs;
+  * f64 brute force with the reference's tolerance;
+  * exactness of the weight products (closed form);
+  * batch == single and thread-count invariance, bit for bit;
+  * the scalar restatement == the AVX2-intrinsics restatement, bit for bit
+    (two independent writings of the same reduction trees);
+  * the committed golden vectors (tests/golden/).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import bits, close
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def f32_from_bits(u):
+    return float(np.array([u], np.uint32).view(np.float32)[0])
+
+
+# ---- runtime.rs:225-241 ---------------------------------------------------------
+
+def test_bf16_round_trip_and_rne(oracle):
+    for f in [0.0, 1.0, -2.5, 3.140625, 2.0 ** -100, -(2.0 ** 100)]:
+        assert oracle.bf16_to_f32(oracle.f32_to_bf16(f)) == np.float32(f)
+    assert oracle.f32_to_bf16(f32_from_bits(0x3F808000)) == 0x3F80
+    assert oracle.f32_to_bf16(f32_from_bits(0x3F818000)) == 0x3F82
+
+
+# ---- kernels/tests.rs:531-553 ---------------------------------------------------
+
+def test_rint_rounds_half_to_even(oracle):
+    for v in [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5, 0.49999997, 3.7, -3.7, 1e9, -1e9,
+              4_194_304.5, 8e6 + 0.5]:
+        v32 = np.float32(v)
+        assert oracle.rint(float(v32)) == int(np.rint(v32)), v
+    assert oracle.rint(float("nan")) == 0
+    assert oracle.rint(3e10) == 2**31 - 1 and oracle.rint(-3e10) == -(2**31)
+
+
+# ---- kernels/tests.rs:502-529 ---------------------------------------------------
+
+def test_q8_0_quantize_roundtrip(oracle):
+    rng = oracle.Rng(0xC0FFEE)
+    w = rng.vec(3 * 64, -2.5, 2.5)
+    wb = oracle.bf16_array_to_f32(np.array([oracle.f32_to_bf16(float(v)) for v in w], np.uint16))
+    qs, sc = oracle.quantize_q8_0(wb)
+    s = oracle.bf16_array_to_f32(sc).repeat(32)
+    assert np.all(np.abs(s * qs.astype(np.float32) - wb) <= s + 1e-6)
+    assert qs.min() >= -127 and qs.max() <= 127
+    src = np.zeros(32, np.float32)
+    src[5], src[9] = -3.0, 1.5
+    q, s1 = oracle.quantize_q8_0(src)
+    assert oracle.bf16_to_f32(int(s1[0])) == oracle.bf16_to_f32(oracle.f32_to_bf16(3.0 / 127.0))
+    assert (q[5], q[0]) == (-127, 0)
+    q, s1 = oracle.quantize_q8_0(np.zeros(32, np.float32))
+    assert s1[0] == 0 and not q.any()
+
+
+def test_scales_are_times_reciprocal(oracle):
+    # quant.rs:49-53,86-88: amax * (1/127) and (hi - lo) * (1/15), not a
+    # division. These inputs (found by scanning every f32 in [1, 2)) are
+    # ones where the two round to different BF16 scales.
+    def bf(v):
+        return oracle.f32_to_bf16(float(v))
+
+    amax = np.float32(f32_from_bits(0x3FFEFE01))
+    prod, quot = amax * np.float32(1.0 / 127.0), amax / np.float32(127.0)
+    assert bf(prod) != bf(quot)
+    src = np.zeros(32, np.float32)
+    src[3] = amax
+    assert oracle.quantize_q8_0(src)[1][0] == bf(prod)
+    span = np.float32(f32_from_bits(0x3F895800))
+    prod, quot = span * np.float32(1.0 / 15.0), span / np.float32(15.0)
+    assert bf(prod) != bf(quot)
+    src = np.zeros(32, np.float32)
+    src[7] = span
+    assert oracle.quantize_q4(src)[1][0] == bf(prod)
+
+
+# ---- kernels/tests.rs:578-614 ---------------------------------------------------
+
+def test_q4_quantize_roundtrip(oracle):
+    src = np.zeros(64, np.float32)
+    for i in range(32):
+        src[i] = -2.0 + (i % 16) * 0.25
+        src[32 + i] = 4.0 + (i % 16) * 0.5
+    qs, sc, bi = oracle.quantize_q4(src)
+    for b, (s, bias) in enumerate([(0.25, -2.0), (0.5, 4.0)]):
+        assert (oracle.bf16_to_f32(int(sc[b])), oracle.bf16_to_f32(int(bi[b]))) == (s, bias)
+        for k in range(16):
+            byte = int(qs[16 * b + k])
+            assert s * (byte & 15) + bias == src[32 * b + k]
+            assert s * (byte >> 4) + bias == src[32 * b + k + 16]
+    rng = oracle.Rng(0x4B15)
+    src = rng.vec(32, -3.0, 7.0)
+    qs, sc, bi = oracle.quantize_q4(src)
+    s, bias = oracle.bf16_to_f32(int(sc[0])), oracle.bf16_to_f32(int(bi[0]))
+    tol = 0.5 * s + (15.0 * s + abs(bias)) * 0.00391 + 1e-6
+    for k in range(16):
+        assert abs(s * (qs[k] & 15) + bias - src[k]) <= tol
+        assert abs(s * (qs[k] >> 4) + bias - src[k + 16]) <= tol
+    qs, sc, bi = oracle.quantize_q4(np.full(32, 3.5, np.float32))
+    assert (oracle.bf16_to_f32(int(sc[0])), oracle.bf16_to_f32(int(bi[0]))) == (0.0, 3.5)
+    assert not qs.any()
+
+
+# ---- kernels/tests.rs:360-372 ---------------------------------------------------
+
+def test_block_sums_match_reference(oracle):
+    rng = oracle.Rng(0xB10C)
+    x = rng.vec(128, -4.0, 4.0)
+    out = oracle.block_sums(x)
+    want = x.astype(np.float64).reshape(4, 32).sum(1)
+    assert close(out, want, 1e-5).all()
+
+
+def test_block_sums_order(oracle):
+    # Values whose f32 sum depends on the order: the tree is
+    # hsum8(((c[l]+c[8+l])+c[16+l])+c[24+l]); a sequential sum gives 0 here.
+    c = np.zeros(32, np.float32)
+    c[0], c[8], c[1] = 2.0 ** 24, 1.0, 1.0
+    out = oracle.block_sums(c)[0]
+    # lane 0: (2^24 + 1) -> 2^24; lane 1: 1; hsum8: (v0+v4)+(v1+v5) = 2^24 + 1 -> 2^24 (tie to even)
+    assert out == np.float32(2.0 ** 24)
+    c[:] = 0
+    c[0], c[1], c[4] = 2.0 ** 24, 1.0, 1.0
+    # (v0+v4) = 2^24+1 -> 2^24 (tie, even); (v1+v5) = 1 -> total 2^24+1 -> 2^24
+    assert oracle.block_sums(c)[0] == np.float32(2.0 ** 24)
+    c[:] = 0
+    c[1], c[5], c[0] = 1.0, 1.0, 2.0 ** 24
+    # (v1+v5) = 2 first, then 2^24 + 2 is exact.
+    assert oracle.block_sums(c)[0] == np.float32(2.0 ** 24 + 2)
+
+
+# ---- gemv against f64 brute force (kernels/tests.rs:555-576, 616-639) ------------
+
+Q8_SHAPES = [(1, 32), (8, 64), (64, 128), (256, 256), (512, 512), (2048, 2048)]
+Q4_SHAPES = [(1, 32), (8, 64), (64, 128), (256, 256), (512, 512), (1024, 2048), (300, 640)]
+
+
+@pytest.mark.parametrize("dtype,shapes,seed", [(1, Q8_SHAPES, 0xC8E2), (2, Q4_SHAPES, 0x40E5)])
+def test_gemv_matches_f64(oracle, dtype, shapes, seed):
+    rng = oracle.Rng(seed)
+    for rows, cols in shapes:
+        w = rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols)
+        if dtype == 1:
+            w = oracle.bf16_array_to_f32(np.array([oracle.f32_to_bf16(float(v)) for v in w.ravel()], np.uint16)
+                                         ).reshape(rows, cols) if rows * cols <= 4096 else w
+        m = oracle.QMatrix.from_f32(dtype, w)
+        x = rng.vec(cols, -1.0, 1.0)
+        want = m.dequant().astype(np.float64) @ x.astype(np.float64)
+        for backend in ("scalar", "avx2"):
+            y = oracle.gemv_batch(m, x, backend=backend)
+            assert close(y, want, 1e-3).all(), (rows, cols, backend)
+
+
+def test_weight_products_are_exact(oracle):
+    # f32(q) * bf16(scale) is exact for every Q8 quant and Q4 nibble, so
+    # dequantizing in f64 and rounding never differs from the f32 product.
+    rng = oracle.Rng(7)
+    sc = np.array([oracle.f32_to_bf16(float(v)) for v in rng.vec(2000, 1e-6, 10.0)], np.uint16)
+    s = oracle.bf16_array_to_f32(sc).astype(np.float64)
+    q = np.arange(-127, 128, dtype=np.float64)
+    exact = np.outer(s, q)
+    assert np.array_equal(exact.astype(np.float32).astype(np.float64), exact)
+
+
+# ---- invariants (kernels/tests.rs:641-741) ----------------------------------------
+
+def test_gemv_batch_matches_rows(oracle):
+    rng = oracle.Rng(0xBA7C)
+    for n_batch in (2, 3, 4, 7):
+        for rows, cols in [(64, 256), (512, 2048), (68, 96), (6, 64)]:
+            w = rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols)
+            xs, ys = cols + 32, rows + 3
+            x = rng.vec(n_batch * xs, -1.0, 1.0)
+            for dtype in (1, 2):
+                m = oracle.QMatrix.from_f32(dtype, w)
+                for backend in ("scalar", "avx2"):
+                    yb = oracle.gemv_batch(m, x, n_batch, xs, ys, backend=backend)
+                    for t in range(n_batch):
+                        y1 = oracle.gemv_batch(m, x[t * xs:t * xs + cols], backend=backend)
+                        assert np.array_equal(bits(y1), bits(yb[t * ys:t * ys + rows])), (n_batch, rows, cols)
+
+
+def test_scalar_equals_avx2_bits(oracle):
+    if not oracle.avx_available():
+        pytest.skip("no AVX2+FMA on this host")
+    rng = oracle.Rng(0x5CA1)
+    for rows, cols in [(300, 640), (64, 1152), (17, 6912), (5, 96)]:
+        w = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+        x = rng.normals(3 * cols, 1.0)
+        for dtype in (1, 2):
+            m = oracle.QMatrix.from_f32(dtype, w)
+            for n in (1, 3):
+                a = oracle.gemv_batch(m, x, n, cols, rows, backend="scalar")
+                b = oracle.gemv_batch(m, x, n, cols, rows, backend="avx2")
+                assert np.array_equal(bits(a), bits(b)), (rows, cols, dtype, n)
+
+
+def test_results_do_not_depend_on_thread_count(oracle):
+    rng = oracle.Rng(0x7417)
+    rows, cols, n_batch = 1024, 512, 5
+    w = rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols)
+    x = rng.vec(n_batch * cols, -1.0, 1.0)
+    old = oracle.avx_threads()
+    try:
+        outs = {}
+        for nt in (1, 2, 3, 7, 16):
+            oracle.avx_set_threads(nt)
+            outs[nt] = [bits(oracle.gemv_batch(oracle.QMatrix.from_f32(d, w), x, n, cols, rows, backend="avx2"))
+                        for d in (1, 2) for n in (1, n_batch)]
+        for nt in (2, 3, 7, 16):
+            for a, b in zip(outs[1], outs[nt]):
+                assert np.array_equal(a, b), nt
+    finally:
+        oracle.avx_set_threads(old)
+
+
+# ---- model/tests.rs:404-423: a wide Q4 with an exact answer -----------------------
+
+def test_wide_q4_exact(oracle):
+    cols, rows = 32 * 1025, 2
+    n = cols * rows
+    qs = np.full(n // 2, 0x11, np.uint8)
+    sc = np.full(n // 32, 0x3F80, np.uint16)
+    bi = np.full(n // 32, 0x3F00, np.uint16)
+    m = oracle.QMatrix(2, rows, cols, (qs, sc, bi))
+    y = oracle.gemv_batch(m, np.ones(cols, np.float32))
+    assert np.array_equal(y, np.full(2, 1.5 * cols, np.float32))
+
+
+# ---- argmax (model/forward.rs:1003-1011) ------------------------------------------
+
+def test_argmax_ties_and_nan(oracle):
+    v = np.array([1.0, 3.0, 2.0, 3.0], np.float32)
+    assert oracle.argmax(v) == 1
+    v = np.array([np.nan, 5.0, 1.0], np.float32)
+    assert oracle.argmax(v) == 0
+    v = np.array([1.0, np.nan, 5.0, 5.0], np.float32)
+    assert oracle.argmax(v) == 2
+    v = np.array([-0.0, 0.0], np.float32)
+    assert oracle.argmax(v) == 0
+
+
+# ---- dot_bf16_f32 (scalar.rs:334-347) ----------------------------------------------
+
+def test_dot_bf16_tail_is_unfused(oracle):
+    rng = oracle.Rng(0xD07)
+    for n in (1, 7, 8, 9, 36, 37, 1025):
+        a = np.array([oracle.f32_to_bf16(float(v)) for v in rng.vec(n, -1, 1)], np.uint16)
+        b = rng.vec(n, -1, 1)
+        want = (oracle.bf16_array_to_f32(a).astype(np.float64) * b).sum()
+        assert abs(oracle.dot_bf16_f32(a, b) - want) <= 1e-5 * max(1.0, abs(want))
+
+
+# ---- int8 path: exact block dots and the exact-sum reference -----------------------
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_block_dots_brute_force(oracle, dtype):
+    rng = oracle.Rng(0x1D07 + dtype)
+    rows, cols = 24, 160
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    qx, sx = oracle.quantize_act(rng.normals(cols, 1.0))
+    P = oracle.block_dots(m, qx)
+    if dtype == 1:
+        qw = m.parts[0].astype(np.int64).reshape(rows, cols // 32, 32)
+    else:
+        blk = m.parts[0].reshape(rows, cols // 32, 16).astype(np.int64)
+        qw = np.concatenate([blk & 15, blk >> 4], axis=2)
+    want = (qw * qx.astype(np.int64).reshape(1, cols // 32, 32)).sum(2)
+    assert np.array_equal(P, want)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_i8_exact_sum_within_reference_error(oracle, dtype):
+    # The exact-sum value vs the reference kernel fed the dequantized
+    # activations: the north-star tolerances, 1e-3 relative L2, 1e-5 abs.
+    rng = oracle.Rng(0xE8 + dtype)
+    rows, cols = 256, 4096
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    qx, sx = oracle.quantize_act(rng.normals(cols, 1.0))
+    exact = oracle.gemv_i8_exact(m, qx, sx)
+    ref = oracle.gemv_batch(m, oracle.dequant_act(qx, sx))
+    f64 = m.dequant().astype(np.float64) @ oracle.dequant_act(qx, sx).astype(np.float64)
+    assert np.abs(exact - f64).max() <= np.spacing(np.abs(f64).astype(np.float32)).max()
+    assert np.abs(exact - ref).max() <= 1e-5
+    assert np.linalg.norm(exact - ref) <= 1e-3 * np.linalg.norm(ref)
+
+
+# ---- golden vectors -----------------------------------------------------------------
+
+def _golden_cases():
+    path = os.path.join(GOLDEN, "manifest.json")
+    if not os.path.exists(path):
+        return []
+    return json.load(open(path))["cases"]
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["name"])
+def test_oracle_matches_golden(oracle, case):
+    from golden_io import load_case
+    m, x, y, extra = load_case(oracle, case)
+    if case["kind"] == "gemv_f32":
+        got = oracle.gemv_batch(m, x, case["n_tok"], case["x_stride"], case["y_stride"])
+        assert np.array_equal(bits(got), bits(y))
+    elif case["kind"] == "gemv_i8":
+        qx, sx = oracle.quantize_act(x)
+        assert np.array_equal(qx, extra["qx"]) and np.array_equal(sx, extra["sx"])
+        assert np.array_equal(bits(oracle.gemv_i8_exact(m, qx, sx)), bits(y))
+        assert np.array_equal(oracle.block_dots(m, qx), extra["P"])
