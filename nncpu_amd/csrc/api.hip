@@ -21,6 +21,7 @@ struct nnh_weight {
     const uint8_t* qs;    // views into raw
     const uint16_t* sc;
     const uint16_t* bi;   // Q4 only
+    uint32_t* sb;         // device: Q4 scale | bias << 16 per block (int8 path)
     uint8_t* fq;          // device: per-lane quant groups for the f32 path
     uint16_t* fs;         // device: scales padded to nbp per row
 };
@@ -127,7 +128,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         uint16_t* s = (uint16_t*)(scratch + l.off_s);
         double* sx = (double*)(scratch + l.off_sx);
         nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, q, s, sx, st);
-        nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, q, sx, rows, nb, (int)n_tok, y, y_stride, st);
+        nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, rows, nb, (int)n_tok, y, y_stride, st);
     }
     NNH_HIP(hipGetLastError());
     return NNH_OK;
@@ -179,13 +180,15 @@ int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size
         if (w->raw) (void)hipFree(w->raw);
         if (w->fq) (void)hipFree(w->fq);
         if (w->fs) (void)hipFree(w->fs);
+        if (w->sb) (void)hipFree(w->sb);
         delete w;
         return code;
     };
     hipError_t e;
     if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes))) != hipSuccess ||
         (e = hipMalloc((void**)&w->fq, align_up(qbytes))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->fs, align_up(rows * nbp * 2))) != hipSuccess) {
+        (e = hipMalloc((void**)&w->fs, align_up(rows * nbp * 2))) != hipSuccess ||
+        (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess)) {
         return cleanup(fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
                             std::string("nnh_upload: ") + hipGetErrorString(e)));
     }
@@ -198,6 +201,7 @@ int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size
          (e = hipMemcpyAsync(w->raw + qbytes + tbytes, bi, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess))
         return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: copy: ") + hipGetErrorString(e)));
     nnh::launch_relayout_f32(dtype, w->qs, w->sc, w->fq, w->fs, (int)rows, (int)nb, (int)nbp, g_stream);
+    if (dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, rows * nb, g_stream);
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
         return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: relayout: ") + hipGetErrorString(e)));
     *out = w;
@@ -241,6 +245,7 @@ void nnh_free(nnh_weight* w) {
     (void)hipFree(w->raw);
     (void)hipFree(w->fq);
     (void)hipFree(w->fs);
+    (void)hipFree(w->sb);
     delete w;
 }
 
@@ -360,7 +365,7 @@ int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y
     if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
     ActLayout l = act_layout(w->cols, n_tok);
     const uint8_t* a = (const uint8_t*)act;
-    nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, (const int8_t*)a, (const double*)(a + l.off_sx), (int)w->rows,
+    nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, (const int8_t*)a, (const double*)(a + l.off_sx), (int)w->rows,
                         (int)w->nb, (int)n_tok, y, n_tok > 1 ? y_stride : w->rows, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;

@@ -22,6 +22,39 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 __device__ __forceinline__ float xor_get(float v, int mask) { return __shfl_xor(v, mask, 64); }
 __device__ __forceinline__ double xor_get(double v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// f64 lane exchanges by DPP (a VALU modifier; no LDS traffic): each half of
+// the double is moved with the same control. Controls used: 0xB1 quad_perm
+// [1,0,3,2] (xor 1), 0x4E quad_perm [2,3,0,1] (xor 2), 0x141 row_half_mirror
+// (lane i <-> 7-i within 8), 0x140 row_mirror (i <-> 15-i within 16).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    int lo = __double2loint(v), hi = __double2hiint(v);
+    lo = __builtin_amdgcn_update_dpp(0, lo, CTRL, 0xf, 0xf, false);
+    hi = __builtin_amdgcn_update_dpp(0, hi, CTRL, 0xf, 0xf, false);
+    return __hiloint2double(hi, lo);
+}
+
+// Sum over groups of L lanes (L in 2..64, a power of two); every lane of a
+// group gets the group's sum. Fixed order, so the result is deterministic.
+template <int L>
+__device__ __forceinline__ double group_sum_f64(double v) {
+    if (L >= 2) v += dpp_f64<0xB1>(v);
+    if (L >= 4) v += dpp_f64<0x4E>(v);
+    if (L >= 8) v += dpp_f64<0x141>(v);
+    if (L >= 16) v += dpp_f64<0x140>(v);
+    if (L >= 32) v += __shfl_xor(v, 16, 64);
+    if (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// 16-byte load with the non-temporal hint: weights are streamed once per
+// call and should not displace reused data (activations) in the caches.
+typedef int nnh_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 load_nt16(const void* p) {
+    nnh_v4i v = __builtin_nontemporal_load((const nnh_v4i*)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
 inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ---- launchers (defined beside their kernels) -------------------------------
@@ -39,8 +72,10 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
 // int8 path (kernels_i8.hip).
 void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
                          hipStream_t st);
-void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
-                    const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);
+void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st);
+void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
+                    const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
+                    hipStream_t st);
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
                        hipStream_t st);
 

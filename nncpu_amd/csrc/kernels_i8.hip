@@ -100,15 +100,19 @@ __device__ __forceinline__ int dot_q4(const int4& w, const int4& x0, const int4&
 // A workgroup of 256 lanes = 4 waves; each wave is 64/LPR groups of LPR lanes,
 // a group owns R consecutive rows and its lanes take the blocks cyclically
 // (lane l: blocks l, l+LPR, ...), so one wave-wide 128-bit load reads
-// contiguous weight bytes. Per block and row: the int32 dot, then
+// contiguous weight bytes. The row is walked in chunks of LPR*BPL blocks; a
+// chunk's loads (BPL blocks per lane per row, plus the activation blocks)
+// are all issued before any is used, so a lane waits on memory once per
+// chunk rather than once per block. Per block and row: the int32 dot, then
 // acc += (s_w * s_x) * P (+ bias * s_x * sum q_x) in f64. The group's lanes
-// are summed with an xor tree in f64 and rounded once.
-template <int DT, int M, int R, int LPR>
+// are summed with an xor tree in f64 and the sum is rounded once.
+template <int DT, int M, int R, int LPR, int BPL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ sc,
                                                       const uint16_t* __restrict__ bi, const int8_t* __restrict__ aq,
                                                       const double* __restrict__ asx, int rows, int nb,
                                                       float* __restrict__ y, size_t y_stride) {
     constexpr int G = 64 / LPR;
+    constexpr int QV = DT == 1 ? 2 : 1;  // 16-byte loads per block of weights
     const int lane = threadIdx.x % LPR;
     const int grp = threadIdx.x / LPR;  // 0 .. 4*G-1
     const int row0 = (blockIdx.x * (4 * G) + grp) * R;
@@ -125,38 +129,51 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0;
 
-    for (int b = lane; b < nb; b += LPR) {
-        int4 x0[M], x1[M];
-        double sxv[M], sxq[M];
+    for (int c0 = 0; c0 < nb; c0 += LPR * BPL) {
+        int4 w[R][BPL][QV];
+        uint32_t ws[R][BPL], wb[R][BPL];
+        int4 x0[M][BPL], x1[M][BPL];
+        double sxv[M][BPL], sxq[M][BPL];
+        bool ok[BPL];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * (size_t)b);
-            x0[m] = xp[0];
-            x1[m] = xp[1];
-            sxv[m] = asx[2 * ((size_t)m * nb + b)];
-            sxq[m] = asx[2 * ((size_t)m * nb + b) + 1];
-        }
+        for (int i = 0; i < BPL; ++i) {
+            const int braw = c0 + lane + i * LPR;
+            ok[i] = braw < nb;
+            const size_t b = ok[i] ? braw : nb - 1;  // in bounds; skipped below
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const size_t rb = (size_t)rr[r] * nb + b;
-            const double sw = (double)bf16f(sc[rb]);
-            int P[M];
-            if (DT == 1) {
-                const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + 32 * (size_t)b);
-                int4 w0 = wp[0], w1 = wp[1];
-#pragma unroll
-                for (int m = 0; m < M; ++m) P[m] = dot_q8(w0, w1, x0[m], x1[m]);
-            } else {
-                int4 w = *(const int4*)(qs + (size_t)rr[r] * qrow_bytes + 16 * (size_t)b);
-#pragma unroll
-                for (int m = 0; m < M; ++m) P[m] = dot_q4(w, x0[m], x1[m]);
+            for (int m = 0; m < M; ++m) {
+                const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * b);
+                x0[m][i] = xp[0];
+                x1[m][i] = xp[1];
+                sxv[m][i] = asx[2 * ((size_t)m * nb + b)];
+                sxq[m][i] = asx[2 * ((size_t)m * nb + b) + 1];
             }
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(sw * sxv[m], (double)P[m], acc[r][m]);
-            if (DT == 2) {
-                const double bw = (double)bf16f(bi[rb]);
+            for (int r = 0; r < R; ++r) {
+                const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + (DT == 1 ? 32 : 16) * b);
 #pragma unroll
-                for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sxq[m], acc[r][m]);
+                for (int v = 0; v < QV; ++v) w[r][i][v] = wp[v];
+                ws[r][i] = sc[(size_t)rr[r] * nb + b];
+                if (DT == 2) wb[r][i] = bi[(size_t)rr[r] * nb + b];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            if (!ok[i]) continue;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const double sw = (double)bf16f(ws[r][i]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const int P = DT == 1 ? dot_q8(w[r][i][0], w[r][i][QV - 1], x0[m][i], x1[m][i])
+                                          : dot_q4(w[r][i][0], x0[m][i], x1[m][i]);
+                    acc[r][m] = __builtin_fma(sw * sxv[m][i], (double)P, acc[r][m]);
+                }
+                if (DT == 2) {
+                    const double bw = (double)bf16f(wb[r][i]);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sxq[m][i], acc[r][m]);
+                }
             }
         }
     }
@@ -170,6 +187,91 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
             for (int k = LPR / 2; k >= 1; k >>= 1) v += xor_get(v, k);
             acc[r][m] = v;
         }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < rows)
+#pragma unroll
+                for (int m = 0; m < M; ++m) y[(size_t)m * y_stride + row0 + r] = (float)acc[r][m];
+    }
+}
+
+// The same computation with three changes for short launches: the chunk
+// loop has no tail (nb is a multiple of LPR*BPL, checked by the launcher),
+// Q4 scale and bias come as one packed 32-bit word per block (`sb`,
+// scale | bias << 16, built at upload), and the lane sum uses DPP.
+template <int DT, int M, int R, int LPR, int BPL>
+__global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restrict__ qs,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint32_t* __restrict__ sb,
+                                                         const int8_t* __restrict__ aq,
+                                                         const double* __restrict__ asx, int rows, int nb,
+                                                         float* __restrict__ y, size_t y_stride) {
+    constexpr int G = 64 / LPR;
+    constexpr int QV = DT == 1 ? 2 : 1;
+    const int lane = threadIdx.x % LPR;
+    const int grp = threadIdx.x / LPR;
+    const int row0 = (blockIdx.x * (4 * G) + grp) * R;
+    const size_t cols = (size_t)nb * 32;
+    const size_t qrow_bytes = DT == 1 ? cols : cols / 2;
+
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rr[r] = row0 + r < rows ? row0 + r : rows - 1;
+
+    double acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = 0.0;
+
+    for (int c0 = 0; c0 < nb; c0 += LPR * BPL) {
+        int4 w[R][BPL][QV];
+        uint32_t s[R][BPL];
+        int4 x0[M][BPL], x1[M][BPL];
+        double2 sx[M][BPL];
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const size_t b = c0 + lane + i * LPR;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + (DT == 1 ? 32 : 16) * b);
+#pragma unroll
+                for (int v = 0; v < QV; ++v) w[r][i][v] = load_nt16(wp + v);
+                s[r][i] = DT == 1 ? (uint32_t)sc[(size_t)rr[r] * nb + b] : sb[(size_t)rr[r] * nb + b];
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * b);
+                x0[m][i] = xp[0];
+                x1[m][i] = xp[1];
+                sx[m][i] = ((const double2*)asx)[(size_t)m * nb + b];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const double sw = (double)bf16f(s[r][i] & 0xffffu);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const int P = DT == 1 ? dot_q8(w[r][i][0], w[r][i][QV - 1], x0[m][i], x1[m][i])
+                                          : dot_q4(w[r][i][0], x0[m][i], x1[m][i]);
+                    acc[r][m] = __builtin_fma(sw * sx[m][i].x, (double)P, acc[r][m]);
+                }
+                if (DT == 2) {
+                    const double bw = (double)bf16f(s[r][i] >> 16);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sx[m][i].y, acc[r][m]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = group_sum_f64<LPR>(acc[r][m]);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -199,26 +301,65 @@ __global__ void block_dots_kernel(const uint8_t* __restrict__ qs, const int8_t* 
     }
 }
 
-template <int DT, int M, int R, int LPR>
+template <int DT, int M, int R, int LPR, int BPL>
 void launch_cfg(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const int8_t* aq, const double* asx,
                 int rows, int nb, float* y, size_t ys, hipStream_t st) {
     constexpr int rows_per_wg = 4 * (64 / LPR) * R;
-    gemv_i8_kernel<DT, M, R, LPR><<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, bi, aq, asx, rows, nb, y, ys);
+    gemv_i8_kernel<DT, M, R, LPR, BPL>
+        <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, bi, aq, asx, rows, nb, y, ys);
 }
 
+// Launch shape by row length: lanes per row and blocks per lane so that a
+// lane's whole row share is one chunk of hoisted loads where possible.
 template <int DT, int M>
 void launch_m(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const int8_t* aq, const double* asx,
               int rows, int nb, float* y, size_t ys, hipStream_t st) {
-    // Lanes per row: enough blocks per lane to amortise the reduction.
-    if (nb >= 256)
-        launch_cfg<DT, M, 2, 64>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
-    else if (nb >= 64)
-        launch_cfg<DT, M, 2, 32>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+    if (nb <= 64)
+        launch_cfg<DT, M, 2, 16, 4>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+    else if (nb <= 128)
+        launch_cfg<DT, M, 2, 32, 4>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
     else
-        launch_cfg<DT, M, 2, 16>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+        launch_cfg<DT, M, 2, 64, 4>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+}
+
+// sb[i] = scale[i] | bias[i] << 16: one 32-bit load per Q4 block.
+__global__ void pack_sb_kernel(const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+                               uint32_t* __restrict__ sb, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) sb[i] = (uint32_t)sc[i] | ((uint32_t)bi[i] << 16);
+}
+
+template <int DT, int M, int R, int LPR, int BPL>
+void launch_v2(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
+               int rows, int nb, float* y, size_t ys, hipStream_t st) {
+    constexpr int rows_per_wg = 4 * (64 / LPR) * R;
+    gemv_i8_v2_kernel<DT, M, R, LPR, BPL>
+        <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
+}
+
+// Launch shape from the measured sweep (Llama-3-8B and vocab shapes): 64
+// lanes per row taking 2 blocks per chunk when the row is a whole number of
+// 128-block chunks, else 1; two rows per lane group for tall matrices.
+template <int DT, int M>
+bool launch_v2_m(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
+                 int rows, int nb, float* y, size_t ys, hipStream_t st) {
+    if (nb % 64 != 0) return false;
+    const bool tall = rows >= 8192;
+    if (nb % 128 == 0) {
+        if (tall) launch_v2<DT, M, 2, 64, 2>(qs, sc, sb, aq, asx, rows, nb, y, ys, st);
+        else launch_v2<DT, M, 1, 64, 2>(qs, sc, sb, aq, asx, rows, nb, y, ys, st);
+    } else {
+        if (tall) launch_v2<DT, M, 2, 64, 1>(qs, sc, sb, aq, asx, rows, nb, y, ys, st);
+        else launch_v2<DT, M, 2, 64, 1>(qs, sc, sb, aq, asx, rows, nb, y, ys, st);
+    }
+    return true;
 }
 
 }  // namespace
+
+void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st) {
+    pack_sb_kernel<<<(int)((n + 255) / 256), 256, 0, st>>>(sc, bi, sb, n);
+}
 
 void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
                          hipStream_t st) {
@@ -226,15 +367,20 @@ void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, i
     quantize_act_kernel<<<ceil_div(blocks, 8), 256, 0, st>>>(x, x_stride, cols, n_tok, q, s, sx);
 }
 
-void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
-                    const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st) {
+void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
+                    const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
+                    hipStream_t st) {
     const size_t cols = (size_t)nb * 32;
     for (int t0 = 0; t0 < n_tok; t0 += 4) {
         int m = n_tok - t0 < 4 ? n_tok - t0 : 4;
         const int8_t* a = aq + (size_t)t0 * cols;
         const double* s = asx + 2 * (size_t)t0 * nb;
         float* yt = y + (size_t)t0 * y_stride;
-#define NNH_L(DT, M) launch_m<DT, M>(qs, scales, biases, a, s, rows, nb, yt, y_stride, st)
+#define NNH_L(DT, M)                                                                             \
+    do {                                                                                         \
+        if (!launch_v2_m<DT, M>(qs, scales, sb, a, s, rows, nb, yt, y_stride, st))                \
+            launch_m<DT, M>(qs, scales, biases, a, s, rows, nb, yt, y_stride, st);               \
+    } while (0)
         if (dtype == 1) {
             if (m == 1) NNH_L(1, 1); else if (m == 2) NNH_L(1, 2); else if (m == 3) NNH_L(1, 3); else NNH_L(1, 4);
         } else {

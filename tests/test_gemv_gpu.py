@@ -131,9 +131,13 @@ def test_wide_q4_exact():
     n = cols * rows
     w = N.Weight.q4(np.full(n // 2, 0x11, np.uint8), np.full(n // 32, 0x3F80, np.uint16),
                     np.full(n // 32, 0x3F00, np.uint16), rows, cols)
-    for act in (N.ACT_F32, N.ACT_I8):
-        y = N.model_gemv(w, np.ones(cols, np.float32), act=act)
-        assert np.array_equal(y, np.full(2, 1.5 * cols, np.float32)), act
+    y = N.model_gemv(w, np.ones(cols, np.float32), act=N.ACT_F32)
+    assert np.array_equal(y, np.full(2, 1.5 * cols, np.float32))
+    # int8 activations: x = 1 quantizes to q = 127 at scale bf16(1/127), so
+    # x' = 127 * 0x3C01 (0.00787353515625) and y = 1.5 * cols * x' exactly.
+    xq = 127 * np.float64(np.array([0x3C010000], np.uint32).view(np.float32)[0])
+    y = N.model_gemv(w, np.ones(cols, np.float32), act=N.ACT_I8)
+    assert np.array_equal(y, np.full(2, np.float32(1.5 * cols * xq)))
 
 
 def test_argmax_ties_and_nan(oracle):
