@@ -161,6 +161,55 @@ def q4_sweep(args, N, O):
     return result, shapes
 
 
+QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
+VERIFY_SHAPES = [(6144, 1536), (1536, 6144), (2048, 1536), (1536, 1536)]
+GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912), (262144, 1152)]
+
+
+def measure_cases(args, N, O, cases, act_mode, label):
+    """Time each (dtype, n, k, m) case alone: `args.steps` launches captured in
+    a graph over rotating weight copies (>= 512 MB), inputs resident in HBM.
+    act_mode: ACT_I8 times the int8 matmul on pre-quantized activations;
+    ACT_F32 times the bit-exact f32 path (block sums included for Q4)."""
+    import torch
+    st = Stream()
+    out = []
+    for ci, (dtype, n, k, m) in enumerate(cases):
+        wq = make_weight(O, dtype, n, k, 0x5EED10 + 7 * ci + dtype)
+        wb = weight_bytes(dtype, n, k)
+        copies = max(2, math.ceil(ROTATE_BYTES / wb))
+        ws = [N.Weight.from_split(dtype, wq.buf, n, k) for _ in range(copies)]
+        x = torch.from_numpy(O.Rng(0xA11 + ci).normals(m * k, 1.0)).cuda()
+        y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+        _, _, abytes = N.act_layout(k, m)
+        act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
+        N.quantize_act_dev(x.data_ptr(), k, k, m, act.data_ptr(), st.handle)
+        state = {"i": 0}
+
+        def launch(ws=ws, state=state, act=act, x=x, y=y, n=n, k=k, m=m):
+            w = ws[state["i"] % len(ws)]
+            state["i"] += 1
+            if act_mode == N.ACT_I8:
+                N.gemv_i8_dev(w, act.data_ptr(), m, y.data_ptr(), n, st.handle)
+            else:
+                N.gemv_batch_dev(w, x.data_ptr(), k, y.data_ptr(), n, m, N.ACT_F32, st.handle)
+
+        torch.cuda.synchronize()
+        steps = max(10, min(args.steps, int(2e5 / max(1.0, wb / 1e6))))  # bound the timed work
+        secs = time_gemv_set(N, st, [launch], steps, min(args.warmup, 10))
+        us = secs / steps * 1e6
+        byts = gemv_bytes(dtype, n, k, m)
+        ops = 2.0 * m * n * k
+        e = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} {n}x{k} M={m}", us=round(us, 3),
+                 gbs=round(byts / us / 1e3, 1), hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+                 tops=round(ops / us / 1e6, 2), int8_frac=round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), steps=steps)
+        log(f"{label}: {e}")
+        out.append(e)
+        del ws
+        torch.cuda.synchronize()
+    return out
+
+
 def cpu_baseline_q4(O, shapes, budget_s=12.0):
     """nncpu's AVX2 kernels (restated, oracle/avx2.cpp) on this host's cores,
     fed the dequantized int8 activations, rotating >= 256 MB of weight copies
@@ -204,7 +253,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="q4_sweep", choices=["q4_sweep"])
+    ap.add_argument("--workload", default="q4_sweep",
+                    choices=["q4_sweep", "prefill", "q8_vocab", "verify", "decode_f32", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -216,6 +266,21 @@ def main():
     from oracle import oracle as O
     N.init(0)
     torch.cuda.set_device(0)
+    extra = {}
+    if args.workload in ("prefill", "all"):
+        extra["prefill_m512"] = measure_cases(args, N, O, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
+                                              N.ACT_I8, "prefill")
+    if args.workload in ("q8_vocab", "all"):
+        extra["q8_vocab_m1"] = measure_cases(args, N, O, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
+    if args.workload in ("verify", "all"):
+        extra["verify"] = measure_cases(args, N, O, [(d, n, k, m) for d in (1, 2) for n, k in VERIFY_SHAPES[:2]
+                                                     for m in (2, 4, 8, 16)], N.ACT_I8, "verify")
+    if args.workload in ("decode_f32", "all"):
+        extra["decode_f32_bit_exact"] = measure_cases(args, N, O, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
+                                                      N.ACT_F32, "decode_f32")
+    if args.workload not in ("q4_sweep", "all"):
+        print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
+        return
     result, shapes = q4_sweep(args, N, O)
     cpu = None if args.no_cpu_baseline else cpu_baseline_q4(O, shapes)
     line = dict(metric=result["metric"], value=result["value"], unit=result["unit"], n_gpus=1, steps=args.steps,
@@ -223,6 +288,8 @@ def main():
                 scaling="weak", vs_baseline=None, dtype=result["dtype"], data="synthetic (seeded)",
                 config=result["config"], roofline=result["roofline"], cpu_baseline=cpu,
                 per_shape=result["per_shape"])
+    if extra:
+        line["extra"] = extra
     print(json.dumps(line), flush=True)
 
 

@@ -110,6 +110,19 @@ int check_weight(const nnh_weight* w) {
     return NNH_OK;
 }
 
+// The int8 matmul on quantized activations: the GEMV for a few vectors,
+// the MFMA GEMM beyond.
+constexpr size_t GEMM_MIN_TOKENS = 5;
+
+void launch_i8(const nnh_weight* w, const int8_t* q, const double* sx, size_t n_tok, float* y, size_t y_stride,
+               hipStream_t st) {
+    if (n_tok >= GEMM_MIN_TOKENS)
+        nnh::launch_gemm_i8(w->dtype, w->qs, w->sc, w->bi, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride, st);
+    else
+        nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y,
+                            y_stride, st);
+}
+
 // Queue the matmul for device x / y; `scratch` holds xsum or the act buffer.
 int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok, int act,
              uint8_t* scratch, hipStream_t st) {
@@ -128,7 +141,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         uint16_t* s = (uint16_t*)(scratch + l.off_s);
         double* sx = (double*)(scratch + l.off_sx);
         nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, q, s, sx, st);
-        nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, rows, nb, (int)n_tok, y, y_stride, st);
+        launch_i8(w, q, sx, n_tok, y, y_stride, st);
     }
     NNH_HIP(hipGetLastError());
     return NNH_OK;
@@ -365,8 +378,8 @@ int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y
     if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
     ActLayout l = act_layout(w->cols, n_tok);
     const uint8_t* a = (const uint8_t*)act;
-    nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, (const int8_t*)a, (const double*)(a + l.off_sx), (int)w->rows,
-                        (int)w->nb, (int)n_tok, y, n_tok > 1 ? y_stride : w->rows, (hipStream_t)stream);
+    launch_i8(w, (const int8_t*)a, (const double*)(a + l.off_sx), n_tok, y, n_tok > 1 ? y_stride : w->rows,
+              (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;
 }

@@ -76,6 +76,9 @@ void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
                     const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
                     hipStream_t st);
+// int8 MFMA GEMM for many vectors (kernels_gemm.hip).
+void launch_gemm_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
+                    const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
                        hipStream_t st);
 

@@ -273,3 +273,41 @@ def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
         if rows * cols <= 4096 * 4096:
             exact = oracle.gemv_i8_exact(m, qx, sx)
             assert np.all(np.abs(got - exact) <= np.spacing(np.abs(exact)))
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols,n_tok", [
+    (512, 3584, 512),   # Qwen2.5-7B k/v projection, a full 512-token prefill (config 5)
+    (300, 640, 100),    # ragged rows and tokens
+    (1536, 1536, 16),   # Gemma-4-E2B-like verify, M = 16 (config 4)
+    (200, 96, 37),      # nb = 3
+    (129, 6144, 5),     # the smallest GEMM batch, K = 6144
+])
+def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
+    # The MFMA GEMM forms every block dot exactly; each output must be within
+    # one f32 ulp of the oracle's exact sum (any wrong P_b would be far off),
+    # and within the north-star tolerance of nncpu's kernel fed x'.
+    say("gemm", dtype, rows, cols, n_tok)
+    rng = oracle.Rng(0x6E33 + rows + cols + n_tok + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    xs, ys = cols + 32, rows + 7
+    x = rng.normals(n_tok * xs, 1.0)
+    y = np.full(n_tok * ys, 7.0, np.float32)
+    N.gemv_batch(w, x, xs, y, ys, n_tok, N.ACT_I8)
+    deq = []
+    for t in range(n_tok):
+        qx, sx = oracle.quantize_act(x[t * xs:t * xs + cols])
+        exact = oracle.gemv_i8_exact(m, qx, sx)
+        got = y[t * ys:t * ys + rows]
+        assert np.all(np.abs(got - exact) <= np.spacing(np.abs(exact))), t
+        assert np.all(y[t * ys + rows:(t + 1) * ys] == 7.0) or t == n_tok - 1
+        deq.append(oracle.dequant_act(qx, sx))
+    sample = list(range(0, n_tok, max(1, n_tok // 8)))
+    xd = np.concatenate([deq[t] for t in sample])
+    ref = oracle.gemv_batch(m, xd, len(sample), cols, rows)
+    for i, t in enumerate(sample):
+        got = y[t * ys:t * ys + rows]
+        r = ref[i * rows:(i + 1) * rows]
+        assert np.abs(got - r).max() <= 1e-5
+        assert np.linalg.norm(got - r) <= 1e-3 * np.linalg.norm(r)
