@@ -51,12 +51,25 @@ def gemv_bytes(dtype: int, n: int, k: int, m: int = 1) -> int:
     return weight_bytes(dtype, n, k) + 4 * k * m + 4 * n * m
 
 
-def make_weight(O, dtype: int, n: int, k: int, seed: int):
-    """0.02*N(0,1) weights (the reference's test generator, seeded) re-encoded
-    by nncpu's Q8_0 / Q4 encoder (restated in oracle/oracle.cpp)."""
-    rng = O.Rng(seed)
-    w = rng.normals(n * k, 0.02).reshape(n, k)
-    return O.QMatrix.from_f32(dtype, w)
+def make_weights(N, dtype: int, n: int, k: int, seed: int, copies: int, stream: int = 0):
+    """`copies` device weights of 0.02*N(0,1) values (a seeded torch
+    generator on the GPU), each re-encoded by the library's device encoder,
+    which is nncpu's load-time encoder bit for bit."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    w = torch.randn(n * k, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+    torch.cuda.synchronize()
+    ws = [N.Weight.encode_dev(dtype, w.data_ptr(), n, k, stream) for _ in range(copies)]
+    del w
+    return ws
+
+
+def make_x(k: int, m: int, seed: int):
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return torch.randn(m * k, generator=g, device="cuda", dtype=torch.float32)
 
 
 class Stream:
@@ -98,20 +111,20 @@ def time_gemv_set(N, st, launches, steps, warmup):
     return e0.elapsed_time(e1) / 1e3
 
 
-def q4_sweep(args, N, O):
+def q4_sweep(args, N):
     import torch
     st = Stream()
     shapes = Q4_SWEEP
     per_shape = []
+    inputs = []
     all_launch = []
     keep = []
     total_bytes_step = 0
     for i, (n, k) in enumerate(shapes):
-        m = make_weight(O, 2, n, k, 0x5EED01 + i)
         wb = weight_bytes(2, n, k)
         copies = max(2, math.ceil(ROTATE_BYTES / wb))
-        ws = [N.Weight.from_split(2, m.buf, n, k) for _ in range(copies)]
-        x = torch.from_numpy(O.Rng(0xA11 + i).normals(k, 1.0)).cuda()
+        ws = make_weights(N, 2, n, k, 0x5EED01 + i, copies)
+        x = make_x(k, 1, 0xA11 + i)
         _, _, abytes = N.act_layout(k, 1)
         act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
         N.quantize_act_dev(x.data_ptr(), k, k, 1, act.data_ptr(), st.handle)
@@ -127,6 +140,7 @@ def q4_sweep(args, N, O):
         all_launch.append(launch)
         total_bytes_step += gemv_bytes(2, n, k)
         per_shape.append(dict(shape=f"{n}x{k}", copies=copies, bytes=gemv_bytes(2, n, k), launch=launch))
+        inputs.append((ws[0], act, k))
         log(f"shape {n}x{k}: {copies} copies of {wb / 1e6:.1f} MB")
     torch.cuda.synchronize()
 
@@ -158,7 +172,7 @@ def q4_sweep(args, N, O):
                       avg_launch_us=round(kernel_us, 3)),
         per_shape=[{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p.items()} for p in per_shape],
     )
-    return result, shapes
+    return result, inputs
 
 
 QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
@@ -166,7 +180,7 @@ VERIFY_SHAPES = [(6144, 1536), (1536, 6144), (2048, 1536), (1536, 1536)]
 GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912), (262144, 1152)]
 
 
-def measure_cases(args, N, O, cases, act_mode, label):
+def measure_cases(args, N, cases, act_mode, label):
     """Time each (dtype, n, k, m) case alone: `args.steps` launches captured in
     a graph over rotating weight copies (>= 512 MB), inputs resident in HBM.
     act_mode: ACT_I8 times the int8 matmul on pre-quantized activations;
@@ -175,11 +189,10 @@ def measure_cases(args, N, O, cases, act_mode, label):
     st = Stream()
     out = []
     for ci, (dtype, n, k, m) in enumerate(cases):
-        wq = make_weight(O, dtype, n, k, 0x5EED10 + 7 * ci + dtype)
         wb = weight_bytes(dtype, n, k)
         copies = max(2, math.ceil(ROTATE_BYTES / wb))
-        ws = [N.Weight.from_split(dtype, wq.buf, n, k) for _ in range(copies)]
-        x = torch.from_numpy(O.Rng(0xA11 + ci).normals(m * k, 1.0)).cuda()
+        ws = make_weights(N, dtype, n, k, 0x5EED10 + 7 * ci + dtype, copies)
+        x = make_x(k, m, 0xA11 + ci)
         y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
         _, _, abytes = N.act_layout(k, m)
         act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
@@ -210,23 +223,26 @@ def measure_cases(args, N, O, cases, act_mode, label):
     return out
 
 
-def cpu_baseline_q4(O, shapes, budget_s=12.0):
+def cpu_baseline_q4(N, O, inputs, budget_s=12.0):
     """nncpu's AVX2 kernels (restated, oracle/avx2.cpp) on this host's cores,
-    fed the dequantized int8 activations, rotating >= 256 MB of weight copies
-    as the reference's bench_gemv does; best of 3 passes after a warm-up."""
+    on the same weights (downloaded from the GPU) and the same quantized
+    activations (dequantized: the values nncpu's f32 kernel would be fed),
+    rotating >= 256 MB of weight copies as the reference's bench_gemv does;
+    best of 3 passes after a warm-up."""
     if not O.avx_available():
         return None
     threads = min(8, os.cpu_count() or 1)
     O.avx_set_threads(threads)
     tot_bytes, tot_secs, sample = 0, 0.0, []
     t_start = time.time()
-    for i, (n, k) in enumerate(shapes):
-        m = make_weight(O, 2, n, k, 0x5EED01 + i)
-        wb = weight_bytes(2, n, k)
-        copies = max(2, math.ceil((256 << 20) / wb))
+    for w, act, k in inputs:
+        n = w.rows()
+        m = O.QMatrix.from_split(2, n, k, w.download())
+        copies = max(2, math.ceil((256 << 20) / weight_bytes(2, n, k)))
         mats = [m] + [O.QMatrix(2, n, k, tuple(p.copy() for p in m.parts)) for _ in range(copies - 1)]
-        qx, sx = O.quantize_act(O.Rng(0xA11 + i).normals(k, 1.0))
-        xd = O.dequant_act(qx, sx)
+        off_s, _, _ = N.act_layout(k, 1)
+        a = act.cpu().numpy()
+        xd = O.dequant_act(a[:k].view(np.int8), a[off_s:off_s + k // 16].view(np.uint16))
         best = float("inf")
         for rep in range(4):
             t0 = time.perf_counter()
@@ -244,7 +260,8 @@ def cpu_baseline_q4(O, shapes, budget_s=12.0):
     gbs = tot_bytes / tot_secs / 1e9
     return dict(value=round(gbs, 2), unit="GB/s", cores=threads, kind="port",
                 sample="Q4 GEMV M=1 at " + ", ".join(sample) + f"; {threads} threads (nncpu default min(8, CPUs)), "
-                "AVX2 restatement of q4_rows_raw, >=256 MB rotation, best of 3",
+                "AVX2 restatement of q4_rows_raw on the same weights and dequantized int8 activations, "
+                ">=256 MB rotation, best of 3",
                 host_stream_gbs_1thread=round(O.avx_stream_gbs(256 << 20, 2), 1))
 
 
@@ -263,26 +280,28 @@ def main():
         sys.exit(2)
     import torch
     import nncpu_amd as N
-    from oracle import oracle as O
     N.init(0)
     torch.cuda.set_device(0)
     extra = {}
     if args.workload in ("prefill", "all"):
-        extra["prefill_m512"] = measure_cases(args, N, O, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
+        extra["prefill_m512"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
                                               N.ACT_I8, "prefill")
     if args.workload in ("q8_vocab", "all"):
-        extra["q8_vocab_m1"] = measure_cases(args, N, O, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
+        extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
     if args.workload in ("verify", "all"):
-        extra["verify"] = measure_cases(args, N, O, [(d, n, k, m) for d in (1, 2) for n, k in VERIFY_SHAPES[:2]
+        extra["verify"] = measure_cases(args, N, [(d, n, k, m) for d in (1, 2) for n, k in VERIFY_SHAPES[:2]
                                                      for m in (2, 4, 8, 16)], N.ACT_I8, "verify")
     if args.workload in ("decode_f32", "all"):
-        extra["decode_f32_bit_exact"] = measure_cases(args, N, O, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
+        extra["decode_f32_bit_exact"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
                                                       N.ACT_F32, "decode_f32")
     if args.workload not in ("q4_sweep", "all"):
         print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
         return
-    result, shapes = q4_sweep(args, N, O)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_q4(O, shapes)
+    result, inputs = q4_sweep(args, N)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O  # the CPU baseline leg only
+        cpu = cpu_baseline_q4(N, O, inputs)
     line = dict(metric=result["metric"], value=result["value"], unit=result["unit"], n_gpus=1, steps=args.steps,
                 warmup=args.warmup, ms_per_step=round(result["ms_per_step"], 5), higher_is_better=True,
                 scaling="weak", vs_baseline=None, dtype=result["dtype"], data="synthetic (seeded)",

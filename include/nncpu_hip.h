@@ -84,6 +84,16 @@ int nnh_upload_q4(const uint8_t* qs, const uint16_t* scales, const uint16_t* bia
                   nnh_weight** out);
 int nnh_upload(int dtype, const void* data, size_t rows, size_t cols, nnh_weight** out);
 
+/* Encode f32 weights (device memory, rows x cols row-major) with nncpu's
+ * load-time re-encoder (kernels/quant.rs:31-95, as model/load.rs:182-206
+ * calls it), bit for bit, straight into a device weight. Waits for
+ * `stream` first; synchronous. */
+int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weight** out, void* stream);
+
+/* Copy a weight back to the host in nncpu's split layout (`bytes` >= the
+ * layout's size: Q8_0 n + n/16, Q4 n/2 + n/8 for n = rows*cols). */
+int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes);
+
 /* Release a weight (NULL is a no-op). */
 void nnh_free(nnh_weight* w);
 
@@ -118,7 +128,7 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
  * nncpu's Q8_0 encoder, laid out as:
  *   int8_t   q[n_tok][cols]          the quants
  *   uint16_t s[n_tok][cols/32]       the BF16 block scales
- *   float    sx[n_tok][cols/32][2]   {bf16(s) as f32, s * sum(q of block)}
+ *   double   sx[n_tok][cols/32][2]   {bf16(s), s * sum(q of block)}, both exact
  * at the offsets nnh_act_layout() reports. */
 int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes);
 

@@ -80,6 +80,24 @@ class Weight:
         check(lib().nnh_upload_q4(_ptr(qs), _ptr(scales), _ptr(biases), rows, cols, C.byref(h)))
         return cls(h, Q4S, rows, cols)
 
+    @classmethod
+    def encode_dev(cls, dtype: int, w_ptr: int, rows: int, cols: int, stream: int = 0) -> "Weight":
+        """Encode f32 weights already in device memory with nncpu's re-encoder
+        (kernels/quant.rs:31-95) on the device."""
+        h = C.c_void_p()
+        check(lib().nnh_encode_dev(dtype, w_ptr, rows, cols, C.byref(h), stream or None))
+        return cls(h, dtype, rows, cols)
+
+    def split_bytes(self) -> int:
+        n = self._rows * self._cols
+        return n + n // 16 if self.dtype == Q8_0 else n // 2 + n // 8
+
+    def download(self) -> np.ndarray:
+        """The weight in nncpu's split layout, as host bytes."""
+        out = np.empty(self.split_bytes(), np.uint8)
+        check(lib().nnh_weight_download(self.handle, _ptr(out), out.size))
+        return out
+
     def rows(self) -> int:
         """Rows: the output length of a gemv over this matrix (runtime.rs:103-107)."""
         return self._rows

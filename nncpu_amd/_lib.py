@@ -67,6 +67,8 @@ def _declare(L):
     L.nnh_upload_q4.argtypes, L.nnh_upload_q4.restype = [vp, vp, vp, sz, sz, P(vp)], i32
     L.nnh_upload.argtypes, L.nnh_upload.restype = [i32, vp, sz, sz, P(vp)], i32
     L.nnh_free.argtypes, L.nnh_free.restype = [vp], None
+    L.nnh_encode_dev.argtypes, L.nnh_encode_dev.restype = [i32, vp, sz, sz, P(vp), vp], i32
+    L.nnh_weight_download.argtypes, L.nnh_weight_download.restype = [vp, vp, sz], i32
     L.nnh_weight_info.argtypes, L.nnh_weight_info.restype = [vp, P(i32), P(sz), P(sz)], i32
     L.nnh_model_gemv.argtypes, L.nnh_model_gemv.restype = [vp, vp, vp, i32], i32
     L.nnh_gemv_batch.argtypes, L.nnh_gemv_batch.restype = [vp, vp, sz, vp, sz, sz, i32], i32

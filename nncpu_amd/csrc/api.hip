@@ -162,61 +162,90 @@ int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_t
     return NNH_OK;
 }
 
-int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size_t rows, size_t cols,
-                 nnh_weight** out) {
-    if (!out) return fail(NNH_E_INVALID, "nnh_upload: null out");
-    *out = nullptr;
-    if (dtype != NNH_Q8_0 && dtype != NNH_Q4S) return fail(NNH_E_INVALID, "nnh_upload: unknown dtype");
-    if (!qs || !sc || (dtype == NNH_Q4S && !bi)) return fail(NNH_E_INVALID, "nnh_upload: null data");
-    if (rows == 0 || cols == 0) return fail(NNH_E_INVALID, "nnh_upload: empty matrix");
-    if (cols % 32 != 0) return fail(NNH_E_INVALID, "nnh_upload: cols is not a multiple of 32");
+int check_shape(int dtype, size_t rows, size_t cols) {
+    if (dtype != NNH_Q8_0 && dtype != NNH_Q4S) return fail(NNH_E_INVALID, "unknown dtype");
+    if (rows == 0 || cols == 0) return fail(NNH_E_INVALID, "empty matrix");
+    if (cols % 32 != 0) return fail(NNH_E_INVALID, "cols is not a multiple of 32");
     if (rows >= ((size_t)1 << 31) || cols >= ((size_t)1 << 31) || rows > ((size_t)1 << 62) / cols)
-        return fail(NNH_E_INVALID, "nnh_upload: matrix too large");
-    std::lock_guard<std::mutex> g(g_mu);
-    int rc = ensure_locked();
-    if (rc) return rc;
+        return fail(NNH_E_INVALID, "matrix too large");
+    return NNH_OK;
+}
+
+size_t raw_bytes_of(int dtype, size_t rows, size_t cols) {
+    const size_t n = rows * cols;
+    return dtype == NNH_Q8_0 ? n + n / 16 : n / 2 + n / 8;
+}
+
+void release(nnh_weight* w) {
+    if (w->raw) (void)hipFree(w->raw);
+    if (w->fq) (void)hipFree(w->fq);
+    if (w->fs) (void)hipFree(w->fs);
+    if (w->sb) (void)hipFree(w->sb);
+    delete w;
+}
+
+// Allocate a weight's device buffers; caller holds g_mu.
+int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     const size_t n = rows * cols, nb = cols / 32;
     const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2;
-    const size_t tbytes = (n / 32) * 2;
-    const size_t raw_bytes = qbytes + tbytes * (dtype == NNH_Q8_0 ? 1 : 2);
     const size_t group = dtype == NNH_Q8_0 ? 8 : 16;
-    const size_t nbp = (nb + group - 1) / group * group;
-
     nnh_weight* w = new nnh_weight();
     w->dtype = dtype;
     w->device = g_device;
     w->rows = rows;
     w->cols = cols;
     w->nb = nb;
-    w->nbp = nbp;
-    auto cleanup = [&](int code) {
-        if (w->raw) (void)hipFree(w->raw);
-        if (w->fq) (void)hipFree(w->fq);
-        if (w->fs) (void)hipFree(w->fs);
-        if (w->sb) (void)hipFree(w->sb);
-        delete w;
-        return code;
-    };
+    w->nbp = (nb + group - 1) / group * group;
     hipError_t e;
-    if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes))) != hipSuccess ||
+    if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
         (e = hipMalloc((void**)&w->fq, align_up(qbytes))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->fs, align_up(rows * nbp * 2))) != hipSuccess ||
+        (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
         (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess)) {
-        return cleanup(fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
-                            std::string("nnh_upload: ") + hipGetErrorString(e)));
+        release(w);
+        return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE, std::string("weight alloc: ") + hipGetErrorString(e));
     }
     w->qs = w->raw;
     w->sc = (const uint16_t*)(w->raw + qbytes);
-    w->bi = dtype == NNH_Q4S ? (const uint16_t*)(w->raw + qbytes + tbytes) : nullptr;
+    w->bi = dtype == NNH_Q4S ? (const uint16_t*)(w->raw + qbytes + (n / 32) * 2) : nullptr;
+    *out = w;
+    return NNH_OK;
+}
+
+// Build the derived layouts from `raw` and wait; caller holds g_mu.
+int finalize_weight(nnh_weight* w) {
+    nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, g_stream);
+    if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
+    hipError_t e;
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
+        return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
+    return NNH_OK;
+}
+
+int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size_t rows, size_t cols,
+                 nnh_weight** out) {
+    if (!out) return fail(NNH_E_INVALID, "nnh_upload: null out");
+    *out = nullptr;
+    int rc = check_shape(dtype, rows, cols);
+    if (rc) return rc;
+    if (!qs || !sc || (dtype == NNH_Q4S && !bi)) return fail(NNH_E_INVALID, "nnh_upload: null data");
+    std::lock_guard<std::mutex> g(g_mu);
+    if ((rc = ensure_locked())) return rc;
+    nnh_weight* w;
+    if ((rc = alloc_weight(dtype, rows, cols, &w))) return rc;
+    const size_t n = rows * cols;
+    const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2, tbytes = (n / 32) * 2;
+    hipError_t e;
     if ((e = hipMemcpyAsync(w->raw, qs, qbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
         (e = hipMemcpyAsync(w->raw + qbytes, sc, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
         (dtype == NNH_Q4S &&
-         (e = hipMemcpyAsync(w->raw + qbytes + tbytes, bi, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess))
-        return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: copy: ") + hipGetErrorString(e)));
-    nnh::launch_relayout_f32(dtype, w->qs, w->sc, w->fq, w->fs, (int)rows, (int)nb, (int)nbp, g_stream);
-    if (dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, rows * nb, g_stream);
-    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
-        return cleanup(fail(NNH_E_DEVICE, std::string("nnh_upload: relayout: ") + hipGetErrorString(e)));
+         (e = hipMemcpyAsync(w->raw + qbytes + tbytes, bi, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess)) {
+        release(w);
+        return fail(NNH_E_DEVICE, std::string("nnh_upload: copy: ") + hipGetErrorString(e));
+    }
+    if ((rc = finalize_weight(w))) {
+        release(w);
+        return rc;
+    }
     *out = w;
     return NNH_OK;
 }
@@ -255,11 +284,39 @@ void nnh_free(nnh_weight* w) {
     std::lock_guard<std::mutex> g(g_mu);
     (void)hipSetDevice(w->device);
     (void)hipDeviceSynchronize();
-    (void)hipFree(w->raw);
-    (void)hipFree(w->fq);
-    (void)hipFree(w->fs);
-    (void)hipFree(w->sb);
-    delete w;
+    release(w);
+}
+
+int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weight** out, void* stream) {
+    if (!out) return fail(NNH_E_INVALID, "nnh_encode_dev: null out");
+    *out = nullptr;
+    int rc = check_shape(dtype, rows, cols);
+    if (rc) return rc;
+    if (!w) return fail(NNH_E_INVALID, "nnh_encode_dev: null weights");
+    std::lock_guard<std::mutex> g(g_mu);
+    if ((rc = ensure_locked())) return rc;
+    NNH_HIP(hipStreamSynchronize((hipStream_t)stream));  // w may come from work queued on `stream`
+    nnh_weight* d;
+    if ((rc = alloc_weight(dtype, rows, cols, &d))) return rc;
+    nnh::launch_encode(dtype, w, rows * cols, d->raw, (uint16_t*)d->sc, (uint16_t*)d->bi, g_stream);
+    if ((rc = finalize_weight(d))) {
+        release(d);
+        return rc;
+    }
+    *out = d;
+    return NNH_OK;
+}
+
+int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes) {
+    if (!w || !data) return fail(NNH_E_INVALID, "nnh_weight_download: null pointer");
+    const size_t need = raw_bytes_of(w->dtype, w->rows, w->cols);
+    if (bytes < need) return fail(NNH_E_INVALID, "nnh_weight_download: buffer too small");
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    NNH_HIP(hipMemcpyAsync(data, w->raw, need, hipMemcpyDeviceToHost, g_stream));
+    NNH_HIP(hipStreamSynchronize(g_stream));
+    return NNH_OK;
 }
 
 int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols) {

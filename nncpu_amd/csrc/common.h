@@ -76,6 +76,8 @@ void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
                     const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
                     hipStream_t st);
+// f32 -> Q8_0 / Q4 split layout on the device (kernels_encode.hip).
+void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* sc, uint16_t* bi, hipStream_t st);
 // int8 MFMA GEMM for many vectors (kernels_gemm.hip).
 void launch_gemm_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
                     const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);

@@ -159,6 +159,18 @@ class QMatrix:
         parts = quantize_q8_0(w) if dtype == Q8_0 else quantize_q4(w)
         return QMatrix(dtype, rows, cols, parts)
 
+    @staticmethod
+    def from_split(dtype: int, rows: int, cols: int, buf: np.ndarray) -> "QMatrix":
+        """Wrap bytes in the split layout (runtime.rs:136-164)."""
+        buf = np.ascontiguousarray(buf).view(np.uint8)
+        n = rows * cols
+        if dtype == Q8_0:
+            parts = (buf[:n].view(np.int8), buf[n:n + n // 16].view(np.uint16))
+        else:
+            parts = (buf[:n // 2], buf[n // 2:n // 2 + n // 16].view(np.uint16),
+                     buf[n // 2 + n // 16:n // 2 + n // 8].view(np.uint16))
+        return QMatrix(dtype, rows, cols, parts)
+
     def dequant(self) -> np.ndarray:
         """f32 weights the kernels multiply by (kernels/tests.rs:380-397)."""
         if self.dtype == Q8_0:

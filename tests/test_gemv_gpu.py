@@ -311,3 +311,51 @@ def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
         r = ref[i * rows:(i + 1) * rows]
         assert np.abs(got - r).max() <= 1e-5
         assert np.linalg.norm(got - r) <= 1e-3 * np.linalg.norm(r)
+
+
+# ---- device re-encoder (kernels/quant.rs:31-95 on the GPU) ----------------------------
+
+def encode_on_device(dtype, w, rows, cols):
+    import torch
+    dw = torch_dev(np.ascontiguousarray(w, np.float32).ravel())
+    return N.Weight.encode_dev(dtype, dw.data_ptr(), rows, cols)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_device_encoder_bit_exact(oracle, dtype):
+    rng = oracle.Rng(0xE7C0 + dtype)
+    rows, cols = 333, 1152
+    w = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+    # Edge blocks: signed zeros (first occurrence wins for Q4 lo/hi), flat,
+    # all zero, NaN in b[0] and elsewhere, large values, reciprocal ties.
+    w[0, :32] = 0.0
+    w[0, 5] = -0.0
+    w[1, :32] = np.where(np.arange(32) % 2 == 0, -0.0, 0.0)
+    w[2, :32] = 3.5
+    w[3, 0] = np.nan
+    w[4, 7] = np.nan
+    w[5, :32] = rng.vec(32, -3e4, 3e4)
+    w[6, :32] = 0.0
+    w[6, 3] = np.array([0x3FFEFE01], np.uint32).view(np.float32)[0]
+    w[7, :32] = 0.0
+    w[7, 9] = np.array([0x3F895800], np.uint32).view(np.float32)[0]
+    w[8, 32:64] = -1.0
+    w[8, 40] = 2.0
+    dev = encode_on_device(dtype, w, rows, cols)
+    got = dev.download()
+    want = oracle.QMatrix.from_f32(dtype, w).buf
+    assert got.size == want.size
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_device_encoded_weight_matmul(oracle, dtype):
+    # The encoded weight is a complete weight: its f32 matmul matches the
+    # oracle bit for bit.
+    rng = oracle.Rng(0xE7C5 + dtype)
+    rows, cols = 1024, 4096
+    w = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+    dev = encode_on_device(dtype, w, rows, cols)
+    m = oracle.QMatrix.from_f32(dtype, w)
+    x = rng.normals(cols, 1.0)
+    assert np.array_equal(bits(N.model_gemv(dev, x)), bits(oracle.gemv_batch(m, x)))
