@@ -1,0 +1,121 @@
+"""Gemma-3 decode through the GPU matmul.
+
+A Gemma-3-architecture model with seeded random weights: every weight matrix
+is 0.02*N(0,1) (a seeded torch generator on the GPU), re-encoded to nncpu's
+Q8_0 layout by the library's device encoder (nncpu's load-time encoder, bit
+for bit), norms 1 + 0.1*N(0,1). The forward pass is nncpu's
+(nncpu_amd/host/gemma3.cpp, restating crates/nncpu/src/model/forward.rs) on
+the CPU; its weight matmuls run through `nnh_gemv_batch` in the bit-exact
+f32 mode and the greedy lm_head through `nnh_model_argmax`. The prompt is
+evaluated in 16-token batches (session/engine.rs:362-380, PREFILL_BATCH).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import ACT_F32, Q8_0, Weight, check, lib
+from ._lib import _PKG
+
+GEMMA_LIB = os.path.join(_PKG, "lib", "libnncpu_gemma.so")
+
+
+class NngConfig(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int), ("n_kv", C.c_int),
+                ("head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
+                ("rms_eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
+                ("attn_scale", C.c_float), ("window", C.c_int), ("swa_period", C.c_int)]
+
+
+class NngGpuCtx(C.Structure):
+    _fields_ = [("w", C.POINTER(C.c_void_p)), ("n", C.c_int), ("act", C.c_int)]
+
+
+def gemma3_1b_config(n_ctx: int = 256, n_layer: int = 26, n_vocab: int = 262144) -> NngConfig:
+    """Gemma-3-1B's architecture (26 layers, d 1152, FFN 6912, 4 query heads /
+    1 KV head, head_dim 256, vocab 262144, sliding window 512 with every 6th
+    layer global, RoPE bases 1e6 / 1e4, attention scale 1/16)."""
+    return NngConfig(n_layer=n_layer, n_embd=1152, n_head=4, n_kv=1, head_dim=256, n_ff=6912, n_vocab=n_vocab,
+                     n_ctx=n_ctx, rms_eps=1e-6, rope_base=1e6, rope_base_swa=1e4, attn_scale=1.0 / 16.0,
+                     window=512, swa_period=6)
+
+
+def matrix_shapes(cfg: NngConfig) -> list[tuple[int, int]]:
+    """(rows, cols) of matrix id = 7*layer + {q, k, v, o, gate, up, down}; the tied lm_head last."""
+    E, hd, ff = cfg.n_embd, cfg.head_dim, cfg.n_ff
+    per = [(cfg.n_head * hd, E), (cfg.n_kv * hd, E), (cfg.n_kv * hd, E), (E, cfg.n_head * hd),
+           (ff, E), (ff, E), (E, ff)]
+    return per * cfg.n_layer + [(cfg.n_vocab, E)]
+
+
+def _gemma_lib():
+    L = C.CDLL(GEMMA_LIB)
+    L.nng_create.argtypes = [C.POINTER(NngConfig), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.nng_create.restype = C.c_void_p
+    L.nng_free.argtypes = [C.c_void_p]
+    L.nng_error.argtypes, L.nng_error.restype = [C.c_void_p], C.c_char_p
+    L.nng_generate.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p,
+                               C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    L.nng_generate.restype = C.c_int
+    return L
+
+
+class Gemma3:
+    """Device weights of a seeded random Gemma-3 model, plus the host copies
+    (norms, the Q8_0 embedding table) the CPU forward reads."""
+
+    def __init__(self, cfg: NngConfig, seed: int = 0x6E33A):
+        import torch
+        self.cfg = cfg
+        self.shapes = matrix_shapes(cfg)
+        self.weights: list[Weight] = []
+        g = torch.Generator(device="cuda")
+        for i, (r, c) in enumerate(self.shapes):
+            g.manual_seed(seed + i)
+            w = torch.randn(r * c, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+            torch.cuda.synchronize()
+            self.weights.append(Weight.encode_dev(Q8_0, w.data_ptr(), r, c))
+            del w
+        rng = np.random.default_rng(seed)
+        E, hd = cfg.n_embd, cfg.head_dim
+        n_norm = (4 * E + 2 * hd) * cfg.n_layer + E
+        self.norms = (1.0 + 0.1 * rng.standard_normal(n_norm)).astype(np.float32)
+        self.token_embd = self.weights[-1].download()  # the tied embedding / lm_head table
+        self._lib = _gemma_lib()
+
+    def generate(self, prompt: np.ndarray, n_gen: int, gemv_ptr: int, argmax_ptr: int | None, ctx,
+                 batch: int = 16):
+        """(tokens, per-layer hashes, prefill seconds, decode seconds)."""
+        L = self._lib
+        m = L.nng_create(C.byref(self.cfg), self.norms.ctypes.data_as(C.c_void_p),
+                         self.token_embd.ctypes.data_as(C.c_void_p), gemv_ptr, argmax_ptr, C.cast(ctx, C.c_void_p))
+        try:
+            prompt = np.ascontiguousarray(prompt, np.int32)
+            out = np.zeros(n_gen, np.int32)
+            n_fwd = (len(prompt) + batch - 1) // batch + n_gen
+            hashes = np.zeros(n_fwd * self.cfg.n_layer, np.uint64)
+            nh, tp, td = C.c_size_t(), C.c_double(), C.c_double()
+            rc = L.nng_generate(m, prompt.ctypes.data_as(C.c_void_p), len(prompt), batch, n_gen,
+                                out.ctypes.data_as(C.c_void_p), hashes.ctypes.data_as(C.c_void_p), C.byref(nh),
+                                C.byref(tp), C.byref(td))
+            if rc != 0:
+                raise RuntimeError(L.nng_error(m).decode())
+            return out, hashes[:nh.value], tp.value, td.value
+        finally:
+            L.nng_free(m)
+
+    def generate_gpu(self, prompt: np.ndarray, n_gen: int, act: int = ACT_F32):
+        """The decode run with every matmul on the GPU."""
+        arr = (C.c_void_p * len(self.weights))(*[w.handle for w in self.weights])
+        ctx = NngGpuCtx(w=C.cast(arr, C.POINTER(C.c_void_p)), n=len(self.weights), act=act)
+        self._keep = (arr, ctx)
+        gemv = C.cast(self._lib.nng_gpu_gemv, C.c_void_p).value
+        argmax = C.cast(self._lib.nng_gpu_argmax, C.c_void_p).value
+        return self.generate(prompt, n_gen, gemv, argmax, C.pointer(ctx))
+
+
+def random_prompt(n: int, n_vocab: int, seed: int = 0x9A0) -> np.ndarray:
+    """A uniform-random prompt of n token ids."""
+    return np.random.default_rng(seed).integers(0, n_vocab, n).astype(np.int32)

@@ -372,6 +372,22 @@ int avx_gemv_batch(int dtype, const void* w, size_t rows, size_t cols, const flo
     return -1;
 }
 
+// A gemv callback for the Gemma-3 harness (nncpu_amd/host/gemma3.cpp):
+// matrix `id` of a table of split-layout buffers, on the AVX2 restatement.
+struct or_model_table {
+    int n, dtype;
+    const void* const* bufs;
+    const size_t* rows;
+    const size_t* cols;
+};
+
+int or_model_gemv_cb(void* ctx, int id, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok) {
+    const or_model_table* t = (const or_model_table*)ctx;
+    if (id < 0 || id >= t->n) return 1;
+    return avx_gemv_batch(t->dtype, t->bufs[id], t->rows[id], t->cols[id], x, x_stride, y,
+                          n_tok > 1 ? y_stride : t->rows[id], n_tok) != 0;
+}
+
 // The reference's "load-only roofline" calibration (kernels/tests.rs:1306-1321):
 // one thread streams a buffer with almost no work per byte; best of reps.
 __attribute__((target("avx2,fma"))) double avx_stream_gbs(size_t bytes, int reps) {

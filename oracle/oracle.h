@@ -47,4 +47,5 @@ int avx_threads(void);
 int avx_gemv_batch(int dtype, const void* w, size_t rows, size_t cols, const float* x, size_t x_stride, float* y,
                    size_t y_stride, size_t n_tok);
 double avx_stream_gbs(size_t bytes, int reps);
+int or_model_gemv_cb(void* ctx, int id, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok);
 }
