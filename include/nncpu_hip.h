@@ -129,7 +129,10 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
  *   int8_t   q[n_tok][cols]          the quants
  *   uint16_t s[n_tok][cols/32]       the BF16 block scales
  *   double   sx[n_tok][cols/32][2]   {bf16(s), s * sum(q of block)}, both exact
- * at the offsets nnh_act_layout() reports. */
+ *   float    sxT[2][cols/32][P]      the same two values block-major, for the
+ *                                    MFMA GEMM (P = n_tok rounded up to 128)
+ * at the offsets nnh_act_layout() reports (sxT follows sx); `bytes` is the
+ * whole buffer. */
 int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes);
 
 /* Quantize n_tok f32 vectors (device, x_stride apart) into `act`. */

@@ -24,6 +24,7 @@ struct nnh_weight {
     uint32_t* sb;         // device: Q4 scale | bias << 16 per block (int8 path)
     uint8_t* fq;          // device: per-lane quant groups for the f32 path
     uint16_t* fs;         // device: scales padded to nbp per row
+    float* swT;           // device: [nb][rows padded] f32 scales, Q4 biases after (MFMA GEMM)
 };
 
 namespace {
@@ -92,15 +93,18 @@ int scratch_locked(size_t bytes, uint8_t** out) {
 }
 
 struct ActLayout {
-    size_t off_s, off_sx, bytes;
+    size_t off_s, off_sx, off_sxT, bytes;
 };
 
+// q[n_tok][cols] i8, s[n_tok][nb] bf16, sx[n_tok][nb][2] f64, then the
+// GEMM's block-major copies sxT[2][nb][tok_pad] f32.
 ActLayout act_layout(size_t cols, size_t n_tok) {
     size_t nb = cols / 32;
     ActLayout l;
     l.off_s = align_up(n_tok * cols);
     l.off_sx = l.off_s + align_up(n_tok * nb * 2);
-    l.bytes = l.off_sx + align_up(n_tok * nb * 16);
+    l.off_sxT = l.off_sx + align_up(n_tok * nb * 16);
+    l.bytes = l.off_sxT + align_up(2 * nb * (size_t)nnh::gemm_tok_pad((int)n_tok) * 4);
     return l;
 }
 
@@ -114,10 +118,13 @@ int check_weight(const nnh_weight* w) {
 // the MFMA GEMM beyond.
 constexpr size_t GEMM_MIN_TOKENS = 5;
 
-void launch_i8(const nnh_weight* w, const int8_t* q, const double* sx, size_t n_tok, float* y, size_t y_stride,
-               hipStream_t st) {
+void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, size_t y_stride, hipStream_t st) {
+    const ActLayout l = act_layout(w->cols, n_tok);
+    const int8_t* q = (const int8_t*)act;
+    const double* sx = (const double*)(act + l.off_sx);
     if (n_tok >= GEMM_MIN_TOKENS)
-        nnh::launch_gemm_i8(w->dtype, w->qs, w->sc, w->bi, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride, st);
+        nnh::launch_gemm_i8(w->dtype, w->qs, w->swT, q, (const float*)(act + l.off_sxT), (int)w->rows, (int)w->nb,
+                            (int)n_tok, y, y_stride, st);
     else
         nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y,
                             y_stride, st);
@@ -136,12 +143,11 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
                              y, y_stride, st);
     } else {
-        ActLayout l = act_layout(w->cols, n_tok);
-        int8_t* q = (int8_t*)scratch;
-        uint16_t* s = (uint16_t*)(scratch + l.off_s);
-        double* sx = (double*)(scratch + l.off_sx);
-        nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, q, s, sx, st);
-        launch_i8(w, q, sx, n_tok, y, y_stride, st);
+        const ActLayout l = act_layout(w->cols, n_tok);
+        nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, (int8_t*)scratch, (uint16_t*)(scratch + l.off_s),
+                                 (double*)(scratch + l.off_sx), (float*)(scratch + l.off_sxT),
+                                 nnh::gemm_tok_pad((int)n_tok), st);
+        launch_i8(w, scratch, n_tok, y, y_stride, st);
     }
     NNH_HIP(hipGetLastError());
     return NNH_OK;
@@ -181,6 +187,7 @@ void release(nnh_weight* w) {
     if (w->fq) (void)hipFree(w->fq);
     if (w->fs) (void)hipFree(w->fs);
     if (w->sb) (void)hipFree(w->sb);
+    if (w->swT) (void)hipFree(w->swT);
     delete w;
 }
 
@@ -200,7 +207,9 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
         (e = hipMalloc((void**)&w->fq, align_up(qbytes))) != hipSuccess ||
         (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
-        (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess)) {
+        (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||
+        (e = hipMalloc((void**)&w->swT, align_up((size_t)nnh::gemm_rows_pad((int)rows) * nb * 4 *
+                                                  (dtype == NNH_Q4S ? 2 : 1)))) != hipSuccess) {
         release(w);
         return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE, std::string("weight alloc: ") + hipGetErrorString(e));
     }
@@ -215,6 +224,7 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
 int finalize_weight(nnh_weight* w) {
     nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, g_stream);
     if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
+    nnh::launch_gemm_scales(w->sc, w->bi, w->swT, (int)w->rows, (int)w->nb, g_stream);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
         return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
@@ -421,7 +431,8 @@ int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_
     ActLayout l = act_layout(cols, n_tok);
     uint8_t* a = (uint8_t*)act;
     nnh::launch_quantize_act(x, n_tok > 1 ? x_stride : cols, (int)cols, (int)n_tok, (int8_t*)a,
-                             (uint16_t*)(a + l.off_s), (double*)(a + l.off_sx), (hipStream_t)stream);
+                             (uint16_t*)(a + l.off_s), (double*)(a + l.off_sx), (float*)(a + l.off_sxT),
+                             nnh::gemm_tok_pad((int)n_tok), (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;
 }
@@ -433,10 +444,7 @@ int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y
     if ((rc = check_call(w, 0, y_stride, n_tok, NNH_ACT_I8))) return rc;
     if (n_tok == 0) return NNH_OK;
     if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
-    ActLayout l = act_layout(w->cols, n_tok);
-    const uint8_t* a = (const uint8_t*)act;
-    launch_i8(w, (const int8_t*)a, (const double*)(a + l.off_sx), n_tok, y, n_tok > 1 ? y_stride : w->rows,
-              (hipStream_t)stream);
+    launch_i8(w, (const uint8_t*)act, n_tok, y, n_tok > 1 ? y_stride : w->rows, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;
 }

@@ -71,7 +71,7 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
 
 // int8 path (kernels_i8.hip).
 void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
-                         hipStream_t st);
+                         float* sxT, int tok_pad, hipStream_t st);
 void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st);
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
                     const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
@@ -79,8 +79,11 @@ void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const 
 // f32 -> Q8_0 / Q4 split layout on the device (kernels_encode.hip).
 void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* sc, uint16_t* bi, hipStream_t st);
 // int8 MFMA GEMM for many vectors (kernels_gemm.hip).
-void launch_gemm_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const int8_t* aq,
-                    const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);
+int gemm_rows_pad(int rows);
+int gemm_tok_pad(int n_tok);
+void launch_gemm_scales(const uint16_t* sc, const uint16_t* bi, float* swT, int rows, int nb, hipStream_t st);
+void launch_gemm_i8(int dtype, const uint8_t* qs, const float* swT, const int8_t* aq, const float* sxT, int rows,
+                    int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
                        hipStream_t st);
 

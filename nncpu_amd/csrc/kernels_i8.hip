@@ -31,7 +31,8 @@ __device__ __forceinline__ int rint_sat(float v) {
 // One 32-lane half-wave per block of 32 values.
 __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, size_t x_stride, int cols,
                                                            int n_tok, int8_t* __restrict__ q,
-                                                           uint16_t* __restrict__ s, double* __restrict__ sx) {
+                                                           uint16_t* __restrict__ s, double* __restrict__ sx,
+                                                           float* __restrict__ sxT, int tok_pad) {
     const int nb = cols >> 5;
     const int k = threadIdx.x & 31;
     const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
@@ -60,6 +61,11 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restri
         s[(size_t)t * nb + b] = (uint16_t)sbits;
         sx[2 * ((size_t)t * nb + b)] = (double)scale;
         sx[2 * ((size_t)t * nb + b) + 1] = (double)scale * (double)qsum;  // exact: s_x * sum(q_x)
+        // Block-major f32 copies for the GEMM: [b][tok_pad] scale, then [b][tok_pad] scale * sum(q).
+        if (sxT) {
+            sxT[(size_t)b * tok_pad + t] = scale;
+            sxT[(size_t)nb * tok_pad + (size_t)b * tok_pad + t] = scale * (float)qsum;  // exact: 8 + 13 bits
+        }
     }
 }
 
@@ -362,9 +368,9 @@ void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t
 }
 
 void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
-                         hipStream_t st) {
+                         float* sxT, int tok_pad, hipStream_t st) {
     int blocks = (cols / 32) * n_tok;
-    quantize_act_kernel<<<ceil_div(blocks, 8), 256, 0, st>>>(x, x_stride, cols, n_tok, q, s, sx);
+    quantize_act_kernel<<<ceil_div(blocks, 8), 256, 0, st>>>(x, x_stride, cols, n_tok, q, s, sx, sxT, tok_pad);
 }
 
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
