@@ -139,7 +139,9 @@ int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, siz
 int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream);
 
 /* y (device, y_stride apart) = W x for activations already in `act`: the
- * int8 path without the quantization step. */
+ * int8 path without the quantization step. Batches of 5 or more vectors on
+ * small matrices keep split-K partial sums in the library's scratch buffer:
+ * calls on different streams must not overlap. */
 int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream);
 
 /* Diagnostics: the exact int32 block dot products P[n][r][b] =

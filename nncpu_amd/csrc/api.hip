@@ -118,13 +118,19 @@ int check_weight(const nnh_weight* w) {
 // the MFMA GEMM beyond.
 constexpr size_t GEMM_MIN_TOKENS = 5;
 
-void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, size_t y_stride, hipStream_t st) {
+// Device workspace the int8 matmul needs beyond the activation buffer.
+size_t i8_workspace_bytes(const nnh_weight* w, size_t n_tok) {
+    return n_tok >= GEMM_MIN_TOKENS ? nnh::gemm_workspace_bytes((int)w->rows, (int)w->nb, (int)n_tok) : 0;
+}
+
+void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, size_t y_stride, uint8_t* ws,
+               hipStream_t st) {
     const ActLayout l = act_layout(w->cols, n_tok);
     const int8_t* q = (const int8_t*)act;
     const double* sx = (const double*)(act + l.off_sx);
     if (n_tok >= GEMM_MIN_TOKENS)
         nnh::launch_gemm_i8(w->dtype, w->qs, w->swT, q, (const float*)(act + l.off_sxT), (int)w->rows, (int)w->nb,
-                            (int)n_tok, y, y_stride, st);
+                            (int)n_tok, y, y_stride, (double*)ws, st);
     else
         nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y,
                             y_stride, st);
@@ -147,7 +153,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, (int8_t*)scratch, (uint16_t*)(scratch + l.off_s),
                                  (double*)(scratch + l.off_sx), (float*)(scratch + l.off_sxT),
                                  nnh::gemm_tok_pad((int)n_tok), st);
-        launch_i8(w, scratch, n_tok, y, y_stride, st);
+        launch_i8(w, scratch, n_tok, y, y_stride, scratch + l.bytes, st);
     }
     NNH_HIP(hipGetLastError());
     return NNH_OK;
@@ -155,7 +161,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
 
 size_t gemv_scratch_bytes(const nnh_weight* w, size_t n_tok, int act) {
     if (act == NNH_ACT_F32) return w->dtype == NNH_Q4S ? align_up(n_tok * w->nb * 4) : 0;
-    return act_layout(w->cols, n_tok).bytes;
+    return act_layout(w->cols, n_tok).bytes + i8_workspace_bytes(w, n_tok);
 }
 
 int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_tok, int act) {
@@ -444,7 +450,10 @@ int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y
     if ((rc = check_call(w, 0, y_stride, n_tok, NNH_ACT_I8))) return rc;
     if (n_tok == 0) return NNH_OK;
     if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
-    launch_i8(w, (const uint8_t*)act, n_tok, y, n_tok > 1 ? y_stride : w->rows, (hipStream_t)stream);
+    uint8_t* ws = nullptr;
+    const size_t wsb = i8_workspace_bytes(w, n_tok);
+    if (wsb && (rc = scratch_locked(wsb, &ws))) return rc;
+    launch_i8(w, (const uint8_t*)act, n_tok, y, n_tok > 1 ? y_stride : w->rows, ws, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;
 }

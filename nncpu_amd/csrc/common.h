@@ -82,8 +82,9 @@ void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* s
 int gemm_rows_pad(int rows);
 int gemm_tok_pad(int n_tok);
 void launch_gemm_scales(const uint16_t* sc, const uint16_t* bi, float* swT, int rows, int nb, hipStream_t st);
+size_t gemm_workspace_bytes(int rows, int nb, int n_tok);  // split-K partials; 0 if unsplit
 void launch_gemm_i8(int dtype, const uint8_t* qs, const float* swT, const int8_t* aq, const float* sxT, int rows,
-                    int nb, int n_tok, float* y, size_t y_stride, hipStream_t st);
+                    int nb, int n_tok, float* y, size_t y_stride, double* ws, hipStream_t st);
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
                        hipStream_t st);
 

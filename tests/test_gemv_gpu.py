@@ -282,6 +282,7 @@ def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
     (1536, 1536, 16),   # Gemma-4-E2B-like verify, M = 16 (config 4)
     (200, 96, 37),      # nb = 3
     (129, 6144, 5),     # the smallest GEMM batch, K = 6144
+    (1536, 64, 2048),   # 192 tiles: the unsplit path, nb = 2 (one partial chunk)
 ])
 def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
     # The MFMA GEMM forms every block dot exactly; each output must be within
