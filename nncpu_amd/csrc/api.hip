@@ -114,13 +114,16 @@ int check_weight(const nnh_weight* w) {
     return NNH_OK;
 }
 
-// The int8 matmul on quantized activations: the GEMV for a few vectors,
-// the MFMA GEMM beyond.
-constexpr size_t GEMM_MIN_TOKENS = 5;
+// The int8 matmul on quantized activations: the sdot4 GEMV for up to 4
+// vectors, the few-token MFMA kernel up to 16, the MFMA GEMM beyond.
+constexpr size_t SKINNY_MIN_TOKENS = 5;
+constexpr size_t GEMM_MIN_TOKENS = 17;
 
 // Device workspace the int8 matmul needs beyond the activation buffer.
 size_t i8_workspace_bytes(const nnh_weight* w, size_t n_tok) {
-    return n_tok >= GEMM_MIN_TOKENS ? nnh::gemm_workspace_bytes((int)w->rows, (int)w->nb, (int)n_tok) : 0;
+    if (n_tok >= GEMM_MIN_TOKENS) return nnh::gemm_workspace_bytes((int)w->rows, (int)w->nb, (int)n_tok);
+    if (n_tok >= SKINNY_MIN_TOKENS) return nnh::skinny_workspace_bytes((int)w->rows, (int)w->nb);
+    return 0;
 }
 
 void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, size_t y_stride, uint8_t* ws,
@@ -128,9 +131,13 @@ void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, 
     const ActLayout l = act_layout(w->cols, n_tok);
     const int8_t* q = (const int8_t*)act;
     const double* sx = (const double*)(act + l.off_sx);
+    const float* sxT = (const float*)(act + l.off_sxT);
     if (n_tok >= GEMM_MIN_TOKENS)
-        nnh::launch_gemm_i8(w->dtype, w->qs, w->swT, q, (const float*)(act + l.off_sxT), (int)w->rows, (int)w->nb,
-                            (int)n_tok, y, y_stride, (double*)ws, st);
+        nnh::launch_gemm_i8(w->dtype, w->qs, w->swT, q, sxT, (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride,
+                            (double*)ws, st);
+    else if (n_tok >= SKINNY_MIN_TOKENS)
+        nnh::launch_skinny_i8(w->dtype, w->qs, w->swT, q, sxT, (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride,
+                              (double*)ws, st);
     else
         nnh::launch_gemv_i8(w->dtype, w->qs, w->sc, w->bi, w->sb, q, sx, (int)w->rows, (int)w->nb, (int)n_tok, y,
                             y_stride, st);

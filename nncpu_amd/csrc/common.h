@@ -83,6 +83,10 @@ int gemm_rows_pad(int rows);
 int gemm_tok_pad(int n_tok);
 void launch_gemm_scales(const uint16_t* sc, const uint16_t* bi, float* swT, int rows, int nb, hipStream_t st);
 size_t gemm_workspace_bytes(int rows, int nb, int n_tok);  // split-K partials; 0 if unsplit
+// int8 MFMA matmul for 5..16 vectors (kernels_skinny.hip).
+size_t skinny_workspace_bytes(int rows, int nb);  // K-split partials; 0 if unsplit
+void launch_skinny_i8(int dtype, const uint8_t* qs, const float* swT, const int8_t* aq, const float* sxT, int rows,
+                      int nb, int n_tok, float* y, size_t y_stride, double* ws, hipStream_t st);
 void launch_gemm_i8(int dtype, const uint8_t* qs, const float* swT, const int8_t* aq, const float* sxT, int rows,
                     int nb, int n_tok, float* y, size_t y_stride, double* ws, hipStream_t st);
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,
