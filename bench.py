@@ -34,6 +34,10 @@ INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 512 << 20
 
 Q4_SWEEP = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+# HBM bytes per launch of the sweep's GEMVs, from rocprofv3 --pmc FETCH_SIZE
+# (x2.0, the factor a 64 MiB device copy gives) + WRITE_SIZE, in the order of
+# Q4_SWEEP; the runs are in profiles/gemv_i8_q4_llama3_8b_sweep.md.
+Q4_SWEEP_TRAFFIC = [10_603_212, 2_713_600, 36_853_350, 36_929_126]
 Q8_VOCAB = [(262144, 1152), (151936, 3584)]
 
 
@@ -167,8 +171,9 @@ def q4_sweep(args, N):
                     activations="N(0,1) f32 -> int8 blocks (nncpu Q8_0) on device", parallelism="none",
                     rotate_mb=ROTATE_BYTES >> 20),
         roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                      kernel="gemv_i8_kernel (Q4)", bytes_per_launch=bytes_per_launch,
+                      frac=round(achieved / HBM_PEAK_GBS, 4),
+                      traffic=round(sum(Q4_SWEEP_TRAFFIC) / len(Q4_SWEEP_TRAFFIC)),
+                      kernel="gemv_i8_v2_kernel (Q4, M=1)", bytes_per_launch=bytes_per_launch,
                       avg_launch_us=round(kernel_us, 3)),
         per_shape=[{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p.items()} for p in per_shape],
     )
