@@ -7,6 +7,7 @@
 // priority, a growable device scratch buffer and pinned staging) guarded by
 // a mutex, as the reference's pool serialises dispatch (pool.rs:7-9,253).
 
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -35,6 +36,8 @@ int g_device = -1;
 hipStream_t g_stream = nullptr;
 uint8_t* g_scratch = nullptr;
 size_t g_scratch_bytes = 0;
+uint8_t* g_pinned = nullptr;  // pinned host staging for the host-buffer calls
+size_t g_pinned_bytes = 0;
 
 int fail(int code, const std::string& msg) {
     t_err = msg;
@@ -89,6 +92,23 @@ int scratch_locked(size_t bytes, uint8_t** out) {
         g_scratch_bytes = want;
     }
     *out = g_scratch;
+    return NNH_OK;
+}
+
+// Grow the pinned host staging buffer to `bytes`; caller holds g_mu and no
+// queued work reads the old one (every host-buffer call ends synchronised).
+int pinned_locked(size_t bytes, uint8_t** out) {
+    if (bytes > g_pinned_bytes) {
+        if (g_pinned) {
+            NNH_HIP(hipHostFree(g_pinned));
+            g_pinned = nullptr;
+            g_pinned_bytes = 0;
+        }
+        size_t want = align_up(bytes + bytes / 4);
+        NNH_HIP(hipHostMalloc((void**)&g_pinned, want, hipHostMallocDefault));
+        g_pinned_bytes = want;
+    }
+    *out = g_pinned;
     return NNH_OK;
 }
 
@@ -364,15 +384,21 @@ int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* 
     const size_t y_elems = (n_tok - 1) * ys + w->rows;
     const size_t off_y = align_up(x_elems * 4);
     const size_t off_s = off_y + align_up(y_elems * 4);
-    uint8_t* s;
+    uint8_t *s, *h;
     if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, n_tok, act), &s))) return rc;
+    if ((rc = pinned_locked(off_s, &h))) return rc;
     float* dx = (float*)s;
     float* dy = (float*)(s + off_y);
-    NNH_HIP(hipMemcpyAsync(dx, x, x_elems * 4, hipMemcpyHostToDevice, g_stream));
+    // Through pinned staging: the DMA engines copy pinned memory directly,
+    // where pageable copies go through the runtime's own bounce buffers.
+    std::memcpy(h, x, x_elems * 4);
+    NNH_HIP(hipMemcpyAsync(dx, h, x_elems * 4, hipMemcpyHostToDevice, g_stream));
     if ((rc = run_gemv(w, dx, xs, dy, ys, n_tok, act, s + off_s, g_stream))) return rc;
-    // Only each vector's rows: the reference leaves the stride gaps alone.
-    NNH_HIP(hipMemcpy2DAsync(y, ys * 4, dy, ys * 4, w->rows * 4, n_tok, hipMemcpyDeviceToHost, g_stream));
+    float* hy = (float*)(h + off_y);
+    NNH_HIP(hipMemcpyAsync(hy, dy, y_elems * 4, hipMemcpyDeviceToHost, g_stream));
     NNH_HIP(hipStreamSynchronize(g_stream));
+    // Only each vector's rows: the reference leaves the stride gaps alone.
+    for (size_t t = 0; t < n_tok; ++t) std::memcpy(y + t * ys, hy + t * ys, w->rows * 4);
     return NNH_OK;
 }
 
@@ -391,19 +417,21 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
     const size_t off_p = off_y + align_up(w->rows * 4);
     const size_t off_o = off_p + align_up(nnh::argmax_partial_words(w->rows) * 8);
     const size_t off_s = off_o + ALIGN;
-    uint8_t* s;
+    uint8_t *s, *h;
     if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, 1, act), &s))) return rc;
+    if ((rc = pinned_locked(off_y + ALIGN, &h))) return rc;
     float* dx = (float*)s;
     float* dy = (float*)(s + off_y);
     uint64_t* dout = (uint64_t*)(s + off_o);
-    NNH_HIP(hipMemcpyAsync(dx, x, w->cols * 4, hipMemcpyHostToDevice, g_stream));
+    std::memcpy(h, x, w->cols * 4);
+    NNH_HIP(hipMemcpyAsync(dx, h, w->cols * 4, hipMemcpyHostToDevice, g_stream));
     if ((rc = run_gemv(w, dx, w->cols, dy, w->rows, 1, act, s + off_s, g_stream))) return rc;
     nnh::launch_argmax(dy, w->rows, (uint64_t*)(s + off_p), dout, g_stream);
     NNH_HIP(hipGetLastError());
-    uint64_t idx = 0;
-    NNH_HIP(hipMemcpyAsync(&idx, dout, 8, hipMemcpyDeviceToHost, g_stream));
+    uint64_t* hidx = (uint64_t*)(h + off_y);
+    NNH_HIP(hipMemcpyAsync(hidx, dout, 8, hipMemcpyDeviceToHost, g_stream));
     NNH_HIP(hipStreamSynchronize(g_stream));
-    *out_row = (size_t)idx;
+    *out_row = (size_t)*hidx;
     return NNH_OK;
 }
 

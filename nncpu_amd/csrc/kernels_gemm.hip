@@ -41,6 +41,7 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int TILE = 128;  // weight rows and tokens per workgroup
+constexpr int GEMM_MAX_SPLITS = 8;
 constexpr int NW = 16;     // waves per workgroup (4 per SIMD: latency hiding)
 constexpr int WN = 4;      // waves along the rows: each wave owns TILE / WN rows ...
 constexpr int WM = 4;      // ... and TILE / WM tokens
@@ -236,16 +237,17 @@ __device__ __forceinline__ void pipeline_step(GStage<DT, KB>& cur, GStage<DT, KB
     compute_stage<DT, KB>(cur, acc, nblk, wn * 32, wm * 32, h, lane & 31);
 }
 
-// Turn a wave's 32 x 32 tile around in LDS (`wout`, 4 KB), as
-// [token][row ^ token] f32 (the XOR spreads both passes over the banks), and
-// store 32-float runs of y rows.
-__device__ __forceinline__ void store_tile(float* wout, const double (&acc)[16], int n0, int m0, int h, int c,
-                                           int rows, int n_tok, float* __restrict__ y, size_t y_stride) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = (r / 4) * 8 + 4 * h + (r % 4);
-        wout[c * 32 + (row ^ c)] = (float)acc[r];
-    }
+// A wave's 32 x 32 result tile turned around in LDS (`wout`, 4 KB), as
+// [token][row ^ token] f32: the XOR spreads both passes over the banks.
+// tile_put writes result register r of the lane; tile_store then writes
+// 32-float runs of y rows.
+__device__ __forceinline__ void tile_put(float* wout, int r, double v, int h, int c) {
+    const int row = (r / 4) * 8 + 4 * h + (r % 4);
+    wout[c * 32 + (row ^ c)] = (float)v;
+}
+
+__device__ __forceinline__ void tile_store(const float* wout, int n0, int m0, int h, int c, int rows, int n_tok,
+                                           float* __restrict__ y, size_t y_stride) {
     const int n = n0 + c;
 #pragma unroll 4
     for (int k = 0; k < 16; ++k) {
@@ -254,6 +256,13 @@ __device__ __forceinline__ void store_tile(float* wout, const double (&acc)[16],
         const float v = wout[t * 32 + (c ^ t)];
         if (n < rows && m < n_tok) y[(size_t)m * y_stride + n] = v;
     }
+}
+
+__device__ __forceinline__ void store_tile(float* wout, const double (&acc)[16], int n0, int m0, int h, int c,
+                                           int rows, int n_tok, float* __restrict__ y, size_t y_stride) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tile_put(wout, r, acc[r], h, c);
+    tile_store(wout, n0, m0, h, c, rows, n_tok, y, y_stride);
 }
 
 template <int DT, int KB>
@@ -307,23 +316,35 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_kernel(GArgs g, float* __rest
 }
 
 // y = the sum of the split-K partial tiles, in split order (f64), rounded
-// once. One 64-lane workgroup per wave tile of the GEMM.
+// once. One 64-lane workgroup per wave tile of the GEMM; four result
+// registers at a time, their partials loaded for every split before the
+// first add so the latencies overlap.
 __global__ __launch_bounds__(64) void gemm_reduce_kernel(const double* __restrict__ ws, int splits, int tiles,
                                                          int mtiles, int rows, int n_tok, float* __restrict__ y,
                                                          size_t y_stride) {
     __shared__ float out[32 * 32];
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x, h = lane >> 5, c = lane & 31;
     const int tile = blockIdx.x / NW, wave = blockIdx.x % NW;
-    double acc[16];
+    const double* base = ws + ((size_t)tile * NW + wave) * 1024 + lane;
+    const size_t split_stride = (size_t)tiles * NW * 1024;
+#pragma unroll 1
+    for (int r0 = 0; r0 < 16; r0 += 4) {
+        double p[GEMM_MAX_SPLITS][4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0;
-    for (int sp = 0; sp < splits; ++sp) {
-        const double* p = ws + (((size_t)sp * tiles + tile) * NW + wave) * 1024 + lane;
+        for (int sp = 0; sp < GEMM_MAX_SPLITS; ++sp)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += p[r * 64];
+            for (int r = 0; r < 4; ++r) p[sp][r] = sp < splits ? base[sp * split_stride + (r0 + r) * 64] : 0.0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            double s = 0.0;
+#pragma unroll
+            for (int sp = 0; sp < GEMM_MAX_SPLITS; ++sp)
+                if (sp < splits) s += p[sp][r];
+            tile_put(out, r0 + r, s, h, c);
+        }
     }
     const int n0 = (tile / mtiles) * TILE + (wave / WM) * 32, m0 = (tile % mtiles) * TILE + (wave % WM) * 32;
-    store_tile(out, acc, n0, m0, lane >> 5, lane & 31, rows, n_tok, y, y_stride);
+    tile_store(out, n0, m0, h, c, rows, n_tok, y, y_stride);
 }
 
 // swT[b][n] = f32(scale[n][b]) and, for Q4, the biases in a second table
@@ -355,7 +376,6 @@ void launch_gemm_scales(const uint16_t* sc, const uint16_t* bi, float* swT, int 
 // Blocks per ring stage.
 constexpr int GEMM_KB = 4;
 
-constexpr int GEMM_MAX_SPLITS = 8;
 
 // Split-K factor: small tile grids are split along K until they cover the
 // 256 CUs (one workgroup each), keeping at least two ring chunks per split.

@@ -13,10 +13,9 @@
 // outer-product MFMA, f64 accumulation), so every output is within one f32
 // ulp of the exact sum.
 //
-// Workgroup: 8 waves on 32 weight rows; the waves split the blocks into
+// Workgroup: 4 waves on 32 weight rows; the waves split the blocks into
 // contiguous ranges and stream them straight into registers (16 bytes per
-// lane and block, nontemporal), eight blocks per group, double-buffered, so
-// 16 blocks of weights and activations are in flight per wave. Partial sums
+// lane and block, nontemporal), four blocks per group, double-buffered. Partial sums
 // meet in LDS and are added in wave order. Matrices with few row groups are
 // split along K over several workgroups as well; those partials go to a
 // workspace (f64) and a second kernel adds them in split order.
@@ -30,8 +29,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-constexpr int SK_W = 8;  // waves per workgroup
-constexpr int SK_G = 8;  // blocks per load group (even: scale products go in pairs)
+constexpr int SK_W = 4;           // waves per workgroup
+constexpr int SK_G = 4;           // blocks per load group (even: scale products go in pairs)
+constexpr int SK_MAX_SPLITS = 8;  // K-split workgroups per row group
 
 struct KArgs {
     const uint8_t* qs;  // weights, nncpu row-major quants
@@ -146,13 +146,17 @@ __global__ __launch_bounds__(SK_W * 64) void skinny_i8_kernel(KArgs g, float* __
 #pragma unroll
     for (int r = 0; r < NR; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    if (tid < NR * 64) {
-        const int r = tid >> 6, l = tid & 63;
+    // Thread (r, l) finishes result register r of lane l: the SK_W * 64
+    // threads cover the NR * 64 outputs in NR / SK_W rounds.
+    static_assert(NR % SK_W == 0, "whole rounds");
+    const int l = tid & 63;
+    const int row = n0 + (l & 31);
+#pragma unroll
+    for (int r = tid >> 6; r < NR; r += SK_W) {
         double s = 0.0;
 #pragma unroll
         for (int w = 0; w < SK_W; ++w) s += red[w][r][l];
         const int i = (r / 4) * 8 + 4 * (l >> 5) + (r % 4);  // token
-        const int row = n0 + (l & 31);
         if (i < g.n_tok && row < g.rows) {
             if (g.ksplit == 1)
                 y[(size_t)i * y_stride + row] = (float)s;
@@ -163,12 +167,18 @@ __global__ __launch_bounds__(SK_W * 64) void skinny_i8_kernel(KArgs g, float* __
 }
 
 // y = the sum of the K-split partials in split order (f64), rounded once.
+// All partials are loaded before the first add, so their latencies overlap.
 __global__ void skinny_reduce_kernel(const double* __restrict__ ws, int ksplit, int rows, int rows_pad, int n_tok,
                                      float* __restrict__ y, size_t y_stride) {
     const int row = blockIdx.x * blockDim.x + threadIdx.x, i = blockIdx.y;
     if (row >= rows) return;
+    double p[SK_MAX_SPLITS];
+#pragma unroll
+    for (int k = 0; k < SK_MAX_SPLITS; ++k) p[k] = k < ksplit ? ws[((size_t)k * 16 + i) * rows_pad + row] : 0.0;
     double s = 0.0;
-    for (int k = 0; k < ksplit; ++k) s += ws[((size_t)k * 16 + i) * rows_pad + row];
+#pragma unroll
+    for (int k = 0; k < SK_MAX_SPLITS; ++k)
+        if (k < ksplit) s += p[k];
     y[(size_t)i * y_stride + row] = (float)s;
 }
 
@@ -182,6 +192,7 @@ int skinny_splits(int rows, int nb) {
     int ks = ceil_div(256, groups);
     const int most = nb / (2 * SK_W);
     if (ks > most) ks = most;
+    if (ks > SK_MAX_SPLITS) ks = SK_MAX_SPLITS;
     return ks < 1 ? 1 : ks;
 }
 
