@@ -24,6 +24,7 @@ struct nnh_weight {
     const uint16_t* bi;   // Q4 only
     uint32_t* sb;         // device: Q4 scale | bias << 16 per block (int8 path)
     uint8_t* fq;          // device: per-lane quant groups for the f32 path
+    bool f32v2;           // fq in the 8-lane layout (tall matrices)
     uint16_t* fs;         // device: scales padded to nbp per row
     float* swT;           // device: [nb][rows padded] f32 scales, Q4 biases after (MFMA GEMM)
 };
@@ -174,7 +175,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
             nnh::launch_block_sums(x, x_stride, nb, (int)n_tok, xsum, st);
         }
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
-                             y, y_stride, st);
+                             y, y_stride, w->f32v2, st);
     } else {
         const ActLayout l = act_layout(w->cols, n_tok);
         nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, (int8_t*)scratch, (uint16_t*)(scratch + l.off_s),
@@ -224,6 +225,13 @@ void release(nnh_weight* w) {
     delete w;
 }
 
+// Matrices from this many rows get the bit-exact path's 8-lane layout:
+// enough rows to fill the GPU at 8 lanes per row.
+#ifndef NNH_F32_V2_MIN_ROWS
+#define NNH_F32_V2_MIN_ROWS 16384
+#endif
+constexpr size_t F32_V2_MIN_ROWS = NNH_F32_V2_MIN_ROWS;
+
 // Allocate a weight's device buffers; caller holds g_mu.
 int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     const size_t n = rows * cols, nb = cols / 32;
@@ -236,9 +244,11 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     w->cols = cols;
     w->nb = nb;
     w->nbp = (nb + group - 1) / group * group;
+    w->f32v2 = rows >= F32_V2_MIN_ROWS && cols * 4 <= (size_t)nnh::F32_V2_MAX_LDS;
     hipError_t e;
     if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->fq, align_up(qbytes))) != hipSuccess ||
+        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2)))) !=
+            hipSuccess ||
         (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
         (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||
         (e = hipMalloc((void**)&w->swT, align_up((size_t)nnh::gemm_rows_pad((int)rows) * nb * 4 *
@@ -255,7 +265,8 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
 
 // Build the derived layouts from `raw` and wait; caller holds g_mu.
 int finalize_weight(nnh_weight* w) {
-    nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, g_stream);
+    nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, w->f32v2,
+                             g_stream);
     if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
     nnh::launch_gemm_scales(w->sc, w->bi, w->swT, (int)w->rows, (int)w->nb, g_stream);
     hipError_t e;

@@ -54,20 +54,29 @@ __device__ __forceinline__ int4 load_nt16(const void* p) {
     nnh_v4i v = __builtin_nontemporal_load((const nnh_v4i*)p);
     return make_int4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint4 load_nt16u(const void* p) {
+    nnh_v4i v = __builtin_nontemporal_load((const nnh_v4i*)p);
+    return make_uint4((unsigned)v.x, (unsigned)v.y, (unsigned)v.z, (unsigned)v.w);
+}
 
 inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ---- launchers (defined beside their kernels) -------------------------------
 
 // Upload-time relayouts for the bit-exact f32 path (kernels_f32.hip).
+// `v2`: the 8-lane layout and kernel (tall matrices, x of one token within
+// F32_V2_MAX_LDS bytes); f32_quant_bytes is the size of the quant layout
+// either way.
+constexpr int F32_V2_MAX_LDS = 64 * 1024;
+size_t f32_quant_bytes(int dtype, int rows, int nb, bool v2);
 void launch_relayout_f32(int dtype, const uint8_t* raw_qs, const uint16_t* raw_scales, uint8_t* fq, uint16_t* fs,
-                         int rows, int nb, int nbp, hipStream_t st);
+                         int rows, int nb, int nbp, bool v2, hipStream_t st);
 // Q4 block sums of n_tok vectors (kernels/scalar.rs:355-359 tree).
 void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float* xsum, hipStream_t st);
 // Bit-exact f32 gemv for n_tok <= 16 vectors.
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
                      size_t x_stride, const float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
-                     size_t y_stride, hipStream_t st);
+                     size_t y_stride, bool v2, hipStream_t st);
 
 // int8 path (kernels_i8.hip).
 void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,

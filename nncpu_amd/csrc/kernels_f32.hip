@@ -27,6 +27,21 @@
 //         t < 16 blocks gives each lane t bytes at offset t*j.
 // Scales are copied to rows padded to nbp (a multiple of 8 / 16) so a
 // group's scales are one aligned 16-byte load per 8.
+//
+// A second mapping for tall matrices (the lm_head): 8 lanes per row, lane j
+// owning chains 4j..4j+3, so one 16-byte load of x serves four chains of a
+// block and a wave covers 8 rows. Its quant layout: per row, groups of 128
+// bytes (one 16-byte piece per lane),
+//   Q8_0: groups of 4 blocks; lane j's piece holds bytes 4j..4j+3 of each.
+//   Q4:   groups of 8 blocks; lane j's piece is 4 words, word k holding
+//         elements 4j..4j+3 of block 2k in its low nibbles (one per byte)
+//         and of block 2k+1 in its high nibbles;
+// stored tile-major: for each tile of 32 rows (one workgroup), group g of
+// the 32 rows is one 4 KB run, so every wave load reads 1 KB contiguous and
+// a workgroup streams one contiguous region. Rows are padded to whole
+// groups and tiles with zeros (never multiplied: the block loop stops at
+// nb). The reduction becomes xor-2, xor-4 (the accumulator pairs), xor-1
+// and an in-lane pair sum (hsum8): the same additions.
 
 #include "common.h"
 
@@ -78,6 +93,51 @@ __global__ void relayout_q4_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
         off = (size_t)ng * 256 + (size_t)j * t + (b - ng * Q4_GROUP);
     }
     fq[r * row_bytes + off] = raw[idx];
+}
+
+// The 8-lane layout: one thread per destination word.
+__global__ void relayout_q8_v2_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ fq, int rows, int nb) {
+    const int ng = (nb + 3) / 4;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // destination word
+    const size_t tile_words = (size_t)ng * 32 * 32;
+    if (idx >= (size_t)((rows + 31) / 32) * tile_words) return;
+    const size_t tile = idx / tile_words;
+    const int d = (int)(idx - tile * tile_words);
+    const int g = d / 1024, r = (d >> 5) & 31, j = (d >> 2) & 7, i = d & 3;
+    const size_t row = tile * 32 + r;
+    const int b = 4 * g + i;
+    uint32_t v = 0;
+    if (b < nb && row < (size_t)rows) v = *(const uint32_t*)(raw + row * (size_t)nb * 32 + (size_t)b * 32 + 4 * j);
+    ((uint32_t*)fq)[idx] = v;
+}
+
+__global__ void relayout_q4_v2_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ fq, int rows, int nb) {
+    const int ng = (nb + 7) / 8;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // destination word
+    const size_t tile_words = (size_t)ng * 32 * 32;
+    if (idx >= (size_t)((rows + 31) / 32) * tile_words) return;
+    const size_t tile = idx / tile_words;
+    const int d = (int)(idx - tile * tile_words);
+    const int g = d / 1024, r = (d >> 5) & 31, j = (d >> 2) & 7, k = d & 3;
+    const size_t rr = tile * 32 + r;
+    uint32_t v = 0;
+    if (rr >= (size_t)rows) {
+        ((uint32_t*)fq)[idx] = 0;
+        return;
+    }
+    const uint8_t* row = raw + rr * (size_t)nb * 16;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int b = 8 * g + 2 * k + half;
+        if (b >= nb) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = 4 * j + e;  // element of the block: byte c % 16, high nibble when c >= 16
+            const uint32_t nib = (row[(size_t)b * 16 + (c & 15)] >> (c >= 16 ? 4 : 0)) & 15u;
+            v |= nib << (8 * e + 4 * half);
+        }
+    }
+    ((uint32_t*)fq)[idx] = v;
 }
 
 __global__ void pad_scales_kernel(const uint16_t* __restrict__ s, uint16_t* __restrict__ fs, int rows, int nb,
@@ -229,6 +289,200 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
     }
 }
 
+// The 8-lane mapping (tall matrices).
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int V2_R = 4;  // rows per lane group: four rows share every x load
+
+// One block for the lane group's V2_R rows: w[r][e] (exact weights) against
+// x[32b + 4j + e] of every token, read from the workgroup's LDS copy of x
+// (LDS reads wait on their own counter, so they never wait for the weight
+// loads in flight).
+template <int M>
+__device__ __forceinline__ void v2_block(float (&acc)[V2_R][M][4], const float (&w)[V2_R][4],
+                                         const float* xl, int cols, int e0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float4 xv = *(const float4*)(xl + m * cols + e0);
+#pragma unroll
+        for (int r = 0; r < V2_R; ++r) {
+            acc[r][m][0] = __builtin_fmaf(w[r][0], xv.x, acc[r][m][0]);
+            acc[r][m][1] = __builtin_fmaf(w[r][1], xv.y, acc[r][m][1]);
+            acc[r][m][2] = __builtin_fmaf(w[r][2], xv.z, acc[r][m][2]);
+            acc[r][m][3] = __builtin_fmaf(w[r][3], xv.w, acc[r][m][3]);
+        }
+    }
+}
+
+template <int DT>
+struct V2Group {
+    uint4 q[V2_R], s[V2_R];
+};
+
+template <int DT>
+__device__ __forceinline__ void v2_load(V2Group<DT>& gr, const uint4* const (&qrow)[V2_R],
+                                        const uint16_t* const (&srow)[V2_R], int g) {
+#pragma unroll
+    for (int r = 0; r < V2_R; ++r) {
+        gr.q[r] = load_nt16u(qrow[r] + (size_t)g * 32 * 8);
+        if (DT == 1) {
+            const uint2 v = *(const uint2*)(srow[r] + 4 * g);
+            gr.s[r] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            gr.s[r] = *(const uint4*)(srow[r] + 8 * g);
+        }
+    }
+}
+
+template <int DT, int M>
+__device__ __forceinline__ void v2_group(float (&acc)[V2_R][M][4], const V2Group<DT>& gr, int g, int nb,
+                                         const float* xl, int j) {
+    if (DT == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = 4 * g + i;
+            if (b >= nb) break;
+            float w[V2_R][4];
+#pragma unroll
+            for (int r = 0; r < V2_R; ++r) {
+                const uint32_t qw = i == 0 ? gr.q[r].x : i == 1 ? gr.q[r].y : i == 2 ? gr.q[r].z : gr.q[r].w;
+                const float s = bf16f(half_of(gr.s[r], i));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[r][e] = (float)(int8_t)(qw >> (8 * e)) * s;  // exact
+            }
+            v2_block<M>(acc, w, xl, nb * 32, 32 * b + 4 * j);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int b = 8 * g + 2 * k + half;
+                if (b >= nb) break;
+                float w[V2_R][4];
+#pragma unroll
+                for (int r = 0; r < V2_R; ++r) {
+                    const uint32_t qw = k == 0 ? gr.q[r].x : k == 1 ? gr.q[r].y : k == 2 ? gr.q[r].z : gr.q[r].w;
+                    const uint32_t nib = (qw >> (4 * half)) & 0x0f0f0f0fu;
+                    const float s = bf16f(half_of(gr.s[r], 2 * k + half));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[r][e] = (float)((nib >> (8 * e)) & 0xffu) * s;  // exact
+                }
+                v2_block<M>(acc, w, xl, nb * 32, 32 * b + 4 * j);
+            }
+        }
+    }
+}
+
+// Workgroup: 4 waves = 32 lane groups; lane group lg of workgroup wg runs
+// rows (wg * V2_R + r) * 32 + lg for r < V2_R, one row from each of V2_R
+// consecutive 32-row tiles.
+template <int DT, int M>
+__global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restrict__ fq,
+                                                          const uint16_t* __restrict__ fs,
+                                                          const uint16_t* __restrict__ biases,
+                                                          const float* __restrict__ x, size_t x_stride,
+                                                          const float* __restrict__ xsum, int rows, int nb, int nbp,
+                                                          float* __restrict__ y, size_t y_stride) {
+    constexpr int G = DT == 1 ? 4 : 8;
+    const int j = threadIdx.x & 7, lg = threadIdx.x >> 3;
+    const int ng = (nb + G - 1) / G;
+    int row[V2_R];
+    const uint4* qrow[V2_R];
+    const uint16_t* srow[V2_R];
+#pragma unroll
+    for (int r = 0; r < V2_R; ++r) {
+        const int tile = blockIdx.x * V2_R + r;
+        const int raw = tile * 32 + lg;
+        row[r] = raw < rows ? raw : rows - 1;  // keep loads in bounds; stores are skipped
+        const int t = row[r] / 32;
+        // Tile-major: group g of this row at ((tile * ng + g) * 32 + row % 32) * 128.
+        qrow[r] = (const uint4*)(fq + ((size_t)t * ng * 32 + (row[r] % 32)) * 128) + j;
+        srow[r] = fs + (size_t)row[r] * nbp;
+    }
+
+    float acc[V2_R][M][4];
+#pragma unroll
+    for (int r = 0; r < V2_R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[r][m][e] = 0.0f;
+
+    // The first weight group is in flight while x is copied to LDS.
+    V2Group<DT> ga, gb;
+    v2_load<DT>(ga, qrow, srow, 0);
+    extern __shared__ float xl[];  // [M][cols]
+    const int cols = nb * 32;
+    for (int m = 0; m < M; ++m)
+        for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256)
+            *(float4*)(xl + m * cols + i) = __builtin_bit_cast(float4, *(const f4u*)(x + (size_t)m * x_stride + i));
+    __syncthreads();
+
+    // One group ahead: its quants and scales load while this one is used.
+    for (int g = 0; g < ng; g += 2) {
+        if (g + 1 < ng) v2_load<DT>(gb, qrow, srow, g + 1);
+        v2_group<DT, M>(acc, ga, g, nb, xl, j);
+        if (g + 1 >= ng) break;
+        if (g + 2 < ng) v2_load<DT>(ga, qrow, srow, g + 2);
+        v2_group<DT, M>(acc, gb, g + 1, nb, xl, j);
+    }
+
+#pragma unroll
+    for (int r = 0; r < V2_R; ++r) {
+        const bool valid = (blockIdx.x * V2_R + r) * 32 + lg < rows;
+        float bdot[M];
+        if (DT == 2) {
+            // dot_bf16_f32 (scalar.rs:334-347): lane j runs accumulator lane j
+            // over whole groups of 8 blocks, then hsum8 (xor-4, xor-1, xor-2)
+            // and the unfused tail.
+            const uint16_t* brow = biases + (size_t)row[r] * nb;
+            const int body = nb & ~7;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float* xs = xsum + (size_t)m * nb;
+                float a = 0.0f;
+                for (int i = j; i < body; i += 8) a = __builtin_fmaf(bf16f(brow[i]), xs[i], a);
+                float p = __fadd_rn(a, xor_get(a, 4));
+                float q = __fadd_rn(p, xor_get(p, 1));
+                float s = __fadd_rn(q, xor_get(q, 2));
+                for (int i = body; i < nb; ++i) s = __fadd_rn(s, __fmul_rn(bf16f(brow[i]), xs[i]));
+                bdot[m] = s;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            // Lane p in {0, 1} ends with v[4p + e] in slot e: chains l, 8+l sit
+            // in lanes l/4 and l/4 + 2, chains 16+l, 24+l in l/4 + 4 and l/4 + 6.
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float t = __fadd_rn(acc[r][m][e], xor_get(acc[r][m][e], 2));
+                v[e] = __fadd_rn(t, xor_get(t, 4));
+            }
+            float w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = __fadd_rn(v[e], xor_get(v[e], 1));  // v[e] + v[4+e] at lane 0
+            float res = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
+            if (DT == 2) res = __fadd_rn(res, bdot[m]);
+            if (valid && j == 0) y[(size_t)m * y_stride + row[r]] = res;
+        }
+    }
+}
+
+template <int DT>
+void launch_dt_v2(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, size_t xs,
+                  const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, hipStream_t st) {
+    dim3 grid(ceil_div(rows, 32 * V2_R)), block(256);
+    const size_t lds = (size_t)M * nb * 32 * sizeof(float);
+    switch (M) {
+        case 1: gemv_f32_v2_kernel<DT, 1><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
+        case 2: gemv_f32_v2_kernel<DT, 2><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
+        case 3: gemv_f32_v2_kernel<DT, 3><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
+        default: gemv_f32_v2_kernel<DT, 4><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
+    }
+}
+
 template <int DT>
 void launch_dt(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, size_t xs,
                const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, hipStream_t st) {
@@ -243,14 +497,29 @@ void launch_dt(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* bi,
 
 }  // namespace
 
+size_t f32_quant_bytes(int dtype, int rows, int nb, bool v2) {
+    if (!v2) return (size_t)rows * nb * (dtype == 1 ? 32 : 16);
+    const int g = dtype == 1 ? 4 : 8;
+    return (size_t)((rows + 31) / 32) * 32 * ((nb + g - 1) / g) * 128;
+}
+
 void launch_relayout_f32(int dtype, const uint8_t* raw_qs, const uint16_t* raw_scales, uint8_t* fq, uint16_t* fs,
-                         int rows, int nb, int nbp, hipStream_t st) {
-    size_t qbytes = (size_t)rows * nb * (dtype == 1 ? 32 : 16);
-    int blocks = (int)((qbytes + 255) / 256);
-    if (dtype == 1)
-        relayout_q8_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
-    else
-        relayout_q4_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
+                         int rows, int nb, int nbp, bool v2, hipStream_t st) {
+    if (v2) {
+        const size_t words = f32_quant_bytes(dtype, rows, nb, true) / 4;
+        const unsigned blocks = (unsigned)((words + 255) / 256);
+        if (dtype == 1)
+            relayout_q8_v2_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
+        else
+            relayout_q4_v2_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
+    } else {
+        size_t qbytes = (size_t)rows * nb * (dtype == 1 ? 32 : 16);
+        int blocks = (int)((qbytes + 255) / 256);
+        if (dtype == 1)
+            relayout_q8_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
+        else
+            relayout_q4_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
+    }
     size_t sn = (size_t)rows * nbp;
     pad_scales_kernel<<<(int)((sn + 255) / 256), 256, 0, st>>>(raw_scales, fs, rows, nb, nbp);
 }
@@ -264,16 +533,25 @@ void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float
 // independent, so the chunking never changes a bit.
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
                      size_t x_stride, const float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
-                     size_t y_stride, hipStream_t st) {
-    for (int t0 = 0; t0 < n_tok; t0 += 4) {
-        int m = n_tok - t0 < 4 ? n_tok - t0 : 4;
+                     size_t y_stride, bool v2, hipStream_t st) {
+    // The 8-lane kernel keeps x in LDS: at most 64 KB of it per launch.
+    int per = 4;
+    if (v2 && per * nb * 32 * 4 > F32_V2_MAX_LDS) per = F32_V2_MAX_LDS / (nb * 32 * 4);
+    for (int t0 = 0; t0 < n_tok; t0 += per) {
+        int m = n_tok - t0 < per ? n_tok - t0 : per;
         const float* xt = x + (size_t)t0 * x_stride;
         const float* st_xsum = xsum ? xsum + (size_t)t0 * nb : nullptr;
         float* yt = y + (size_t)t0 * y_stride;
-        if (dtype == 1)
+        if (v2) {
+            if (dtype == 1)
+                launch_dt_v2<1>(m, fq, fs, biases, xt, x_stride, st_xsum, rows, nb, nbp, yt, y_stride, st);
+            else
+                launch_dt_v2<2>(m, fq, fs, biases, xt, x_stride, st_xsum, rows, nb, nbp, yt, y_stride, st);
+        } else if (dtype == 1) {
             launch_dt<1>(m, fq, fs, biases, xt, x_stride, st_xsum, rows, nb, nbp, yt, y_stride, st);
-        else
+        } else {
             launch_dt<2>(m, fq, fs, biases, xt, x_stride, st_xsum, rows, nb, nbp, yt, y_stride, st);
+        }
     }
 }
 

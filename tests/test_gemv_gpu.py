@@ -112,6 +112,28 @@ def test_f32_batch_equals_single(oracle, dtype):
                 assert np.array_equal(bits(y1), bits(oracle.gemv_batch(m, x[t * xs:t * xs + cols])))
 
 
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols", [(16400, 96), (16390, 1056), (16384, 32), (16384, 544), (16384, 8192)])
+def test_f32_tall_layout_bit_exact(oracle, dtype, rows, cols):
+    # Matrices of 16384 rows or more take the 8-lane layout; these shapes give
+    # it partial groups (nb = 3, 33, 1, 17), a ragged last workgroup, strided
+    # batches, the Q4 bias tail, and (K = 8192) x too big for four tokens in
+    # LDS at once (two per launch).
+    say("tall", dtype, rows, cols)
+    rng = oracle.Rng(0x7A11 + rows + cols + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols))
+    w = upload(m)
+    for n_tok in ((1, 3) if cols > 4096 else (1, 3, 4, 6)):
+        xs, ys = cols + 32, rows + 3
+        x = rng.vec(n_tok * xs, -1.0, 1.0)
+        y = np.full(n_tok * ys, 5.0, np.float32)
+        N.gemv_batch(w, x, xs, y, ys, n_tok)
+        ref = oracle.gemv_batch(m, x, n_tok, xs, ys)
+        for t in range(n_tok):
+            assert np.array_equal(bits(y[t * ys:t * ys + rows]), bits(ref[t * ys:t * ys + rows])), (n_tok, t)
+            assert np.all(y[t * ys + rows:(t + 1) * ys] == 5.0) or t == n_tok - 1
+
+
 def test_f32_lm_head_gemma_vocab(oracle):
     # The largest decode gemv: the tied Gemma-3 lm_head, 262144 x 1152, Q8_0.
     rows, cols = 262144, 1152
