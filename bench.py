@@ -228,6 +228,114 @@ def measure_cases(args, N, cases, act_mode, label):
     return out
 
 
+def qwen_prefill(args, N, dtype: int, n_tok: int = 512, n_layer: int = 28):
+    """BASELINE configs[4], end to end: a Qwen2.5-7B-shaped model (d 3584,
+    FFN 18944, 28 query / 4 KV heads of 128, RoPE base 1e6, RMSNorm, SwiGLU,
+    q/k/v biases) with random weights 0.02*N(0,1) encoded by the library's
+    device encoder (nncpu Q8_0 / Q4), prefilling 512 tokens of random
+    embeddings through all 28 layers and the last token's lm_head row
+    (152064 x 3584). Every weight matmul is the library's int8 path
+    (activations quantized on the device, MFMA GEMM); q/k/v and gate/up are
+    uploaded as one concatenated matrix each, as serving engines load them.
+    The rest of the layer (norms, RoPE, causal GQA attention, SiLU) is torch
+    float32 on the GPU: harness, not the measured path. One step = one full
+    prefill; returns ms and tokens/s, plus the matmul share from HIP events."""
+    import torch
+    import torch.nn.functional as F
+    d, ff, nh, nkv, hd, vocab = 3584, 18944, 28, 4, 128, 152064
+    dev = "cuda"
+    st = Stream()
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x9E11 + dtype)
+
+    def weight(rows, cols):
+        w = torch.randn(rows * cols, generator=g, device=dev).mul_(0.02)
+        torch.cuda.synchronize()
+        out = N.Weight.encode_dev(dtype, w.data_ptr(), rows, cols)
+        del w
+        return out
+
+    layers = []
+    for _ in range(n_layer):
+        layers.append(dict(
+            qkv=weight(d + 2 * nkv * hd, d), o=weight(d, d), gu=weight(2 * ff, d), down=weight(d, ff),
+            bqkv=torch.randn(d + 2 * nkv * hd, generator=g, device=dev).mul_(0.02),
+            n1=1.0 + 0.1 * torch.randn(d, generator=g, device=dev),
+            n2=1.0 + 0.1 * torch.randn(d, generator=g, device=dev)))
+    lm_head = weight(vocab, d)
+    norm_f = 1.0 + 0.1 * torch.randn(d, generator=g, device=dev)
+    x0 = torch.randn(n_tok, d, generator=g, device=dev)
+    pos = torch.arange(n_tok, device=dev, dtype=torch.float32)
+    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+    ang = pos[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    mm_events = []
+
+    def mm(w, x, rows):
+        y = torch.empty(x.shape[0], rows, device=dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st.s)
+        N.gemv_batch_dev(w, x.data_ptr(), x.shape[1], y.data_ptr(), rows, x.shape[0], N.ACT_I8, st.handle)
+        e1.record(st.s)
+        mm_events.append((e0, e1))
+        return y
+
+    def rms(x, wgt):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * wgt
+
+    def rope(t):  # t [tokens, heads, hd], NeoX halves
+        a, b = t[..., :hd // 2], t[..., hd // 2:]
+        c, s_ = cos[:, None, :], sin[:, None, :]
+        return torch.cat([a * c - b * s_, b * c + a * s_], dim=-1)
+
+    def forward():
+        x = x0.clone()
+        for L in layers:
+            h = rms(x, L["n1"]).contiguous()
+            qkv = mm(L["qkv"], h, d + 2 * nkv * hd) + L["bqkv"]
+            q = rope(qkv[:, :d].view(n_tok, nh, hd))
+            k = rope(qkv[:, d:d + nkv * hd].view(n_tok, nkv, hd))
+            v = qkv[:, d + nkv * hd:].view(n_tok, nkv, hd)
+            k = k.repeat_interleave(nh // nkv, dim=1)
+            v = v.repeat_interleave(nh // nkv, dim=1)
+            a = F.scaled_dot_product_attention(q.transpose(0, 1).contiguous(), k.transpose(0, 1).contiguous(),
+                                               v.transpose(0, 1).contiguous(), is_causal=True)
+            a = a.transpose(0, 1).reshape(n_tok, d).contiguous()
+            x = x + mm(L["o"], a, d)
+            h = rms(x, L["n2"]).contiguous()
+            gu = mm(L["gu"], h, 2 * ff)
+            x = x + mm(L["down"], (F.silu(gu[:, :ff]) * gu[:, ff:]).contiguous(), d)
+        last = rms(x[-1:], norm_f).contiguous()
+        return mm(lm_head, last, vocab)
+
+    with torch.cuda.stream(st.s):
+        for _ in range(2):
+            forward()
+        torch.cuda.synchronize()
+        mm_events.clear()
+        steps = max(1, min(args.steps, 5))
+        e0 = st.event()
+        for _ in range(steps):
+            logits = forward()
+        e1 = st.event()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    mm_ms = sum(a.elapsed_time(b) for a, b in mm_events) / steps
+    per_layer = 2 * n_tok * d * ((d + 2 * nkv * hd) + d + 2 * ff + ff)
+    ops = n_layer * per_layer + 2 * d * vocab
+    assert torch.isfinite(logits).all()
+    res = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} Qwen2.5-7B-shaped prefill, {n_layer} layers, {n_tok} tokens",
+               ms=round(ms, 3), tokens_per_s=round(n_tok / ms * 1e3, 1), matmul_ms=round(mm_ms, 3),
+               matmul_tops=round(ops / mm_ms / 1e9, 1), steps=steps)
+    log(f"qwen_prefill: {res}")
+    for L in layers:
+        for key in ("qkv", "o", "gu", "down"):
+            L[key].free()
+    lm_head.free()
+    return res
+
+
 def cpu_baseline_q4(N, O, inputs, budget_s=12.0):
     """nncpu's AVX2 kernels (restated, oracle/avx2.cpp) on this host's cores,
     on the same weights (downloaded from the GPU) and the same quantized
@@ -276,7 +384,7 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="q4_sweep",
-                    choices=["q4_sweep", "prefill", "q8_vocab", "verify", "decode_f32", "all"])
+                    choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -291,6 +399,8 @@ def main():
     if args.workload in ("prefill", "all"):
         extra["prefill_m512"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
                                               N.ACT_I8, "prefill")
+    if args.workload in ("qwen_prefill", "all"):
+        extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d) for d in (1, 2)]
     if args.workload in ("q8_vocab", "all"):
         extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
     if args.workload in ("verify", "all"):
