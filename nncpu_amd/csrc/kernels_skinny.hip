@@ -3,22 +3,24 @@
 // 32-token MFMA.
 //
 // One v_mfma_i32_32x32x32_i8 per (32 weight rows, block): A = the
-// activations (MFMA rows i = tokens, padded to 32 by repeating the last
-// one), B = the weights (MFMA columns j = weight rows). Result element
-// (i, j) sits in lane j + 32h, register r with i = (r/4)*8 + 4h + r%4, so
-// tokens 0..7 are registers 0..3 and tokens 8..15 registers 4..7 of every
-// lane: only NR = 4 or 8 registers per lane carry real outputs, and the
-// scaling epilogue runs on those alone. The block dot products are exact;
-// the epilogue is the GEMM's (exact scale products from a two-block f32
-// outer-product MFMA, f64 accumulation), so every output is within one f32
-// ulp of the exact sum.
+// activations (MFMA rows i = tokens, padded to 32), B = the weights (MFMA
+// columns j = weight rows). Result element (i, j) sits in lane j + 32h,
+// register r with i = (r/4)*8 + 4h + r%4, so tokens 0..7 are registers 0..3
+// and tokens 8..15 registers 4..7 of every lane: only NR = 4 or 8 registers
+// per lane carry real outputs, and the scaling epilogue runs on those alone.
+// The block dot products are exact; the epilogue is the GEMM's (exact scale
+// products from a two-block f32 outer-product MFMA, f64 accumulation), so
+// every output is within one f32 ulp of the exact sum.
 //
-// Workgroup: 4 waves on 32 weight rows; the waves split the blocks into
-// contiguous ranges and stream them straight into registers (16 bytes per
-// lane and block, nontemporal), four blocks per group, double-buffered. Partial sums
-// meet in LDS and are added in wave order. Matrices with few row groups are
-// split along K over several workgroups as well; those partials go to a
-// workspace (f64) and a second kernel adds them in split order.
+// Workgroup: 4 waves on 32 weight rows. Weights, activations (tokens 0..15)
+// and scales stream through a ring of three LDS stages of 16 blocks, filled
+// by direct global -> LDS loads in which consecutive lanes read consecutive
+// 16-byte pieces of a row (coalesced), placed XOR-swizzled so the MFMA
+// operand reads are free of bank conflicts. Each wave computes 4 blocks of
+// a stage; the partial sums meet in LDS and are added in wave order.
+// Matrices with few row groups are split along K over several workgroups
+// as well; those partials go to a workspace (f64) and a second kernel adds
+// them in split order.
 
 #include "common.h"
 
@@ -28,9 +30,11 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int SK_W = 4;           // waves per workgroup
-constexpr int SK_G = 4;           // blocks per load group (even: scale products go in pairs)
+constexpr int SK_KC = 16;         // blocks per ring stage: 4 per wave
+constexpr int SK_TOK = 16;        // activation rows staged (tokens 0..15)
 constexpr int SK_MAX_SPLITS = 8;  // K-split workgroups per row group
 
 struct KArgs {
@@ -43,53 +47,128 @@ struct KArgs {
     size_t qrow, cols;
 };
 
-// One load group: the lane's 16 weight and 16 activation bytes of SK_G
-// blocks, and the scales of the pair members it contributes to the outer
-// products (lane half h gives block 2p + h of pair p).
+// One ring stage: SK_KC blocks of the workgroup's 32 weight rows and of
+// tokens 0..15, with their scales. Quant rows are XOR-swizzled at 16-byte
+// granularity (piece q of row r at position q ^ (r % 16)), so the MFMA
+// operand reads (32 rows, one piece each) hit 16 distinct bank groups.
 template <int DT>
-struct Group {
-    int4 w[SK_G], a[SK_G];
-    float sw[SK_G / 2], sx[SK_G / 2];
-    float bi[DT == 2 ? SK_G : 1], sxq[DT == 2 ? SK_G / 2 : 1];
+struct KStage {
+    static constexpr int QB = DT == 1 ? 32 : 16;  // weight bytes per row and block
+    static constexpr int WROW = SK_KC * QB;       // bytes per staged weight row
+    static constexpr int XROW = SK_KC * 32;       // bytes per staged token row
+    uint8_t W[32 * WROW];
+    int8_t X[SK_TOK * XROW];
+    float SW[SK_KC * 32];  // [blk][row]
+    float SX[SK_KC * 32];  // [blk][token]
+    float BI[DT == 2 ? SK_KC * 32 : 4];
+    float SXQ[DT == 2 ? SK_KC * 32 : 4];
 };
 
 template <int DT>
-__device__ __forceinline__ void load_group(Group<DT>& gr, const KArgs& g, const uint8_t* wrow, const int8_t* arow,
-                                           int b0, int kb1, int n0, int h, int c) {
+struct KPlan {
+    static constexpr int I_W = 32 * KStage<DT>::WROW / 1024;      // 1 KB per load instruction
+    static constexpr int I_X = SK_TOK * KStage<DT>::XROW / 1024;
+    static constexpr int I_S = SK_KC * 32 * 4 / 1024;              // per scale table
+    static constexpr int N_S = (DT == 2 ? 4 : 2) * I_S;
+    static constexpr int I_TOTAL = I_W + I_X + N_S;
+    static constexpr int PER_WAVE = I_TOTAL / SK_W;
+    static_assert(I_TOTAL % SK_W == 0 && I_W % SK_W == 0 && I_X % SK_W == 0, "loads split evenly over the waves");
+    static_assert(KStage<DT>::WROW / 16 >= 16 && KStage<DT>::XROW / 16 >= 16, "swizzle needs 16 pieces per row");
+    static_assert(2 * PER_WAVE < 64, "vmcnt holds at most 63");
+};
+
+// The load feeding staged position `pos` (16-byte units) of a swizzled
+// region with `ppr` pieces per row: row pos / ppr, global piece (pos % ppr)
+// ^ (row % 16). Consecutive lanes cover whole rows: coalesced.
+__device__ __forceinline__ void swz_src(int pos, int ppr, int& row, int& piece) {
+    row = pos / ppr;
+    piece = (pos - row * ppr) ^ (row & 15);
+}
+
+template <int DT>
+__device__ __forceinline__ void k_issue(KStage<DT>& st, const KArgs& g, int b0, int kb1, int wave, int lane, int n0) {
+    using P = KPlan<DT>;
+    constexpr int QB = KStage<DT>::QB;
 #pragma unroll
-    for (int k = 0; k < SK_G; ++k) {
-        const int b = b0 + k < kb1 ? b0 + k : kb1 - 1;  // past the range: reload the last block, unused
-        if (DT == 1)
-            gr.w[k] = load_nt16(wrow + (size_t)b * 32 + 16 * h);
-        else
-            gr.w[k] = load_nt16(wrow + (size_t)b * 16);
-        gr.a[k] = *(const int4*)(arow + (size_t)b * 32 + 16 * h);
-        if (DT == 2) gr.bi[k] = g.swT[(size_t)g.nb * g.rows_pad + (size_t)b * g.rows_pad + n0 + c];
-    }
-#pragma unroll
-    for (int p = 0; p < SK_G / 2; ++p) {
-        const int b = b0 + 2 * p + h < kb1 ? b0 + 2 * p + h : kb1 - 1;
-        gr.sw[p] = g.swT[(size_t)b * g.rows_pad + n0 + c];
-        gr.sx[p] = g.sxT[(size_t)b * g.tok_pad + c];
-        if (DT == 2) gr.sxq[p] = g.sxT[(size_t)g.nb * g.tok_pad + (size_t)b * g.tok_pad + c];
+    for (int k = 0; k < P::PER_WAVE; ++k) {
+        const int ins = SK_W * k + wave;  // uniform per wave
+        const void* src;
+        lds_ptr_t dst;
+        if (ins < P::I_W) {
+            int row, piece;
+            swz_src(ins * 64 + lane, KStage<DT>::WROW / 16, row, piece);
+            const int n = n0 + row < g.rows ? n0 + row : g.rows - 1;
+            // Pieces past the range repeat the last block (never used).
+            int b = b0 + piece * 16 / QB;
+            const int within = piece * 16 - (piece * 16 / QB) * QB;
+            if (b >= kb1) b = kb1 - 1;
+            src = g.qs + (size_t)n * g.qrow + (size_t)b * QB + within;
+            dst = (lds_ptr_t)&st.W[ins * 1024];
+        } else if (ins < P::I_W + P::I_X) {
+            const int i = ins - P::I_W;
+            int row, piece;
+            swz_src(i * 64 + lane, KStage<DT>::XROW / 16, row, piece);
+            const int t = row < g.n_tok ? row : g.n_tok - 1;
+            int b = b0 + (piece >> 1);
+            if (b >= kb1) b = kb1 - 1;
+            src = g.aq + (size_t)t * g.cols + (size_t)b * 32 + 16 * (piece & 1);
+            dst = (lds_ptr_t)&st.X[i * 1024];
+        } else {
+            // Scale tables, [blk][32] f32: 8 pieces of 4 floats per block.
+            const int i = ins - P::I_W - P::I_X;
+            const int table = i / P::I_S, j = i - table * P::I_S;
+            const int p = j * 64 + lane;
+            const int blk = p >> 3, r4 = (p & 7) * 4;
+            int b = b0 + blk;
+            if (b >= kb1) b = kb1 - 1;
+            float* base;
+            if (table == 0) {
+                src = g.swT + (size_t)b * g.rows_pad + n0 + r4;
+                base = st.SW;
+            } else if (table == 1) {
+                src = g.sxT + (size_t)b * g.tok_pad + r4;
+                base = st.SX;
+            } else if (table == 2) {
+                src = g.swT + (size_t)g.nb * g.rows_pad + (size_t)b * g.rows_pad + n0 + r4;
+                base = st.BI;
+            } else {
+                src = g.sxT + (size_t)g.nb * g.tok_pad + (size_t)b * g.tok_pad + r4;
+                base = st.SXQ;
+            }
+            dst = (lds_ptr_t)&base[j * 256];
+        }
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
     }
 }
 
+// s_waitcnt immediate with vmcnt = n (bits 3:0 and 15:14); expcnt and
+// lgkmcnt at their maxima, so they do not wait.
+#define NNH_SK_VMCNT(n) ((((n)&0xF) | (0x7 << 4) | (0xF << 8) | ((((n) >> 4) & 0x3) << 14)))
+
+// This wave's blocks 4w..4w+3 of the stage (those below nblk), in pairs for
+// the two-block scale outer products.
 template <int DT, int NR>
-__device__ __forceinline__ void compute_group(const Group<DT>& gr, double (&acc)[NR], int nblk, int h) {
+__device__ __forceinline__ void k_compute(const KStage<DT>& st, double (&acc)[NR], int nblk, int wave, int h,
+                                          int c) {
+    constexpr int QB = KStage<DT>::QB;
+    const int tc = c < SK_TOK ? c : SK_TOK - 1;  // tokens past 15: any staged row (results unused)
 #pragma unroll
-    for (int p = 0; p < SK_G / 2; ++p) {
-        if (2 * p >= nblk) break;
+    for (int jp = 0; jp < 4; jp += 2) {
+        const int j0 = 4 * wave + jp;
+        if (j0 >= nblk) break;
+        const int jh = j0 + h;  // this lane's block of the pair for the scale products
         const v32f z = {};
-        // s_x[token i] * s_w[row j] for blocks 2p and 2p + 1, exact in f32.
-        const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(gr.sx[p], gr.sw[p], z, 0, 0, 0);
+        // s_x[token i] * s_w[row j] for blocks j0 and j0 + 1, exact in f32.
+        const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(st.SX[jh * 32 + c], st.SW[jh * 32 + c], z, 0, 0, 0);
         v32f Q;
-        if (DT == 2) Q = __builtin_amdgcn_mfma_f32_32x32x1f32(gr.sxq[p], 1.0f, z, 0, 0, 0);  // s_x sum(q_x) [i]
+        if (DT == 2) Q = __builtin_amdgcn_mfma_f32_32x32x1f32(st.SXQ[jh * 32 + c], 1.0f, z, 0, 0, 0);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
-            const int k = 2 * p + jj;
-            if (k >= nblk) break;
-            int4 w = gr.w[k];
+            const int j = j0 + jj;
+            if (j >= nblk) break;
+            // Weights: row c, piece (QB == 32 ? 2j + h : j); activations: token tc, piece 2j + h.
+            const int wq = QB == 32 ? 2 * j + h : j;
+            int4 w = *(const int4*)&st.W[c * KStage<DT>::WROW + 16 * (wq ^ (c & 15))];
             if (DT == 2) {
                 const int sh = 4 * h, mk = 0x0f0f0f0f;
                 w.x = (int)((unsigned)w.x >> sh) & mk;
@@ -97,13 +176,14 @@ __device__ __forceinline__ void compute_group(const Group<DT>& gr, double (&acc)
                 w.z = (int)((unsigned)w.z >> sh) & mk;
                 w.w = (int)((unsigned)w.w >> sh) & mk;
             }
+            const int4 a = *(const int4*)&st.X[tc * KStage<DT>::XROW + 16 * ((2 * j + h) ^ (tc & 15))];
             const v16i zi = {};
-            const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(v4i{gr.a[k].x, gr.a[k].y, gr.a[k].z, gr.a[k].w},
-                                                                 v4i{w.x, w.y, w.z, w.w}, zi, 0, 0, 0);
+            const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(v4i{a.x, a.y, a.z, a.w}, v4i{w.x, w.y, w.z, w.w},
+                                                                 zi, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < NR; ++r) acc[r] = __builtin_fma((double)P[r], (double)S[16 * jj + r], acc[r]);
             if (DT == 2) {
-                const double bi = (double)gr.bi[k];  // bias[row] * (s_x sum q_x)[token], exact in f64
+                const double bi = (double)st.BI[j * 32 + c];  // bias[row] * (s_x sum q_x)[token], exact in f64
 #pragma unroll
                 for (int r = 0; r < NR; ++r) acc[r] = __builtin_fma(bi, (double)Q[16 * jj + r], acc[r]);
             }
@@ -112,35 +192,42 @@ __device__ __forceinline__ void compute_group(const Group<DT>& gr, double (&acc)
 }
 
 template <int DT, int NR>
+__device__ __forceinline__ void k_step(KStage<DT>& cur, KStage<DT>& nxt, const KArgs& g, int c, int nchunks, int kb0,
+                                       int kb1, double (&acc)[NR], int wave, int lane, int n0) {
+    if (c >= nchunks) return;
+    // This wave's loads of chunk c are done once at most chunk c + 1's are outstanding.
+    if (c + 1 < nchunks)
+        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT(KPlan<DT>::PER_WAVE));
+    else
+        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT(0));
+    __builtin_amdgcn_s_barrier();  // every wave's loads landed; every wave done with chunk c - 1
+    if (c + 2 < nchunks) k_issue<DT>(nxt, g, kb0 + (c + 2) * SK_KC, kb1, wave, lane, n0);
+    const int left = kb1 - kb0 - c * SK_KC;
+    k_compute<DT, NR>(cur, acc, left < SK_KC ? left : SK_KC, wave, lane >> 5, lane & 31);
+}
+
+template <int DT, int NR>
 __global__ __launch_bounds__(SK_W * 64) void skinny_i8_kernel(KArgs g, float* __restrict__ y, size_t y_stride) {
+    // Distinct objects, so the compiler sees that loads into one stage do not
+    // alias reads of another (one array would make it wait for every load).
+    __shared__ __attribute__((aligned(16))) KStage<DT> s0, s1, s2;
     __shared__ double red[SK_W][NR][64];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int h = lane >> 5, c = lane & 31;
     const int rg = blockIdx.x / g.ksplit, ks = blockIdx.x % g.ksplit;
     const int n0 = rg * 32;
-    const int n = n0 + c < g.rows ? n0 + c : g.rows - 1;  // rows and tokens past the end repeat the last
-    const int m = c < g.n_tok ? c : g.n_tok - 1;
-    const int parts = g.ksplit * SK_W, part = ks * SK_W + wave;
-    const int kb0 = (int)((long)part * g.nb / parts), kb1 = (int)((long)(part + 1) * g.nb / parts);
-    const uint8_t* wrow = g.qs + (size_t)n * g.qrow;
-    const int8_t* arow = g.aq + (size_t)m * g.cols;
+    const int kb0 = (int)((long)ks * g.nb / g.ksplit), kb1 = (int)((long)(ks + 1) * g.nb / g.ksplit);
+    const int nchunks = (kb1 - kb0 + SK_KC - 1) / SK_KC;
 
     double acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.0;
-    if (kb1 > kb0) {
-        const int ngroups = (kb1 - kb0 + SK_G - 1) / SK_G;
-        Group<DT> ga, gb;
-        load_group<DT>(ga, g, wrow, arow, kb0, kb1, n0, h, c);
-        for (int gi = 0; gi < ngroups; gi += 2) {
-            const int b0 = kb0 + gi * SK_G;
-            if (gi + 1 < ngroups) load_group<DT>(gb, g, wrow, arow, b0 + SK_G, kb1, n0, h, c);
-            compute_group<DT, NR>(ga, acc, kb1 - b0, h);
-            if (gi + 1 >= ngroups) break;
-            if (gi + 2 < ngroups) load_group<DT>(ga, g, wrow, arow, b0 + 2 * SK_G, kb1, n0, h, c);
-            compute_group<DT, NR>(gb, acc, kb1 - b0 - SK_G, h);
-        }
+    if (nchunks > 0) k_issue<DT>(s0, g, kb0, kb1, wave, lane, n0);
+    if (nchunks > 1) k_issue<DT>(s1, g, kb0 + SK_KC, kb1, wave, lane, n0);
+    for (int c = 0; c < nchunks; c += 3) {
+        k_step<DT, NR>(s0, s2, g, c, nchunks, kb0, kb1, acc, wave, lane, n0);
+        k_step<DT, NR>(s1, s0, g, c + 1, nchunks, kb0, kb1, acc, wave, lane, n0);
+        k_step<DT, NR>(s2, s1, g, c + 2, nchunks, kb0, kb1, acc, wave, lane, n0);
     }
 
 #pragma unroll
@@ -185,12 +272,12 @@ __global__ void skinny_reduce_kernel(const double* __restrict__ ws, int ksplit, 
 }  // namespace
 
 // K-split over workgroups when the row groups alone do not cover the CUs;
-// each wave keeps at least two blocks.
+// each split keeps at least one full ring stage.
 int skinny_splits(int rows, int nb) {
     const int groups = ceil_div(rows, 32);
     if (groups >= 160) return 1;
-    int ks = ceil_div(256, groups);
-    const int most = nb / (2 * SK_W);
+    int ks = 256 / groups;  // one workgroup per CU (the ring takes most of the LDS)
+    const int most = nb / SK_KC;
     if (ks > most) ks = most;
     if (ks > SK_MAX_SPLITS) ks = SK_MAX_SPLITS;
     return ks < 1 ? 1 : ks;

@@ -307,6 +307,8 @@ def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
     (1536, 64, 2048),   # 192 tiles: the unsplit path, nb = 2 (one partial chunk)
     (4100, 1536, 12),   # few-token kernel: ragged row group, K split over 2 workgroups
     (200, 96, 9),       # few-token kernel: nb = 3, a lone block in the last pair
+    (1536, 6144, 5),    # few-token kernel at its lower bound, K split over 5 workgroups
+    (96, 4128, 11),     # few-token kernel: nb = 129, a partial last stage, 3 row groups
     (6144, 1536, 8),    # few-token kernel, unsplit, tokens in registers 0-3 only
 ])
 def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
