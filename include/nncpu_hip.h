@@ -100,6 +100,13 @@ void nnh_free(nnh_weight* w);
 /* Shape and format of an uploaded weight. */
 int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols);
 
+/* Device address of the weight's split layout as uploaded (runtime.rs:136-164:
+ * quants, then BF16 scales, then Q4 biases), read-only, valid until
+ * nnh_free: the device form of Tensor::data, for callers that read rows
+ * directly, as the embedding lookup does with the tied token_embd
+ * (model/mod.rs:448-460). NULL for a NULL weight. */
+const void* nnh_weight_device_data(const nnh_weight* w);
+
 /* model_gemv (model/mod.rs:417-444): y[0..rows) = W x[0..cols).
  * Host buffers; synchronous. */
 int nnh_model_gemv(const nnh_weight* w, const float* x, float* y, int act);
@@ -122,6 +129,15 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
  * activations: calls on different streams must not overlap. */
 int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
                        size_t n_tok, int act, void* stream);
+
+/* Device-resident argmax of model_argmax (model/forward.rs:1003-1011) over
+ * n logits at v (device): the first largest value, NaN never winning and a
+ * NaN at index 0 keeping 0. Writes the index to *out_row (device, u64);
+ * asynchronous on `stream`. `work` is device memory of
+ * nnh_argmax_work_bytes(n) bytes, owned by the caller (so the call
+ * allocates nothing and can be captured in a HIP graph). */
+size_t nnh_argmax_work_bytes(size_t n);
+int nnh_argmax_dev(const float* v, size_t n, void* work, uint64_t* out_row, void* stream);
 
 /* ---- int8 activation blocks (device memory, caller-owned) ----
  * An activation buffer holds n_tok vectors of `cols` values quantized with

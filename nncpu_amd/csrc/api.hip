@@ -374,6 +374,21 @@ int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes) {
     return NNH_OK;
 }
 
+const void* nnh_weight_device_data(const nnh_weight* w) { return w ? (const void*)w->raw : nullptr; }
+
+size_t nnh_argmax_work_bytes(size_t n) { return nnh::argmax_partial_words(n) * 8; }
+
+int nnh_argmax_dev(const float* v, size_t n, void* work, uint64_t* out_row, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if (n == 0 || n >= ((size_t)1 << 32)) return fail(NNH_E_INVALID, "argmax: n must be in [1, 2^32)");
+    if (!v || !work || !out_row) return fail(NNH_E_INVALID, "argmax: null pointer");
+    nnh::launch_argmax(v, n, (uint64_t*)work, out_row, (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
 int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols) {
     if (!w) return fail(NNH_E_INVALID, "null weight");
     if (dtype) *dtype = w->dtype;

@@ -8,6 +8,11 @@ for bit), norms 1 + 0.1*N(0,1). The forward pass is nncpu's
 the CPU; its weight matmuls run through `nnh_gemv_batch` in the bit-exact
 f32 mode and the greedy lm_head through `nnh_model_argmax`. The prompt is
 evaluated in 16-token batches (session/engine.rs:362-380, PREFILL_BATCH).
+
+`Gemma3.generate_device` runs the same prefill, then decodes on the GPU
+alone (nncpu_amd/host/gemma3_gpu.hip): the forward's non-matmul steps as
+HIP kernels with the CPU restatement's arithmetic, one step captured in a
+HIP graph and replayed per token.
 """
 from __future__ import annotations
 
@@ -59,6 +64,18 @@ def _gemma_lib():
     L.nng_generate.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p,
                                C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(C.c_double), C.POINTER(C.c_double)]
     L.nng_generate.restype = C.c_int
+    L.nng_forward.argtypes, L.nng_forward.restype = [C.c_void_p, C.c_void_p, C.c_size_t], C.c_int
+    L.nng_argmax_last.argtypes, L.nng_argmax_last.restype = [C.c_void_p, C.c_size_t, C.POINTER(C.c_int32)], C.c_int
+    L.nng_state.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(C.c_size_t),
+                            C.POINTER(C.POINTER(C.c_uint64)), C.POINTER(C.c_size_t)]
+    L.nng_fnv_many.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
+    L.nngd_create.argtypes = [C.POINTER(NngConfig), C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+    L.nngd_create.restype = C.c_int
+    L.nngd_free.argtypes = [C.c_void_p]
+    L.nngd_error.argtypes, L.nngd_error.restype = [C.c_void_p], C.c_char_p
+    L.nngd_decode.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int, C.c_void_p, C.c_void_p,
+                              C.POINTER(C.c_double)]
+    L.nngd_decode.restype = C.c_int
     return L
 
 
@@ -114,6 +131,62 @@ class Gemma3:
         gemv = C.cast(self._lib.nng_gpu_gemv, C.c_void_p).value
         argmax = C.cast(self._lib.nng_gpu_argmax, C.c_void_p).value
         return self.generate(prompt, n_gen, gemv, argmax, C.pointer(ctx))
+
+    def generate_device(self, prompt: np.ndarray, n_gen: int, batch: int = 16):
+        """The prompt as in generate_gpu (CPU forward, GPU matmuls), then the
+        decode resident on the GPU. (tokens, per-layer hashes, prefill
+        seconds, decode seconds)."""
+        import time
+        L = self._lib
+        arr = (C.c_void_p * len(self.weights))(*[w.handle for w in self.weights])
+        ctx = NngGpuCtx(w=C.cast(arr, C.POINTER(C.c_void_p)), n=len(self.weights), act=ACT_F32)
+        self._keep = (arr, ctx)
+        gemv = C.cast(L.nng_gpu_gemv, C.c_void_p).value
+        argmax = C.cast(L.nng_gpu_argmax, C.c_void_p).value
+        m = L.nng_create(C.byref(self.cfg), self.norms.ctypes.data_as(C.c_void_p),
+                         self.token_embd.ctypes.data_as(C.c_void_p), gemv, argmax, C.cast(C.pointer(ctx), C.c_void_p))
+        try:
+            t0 = time.perf_counter()
+            prompt = np.ascontiguousarray(prompt, np.int32)
+            last = 0
+            for p in range(0, len(prompt), batch):
+                n = min(batch, len(prompt) - p)
+                if L.nng_forward(m, prompt[p:].ctypes.data_as(C.c_void_p), n):
+                    raise RuntimeError(L.nng_error(m).decode())
+                last = n
+            tok = C.c_int32()
+            if L.nng_argmax_last(m, last, C.byref(tok)):
+                raise RuntimeError(L.nng_error(m).decode())
+            t_prefill = time.perf_counter() - t0
+            if getattr(self, "_dev", None) is None:
+                md = C.c_void_p()
+                rc = L.nngd_create(C.byref(self.cfg), self.norms.ctypes.data_as(C.c_void_p), arr, len(self.weights),
+                                   max(n_gen, 1), C.byref(md))
+                if rc:
+                    msg = L.nngd_error(md).decode()
+                    L.nngd_free(md)
+                    raise RuntimeError(msg)
+                self._dev = md
+            E, nl = self.cfg.n_embd, self.cfg.n_layer
+            out = np.zeros(n_gen, np.int32)
+            record = np.zeros(max(n_gen - 1, 0) * nl * E, np.float32)
+            secs = C.c_double()
+            if L.nngd_decode(self._dev, m, tok.value, n_gen, out.ctypes.data_as(C.c_void_p),
+                             record.ctypes.data_as(C.c_void_p), C.byref(secs)):
+                raise RuntimeError(L.nngd_error(self._dev).decode())
+            hp, nh = C.POINTER(C.c_uint64)(), C.c_size_t()
+            L.nng_state(m, None, None, None, C.byref(hp), C.byref(nh))
+            pre = np.ctypeslib.as_array(hp, shape=(nh.value,)).copy() if nh.value else np.zeros(0, np.uint64)
+            dec = np.zeros(max(n_gen - 1, 0) * nl, np.uint64)
+            L.nng_fnv_many(record.ctypes.data_as(C.c_void_p), E, len(dec), dec.ctypes.data_as(C.c_void_p))
+            return out, np.concatenate([pre, dec]), t_prefill, secs.value
+        finally:
+            L.nng_free(m)
+
+    def free(self):
+        if getattr(self, "_dev", None) is not None:
+            self._lib.nngd_free(self._dev)
+            self._dev = None
 
 
 def random_prompt(n: int, n_vocab: int, seed: int = 0x9A0) -> np.ndarray:

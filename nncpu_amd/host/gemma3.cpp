@@ -19,6 +19,7 @@
 #include <string>
 #include <vector>
 
+#include "gemma3.h"
 #include "nncpu_hip.h"
 
 namespace {
@@ -214,12 +215,6 @@ void attn_span(size_t window, size_t pos, size_t n_seq, size_t* first, size_t* l
 
 extern "C" {
 
-// The hyperparameters of a Gemma-3 model (model/load.rs:431-595).
-struct nng_config {
-    int n_layer, n_embd, n_head, n_kv, head_dim, n_ff, n_vocab, n_ctx;
-    float rms_eps, rope_base, rope_base_swa, attn_scale;
-    int window, swa_period;
-};
 
 // y (n_tok vectors, y_stride apart) = matrix `id` x (x_stride apart), the
 // gemv_batch contract; returns 0 on success. id = 7*layer + {0 q, 1 k, 2 v,
@@ -275,6 +270,12 @@ static uint64_t fnv(const float* v, size_t n) {
     const uint8_t* p = (const uint8_t*)v;
     for (size_t i = 0; i < 4 * n; ++i) h = (h ^ p[i]) * 1099511628211ull;
     return h;
+}
+
+// The per-layer hash the forward records (FNV-1a of the residual's bytes),
+// for hidden states recorded elsewhere: count states of n floats each.
+void nng_fnv_many(const float* v, size_t n, size_t count, uint64_t* out) {
+    for (size_t i = 0; i < count; ++i) out[i] = fnv(v + i * n, n);
 }
 
 // model_forward (forward.rs:848-965) for n_tok tokens at cur_pos.
@@ -388,6 +389,18 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
     }
     rmsnorm_gamma_multi(m->x.data(), m->x.data(), n_tok * E, E, m->norms.data() + ns * c.n_layer, c.rms_eps);
     m->cur_pos = pos0 + n_tok;
+    return 0;
+}
+
+// The decode state after the forwards so far: KV caches ([n_layer][n_ctx]
+// [kv_dim] BF16), the next position, and the per-layer hashes recorded.
+int nng_state(nng_model* m, const uint16_t** kcache, const uint16_t** vcache, size_t* pos, const uint64_t** hashes,
+              size_t* n_hashes) {
+    if (kcache) *kcache = m->kcache.data();
+    if (vcache) *vcache = m->vcache.data();
+    if (pos) *pos = m->cur_pos;
+    if (hashes) *hashes = m->layer_hash.data();
+    if (n_hashes) *n_hashes = m->layer_hash.size();
     return 0;
 }
 

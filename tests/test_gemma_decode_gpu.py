@@ -48,20 +48,50 @@ def cpu_generate(oracle, model, prompt, n_gen):
     return out
 
 
-def test_gemma3_1b_decode_token_identical(oracle, model):
+PROMPT_LEN, N_GEN = 32, 128
+
+
+@pytest.fixture(scope="module")
+def cpu_run(oracle, model):
     from nncpu_amd.gemma import random_prompt
-    prompt = random_prompt(32, model.cfg.n_vocab)
-    print("gpu decode", flush=True)
-    tg, hg, tpg, tdg = model.generate_gpu(prompt, 128)
-    print(f"gpu: prefill {tpg:.3f}s decode {tdg:.3f}s ({127 / tdg:.1f} tok/s)", flush=True)
+    prompt = random_prompt(PROMPT_LEN, model.cfg.n_vocab)
     print("cpu decode", flush=True)
-    tc, hc, tpc, tdc = cpu_generate(oracle, model, prompt, 128)
-    print(f"cpu: prefill {tpc:.3f}s decode {tdc:.3f}s ({127 / tdc:.1f} tok/s)", flush=True)
-    assert len(hg) == len(hc) == (2 + 127) * model.cfg.n_layer
+    tc, hc, tpc, tdc = cpu_generate(oracle, model, prompt, N_GEN)
+    print(f"cpu: prefill {tpc:.3f}s decode {tdc:.3f}s ({(N_GEN - 1) / tdc:.1f} tok/s)", flush=True)
+    return prompt, tc, hc
+
+
+def check_same(model, tg, hg, tc, hc):
+    assert len(hg) == len(hc) == (2 + N_GEN - 1) * model.cfg.n_layer
     assert np.array_equal(tg, tc), np.nonzero(tg != tc)[0][:5]
     assert np.array_equal(hg, hc), np.nonzero(hg != hc)[0][:5]
     # Random weights settle greedy decoding on few tokens, but every step's
     # hidden state is new: the last layer's hashes are all distinct.
     last = hg[model.cfg.n_layer - 1::model.cfg.n_layer]
     assert len(set(last.tolist())) == len(last)
+
+
+def test_gemma3_1b_decode_token_identical(model, cpu_run):
+    prompt, tc, hc = cpu_run
+    print("gpu decode (matmuls on the GPU)", flush=True)
+    tg, hg, tpg, tdg = model.generate_gpu(prompt, N_GEN)
+    print(f"gpu: prefill {tpg:.3f}s decode {tdg:.3f}s ({(N_GEN - 1) / tdg:.1f} tok/s)", flush=True)
+    check_same(model, tg, hg, tc, hc)
+    sys.stdout.flush()
+
+
+def test_gemma3_1b_device_decode_token_identical(model, cpu_run):
+    # The decode step resident on the GPU (norms, RoPE, attention, GELU as
+    # HIP kernels; one step captured in a HIP graph and replayed per token):
+    # the same tokens and per-layer hidden states as the CPU run, including
+    # every graph replay.
+    prompt, tc, hc = cpu_run
+    print("device-resident decode", flush=True)
+    tg, hg, tpg, tdg = model.generate_device(prompt, N_GEN)
+    print(f"device: prefill {tpg:.3f}s decode {tdg:.3f}s ({(N_GEN - 1) / tdg:.1f} tok/s)", flush=True)
+    check_same(model, tg, hg, tc, hc)
+    # A second run replays the captured graph from a fresh prefill.
+    tg2, hg2, _, tdg2 = model.generate_device(prompt, N_GEN)
+    print(f"device (graph reused): decode {tdg2:.3f}s ({(N_GEN - 1) / tdg2:.1f} tok/s)", flush=True)
+    check_same(model, tg2, hg2, tc, hc)
     sys.stdout.flush()
