@@ -107,6 +107,25 @@ int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols)
  * (model/mod.rs:448-460). NULL for a NULL weight. */
 const void* nnh_weight_device_data(const nnh_weight* w);
 
+/* The bit-exact f32 path's device layout of a weight: the quants regrouped
+ * per lane (16 lanes per row: Q8_0 groups of 8 blocks, lane j's 16 bytes
+ * holding elements j and j + 16 of each block; Q4 groups of 16 blocks, lane
+ * j's 16 bytes holding byte j of each), the BF16 scale rows padded to `nbp`
+ * blocks, and the Q4 biases as uploaded. For callers that fuse their own
+ * work around that matmul, as the device-resident decode step does; no
+ * counterpart in the reference, whose forward calls the matmul per weight.
+ * NNH_E_INVALID when the weight is tall (16384 rows or more with x of at
+ * most 64 KB: those take the 8-lane layout instead). Read-only, valid until
+ * nnh_free. */
+typedef struct {
+    const void* quants;
+    const uint16_t* scales;
+    const uint16_t* biases; /* Q4 only, else NULL */
+    size_t rows, cols, nb, nbp;
+    int dtype;
+} nnh_f32_layout;
+int nnh_weight_f32_layout(const nnh_weight* w, nnh_f32_layout* out);
+
 /* model_gemv (model/mod.rs:417-444): y[0..rows) = W x[0..cols).
  * Host buffers; synchronous. */
 int nnh_model_gemv(const nnh_weight* w, const float* x, float* y, int act);

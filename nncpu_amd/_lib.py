@@ -80,6 +80,7 @@ def _declare(L):
     L.nnh_block_dots_dev.argtypes, L.nnh_block_dots_dev.restype = [vp, vp, sz, vp, vp], i32
     L.nnh_sync.argtypes, L.nnh_sync.restype = [vp], i32
     L.nnh_weight_device_data.argtypes, L.nnh_weight_device_data.restype = [vp], vp
+    L.nnh_weight_f32_layout.argtypes, L.nnh_weight_f32_layout.restype = [vp, vp], i32
     L.nnh_argmax_work_bytes.argtypes, L.nnh_argmax_work_bytes.restype = [sz], sz
     L.nnh_argmax_dev.argtypes, L.nnh_argmax_dev.restype = [vp, sz, vp, vp, vp], i32
 

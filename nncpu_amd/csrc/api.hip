@@ -170,11 +170,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
              uint8_t* scratch, hipStream_t st) {
     const int rows = (int)w->rows, nb = (int)w->nb;
     if (act == NNH_ACT_F32) {
-        float* xsum = nullptr;
-        if (w->dtype == NNH_Q4S) {
-            xsum = (float*)scratch;
-            nnh::launch_block_sums(x, x_stride, nb, (int)n_tok, xsum, st);
-        }
+        float* xsum = w->dtype == NNH_Q4S ? (float*)scratch : nullptr;
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
                              y, y_stride, w->f32v2, st);
     } else {
@@ -248,7 +244,9 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     w->f32v2 = rows >= F32_V2_MIN_ROWS && cols * 4 <= (size_t)nnh::F32_V2_MAX_LDS;
     hipError_t e;
     if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2)))) !=
+        // 256 spare bytes: the one-vector kernel's first group load of the
+        // last row stays inside the allocation when a row has no whole group.
+        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2) + 256))) !=
             hipSuccess ||
         (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
         (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||
@@ -386,6 +384,15 @@ int nnh_argmax_dev(const float* v, size_t n, void* work, uint64_t* out_row, void
     if (!v || !work || !out_row) return fail(NNH_E_INVALID, "argmax: null pointer");
     nnh::launch_argmax(v, n, (uint64_t*)work, out_row, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_weight_f32_layout(const nnh_weight* w, nnh_f32_layout* out) {
+    int rc = check_weight(w);
+    if (rc) return rc;
+    if (!out) return fail(NNH_E_INVALID, "f32 layout: null output");
+    if (w->f32v2) return fail(NNH_E_INVALID, "f32 layout: tall weight (8-lane layout)");
+    *out = nnh_f32_layout{w->fq, w->fs, w->bi, w->rows, w->cols, w->nb, w->nbp, w->dtype};
     return NNH_OK;
 }
 

@@ -73,9 +73,10 @@ void launch_relayout_f32(int dtype, const uint8_t* raw_qs, const uint16_t* raw_s
                          int rows, int nb, int nbp, bool v2, hipStream_t st);
 // Q4 block sums of n_tok vectors (kernels/scalar.rs:355-359 tree).
 void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float* xsum, hipStream_t st);
-// Bit-exact f32 gemv for n_tok <= 16 vectors.
+// Bit-exact f32 gemv for n_tok <= 16 vectors; for Q4, xsum is scratch of
+// n_tok * nb floats (the block sums of x).
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
-                     size_t x_stride, const float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
+                     size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st);
 
 // int8 path (kernels_i8.hip).

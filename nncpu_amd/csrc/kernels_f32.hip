@@ -44,6 +44,7 @@
 // and an in-lane pair sum (hsum8): the same additions.
 
 #include "common.h"
+#include "f32_m1.h"
 
 namespace nnh {
 namespace {
@@ -164,16 +165,6 @@ __global__ void block_sums_kernel(const float* __restrict__ x, size_t x_stride, 
                           __fadd_rn(__fadd_rn(v[2], v[6]), __fadd_rn(v[3], v[7])));
 }
 
-__device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
-    uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
-    return (w >> (8 * (i & 3))) & 0xffu;
-}
-
-__device__ __forceinline__ uint32_t half_of(const uint4& v, int i) {
-    uint32_t w = i < 2 ? v.x : i < 4 ? v.y : i < 6 ? v.z : v.w;
-    return (w >> (16 * (i & 1))) & 0xffffu;
-}
-
 // Per-token FMA step for the lane's two chains of block b.
 template <int M>
 __device__ __forceinline__ void step(float (&a0)[M], float (&a1)[M], float w0, float w1, const float* __restrict__ x,
@@ -289,8 +280,169 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
     }
 }
 
-// The 8-lane mapping (tall matrices).
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+// One vector (f32_m1.h): 16 rows per workgroup, x in LDS, a ring of D
+// weight groups in flight per lane. LDS: x [cols]; Q4 adds the block sums
+// [nb] and the workgroup's biases [16][nb]. Loads issued before the ring are
+// unconditional (clamped indices), so waiting for them never waits for it.
+constexpr int M1_MAX_NB = 256;               // x of at most 8192 columns
+constexpr int M1_XCH = M1_MAX_NB * 32 / 1024;  // 16-byte x pieces per thread
+constexpr int M1_BCH = M1_ROWS * M1_MAX_NB / 256;  // Q4 biases per thread
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void gemv_f32_m1_kernel(F32Mat m, const float* __restrict__ x,
+                                                          float* __restrict__ y) {
+    extern __shared__ float lds[];
+    const int tid = threadIdx.x, nb = m.nb, cols = nb * 32, n4 = cols / 4;
+    float4 xr[M1_XCH];
+#pragma unroll
+    for (int k = 0; k < M1_XCH; ++k)
+        xr[k] = __builtin_bit_cast(float4, *(const f4u*)(x + 4 * min(tid + 256 * k, n4 - 1)));
+    const int row0 = blockIdx.x * M1_ROWS;
+    const int nbias = DT == 2 ? min(M1_ROWS, m.rows - row0) * nb : 0;
+    uint16_t br[M1_BCH];
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < M1_BCH; ++k) br[k] = m.bi[(size_t)row0 * nb + min(tid + 256 * k, nbias - 1)];
+    }
+    const int row_raw = row0 + (tid >> 4);
+    const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
+    M1Lane<DT, D> L;
+    L.init(m, row, tid & 15);
+    // Keep the order: the loads above, then the ring, then the LDS stores that
+    // wait for the former only.
+    __builtin_amdgcn_sched_barrier(0);
+    L.prefetch();
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional stores (a clamped piece stores its own values again): a
+    // conditional one would let the compiler sink the x load past the ring.
+#pragma unroll
+    for (int k = 0; k < M1_XCH; ++k) *(float4*)(lds + 4 * min(tid + 256 * k, n4 - 1)) = xr[k];
+    float* xs = lds + cols;
+    uint16_t* bl = (uint16_t*)(xs + nb);
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < M1_BCH; ++k) bl[min(tid + 256 * k, nbias - 1)] = br[k];
+    }
+    lds_barrier();
+    if (DT == 2) {
+        for (int b = tid; b < nb; b += 256) xs[b] = m1_block_sum(lds + 32 * b);
+        lds_barrier();
+    }
+    L.run(lds);
+    float r = L.reduce();
+    if (DT == 2) r = __fadd_rn(r, m1_bias_dot(bl + (row - row0) * nb, xs, nb, tid & 15));
+    if (row_raw < m.rows && (tid & 15) == 0) y[row_raw] = r;
+}
+
+// The wide one-vector kernel (long rows): 32 lanes per row, 8 rows per
+// workgroup, every group of a row in flight at once. LDS: x transposed
+// [32][S], the workgroup's scale rows [8][nbp]; Q4 adds the block sums [nb]
+// and the biases [8][nb].
+constexpr int M1W_ROWS = 8;
+constexpr int M1W_MIN_NB = 64;  // rows of at least 2048 columns
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void gemv_f32_m1w_kernel(F32Mat m, const float* __restrict__ x,
+                                                           float* __restrict__ y) {
+    extern __shared__ float lds[];
+    const int tid = threadIdx.x, nb = m.nb, cols = nb * 32, n4 = cols / 4, S = m1w_stride(nb);
+    float4 xr[M1_XCH];
+#pragma unroll
+    for (int k = 0; k < M1_XCH; ++k)
+        xr[k] = __builtin_bit_cast(float4, *(const f4u*)(x + 4 * min(tid + 256 * k, n4 - 1)));
+    const int row0 = blockIdx.x * M1W_ROWS, nrows = min(M1W_ROWS, m.rows - row0);
+    // The scale rows (16-byte pieces; nbp is a multiple of 8).
+    constexpr int SCH = M1W_ROWS * M1_MAX_NB * 2 / 16 / 256;
+    const int nsp = nrows * m.nbp / 8;
+    uint4 sr[SCH];
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) sr[k] = *(const uint4*)(m.fs + (size_t)row0 * m.nbp + 8 * min(tid + 256 * k, nsp - 1));
+    const int nbias = DT == 2 ? nrows * nb : 0;
+    constexpr int BCH = M1W_ROWS * M1_MAX_NB / 256;
+    uint16_t br[BCH];
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < BCH; ++k) br[k] = m.bi[(size_t)row0 * nb + min(tid + 256 * k, nbias - 1)];
+    }
+    const int row_raw = row0 + (tid >> 5);
+    const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
+    M1Wide<DT, D> L;
+    L.init(m, row, tid & 31);
+    // Keep the order: the loads above, then the ring, then the LDS stores that
+    // wait for the former only.
+    __builtin_amdgcn_sched_barrier(0);
+    L.prefetch();
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional stores (a clamped piece stores its own values again): a
+    // conditional one would let the compiler sink the x load past the ring.
+#pragma unroll
+    for (int k = 0; k < M1_XCH; ++k) {
+        const int p = min(tid + 256 * k, n4 - 1);
+        const int b = p >> 3, c = (4 * p) & 31;
+        lds[m1w_xpos(b, c, S)] = xr[k].x;
+        lds[m1w_xpos(b, c + 1, S)] = xr[k].y;
+        lds[m1w_xpos(b, c + 2, S)] = xr[k].z;
+        lds[m1w_xpos(b, c + 3, S)] = xr[k].w;
+    }
+    uint16_t* sl = (uint16_t*)(lds + 32 * S);
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) *(uint4*)(sl + 8 * min(tid + 256 * k, nsp - 1)) = sr[k];
+    float* xs = (float*)(sl + M1W_ROWS * m.nbp);
+    uint16_t* bl = (uint16_t*)(xs + nb);
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < BCH; ++k) bl[min(tid + 256 * k, nbias - 1)] = br[k];
+    }
+    lds_barrier();
+    if (DT == 2) {
+        for (int b = tid; b < nb; b += 256) {
+            float c[32];
+#pragma unroll
+            for (int e = 0; e < 32; ++e) c[e] = lds[m1w_xpos(b, e, S)];
+            xs[b] = m1_block_sum(c);
+        }
+        lds_barrier();
+    }
+    L.run(lds, sl + (row - row0) * m.nbp);
+    float r = L.reduce();
+    if (DT == 2) r = __fadd_rn(r, m1_bias_dot(bl + (row - row0) * nb, xs, nb, tid & 31));
+    if (row_raw < m.rows && (tid & 31) == 0) y[row_raw] = r;
+}
+
+// Ring depth: eight groups where the row has them (Q4: four of 16 blocks),
+// else four (two), so a short row loads no group twice; rows of M1W_MIN_NB
+// blocks or more take the wide kernel with sixteen (eight).
+template <int DT>
+void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, int rows, int nb, int nbp,
+               float* y, hipStream_t st) {
+    const F32Mat m{fq, fs, bi, rows, nb, nbp};
+    const int ng = nb / (DT == 1 ? 8 : 16), deep = DT == 1 ? 8 : 4;
+    const dim3 block(256);
+    if (nb >= M1W_MIN_NB) {
+        // Ring slots for every group: 8, 16 or 32 (Q8 groups number nb / 8 <= 32).
+        const size_t S = ((nb + 3) & ~3) + (((nb + 3) & 4) ? 0 : 4);
+        const size_t lds = 32 * S * 4 + (size_t)M1W_ROWS * nbp * 2 +
+                           (DT == 2 ? (size_t)nb * 4 + (size_t)M1W_ROWS * nb * 2 : 0);
+        const dim3 grid(ceil_div(rows, M1W_ROWS));
+        if (ng <= 8)
+            gemv_f32_m1w_kernel<DT, 8><<<grid, block, lds, st>>>(m, x, y);
+        else if (ng <= 16)
+            gemv_f32_m1w_kernel<DT, 16><<<grid, block, lds, st>>>(m, x, y);
+        else
+            gemv_f32_m1w_kernel<DT, 32><<<grid, block, lds, st>>>(m, x, y);
+        return;
+    }
+    const size_t lds = (size_t)nb * 32 * 4 + (DT == 2 ? (size_t)nb * 4 + (size_t)M1_ROWS * nb * 2 : 0);
+    const dim3 grid(ceil_div(rows, M1_ROWS));
+    if (ng >= deep)
+        gemv_f32_m1_kernel<DT, DT == 1 ? 8 : 4><<<grid, block, lds, st>>>(m, x, y);
+    else
+        gemv_f32_m1_kernel<DT, DT == 1 ? 4 : 2><<<grid, block, lds, st>>>(m, x, y);
+}
+
+// The 8-lane mapping (tall matrices).
 
 constexpr int V2_R = 4;  // rows per lane group: four rows share every x load
 
@@ -532,8 +684,10 @@ void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float
 // Tokens in chunks of up to four per launch: every token's chains are
 // independent, so the chunking never changes a bit.
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
-                     size_t x_stride, const float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
+                     size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st) {
+    // Q4 block sums, except for the one-vector kernel, which forms its own.
+    if (dtype == 2 && !(n_tok == 1 && !v2 && nb <= M1_MAX_NB)) launch_block_sums(x, x_stride, nb, n_tok, xsum, st);
     // The 8-lane kernel keeps x in LDS: at most 64 KB of it per launch.
     int per = 4;
     if (v2 && per * nb * 32 * 4 > F32_V2_MAX_LDS) per = F32_V2_MAX_LDS / (nb * 32 * 4);
@@ -542,7 +696,12 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
         const float* xt = x + (size_t)t0 * x_stride;
         const float* st_xsum = xsum ? xsum + (size_t)t0 * nb : nullptr;
         float* yt = y + (size_t)t0 * y_stride;
-        if (v2) {
+        if (m == 1 && !v2 && nb <= M1_MAX_NB) {
+            if (dtype == 1)
+                launch_m1<1>(fq, fs, biases, xt, rows, nb, nbp, yt, st);
+            else
+                launch_m1<2>(fq, fs, biases, xt, rows, nb, nbp, yt, st);
+        } else if (v2) {
             if (dtype == 1)
                 launch_dt_v2<1>(m, fq, fs, biases, xt, x_stride, st_xsum, rows, nb, nbp, yt, y_stride, st);
             else

@@ -2,11 +2,30 @@
 // (crates/nncpu/src/model/forward.rs:197-439, 719-965 with the scalar.rs
 // non-matmul kernels) for one token, with every operation in the same order
 // and rounding as that CPU restatement, so a decode gives the same tokens and
-// the same per-layer hidden states bit for bit. The weight matmuls are the
-// library's bit-exact f32 path (nnh_gemv_batch_dev), the lm_head argmax is
-// nnh_argmax_dev, the token and the position live in device memory, and one
-// step is captured once in a HIP graph and replayed per generated token: no
-// host round trip inside the decode loop.
+// the same per-layer hidden states bit for bit. The token and the position
+// live in device memory, and one step is captured once in a HIP graph and
+// replayed per generated token: no host round trip inside the decode loop.
+//
+// Five kernels per layer. Every kernel boundary costs a few microseconds on
+// this GPU, so the non-matmul work rides on the matmul kernels around it:
+//   qkv   the previous layer's post-FFW RMSNorm and residual add (or, in
+//         layer 0, the embedding row), the attention RMSNorm, then the q, k
+//         and v matmuls (one launch over the three matrices);
+//   attn  the q / k RMSNorms, NeoX RoPE, the K/V append and the attention,
+//         one workgroup per query head;
+//   o     the output projection (the library's one-vector kernel);
+//   ffn   the post-attention RMSNorm and residual, the FFN RMSNorm, then the
+//         gate and up matmuls with GELU(gate) * up in the epilogue (a
+//         workgroup runs eight rows of each);
+//   down  the down projection (the library's one-vector kernel).
+// The residual and norm prologue is recomputed by every workgroup of its
+// kernel (the same operations, so the same bits), while the weight loads of
+// the matmul are already in flight; workgroup 0 stores the new residual.
+// The residual stream alternates between two buffers, so no kernel reads the
+// buffer it writes. The matmuls are the library's bit-exact f32 path: its
+// one-vector core (f32_m1.h) on the 16-lane weight layout that
+// nnh_weight_f32_layout exposes, and nnh_gemv_batch_dev / nnh_argmax_dev for
+// the lm_head.
 //
 // What is taken from the host: RoPE's cos / sin per position (computed with
 // the CPU restatement's own libm calls, uploaded once) and the embedding
@@ -23,14 +42,25 @@
 #include <string>
 #include <vector>
 
+#include "f32_m1.h"
 #include "gemma3.h"
 #include "nncpu_hip.h"
 
 namespace {
 
-constexpr int ATTN_BLOCK = 256;  // model/mod.rs:84-87
+using nnh::F32Mat;
+using nnh::lds_barrier;
+using nnh::M1_ROWS;
+using nnh::M1Lane;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 
-__device__ __forceinline__ float bf16f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+constexpr int ATTN_BLOCK = 256;  // model/mod.rs:84-87
+constexpr int WG = 256;          // threads per workgroup
+constexpr int E_MAX = 2048;      // residual width: two 4-float pieces per thread
+constexpr int ECH = E_MAX / 4 / WG;
+
+__device__ __forceinline__ float bf16f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ uint16_t to_bf16(float f) {
     const uint32_t u = __float_as_uint(f);
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
@@ -39,6 +69,14 @@ __device__ __forceinline__ float hsum8(const float* v) {
     return __fadd_rn(__fadd_rn(__fadd_rn(v[0], v[4]), __fadd_rn(v[1], v[5])),
                      __fadd_rn(__fadd_rn(v[2], v[6]), __fadd_rn(v[3], v[7])));
 }
+// hsum8 of lanes 0..7's values, by lane exchanges (valid at lane 0):
+// xor-4 gives v_l + v_{l+4}, xor-1 and xor-2 then add those pairs as hsum8 does.
+__device__ __forceinline__ float hsum8_lanes(float a) {
+    const float p = __fadd_rn(a, __shfl_xor(a, 4, 64));
+    const float q = __fadd_rn(p, __shfl_xor(p, 1, 64));
+    return __fadd_rn(q, __shfl_xor(q, 2, 64));
+}
+__device__ __forceinline__ float4 ld4(const float* p) { return __builtin_bit_cast(float4, *(const f4u*)p); }
 
 // scalar.rs:19-84 (gemma3.cpp exp_lane).
 __device__ float exp_lane(float x) {
@@ -72,160 +110,444 @@ __device__ float gelu_lane(float v) {
     return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, t));
 }
 
-// RMSNorm x gamma of one group of `dim` values by the whole workgroup
-// (scalar.rs:232-292, gemma3.cpp sum_sq / rmsnorm_gamma_multi): eight FMA
-// lanes over whole chunks of 8, hsum8, the tail in f64, scale
-// (float)(1 / sqrt(ss * inv_dim + eps)) in f64. y may alias x.
-__device__ void rmsnorm_wg(const float* x, const float* gamma, float* y, int dim, float eps) {
-    __shared__ float lanes[8];
-    __shared__ float scale_s;
-    const int body = dim & ~7;
-    if (threadIdx.x < 8) {
-        float a = 0.0f;
-        for (int i = 0; i < body; i += 8) a = __fmaf_rn(x[i + threadIdx.x], x[i + threadIdx.x], a);
-        lanes[threadIdx.x] = a;
+// A chain input in LDS, transposed: element e of a dim-vector (dim a
+// multiple of 32) at (e % 8) * S + e / 8, S = dim / 8 + 4, so FMA lane l's
+// values are contiguous (16-byte reads) and the 4-float pad spreads the eight
+// lanes' reads over the banks.
+__device__ __forceinline__ int tstride(int dim) { return dim / 8 + 4; }
+__device__ __forceinline__ void tput4(float* xt, int S, int piece, float4 v) {
+    float* p = xt + 4 * (piece & 1) * S + (piece >> 1);
+    p[0] = v.x;
+    p[S] = v.y;
+    p[2 * S] = v.z;
+    p[3 * S] = v.w;
+}
+
+// hsum8 of the eight FMA lanes' sums of squares of a transposed dim-vector
+// (dim % 32 == 0), run by lanes 0..7 of the calling wave; valid at lane 0.
+__device__ __forceinline__ float chain_sumsq(const float* xt, int dim, int lane) {
+    float a = 0.0f;
+    if (lane < 8) {
+        const float4* p = (const float4*)(xt + lane * tstride(dim));
+#pragma unroll 12
+        for (int m = 0; m < dim / 32; ++m) {
+            const float4 v = p[m];
+            a = __fmaf_rn(v.x, v.x, a);
+            a = __fmaf_rn(v.y, v.y, a);
+            a = __fmaf_rn(v.z, v.z, a);
+            a = __fmaf_rn(v.w, v.w, a);
+        }
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double s = dim >= 8 ? (double)hsum8(lanes) : 0.0;
-        for (int i = body; i < dim; ++i) s = __dadd_rn(s, __dmul_rn((double)x[i], (double)x[i]));
-        const float inv_dim = __fdiv_rn(1.0f, (float)dim);
-        scale_s = (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn(s, (double)inv_dim), (double)eps)));
+    return hsum8_lanes(a);
+}
+
+// The RMSNorm scale of a transposed dim-vector xt (scalar.rs:232-292,
+// gemma3.cpp sum_sq / rmsnorm_gamma_multi): lanes 0..7 of wave 0 run the
+// eight FMA lanes over the chunks of 8 in order, hsum8, lane 0 forms
+// (float)(1 / sqrt(ss * inv_dim + eps)) in f64 (dim % 8 == 0: no tail).
+// xt written before a barrier; every thread gets the scale (bc: one LDS float).
+__device__ float wg_rms_scale(const float* xt, int dim, float eps, float* bc) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const float r = chain_sumsq(xt, dim, tid);
+        if (tid == 0) {
+            const float inv_dim = __fdiv_rn(1.0f, (float)dim);
+            bc[0] = (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn((double)r, (double)inv_dim), (double)eps)));
+        }
     }
-    __syncthreads();
-    const float scale = scale_s;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) y[i] = __fmul_rn(__fmul_rn(x[i], scale), gamma[i]);
-    __syncthreads();
+    lds_barrier();
+    return bc[0];
+}
+
+// ---- the matmul kernels' prologues --------------------------------------------------------
+
+// One thread's pieces (4 floats each, pieces tid and tid + 256) of a
+// prologue's inputs: the block output o, the residual x, two gammas.
+struct ResIn {
+    float4 o[ECH], x[ECH], g1[ECH], g2[ECH];
+};
+
+__device__ __forceinline__ void res_load(ResIn& r, const float* o, const float* x, const float* g1, const float* g2,
+                                         int E) {
+#pragma unroll
+    for (int k = 0; k < ECH; ++k) {
+        const int i = 4 * min((int)threadIdx.x + WG * k, E / 4 - 1);
+        r.o[k] = ld4(o + i);
+        r.x[k] = ld4(x + i);
+        r.g1[k] = ld4(g1 + i);
+        r.g2[k] = ld4(g2 + i);
+    }
+}
+
+__device__ __forceinline__ float4 add_normed(float4 x, float4 o, float s, float4 g) {
+    return make_float4(__fadd_rn(x.x, __fmul_rn(__fmul_rn(o.x, s), g.x)),
+                       __fadd_rn(x.y, __fmul_rn(__fmul_rn(o.y, s), g.y)),
+                       __fadd_rn(x.z, __fmul_rn(__fmul_rn(o.z, s), g.z)),
+                       __fadd_rn(x.w, __fmul_rn(__fmul_rn(o.w, s), g.w)));
+}
+__device__ __forceinline__ float4 normed(float4 x, float s, float4 g) {
+    return make_float4(__fmul_rn(__fmul_rn(x.x, s), g.x), __fmul_rn(__fmul_rn(x.y, s), g.y),
+                       __fmul_rn(__fmul_rn(x.z, s), g.z), __fmul_rn(__fmul_rn(x.w, s), g.w));
+}
+
+// y = RMSNorm(x, g) into LDS yl, x already in LDS xs (transposed) and in the
+// thread's registers; ends with a barrier.
+__device__ __forceinline__ void norm_to(const float4 (&xn)[ECH], const float4 (&g)[ECH], int E, float eps,
+                                        const float* xs, float* yl, float* bc) {
+    const float s = wg_rms_scale(xs, E, eps, bc);
+#pragma unroll
+    for (int k = 0; k < ECH; ++k)
+        if ((int)threadIdx.x + WG * k < E / 4) *(float4*)(yl + 4 * (threadIdx.x + WG * k)) = normed(xn[k], s, g[k]);
+    lds_barrier();
+}
+
+// Keep x (the new residual) in xs (transposed) and, from workgroup 0, in
+// x_out and rec.
+__device__ __forceinline__ void keep_residual(const float4 (&xn)[ECH], int E, float* xs, float* x_out, float* rec) {
+#pragma unroll
+    for (int k = 0; k < ECH; ++k) {
+        const int i = threadIdx.x + WG * k;
+        if (i < E / 4) {
+            tput4(xs, tstride(E), i, xn[k]);
+            if (blockIdx.x == 0) {
+                *(float4*)(x_out + 4 * i) = xn[k];
+                if (rec) *(float4*)(rec + 4 * i) = xn[k];
+            }
+        }
+    }
+    lds_barrier();
+}
+
+// x_new = x + RMSNorm(o, g1), y = RMSNorm(x_new, g2) (forward.rs:749-803):
+// a block's post-norm and residual add, then the next pre-norm. y goes to
+// LDS yl (the matmul's x). xs: LDS scratch of E + 32 floats.
+__device__ void res_norm(const ResIn& r, int E, float eps, float* xs, float* yl, float* bc, float* x_out,
+                         float* rec) {
+#pragma unroll
+    for (int k = 0; k < ECH; ++k)
+        if ((int)threadIdx.x + WG * k < E / 4) tput4(xs, tstride(E), threadIdx.x + WG * k, r.o[k]);
+    lds_barrier();
+    const float s1 = wg_rms_scale(xs, E, eps, bc);
+    float4 xn[ECH];
+#pragma unroll
+    for (int k = 0; k < ECH; ++k) xn[k] = add_normed(r.x[k], r.o[k], s1, r.g1[k]);
+    keep_residual(xn, E, xs, x_out, rec);
+    norm_to(xn, r.g2, E, eps, xs, yl, bc);
+}
+
+// Layer 0's input: the token's Q8_0 row of the tied token_embd times
+// sqrt(n_embd) (kernels/mod.rs:917-929: f32(q) * (bf16(s) * scale)).
+struct EmbIn {
+    uint32_t q[ECH], s[ECH];  // four quants, their block's BF16 scale
+    float4 g[ECH];
+};
+
+__device__ __forceinline__ void emb_load(EmbIn& r, const uint64_t* tok, const int8_t* tq, const uint16_t* ts,
+                                         const float* g, int E) {
+    const size_t t = (size_t)*tok;
+#pragma unroll
+    for (int k = 0; k < ECH; ++k) {
+        const int i = 4 * min((int)threadIdx.x + WG * k, E / 4 - 1);
+        r.q[k] = *(const uint32_t*)(tq + t * E + i);
+        r.s[k] = ts[t * (E / 32) + i / 32];
+        r.g[k] = ld4(g + i);
+    }
+}
+
+__device__ void emb_norm(const EmbIn& r, int E, float eps, float embd_scale, float* xs, float* yl, float* bc,
+                         float* x_out) {
+    float4 xn[ECH];
+#pragma unroll
+    for (int k = 0; k < ECH; ++k) {
+        const float vs = __fmul_rn(bf16f(r.s[k]), embd_scale);
+        xn[k] = make_float4(__fmul_rn((float)(int8_t)(r.q[k] & 0xffu), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 8), vs),
+                            __fmul_rn((float)(int8_t)(r.q[k] >> 16), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 24), vs));
+    }
+    keep_residual(xn, E, xs, x_out, nullptr);
+    norm_to(xn, r.g, E, eps, xs, yl, bc);
 }
 
 // ---- the step's kernels -----------------------------------------------------------------
 
-// Embedding row times sqrt(n_embd) (kernels/mod.rs:917-929): the Q8_0 row of
-// the tied token_embd, f32(q) * (bf16(s) * scale).
-__global__ void embed_kernel(const uint64_t* tok, const int8_t* tq, const uint16_t* ts, int E, float embd_scale,
-                             float* x) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= E) return;
-    const size_t t = (size_t)*tok;
-    const float vs = __fmul_rn(bf16f(ts[t * (E / 32) + i / 32]), embd_scale);
-    x[i] = __fmul_rn((float)tq[t * E + i], vs);
-}
+struct QkvArgs {
+    F32Mat m[3];  // q, k, v
+    float* y[3];
+    int wg[3];  // workgroups per matrix
+    const float *o, *x_in, *post, *norm;  // post: the previous layer's post-FFW gamma; norm: attention's
+    float* x_out;
+    float* rec;  // this layer's slot of the step-0 record (advanced by *step_p * rec_stride), or null
+    const int* step_p;
+    size_t rec_stride;
+    const uint64_t* tok;  // layer 0: the token and the embedding table
+    const int8_t* tq;
+    const uint16_t* ts;
+    float embd_scale;
+    int E;
+    float eps;
+};
 
-__global__ void rmsnorm_kernel(const float* x, const float* gamma, float* y, int dim, float eps) {
-    rmsnorm_wg(x, gamma, y, dim, eps);
-}
-
-// Per head: q / k RMSNorm, NeoX RoPE at the current position, then the K/V
-// append to the BF16 caches (forward.rs:326-351). Workgroups 0..H-1 take the
-// query heads, H..H+KV-1 the key heads.
-__global__ void qk_kernel(float* q, float* k, const float* v, const float* q_norm, const float* k_norm,
-                          const float* cos_t, const float* sin_t, const int* pos_p, uint16_t* kc, uint16_t* vc,
-                          int H, int KV, int hd, float eps) {
-    const int pos = *pos_p;
-    const int head = blockIdx.x;
-    const bool is_q = head < H;
-    float* x = is_q ? q + head * hd : k + (head - H) * hd;
-    rmsnorm_wg(x, is_q ? q_norm : k_norm, x, hd, eps);
-    const int half = hd / 2;
-    const float* cs = cos_t + (size_t)pos * half;
-    const float* sn = sin_t + (size_t)pos * half;
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float a = x[i], b = x[i + half];
-        x[i] = __fsub_rn(__fmul_rn(cs[i], a), __fmul_rn(sn[i], b));
-        x[i + half] = __fadd_rn(__fmul_rn(sn[i], a), __fmul_rn(cs[i], b));
-    }
-    if (!is_q) {
-        __syncthreads();
-        const int kvh = head - H, kv_dim = KV * hd;
-        for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-            kc[(size_t)pos * kv_dim + kvh * hd + i] = to_bf16(x[i]);
-            vc[(size_t)pos * kv_dim + kvh * hd + i] = to_bf16(v[kvh * hd + i]);
+template <int D, bool FIRST>
+__global__ __launch_bounds__(WG) void qkv_kernel(QkvArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
+    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
+    __shared__ float bc[4];
+    const int tid = threadIdx.x;
+    ResIn r;
+    EmbIn e;
+    if (FIRST)
+        emb_load(e, a.tok, a.tq, a.ts, a.norm, a.E);
+    else
+        res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
+    int b = blockIdx.x, seg = 0;
+    if (b >= a.wg[0]) {
+        b -= a.wg[0];
+        seg = 1;
+        if (b >= a.wg[1]) {
+            b -= a.wg[1];
+            seg = 2;
         }
     }
+    const F32Mat m = a.m[seg];
+    const int row_raw = b * M1_ROWS + (tid >> 4);
+    const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
+    M1Lane<1, D> L;
+    L.init(m, row, tid & 15);
+    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads, then the ring, then the prologue
+    L.prefetch();
+    __builtin_amdgcn_sched_barrier(0);
+    if (FIRST)
+        emb_norm(e, a.E, a.eps, a.embd_scale, xs, yl, bc, a.x_out);
+    else
+        res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec ? a.rec + (size_t)*a.step_p * a.rec_stride : nullptr);
+    L.run(yl);
+    const float v = L.reduce();
+    if (row_raw < m.rows && (tid & 15) == 0) a.y[seg][row_raw] = v;
 }
 
-// One query head over its key span, in one key block (attn_block,
-// attn_finish: scalar.rs:444-548): scores by 8-lane FMA dots and hsum8,
-// times the attention scale; the first-maximum; exp_lane; the 8-lane sum of
-// the weights over whole chunks, hsum8, then the tail in order; the V sum
-// as one FMA chain per output element over the keys in order; / sum.
-__global__ __launch_bounds__(256) void attn_kernel(const float* q, const uint16_t* kc, const uint16_t* vc,
-                                                   const int* pos_p, int group, int KV, int hd, int window,
-                                                   float scale, float* out) {
-    __shared__ float sc[ATTN_BLOCK];
-    __shared__ float vsum[8];
-    __shared__ float m_s, inv_s;
-    const int pos = *pos_p, h = blockIdx.x, kvh = h / group;
-    const int first = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-    const int n_keys = pos + 1 - first;
-    const int kv_dim = KV * hd, hd8 = hd & ~7;
-    const float* qh = q + h * hd;
-    for (int t = threadIdx.x; t < n_keys; t += blockDim.x) {
-        const uint16_t* krow = kc + (size_t)(first + t) * kv_dim + kvh * hd;
-        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int i = 0; i < hd8; i += 8)
+struct FfnArgs {
+    F32Mat gate, up;
+    float* h;  // GELU(gate) * up
+    int F;
+    const float *o, *x_in, *post, *norm;  // post_attention_norm, ffn_norm
+    float* x_out;
+    int E;
+    float eps;
+};
+
+// Workgroup g runs gate rows 8g..8g+7 (row slots 0..7) and the same up rows
+// (slots 8..15); h = GELU(gate) * up (forward.rs:771-777).
+template <int D>
+__global__ __launch_bounds__(WG) void ffn_kernel(FfnArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
+    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
+    __shared__ float bc[4], res[M1_ROWS];
+    const int tid = threadIdx.x, slot = tid >> 4, r0 = blockIdx.x * (M1_ROWS / 2);
+    ResIn r;
+    res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
+    const int row = r0 + (slot & 7) < a.F ? r0 + (slot & 7) : a.F - 1;
+    M1Lane<1, D> L;
+    L.init(slot < 8 ? a.gate : a.up, row, tid & 15);
+    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads, then the ring, then the prologue
+    L.prefetch();
+    __builtin_amdgcn_sched_barrier(0);
+    res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, nullptr);
+    L.run(yl);
+    const float v = L.reduce();
+    if ((tid & 15) == 0) res[slot] = v;
+    lds_barrier();
+    if (tid < 8 && r0 + tid < a.F) a.h[r0 + tid] = __fmul_rn(gelu_lane(res[tid]), res[8 + tid]);
+}
+
+struct FinalArgs {
+    const float *o, *x_in, *post, *norm;  // the last post-FFW gamma, output_norm
+    float *x_out, *y, *rec;
+    const int* step_p;
+    size_t rec_stride;
+    int E;
+    float eps;
+};
+
+// After the last layer: its residual, then y = RMSNorm(x, output_norm).
+__global__ __launch_bounds__(WG) void final_kernel(FinalArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
+    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
+    __shared__ float bc[4];
+    ResIn r;
+    res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
+    res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec + (size_t)*a.step_p * a.rec_stride);
+    for (int i = threadIdx.x; i < a.E / 4; i += WG) *(float4*)(a.y + 4 * i) = *(const float4*)(yl + 4 * i);
+}
+
+struct AttnArgs {
+    const float *q, *k, *v;  // the projections
+    const float *q_norm, *k_norm, *cos_t, *sin_t;
+    const int* pos_p;
+    uint16_t *kc, *vc;  // this layer's caches [n_ctx][n_kv * HD]
+    int group, KV, window;
+    float scale, eps;
+    float* out;
+};
+
+// The first-maximum scan's step (scalar.rs attn_block): b follows a.
+__device__ __forceinline__ float first_max(float a, float b) { return a < b ? b : a; }
+
+// One query head, one key block (forward.rs:326-351 and attn_block /
+// attn_finish, scalar.rs:444-548): q / k RMSNorm, NeoX RoPE at the current
+// position, the K/V append (by the first head of each KV group), scores by
+// 8-lane FMA dots and hsum8 times the scale, the first maximum, exp_lane,
+// the 8-lane sum of the weights over whole chunks then the tail in order,
+// and the V sum as one FMA chain per output element over the keys in order,
+// / sum. Thread t scores key t; the cached values of keys 0..n-2 are copied
+// into LDS at the start; the new key and value come from LDS.
+template <int HD>
+__global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
+    static_assert(HD % 8 == 0 && HD <= WG, "head size");
+    constexpr int HALF = HD / 2, CH = HD / 8;
+    __shared__ __attribute__((aligned(16))) uint16_t vs[ATTN_BLOCK * HD];
+    constexpr int ST = ATTN_BLOCK / 8 + 4;  // transposed weights: lane l's run at l * ST
+    __shared__ __attribute__((aligned(16))) float qs[HD];
+    __shared__ __attribute__((aligned(16))) float ks[HD];
+    __shared__ __attribute__((aligned(16))) float qt[HD + 32];
+    __shared__ __attribute__((aligned(16))) float kt[HD + 32];
+    __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
+    __shared__ uint16_t vn[HD];
+    __shared__ __attribute__((aligned(16))) float sc[ATTN_BLOCK];
+    __shared__ __attribute__((aligned(16))) float sct[8 * ST];
+    __shared__ float red[8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = *a.pos_p, h = blockIdx.x, kvh = h / a.group;
+    const int first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+    const int n = pos + 1 - first;  // keys; the last is the new one
+    const size_t kv_dim = (size_t)a.KV * HD;
+    const int i = tid < HD ? tid : HD - 1;
+    const float qv = a.q[h * HD + i], kv = a.k[kvh * HD + i], vv = a.v[kvh * HD + i];
+    const float qg = a.q_norm[i], kg = a.k_norm[i];
+    const float cs = a.cos_t[(size_t)pos * HALF + i % HALF], sn = a.sin_t[(size_t)pos * HALF + i % HALF];
+    // Cached key tid (first..pos-1), unused for the new key and past the end.
+    const uint16_t* kbase = a.kc + kvh * HD;
+    const int krow = first + (tid < n - 1 ? tid : 0);
+    uint4 kr[CH];
 #pragma unroll
-            for (int l = 0; l < 8; ++l) acc[l] = __fmaf_rn(qh[i + l], bf16f(krow[i + l]), acc[l]);
-        float s = hsum8(acc);
-        for (int i = hd8; i < hd; ++i) s = __fadd_rn(s, __fmul_rn(qh[i], bf16f(krow[i])));
-        sc[t] = __fmul_rn(s, scale);
+    for (int c = 0; c < CH; ++c) kr[c] = *(const uint4*)(kbase + (size_t)krow * kv_dim + 8 * c);
+    // Cached values of keys 0..n-2, straight into LDS: 16 bytes per lane, 1 KB
+    // per wave instruction, pieces past the end repeating the last one.
+    const int nch = (n - 1) * CH, nins = (nch + 63) / 64;
+    const uint16_t* vbase = a.vc + kvh * HD;
+    for (int k = wave; k < nins; k += WG / 64) {
+        const int u = min(64 * k + lane, nch - 1);
+        const int t = u / CH, p = u - t * CH;
+        __builtin_amdgcn_global_load_lds((const void*)(vbase + (size_t)(first + t) * kv_dim + 8 * p),
+                                         (lds_ptr_t)(vs + 512 * k), 16, 0, 0);
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = sc[0];
-        for (int i = 1; i < n_keys; ++i)
-            if (m < sc[i]) m = sc[i];
-        m_s = m;
+    // q and k RMSNorm: wave 0 runs q's chains, wave 1 k's (transposed copies).
+    if (tid < HD) {
+        qt[(tid & 7) * tstride(HD) + (tid >> 3)] = qv;
+        kt[(tid & 7) * tstride(HD) + (tid >> 3)] = kv;
     }
-    __syncthreads();
-    const float m = m_s;
-    for (int t = threadIdx.x; t < n_keys; t += blockDim.x) sc[t] = exp_lane(__fsub_rn(sc[t], m));
-    __syncthreads();
-    const int body = n_keys & ~7;
-    if (threadIdx.x < 8) {
-        float a = 0.0f;
-        for (int i = 0; i < body; i += 8) a = __fadd_rn(a, sc[i + threadIdx.x]);
-        vsum[threadIdx.x] = a;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float l = hsum8(vsum);
-        for (int i = body; i < n_keys; ++i) l = __fadd_rn(l, sc[i]);
-        inv_s = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        const uint16_t* vcol = vc + (size_t)first * kv_dim + kvh * hd + i;
-        float o = __fmul_rn(sc[0], bf16f(vcol[0]));
-        if (i < hd8) {
-            for (int t = 1; t < n_keys; ++t) o = __fmaf_rn(sc[t], bf16f(vcol[(size_t)t * kv_dim]), o);
-        } else {
-            for (int t = 1; t < n_keys; ++t) o = __fadd_rn(o, __fmul_rn(sc[t], bf16f(vcol[(size_t)t * kv_dim])));
+    lds_barrier();
+    if (wave < 2) {
+        const float ss = chain_sumsq(wave == 0 ? qt : kt, HD, lane);
+        if (lane == 0) {
+            const float inv_dim = __fdiv_rn(1.0f, (float)HD);
+            red[wave] = (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn((double)ss, (double)inv_dim), (double)a.eps)));
         }
-        out[h * hd + i] = __fmul_rn(o, inv);
     }
-}
-
-// x += RMSNorm(o, post); y = RMSNorm(x, next) (forward.rs:749-803): the
-// post-attention / post-FFW norm, the residual, and the next norm. When
-// `record` is set, x is also copied there (the per-layer hidden state).
-__global__ __launch_bounds__(1024) void residual_kernel(float* o, float* x, const float* post, const float* next,
-                                                        float* y, int E, float eps, float* record,
-                                                        const int* step_p, int rec_stride) {
-    rmsnorm_wg(o, post, o, E, eps);
-    for (int i = threadIdx.x; i < E; i += blockDim.x) x[i] = __fadd_rn(x[i], o[i]);
-    __syncthreads();
-    if (record) {
-        float* r = record + (size_t)*step_p * rec_stride;
-        for (int i = threadIdx.x; i < E; i += blockDim.x) r[i] = x[i];
+    lds_barrier();
+    if (tid < HD) {
+        qs[tid] = __fmul_rn(__fmul_rn(qv, red[0]), qg);
+        ks[tid] = __fmul_rn(__fmul_rn(kv, red[1]), kg);
+        vn[tid] = to_bf16(vv);
     }
-    rmsnorm_wg(x, next, y, E, eps);
-}
-
-__global__ void gelu_mul_kernel(float* gate, const float* up, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) gate[i] = __fmul_rn(gelu_lane(gate[i]), up[i]);
+    lds_barrier();
+    // RoPE: threads 0..HALF-1 rotate q's pairs (j, j + HALF), HALF..HD-1 k's.
+    if (tid < HALF) {
+        const float x0 = qs[tid], x1 = qs[tid + HALF];
+        qs[tid] = __fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1));
+        qs[tid + HALF] = __fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1));
+    } else if (tid < HD) {
+        const int j = tid - HALF;
+        const float x0 = ks[j], x1 = ks[j + HALF];
+        kn[j] = to_bf16(__fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1)));
+        kn[j + HALF] = to_bf16(__fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1)));
+    }
+    lds_barrier();
+    if (h % a.group == 0 && tid < HD) {
+        a.kc[(size_t)pos * kv_dim + kvh * HD + tid] = kn[tid];
+        a.vc[(size_t)pos * kv_dim + kvh * HD + tid] = vn[tid];
+    }
+    // Scores.
+    float s_t = -INFINITY;
+    if (tid < n) {
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        const bool last = tid == n - 1;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const uint4 kk = last ? *(const uint4*)(kn + 8 * c) : kr[c];
+            const float4 q0 = *(const float4*)(qs + 8 * c), q1 = *(const float4*)(qs + 8 * c + 4);
+            acc[0] = __fmaf_rn(q0.x, bf16f(kk.x & 0xffffu), acc[0]);
+            acc[1] = __fmaf_rn(q0.y, bf16f(kk.x >> 16), acc[1]);
+            acc[2] = __fmaf_rn(q0.z, bf16f(kk.y & 0xffffu), acc[2]);
+            acc[3] = __fmaf_rn(q0.w, bf16f(kk.y >> 16), acc[3]);
+            acc[4] = __fmaf_rn(q1.x, bf16f(kk.z & 0xffffu), acc[4]);
+            acc[5] = __fmaf_rn(q1.y, bf16f(kk.z >> 16), acc[5]);
+            acc[6] = __fmaf_rn(q1.z, bf16f(kk.w & 0xffffu), acc[6]);
+            acc[7] = __fmaf_rn(q1.w, bf16f(kk.w >> 16), acc[7]);
+        }
+        s_t = __fmul_rn(hsum8(acc), a.scale);
+    }
+    // The first maximum over keys in order: a leftmost-maximum tree, with a
+    // NaN after key 0 never taken (as the scan's comparison never takes one)
+    // and a NaN at key 0 kept (it is never replaced).
+    float mv = (tid > 0 && s_t != s_t) ? -INFINITY : s_t;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+        const float o = __shfl_xor(mv, k, 64);
+        mv = (lane & k) ? first_max(o, mv) : first_max(mv, o);
+    }
+    if (lane == 0) red[2 + wave] = mv;
+    lds_barrier();
+    float m = red[2];
+#pragma unroll
+    for (int w = 1; w < WG / 64; ++w) m = first_max(m, red[2 + w]);
+    if (tid < n) {
+        const float pw = exp_lane(__fsub_rn(s_t, m));
+        sc[tid] = pw;
+        sct[(tid & 7) * ST + (tid >> 3)] = pw;
+    }
+    lds_barrier();
+    if (tid < 64) {
+        // The eight add lanes over the whole chunks of 8, in order.
+        const int body = n & ~7, K = body / 8;
+        float acc = 0.0f;
+        if (tid < 8) {
+            const float* p = sct + tid * ST;
+            int k = 0;
+            for (; k + 4 <= K; k += 4) {
+                const float4 v = *(const float4*)(p + k);
+                acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, v.x), v.y), v.z), v.w);
+            }
+            for (; k < K; ++k) acc = __fadd_rn(acc, p[k]);
+        }
+        float l = hsum8_lanes(acc);
+        if (tid == 0) {
+            for (int j = body; j < n; ++j) l = __fadd_rn(l, sc[j]);
+            red[6] = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the cached values in LDS
+    lds_barrier();
+    if (tid < HD) {
+        float o;
+        if (n == 1) {
+            o = __fmul_rn(sc[0], bf16f(vn[tid]));
+        } else {
+            o = __fmul_rn(sc[0], bf16f(vs[tid]));
+#pragma unroll 16
+            for (int t = 1; t < n - 1; ++t) o = __fmaf_rn(sc[t], bf16f(vs[t * HD + tid]), o);
+            o = __fmaf_rn(sc[n - 1], bf16f(vn[tid]), o);
+        }
+        a.out[h * HD + tid] = __fmul_rn(o, red[6]);
+    }
 }
 
 // End of a step: the greedy token is recorded, the position advances.
@@ -244,6 +566,16 @@ __global__ void step_end_kernel(const uint64_t* tok, int* tokens_out, int* pos_p
         }                                                                                  \
     } while (0)
 
+// Ring depth of the fused matmuls: eight 8-block groups when the rows have
+// them, else four (no group is loaded twice).
+template <bool FIRST>
+static void launch_qkv(const QkvArgs& a, int nb, int wgs, hipStream_t st) {
+    if (nb / 8 >= 8)
+        qkv_kernel<8, FIRST><<<wgs, WG, 0, st>>>(a);
+    else
+        qkv_kernel<4, FIRST><<<wgs, WG, 0, st>>>(a);
+}
+
 }  // namespace
 
 extern "C" {
@@ -251,11 +583,13 @@ extern "C" {
 struct nngd_model {
     nng_config c;
     std::vector<nnh_weight*> w;  // 7 * n_layer + 1, lm_head (the tied token_embd) last
+    std::vector<F32Mat> f;       // the 16-lane layouts of the 7 * n_layer layer weights
     float* norms = nullptr;      // device copy, layout of nng_create
     uint16_t *kc = nullptr, *vc = nullptr;
     float *cos_t = nullptr, *sin_t = nullptr;  // [2][n_ctx][hd/2]: sliding (local) base, then global
-    float *x = nullptr, *y = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *o = nullptr;
-    float *gate = nullptr, *up = nullptr, *logits = nullptr, *record = nullptr;
+    float *xa = nullptr, *xb = nullptr;        // the residual stream, alternating
+    float *y = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *o = nullptr;
+    float *h = nullptr, *logits = nullptr, *record = nullptr;
     void* work = nullptr;
     uint64_t* tok = nullptr;
     int *pos = nullptr, *step = nullptr, *tokens = nullptr;
@@ -272,8 +606,8 @@ const char* nngd_error(nngd_model* m) { return m->err.c_str(); }
 void nngd_free(nngd_model* m) {
     if (!m) return;
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    void* bufs[] = {m->norms, m->kc, m->vc, m->cos_t, m->sin_t, m->x, m->y, m->q, m->k, m->v, m->attn, m->o,
-                    m->gate, m->up, m->logits, m->record, m->work, m->tok, m->pos, m->step, m->tokens};
+    void* bufs[] = {m->norms, m->kc, m->vc, m->cos_t, m->sin_t, m->xa, m->xb, m->y, m->q, m->k, m->v, m->attn, m->o,
+                    m->h, m->logits, m->record, m->work, m->tok, m->pos, m->step, m->tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->st) (void)hipStreamDestroy(m->st);
@@ -310,7 +644,25 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
         m->err = "bad weight count or head grouping";
         return 1;
     }
+    if (c.n_embd % 32 || c.n_embd > E_MAX || (c.head_dim != 128 && c.head_dim != 256) || c.n_ff % 32) {
+        m->err = "the fused step needs n_embd a multiple of 32 up to 2048, head_dim 128 or 256";
+        return 1;
+    }
     m->w.assign(weights, weights + n_weights);
+    // The fused kernels read q, k, v, gate and up in the 16-lane Q8_0 layout.
+    for (int i = 0; i < 7 * c.n_layer; ++i) {
+        nnh_f32_layout l;
+        if (nnh_weight_f32_layout(weights[i], &l)) {
+            m->err = std::string("weight layout: ") + nnh_last_error();
+            return 1;
+        }
+        const int kind = i % 7;
+        if (kind != 3 && kind != 6 && (l.dtype != NNH_Q8_0 || l.cols != (size_t)c.n_embd)) {
+            m->err = "the fused q, k, v, gate and up matmuls take Q8_0 weights of n_embd columns";
+            return 1;
+        }
+        m->f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, l.biases, (int)l.rows, (int)l.nb, (int)l.nbp});
+    }
     m->n_gen_max = n_gen_max;
     const size_t E = c.n_embd, hd = c.head_dim, qd = (size_t)c.n_head * hd, kvd = (size_t)c.n_kv * hd;
     const size_t nn = norm_stride(c) * c.n_layer + E, half = hd / 2;
@@ -326,15 +678,15 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     GD_HIP(hipMalloc((void**)&m->sin_t, sn.size() * 4));
     GD_HIP(hipMemcpy(m->cos_t, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
     GD_HIP(hipMemcpy(m->sin_t, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-    GD_HIP(hipMalloc((void**)&m->x, E * 4));
+    GD_HIP(hipMalloc((void**)&m->xa, E * 4));
+    GD_HIP(hipMalloc((void**)&m->xb, E * 4));
     GD_HIP(hipMalloc((void**)&m->y, E * 4));
     GD_HIP(hipMalloc((void**)&m->o, E * 4));
     GD_HIP(hipMalloc((void**)&m->q, qd * 4));
     GD_HIP(hipMalloc((void**)&m->k, kvd * 4));
     GD_HIP(hipMalloc((void**)&m->v, kvd * 4));
     GD_HIP(hipMalloc((void**)&m->attn, qd * 4));
-    GD_HIP(hipMalloc((void**)&m->gate, (size_t)c.n_ff * 4));
-    GD_HIP(hipMalloc((void**)&m->up, (size_t)c.n_ff * 4));
+    GD_HIP(hipMalloc((void**)&m->h, (size_t)c.n_ff * 4));
     GD_HIP(hipMalloc((void**)&m->logits, (size_t)c.n_vocab * 4));
     GD_HIP(hipMalloc((void**)&m->record, (size_t)n_gen_max * c.n_layer * E * 4));
     GD_HIP(hipMalloc(&m->work, nnh_argmax_work_bytes((size_t)c.n_vocab)));
@@ -348,53 +700,75 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
 // Queue one decode step on m->st (eagerly, or into a graph being captured).
 static int queue_step(nngd_model* m) {
     const nng_config& c = m->c;
-    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, F = c.n_ff;
-    const size_t ns = norm_stride(c);
+    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, F = c.n_ff, nb = E / 32;
+    const size_t ns = norm_stride(c), rs = (size_t)c.n_layer * E;
     hipStream_t st = m->st;
     const uint8_t* te = (const uint8_t*)nnh_weight_device_data(m->w.back());
-    const int8_t* tq = (const int8_t*)te;
-    const uint16_t* ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
     const float eps = c.rms_eps;
-    embed_kernel<<<(E + 255) / 256, 256, 0, st>>>(m->tok, tq, ts, E, std::sqrt((float)E), m->x);
-    rmsnorm_kernel<<<1, 1024, 0, st>>>(m->x, m->norms, m->y, E, eps);
     for (int li = 0; li < c.n_layer; ++li) {
         const float* nr = m->norms + ns * li;
-        const float *q_norm = nr + E, *k_norm = nr + E + hd, *post_attn = nr + E + 2 * hd,
-                    *ffn_norm = nr + 2 * E + 2 * hd, *post_ffw = nr + 3 * E + 2 * hd;
-        const float* next = li + 1 < c.n_layer ? m->norms + ns * (li + 1) : m->norms + ns * c.n_layer;
+        const float *attn_norm = nr, *q_norm = nr + E, *k_norm = nr + E + hd, *post_attn = nr + E + 2 * hd,
+                    *ffn_norm = nr + 2 * E + 2 * hd;
         const bool sliding = c.swa_period > 0 && (li + 1) % c.swa_period != 0;  // load.rs:1156-1160
         const size_t half = hd / 2, tab = sliding ? 0 : (size_t)c.n_ctx * half;
+        const F32Mat* f = m->f.data() + 7 * li;
         nnh_weight* const* w = m->w.data() + 7 * li;
         const size_t kvd = (size_t)KV * hd, cache = (size_t)li * c.n_ctx * kvd;
-        if (nnh_gemv_batch_dev(w[0], m->y, E, m->q, H * hd, 1, NNH_ACT_F32, st) ||
-            nnh_gemv_batch_dev(w[1], m->y, E, m->k, kvd, 1, NNH_ACT_F32, st) ||
-            nnh_gemv_batch_dev(w[2], m->y, E, m->v, kvd, 1, NNH_ACT_F32, st)) {
-            m->err = std::string("gemv: ") + nnh_last_error();
-            return 1;
+        // The previous layer's post-FFW residual (or the embedding), attention's norm, q / k / v.
+        QkvArgs qa{};
+        int wgs = 0;
+        float* outs[3] = {m->q, m->k, m->v};
+        for (int j = 0; j < 3; ++j) {
+            qa.m[j] = f[j];
+            qa.y[j] = outs[j];
+            qa.wg[j] = (f[j].rows + M1_ROWS - 1) / M1_ROWS;
+            wgs += qa.wg[j];
         }
-        qk_kernel<<<H + KV, 256, 0, st>>>(m->q, m->k, m->v, q_norm, k_norm, m->cos_t + tab, m->sin_t + tab, m->pos,
-                                          m->kc + cache, m->vc + cache, H, KV, hd, eps);
-        attn_kernel<<<H, 256, 0, st>>>(m->q, m->kc + cache, m->vc + cache, m->pos, H / KV, KV, hd,
-                                       sliding ? c.window : 0, c.attn_scale, m->attn);
+        qa.norm = attn_norm;
+        qa.x_out = m->xa;
+        qa.E = E;
+        qa.eps = eps;
+        if (li == 0) {
+            qa.tok = m->tok;
+            qa.tq = (const int8_t*)te;
+            qa.ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
+            qa.embd_scale = std::sqrt((float)E);
+            launch_qkv<true>(qa, nb, wgs, st);
+        } else {
+            qa.o = m->o;
+            qa.x_in = m->xb;
+            qa.post = m->norms + ns * (li - 1) + 3 * E + 2 * hd;
+            qa.rec = m->record + (size_t)(li - 1) * E;
+            qa.step_p = m->step;
+            qa.rec_stride = rs;
+            launch_qkv<false>(qa, nb, wgs, st);
+        }
+        AttnArgs aa{m->q,  m->k,         m->v,         q_norm, k_norm, m->cos_t + tab, m->sin_t + tab, m->pos,
+                    m->kc + cache, m->vc + cache, H / KV, KV, sliding ? c.window : 0, c.attn_scale, eps, m->attn};
+        if (hd == 256)
+            attn_kernel<256><<<H, WG, 0, st>>>(aa);
+        else
+            attn_kernel<128><<<H, WG, 0, st>>>(aa);
         if (nnh_gemv_batch_dev(w[3], m->attn, H * hd, m->o, E, 1, NNH_ACT_F32, st)) {
             m->err = std::string("gemv: ") + nnh_last_error();
             return 1;
         }
-        residual_kernel<<<1, 1024, 0, st>>>(m->o, m->x, post_attn, ffn_norm, m->y, E, eps, nullptr, nullptr, 0);
-        if (nnh_gemv_batch_dev(w[4], m->y, E, m->gate, F, 1, NNH_ACT_F32, st) ||
-            nnh_gemv_batch_dev(w[5], m->y, E, m->up, F, 1, NNH_ACT_F32, st)) {
+        FfnArgs fa{f[4], f[5], m->h, F, m->o, m->xa, post_attn, ffn_norm, m->xb, E, eps};
+        const int fwgs = (F + M1_ROWS / 2 - 1) / (M1_ROWS / 2);
+        if (nb / 8 >= 8)
+            ffn_kernel<8><<<fwgs, WG, 0, st>>>(fa);
+        else
+            ffn_kernel<4><<<fwgs, WG, 0, st>>>(fa);
+        if (nnh_gemv_batch_dev(w[6], m->h, F, m->o, E, 1, NNH_ACT_F32, st)) {
             m->err = std::string("gemv: ") + nnh_last_error();
             return 1;
         }
-        gelu_mul_kernel<<<(F + 255) / 256, 256, 0, st>>>(m->gate, m->up, F);
-        if (nnh_gemv_batch_dev(w[6], m->gate, F, m->o, E, 1, NNH_ACT_F32, st)) {
-            m->err = std::string("gemv: ") + nnh_last_error();
-            return 1;
-        }
-        residual_kernel<<<1, 1024, 0, st>>>(m->o, m->x, post_ffw, next, m->y, E, eps, m->record + (size_t)li * E,
-                                            m->step, c.n_layer * E);
     }
-    // y = RMSNorm(x, output_norm): the greedy token is the lm_head argmax of y.
+    // The last residual and y = RMSNorm(x, output_norm); the greedy token is the lm_head argmax of y.
+    FinalArgs fin{m->o,    m->xb,   m->norms + ns * (c.n_layer - 1) + 3 * E + 2 * hd, m->norms + ns * c.n_layer,
+                  m->xa,   m->y,    m->record + (size_t)(c.n_layer - 1) * E,          m->step,
+                  rs,      E,       eps};
+    final_kernel<<<1, WG, 0, st>>>(fin);
     if (nnh_gemv_batch_dev(m->w.back(), m->y, E, m->logits, c.n_vocab, 1, NNH_ACT_F32, st) ||
         nnh_argmax_dev(m->logits, (size_t)c.n_vocab, m->work, m->tok, st)) {
         m->err = std::string("lm_head: ") + nnh_last_error();

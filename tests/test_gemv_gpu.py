@@ -95,6 +95,20 @@ def test_f32_baseline_shapes_bit_exact(oracle, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols", [(5, 224), (3, 480), (33, 4512), (17, 8192), (17, 8224), (40, 2080)])
+def test_f32_one_vector_ring_shapes(oracle, dtype, rows, cols):
+    # One vector takes the ring kernel up to 8192 columns: rows without a
+    # whole group (224 / 480 columns), ring depths 4 and 8 with every tail
+    # length class, the 8192-column limit and the first width past it.
+    say("ring", dtype, rows, cols)
+    rng = oracle.Rng(0x0E1 + rows + cols + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = rng.normals(cols, 1.0)
+    assert np.array_equal(bits(N.model_gemv(w, x)), bits(oracle.gemv_batch(m, x)))
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
 def test_f32_batch_equals_single(oracle, dtype):
     # kernels/tests.rs:641-691: every vector of a batch gets the single-vector bits.
     rng = oracle.Rng(0xBA7C + dtype)
