@@ -378,13 +378,60 @@ def cpu_baseline_q4(N, O, inputs, budget_s=12.0):
                 host_stream_gbs_1thread=round(O.avx_stream_gbs(256 << 20, 2), 1))
 
 
+def gemma_decode(args, N, cpu: bool):
+    """Gemma-3-1B-shaped greedy decode of 128 tokens from a
+    32-token prompt, on the device-resident step (seeded random Q8_0 weights).
+    tok/s counts the 127 decode forwards after the prompt; the timed run is
+    the second one (the first captures the step's graph). With `cpu`, the CPU
+    baseline leg: the same decode with nncpu's CPU gemv (the oracle's AVX2
+    restatement, 8 threads) in the shared C++ forward, timed, and its tokens
+    compared with the device run's."""
+    import ctypes as C
+    from nncpu_amd.gemma import Gemma3, gemma3_1b_config, random_prompt
+    t0 = time.perf_counter()
+    m = Gemma3(gemma3_1b_config(n_ctx=256))
+    log(f"gemma3-1b model built in {time.perf_counter() - t0:.1f}s")
+    prompt, n_gen = random_prompt(32, m.cfg.n_vocab), 128
+    m.generate_device(prompt, n_gen)
+    tg, hg, tp, td = m.generate_device(prompt, n_gen)
+    out = dict(config="gemma-3-1b architecture, Q8_0 weights 0.02*N(0,1), 32-token prompt, 128 greedy tokens",
+               tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
+               prefill_s=round(tp, 4), kernels_per_token=5 * m.cfg.n_layer + 5)
+    log(f"gemma3-1b device decode: {out['tok_s']} tok/s")
+    if cpu:
+        from oracle import oracle as O  # the CPU baseline leg only
+
+        class Table(C.Structure):
+            _fields_ = [("n", C.c_int), ("dtype", C.c_int), ("bufs", C.POINTER(C.c_void_p)),
+                        ("rows", C.POINTER(C.c_size_t)), ("cols", C.POINTER(C.c_size_t))]
+        bufs = [w.download() for w in m.weights]
+        arr = (C.c_void_p * len(bufs))(*[b.ctypes.data for b in bufs])
+        rows = (C.c_size_t * len(bufs))(*[r for r, _ in m.shapes])
+        cols = (C.c_size_t * len(bufs))(*[c for _, c in m.shapes])
+        table = Table(n=len(bufs), dtype=1, bufs=C.cast(arr, C.POINTER(C.c_void_p)),
+                      rows=C.cast(rows, C.POINTER(C.c_size_t)), cols=C.cast(cols, C.POINTER(C.c_size_t)))
+        threads = 8
+        O.avx_set_threads(threads)
+        gemv = C.cast(O.lib().or_model_gemv_cb, C.c_void_p).value
+        tc, hc, _, tdc = m.generate(prompt, n_gen, gemv, None, C.pointer(table))
+        out["cpu_baseline"] = dict(tok_s=round((n_gen - 1) / tdc, 1), cores=threads, kind="port",
+                                   sample="the same decode, CPU gemv (AVX2 restatement of nncpu's) in the shared "
+                                          "C++ forward",
+                                   tokens_identical=bool(np.array_equal(tg, tc)),
+                                   layer_states_identical=bool(np.array_equal(hg, hc)))
+        log(f"gemma3-1b cpu decode: {out['cpu_baseline']}")
+    m.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="q4_sweep",
-                    choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "all"])
+                    choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "gemma_decode",
+                             "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -409,6 +456,8 @@ def main():
     if args.workload in ("decode_f32", "all"):
         extra["decode_f32_bit_exact"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
                                                       N.ACT_F32, "decode_f32")
+    if args.workload in ("gemma_decode", "q4_sweep", "all"):
+        extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
     if args.workload not in ("q4_sweep", "all"):
         print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
         return

@@ -244,9 +244,7 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     w->f32v2 = rows >= F32_V2_MIN_ROWS && cols * 4 <= (size_t)nnh::F32_V2_MAX_LDS;
     hipError_t e;
     if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
-        // 256 spare bytes: the one-vector kernel's first group load of the
-        // last row stays inside the allocation when a row has no whole group.
-        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2) + 256))) !=
+        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2)))) !=
             hipSuccess ||
         (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
         (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||

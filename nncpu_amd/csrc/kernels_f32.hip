@@ -20,13 +20,13 @@
 // Layout (built once at upload, on the device): per row, quants regrouped so
 // each lane reads its own bytes with one 128-bit load per group:
 //   Q8_0: groups of 8 blocks; lane j's 16 bytes are, for i = 0..7,
-//         q[b0+i][j], q[b0+i][j+16]. A tail of t < 8 blocks gives each lane
-//         2t bytes at offset 2t*j.
+//         q[b0+i][j], q[b0+i][j+16].
 //   Q4:   groups of 16 blocks; lane j's 16 bytes are byte j of blocks
-//         b0..b0+15 (low nibble = chain j, high = chain j+16). A tail of
-//         t < 16 blocks gives each lane t bytes at offset t*j.
-// Scales are copied to rows padded to nbp (a multiple of 8 / 16) so a
-// group's scales are one aligned 16-byte load per 8.
+//         b0..b0+15 (low nibble = chain j, high = chain j+16).
+// A row is ngp = ceil(nb / group) whole groups of 256 bytes; the last one is
+// zero-filled past block nb (never multiplied: the block loops stop at nb).
+// Scales are copied to rows padded to nbp = ngp * group, so a group's scales
+// are one aligned 16-byte load per 8.
 //
 // A second mapping for tall matrices (the lm_head): 8 lanes per row, lane j
 // owning chains 4j..4j+3, so one 16-byte load of x serves four chains of a
@@ -52,48 +52,29 @@ namespace {
 constexpr int Q8_GROUP = 8;
 constexpr int Q4_GROUP = 16;
 
-// One thread per source quant byte: raw split layout -> per-lane groups.
+// One thread per destination byte: raw split layout -> per-lane groups.
 __global__ void relayout_q8_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ fq, int rows, int nb) {
-    size_t row_bytes = (size_t)nb * 32;
-    size_t total = (size_t)rows * row_bytes;
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    size_t r = idx / row_bytes;
-    int within = (int)(idx - r * row_bytes);
-    int b = within >> 5, k = within & 31;
-    int j = k & 15, h = k >> 4;
-    int ng = nb / Q8_GROUP;
-    int g = b / Q8_GROUP;
-    size_t off;
-    if (g < ng) {
-        int i = b - g * Q8_GROUP;
-        off = (size_t)g * 256 + j * 16 + 2 * i + h;
-    } else {
-        int t = nb - ng * Q8_GROUP;
-        int i = b - ng * Q8_GROUP;
-        off = (size_t)ng * 256 + (size_t)j * 2 * t + 2 * i + h;
-    }
-    fq[r * row_bytes + off] = raw[idx];
+    const int ngp = (nb + Q8_GROUP - 1) / Q8_GROUP;
+    const size_t row_bytes = (size_t)ngp * 256;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * row_bytes) return;
+    const size_t r = idx / row_bytes;
+    const int d = (int)(idx - r * row_bytes);
+    const int g = d >> 8, j = (d >> 4) & 15, k = d & 15;
+    const int b = g * Q8_GROUP + (k >> 1), e = j + 16 * (k & 1);
+    fq[idx] = b < nb ? raw[r * (size_t)nb * 32 + (size_t)b * 32 + e] : (uint8_t)0;
 }
 
 __global__ void relayout_q4_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ fq, int rows, int nb) {
-    size_t row_bytes = (size_t)nb * 16;
-    size_t total = (size_t)rows * row_bytes;
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    size_t r = idx / row_bytes;
-    int within = (int)(idx - r * row_bytes);
-    int b = within >> 4, j = within & 15;
-    int ng = nb / Q4_GROUP;
-    int g = b / Q4_GROUP;
-    size_t off;
-    if (g < ng) {
-        off = (size_t)g * 256 + j * 16 + (b - g * Q4_GROUP);
-    } else {
-        int t = nb - ng * Q4_GROUP;
-        off = (size_t)ng * 256 + (size_t)j * t + (b - ng * Q4_GROUP);
-    }
-    fq[r * row_bytes + off] = raw[idx];
+    const int ngp = (nb + Q4_GROUP - 1) / Q4_GROUP;
+    const size_t row_bytes = (size_t)ngp * 256;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * row_bytes) return;
+    const size_t r = idx / row_bytes;
+    const int d = (int)(idx - r * row_bytes);
+    const int g = d >> 8, j = (d >> 4) & 15, i = d & 15;
+    const int b = g * Q4_GROUP + i;
+    fq[idx] = b < nb ? raw[r * (size_t)nb * 16 + (size_t)b * 16 + j] : (uint8_t)0;
 }
 
 // The 8-lane layout: one thread per destination word.
@@ -194,7 +175,7 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
 
     const uint16_t* srow = fs + (size_t)row * nbp;
     if (DT == 1) {
-        const uint8_t* qrow = fq + (size_t)row * nb * 32;
+        const uint8_t* qrow = fq + (size_t)row * ((nb + Q8_GROUP - 1) / Q8_GROUP) * 256;
         const int ng = nb / Q8_GROUP;
         for (int g = 0; g < ng; ++g) {
             uint4 qv = *(const uint4*)(qrow + (size_t)g * 256 + j * 16);
@@ -207,17 +188,23 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
                 step<M>(a0, a1, w0, w1, x, x_stride, (size_t)32 * (g * Q8_GROUP + i) + j);
             }
         }
+        // The partial last group: its first t blocks.
         const int t = nb - ng * Q8_GROUP;
-        const uint8_t* tq = qrow + (size_t)ng * 256 + (size_t)j * 2 * t;
-        for (int i = 0; i < t; ++i) {
-            int b = ng * Q8_GROUP + i;
-            float s = bf16f(srow[b]);
-            float w0 = (float)(int8_t)tq[2 * i] * s;
-            float w1 = (float)(int8_t)tq[2 * i + 1] * s;
-            step<M>(a0, a1, w0, w1, x, x_stride, (size_t)32 * b + j);
+        if (t) {
+            uint4 qv = *(const uint4*)(qrow + (size_t)ng * 256 + j * 16);
+            uint4 sv = *(const uint4*)(srow + ng * Q8_GROUP);
+#pragma unroll
+            for (int i = 0; i < Q8_GROUP - 1; ++i) {
+                if (i < t) {
+                    float s = bf16f(half_of(sv, i));
+                    float w0 = (float)(int8_t)byte_of(qv, 2 * i) * s;
+                    float w1 = (float)(int8_t)byte_of(qv, 2 * i + 1) * s;
+                    step<M>(a0, a1, w0, w1, x, x_stride, (size_t)32 * (ng * Q8_GROUP + i) + j);
+                }
+            }
         }
     } else {
-        const uint8_t* qrow = fq + (size_t)row * nb * 16;
+        const uint8_t* qrow = fq + (size_t)row * ((nb + Q4_GROUP - 1) / Q4_GROUP) * 256;
         const int ng = nb / Q4_GROUP;
         for (int g = 0; g < ng; ++g) {
             uint4 qv = *(const uint4*)(qrow + (size_t)g * 256 + j * 16);
@@ -233,14 +220,20 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
             }
         }
         const int t = nb - ng * Q4_GROUP;
-        const uint8_t* tq = qrow + (size_t)ng * 256 + (size_t)j * t;
-        for (int i = 0; i < t; ++i) {
-            int b = ng * Q4_GROUP + i;
-            float s = bf16f(srow[b]);
-            uint32_t byte = tq[i];
-            float w0 = (float)(byte & 15u) * s;
-            float w1 = (float)(byte >> 4) * s;
-            step<M>(a0, a1, w0, w1, x, x_stride, (size_t)32 * b + j);
+        if (t) {
+            uint4 qv = *(const uint4*)(qrow + (size_t)ng * 256 + j * 16);
+            uint4 s0 = *(const uint4*)(srow + ng * Q4_GROUP);
+            uint4 s1 = *(const uint4*)(srow + ng * Q4_GROUP + 8);
+#pragma unroll
+            for (int i = 0; i < Q4_GROUP - 1; ++i) {
+                if (i < t) {
+                    float s = bf16f(i < 8 ? half_of(s0, i) : half_of(s1, i - 8));
+                    uint32_t byte = byte_of(qv, i);
+                    float w0 = (float)(byte & 15u) * s;
+                    float w1 = (float)(byte >> 4) * s;
+                    step<M>(a0, a1, w0, w1, x, x_stride, (size_t)32 * (ng * Q4_GROUP + i) + j);
+                }
+            }
         }
     }
 
@@ -282,101 +275,100 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const uint8_t* __restrict
 
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 
-// One vector (f32_m1.h): 16 rows per workgroup, x in LDS, a ring of D
-// weight groups in flight per lane. LDS: x [cols]; Q4 adds the block sums
-// [nb] and the workgroup's biases [16][nb]. Loads issued before the ring are
-// unconditional (clamped indices), so waiting for them never waits for it.
-constexpr int M1_MAX_NB = 256;               // x of at most 8192 columns
+// One vector (f32_m1.h). Loads issued before the weights are unconditional
+// (clamped indices) and so are the LDS stores that consume them (a clamped
+// piece stores its own values again): a conditional store would let the
+// compiler sink its load past the weight loads.
+constexpr int M1_MAX_NB = 256;                 // x of at most 8192 columns
 constexpr int M1_XCH = M1_MAX_NB * 32 / 1024;  // 16-byte x pieces per thread
-constexpr int M1_BCH = M1_ROWS * M1_MAX_NB / 256;  // Q4 biases per thread
+constexpr int M1W_ROWS = 8;                    // rows per workgroup of the wide kernel
+constexpr int M1W_MIN_NB = 64;                 // the wide kernel from 2048 columns
 
+// The Q4 biases of a workgroup's rows and the block sums of x, in LDS.
+template <int R>
+struct BiasStage {
+    static constexpr int K = R * M1_MAX_NB / 256;
+    uint16_t v[K];
+    int n;
+    __device__ __forceinline__ void load(const uint16_t* bi, int row0, int nrows, int nb) {
+        n = nrows * nb;
+#pragma unroll
+        for (int k = 0; k < K; ++k) v[k] = bi[(size_t)row0 * nb + min((int)threadIdx.x + 256 * k, n - 1)];
+    }
+    __device__ __forceinline__ void store(uint16_t* bl) const {
+#pragma unroll
+        for (int k = 0; k < K; ++k) bl[min((int)threadIdx.x + 256 * k, n - 1)] = v[k];
+    }
+};
+
+// 16 lanes per row, 16 rows per workgroup (rows of fewer than M1W_MIN_NB
+// blocks: at most 8 Q8 / 4 Q4 groups, all in flight). LDS: x [cols], the
+// scale rows [16][nbp]; Q4 adds the block sums [nb] and the biases [16][nb].
 template <int DT, int D>
 __global__ __launch_bounds__(256) void gemv_f32_m1_kernel(F32Mat m, const float* __restrict__ x,
                                                           float* __restrict__ y) {
     extern __shared__ float lds[];
     const int tid = threadIdx.x, nb = m.nb, cols = nb * 32, n4 = cols / 4;
-    float4 xr[M1_XCH];
+    const int row0 = blockIdx.x * M1_ROWS, nrows = min(M1_ROWS, m.rows - row0);
+    float4 xr[M1W_MIN_NB * 32 / 1024];
 #pragma unroll
-    for (int k = 0; k < M1_XCH; ++k)
+    for (int k = 0; k < M1W_MIN_NB * 32 / 1024; ++k)
         xr[k] = __builtin_bit_cast(float4, *(const f4u*)(x + 4 * min(tid + 256 * k, n4 - 1)));
-    const int row0 = blockIdx.x * M1_ROWS;
-    const int nbias = DT == 2 ? min(M1_ROWS, m.rows - row0) * nb : 0;
-    uint16_t br[M1_BCH];
-    if (DT == 2) {
-#pragma unroll
-        for (int k = 0; k < M1_BCH; ++k) br[k] = m.bi[(size_t)row0 * nb + min(tid + 256 * k, nbias - 1)];
-    }
+    ScaleStage<256, M1_ROWS * M1W_MIN_NB * 2> ss;
+    ss.load(m, row0, nrows);
+    BiasStage<M1_ROWS> bs;
+    if (DT == 2) bs.load(m.bi, row0, nrows, nb);
     const int row_raw = row0 + (tid >> 4);
     const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
     M1Lane<DT, D> L;
     L.init(m, row, tid & 15);
-    // Keep the order: the loads above, then the ring, then the LDS stores that
-    // wait for the former only.
+    // Keep the order: the loads above, then the weights, then the LDS stores
+    // that wait for the former only.
     __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
-    // Unconditional stores (a clamped piece stores its own values again): a
-    // conditional one would let the compiler sink the x load past the ring.
 #pragma unroll
-    for (int k = 0; k < M1_XCH; ++k) *(float4*)(lds + 4 * min(tid + 256 * k, n4 - 1)) = xr[k];
-    float* xs = lds + cols;
+    for (int k = 0; k < M1W_MIN_NB * 32 / 1024; ++k) *(float4*)(lds + 4 * min(tid + 256 * k, n4 - 1)) = xr[k];
+    uint16_t* sl = (uint16_t*)(lds + cols);
+    ss.store(sl);
+    float* xs = (float*)(sl + M1_ROWS * m.nbp);
     uint16_t* bl = (uint16_t*)(xs + nb);
-    if (DT == 2) {
-#pragma unroll
-        for (int k = 0; k < M1_BCH; ++k) bl[min(tid + 256 * k, nbias - 1)] = br[k];
-    }
+    if (DT == 2) bs.store(bl);
     lds_barrier();
     if (DT == 2) {
         for (int b = tid; b < nb; b += 256) xs[b] = m1_block_sum(lds + 32 * b);
         lds_barrier();
     }
-    L.run(lds);
+    L.run(lds, sl + (row - row0) * m.nbp);
     float r = L.reduce();
     if (DT == 2) r = __fadd_rn(r, m1_bias_dot(bl + (row - row0) * nb, xs, nb, tid & 15));
     if (row_raw < m.rows && (tid & 15) == 0) y[row_raw] = r;
 }
 
-// The wide one-vector kernel (long rows): 32 lanes per row, 8 rows per
-// workgroup, every group of a row in flight at once. LDS: x transposed
-// [32][S], the workgroup's scale rows [8][nbp]; Q4 adds the block sums [nb]
-// and the biases [8][nb].
-constexpr int M1W_ROWS = 8;
-constexpr int M1W_MIN_NB = 64;  // rows of at least 2048 columns
-
+// The wide kernel (long rows): 32 lanes per row, 8 rows per workgroup.
+// LDS: x transposed [32][S], the scale rows [8][nbp]; Q4 adds the block sums
+// [nb] and the biases [8][nb].
 template <int DT, int D>
 __global__ __launch_bounds__(256) void gemv_f32_m1w_kernel(F32Mat m, const float* __restrict__ x,
                                                            float* __restrict__ y) {
     extern __shared__ float lds[];
     const int tid = threadIdx.x, nb = m.nb, cols = nb * 32, n4 = cols / 4, S = m1w_stride(nb);
+    const int row0 = blockIdx.x * M1W_ROWS, nrows = min(M1W_ROWS, m.rows - row0);
     float4 xr[M1_XCH];
 #pragma unroll
     for (int k = 0; k < M1_XCH; ++k)
         xr[k] = __builtin_bit_cast(float4, *(const f4u*)(x + 4 * min(tid + 256 * k, n4 - 1)));
-    const int row0 = blockIdx.x * M1W_ROWS, nrows = min(M1W_ROWS, m.rows - row0);
-    // The scale rows (16-byte pieces; nbp is a multiple of 8).
-    constexpr int SCH = M1W_ROWS * M1_MAX_NB * 2 / 16 / 256;
-    const int nsp = nrows * m.nbp / 8;
-    uint4 sr[SCH];
-#pragma unroll
-    for (int k = 0; k < SCH; ++k) sr[k] = *(const uint4*)(m.fs + (size_t)row0 * m.nbp + 8 * min(tid + 256 * k, nsp - 1));
-    const int nbias = DT == 2 ? nrows * nb : 0;
-    constexpr int BCH = M1W_ROWS * M1_MAX_NB / 256;
-    uint16_t br[BCH];
-    if (DT == 2) {
-#pragma unroll
-        for (int k = 0; k < BCH; ++k) br[k] = m.bi[(size_t)row0 * nb + min(tid + 256 * k, nbias - 1)];
-    }
+    ScaleStage<256, M1W_ROWS * M1_MAX_NB * 2> ss;
+    ss.load(m, row0, nrows);
+    BiasStage<M1W_ROWS> bs;
+    if (DT == 2) bs.load(m.bi, row0, nrows, nb);
     const int row_raw = row0 + (tid >> 5);
     const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
     M1Wide<DT, D> L;
     L.init(m, row, tid & 31);
-    // Keep the order: the loads above, then the ring, then the LDS stores that
-    // wait for the former only.
     __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
-    // Unconditional stores (a clamped piece stores its own values again): a
-    // conditional one would let the compiler sink the x load past the ring.
 #pragma unroll
     for (int k = 0; k < M1_XCH; ++k) {
         const int p = min(tid + 256 * k, n4 - 1);
@@ -387,14 +379,10 @@ __global__ __launch_bounds__(256) void gemv_f32_m1w_kernel(F32Mat m, const float
         lds[m1w_xpos(b, c + 3, S)] = xr[k].w;
     }
     uint16_t* sl = (uint16_t*)(lds + 32 * S);
-#pragma unroll
-    for (int k = 0; k < SCH; ++k) *(uint4*)(sl + 8 * min(tid + 256 * k, nsp - 1)) = sr[k];
+    ss.store(sl);
     float* xs = (float*)(sl + M1W_ROWS * m.nbp);
     uint16_t* bl = (uint16_t*)(xs + nb);
-    if (DT == 2) {
-#pragma unroll
-        for (int k = 0; k < BCH; ++k) bl[min(tid + 256 * k, nbias - 1)] = br[k];
-    }
+    if (DT == 2) bs.store(bl);
     lds_barrier();
     if (DT == 2) {
         for (int b = tid; b < nb; b += 256) {
@@ -411,35 +399,33 @@ __global__ __launch_bounds__(256) void gemv_f32_m1w_kernel(F32Mat m, const float
     if (row_raw < m.rows && (tid & 31) == 0) y[row_raw] = r;
 }
 
-// Ring depth: eight groups where the row has them (Q4: four of 16 blocks),
-// else four (two), so a short row loads no group twice; rows of M1W_MIN_NB
-// blocks or more take the wide kernel with sixteen (eight).
+// Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
+// 16-lane kernel, 8, 16 or 32 (Q4: up to 16) for the wide one.
 template <int DT>
 void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, int rows, int nb, int nbp,
                float* y, hipStream_t st) {
     const F32Mat m{fq, fs, bi, rows, nb, nbp};
-    const int ng = nb / (DT == 1 ? 8 : 16), deep = DT == 1 ? 8 : 4;
+    const int ngp = DT == 1 ? (nb + 7) / 8 : (nb + 15) / 16;
+    const size_t q4 = DT == 2 ? (size_t)nb * 4 : 0;
     const dim3 block(256);
     if (nb >= M1W_MIN_NB) {
-        // Ring slots for every group: 8, 16 or 32 (Q8 groups number nb / 8 <= 32).
         const size_t S = ((nb + 3) & ~3) + (((nb + 3) & 4) ? 0 : 4);
-        const size_t lds = 32 * S * 4 + (size_t)M1W_ROWS * nbp * 2 +
-                           (DT == 2 ? (size_t)nb * 4 + (size_t)M1W_ROWS * nb * 2 : 0);
+        const size_t lds = 32 * S * 4 + (size_t)M1W_ROWS * nbp * 2 + q4 + (DT == 2 ? (size_t)M1W_ROWS * nb * 2 : 0);
         const dim3 grid(ceil_div(rows, M1W_ROWS));
-        if (ng <= 8)
+        if (ngp <= 8)
             gemv_f32_m1w_kernel<DT, 8><<<grid, block, lds, st>>>(m, x, y);
-        else if (ng <= 16)
+        else if (ngp <= 16)
             gemv_f32_m1w_kernel<DT, 16><<<grid, block, lds, st>>>(m, x, y);
         else
             gemv_f32_m1w_kernel<DT, 32><<<grid, block, lds, st>>>(m, x, y);
         return;
     }
-    const size_t lds = (size_t)nb * 32 * 4 + (DT == 2 ? (size_t)nb * 4 + (size_t)M1_ROWS * nb * 2 : 0);
+    const size_t lds = (size_t)nb * 32 * 4 + (size_t)M1_ROWS * nbp * 2 + q4 + (DT == 2 ? (size_t)M1_ROWS * nb * 2 : 0);
     const dim3 grid(ceil_div(rows, M1_ROWS));
-    if (ng >= deep)
-        gemv_f32_m1_kernel<DT, DT == 1 ? 8 : 4><<<grid, block, lds, st>>>(m, x, y);
-    else
+    if (ngp <= (DT == 1 ? 4 : 2))
         gemv_f32_m1_kernel<DT, DT == 1 ? 4 : 2><<<grid, block, lds, st>>>(m, x, y);
+    else
+        gemv_f32_m1_kernel<DT, DT == 1 ? 8 : 4><<<grid, block, lds, st>>>(m, x, y);
 }
 
 // The 8-lane mapping (tall matrices).
@@ -650,7 +636,7 @@ void launch_dt(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* bi,
 }  // namespace
 
 size_t f32_quant_bytes(int dtype, int rows, int nb, bool v2) {
-    if (!v2) return (size_t)rows * nb * (dtype == 1 ? 32 : 16);
+    if (!v2) return (size_t)rows * ((nb + (dtype == 1 ? 7 : 15)) / (dtype == 1 ? 8 : 16)) * 256;
     const int g = dtype == 1 ? 4 : 8;
     return (size_t)((rows + 31) / 32) * 32 * ((nb + g - 1) / g) * 128;
 }
@@ -665,7 +651,7 @@ void launch_relayout_f32(int dtype, const uint8_t* raw_qs, const uint16_t* raw_s
         else
             relayout_q4_v2_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);
     } else {
-        size_t qbytes = (size_t)rows * nb * (dtype == 1 ? 32 : 16);
+        size_t qbytes = f32_quant_bytes(dtype, rows, nb, false);
         int blocks = (int)((qbytes + 255) / 256);
         if (dtype == 1)
             relayout_q8_kernel<<<blocks, 256, 0, st>>>(raw_qs, fq, rows, nb);

@@ -50,15 +50,14 @@ namespace {
 
 using nnh::F32Mat;
 using nnh::lds_barrier;
-using nnh::M1_ROWS;
+using nnh::ScaleStage;
 using nnh::M1Lane;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int ATTN_BLOCK = 256;  // model/mod.rs:84-87
 constexpr int WG = 256;          // threads per workgroup
-constexpr int E_MAX = 2048;      // residual width: two 4-float pieces per thread
-constexpr int ECH = E_MAX / 4 / WG;
+constexpr int E_MAX = 2048;      // residual width
 
 __device__ __forceinline__ float bf16f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ uint16_t to_bf16(float f) {
@@ -111,7 +110,7 @@ __device__ float gelu_lane(float v) {
 }
 
 // A chain input in LDS, transposed: element e of a dim-vector (dim a
-// multiple of 32) at (e % 8) * S + e / 8, S = dim / 8 + 4, so FMA lane l's
+// multiple of 128) at (e % 8) * S + e / 8, S = dim / 8 + 4, so FMA lane l's
 // values are contiguous (16-byte reads) and the 4-float pad spreads the eight
 // lanes' reads over the banks.
 __device__ __forceinline__ int tstride(int dim) { return dim / 8 + 4; }
@@ -125,17 +124,27 @@ __device__ __forceinline__ void tput4(float* xt, int S, int piece, float4 v) {
 
 // hsum8 of the eight FMA lanes' sums of squares of a transposed dim-vector
 // (dim % 32 == 0), run by lanes 0..7 of the calling wave; valid at lane 0.
+// dim % 128 == 0. The LDS reads run four ahead of the FMAs, with no branch
+// between them (left to itself the compiler, short of registers, waits out
+// each read's latency in turn).
 __device__ __forceinline__ float chain_sumsq(const float* xt, int dim, int lane) {
     float a = 0.0f;
     if (lane < 8) {
         const float4* p = (const float4*)(xt + lane * tstride(dim));
-#pragma unroll 12
-        for (int m = 0; m < dim / 32; ++m) {
-            const float4 v = p[m];
-            a = __fmaf_rn(v.x, v.x, a);
-            a = __fmaf_rn(v.y, v.y, a);
-            a = __fmaf_rn(v.z, v.z, a);
-            a = __fmaf_rn(v.w, v.w, a);
+        const int n = dim / 32;
+        float4 b[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) b[k] = p[k];
+        for (int m = 0; m < n; m += 4) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 v = b[k];
+                b[k] = p[min(m + k + 4, n - 1)];  // past the end: a spare read
+                a = __fmaf_rn(v.x, v.x, a);
+                a = __fmaf_rn(v.y, v.y, a);
+                a = __fmaf_rn(v.z, v.z, a);
+                a = __fmaf_rn(v.w, v.w, a);
+            }
         }
     }
     return hsum8_lanes(a);
@@ -160,24 +169,30 @@ __device__ float wg_rms_scale(const float* xt, int dim, float eps, float* bc) {
 }
 
 // ---- the matmul kernels' prologues --------------------------------------------------------
+// NT threads per workgroup; a thread holds pieces (4 floats) tid + NT k of
+// an E-vector.
 
-// One thread's pieces (4 floats each, pieces tid and tid + 256) of a
-// prologue's inputs: the block output o, the residual x, two gammas.
-struct ResIn {
-    float4 o[ECH], x[ECH], g1[ECH], g2[ECH];
+template <int NT>
+struct Pieces {
+    static constexpr int K = (E_MAX / 4 + NT - 1) / NT;
 };
 
-__device__ __forceinline__ void res_load(ResIn& r, const float* o, const float* x, const float* g1, const float* g2,
-                                         int E) {
+// A prologue's inputs: the block output o, the residual x, two gammas.
+template <int NT>
+struct ResIn {
+    static constexpr int K = Pieces<NT>::K;
+    float4 o[K], x[K], g1[K], g2[K];
+    __device__ __forceinline__ void load(const float* po, const float* px, const float* pg1, const float* pg2, int E) {
 #pragma unroll
-    for (int k = 0; k < ECH; ++k) {
-        const int i = 4 * min((int)threadIdx.x + WG * k, E / 4 - 1);
-        r.o[k] = ld4(o + i);
-        r.x[k] = ld4(x + i);
-        r.g1[k] = ld4(g1 + i);
-        r.g2[k] = ld4(g2 + i);
+        for (int k = 0; k < K; ++k) {
+            const int i = 4 * min((int)threadIdx.x + NT * k, E / 4 - 1);
+            o[k] = ld4(po + i);
+            x[k] = ld4(px + i);
+            g1[k] = ld4(pg1 + i);
+            g2[k] = ld4(pg2 + i);
+        }
     }
-}
+};
 
 __device__ __forceinline__ float4 add_normed(float4 x, float4 o, float s, float4 g) {
     return make_float4(__fadd_rn(x.x, __fmul_rn(__fmul_rn(o.x, s), g.x)),
@@ -190,29 +205,34 @@ __device__ __forceinline__ float4 normed(float4 x, float s, float4 g) {
                        __fmul_rn(__fmul_rn(x.z, s), g.z), __fmul_rn(__fmul_rn(x.w, s), g.w));
 }
 
+// Piece index of thread slot k, and whether it is one of the vector's own
+// (slots past the end repeat the last piece: stores of it write its own
+// values again, so they need no condition).
+template <int NT>
+__device__ __forceinline__ int piece(int k, int E) { return min((int)threadIdx.x + NT * k, E / 4 - 1); }
+
 // y = RMSNorm(x, g) into LDS yl, x already in LDS xs (transposed) and in the
 // thread's registers; ends with a barrier.
-__device__ __forceinline__ void norm_to(const float4 (&xn)[ECH], const float4 (&g)[ECH], int E, float eps,
+template <int NT, int K>
+__device__ __forceinline__ void norm_to(const float4 (&xn)[K], const float4 (&g)[K], int E, float eps,
                                         const float* xs, float* yl, float* bc) {
     const float s = wg_rms_scale(xs, E, eps, bc);
 #pragma unroll
-    for (int k = 0; k < ECH; ++k)
-        if ((int)threadIdx.x + WG * k < E / 4) *(float4*)(yl + 4 * (threadIdx.x + WG * k)) = normed(xn[k], s, g[k]);
+    for (int k = 0; k < K; ++k) *(float4*)(yl + 4 * piece<NT>(k, E)) = normed(xn[k], s, g[k]);
     lds_barrier();
 }
 
 // Keep x (the new residual) in xs (transposed) and, from workgroup 0, in
 // x_out and rec.
-__device__ __forceinline__ void keep_residual(const float4 (&xn)[ECH], int E, float* xs, float* x_out, float* rec) {
+template <int NT, int K>
+__device__ __forceinline__ void keep_residual(const float4 (&xn)[K], int E, float* xs, float* x_out, float* rec) {
 #pragma unroll
-    for (int k = 0; k < ECH; ++k) {
-        const int i = threadIdx.x + WG * k;
-        if (i < E / 4) {
-            tput4(xs, tstride(E), i, xn[k]);
-            if (blockIdx.x == 0) {
-                *(float4*)(x_out + 4 * i) = xn[k];
-                if (rec) *(float4*)(rec + 4 * i) = xn[k];
-            }
+    for (int k = 0; k < K; ++k) {
+        const int i = piece<NT>(k, E);
+        tput4(xs, tstride(E), i, xn[k]);
+        if (blockIdx.x == 0) {
+            *(float4*)(x_out + 4 * i) = xn[k];
+            if (rec) *(float4*)(rec + 4 * i) = xn[k];
         }
     }
     lds_barrier();
@@ -220,54 +240,71 @@ __device__ __forceinline__ void keep_residual(const float4 (&xn)[ECH], int E, fl
 
 // x_new = x + RMSNorm(o, g1), y = RMSNorm(x_new, g2) (forward.rs:749-803):
 // a block's post-norm and residual add, then the next pre-norm. y goes to
-// LDS yl (the matmul's x). xs: LDS scratch of E + 32 floats.
-__device__ void res_norm(const ResIn& r, int E, float eps, float* xs, float* yl, float* bc, float* x_out,
-                         float* rec) {
+// LDS yl (the matmul's x). xs: LDS scratch of E + 32 floats. In two parts:
+// res_stage puts o in LDS (so every input load has landed when it returns),
+// res_norm does the rest.
+template <int NT>
+__device__ __forceinline__ void res_stage(const ResIn<NT>& r, int E, float* xs) {
 #pragma unroll
-    for (int k = 0; k < ECH; ++k)
-        if ((int)threadIdx.x + WG * k < E / 4) tput4(xs, tstride(E), threadIdx.x + WG * k, r.o[k]);
+    for (int k = 0; k < Pieces<NT>::K; ++k) tput4(xs, tstride(E), piece<NT>(k, E), r.o[k]);
     lds_barrier();
+}
+
+template <int NT>
+__device__ void res_norm(const ResIn<NT>& r, int E, float eps, float* xs, float* yl, float* bc, float* x_out,
+                         float* rec) {
+    constexpr int K = Pieces<NT>::K;
     const float s1 = wg_rms_scale(xs, E, eps, bc);
-    float4 xn[ECH];
+    float4 xn[K];
 #pragma unroll
-    for (int k = 0; k < ECH; ++k) xn[k] = add_normed(r.x[k], r.o[k], s1, r.g1[k]);
-    keep_residual(xn, E, xs, x_out, rec);
-    norm_to(xn, r.g2, E, eps, xs, yl, bc);
+    for (int k = 0; k < K; ++k) xn[k] = add_normed(r.x[k], r.o[k], s1, r.g1[k]);
+    keep_residual<NT>(xn, E, xs, x_out, rec);
+    norm_to<NT>(xn, r.g2, E, eps, xs, yl, bc);
 }
 
 // Layer 0's input: the token's Q8_0 row of the tied token_embd times
 // sqrt(n_embd) (kernels/mod.rs:917-929: f32(q) * (bf16(s) * scale)).
+template <int NT>
 struct EmbIn {
-    uint32_t q[ECH], s[ECH];  // four quants, their block's BF16 scale
-    float4 g[ECH];
+    static constexpr int K = Pieces<NT>::K;
+    uint32_t q[K], s[K];  // four quants, their block's BF16 scale
+    float4 g[K];
+    __device__ __forceinline__ void load(const uint64_t* tok, const int8_t* tq, const uint16_t* ts, const float* pg,
+                                         int E) {
+        const size_t t = (size_t)*tok;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int i = 4 * piece<NT>(k, E);
+            q[k] = *(const uint32_t*)(tq + t * E + i);
+            s[k] = ts[t * (E / 32) + i / 32];
+            g[k] = ld4(pg + i);
+        }
+    }
 };
 
-__device__ __forceinline__ void emb_load(EmbIn& r, const uint64_t* tok, const int8_t* tq, const uint16_t* ts,
-                                         const float* g, int E) {
-    const size_t t = (size_t)*tok;
-#pragma unroll
-    for (int k = 0; k < ECH; ++k) {
-        const int i = 4 * min((int)threadIdx.x + WG * k, E / 4 - 1);
-        r.q[k] = *(const uint32_t*)(tq + t * E + i);
-        r.s[k] = ts[t * (E / 32) + i / 32];
-        r.g[k] = ld4(g + i);
-    }
-}
-
-__device__ void emb_norm(const EmbIn& r, int E, float eps, float embd_scale, float* xs, float* yl, float* bc,
+template <int NT>
+__device__ void emb_norm(const EmbIn<NT>& r, int E, float eps, float embd_scale, float* xs, float* yl, float* bc,
                          float* x_out) {
-    float4 xn[ECH];
+    constexpr int K = Pieces<NT>::K;
+    float4 xn[K];
 #pragma unroll
-    for (int k = 0; k < ECH; ++k) {
+    for (int k = 0; k < K; ++k) {
         const float vs = __fmul_rn(bf16f(r.s[k]), embd_scale);
         xn[k] = make_float4(__fmul_rn((float)(int8_t)(r.q[k] & 0xffu), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 8), vs),
                             __fmul_rn((float)(int8_t)(r.q[k] >> 16), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 24), vs));
     }
-    keep_residual(xn, E, xs, x_out, nullptr);
-    norm_to(xn, r.g, E, eps, xs, yl, bc);
+    keep_residual<NT>(xn, E, xs, x_out, nullptr);
+    norm_to<NT>(xn, r.g, E, eps, xs, yl, bc);
 }
 
 // ---- the step's kernels -----------------------------------------------------------------
+// One workgroup per CU for the matmul kernels (the grids stay under 256
+// workgroups), so the wave that runs a norm's FMA chain has its SIMD to
+// itself while the others wait at the barrier.
+
+constexpr int QKV_NT = 512;   // 32 rows of one matrix per workgroup
+constexpr int FFN_NT = 1024;  // 32 gate rows and the same 32 up rows
+constexpr int MAX_NBP = E_MAX / 32;
 
 struct QkvArgs {
     F32Mat m[3];  // q, k, v
@@ -287,17 +324,19 @@ struct QkvArgs {
 };
 
 template <int D, bool FIRST>
-__global__ __launch_bounds__(WG) void qkv_kernel(QkvArgs a) {
+__global__ __launch_bounds__(QKV_NT) void qkv_kernel(QkvArgs a) {
+    constexpr int NT = QKV_NT, R = NT / 16;
     __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
     __shared__ __attribute__((aligned(16))) float yl[E_MAX];
+    __shared__ __attribute__((aligned(16))) uint16_t sl[R * MAX_NBP];
     __shared__ float bc[4];
     const int tid = threadIdx.x;
-    ResIn r;
-    EmbIn e;
+    ResIn<NT> r;
+    EmbIn<NT> e;
     if (FIRST)
-        emb_load(e, a.tok, a.tq, a.ts, a.norm, a.E);
+        e.load(a.tok, a.tq, a.ts, a.norm, a.E);
     else
-        res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
+        r.load(a.o, a.x_in, a.post, a.norm, a.E);
     int b = blockIdx.x, seg = 0;
     if (b >= a.wg[0]) {
         b -= a.wg[0];
@@ -308,18 +347,25 @@ __global__ __launch_bounds__(WG) void qkv_kernel(QkvArgs a) {
         }
     }
     const F32Mat m = a.m[seg];
-    const int row_raw = b * M1_ROWS + (tid >> 4);
+    const int row0 = b * R, row_raw = row0 + (tid >> 4);
     const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
+    ScaleStage<NT, R * MAX_NBP * 2> ss;
+    ss.load(m, row0, min(R, m.rows - row0));
     M1Lane<1, D> L;
     L.init(m, row, tid & 15);
-    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads, then the ring, then the prologue
+    // The prologue's inputs land first; the weight loads then stream while
+    // the prologue's norm chains run (issued earlier, they would queue
+    // ahead of other workgroups' prologue loads).
+    ss.store(sl);
+    if (!FIRST) res_stage<NT>(r, a.E, xs);
+    __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
     if (FIRST)
-        emb_norm(e, a.E, a.eps, a.embd_scale, xs, yl, bc, a.x_out);
+        emb_norm<NT>(e, a.E, a.eps, a.embd_scale, xs, yl, bc, a.x_out);
     else
-        res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec ? a.rec + (size_t)*a.step_p * a.rec_stride : nullptr);
-    L.run(yl);
+        res_norm<NT>(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec ? a.rec + (size_t)*a.step_p * a.rec_stride : nullptr);
+    L.run(yl, sl + (row - row0) * m.nbp);
     const float v = L.reduce();
     if (row_raw < m.rows && (tid & 15) == 0) a.y[seg][row_raw] = v;
 }
@@ -334,28 +380,39 @@ struct FfnArgs {
     float eps;
 };
 
-// Workgroup g runs gate rows 8g..8g+7 (row slots 0..7) and the same up rows
-// (slots 8..15); h = GELU(gate) * up (forward.rs:771-777).
+// Workgroup g runs gate rows 32g..32g+31 (row slots 0..31) and the same up
+// rows (slots 32..63); h = GELU(gate) * up (forward.rs:771-777).
 template <int D>
-__global__ __launch_bounds__(WG) void ffn_kernel(FfnArgs a) {
+__global__ __launch_bounds__(FFN_NT) void ffn_kernel(FfnArgs a) {
+    constexpr int NT = FFN_NT, R = NT / 16, HR = R / 2;
     __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
     __shared__ __attribute__((aligned(16))) float yl[E_MAX];
-    __shared__ float bc[4], res[M1_ROWS];
-    const int tid = threadIdx.x, slot = tid >> 4, r0 = blockIdx.x * (M1_ROWS / 2);
-    ResIn r;
-    res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
-    const int row = r0 + (slot & 7) < a.F ? r0 + (slot & 7) : a.F - 1;
+    __shared__ __attribute__((aligned(16))) uint16_t sl[R * MAX_NBP];
+    __shared__ float bc[4], res[R];
+    const int tid = threadIdx.x, slot = tid >> 4, r0 = blockIdx.x * HR;
+    ResIn<NT> r;
+    r.load(a.o, a.x_in, a.post, a.norm, a.E);
+    const int nr = min(HR, a.F - r0);
+    ScaleStage<NT, HR * MAX_NBP * 2> sg, su;
+    sg.load(a.gate, r0, nr);
+    su.load(a.up, r0, nr);
+    const int row = r0 + (slot % HR) < a.F ? r0 + (slot % HR) : a.F - 1;
     M1Lane<1, D> L;
-    L.init(slot < 8 ? a.gate : a.up, row, tid & 15);
-    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads, then the ring, then the prologue
+    L.init(slot < HR ? a.gate : a.up, row, tid & 15);
+    // The prologue's inputs land first; the weight loads then stream while
+    // the norm chains run.
+    sg.store(sl);
+    su.store(sl + HR * a.gate.nbp);
+    res_stage<NT>(r, a.E, xs);
+    __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
-    res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, nullptr);
-    L.run(yl);
+    res_norm<NT>(r, a.E, a.eps, xs, yl, bc, a.x_out, nullptr);
+    L.run(yl, sl + (slot < HR ? row - r0 : HR + row - r0) * a.gate.nbp);
     const float v = L.reduce();
     if ((tid & 15) == 0) res[slot] = v;
     lds_barrier();
-    if (tid < 8 && r0 + tid < a.F) a.h[r0 + tid] = __fmul_rn(gelu_lane(res[tid]), res[8 + tid]);
+    if (tid < HR && r0 + tid < a.F) a.h[r0 + tid] = __fmul_rn(gelu_lane(res[tid]), res[HR + tid]);
 }
 
 struct FinalArgs {
@@ -372,9 +429,10 @@ __global__ __launch_bounds__(WG) void final_kernel(FinalArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
     __shared__ __attribute__((aligned(16))) float yl[E_MAX];
     __shared__ float bc[4];
-    ResIn r;
-    res_load(r, a.o, a.x_in, a.post, a.norm, a.E);
-    res_norm(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec + (size_t)*a.step_p * a.rec_stride);
+    ResIn<WG> r;
+    r.load(a.o, a.x_in, a.post, a.norm, a.E);
+    res_stage<WG>(r, a.E, xs);
+    res_norm<WG>(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec + (size_t)*a.step_p * a.rec_stride);
     for (int i = threadIdx.x; i < a.E / 4; i += WG) *(float4*)(a.y + 4 * i) = *(const float4*)(yl + 4 * i);
 }
 
@@ -391,53 +449,73 @@ struct AttnArgs {
 // The first-maximum scan's step (scalar.rs attn_block): b follows a.
 __device__ __forceinline__ float first_max(float a, float b) { return a < b ? b : a; }
 
+// Attention workgroups per query head: each runs every score of its head
+// and the V chains of HD / ATTN_SPLIT output elements.
+constexpr int ATTN_SPLIT = 8;
+
 // One query head, one key block (forward.rs:326-351 and attn_block /
 // attn_finish, scalar.rs:444-548): q / k RMSNorm, NeoX RoPE at the current
-// position, the K/V append (by the first head of each KV group), scores by
-// 8-lane FMA dots and hsum8 times the scale, the first maximum, exp_lane,
-// the 8-lane sum of the weights over whole chunks then the tail in order,
-// and the V sum as one FMA chain per output element over the keys in order,
-// / sum. Thread t scores key t; the cached values of keys 0..n-2 are copied
-// into LDS at the start; the new key and value come from LDS.
+// position, the K/V append (by one workgroup per KV head), scores by 8-lane
+// FMA dots and hsum8 times the scale, the first maximum, exp_lane, the
+// 8-lane sum of the weights over whole chunks then the tail in order, and
+// the V sum as one FMA chain per output element over the keys in order,
+// / sum. Workgroup (h, e) of ATTN_SPLIT per head computes all of head h's
+// scores (thread t scores key t) and output elements e * EW .. e * EW + EW - 1.
+// The cached keys 0..n-2 and the workgroup's slice of their values are
+// copied into LDS at the start by coalesced direct loads; a key row's
+// 16-byte chunks are stored XOR-swizzled by the row index, so the score
+// threads (one row each) read different banks. The new key and value come
+// from LDS.
 template <int HD>
 __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
-    static_assert(HD % 8 == 0 && HD <= WG, "head size");
-    constexpr int HALF = HD / 2, CH = HD / 8;
-    __shared__ __attribute__((aligned(16))) uint16_t vs[ATTN_BLOCK * HD];
+    static_assert(HD % 64 == 0 && HD <= WG, "head size");
+    constexpr int HALF = HD / 2, CH = HD / 8, EW = HD / ATTN_SPLIT, VCH = EW / 8;
     constexpr int ST = ATTN_BLOCK / 8 + 4;  // transposed weights: lane l's run at l * ST
+    constexpr int VS = ATTN_BLOCK + 8;  // transposed value rows: element e's keys at e * VS
+    constexpr int VL = (ATTN_BLOCK * VCH + WG - 1) / WG;  // value pieces per thread
+    __shared__ __attribute__((aligned(16))) uint16_t ks_lds[ATTN_BLOCK * HD];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[EW * VS];
     __shared__ __attribute__((aligned(16))) float qs[HD];
     __shared__ __attribute__((aligned(16))) float ks[HD];
     __shared__ __attribute__((aligned(16))) float qt[HD + 32];
     __shared__ __attribute__((aligned(16))) float kt[HD + 32];
     __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
-    __shared__ uint16_t vn[HD];
     __shared__ __attribute__((aligned(16))) float sc[ATTN_BLOCK];
     __shared__ __attribute__((aligned(16))) float sct[8 * ST];
     __shared__ float red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = *a.pos_p, h = blockIdx.x, kvh = h / a.group;
+    const int pos = *a.pos_p, h = blockIdx.x / ATTN_SPLIT, es = blockIdx.x % ATTN_SPLIT, kvh = h / a.group;
     const int first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
     const int n = pos + 1 - first;  // keys; the last is the new one
     const size_t kv_dim = (size_t)a.KV * HD;
     const int i = tid < HD ? tid : HD - 1;
-    const float qv = a.q[h * HD + i], kv = a.k[kvh * HD + i], vv = a.v[kvh * HD + i];
+    const float qv = a.q[h * HD + i], kv = a.k[kvh * HD + i];
+    const float vv = a.v[kvh * HD + es * EW + (tid < EW ? tid : EW - 1)];
     const float qg = a.q_norm[i], kg = a.k_norm[i];
     const float cs = a.cos_t[(size_t)pos * HALF + i % HALF], sn = a.sin_t[(size_t)pos * HALF + i % HALF];
-    // Cached key tid (first..pos-1), unused for the new key and past the end.
-    const uint16_t* kbase = a.kc + kvh * HD;
-    const int krow = first + (tid < n - 1 ? tid : 0);
-    uint4 kr[CH];
+    // This slice of the cached values (keys first .. pos - 1), 16-byte pieces
+    // into registers (a fixed count per thread, clamped), stored transposed
+    // into LDS once they land.
+    const uint16_t* vbase = a.vc + kvh * HD + es * EW + (size_t)first * kv_dim;
+    const int nv = max((n - 1) * VCH, 1);
+    uint4 vr[VL];
 #pragma unroll
-    for (int c = 0; c < CH; ++c) kr[c] = *(const uint4*)(kbase + (size_t)krow * kv_dim + 8 * c);
-    // Cached values of keys 0..n-2, straight into LDS: 16 bytes per lane, 1 KB
-    // per wave instruction, pieces past the end repeating the last one.
-    const int nch = (n - 1) * CH, nins = (nch + 63) / 64;
-    const uint16_t* vbase = a.vc + kvh * HD;
-    for (int k = wave; k < nins; k += WG / 64) {
-        const int u = min(64 * k + lane, nch - 1);
-        const int t = u / CH, p = u - t * CH;
-        __builtin_amdgcn_global_load_lds((const void*)(vbase + (size_t)(first + t) * kv_dim + 8 * p),
-                                         (lds_ptr_t)(vs + 512 * k), 16, 0, 0);
+    for (int k = 0; k < VL; ++k) {
+        const int u = min(tid + WG * k, nv - 1);
+        vr[k] = *(const uint4*)(vbase + (size_t)(u / VCH) * kv_dim + 8 * (u % VCH));
+    }
+    // Cached keys, 16 bytes per lane straight into LDS, 1 KB per wave
+    // instruction; pieces past the end repeat the last one (their LDS slots
+    // are never read).
+    {
+        const uint16_t* kbase = a.kc + kvh * HD + (size_t)first * kv_dim;
+        const int nk = (n - 1) * CH, nik = (nk + 63) / 64;
+        for (int k = wave; k < nik; k += WG / 64) {
+            const int u = min(64 * k + lane, nk - 1);
+            const int t = u / CH, c = u % CH;  // LDS chunk c of row t holds key chunk c ^ (t % CH)
+            __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)t * kv_dim + 8 * (c ^ (t % CH))),
+                                             (lds_ptr_t)(ks_lds + 512 * k), 16, 0, 0);
+        }
     }
     // q and k RMSNorm: wave 0 runs q's chains, wave 1 k's (transposed copies).
     if (tid < HD) {
@@ -456,8 +534,8 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     if (tid < HD) {
         qs[tid] = __fmul_rn(__fmul_rn(qv, red[0]), qg);
         ks[tid] = __fmul_rn(__fmul_rn(kv, red[1]), kg);
-        vn[tid] = to_bf16(vv);
     }
+    if (tid < EW) vt[tid * VS + n - 1] = to_bf16(vv);  // the new value: key n - 1
     lds_barrier();
     // RoPE: threads 0..HALF-1 rotate q's pairs (j, j + HALF), HALF..HD-1 k's.
     if (tid < HALF) {
@@ -470,28 +548,67 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         kn[j] = to_bf16(__fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1)));
         kn[j + HALF] = to_bf16(__fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1)));
     }
+    // The cached keys and values have landed (each wave its own copies,
+    // then the barrier for the others').
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < VL; ++k) {
+        const int u = tid + WG * k;
+        if (u < (n - 1) * VCH) {
+            const int t = u / VCH, e0 = 8 * (u % VCH);
+            const uint32_t w[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) vt[(e0 + q) * VS + t] = (uint16_t)(w[q / 2] >> (16 * (q & 1)));
+        }
+    }
     lds_barrier();
     if (h % a.group == 0 && tid < HD) {
-        a.kc[(size_t)pos * kv_dim + kvh * HD + tid] = kn[tid];
-        a.vc[(size_t)pos * kv_dim + kvh * HD + tid] = vn[tid];
+        if (es == 0) a.kc[(size_t)pos * kv_dim + kvh * HD + tid] = kn[tid];
+        if (tid < EW) a.vc[(size_t)pos * kv_dim + kvh * HD + es * EW + tid] = vt[tid * VS + n - 1];
     }
-    // Scores.
+    // Scores: chunks of 8 elements in batches of SB, the next batch's LDS
+    // reads issued before this batch's FMAs.
     float s_t = -INFINITY;
     if (tid < n) {
+        constexpr int SB = 4;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         const bool last = tid == n - 1;
+        const uint16_t* krow = last ? kn : ks_lds + tid * HD;
+        const int sw = last ? 0 : tid % CH;
+        uint4 ka[SB], kb[SB];
+        float4 qa[2 * SB], qb[2 * SB];
+        auto fetch = [&](uint4 (&kk)[SB], float4 (&qq)[2 * SB], int c0) {
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const uint4 kk = last ? *(const uint4*)(kn + 8 * c) : kr[c];
-            const float4 q0 = *(const float4*)(qs + 8 * c), q1 = *(const float4*)(qs + 8 * c + 4);
-            acc[0] = __fmaf_rn(q0.x, bf16f(kk.x & 0xffffu), acc[0]);
-            acc[1] = __fmaf_rn(q0.y, bf16f(kk.x >> 16), acc[1]);
-            acc[2] = __fmaf_rn(q0.z, bf16f(kk.y & 0xffffu), acc[2]);
-            acc[3] = __fmaf_rn(q0.w, bf16f(kk.y >> 16), acc[3]);
-            acc[4] = __fmaf_rn(q1.x, bf16f(kk.z & 0xffffu), acc[4]);
-            acc[5] = __fmaf_rn(q1.y, bf16f(kk.z >> 16), acc[5]);
-            acc[6] = __fmaf_rn(q1.z, bf16f(kk.w & 0xffffu), acc[6]);
-            acc[7] = __fmaf_rn(q1.w, bf16f(kk.w >> 16), acc[7]);
+            for (int u = 0; u < SB; ++u) {
+                kk[u] = *(const uint4*)(krow + 8 * ((c0 + u) ^ sw));
+                qq[2 * u] = *(const float4*)(qs + 8 * (c0 + u));
+                qq[2 * u + 1] = *(const float4*)(qs + 8 * (c0 + u) + 4);
+            }
+        };
+        auto dot = [&](const uint4 (&kk)[SB], const float4 (&qq)[2 * SB]) {
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const uint4 k4 = kk[u];
+                const float4 q0 = qq[2 * u], q1 = qq[2 * u + 1];
+                acc[0] = __fmaf_rn(q0.x, bf16f(k4.x & 0xffffu), acc[0]);
+                acc[1] = __fmaf_rn(q0.y, bf16f(k4.x >> 16), acc[1]);
+                acc[2] = __fmaf_rn(q0.z, bf16f(k4.y & 0xffffu), acc[2]);
+                acc[3] = __fmaf_rn(q0.w, bf16f(k4.y >> 16), acc[3]);
+                acc[4] = __fmaf_rn(q1.x, bf16f(k4.z & 0xffffu), acc[4]);
+                acc[5] = __fmaf_rn(q1.y, bf16f(k4.z >> 16), acc[5]);
+                acc[6] = __fmaf_rn(q1.z, bf16f(k4.w & 0xffffu), acc[6]);
+                acc[7] = __fmaf_rn(q1.w, bf16f(k4.w >> 16), acc[7]);
+            }
+        };
+        fetch(ka, qa, 0);
+#pragma unroll
+        for (int c0 = 0; c0 < CH; c0 += 2 * SB) {
+            fetch(kb, qb, c0 + SB);
+            __builtin_amdgcn_sched_barrier(0);
+            dot(ka, qa);
+            if (c0 + 2 * SB < CH) fetch(ka, qa, c0 + 2 * SB);
+            __builtin_amdgcn_sched_barrier(0);
+            dot(kb, qb);
         }
         s_t = __fmul_rn(hsum8(acc), a.scale);
     }
@@ -534,19 +651,46 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
             red[6] = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
         }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the cached values in LDS
     lds_barrier();
-    if (tid < HD) {
-        float o;
-        if (n == 1) {
-            o = __fmul_rn(sc[0], bf16f(vn[tid]));
-        } else {
-            o = __fmul_rn(sc[0], bf16f(vs[tid]));
-#pragma unroll 16
-            for (int t = 1; t < n - 1; ++t) o = __fmaf_rn(sc[t], bf16f(vs[t * HD + tid]), o);
-            o = __fmaf_rn(sc[n - 1], bf16f(vn[tid]), o);
+    if (tid < EW) {
+        // V: one FMA chain per element over the keys in order, 8 keys per
+        // 16-byte read of the transposed values (and two of the weights),
+        // the next batch's reads issued before this batch's FMAs.
+        const uint16_t* vrow = vt + tid * VS;
+        const int nbat = (n + 7) / 8;
+        float o = 0.0f;
+        uint4 va, vb;
+        float4 pa0, pa1, pb0, pb1;
+        auto fetch = [&](uint4& v, float4& p0, float4& p1, int b) {
+            v = *(const uint4*)(vrow + 8 * b);
+            p0 = *(const float4*)(sc + 8 * b);
+            p1 = *(const float4*)(sc + 8 * b + 4);
+        };
+        auto batch = [&](const uint4& v, const float4& p0, const float4& p1, int b) {
+            const float vv[8] = {bf16f(v.x & 0xffffu), bf16f(v.x >> 16), bf16f(v.y & 0xffffu), bf16f(v.y >> 16),
+                                 bf16f(v.z & 0xffffu), bf16f(v.z >> 16), bf16f(v.w & 0xffffu), bf16f(v.w >> 16)};
+            const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            if (b > 0 && 8 * b + 8 <= n) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o = __fmaf_rn(pp[j], vv[j], o);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int t = 8 * b + j;
+                    if (t < n) o = t == 0 ? __fmul_rn(pp[j], vv[j]) : __fmaf_rn(pp[j], vv[j], o);
+                }
+            }
+        };
+        fetch(va, pa0, pa1, 0);
+        for (int b = 0; b < nbat; b += 2) {
+            fetch(vb, pb0, pb1, min(b + 1, nbat - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            batch(va, pa0, pa1, b);
+            fetch(va, pa0, pa1, min(b + 2, nbat - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 1 < nbat) batch(vb, pb0, pb1, b + 1);
         }
-        a.out[h * HD + tid] = __fmul_rn(o, red[6]);
+        a.out[h * HD + es * EW + tid] = __fmul_rn(o, red[6]);
     }
 }
 
@@ -566,14 +710,24 @@ __global__ void step_end_kernel(const uint64_t* tok, int* tokens_out, int* pos_p
         }                                                                                  \
     } while (0)
 
-// Ring depth of the fused matmuls: eight 8-block groups when the rows have
-// them, else four (no group is loaded twice).
+// Weight-load slots of the fused matmuls: at least the rows' groups.
 template <bool FIRST>
-static void launch_qkv(const QkvArgs& a, int nb, int wgs, hipStream_t st) {
-    if (nb / 8 >= 8)
-        qkv_kernel<8, FIRST><<<wgs, WG, 0, st>>>(a);
+static void launch_qkv(const QkvArgs& a, int ngp, int wgs, hipStream_t st) {
+    if (ngp <= 4)
+        qkv_kernel<4, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
+    else if (ngp <= 6)
+        qkv_kernel<6, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
     else
-        qkv_kernel<4, FIRST><<<wgs, WG, 0, st>>>(a);
+        qkv_kernel<8, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
+}
+
+static void launch_ffn(const FfnArgs& a, int ngp, int wgs, hipStream_t st) {
+    if (ngp <= 4)
+        ffn_kernel<4><<<wgs, FFN_NT, 0, st>>>(a);
+    else if (ngp <= 6)
+        ffn_kernel<6><<<wgs, FFN_NT, 0, st>>>(a);
+    else
+        ffn_kernel<8><<<wgs, FFN_NT, 0, st>>>(a);
 }
 
 }  // namespace
@@ -644,8 +798,8 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
         m->err = "bad weight count or head grouping";
         return 1;
     }
-    if (c.n_embd % 32 || c.n_embd > E_MAX || (c.head_dim != 128 && c.head_dim != 256) || c.n_ff % 32) {
-        m->err = "the fused step needs n_embd a multiple of 32 up to 2048, head_dim 128 or 256";
+    if (c.n_embd % 128 || c.n_embd > E_MAX || (c.head_dim != 128 && c.head_dim != 256) || c.n_ff % 32) {
+        m->err = "the fused step needs n_embd a multiple of 128 up to 2048, head_dim 128 or 256";
         return 1;
     }
     m->w.assign(weights, weights + n_weights);
@@ -700,7 +854,7 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
 // Queue one decode step on m->st (eagerly, or into a graph being captured).
 static int queue_step(nngd_model* m) {
     const nng_config& c = m->c;
-    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, F = c.n_ff, nb = E / 32;
+    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, F = c.n_ff, ngp = (E / 32 + 7) / 8;
     const size_t ns = norm_stride(c), rs = (size_t)c.n_layer * E;
     hipStream_t st = m->st;
     const uint8_t* te = (const uint8_t*)nnh_weight_device_data(m->w.back());
@@ -721,7 +875,7 @@ static int queue_step(nngd_model* m) {
         for (int j = 0; j < 3; ++j) {
             qa.m[j] = f[j];
             qa.y[j] = outs[j];
-            qa.wg[j] = (f[j].rows + M1_ROWS - 1) / M1_ROWS;
+            qa.wg[j] = (f[j].rows + QKV_NT / 16 - 1) / (QKV_NT / 16);
             wgs += qa.wg[j];
         }
         qa.norm = attn_norm;
@@ -733,7 +887,7 @@ static int queue_step(nngd_model* m) {
             qa.tq = (const int8_t*)te;
             qa.ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
             qa.embd_scale = std::sqrt((float)E);
-            launch_qkv<true>(qa, nb, wgs, st);
+            launch_qkv<true>(qa, ngp, wgs, st);
         } else {
             qa.o = m->o;
             qa.x_in = m->xb;
@@ -741,24 +895,20 @@ static int queue_step(nngd_model* m) {
             qa.rec = m->record + (size_t)(li - 1) * E;
             qa.step_p = m->step;
             qa.rec_stride = rs;
-            launch_qkv<false>(qa, nb, wgs, st);
+            launch_qkv<false>(qa, ngp, wgs, st);
         }
         AttnArgs aa{m->q,  m->k,         m->v,         q_norm, k_norm, m->cos_t + tab, m->sin_t + tab, m->pos,
                     m->kc + cache, m->vc + cache, H / KV, KV, sliding ? c.window : 0, c.attn_scale, eps, m->attn};
         if (hd == 256)
-            attn_kernel<256><<<H, WG, 0, st>>>(aa);
+            attn_kernel<256><<<H * ATTN_SPLIT, WG, 0, st>>>(aa);
         else
-            attn_kernel<128><<<H, WG, 0, st>>>(aa);
+            attn_kernel<128><<<H * ATTN_SPLIT, WG, 0, st>>>(aa);
         if (nnh_gemv_batch_dev(w[3], m->attn, H * hd, m->o, E, 1, NNH_ACT_F32, st)) {
             m->err = std::string("gemv: ") + nnh_last_error();
             return 1;
         }
         FfnArgs fa{f[4], f[5], m->h, F, m->o, m->xa, post_attn, ffn_norm, m->xb, E, eps};
-        const int fwgs = (F + M1_ROWS / 2 - 1) / (M1_ROWS / 2);
-        if (nb / 8 >= 8)
-            ffn_kernel<8><<<fwgs, WG, 0, st>>>(fa);
-        else
-            ffn_kernel<4><<<fwgs, WG, 0, st>>>(fa);
+        launch_ffn(fa, ngp, (F + FFN_NT / 32 - 1) / (FFN_NT / 32), st);
         if (nnh_gemv_batch_dev(w[6], m->h, F, m->o, E, 1, NNH_ACT_F32, st)) {
             m->err = std::string("gemv: ") + nnh_last_error();
             return 1;
