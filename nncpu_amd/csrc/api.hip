@@ -138,7 +138,7 @@ int check_weight(const nnh_weight* w) {
 // The int8 matmul on quantized activations: the sdot4 GEMV for up to 4
 // vectors, the few-token MFMA kernel up to 16, the MFMA GEMM beyond
 // (crossovers measured at the verify shapes; at 4 vectors the two are even).
-constexpr size_t SKINNY_MIN_TOKENS = 5;
+constexpr size_t SKINNY_MIN_TOKENS = 4;
 constexpr size_t GEMM_MIN_TOKENS = 17;
 
 // Device workspace the int8 matmul needs beyond the activation buffer.

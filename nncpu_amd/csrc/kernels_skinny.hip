@@ -1,4 +1,4 @@
-// The int8 matmul for a few activation vectors (5..16: batched speculative
+// The int8 matmul for a few activation vectors (4..16: batched speculative
 // verify, short prompts) on the matrix unit: a weight stream with a
 // 32-token MFMA.
 //
@@ -12,12 +12,15 @@
 // products from a two-block f32 outer-product MFMA, f64 accumulation), so
 // every output is within one f32 ulp of the exact sum.
 //
-// Workgroup: 4 waves on 32 weight rows. Weights, activations (tokens 0..15)
-// and scales stream through a ring of three LDS stages of 16 blocks, filled
-// by direct global -> LDS loads in which consecutive lanes read consecutive
-// 16-byte pieces of a row (coalesced), placed XOR-swizzled so the MFMA
-// operand reads are free of bank conflicts. Each wave computes 4 blocks of
-// a stage; the partial sums meet in LDS and are added in wave order.
+// Workgroup: 16 waves on 32 weight rows. Weights, activations (tokens
+// 0..15) and scales stream through a ring of three LDS stages of 16 blocks,
+// filled by direct global -> LDS loads in which consecutive lanes read
+// consecutive 16-byte pieces of a row (coalesced), placed XOR-swizzled so
+// the MFMA operand reads are free of bank conflicts. All 16 waves issue the
+// loads, two per stage each (a wave keeps only a few loads in flight: the
+// same bytes over 16 waves arrive about twice as fast as over 4, measured);
+// the first 8 waves compute two blocks of a stage each, and their partial
+// sums meet in LDS, added in wave order.
 // Matrices with few row groups are split along K over several workgroups
 // as well; those partials go to a workspace (f64) and a second kernel adds
 // them in split order.
@@ -32,9 +35,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int SK_W = 4;           // waves per workgroup
+constexpr int SK_W = 16;          // waves per workgroup (8 where registers are short): all issue loads
+constexpr int SK_CW = 8;          // of which the first SK_CW compute (2 blocks of a stage each)
 constexpr int SK_KC = 16;         // blocks per ring stage: 4 per wave
-constexpr int SK_TOK = 16;        // activation rows staged (tokens 0..15)
 constexpr int SK_MAX_SPLITS = 8;  // K-split workgroups per row group
 
 struct KArgs {
@@ -51,30 +54,35 @@ struct KArgs {
 // tokens 0..15, with their scales. Quant rows are XOR-swizzled at 16-byte
 // granularity (piece q of row r at position q ^ (r % 16)), so the MFMA
 // operand reads (32 rows, one piece each) hit 16 distinct bank groups.
-template <int DT>
+template <int DT, int NW, int TOK>
 struct KStage {
     static constexpr int QB = DT == 1 ? 32 : 16;  // weight bytes per row and block
     static constexpr int WROW = SK_KC * QB;       // bytes per staged weight row
     static constexpr int XROW = SK_KC * 32;       // bytes per staged token row
+    // Load instructions that fill a stage, and the padding that rounds them
+    // up to a whole number per wave (those land in PAD and are never read).
+    static constexpr int I_REAL = (32 * WROW + TOK * XROW + SK_KC * 32 * 4 * (DT == 2 ? 4 : 2)) / 1024;
+    static constexpr int I_PAD = (NW - I_REAL % NW) % NW;
     uint8_t W[32 * WROW];
-    int8_t X[SK_TOK * XROW];
+    int8_t X[TOK * XROW];  // tokens 0..TOK-1
     float SW[SK_KC * 32];  // [blk][row]
     float SX[SK_KC * 32];  // [blk][token]
     float BI[DT == 2 ? SK_KC * 32 : 4];
     float SXQ[DT == 2 ? SK_KC * 32 : 4];
+    uint8_t PAD[I_PAD > 0 ? I_PAD * 1024 : 16];
 };
 
-template <int DT>
+template <int DT, int NW, int TOK>
 struct KPlan {
-    static constexpr int I_W = 32 * KStage<DT>::WROW / 1024;      // 1 KB per load instruction
-    static constexpr int I_X = SK_TOK * KStage<DT>::XROW / 1024;
+    static constexpr int I_W = 32 * KStage<DT, NW, TOK>::WROW / 1024;      // 1 KB per load instruction
+    static constexpr int I_X = TOK * KStage<DT, NW, TOK>::XROW / 1024;
     static constexpr int I_S = SK_KC * 32 * 4 / 1024;              // per scale table
     static constexpr int N_S = (DT == 2 ? 4 : 2) * I_S;
-    static constexpr int I_TOTAL = I_W + I_X + N_S;
-    static constexpr int PER_WAVE = I_TOTAL / SK_W;
-    static_assert(I_TOTAL % SK_W == 0 && I_W % SK_W == 0 && I_X % SK_W == 0, "loads split evenly over the waves");
-    static_assert(KStage<DT>::WROW / 16 >= 16 && KStage<DT>::XROW / 16 >= 16, "swizzle needs 16 pieces per row");
-    static_assert(2 * PER_WAVE < 64, "vmcnt holds at most 63");
+    static constexpr int I_TOTAL = I_W + I_X + N_S + KStage<DT, NW, TOK>::I_PAD;
+    static constexpr int PER_WAVE = I_TOTAL / NW;
+    static_assert(I_TOTAL % NW == 0 && I_W + I_X + N_S == KStage<DT, NW, TOK>::I_REAL, "loads split evenly over the waves");
+    static_assert(KStage<DT, NW, TOK>::WROW / 16 >= 16 && KStage<DT, NW, TOK>::XROW / 16 >= 16, "swizzle needs 16 pieces per row");
+    static_assert(3 * PER_WAVE < 64, "vmcnt holds at most 63");
 };
 
 // The load feeding staged position `pos` (16-byte units) of a swizzled
@@ -85,18 +93,18 @@ __device__ __forceinline__ void swz_src(int pos, int ppr, int& row, int& piece) 
     piece = (pos - row * ppr) ^ (row & 15);
 }
 
-template <int DT>
-__device__ __forceinline__ void k_issue(KStage<DT>& st, const KArgs& g, int b0, int kb1, int wave, int lane, int n0) {
-    using P = KPlan<DT>;
-    constexpr int QB = KStage<DT>::QB;
+template <int DT, int NW, int TOK>
+__device__ __forceinline__ void k_issue(KStage<DT, NW, TOK>& st, const KArgs& g, int b0, int kb1, int wave, int lane, int n0) {
+    using P = KPlan<DT, NW, TOK>;
+    constexpr int QB = KStage<DT, NW, TOK>::QB;
 #pragma unroll
     for (int k = 0; k < P::PER_WAVE; ++k) {
-        const int ins = SK_W * k + wave;  // uniform per wave
+        const int ins = NW * k + wave;  // uniform per wave
         const void* src;
         lds_ptr_t dst;
         if (ins < P::I_W) {
             int row, piece;
-            swz_src(ins * 64 + lane, KStage<DT>::WROW / 16, row, piece);
+            swz_src(ins * 64 + lane, KStage<DT, NW, TOK>::WROW / 16, row, piece);
             const int n = n0 + row < g.rows ? n0 + row : g.rows - 1;
             // Pieces past the range repeat the last block (never used).
             int b = b0 + piece * 16 / QB;
@@ -107,12 +115,16 @@ __device__ __forceinline__ void k_issue(KStage<DT>& st, const KArgs& g, int b0, 
         } else if (ins < P::I_W + P::I_X) {
             const int i = ins - P::I_W;
             int row, piece;
-            swz_src(i * 64 + lane, KStage<DT>::XROW / 16, row, piece);
+            swz_src(i * 64 + lane, KStage<DT, NW, TOK>::XROW / 16, row, piece);
             const int t = row < g.n_tok ? row : g.n_tok - 1;
             int b = b0 + (piece >> 1);
             if (b >= kb1) b = kb1 - 1;
             src = g.aq + (size_t)t * g.cols + (size_t)b * 32 + 16 * (piece & 1);
             dst = (lds_ptr_t)&st.X[i * 1024];
+        } else if (ins >= KStage<DT, NW, TOK>::I_REAL) {
+            // Padding: one valid 16-byte source for every lane, into PAD.
+            src = g.aq;
+            dst = (lds_ptr_t)&st.PAD[(ins - KStage<DT, NW, TOK>::I_REAL) * 1024];
         } else {
             // Scale tables, [blk][32] f32: 8 pieces of 4 floats per block.
             const int i = ins - P::I_W - P::I_X;
@@ -147,15 +159,14 @@ __device__ __forceinline__ void k_issue(KStage<DT>& st, const KArgs& g, int b0, 
 
 // This wave's blocks 4w..4w+3 of the stage (those below nblk), in pairs for
 // the two-block scale outer products.
-template <int DT, int NR>
-__device__ __forceinline__ void k_compute(const KStage<DT>& st, double (&acc)[NR], int nblk, int wave, int h,
+template <int DT, int NR, int NW>
+__device__ __forceinline__ void k_compute(const KStage<DT, NW, 2 * NR>& st, double (&acc)[NR], int nblk, int wave, int h,
                                           int c) {
-    constexpr int QB = KStage<DT>::QB;
-    const int tc = c < SK_TOK ? c : SK_TOK - 1;  // tokens past 15: any staged row (results unused)
-#pragma unroll
-    for (int jp = 0; jp < 4; jp += 2) {
-        const int j0 = 4 * wave + jp;
-        if (j0 >= nblk) break;
+    constexpr int QB = KStage<DT, NW, 2 * NR>::QB;
+    const int tc = c < 2 * NR ? c : 2 * NR - 1;  // unstaged tokens: any staged row (results unused)
+    {
+        const int j0 = 2 * wave;  // this wave's pair of the stage's blocks
+        if (j0 >= nblk) return;
         const int jh = j0 + h;  // this lane's block of the pair for the scale products
         const v32f z = {};
         // s_x[token i] * s_w[row j] for blocks j0 and j0 + 1, exact in f32.
@@ -168,7 +179,7 @@ __device__ __forceinline__ void k_compute(const KStage<DT>& st, double (&acc)[NR
             if (j >= nblk) break;
             // Weights: row c, piece (QB == 32 ? 2j + h : j); activations: token tc, piece 2j + h.
             const int wq = QB == 32 ? 2 * j + h : j;
-            int4 w = *(const int4*)&st.W[c * KStage<DT>::WROW + 16 * (wq ^ (c & 15))];
+            int4 w = *(const int4*)&st.W[c * KStage<DT, NW, 2 * NR>::WROW + 16 * (wq ^ (c & 15))];
             if (DT == 2) {
                 const int sh = 4 * h, mk = 0x0f0f0f0f;
                 w.x = (int)((unsigned)w.x >> sh) & mk;
@@ -176,7 +187,7 @@ __device__ __forceinline__ void k_compute(const KStage<DT>& st, double (&acc)[NR
                 w.z = (int)((unsigned)w.z >> sh) & mk;
                 w.w = (int)((unsigned)w.w >> sh) & mk;
             }
-            const int4 a = *(const int4*)&st.X[tc * KStage<DT>::XROW + 16 * ((2 * j + h) ^ (tc & 15))];
+            const int4 a = *(const int4*)&st.X[tc * KStage<DT, NW, 2 * NR>::XROW + 16 * ((2 * j + h) ^ (tc & 15))];
             const v16i zi = {};
             const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(v4i{a.x, a.y, a.z, a.w}, v4i{w.x, w.y, w.z, w.w},
                                                                  zi, 0, 0, 0);
@@ -191,27 +202,32 @@ __device__ __forceinline__ void k_compute(const KStage<DT>& st, double (&acc)[NR
     }
 }
 
-template <int DT, int NR>
-__device__ __forceinline__ void k_step(KStage<DT>& cur, KStage<DT>& nxt, const KArgs& g, int c, int nchunks, int kb0,
+// Chunks 0..2 are issued at the start (every stage of the ring); after
+// that, chunk c + 2 is issued at step c into the stage chunk c - 1 used.
+template <int DT, int NR, int NW>
+__device__ __forceinline__ void k_step(KStage<DT, NW, 2 * NR>& cur, KStage<DT, NW, 2 * NR>& nxt, const KArgs& g, int c, int nchunks, int kb0,
                                        int kb1, double (&acc)[NR], int wave, int lane, int n0) {
     if (c >= nchunks) return;
-    // This wave's loads of chunk c are done once at most chunk c + 1's are outstanding.
-    if (c + 1 < nchunks)
-        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT(KPlan<DT>::PER_WAVE));
+    // This wave's loads of chunk c are done once only later chunks' are
+    // outstanding: chunks 1 and 2 at step 0, chunk c + 1 after that.
+    if (c == 0 && nchunks > 2)
+        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT((2 * KPlan<DT, NW, 2 * NR>::PER_WAVE)));
+    else if (c + 1 < nchunks)
+        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT((KPlan<DT, NW, 2 * NR>::PER_WAVE)));
     else
         __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT(0));
     __builtin_amdgcn_s_barrier();  // every wave's loads landed; every wave done with chunk c - 1
-    if (c + 2 < nchunks) k_issue<DT>(nxt, g, kb0 + (c + 2) * SK_KC, kb1, wave, lane, n0);
+    if (c >= 1 && c + 2 < nchunks) k_issue<DT, NW, 2 * NR>(nxt, g, kb0 + (c + 2) * SK_KC, kb1, wave, lane, n0);
     const int left = kb1 - kb0 - c * SK_KC;
-    k_compute<DT, NR>(cur, acc, left < SK_KC ? left : SK_KC, wave, lane >> 5, lane & 31);
+    if (wave < SK_CW) k_compute<DT, NR, NW>(cur, acc, left < SK_KC ? left : SK_KC, wave, lane >> 5, lane & 31);
 }
 
-template <int DT, int NR>
-__global__ __launch_bounds__(SK_W * 64) void skinny_i8_kernel(KArgs g, float* __restrict__ y, size_t y_stride) {
+template <int DT, int NR, int NW>
+__global__ __launch_bounds__(NW * 64) void skinny_i8_kernel(KArgs g, float* __restrict__ y, size_t y_stride) {
     // Distinct objects, so the compiler sees that loads into one stage do not
     // alias reads of another (one array would make it wait for every load).
-    __shared__ __attribute__((aligned(16))) KStage<DT> s0, s1, s2;
-    __shared__ double red[SK_W][NR][64];
+    __shared__ __attribute__((aligned(16))) KStage<DT, NW, 2 * NR> s0, s1, s2;
+    __shared__ double red[SK_CW][NR][64];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int rg = blockIdx.x / g.ksplit, ks = blockIdx.x % g.ksplit;
@@ -222,27 +238,30 @@ __global__ __launch_bounds__(SK_W * 64) void skinny_i8_kernel(KArgs g, float* __
     double acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.0;
-    if (nchunks > 0) k_issue<DT>(s0, g, kb0, kb1, wave, lane, n0);
-    if (nchunks > 1) k_issue<DT>(s1, g, kb0 + SK_KC, kb1, wave, lane, n0);
+    if (nchunks > 0) k_issue<DT, NW, 2 * NR>(s0, g, kb0, kb1, wave, lane, n0);
+    if (nchunks > 1) k_issue<DT, NW, 2 * NR>(s1, g, kb0 + SK_KC, kb1, wave, lane, n0);
+    if (nchunks > 2) k_issue<DT, NW, 2 * NR>(s2, g, kb0 + 2 * SK_KC, kb1, wave, lane, n0);
     for (int c = 0; c < nchunks; c += 3) {
-        k_step<DT, NR>(s0, s2, g, c, nchunks, kb0, kb1, acc, wave, lane, n0);
-        k_step<DT, NR>(s1, s0, g, c + 1, nchunks, kb0, kb1, acc, wave, lane, n0);
-        k_step<DT, NR>(s2, s1, g, c + 2, nchunks, kb0, kb1, acc, wave, lane, n0);
+        k_step<DT, NR, NW>(s0, s2, g, c, nchunks, kb0, kb1, acc, wave, lane, n0);
+        k_step<DT, NR, NW>(s1, s0, g, c + 1, nchunks, kb0, kb1, acc, wave, lane, n0);
+        k_step<DT, NR, NW>(s2, s1, g, c + 2, nchunks, kb0, kb1, acc, wave, lane, n0);
     }
 
+    if (wave < SK_CW) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) red[wave][r][lane] = acc[r];
+        for (int r = 0; r < NR; ++r) red[wave][r][lane] = acc[r];
+    }
     __syncthreads();
-    // Thread (r, l) finishes result register r of lane l: the SK_W * 64
-    // threads cover the NR * 64 outputs in NR / SK_W rounds.
-    static_assert(NR % SK_W == 0, "whole rounds");
+    // Thread (r, l) of the first NR waves finishes result register r of lane l.
+    static_assert(NR <= NW, "one round");
     const int l = tid & 63;
     const int row = n0 + (l & 31);
-#pragma unroll
-    for (int r = tid >> 6; r < NR; r += SK_W) {
+    {
+        const int r = tid >> 6;
+        if (r >= NR) return;
         double s = 0.0;
 #pragma unroll
-        for (int w = 0; w < SK_W; ++w) s += red[w][r][l];
+        for (int w = 0; w < SK_CW; ++w) s += red[w][r][l];
         const int i = (r / 4) * 8 + 4 * (l >> 5) + (r % 4);  // token
         if (i < g.n_tok && row < g.rows) {
             if (g.ksplit == 1)
@@ -304,12 +323,13 @@ void launch_skinny_i8(int dtype, const uint8_t* qs, const float* swT, const int8
     g.ksplit = skinny_splits(rows, nb);
     g.cols = (size_t)nb * 32;
     g.qrow = dtype == 1 ? g.cols : g.cols / 2;
-    const dim3 grid(ceil_div(rows, 32) * g.ksplit), block(SK_W * 64);
-#define NNH_SK(DT, NR) skinny_i8_kernel<DT, NR><<<grid, block, 0, st>>>(g, y, y_stride)
+    const dim3 grid(ceil_div(rows, 32) * g.ksplit);
+    // Q4 with 16 tokens needs more registers than 16 waves leave a lane: 8 waves there.
+#define NNH_SK(DT, NR, NW) skinny_i8_kernel<DT, NR, NW><<<grid, NW * 64, 0, st>>>(g, y, y_stride)
     if (dtype == 1) {
-        if (n_tok <= 8) NNH_SK(1, 4); else NNH_SK(1, 8);
+        if (n_tok <= 8) NNH_SK(1, 4, SK_W); else NNH_SK(1, 8, SK_W);
     } else {
-        if (n_tok <= 8) NNH_SK(2, 4); else NNH_SK(2, 8);
+        if (n_tok <= 8) NNH_SK(2, 4, SK_W); else NNH_SK(2, 8, SK_W / 2);
     }
 #undef NNH_SK
     if (g.ksplit > 1)

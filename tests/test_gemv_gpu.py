@@ -324,6 +324,8 @@ def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
     (1536, 6144, 5),    # few-token kernel at its lower bound, K split over 5 workgroups
     (96, 4128, 11),     # few-token kernel: nb = 129, a partial last stage, 3 row groups
     (6144, 1536, 8),    # few-token kernel, unsplit, tokens in registers 0-3 only
+    (333, 1536, 4),     # few-token kernel at its lower bound (4 tokens), ragged rows
+    (1536, 6144, 16),   # few-token kernel, 16 tokens staged, K split
 ])
 def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
     # The MFMA GEMM forms every block dot exactly; each output must be within
