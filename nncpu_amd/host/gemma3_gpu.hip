@@ -452,6 +452,9 @@ __device__ __forceinline__ float first_max(float a, float b) { return a < b ? b 
 // Attention workgroups per query head: each runs every score of its head
 // and the V chains of HD / ATTN_SPLIT output elements.
 constexpr int ATTN_SPLIT = 8;
+// Threads per attention workgroup: all 16 waves issue the cache loads (a
+// wave keeps only a few loads in flight), the first 4 do the rest.
+constexpr int ATTN_NT = 1024;
 
 // One query head, one key block (forward.rs:326-351 and attn_block /
 // attn_finish, scalar.rs:444-548): q / k RMSNorm, NeoX RoPE at the current
@@ -467,12 +470,12 @@ constexpr int ATTN_SPLIT = 8;
 // threads (one row each) read different banks. The new key and value come
 // from LDS.
 template <int HD>
-__global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
-    static_assert(HD % 64 == 0 && HD <= WG, "head size");
+__global__ __launch_bounds__(ATTN_NT) void attn_kernel(AttnArgs a) {
+    static_assert(HD % 64 == 0 && HD <= WG && ATTN_BLOCK <= WG, "head size, key block");
     constexpr int HALF = HD / 2, CH = HD / 8, EW = HD / ATTN_SPLIT, VCH = EW / 8;
     constexpr int ST = ATTN_BLOCK / 8 + 4;  // transposed weights: lane l's run at l * ST
     constexpr int VS = ATTN_BLOCK + 8;  // transposed value rows: element e's keys at e * VS
-    constexpr int VL = (ATTN_BLOCK * VCH + WG - 1) / WG;  // value pieces per thread
+    constexpr int VL = (ATTN_BLOCK * VCH + ATTN_NT - 1) / ATTN_NT;  // value pieces per thread
     __shared__ __attribute__((aligned(16))) uint16_t ks_lds[ATTN_BLOCK * HD];
     __shared__ __attribute__((aligned(16))) uint16_t vt[EW * VS];
     __shared__ __attribute__((aligned(16))) float qs[HD];
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
     __shared__ __attribute__((aligned(16))) float sc[ATTN_BLOCK];
     __shared__ __attribute__((aligned(16))) float sct[8 * ST];
-    __shared__ float red[8];
+    __shared__ float red[2 + ATTN_NT / 64 + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = *a.pos_p, h = blockIdx.x / ATTN_SPLIT, es = blockIdx.x % ATTN_SPLIT, kvh = h / a.group;
     const int first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
@@ -501,7 +504,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     uint4 vr[VL];
 #pragma unroll
     for (int k = 0; k < VL; ++k) {
-        const int u = min(tid + WG * k, nv - 1);
+        const int u = min(tid + ATTN_NT * k, nv - 1);
         vr[k] = *(const uint4*)(vbase + (size_t)(u / VCH) * kv_dim + 8 * (u % VCH));
     }
     // Cached keys, 16 bytes per lane straight into LDS, 1 KB per wave
@@ -510,7 +513,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     {
         const uint16_t* kbase = a.kc + kvh * HD + (size_t)first * kv_dim;
         const int nk = (n - 1) * CH, nik = (nk + 63) / 64;
-        for (int k = wave; k < nik; k += WG / 64) {
+        for (int k = wave; k < nik; k += ATTN_NT / 64) {
             const int u = min(64 * k + lane, nk - 1);
             const int t = u / CH, c = u % CH;  // LDS chunk c of row t holds key chunk c ^ (t % CH)
             __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)t * kv_dim + 8 * (c ^ (t % CH))),
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int k = 0; k < VL; ++k) {
-        const int u = tid + WG * k;
+        const int u = tid + ATTN_NT * k;
         if (u < (n - 1) * VCH) {
             const int t = u / VCH, e0 = 8 * (u % VCH);
             const uint32_t w[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
@@ -570,7 +573,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     // reads issued before this batch's FMAs.
     float s_t = -INFINITY;
     if (tid < n) {
-        constexpr int SB = 4;
+        constexpr int SB = 2;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         const bool last = tid == n - 1;
         const uint16_t* krow = last ? kn : ks_lds + tid * HD;
@@ -625,7 +628,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     lds_barrier();
     float m = red[2];
 #pragma unroll
-    for (int w = 1; w < WG / 64; ++w) m = first_max(m, red[2 + w]);
+    for (int w = 1; w < ATTN_NT / 64; ++w) m = first_max(m, red[2 + w]);
     if (tid < n) {
         const float pw = exp_lane(__fsub_rn(s_t, m));
         sc[tid] = pw;
@@ -648,7 +651,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         float l = hsum8_lanes(acc);
         if (tid == 0) {
             for (int j = body; j < n; ++j) l = __fadd_rn(l, sc[j]);
-            red[6] = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
+            red[2 + ATTN_NT / 64] = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
         }
     }
     lds_barrier();
@@ -690,7 +693,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < nbat) batch(vb, pb0, pb1, b + 1);
         }
-        a.out[h * HD + es * EW + tid] = __fmul_rn(o, red[6]);
+        a.out[h * HD + es * EW + tid] = __fmul_rn(o, red[2 + ATTN_NT / 64]);
     }
 }
 
@@ -900,9 +903,9 @@ static int queue_step(nngd_model* m) {
         AttnArgs aa{m->q,  m->k,         m->v,         q_norm, k_norm, m->cos_t + tab, m->sin_t + tab, m->pos,
                     m->kc + cache, m->vc + cache, H / KV, KV, sliding ? c.window : 0, c.attn_scale, eps, m->attn};
         if (hd == 256)
-            attn_kernel<256><<<H * ATTN_SPLIT, WG, 0, st>>>(aa);
+            attn_kernel<256><<<H * ATTN_SPLIT, ATTN_NT, 0, st>>>(aa);
         else
-            attn_kernel<128><<<H * ATTN_SPLIT, WG, 0, st>>>(aa);
+            attn_kernel<128><<<H * ATTN_SPLIT, ATTN_NT, 0, st>>>(aa);
         if (nnh_gemv_batch_dev(w[3], m->attn, H * hd, m->o, E, 1, NNH_ACT_F32, st)) {
             m->err = std::string("gemv: ") + nnh_last_error();
             return 1;
