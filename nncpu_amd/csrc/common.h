@@ -59,6 +59,17 @@ __device__ __forceinline__ uint4 load_nt16u(const void* p) {
     return make_uint4((unsigned)v.x, (unsigned)v.y, (unsigned)v.z, (unsigned)v.w);
 }
 
+// LDS pointer for __builtin_amdgcn_global_load_lds (global -> LDS, no
+// staging registers): lane l's 16 bytes land at dst + 16 l, dst uniform.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt immediate with vmcnt = n (bits 3:0 and 15:14); expcnt and
+// lgkmcnt at their maxima, so they do not wait. Direct-to-LDS loads count in
+// vmcnt like any other vector memory load.
+#define NNH_VMCNT(n) ((((n)&0xF) | (0x7 << 4) | (0xF << 8) | ((((n) >> 4) & 0x3) << 14)))
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+#define NNH_LGKMCNT0 (0xF | (0x7 << 4) | (0x3 << 14))
+
 inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ---- launchers (defined beside their kernels) -------------------------------

@@ -43,6 +43,8 @@
 // nb). The reduction becomes xor-2, xor-4 (the accumulator pairs), xor-1
 // and an in-lane pair sum (hsum8): the same additions.
 
+#include <algorithm>
+
 #include "common.h"
 #include "f32_m1.h"
 
@@ -399,6 +401,257 @@ __global__ __launch_bounds__(256) void gemv_f32_m1w_kernel(F32Mat m, const float
     if (row_raw < m.rows && (tid & 31) == 0) y[row_raw] = r;
 }
 
+// The staged kernel (long rows): 1024 threads, at most 8 rows per
+// workgroup, about one workgroup per CU. A wave keeps only a few loads in
+// flight, so all 16 waves copy x, the rows' scales and the rows' padded
+// groups into LDS by direct 1 KB loads (no registers; weight chunk i of row
+// r = groups 4i..4i+3, issued in the order c = i * nr + r, copy k of wave w
+// being chunk 16 k + w), and the first ceil(nr / 2) waves run the chains
+// from LDS, 32 lanes per row as in M1Wide, stage by stage behind the copies:
+// once every wave's k-th weight copy has landed, each row holds the groups
+// of the first 16 (k + 1) chunks. Every wait is explicit (vmcnt counts a
+// wave's copies in issue order); the Q4 biases are the only register loads
+// and are consumed after the last wait. The scales are converted to f32 once
+// per workgroup, while the weights are still in flight.
+constexpr int M1S_NT = 1024;
+constexpr int M1S_WAVES = M1S_NT / 64;
+constexpr int M1S_ROWS = 8;  // rows per workgroup at most (4 computing waves)
+
+struct M1sLayout {
+    int ngp, ng4, nx, ns, SR;  // groups and 1 KB weight chunks per row; x and scale chunks; f32 scale row
+    size_t w, x, s, sf, xs, bl, bytes;
+    __host__ __device__ M1sLayout(int dt, int nb, int nbp, int nr) {
+        const int G = dt == 1 ? 8 : 16;
+        ngp = (nb + G - 1) / G;
+        ng4 = (ngp + 3) / 4;
+        nx = (nb + 7) / 8;
+        ns = (nr * nbp * 2 + 1023) / 1024;
+        SR = ngp * G;
+        w = 0;
+        x = w + (size_t)nr * ng4 * 1024;
+        s = x + (size_t)nx * 1024;
+        sf = s + (size_t)ns * 1024;
+        xs = sf + (size_t)nr * SR * 4;
+        bl = xs + (size_t)((nb + 3) & ~3) * 4;
+        bytes = bl + (dt == 2 ? (size_t)nr * nb * 2 : 0);
+    }
+};
+
+// s_waitcnt vmcnt(n) for a uniform n in 0..4.
+__device__ __forceinline__ void wait_vm_upto4(int n) {
+    if (n <= 0)
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
+    else if (n == 1)
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(1));
+    else if (n == 2)
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(2));
+    else if (n == 3)
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(3));
+    else
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(4));
+}
+
+// One 1 KB copy of the bytes [off, off + 1024) of a span of `len` bytes
+// (a multiple of 16) to dst (uniform); lanes past the end repeat the span's
+// last 16 bytes. Issued as asm: for the builtin the compiler cannot tell
+// the copy's LDS destination from any later LDS read and waits for every
+// copy before each read, which would undo the staging (the waits here are
+// explicit instead).
+__device__ __forceinline__ void copy_1k(const void* span, size_t len, size_t off, unsigned char* dst, int lane) {
+    const size_t o = min(off + lane * 16, len - 16);
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const unsigned char*)span + o),
+                 "{m0}"((uint32_t)(uintptr_t)dst)
+                 : "memory");
+}
+
+// One group of a lane's chain: the 16-byte piece, G values of x (row-major
+// x, element j: stride 32) and G f32 scales, all from LDS.
+template <int DT>
+struct M1sGroup {
+    static constexpr int G = DT == 1 ? 8 : 16;
+    uint4 q;
+    float x[G], s[G];
+    __device__ __forceinline__ void read(const unsigned char* wrow, const float* xrow, const float* srow, int g) {
+        q = *(const uint4*)(wrow + g * 256);
+#pragma unroll
+        for (int i = 0; i < G; ++i) x[i] = xrow[32 * (g * G + i)];
+#pragma unroll
+        for (int i = 0; i < G; i += 4) {
+            const float4 u = *(const float4*)(srow + g * G + i);
+            s[i] = u.x, s[i + 1] = u.y, s[i + 2] = u.z, s[i + 3] = u.w;
+        }
+    }
+    // Blocks i < nblk (all when FULL) into the chain a; h: byte (Q4:
+    // nibble) of each pair.
+    template <bool FULL>
+    __device__ __forceinline__ void run(float& a, int h, int nblk) const {
+        const uint32_t dw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            float w;
+            if (DT == 1) {
+                const uint32_t dd = dw[i >> 1] >> (8 * h);
+                w = (float)(int8_t)(dd >> (16 * (i & 1)));
+            } else {
+                const uint32_t dd = (dw[i >> 2] >> (4 * h)) & 0x0f0f0f0fu;
+                w = (float)((dd >> (8 * (i & 3))) & 0xffu);
+            }
+            if (FULL || i < nblk) a = __builtin_fmaf(w * s[i], x[i], a);
+        }
+    }
+};
+
+// nr_max: the largest row count of a workgroup; K: weight copies per wave,
+// ceil(ng4 * nr_max / 16). x must be 16-byte aligned.
+template <int DT, int K>
+__global__ __launch_bounds__(M1S_NT) void gemv_f32_m1s_kernel(F32Mat m, const float* __restrict__ x,
+                                                             float* __restrict__ y, int nr_max) {
+    constexpr int G = DT == 1 ? 8 : 16;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb = m.nb;
+    const M1sLayout L(DT, nb, m.nbp, nr_max);
+    const int row0 = (int)((long)blockIdx.x * m.rows / gridDim.x);
+    const int nr = (int)((long)(blockIdx.x + 1) * m.rows / gridDim.x) - row0;
+
+    // Q4 biases (t >> 7, (t & 127) + 128 k) of the rows: registers, stored
+    // after the last wait.
+    const int br = min(tid >> 7, nr - 1);
+    int bb[2];
+    uint16_t bv[2];
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            bb[k] = min((tid & 127) + 128 * k, nb - 1);
+            bv[k] = m.bi[(size_t)(row0 + br) * nb + bb[k]];
+        }
+    }
+
+    // x and the scale rows first (32 + 4 chunks at most for nb <= 256).
+    const size_t xlen = (size_t)nb * 128, slen = (size_t)nr * m.nbp * 2;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int c = M1S_WAVES * k + wave;
+        if (c < L.nx)
+            copy_1k(x, xlen, (size_t)c * 1024, smem + L.x + (size_t)c * 1024, lane);
+        else if (c < L.nx + L.ns)
+            copy_1k(m.fs + (size_t)row0 * m.nbp, slen, (size_t)(c - L.nx) * 1024,
+                    smem + L.s + (size_t)(c - L.nx) * 1024, lane);
+    }
+    // The weights: this wave's kw copies (chunks wave, wave + 16, ...).
+    const int nc = L.ng4 * nr;
+    const int kw = min(K, (nc - wave + M1S_WAVES - 1) / M1S_WAVES);
+    const size_t rbytes = (size_t)L.ngp * 256;
+    const uint8_t* wbase = m.fq + (size_t)row0 * rbytes;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = M1S_WAVES * k + wave;
+        if (c < nc) {
+            const int i = c / nr, r = c - i * nr;
+            copy_1k(wbase + (size_t)r * rbytes, rbytes, (size_t)i * 1024, smem + L.w + ((size_t)r * L.ng4 + i) * 1024,
+                    lane);
+        }
+    }
+
+    // x and the scales landed (the weights may not have): f32 scales and,
+    // for Q4, the block sums of x (waves 4.. never compute).
+    wait_vm_upto4(kw);
+    lds_barrier();
+    float* sf = (float*)(smem + L.sf);
+    float* xs = (float*)(smem + L.xs);
+    {
+        const uint16_t* sb = (const uint16_t*)(smem + L.s);
+        for (int e = tid; e < nr * nb; e += M1S_NT) {
+            const int r = e / nb, b = e - r * nb;
+            sf[r * L.SR + b] = bf16f(sb[r * m.nbp + b]);
+        }
+        if (DT == 2 && tid >= 256 && tid - 256 < nb)
+            xs[tid - 256] = m1_block_sum((const float*)(smem + L.x) + 32 * (tid - 256));
+    }
+
+    // The chains: lane j of the row's 32 runs element j; lanes j and j + 16
+    // read the same 16-byte piece and take byte (Q4: nibble) h of each pair.
+    // Two groups in flight: the next group's LDS reads are issued before the
+    // current group's arithmetic.
+    const int ncw = (nr + 1) >> 1;
+    const int r = min(2 * wave + (lane >> 5), nr - 1), j = lane & 31, h = j >> 4;
+    const unsigned char* wrow = smem + L.w + (size_t)r * L.ng4 * 1024 + (j & 15) * 16;
+    const float* xrow = (const float*)(smem + L.x) + j;
+    const float* srow = sf + r * L.SR;
+    const int ng = nb / G;
+    float a = 0.0f;
+    int glo = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        wait_vm_upto4(kw - 1 - k);
+        lds_barrier();
+        int ghi = L.ngp;
+        if (k < K - 1) {
+            const int ready = M1S_WAVES * (k + 1) - (nr - 1);
+            ghi = ready <= 0 ? 0 : min(L.ngp, 4 * ((ready + nr - 1) / nr));
+        }
+        if (wave < ncw) {
+            const int gf = min(ghi, ng);  // whole groups of this stage: [glo, gf)
+            if (glo < gf) {
+                M1sGroup<DT> A, B, C;
+                A.read(wrow, xrow, srow, glo);
+                B.read(wrow, xrow, srow, min(glo + 1, gf - 1));
+                __builtin_amdgcn_s_waitcnt(NNH_LGKMCNT0);
+                int g = glo;
+                for (; g + 2 < gf; g += 3) {
+                    C.read(wrow, xrow, srow, g + 2);
+                    __builtin_amdgcn_sched_barrier(0);
+                    A.template run<true>(a, h, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                    A.read(wrow, xrow, srow, min(g + 3, gf - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    B.template run<true>(a, h, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                    B.read(wrow, xrow, srow, min(g + 4, gf - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    C.template run<true>(a, h, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (g < gf) A.template run<true>(a, h, G);
+                if (g + 1 < gf) B.template run<true>(a, h, G);
+            }
+            if (ghi == L.ngp && ng < L.ngp && glo <= ng) {
+                M1sGroup<DT> A;
+                A.read(wrow, xrow, srow, ng);
+                A.template run<false>(a, h, nb - ng * G);
+            }
+        }
+        glo = ghi;
+    }
+    uint16_t* bl = (uint16_t*)(smem + L.bl);
+    if (DT == 2) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) bl[br * nb + bb[k]] = bv[k];
+        lds_barrier();
+    }
+    if (wave >= ncw) return;
+    const float u = __fadd_rn(a, xor_get(a, 8));
+    const float v = __fadd_rn(u, xor_get(u, 16));
+    const float p = __fadd_rn(v, xor_get(v, 4));
+    const float q = __fadd_rn(p, xor_get(p, 1));
+    float res = __fadd_rn(q, xor_get(q, 2));
+    if (DT == 2) res = __fadd_rn(res, m1_bias_dot(bl + r * nb, xs, nb, j));
+    if (2 * wave + (lane >> 5) < nr && j == 0) y[row0 + 2 * wave + (lane >> 5)] = res;
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
 // 16-lane kernel, 8, 16 or 32 (Q4: up to 16) for the wide one.
 template <int DT>
@@ -408,6 +661,25 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
     const int ngp = DT == 1 ? (nb + 7) / 8 : (nb + 15) / 16;
     const size_t q4 = DT == 2 ? (size_t)nb * 4 : 0;
     const dim3 block(256);
+    if (nb >= M1W_MIN_NB) {
+        // About one workgroup per CU, at most M1S_ROWS rows each.
+        const int nwg = std::max(std::min(rows, cu_count()), ceil_div(rows, M1S_ROWS));
+        const int nr = ceil_div(rows, nwg);
+        const M1sLayout L(DT, nb, nbp, nr);
+        const int k = ceil_div((long)L.ng4 * nr, M1S_WAVES);
+        const dim3 g(nwg), b(M1S_NT);
+        if (((uintptr_t)x & 15) == 0 && k <= 4) {
+            if (k <= 1)
+                gemv_f32_m1s_kernel<DT, 1><<<g, b, L.bytes, st>>>(m, x, y, nr);
+            else if (k == 2)
+                gemv_f32_m1s_kernel<DT, 2><<<g, b, L.bytes, st>>>(m, x, y, nr);
+            else if (k == 3)
+                gemv_f32_m1s_kernel<DT, 3><<<g, b, L.bytes, st>>>(m, x, y, nr);
+            else
+                gemv_f32_m1s_kernel<DT, 4><<<g, b, L.bytes, st>>>(m, x, y, nr);
+            return;
+        }
+    }
     if (nb >= M1W_MIN_NB) {
         const size_t S = ((nb + 3) & ~3) + (((nb + 3) & 4) ? 0 : 4);
         const size_t lds = 32 * S * 4 + (size_t)M1W_ROWS * nbp * 2 + q4 + (DT == 2 ? (size_t)M1W_ROWS * nb * 2 : 0);

@@ -9,16 +9,19 @@
 // j + 32h, register r, with i = (r/4)*8 + 4h + r%4: a lane owns one token
 // and 16 weight rows of each 32 x 32 tile.
 //
-// Epilogue per block and output: acc = fma(P, s_w * s_x, acc) (+ Q4
-// acc = fma(bias, s_x * sum q_x, acc)) in f64; P and the scale products are
-// exact, so every output is within one f32 ulp of the exact sum (an f32 sum
-// over K = 18944 would take most of the 1e-5 tolerance next to nncpu's own
-// f32 rounding). The scale products s_w[n] s_x[m] come from the matrix unit
-// too: one v_mfma_f32_32x32x1_2b_f32 forms the outer products of two blocks
-// exactly, already in the result layout, so each lane needs one scale per
-// block instead of sixteen. nncpu's per-32 BF16 scales make this epilogue,
-// not the int8 MFMA, the compute bound: 3 (Q8) / 5 (Q4) VALU ops per output
-// and block against 32 MACs.
+// Epilogue per block and output: acc = fma(f32(P), s_w * s_x, acc) in f32,
+// P and the scale product being exact, with the f32 sum folded into an f64
+// total every 8 blocks (an f32 sum over K = 18944 would take most of the
+// 1e-5 tolerance next to nncpu's own f32 rounding; chunks of 8 keep the
+// error within 8 f32 roundings of the absolute block terms). The scale
+// products s_w[n] s_x[m] come from the matrix unit too: one
+// v_mfma_f32_32x32x1_2b_f32 forms the outer products of two blocks exactly,
+// already in the result layout, so each lane needs one scale per block
+// instead of sixteen; and the Q4 bias term sum_b bias[n,b] (s_x sum q_x)[m,b]
+// is an outer-product sum, one v_mfma_f32_32x32x2f32 per two blocks
+// accumulating into the same f32 tile. nncpu's per-32 BF16 scales make this
+// epilogue, not the int8 MFMA, the compute bound: 2 VALU ops per output and
+// block (the int32 -> f32 conversion and the FMA) against 32 MACs.
 //
 // Workgroup: 128 weight rows x 128 tokens, 16 waves (4 per SIMD, to hide the
 // MFMA -> VALU latency), each wave one 32 x 32 tile. The K loop runs over
@@ -37,8 +40,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int TILE = 128;  // weight rows and tokens per workgroup
 constexpr int GEMM_MAX_SPLITS = 8;
@@ -146,10 +149,6 @@ __device__ __forceinline__ void issue_stage(GStage<DT, KB>& st, const GArgs& g, 
     }
 }
 
-// s_waitcnt immediate with vmcnt = n (bits 3:0 and 15:14); expcnt and
-// lgkmcnt at their maxima, so they do not wait.
-#define NNH_VMCNT(n) ((((n)&0xF) | (0x7 << 4) | (0xF << 8) | ((((n) >> 4) & 0x3) << 14)))
-
 // Two outer products u_0 v_0^T and u_1 v_1^T of 32-vectors, exact in f32
 // (the factors are BF16 values, so every product has at most 16 significant
 // bits), each laid out like the i8 MFMA's result: one
@@ -164,8 +163,8 @@ __device__ __forceinline__ v32f outer32x2(float u, float v) {
 // blocks, two at a time: lanes 0-31 read the scales of the first block of a
 // pair, lanes 32-63 those of the second.
 template <int DT, int KB>
-__device__ __forceinline__ void compute_stage(const GStage<DT, KB>& st, double (&acc)[16], int nblk, int rowA,
-                                              int colB, int h, int c) {
+__device__ __forceinline__ void compute_stage(const GStage<DT, KB>& st, v16f& acc, int nblk, int rowA, int colB, int h,
+                                              int c) {
     constexpr int QB = GStage<DT, KB>::QB;
     static_assert(KB % 2 == 0, "blocks go in pairs");
 #pragma unroll
@@ -193,21 +192,14 @@ __device__ __forceinline__ void compute_stage(const GStage<DT, KB>& st, double (
             const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(v4i{a.x, a.y, a.z, a.w}, v4i{bq.x, bq.y, bq.z, bq.w},
                                                                  z, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = __builtin_fma((double)P[r], (double)S[16 * jj + r], acc[r]);
+            for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf((float)P[r], S[16 * jj + r], acc[r]);
         }
         if (DT == 2) {
-            // Bias term: acc += bias[n] * (s_x * sum q_x)[m], the product in f64
-            // (up to 8 + 20 significant bits); the MFMA spreads bias[n] over the
-            // result layout (bias x ones).
-            const v32f Bo = outer32x2(st.BI[jh * TILE + rowA + c], 1.0f);
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int j = jp + jj;
-                if (j >= nblk) break;
-                const double sxq = (double)st.SXQ[j * TILE + colB + c];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[r] = __builtin_fma((double)Bo[16 * jj + r], sxq, acc[r]);
-            }
+            // Bias term of the pair: acc += sum_j bias[n, j] (s_x sum q_x)[m, j],
+            // lane l giving bias[row l%32] and s_x sum q_x[token l%32] of block
+            // jp + l/32 (zero past the stage's blocks).
+            const float bi = jh < nblk ? st.BI[jh * TILE + rowA + c] : 0.0f;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(bi, st.SXQ[jh * TILE + colB + c], acc, 0, 0, 0);
         }
     }
 }
@@ -216,8 +208,8 @@ __device__ __forceinline__ void compute_stage(const GStage<DT, KB>& st, double (
 // `nxt`, the stage chunk c - 1 was computed from.
 template <int DT, int KB>
 __device__ __forceinline__ void pipeline_step(GStage<DT, KB>& cur, GStage<DT, KB>& nxt, const GArgs& g, int c,
-                                              int nchunks, double (&acc)[16], int wave, int lane, int n0, int m0,
-                                              int wn, int wm, int h) {
+                                              int nchunks, v16f& acc, double (&tot)[16], int wave, int lane, int n0,
+                                              int m0, int wn, int wm, int h) {
     using P = GPlan<DT, KB>;
     if (c >= nchunks) return;
     // This wave's loads of chunk c are done once at most chunk c + 1's are outstanding.
@@ -235,6 +227,14 @@ __device__ __forceinline__ void pipeline_step(GStage<DT, KB>& cur, GStage<DT, KB
     const int left = g.kb1 - g.kb0 - c * KB;
     const int nblk = left < KB ? left : KB;
     compute_stage<DT, KB>(cur, acc, nblk, wn * 32, wm * 32, h, lane & 31);
+    // The f32 sum goes into the f64 total every 8 blocks and at the end.
+    if ((c & 1) || c + 1 == nchunks) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            tot[r] += (double)acc[r];
+            acc[r] = 0.0f;
+        }
+    }
 }
 
 // A wave's 32 x 32 result tile turned around in LDS (`wout`, 4 KB), as
@@ -289,30 +289,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_kernel(GArgs g, float* __rest
     gl.kb1 = (int)((long)(split + 1) * g.nb / g.splits);
     const int nchunks = (gl.kb1 - gl.kb0 + KB - 1) / KB;
 
-    double acc[16];
+    double tot[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0;
+    for (int r = 0; r < 16; ++r) tot[r] = 0.0;
+    v16f acc = {};
 
     issue_stage<DT, KB>(s0, gl, 0, wave, lane, n0, m0);
     if (nchunks > 1) issue_stage<DT, KB>(s1, gl, 1, wave, lane, n0, m0);
     for (int ch = 0; ch < nchunks; ch += 3) {
-        pipeline_step<DT, KB>(s0, s2, gl, ch, nchunks, acc, wave, lane, n0, m0, wn, wm, h);
-        pipeline_step<DT, KB>(s1, s0, gl, ch + 1, nchunks, acc, wave, lane, n0, m0, wn, wm, h);
-        pipeline_step<DT, KB>(s2, s1, gl, ch + 2, nchunks, acc, wave, lane, n0, m0, wn, wm, h);
+        pipeline_step<DT, KB>(s0, s2, gl, ch, nchunks, acc, tot, wave, lane, n0, m0, wn, wm, h);
+        pipeline_step<DT, KB>(s1, s0, gl, ch + 1, nchunks, acc, tot, wave, lane, n0, m0, wn, wm, h);
+        pipeline_step<DT, KB>(s2, s1, gl, ch + 2, nchunks, acc, tot, wave, lane, n0, m0, wn, wm, h);
     }
 
     if (g.splits > 1) {
         // Partial tile to the workspace, register-major: 512-byte runs per store.
         double* p = g.ws + (((size_t)split * g.tiles + rt * g.mtiles + mt) * NW + wave) * 1024 + lane;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r * 64] = acc[r];
+        for (int r = 0; r < 16; ++r) p[r * 64] = tot[r];
         return;
     }
     static_assert(NW == 16 && sizeof(GStage<DT, KB>) >= 8 * 32 * 32 * sizeof(float),
                   "output staging: eight 4 KB wave tiles per stage, two stages");
     __syncthreads();  // every wave is done with the ring (no loads remain in flight)
     float* wout = (wave < 8 ? (float*)&s0 : (float*)&s1) + (wave % 8) * 32 * 32;
-    store_tile(wout, acc, n0 + wn * 32, m0 + wm * 32, h, c, g.rows, g.n_tok, y, y_stride);
+    store_tile(wout, tot, n0 + wn * 32, m0 + wm * 32, h, c, g.rows, g.n_tok, y, y_stride);
 }
 
 // y = the sum of the split-K partial tiles, in split order (f64), rounded

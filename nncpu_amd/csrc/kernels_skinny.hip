@@ -33,7 +33,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int SK_W = 16;          // waves per workgroup (8 where registers are short): all issue loads
 constexpr int SK_CW = 8;          // of which the first SK_CW compute (2 blocks of a stage each)
@@ -153,10 +152,6 @@ __device__ __forceinline__ void k_issue(KStage<DT, NW, TOK>& st, const KArgs& g,
     }
 }
 
-// s_waitcnt immediate with vmcnt = n (bits 3:0 and 15:14); expcnt and
-// lgkmcnt at their maxima, so they do not wait.
-#define NNH_SK_VMCNT(n) ((((n)&0xF) | (0x7 << 4) | (0xF << 8) | ((((n) >> 4) & 0x3) << 14)))
-
 // This wave's blocks 4w..4w+3 of the stage (those below nblk), in pairs for
 // the two-block scale outer products.
 template <int DT, int NR, int NW>
@@ -211,11 +206,11 @@ __device__ __forceinline__ void k_step(KStage<DT, NW, 2 * NR>& cur, KStage<DT, N
     // This wave's loads of chunk c are done once only later chunks' are
     // outstanding: chunks 1 and 2 at step 0, chunk c + 1 after that.
     if (c == 0 && nchunks > 2)
-        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT((2 * KPlan<DT, NW, 2 * NR>::PER_WAVE)));
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT((2 * KPlan<DT, NW, 2 * NR>::PER_WAVE)));
     else if (c + 1 < nchunks)
-        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT((KPlan<DT, NW, 2 * NR>::PER_WAVE)));
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT((KPlan<DT, NW, 2 * NR>::PER_WAVE)));
     else
-        __builtin_amdgcn_s_waitcnt(NNH_SK_VMCNT(0));
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
     __builtin_amdgcn_s_barrier();  // every wave's loads landed; every wave done with chunk c - 1
     if (c >= 1 && c + 2 < nchunks) k_issue<DT, NW, 2 * NR>(nxt, g, kb0 + (c + 2) * SK_KC, kb1, wave, lane, n0);
     const int left = kb1 - kb0 - c * SK_KC;
