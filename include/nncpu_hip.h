@@ -11,7 +11,7 @@
  * and greedy decoding reads the lm_head through model_argmax
  * (model/forward.rs:989-1011). This header replaces those three for the
  * Q8_0 and Q4 ("Q4S") split layouts (crates/nncpu/src/runtime.rs:52-63,
- * 136-164). Weights are uploaded once after load (model/load.rs:1266-1287)
+ * 136-164) and for BF16 weights (DType::BF16, Tensor::bf16()). Weights are uploaded once after load (model/load.rs:1266-1287)
  * and freed when the model drops (model/mod.rs:342-348).
  *
  * Plain C types only. Every function returns NNH_OK or an NNH_E_* code;
@@ -41,10 +41,14 @@ enum {
     NNH_E_STATE = 4
 };
 
-/* Weight formats: nncpu's DType::Q8_0 and DType::Q4S (runtime.rs:52-63). */
+/* Weight formats: nncpu's DType::Q8_0, DType::Q4S and DType::BF16
+ * (runtime.rs:52-63). BF16 weights take f32 activations only; the loader
+ * keeps any matrix whose rows are not whole 32-element blocks in BF16
+ * (model/load.rs:302-303), so a BF16 matrix may have any width. */
 enum {
     NNH_Q8_0 = 1,
-    NNH_Q4S = 2
+    NNH_Q4S = 2,
+    NNH_BF16 = 3
 };
 
 /* Activation modes of a matmul call.
@@ -78,20 +82,27 @@ const char* nnh_last_error(void);
  *   nnh_upload_q4:   qs[rows*cols/2] (byte i of a block: element i low
  *                    nibble, element i+16 high), scales and biases
  *                    [rows*cols/32] (BF16 bits).
- *   nnh_upload:      one buffer as Tensor.data points at it. */
+ *   nnh_upload:      one buffer as Tensor.data points at it (BF16: the
+ *                    rows*cols values).
+ * nnh_upload_bf16 (no 32-column condition): w[rows*cols] BF16 bits, row-major,
+ * as Tensor::bf16() views them. Its matmuls are bit-identical to nncpu's
+ * gemv_bf16 / gemv_bf16_batch (kernels/mod.rs:337-360, 454-485): the 4-row
+ * kernel when rows % 4 == 0 (scalar.rs:555-571), the 1-row kernel otherwise
+ * (scalar.rs:573-591), the f64 fallback when cols % 8 != 0 (mod.rs:556-564). */
 int nnh_upload_q8_0(const int8_t* qs, const uint16_t* scales, size_t rows, size_t cols, nnh_weight** out);
 int nnh_upload_q4(const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, size_t rows, size_t cols,
                   nnh_weight** out);
 int nnh_upload(int dtype, const void* data, size_t rows, size_t cols, nnh_weight** out);
+int nnh_upload_bf16(const uint16_t* w, size_t rows, size_t cols, nnh_weight** out);
 
 /* Encode f32 weights (device memory, rows x cols row-major) with nncpu's
  * load-time re-encoder (kernels/quant.rs:31-95, as model/load.rs:182-206
- * calls it), bit for bit, straight into a device weight. Waits for
- * `stream` first; synchronous. */
+ * calls it; BF16: f32_to_bf16 per value, load.rs:198-202), bit for bit,
+ * straight into a device weight. Waits for `stream` first; synchronous. */
 int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weight** out, void* stream);
 
 /* Copy a weight back to the host in nncpu's split layout (`bytes` >= the
- * layout's size: Q8_0 n + n/16, Q4 n/2 + n/8 for n = rows*cols). */
+ * layout's size: Q8_0 n + n/16, Q4 n/2 + n/8, BF16 2n for n = rows*cols). */
 int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes);
 
 /* Release a weight (NULL is a no-op). */
@@ -139,7 +150,10 @@ int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* 
 
 /* model_argmax (model/forward.rs:989-1011) for a Q8_0/Q4 lm_head: the row of
  * the first largest logit of W x (ties to the lower row; NaN never wins, and
- * a NaN in row 0 keeps row 0). Host x; synchronous. */
+ * a NaN in row 0 keeps row 0). For a BF16 lm_head with rows % 4 == 0 and
+ * cols % 8 == 0, gemv_bf16_argmax's running best (kernels/mod.rs:362-406):
+ * ties to the lower row, NaN and -inf never taken, row 0 when none is.
+ * Host x; synchronous. */
 int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int act);
 
 /* Device-resident form of nnh_gemv_batch: x and y are device pointers, the

@@ -15,16 +15,17 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (NNH_ACT_F32, NNH_ACT_I8, NNH_Q4S, NNH_Q8_0, DeviceOutOfMemory, InvalidArgument, NnhError,
-                   build, check, declared_functions, lib)
+from ._lib import (NNH_ACT_F32, NNH_ACT_I8, NNH_BF16, NNH_Q4S, NNH_Q8_0, DeviceOutOfMemory, InvalidArgument,
+                   NnhError, build, check, declared_functions, lib)
 
 Q8_0 = NNH_Q8_0
 Q4S = NNH_Q4S
+BF16 = NNH_BF16
 ACT_F32 = NNH_ACT_F32
 ACT_I8 = NNH_ACT_I8
 
 __all__ = [
-    "Q8_0", "Q4S", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
+    "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
     "gemv_batch_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
@@ -39,8 +40,9 @@ def init(device: int = 0) -> None:
 
 
 class Weight:
-    """One uploaded Q8_0 / Q4 matrix: the device side of a reference ``Tensor``
-    (runtime.rs:69-75) whose ``dtype`` is ``DType::Q8_0`` or ``DType::Q4S``."""
+    """One uploaded matrix: the device side of a reference ``Tensor``
+    (runtime.rs:69-75) whose ``dtype`` is ``DType::Q8_0``, ``DType::Q4S`` or
+    ``DType::BF16``."""
 
     def __init__(self, handle: C.c_void_p, dtype: int, rows: int, cols: int):
         self._h = handle
@@ -51,8 +53,8 @@ class Weight:
         """Upload from one buffer in the split layout Tensor.data points at."""
         data = np.ascontiguousarray(data).view(np.uint8)
         n = rows * cols
-        need = (n + n // 16) if dtype == Q8_0 else (n // 2 + n // 8)
-        if cols % 32 == 0 and data.size < need:
+        need = 2 * n if dtype == BF16 else (n + n // 16) if dtype == Q8_0 else (n // 2 + n // 8)
+        if (dtype == BF16 or cols % 32 == 0) and data.size < need:
             raise InvalidArgument(1, "split buffer too short")
         h = C.c_void_p()
         check(lib().nnh_upload(dtype, _ptr(data), rows, cols, C.byref(h)))
@@ -81,15 +83,28 @@ class Weight:
         return cls(h, Q4S, rows, cols)
 
     @classmethod
+    def bf16(cls, w: np.ndarray, rows: int, cols: int) -> "Weight":
+        """Upload BF16 weights (rows x cols values as Tensor::bf16() views them; any width)."""
+        w = np.ascontiguousarray(w).view(np.uint16)
+        if w.size < rows * cols:
+            raise InvalidArgument(1, "bf16 weights too short")
+        h = C.c_void_p()
+        check(lib().nnh_upload_bf16(_ptr(w), rows, cols, C.byref(h)))
+        return cls(h, BF16, rows, cols)
+
+    @classmethod
     def encode_dev(cls, dtype: int, w_ptr: int, rows: int, cols: int, stream: int = 0) -> "Weight":
         """Encode f32 weights already in device memory with nncpu's re-encoder
-        (kernels/quant.rs:31-95) on the device."""
+        (kernels/quant.rs:31-95; BF16: f32_to_bf16 per value, load.rs:198-202) on
+        the device."""
         h = C.c_void_p()
         check(lib().nnh_encode_dev(dtype, w_ptr, rows, cols, C.byref(h), stream or None))
         return cls(h, dtype, rows, cols)
 
     def split_bytes(self) -> int:
         n = self._rows * self._cols
+        if self.dtype == BF16:
+            return 2 * n
         return n + n // 16 if self.dtype == Q8_0 else n // 2 + n // 8
 
     def download(self) -> np.ndarray:

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libnncpu_hip.so")
 HEADER = os.path.join(ROOT, "include", "nncpu_hip.h")
 
 NNH_OK, NNH_E_INVALID, NNH_E_OOM, NNH_E_DEVICE, NNH_E_STATE = 0, 1, 2, 3, 4
-NNH_Q8_0, NNH_Q4S = 1, 2
+NNH_Q8_0, NNH_Q4S, NNH_BF16 = 1, 2, 3
 NNH_ACT_F32, NNH_ACT_I8 = 0, 1
 
 
@@ -65,6 +65,7 @@ def _declare(L):
     L.nnh_last_error.argtypes, L.nnh_last_error.restype = [], C.c_char_p
     L.nnh_upload_q8_0.argtypes, L.nnh_upload_q8_0.restype = [vp, vp, sz, sz, P(vp)], i32
     L.nnh_upload_q4.argtypes, L.nnh_upload_q4.restype = [vp, vp, vp, sz, sz, P(vp)], i32
+    L.nnh_upload_bf16.argtypes, L.nnh_upload_bf16.restype = [vp, sz, sz, P(vp)], i32
     L.nnh_upload.argtypes, L.nnh_upload.restype = [i32, vp, sz, sz, P(vp)], i32
     L.nnh_free.argtypes, L.nnh_free.restype = [vp], None
     L.nnh_encode_dev.argtypes, L.nnh_encode_dev.restype = [i32, vp, sz, sz, P(vp), vp], i32

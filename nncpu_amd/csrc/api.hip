@@ -27,6 +27,8 @@ struct nnh_weight {
     bool f32v2;           // fq in the 8-lane layout (tall matrices)
     uint16_t* fs;         // device: scales padded to nbp per row
     float* swT;           // device: [nb][rows padded] f32 scales, Q4 biases after (MFMA GEMM)
+    int bpath;            // BF16 only: the reference kernel this shape takes (nnh::BF16_PATH_*)
+    uint16_t* bl;         // device: BF16 only, the chain layout (none on the f64 path)
 };
 
 namespace {
@@ -170,7 +172,10 @@ void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, 
 int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t n_tok, int act,
              uint8_t* scratch, hipStream_t st) {
     const int rows = (int)w->rows, nb = (int)w->nb;
-    if (act == NNH_ACT_F32) {
+    if (w->dtype == NNH_BF16) {
+        nnh::launch_gemv_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, rows, (int)w->cols, x, x_stride, (int)n_tok, y,
+                              y_stride, st);
+    } else if (act == NNH_ACT_F32) {
         float* xsum = w->dtype == NNH_Q4S ? (float*)scratch : nullptr;
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
                              y, y_stride, w->f32v2, st);
@@ -186,6 +191,7 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
 }
 
 size_t gemv_scratch_bytes(const nnh_weight* w, size_t n_tok, int act) {
+    if (w->dtype == NNH_BF16) return 0;
     if (act == NNH_ACT_F32) return w->dtype == NNH_Q4S ? align_up(n_tok * w->nb * 4) : 0;
     return act_layout(w->cols, n_tok).bytes + i8_workspace_bytes(w, n_tok);
 }
@@ -194,6 +200,8 @@ int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_t
     int rc = check_weight(w);
     if (rc) return rc;
     if (act != NNH_ACT_F32 && act != NNH_ACT_I8) return fail(NNH_E_INVALID, "unknown activation mode");
+    if (w->dtype == NNH_BF16 && act != NNH_ACT_F32)
+        return fail(NNH_E_INVALID, "BF16 weights take f32 activations (the int8 path is for Q8_0 / Q4)");
     if (n_tok > 1 && y_stride < w->rows) return fail(NNH_E_INVALID, "gemv batch: y_stride < rows");
     if (n_tok > (size_t)1 << 20) return fail(NNH_E_INVALID, "gemv batch: too many vectors");
     (void)x_stride;
@@ -201,9 +209,9 @@ int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_t
 }
 
 int check_shape(int dtype, size_t rows, size_t cols) {
-    if (dtype != NNH_Q8_0 && dtype != NNH_Q4S) return fail(NNH_E_INVALID, "unknown dtype");
+    if (dtype != NNH_Q8_0 && dtype != NNH_Q4S && dtype != NNH_BF16) return fail(NNH_E_INVALID, "unknown dtype");
     if (rows == 0 || cols == 0) return fail(NNH_E_INVALID, "empty matrix");
-    if (cols % 32 != 0) return fail(NNH_E_INVALID, "cols is not a multiple of 32");
+    if (dtype != NNH_BF16 && cols % 32 != 0) return fail(NNH_E_INVALID, "cols is not a multiple of 32");
     if (rows >= ((size_t)1 << 31) || cols >= ((size_t)1 << 31) || rows > ((size_t)1 << 62) / cols)
         return fail(NNH_E_INVALID, "matrix too large");
     return NNH_OK;
@@ -211,6 +219,7 @@ int check_shape(int dtype, size_t rows, size_t cols) {
 
 size_t raw_bytes_of(int dtype, size_t rows, size_t cols) {
     const size_t n = rows * cols;
+    if (dtype == NNH_BF16) return 2 * n;
     return dtype == NNH_Q8_0 ? n + n / 16 : n / 2 + n / 8;
 }
 
@@ -220,6 +229,7 @@ void release(nnh_weight* w) {
     if (w->fs) (void)hipFree(w->fs);
     if (w->sb) (void)hipFree(w->sb);
     if (w->swT) (void)hipFree(w->swT);
+    if (w->bl) (void)hipFree(w->bl);
     delete w;
 }
 
@@ -232,6 +242,24 @@ constexpr size_t F32_V2_MIN_ROWS = NNH_F32_V2_MIN_ROWS;
 
 // Allocate a weight's device buffers; caller holds g_mu.
 int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
+    if (dtype == NNH_BF16) {
+        nnh_weight* w = new nnh_weight();
+        w->dtype = dtype;
+        w->device = g_device;
+        w->rows = rows;
+        w->cols = cols;
+        w->bpath = nnh::bf16_path(rows, cols);
+        const size_t lb = nnh::bf16_layout_bytes(w->bpath, rows, cols);
+        hipError_t e;
+        if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
+            (lb && (e = hipMalloc((void**)&w->bl, align_up(lb))) != hipSuccess)) {
+            release(w);
+            return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
+                        std::string("weight alloc: ") + hipGetErrorString(e));
+        }
+        *out = w;
+        return NNH_OK;
+    }
     const size_t n = rows * cols, nb = cols / 32;
     const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2;
     const size_t group = dtype == NNH_Q8_0 ? 8 : 16;
@@ -263,6 +291,13 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
 
 // Build the derived layouts from `raw` and wait; caller holds g_mu.
 int finalize_weight(nnh_weight* w) {
+    if (w->dtype == NNH_BF16) {
+        nnh::launch_relayout_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, (int)w->rows, (int)w->cols, g_stream);
+        hipError_t e;
+        if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
+            return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
+        return NNH_OK;
+    }
     nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, w->f32v2,
                              g_stream);
     if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
@@ -279,16 +314,17 @@ int upload_parts(int dtype, const void* qs, const void* sc, const void* bi, size
     *out = nullptr;
     int rc = check_shape(dtype, rows, cols);
     if (rc) return rc;
-    if (!qs || !sc || (dtype == NNH_Q4S && !bi)) return fail(NNH_E_INVALID, "nnh_upload: null data");
+    if (!qs || (dtype != NNH_BF16 && !sc) || (dtype == NNH_Q4S && !bi)) return fail(NNH_E_INVALID, "nnh_upload: null data");
     std::lock_guard<std::mutex> g(g_mu);
     if ((rc = ensure_locked())) return rc;
     nnh_weight* w;
     if ((rc = alloc_weight(dtype, rows, cols, &w))) return rc;
     const size_t n = rows * cols;
-    const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2, tbytes = (n / 32) * 2;
+    const size_t qbytes = dtype == NNH_BF16 ? 2 * n : dtype == NNH_Q8_0 ? n : n / 2, tbytes = (n / 32) * 2;
     hipError_t e;
     if ((e = hipMemcpyAsync(w->raw, qs, qbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
-        (e = hipMemcpyAsync(w->raw + qbytes, sc, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess ||
+        (dtype != NNH_BF16 &&
+         (e = hipMemcpyAsync(w->raw + qbytes, sc, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess) ||
         (dtype == NNH_Q4S &&
          (e = hipMemcpyAsync(w->raw + qbytes + tbytes, bi, tbytes, hipMemcpyHostToDevice, g_stream)) != hipSuccess)) {
         release(w);
@@ -322,10 +358,15 @@ int nnh_upload_q4(const uint8_t* qs, const uint16_t* scales, const uint16_t* bia
     return upload_parts(NNH_Q4S, qs, scales, biases, rows, cols, out);
 }
 
+int nnh_upload_bf16(const uint16_t* w, size_t rows, size_t cols, nnh_weight** out) {
+    return upload_parts(NNH_BF16, w, nullptr, nullptr, rows, cols, out);
+}
+
 int nnh_upload(int dtype, const void* data, size_t rows, size_t cols, nnh_weight** out) {
     if (!data) return fail(NNH_E_INVALID, "nnh_upload: null data");
     const uint8_t* p = (const uint8_t*)data;
     size_t n = rows * cols;
+    if (dtype == NNH_BF16) return upload_parts(dtype, p, nullptr, nullptr, rows, cols, out);
     if (dtype == NNH_Q8_0) return upload_parts(dtype, p, p + n, nullptr, rows, cols, out);
     if (dtype == NNH_Q4S) return upload_parts(dtype, p, p + n / 2, p + n / 2 + n / 16, rows, cols, out);
     return fail(NNH_E_INVALID, "nnh_upload: unknown dtype");
@@ -350,7 +391,10 @@ int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weig
     NNH_HIP(hipStreamSynchronize((hipStream_t)stream));  // w may come from work queued on `stream`
     nnh_weight* d;
     if ((rc = alloc_weight(dtype, rows, cols, &d))) return rc;
-    nnh::launch_encode(dtype, w, rows * cols, d->raw, (uint16_t*)d->sc, (uint16_t*)d->bi, g_stream);
+    if (dtype == NNH_BF16)
+        nnh::launch_encode_bf16(w, rows * cols, (uint16_t*)d->raw, g_stream);
+    else
+        nnh::launch_encode(dtype, w, rows * cols, d->raw, (uint16_t*)d->sc, (uint16_t*)d->bi, g_stream);
     if ((rc = finalize_weight(d))) {
         release(d);
         return rc;
@@ -390,6 +434,7 @@ int nnh_weight_f32_layout(const nnh_weight* w, nnh_f32_layout* out) {
     int rc = check_weight(w);
     if (rc) return rc;
     if (!out) return fail(NNH_E_INVALID, "f32 layout: null output");
+    if (w->dtype == NNH_BF16) return fail(NNH_E_INVALID, "f32 layout: BF16 weight (no quant layout)");
     if (w->f32v2) return fail(NNH_E_INVALID, "f32 layout: tall weight (8-lane layout)");
     *out = nnh_f32_layout{w->fq, w->fs, w->bi, w->rows, w->cols, w->nb, w->nbp, w->dtype};
     return NNH_OK;
@@ -459,7 +504,10 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
     std::memcpy(h, x, w->cols * 4);
     NNH_HIP(hipMemcpyAsync(dx, h, w->cols * 4, hipMemcpyHostToDevice, g_stream));
     if ((rc = run_gemv(w, dx, w->cols, dy, w->rows, 1, act, s + off_s, g_stream))) return rc;
-    nnh::launch_argmax(dy, w->rows, (uint64_t*)(s + off_p), dout, g_stream);
+    // BF16 with the 4-row kernel streams a running best from -inf
+    // (kernels/mod.rs:384-406), the rest take the first-max argmax.
+    nnh::launch_argmax(dy, w->rows, (uint64_t*)(s + off_p), dout, g_stream,
+                       w->dtype == NNH_BF16 && w->bpath == nnh::BF16_PATH_QUAD ? 1 : 0);
     NNH_HIP(hipGetLastError());
     uint64_t* hidx = (uint64_t*)(h + off_y);
     NNH_HIP(hipMemcpyAsync(hidx, dout, 8, hipMemcpyDeviceToHost, g_stream));
@@ -531,6 +579,7 @@ int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32
     int rc = ensure_locked();
     if (rc) return rc;
     if ((rc = check_weight(w))) return rc;
+    if (w->dtype == NNH_BF16) return fail(NNH_E_INVALID, "block_dots: BF16 weight (no int8 blocks)");
     if (n_tok == 0) return NNH_OK;
     if (!act || !P) return fail(NNH_E_INVALID, "block_dots: null pointer");
     nnh::launch_block_dots(w->dtype, w->qs, (const int8_t*)act, (int)w->rows, (int)w->nb, (int)n_tok, P,

@@ -99,6 +99,14 @@ void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const 
                     hipStream_t st);
 // f32 -> Q8_0 / Q4 split layout on the device (kernels_encode.hip).
 void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* sc, uint16_t* bi, hipStream_t st);
+// BF16 weights (kernels_bf16.hip): the reference's kernel by shape.
+enum { BF16_PATH_F64 = 0, BF16_PATH_QUAD = 1, BF16_PATH_ROW8 = 2, BF16_PATH_ROW32 = 3 };
+int bf16_path(size_t rows, size_t cols);
+size_t bf16_layout_bytes(int path, size_t rows, size_t cols);  // 0 for the f64 path
+void launch_relayout_bf16(int path, const uint16_t* raw, uint16_t* bl, int rows, int cols, hipStream_t st);
+void launch_gemv_bf16(int path, const uint16_t* raw, const uint16_t* bl, int rows, int cols, const float* x,
+                      size_t x_stride, int n_tok, float* y, size_t y_stride, hipStream_t st);
+void launch_encode_bf16(const float* w, size_t n, uint16_t* out, hipStream_t st);
 // int8 MFMA GEMM for many vectors (kernels_gemm.hip).
 int gemm_rows_pad(int rows);
 int gemm_tok_pad(int n_tok);
@@ -114,7 +122,10 @@ void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows,
                        hipStream_t st);
 
 // argmax over n logits (kernels_misc.hip); partial holds 2*ceil(n/2048) words.
-void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st);
+// mode 0: the first largest value, a NaN in row 0 keeping row 0
+// (forward.rs:1003-1011); mode 1: the BF16 4-row kernel's running best from
+// -inf (scalar.rs:612-628): NaN and -inf never taken, none taken gives 0.
+void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st, int mode = 0);
 size_t argmax_partial_words(size_t n);
 
 }  // namespace nnh

@@ -1,7 +1,9 @@
 // argmax over the lm_head logits with the reference's tie and NaN rules
 // (crates/nncpu/src/model/forward.rs:1003-1011): the first largest value
 // wins, a NaN never replaces the running best, and a NaN in row 0 keeps
-// row 0 (every `v[i] > NaN` is false).
+// row 0 (every `v[i] > NaN` is false). Mode 1 is the BF16 4-row kernel's
+// running best (kernels/scalar.rs:612-628): it starts from -inf with no row,
+// so NaN and -inf are never taken and nothing taken gives row 0.
 //
 // Each candidate is one u64 key: an order-preserving image of the value in
 // the high word (-0 folded onto +0, which compare equal), the complement of
@@ -50,15 +52,18 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     if (threadIdx.x == 0) partial[blockIdx.x] = k;
 }
 
+// The key of -inf's high word: the largest key no value is taken with in mode 1.
+constexpr uint32_t NEG_INF_KEY = ~0xff800000u;
+
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ v, const uint64_t* __restrict__ partial,
-                                                           int nparts, uint64_t* __restrict__ out) {
+                                                           int nparts, uint64_t* __restrict__ out, int mode) {
     uint64_t k = 0;
     for (int i = threadIdx.x; i < nparts; i += 256) k = umax64(k, partial[i]);
     k = block_max(k);
     if (threadIdx.x == 0) {
         float v0 = v[0];
-        uint64_t idx = (k == 0 || !(v0 == v0)) ? 0 : (uint64_t)(0xffffffffu - (uint32_t)k);
-        out[0] = idx;
+        const bool none = mode == 1 ? (uint32_t)(k >> 32) <= NEG_INF_KEY : (k == 0 || !(v0 == v0));
+        out[0] = none ? 0 : (uint64_t)(0xffffffffu - (uint32_t)k);
     }
 }
 
@@ -66,10 +71,10 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
 
 size_t argmax_partial_words(size_t n) { return (n + PER_BLOCK - 1) / PER_BLOCK; }
 
-void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st) {
+void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st, int mode) {
     int nparts = (int)argmax_partial_words(n);
     argmax_partial_kernel<<<nparts, 256, 0, st>>>(v, n, partial);
-    argmax_final_kernel<<<1, 256, 0, st>>>(v, partial, nparts, out);
+    argmax_final_kernel<<<1, 256, 0, st>>>(v, partial, nparts, out, mode);
 }
 
 }  // namespace nnh

@@ -304,6 +304,95 @@ size_t or_argmax(const float* v, size_t n) {
     return best;
 }
 
+// ---- BF16 weights (DType::BF16, WeightFormat::Bf16) ----
+
+namespace {
+
+// scalar.rs:555-571: four rows, one 8-lane accumulator each over k += 8 (the
+// x tile shared by the four rows), reduced ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7))
+// (the hadd tree, avx2.rs:1146-1178).
+void bf16_4rows(const uint16_t* w, size_t cols, const float* x, float* out) {
+    float acc[4][8] = {};
+    for (size_t k = 0; k < cols; k += 8)
+        for (int j = 0; j < 4; ++j)
+            for (int l = 0; l < 8; ++l)
+                acc[j][l] = std::fma(bf16_to_f32(w[j * cols + k + l]), x[k + l], acc[j][l]);
+    for (int j = 0; j < 4; ++j) {
+        const float* a = acc[j];
+        out[j] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+    }
+}
+
+// scalar.rs:573-591: one row; four accumulators over 32-element strides
+// when cols % 32 == 0 (add8(add8(a0, a1), add8(a2, a3)) then hsum8), else one
+// (hsum8). Reached only with cols % 8 == 0.
+float bf16_row(const uint16_t* w, const float* x, size_t cols) {
+    if (cols % 32 == 0) {
+        float acc[4][8] = {};
+        for (size_t k = 0; k < cols; k += 32)
+            for (int j = 0; j < 4; ++j)
+                for (int l = 0; l < 8; ++l)
+                    acc[j][l] = std::fma(bf16_to_f32(w[k + 8 * j + l]), x[k + 8 * j + l], acc[j][l]);
+        float v[8];
+        for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+        return hsum8(v);
+    }
+    float a[8] = {};
+    for (size_t k = 0; k + 8 <= cols; k += 8)
+        for (int l = 0; l < 8; ++l) a[l] = std::fma(bf16_to_f32(w[k + l]), x[k + l], a[l]);
+    return hsum8(a);
+}
+
+}  // namespace
+
+// kernels/mod.rs:337-360 (gemv_bf16) with gemv_bf16_f64 (mod.rs:556-564) for
+// cols % 8 != 0, the 4-row kernel when rows % 4 == 0, else the 1-row kernel.
+// The thread split (for_rows) never changes a row's arithmetic.
+void or_gemv_bf16(const uint16_t* w, const float* x, float* y, size_t rows, size_t cols) {
+    if (rows == 0 || cols == 0) return;
+    if (cols % 8 != 0) {
+        for (size_t r = 0; r < rows; ++r) {
+            double s = 0.0;
+            for (size_t k = 0; k < cols; ++k) s += (double)bf16_to_f32(w[r * cols + k]) * (double)x[k];
+            y[r] = (float)s;
+        }
+        return;
+    }
+    if (rows % 4 == 0) {
+        for (size_t r = 0; r < rows; r += 4) bf16_4rows(w + r * cols, cols, x, y + r);
+        return;
+    }
+    for (size_t r = 0; r < rows; ++r) y[r] = bf16_row(w + r * cols, x, cols);
+}
+
+// kernels/mod.rs:454-485 (gemv_bf16_batch): every vector gets the bits of the
+// single-vector gemv (the 4-row kernel per token when rows % 4 == 0 and
+// cols % 8 == 0, else the single gemv per token).
+void or_gemv_bf16_batch(const uint16_t* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t rows,
+                        size_t cols, size_t n_batch) {
+    for (size_t t = 0; t < n_batch; ++t) or_gemv_bf16(w, x + t * x_stride, y + t * y_stride, rows, cols);
+}
+
+// kernels/mod.rs:362-406 (gemv_bf16_argmax): with rows % 4 == 0 and
+// cols % 8 == 0 a running best from -inf over the 4-row kernel's outputs
+// (scalar.rs:612-628: `v > bv`, so NaN and -inf never win, ties go to the
+// lower row, nothing taken gives 0); otherwise the gemv and the first-max
+// argmax (forward.rs:1003-1011).
+size_t or_gemv_bf16_argmax(const uint16_t* w, const float* x, size_t rows, size_t cols) {
+    if (rows == 0 || cols == 0) return 0;
+    std::vector<float> y(rows);
+    or_gemv_bf16(w, x, y.data(), rows, cols);
+    if (rows % 4 != 0 || cols % 8 != 0) return or_argmax(y.data(), rows);
+    size_t best = 0;
+    float bv = -INFINITY;
+    for (size_t r = 0; r < rows; ++r)
+        if (y[r] > bv) {
+            bv = y[r];
+            best = r;
+        }
+    return best;
+}
+
 // ---- int8-activation path (new in this build; no reference counterpart) ----
 
 // Exact int32 block dots P[r*nb + b] = sum_k q_w[r, 32b+k] * q_x[32b+k] for

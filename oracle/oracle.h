@@ -30,6 +30,11 @@ int or_gemv_batch(int dtype, const void* w, size_t rows, size_t cols, const floa
                   size_t y_stride, size_t n_tok);
 size_t or_argmax(const float* v, size_t n);
 
+void or_gemv_bf16(const uint16_t* w, const float* x, float* y, size_t rows, size_t cols);
+void or_gemv_bf16_batch(const uint16_t* w, const float* x, size_t x_stride, float* y, size_t y_stride, size_t rows,
+                        size_t cols, size_t n_batch);
+size_t or_gemv_bf16_argmax(const uint16_t* w, const float* x, size_t rows, size_t cols);
+
 void or_block_dots(int dtype, const void* qs, size_t rows, size_t cols, const int8_t* qx, int32_t* P);
 void or_dequant_act(const int8_t* qx, const uint16_t* sx, size_t n, float* out);
 void or_gemv_i8_exact(int dtype, const void* w, size_t rows, size_t cols, const int8_t* qx, const uint16_t* sx,

@@ -56,6 +56,9 @@ def _declare(L):
     L.or_gemv_q4_batch.argtypes, L.or_gemv_q4_batch.restype = [vp, vp, vp, vp, sz, vp, sz, vp, sz, sz, sz, sz], i32
     L.or_gemv_batch.argtypes, L.or_gemv_batch.restype = [i32, vp, sz, sz, vp, sz, vp, sz, sz], i32
     L.or_argmax.argtypes, L.or_argmax.restype = [vp, sz], sz
+    L.or_gemv_bf16.argtypes = [vp, vp, vp, sz, sz]
+    L.or_gemv_bf16_batch.argtypes = [vp, vp, sz, vp, sz, sz, sz, sz]
+    L.or_gemv_bf16_argmax.argtypes, L.or_gemv_bf16_argmax.restype = [vp, vp, sz, sz], sz
     L.or_block_dots.argtypes = [i32, vp, sz, sz, vp, vp]
     L.or_dequant_act.argtypes = [vp, vp, sz, vp]
     L.or_gemv_i8_exact.argtypes = [i32, vp, sz, sz, vp, vp, vp]
@@ -218,6 +221,36 @@ def gemv_batch(m: QMatrix, x: np.ndarray, n_tok: int = 1, x_stride: int | None =
 def argmax(v: np.ndarray) -> int:
     v = np.ascontiguousarray(v, np.float32)
     return lib().or_argmax(_p(v), v.size)
+
+
+# ---- BF16 weights (kernels/mod.rs:337-406, 454-485; scalar.rs:555-628) -------------
+
+BF16 = 3
+
+
+def f32_array_to_bf16(a: np.ndarray) -> np.ndarray:
+    """runtime.rs:15-21 round to nearest even, vectorised (WeightFormat::Bf16's encoder, load.rs:198-202)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def gemv_bf16(w: np.ndarray, x: np.ndarray, rows: int, cols: int, n_tok: int = 1,
+              x_stride: int | None = None, y_stride: int | None = None) -> np.ndarray:
+    """gemv_bf16 / gemv_bf16_batch on the scalar restatement."""
+    w = np.ascontiguousarray(w, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    xs = cols if x_stride is None else x_stride
+    ys = rows if y_stride is None else y_stride
+    assert w.size >= rows * cols and x.size >= (n_tok - 1) * xs + cols
+    y = np.zeros((n_tok - 1) * ys + rows, np.float32)
+    lib().or_gemv_bf16_batch(_p(w), _p(x), xs, _p(y), ys, rows, cols, n_tok)
+    return y
+
+
+def gemv_bf16_argmax(w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> int:
+    w = np.ascontiguousarray(w, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    return lib().or_gemv_bf16_argmax(_p(w), _p(x), rows, cols)
 
 
 def quantize_act(x: np.ndarray):

@@ -318,3 +318,116 @@ def test_oracle_matches_golden(oracle, case):
         assert np.array_equal(qx, extra["qx"]) and np.array_equal(sx, extra["sx"])
         assert np.array_equal(bits(oracle.gemv_i8_exact(m, qx, sx)), bits(y))
         assert np.array_equal(oracle.block_dots(m, qx), extra["P"])
+
+
+# ---- BF16 weights (kernels/tests.rs:433-498; kernels/mod.rs:337-406) ---------------
+
+BF16_SHAPES = [(1, 8), (7, 5), (16, 1536), (1536, 1536), (2048, 1536), (6144, 1536), (6, 64), (5, 24), (260, 512)]
+
+
+def bf16s(oracle, rng, n, lo, hi):
+    """kernels/tests.rs:47-49: f32_to_bf16 of each uniform draw."""
+    return oracle.f32_array_to_bf16(rng.vec(n, lo, hi))
+
+
+def test_bf16_encoder_matches_scalar(oracle):
+    rng = oracle.Rng(0xBF16)
+    v = np.concatenate([rng.vec(4096, -1e4, 1e4),
+                        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -3.4e38], np.float32),
+                        np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF], np.uint32).view(np.float32)])
+    want = np.array([oracle.f32_to_bf16(float(x)) for x in v], np.uint16)
+    assert np.array_equal(oracle.f32_array_to_bf16(v), want)
+
+
+def test_bf16_gemv_matches_f64(oracle):
+    # kernels/tests.rs:433-459: U(-1,1) BF16 weights and x, f64 reference, 1e-3;
+    # the shapes take every path (f64 fallback, 4-row, 1-row with and without
+    # cols % 32).
+    rng = oracle.Rng(0xB16E)
+    for rows, cols in BF16_SHAPES:
+        w = bf16s(oracle, rng, rows * cols, -1.0, 1.0)
+        x = rng.vec(cols, -1.0, 1.0)
+        want = oracle.bf16_array_to_f32(w).astype(np.float64).reshape(rows, cols) @ x.astype(np.float64)
+        y = oracle.gemv_bf16(w, x, rows, cols)
+        assert close(y, want, 1e-3).all(), (rows, cols)
+
+
+# One product per step (x = 1, exact BF16 weights), chosen so the candidate
+# reduction orders give different f32 sums: the 4-row kernel's hadd tree
+# ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) (scalar.rs:555-571), the 1-row kernel's
+# hsum8 ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)) (scalar.rs:108-117, 573-591), and
+# with 32 columns the 4-row kernel's sequential chains (a_l over elements l,
+# 8+l, 16+l, 24+l) against the 1-row kernel's add8 of four accumulators.
+TREE8 = [0.00164794921875, -0.15625, -8704.0, -1.1953125, -0.83984375, 0.09375, -0.0015106201171875,
+         -0.002838134765625]
+TREE8_QUAD, TREE8_HSUM8 = -8706.099609375, -8706.1005859375
+TREE32 = [-0.00579833984375, 0.0869140625, -1.9453125, 2.75, -0.00183868408203125, 5824.0, 1.375,
+          -0.021240234375, -0.0166015625, 163.0, 1.2265625, 0.06640625, -1.5390625, -0.0225830078125,
+          0.00799560546875, 0.14453125, 15744.0, -0.004425048828125, -11.0, 8000.0, -2.234375, -0.3515625,
+          14.4375, 0.015869140625, -68.5, 0.00188446044921875, 13.5, -0.0024566650390625, -0.00144195556640625,
+          0.0390625, 242.0, 1.953125]
+TREE32_QUAD, TREE32_ROW = 29922.95703125, 29922.958984375
+
+
+def test_bf16_reduction_trees(oracle):
+    for vals, quad, row in ((TREE8, TREE8_QUAD, TREE8_HSUM8), (TREE32, TREE32_QUAD, TREE32_ROW)):
+        cols = len(vals)
+        wrow = oracle.f32_array_to_bf16(np.array(vals, np.float32))
+        assert np.array_equal(oracle.bf16_array_to_f32(wrow), np.array(vals, np.float32))  # exact BF16
+        x = np.ones(cols, np.float32)
+        y4 = oracle.gemv_bf16(np.tile(wrow, 4), x, 4, cols)   # rows % 4 == 0: the 4-row kernel
+        y5 = oracle.gemv_bf16(np.tile(wrow, 5), x, 5, cols)   # else the 1-row kernel
+        assert quad != row
+        assert np.all(y4 == np.float32(quad)), (cols, y4)
+        assert np.all(y5 == np.float32(row)), (cols, y5)
+
+
+def test_bf16_f64_fallback(oracle):
+    # cols % 8 != 0 (mod.rs:556-564): f64 products summed in order, one rounding.
+    rng = oracle.Rng(0xF64)
+    for rows, cols in ((3, 5), (8, 13), (4, 1001)):
+        w = bf16s(oracle, rng, rows * cols, -1.0, 1.0)
+        x = rng.vec(cols, -1.0, 1.0)
+        wf = oracle.bf16_array_to_f32(w).astype(np.float64).reshape(rows, cols)
+        want = np.empty(rows, np.float32)
+        for r in range(rows):
+            s = 0.0
+            for k in range(cols):
+                s += wf[r, k] * float(x[k])
+            want[r] = np.float32(s)
+        assert np.array_equal(bits(oracle.gemv_bf16(w, x, rows, cols)), bits(want))
+
+
+def test_bf16_argmax(oracle):
+    # kernels/tests.rs:461-498: against the gemv (first max), a tie to the
+    # lower row, and all-NaN gives 0.
+    rng = oracle.Rng(0xA12A)
+    for rows, cols in [(4, 32), (16, 256), (2048, 256), (256, 1536), (7, 5), (6, 64)]:
+        w = bf16s(oracle, rng, rows * cols, -1.0, 1.0)
+        x = rng.vec(cols, -1.0, 1.0)
+        y = oracle.gemv_bf16(w, x, rows, cols)
+        assert oracle.gemv_bf16_argmax(w, x, rows, cols) == oracle.argmax(y), (rows, cols)
+    rows, cols = 512, 256
+    w = np.zeros(rows * cols, np.uint16)
+    for r in (100, 300, 301):
+        w[r * cols] = oracle.f32_to_bf16(1.0)
+    x = np.zeros(cols, np.float32)
+    x[0] = 2.0
+    assert oracle.gemv_bf16_argmax(w, x, rows, cols) == 100
+    x[0] = np.nan
+    assert oracle.gemv_bf16_argmax(w, x, rows, cols) == 0
+    # The 4-row kernel's running best starts from -inf with no row (scalar.rs:
+    # 612-628): a NaN row 0 is passed over, where the first-max argmax of the
+    # materialised logits (rows % 4 != 0) keeps row 0.
+    cols = 8
+    for rows, want in ((8, 5), (7, 0)):
+        w = np.zeros(rows * cols, np.uint16)
+        w[0] = 0x7FC0  # NaN weight: row 0 is NaN
+        for r in range(1, rows):
+            w[r * cols] = oracle.f32_to_bf16(float(r if r != 5 else 50))
+        x = np.ones(cols, np.float32)
+        assert oracle.gemv_bf16_argmax(w, x, rows, cols) == want, rows
+    # -inf is never taken either: all rows -inf gives 0 as well.
+    w = np.full(8 * 8, 0, np.uint16)
+    w[::8] = 0xFF80  # -inf
+    assert oracle.gemv_bf16_argmax(w, np.ones(8, np.float32), 8, 8) == 0
