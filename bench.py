@@ -48,6 +48,8 @@ def log(*a):
 def weight_bytes(dtype: int, n: int, k: int) -> int:
     """model/mod.rs:391-398: what a gemv streams from the weight."""
     e = n * k
+    if dtype == 3:
+        return 2 * e
     return e + e // 16 if dtype == 1 else e // 2 + e // 8
 
 
@@ -183,6 +185,9 @@ def q4_sweep(args, N):
 QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
 VERIFY_SHAPES = [(6144, 1536), (1536, 6144), (2048, 1536), (1536, 1536)]
 GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912), (262144, 1152)]
+# BF16 weights: the reference's own BF16 test shapes (Gemma E2B/E4B, kernels/tests.rs:435-447) and
+# Llama-3-8B projections.
+BF16_SHAPES = [(1536, 1536), (2048, 1536), (6144, 1536), (4096, 4096), (14336, 4096)]
 
 
 def measure_cases(args, N, cases, act_mode, label):
@@ -218,7 +223,7 @@ def measure_cases(args, N, cases, act_mode, label):
         us = secs / steps * 1e6
         byts = gemv_bytes(dtype, n, k, m)
         ops = 2.0 * m * n * k
-        e = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} {n}x{k} M={m}", us=round(us, 3),
+        e = dict(case=f"{ {1: 'Q8', 2: 'Q4', 3: 'BF16'}[dtype]} {n}x{k} M={m}", us=round(us, 3),
                  gbs=round(byts / us / 1e3, 1), hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
                  tops=round(ops / us / 1e6, 2), int8_frac=round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), steps=steps)
         log(f"{label}: {e}")
@@ -431,7 +436,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "all"])
+                             "bf16", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -456,6 +461,9 @@ def main():
     if args.workload in ("decode_f32", "all"):
         extra["decode_f32_bit_exact"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
                                                       N.ACT_F32, "decode_f32")
+    if args.workload in ("bf16", "all"):
+        extra["bf16_bit_exact"] = measure_cases(args, N, [(3, n, k, m) for n, k in BF16_SHAPES for m in (1, 4)],
+                                                N.ACT_F32, "bf16")
     if args.workload in ("gemma_decode", "q4_sweep", "all"):
         extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
     if args.workload not in ("q4_sweep", "all"):

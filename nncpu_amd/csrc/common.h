@@ -70,6 +70,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
 #define NNH_LGKMCNT0 (0xF | (0x7 << 4) | (0x3 << 14))
 
+// Compute units of the current device (kernels_misc.hip).
+int cu_count();
+
 inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ---- launchers (defined beside their kernels) -------------------------------

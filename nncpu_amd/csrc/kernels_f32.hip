@@ -639,19 +639,6 @@ __global__ __launch_bounds__(M1S_NT) void gemv_f32_m1s_kernel(F32Mat m, const fl
     if (2 * wave + (lane >> 5) < nr && j == 0) y[row0 + 2 * wave + (lane >> 5)] = res;
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
 // 16-lane kernel, 8, 16 or 32 (Q4: up to 16) for the wide one.
 template <int DT>

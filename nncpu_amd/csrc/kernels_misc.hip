@@ -69,6 +69,19 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
 
 }  // namespace
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 size_t argmax_partial_words(size_t n) { return (n + PER_BLOCK - 1) / PER_BLOCK; }
 
 void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st, int mode) {
