@@ -101,6 +101,21 @@ int nnh_upload_bf16(const uint16_t* w, size_t rows, size_t cols, nnh_weight** ou
  * straight into a device weight. Waits for `stream` first; synchronous. */
 int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weight** out, void* stream);
 
+/* Load-time GGUF decoding on the device (kernels/quant.rs:97-156,
+ * dequantize_to_f32), bit for bit: ggml types F32 (0), F16 (1), BF16 (30),
+ * Q4_0 (2), Q4_1 (3), Q5_0 (6), Q5_1 (7), Q8_0 (8), Q4_K (12), Q5_K (13),
+ * Q6_K (14). NNH_E_INVALID, dst untouched, for other types, when n is not a
+ * whole number of blocks or `nbytes` holds fewer blocks than n needs.
+ *   nnh_dequantize_dev: device blocks -> device dst[0..n), asynchronous on
+ *                       `stream`.
+ *   nnh_upload_gguf:    host blocks of one rows x cols matrix -> decoded on
+ *                       the device -> re-encoded to `dtype` (NNH_Q8_0,
+ *                       NNH_Q4S, NNH_BF16) as model/load.rs:182-206 does on
+ *                       the CPU -> a new weight. Synchronous. */
+int nnh_dequantize_dev(uint32_t ggml_type, const void* blocks, size_t nbytes, float* dst, size_t n, void* stream);
+int nnh_upload_gguf(uint32_t ggml_type, const void* blocks, size_t nbytes, size_t rows, size_t cols, int dtype,
+                    nnh_weight** out);
+
 /* Copy a weight back to the host in nncpu's split layout (`bytes` >= the
  * layout's size: Q8_0 n + n/16, Q4 n/2 + n/8, BF16 2n for n = rows*cols). */
 int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes);

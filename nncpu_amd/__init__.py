@@ -26,7 +26,7 @@ ACT_I8 = NNH_ACT_I8
 
 __all__ = [
     "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
-    "gemv_batch_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
+    "gemv_batch_dev", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
 
@@ -91,6 +91,15 @@ class Weight:
         h = C.c_void_p()
         check(lib().nnh_upload_bf16(_ptr(w), rows, cols, C.byref(h)))
         return cls(h, BF16, rows, cols)
+
+    @classmethod
+    def from_gguf(cls, ggml_type: int, blocks: np.ndarray, rows: int, cols: int, dtype: int) -> "Weight":
+        """Decode one matrix's GGUF blocks on the device (kernels/quant.rs:107-156) and
+        re-encode it to ``dtype`` (model/load.rs:182-206)."""
+        blocks = np.ascontiguousarray(blocks).view(np.uint8)
+        h = C.c_void_p()
+        check(lib().nnh_upload_gguf(ggml_type, _ptr(blocks), blocks.size, rows, cols, dtype, C.byref(h)))
+        return cls(h, dtype, rows, cols)
 
     @classmethod
     def encode_dev(cls, dtype: int, w_ptr: int, rows: int, cols: int, stream: int = 0) -> "Weight":
@@ -201,6 +210,11 @@ def gemv_i8_dev(w: Weight, act_ptr: int, n_tok: int, y_ptr: int, y_stride: int, 
 
 def block_dots_dev(w: Weight, act_ptr: int, n_tok: int, P_ptr: int, stream: int = 0) -> None:
     check(lib().nnh_block_dots_dev(w.handle, act_ptr, n_tok, P_ptr, stream or None))
+
+
+def dequantize_dev(ggml_type: int, blocks_ptr: int, nbytes: int, dst_ptr: int, n: int, stream: int = 0) -> None:
+    """kernels/quant.rs:107-156 on the device: n values of GGUF blocks into f32 dst."""
+    check(lib().nnh_dequantize_dev(ggml_type, blocks_ptr, nbytes, dst_ptr, n, stream or None))
 
 
 def sync(stream: int = 0) -> None:

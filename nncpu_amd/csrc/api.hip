@@ -403,6 +403,70 @@ int nnh_encode_dev(int dtype, const float* w, size_t rows, size_t cols, nnh_weig
     return NNH_OK;
 }
 
+// dequantize_to_f32's conditions (kernels/quant.rs:112-124).
+int check_blocks(uint32_t type, size_t nbytes, size_t n) {
+    size_t bytes, per;
+    if (!nnh::ggml_block(type, &bytes, &per)) return fail(NNH_E_INVALID, "dequantize: type not decodable");
+    if (n % per != 0) return fail(NNH_E_INVALID, "dequantize: not a whole number of blocks");
+    if (nbytes / bytes < n / per) return fail(NNH_E_INVALID, "dequantize: fewer blocks than values");
+    return NNH_OK;
+}
+
+int nnh_dequantize_dev(uint32_t ggml_type, const void* blocks, size_t nbytes, float* dst, size_t n, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_blocks(ggml_type, nbytes, n))) return rc;
+    if (n == 0) return NNH_OK;
+    if (!blocks || !dst) return fail(NNH_E_INVALID, "dequantize: null pointer");
+    nnh::launch_dequantize(ggml_type, (const uint8_t*)blocks, n, dst, (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_upload_gguf(uint32_t ggml_type, const void* blocks, size_t nbytes, size_t rows, size_t cols, int dtype,
+                    nnh_weight** out) {
+    if (!out) return fail(NNH_E_INVALID, "nnh_upload_gguf: null out");
+    *out = nullptr;
+    int rc = check_shape(dtype, rows, cols);
+    if (rc) return rc;
+    if ((rc = check_blocks(ggml_type, nbytes, rows * cols))) return rc;
+    if (!blocks) return fail(NNH_E_INVALID, "nnh_upload_gguf: null blocks");
+    size_t bytes, per;
+    nnh::ggml_block(ggml_type, &bytes, &per);
+    const size_t n = rows * cols, used = n / per * bytes;
+    uint8_t* dblk = nullptr;
+    float* df = nullptr;
+    {
+        std::lock_guard<std::mutex> g(g_mu);
+        if ((rc = ensure_locked())) return rc;
+        hipError_t e;
+        if ((e = hipMalloc((void**)&dblk, align_up(used))) != hipSuccess ||
+            (e = hipMalloc((void**)&df, align_up(n * 4))) != hipSuccess) {
+            if (dblk) (void)hipFree(dblk);
+            return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
+                        std::string("nnh_upload_gguf: alloc: ") + hipGetErrorString(e));
+        }
+        if ((e = hipMemcpyAsync(dblk, blocks, used, hipMemcpyHostToDevice, g_stream)) != hipSuccess) {
+            (void)hipFree(dblk);
+            (void)hipFree(df);
+            return fail(NNH_E_DEVICE, std::string("nnh_upload_gguf: copy: ") + hipGetErrorString(e));
+        }
+        nnh::launch_dequantize(ggml_type, dblk, n, df, g_stream);
+        if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess) {
+            (void)hipFree(dblk);
+            (void)hipFree(df);
+            return fail(NNH_E_DEVICE, std::string("nnh_upload_gguf: decode: ") + hipGetErrorString(e));
+        }
+        (void)hipFree(dblk);
+    }
+    // Re-encode (load.rs:182-206) as nnh_encode_dev does; g_stream is idle.
+    rc = nnh_encode_dev(dtype, df, rows, cols, out, nullptr);
+    std::lock_guard<std::mutex> g(g_mu);
+    (void)hipFree(df);
+    return rc;
+}
+
 int nnh_weight_download(const nnh_weight* w, void* data, size_t bytes) {
     if (!w || !data) return fail(NNH_E_INVALID, "nnh_weight_download: null pointer");
     const size_t need = raw_bytes_of(w->dtype, w->rows, w->cols);

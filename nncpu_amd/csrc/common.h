@@ -110,6 +110,10 @@ void launch_relayout_bf16(int path, const uint16_t* raw, uint16_t* bl, int rows,
 void launch_gemv_bf16(int path, const uint16_t* raw, const uint16_t* bl, int rows, int cols, const float* x,
                       size_t x_stride, int n_tok, float* y, size_t y_stride, hipStream_t st);
 void launch_encode_bf16(const float* w, size_t n, uint16_t* out, hipStream_t st);
+// GGUF tensor blocks -> f32 (kernels_gguf.hip): bytes and values per block
+// of a decodable ggml type; the decode itself (n a whole number of blocks).
+bool ggml_block(uint32_t type, size_t* bytes, size_t* per);
+void launch_dequantize(uint32_t type, const uint8_t* src, size_t n, float* dst, hipStream_t st);
 // int8 MFMA GEMM for many vectors (kernels_gemm.hip).
 int gemm_rows_pad(int rows);
 int gemm_tok_pad(int n_tok);

@@ -393,6 +393,183 @@ size_t or_gemv_bf16_argmax(const uint16_t* w, const float* x, size_t rows, size_
     return best;
 }
 
+// ---- GGUF block decoding (kernels/quant.rs:97-291), the load-time step ----
+
+namespace {
+
+// runtime.rs:25-48: IEEE half -> f32 by bits (subnormals renormalised, NaN
+// payloads kept).
+float f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1f, mant = h & 0x3ff, bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = 127 - 15 + 1;
+            uint32_t m = mant;
+            while (!(m & 0x400)) {
+                m <<= 1;
+                e -= 1;
+            }
+            bits = sign | ((uint32_t)e << 23) | ((m & 0x3ff) << 13);
+        }
+    } else if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+float f16_at(const uint8_t* b, size_t i) { return f16_to_f32((uint16_t)(b[i] | (b[i + 1] << 8))); }
+
+// quant.rs:163-195: Q4_0 / Q4_1 / Q5_0 / Q5_1 (optional fp16 min, optional
+// fifth bit per value; centred on 8, or 16 with the fifth bit, when no min).
+void dequant_legacy(const uint8_t* src, size_t nblocks, bool has_min, bool has_high, float* dst) {
+    const size_t bytes = 2 + (has_min ? 2 : 0) + (has_high ? 4 : 0) + 16;
+    const int centre = has_min ? 0 : has_high ? 16 : 8;
+    for (size_t bi = 0; bi < nblocks; ++bi) {
+        const uint8_t* p = src + bi * bytes;
+        float* y = dst + 32 * bi;
+        const float d = f16_at(p, 0), m = has_min ? f16_at(p, 2) : 0.0f;
+        const size_t o = has_min ? 4 : 2;
+        const uint32_t qh = has_high ? (uint32_t)p[o] | (uint32_t)p[o + 1] << 8 | (uint32_t)p[o + 2] << 16 |
+                                           (uint32_t)p[o + 3] << 24
+                                     : 0u;
+        const uint8_t* qs = p + bytes - 16;
+        for (int j = 0; j < 16; ++j) {
+            const int hi0 = (int)(((qh >> j) << 4) & 0x10), hi1 = (int)((qh >> (j + 12)) & 0x10);
+            y[j] = (float)(((int)(qs[j] & 0x0f) | hi0) - centre) * d + m;
+            y[j + 16] = (float)(((int)(qs[j] >> 4) | hi1) - centre) * d + m;
+        }
+    }
+}
+
+// quant.rs:197-211 (ggml's packing of 6-bit scales and mins).
+void scale_min_k4(int j, const uint8_t* q, float* d, float* m) {
+    uint8_t dd, mm;
+    if (j < 4) {
+        dd = q[j] & 63;
+        mm = q[j + 4] & 63;
+    } else {
+        dd = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        mm = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+    *d = (float)dd;
+    *m = (float)mm;
+}
+
+// quant.rs:213-236 (Q4_K) and :238-266 (Q5_K, qh with each value's fifth bit).
+void dequant_qk(const uint8_t* src, size_t nblocks, bool q5, float* dst) {
+    const size_t bytes = q5 ? 176 : 144;
+    for (size_t bi = 0; bi < nblocks; ++bi) {
+        const uint8_t* b = src + bi * bytes;
+        float* y = dst + 256 * bi;
+        const float d = f16_at(b, 0), dmin = f16_at(b, 2);
+        const uint8_t* scales = b + 4;
+        const uint8_t* qh = b + 16;
+        const uint8_t* qs = b + (q5 ? 48 : 16);
+        uint8_t u1 = 1, u2 = 2;
+        for (int j = 0; j < 4; ++j) {
+            float sc, mn;
+            scale_min_k4(2 * j, scales, &sc, &mn);
+            const float d1 = d * sc, m1 = dmin * mn;
+            scale_min_k4(2 * j + 1, scales, &sc, &mn);
+            const float d2 = d * sc, m2 = dmin * mn;
+            const uint8_t* q = qs + 32 * j;
+            for (int l = 0; l < 32; ++l) {
+                const int h1 = q5 && (qh[l] & u1) ? 16 : 0, h2 = q5 && (qh[l] & u2) ? 16 : 0;
+                y[64 * j + l] = d1 * (float)((q[l] & 0x0f) + h1) - m1;
+                y[64 * j + l + 32] = d2 * (float)((q[l] >> 4) + h2) - m2;
+            }
+            u1 = (uint8_t)(u1 << 2);
+            u2 = (uint8_t)(u2 << 2);
+        }
+    }
+}
+
+// quant.rs:268-291 (Q6_K: 4 low bits in ql, 2 high bits in qh, an int8
+// scale per 16 values).
+void dequant_q6k(const uint8_t* src, size_t nblocks, float* dst) {
+    for (size_t bi = 0; bi < nblocks; ++bi) {
+        const uint8_t* b = src + bi * 210;
+        const float d = f16_at(b, 208);
+        for (int h = 0; h < 2; ++h) {
+            const uint8_t *ql = b + 64 * h, *qh = b + 128 + 32 * h;
+            const int8_t* sc = (const int8_t*)(b + 192 + 8 * h);
+            float* y = dst + 256 * bi + 128 * h;
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = (int)((ql[l] & 0x0f) | ((qh[l] & 3) << 4)) - 32;
+                const int q2 = (int)((ql[l + 32] & 0x0f) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l] = d * (float)sc[is] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// gguf.rs:335-355 for the decodable types: bytes and elements per block.
+int or_ggml_block(uint32_t t, size_t* bytes, size_t* per) {
+    switch (t) {
+        case 0: *bytes = 4, *per = 1; return 1;
+        case 1: *bytes = 2, *per = 1; return 1;
+        case 30: *bytes = 2, *per = 1; return 1;
+        case 2: *bytes = 18, *per = 32; return 1;
+        case 3: *bytes = 20, *per = 32; return 1;
+        case 6: *bytes = 22, *per = 32; return 1;
+        case 7: *bytes = 24, *per = 32; return 1;
+        case 8: *bytes = 34, *per = 32; return 1;
+        case 12: *bytes = 144, *per = 256; return 1;
+        case 13: *bytes = 176, *per = 256; return 1;
+        case 14: *bytes = 210, *per = 256; return 1;
+        default: return 0;
+    }
+}
+
+// quant.rs:107-156 (dequantize_to_f32): 0 (dst untouched) for other types,
+// when n is not a whole number of blocks or blocks holds fewer than needed.
+int or_dequantize_to_f32(uint32_t t, const uint8_t* blocks, size_t nbytes, float* dst, size_t n) {
+    size_t bytes, per;
+    if (!or_ggml_block(t, &bytes, &per)) return 0;
+    if (n % per != 0 || nbytes / bytes < n / per) return 0;
+    const size_t nb = n / per;
+    switch (t) {
+        case 0:
+            std::memcpy(dst, blocks, 4 * n);
+            break;
+        case 1:
+            for (size_t i = 0; i < n; ++i) dst[i] = f16_at(blocks, 2 * i);
+            break;
+        case 30:
+            for (size_t i = 0; i < n; ++i) dst[i] = bf16_to_f32((uint16_t)(blocks[2 * i] | (blocks[2 * i + 1] << 8)));
+            break;
+        case 8:
+            for (size_t bi = 0; bi < nb; ++bi) {
+                const uint8_t* b = blocks + 34 * bi;
+                const float d = f16_at(b, 0);
+                for (int k = 0; k < 32; ++k) dst[32 * bi + k] = d * (float)(int8_t)b[2 + k];
+            }
+            break;
+        case 2: dequant_legacy(blocks, nb, false, false, dst); break;
+        case 3: dequant_legacy(blocks, nb, true, false, dst); break;
+        case 6: dequant_legacy(blocks, nb, false, true, dst); break;
+        case 7: dequant_legacy(blocks, nb, true, true, dst); break;
+        case 12: dequant_qk(blocks, nb, false, dst); break;
+        case 13: dequant_qk(blocks, nb, true, dst); break;
+        case 14: dequant_q6k(blocks, nb, dst); break;
+    }
+    return 1;
+}
+
 // ---- int8-activation path (new in this build; no reference counterpart) ----
 
 // Exact int32 block dots P[r*nb + b] = sum_k q_w[r, 32b+k] * q_x[32b+k] for

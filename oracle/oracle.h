@@ -35,6 +35,9 @@ void or_gemv_bf16_batch(const uint16_t* w, const float* x, size_t x_stride, floa
                         size_t cols, size_t n_batch);
 size_t or_gemv_bf16_argmax(const uint16_t* w, const float* x, size_t rows, size_t cols);
 
+int or_ggml_block(uint32_t t, size_t* bytes, size_t* per);
+int or_dequantize_to_f32(uint32_t t, const uint8_t* blocks, size_t nbytes, float* dst, size_t n);
+
 void or_block_dots(int dtype, const void* qs, size_t rows, size_t cols, const int8_t* qx, int32_t* P);
 void or_dequant_act(const int8_t* qx, const uint16_t* sx, size_t n, float* out);
 void or_gemv_i8_exact(int dtype, const void* w, size_t rows, size_t cols, const int8_t* qx, const uint16_t* sx,

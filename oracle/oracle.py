@@ -59,6 +59,7 @@ def _declare(L):
     L.or_gemv_bf16.argtypes = [vp, vp, vp, sz, sz]
     L.or_gemv_bf16_batch.argtypes = [vp, vp, sz, vp, sz, sz, sz, sz]
     L.or_gemv_bf16_argmax.argtypes, L.or_gemv_bf16_argmax.restype = [vp, vp, sz, sz], sz
+    L.or_dequantize_to_f32.argtypes, L.or_dequantize_to_f32.restype = [C.c_uint32, vp, sz, vp, sz], i32
     L.or_block_dots.argtypes = [i32, vp, sz, sz, vp, vp]
     L.or_dequant_act.argtypes = [vp, vp, sz, vp]
     L.or_gemv_i8_exact.argtypes = [i32, vp, sz, sz, vp, vp, vp]
@@ -245,6 +246,19 @@ def gemv_bf16(w: np.ndarray, x: np.ndarray, rows: int, cols: int, n_tok: int = 1
     y = np.zeros((n_tok - 1) * ys + rows, np.float32)
     lib().or_gemv_bf16_batch(_p(w), _p(x), xs, _p(y), ys, rows, cols, n_tok)
     return y
+
+
+# gguf.rs:335-355 (decodable types): ggml type code -> (bytes, elements) per block.
+GGML_BLOCKS = {0: (4, 1), 1: (2, 1), 30: (2, 1), 2: (18, 32), 3: (20, 32), 6: (22, 32), 7: (24, 32),
+               8: (34, 32), 12: (144, 256), 13: (176, 256), 14: (210, 256)}
+
+
+def dequantize_to_f32(ggml_type: int, blocks: np.ndarray, n: int, fill: float = 9.0):
+    """kernels/quant.rs:107-156: (ok, dst); dst is left at `fill` when not ok."""
+    blocks = np.ascontiguousarray(blocks).view(np.uint8)
+    dst = np.full(n, fill, np.float32)
+    ok = lib().or_dequantize_to_f32(ggml_type, _p(blocks), blocks.size, _p(dst), n)
+    return bool(ok), dst
 
 
 def gemv_bf16_argmax(w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> int:

@@ -431,3 +431,177 @@ def test_bf16_argmax(oracle):
     w = np.full(8 * 8, 0, np.uint16)
     w[::8] = 0xFF80  # -inf
     assert oracle.gemv_bf16_argmax(w, np.ones(8, np.float32), 8, 8) == 0
+
+
+# ---- GGUF block decoding (kernels/quant.rs:97-291; kernels/tests.rs:745-950) -------
+
+def fp32_to_fp16(f):
+    """kernels/tests.rs:747-771: binary32 -> binary16, round to nearest even (normals only)."""
+    b = int(np.array([f], np.float32).view(np.uint32)[0])
+    s, e, m = (b >> 31) & 1, ((b >> 23) & 0xFF) - 127 + 15, b & 0x7FFFFF
+    inf = (s << 15) | (0x1F << 10)
+    if e >= 31:
+        return inf
+    if e <= 0:
+        return s << 15
+    rnd, sticky = (m >> 12) & 1, int(m & 0xFFF != 0)
+    mh = (m >> 13) + (rnd & (sticky | ((m >> 13) & 1)))
+    if mh & 0x400:
+        mh, e = 0, e + 1
+        if e >= 31:
+            return inf
+    return (s << 15) | (e << 10) | (mh & 0x3FF)
+
+
+def le16(v):
+    return [v & 0xFF, (v >> 8) & 0xFF]
+
+
+def q4k_unit_block(qs):
+    b = np.zeros(144, np.uint8)
+    b[:2] = le16(fp32_to_fp16(1.0))
+    b[4:8] = 1
+    b[12:16] = 1
+    b[16:] = qs
+    return b
+
+
+def test_dequantize_q8_0_kat(oracle):
+    blocks = np.zeros(68, np.uint8)
+    blocks[:2] = le16(fp32_to_fp16(0.25))
+    blocks[34:36] = le16(fp32_to_fp16(-2.0))
+    for k in range(32):
+        blocks[2 + k] = np.uint8((k - 16) & 0xFF)
+        blocks[36 + k] = np.uint8((127 - 4 * k) & 0xFF)
+    ok, out = oracle.dequantize_to_f32(8, blocks, 64)
+    assert ok
+    for k in range(32):
+        assert out[k] == 0.25 * (k - 16.0)
+        assert out[32 + k] == -2.0 * (127 - 4 * k)
+
+
+def test_dequantize_legacy_kat(oracle):
+    d, m = 0.5, -1.25
+    for ty, has_min, has_high in [(2, False, False), (3, True, False), (6, False, True), (7, True, True)]:
+        q = [((j * 11 + 5) % 32) if has_high else ((j * 7 + 3) % 16) for j in range(32)]
+        block = le16(fp32_to_fp16(d))
+        if has_min:
+            block += le16(fp32_to_fp16(m))
+        if has_high:
+            qh = 0
+            for j in range(32):
+                qh |= ((q[j] >> 4) & 1) << j
+            block += [(qh >> (8 * i)) & 0xFF for i in range(4)]
+        block += [(q[j] & 0x0F) | ((q[j + 16] & 0x0F) << 4) for j in range(16)]
+        ok, out = oracle.dequantize_to_f32(ty, np.array(block, np.uint8), 32)
+        assert ok
+        centre = 0 if has_min else 16 if has_high else 8
+        want = np.array([np.float32(q[j] - centre) * np.float32(d) + np.float32(m if has_min else 0.0)
+                         for j in range(32)], np.float32)
+        assert np.array_equal(out, want), ty
+
+
+def test_dequantize_k_quants_kat(oracle):
+    # Q4_K: low nibbles 1, high nibbles 2 -> each 64-run is 32 ones then 32 twos.
+    ok, out = oracle.dequantize_to_f32(12, q4k_unit_block(np.full(128, 0x21, np.uint8)), 256)
+    assert ok and all((run[:32] == 1).all() and (run[32:] == 2).all() for run in out.reshape(4, 64))
+    # Q5_K: the same with qh all 0 / all 1.
+    b = np.zeros(176, np.uint8)
+    b[:2] = le16(fp32_to_fp16(1.0))
+    b[4:8] = 1
+    b[12:16] = 1
+    b[48:] = 0x21
+    for qh, lo, hi in [(0x00, 1.0, 2.0), (0xFF, 17.0, 18.0)]:
+        b[16:48] = qh
+        ok, out = oracle.dequantize_to_f32(13, b, 256)
+        assert ok and all((run[:32] == lo).all() and (run[32:] == hi).all() for run in out.reshape(4, 64))
+    # Subnormal fp16 super-scale (kernels/tests.rs:889-900): d = 2^-24.
+    b = np.zeros(144, np.uint8)
+    b[:2] = le16(1)
+    b[4] = 1
+    b[16:] = 0x11
+    ok, out = oracle.dequantize_to_f32(12, b, 256)
+    assert ok and out[0] == np.float32(2.0 ** -24)
+    # Q6_K: d = 1, scales 1, ql = 0x10, qh = 0 -> -32 and -31.
+    b = np.zeros(210, np.uint8)
+    b[:128] = 0x10
+    b[192:208] = 1
+    b[208:] = le16(fp32_to_fp16(1.0))
+    ok, out = oracle.dequantize_to_f32(14, b, 256)
+    assert ok and all((h[:64] == -32).all() and (h[64:] == -31).all() for h in out.reshape(2, 128))
+
+
+def test_dequantize_k_quant_bit_positions(oracle):
+    # Where each high bit and each packed 6-bit scale / min lands (ggml's
+    # layout as quant.rs:197-291 reads it), one bit or one field at a time.
+    base = np.zeros(176, np.uint8)
+    base[:2] = le16(fp32_to_fp16(1.0))
+    base[4:8] = 1
+    base[12:16] = 1
+    for run in range(4):
+        for half in range(2):
+            for l in (0, 13, 31):
+                b = base.copy()
+                b[16 + l] = 1 << (2 * run + half)  # qh bit 2j (low nibbles) / 2j+1 (high) of byte l
+                ok, out = oracle.dequantize_to_f32(13, b, 256)
+                want = np.zeros(256, np.float32)
+                want[64 * run + 32 * half + l] = 16.0
+                assert ok and np.array_equal(out, want), (run, half, l)
+    # Q4_K scales: sub-block j < 4 scale = byte 4+j & 63, min = byte 8+j & 63;
+    # j >= 4 scale = (byte 12+j-4 & 15) | (byte 4+j-4 >> 6) << 4, min = (byte
+    # 12+j-4 >> 4) | (byte 8+j-4 >> 6) << 4.
+    b = np.zeros(144, np.uint8)
+    b[:2] = le16(fp32_to_fp16(1.0))
+    b[2:4] = le16(fp32_to_fp16(1.0))
+    b[4:16] = [0x41, 0x82, 0xC3, 0x04, 0x45, 0x86, 0xC7, 0x08, 0x9A, 0xBC, 0xDE, 0xF1]
+    b[16:] = 0x11  # q = 1 everywhere
+    ok, out = oracle.dequantize_to_f32(12, b, 256)
+    sc = b[4:16].astype(int)
+    for j in range(8):
+        if j < 4:
+            d, m = sc[j] & 63, sc[j + 4] & 63
+        else:
+            d, m = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4), (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)
+        seg = out[32 * j:32 * (j + 1)]
+        assert ok and (seg == np.float32(d) - np.float32(m)).all(), j
+    # Q6_K: bit pairs of qh and the int8 scale per 16 values.
+    for h in range(2):
+        for l in (0, 17, 31):
+            for pair in range(4):
+                b = np.zeros(210, np.uint8)
+                b[192:208] = [(i + 1) & 0xFF for i in range(16)]
+                b[192 + 8 * h + 3] = 0xFE  # a negative scale (-2)
+                b[208:] = le16(fp32_to_fp16(1.0))
+                b[:128] = 0x00
+                b[128 + 32 * h + l] = 1 << (2 * pair)  # value 16 in the 2 high bits of output pair
+                ok, out = oracle.dequantize_to_f32(14, b, 256)
+                is_ = l // 16 + 2 * pair
+                s = np.float32(np.int8(b[192 + 8 * h + is_]))
+                e = 128 * h + 32 * pair + l
+                assert ok and out[e] == np.float32(1.0) * s * np.float32(16 - 32), (h, l, pair)
+
+
+def test_dequantize_float_types_and_rejects(oracle):
+    vals = np.array([1.5, -2.25, 0.0, 3e-3, -7.0], np.float32)
+    ok, out = oracle.dequantize_to_f32(0, vals.view(np.uint8), 5)
+    assert ok and np.array_equal(out, vals)
+    f16 = np.array([fp32_to_fp16(float(v)) for v in vals], np.uint16)
+    ok, out = oracle.dequantize_to_f32(1, f16.view(np.uint8), 5)
+    assert ok and (np.abs(out - vals) <= np.abs(vals) * 1e-3).all()
+    assert np.array_equal(out, f16.view(np.float16).astype(np.float32))  # IEEE half, exactly
+    bf = oracle.f32_array_to_bf16(vals)
+    ok, out = oracle.dequantize_to_f32(30, bf.view(np.uint8), 5)
+    assert ok and np.array_equal(out, oracle.bf16_array_to_f32(bf))
+    # Every half bit pattern, subnormals, infinities and NaN payloads included.
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ok, out = oracle.dequantize_to_f32(1, allh.view(np.uint8), 65536)
+    want = allh.view(np.float16).astype(np.float32)
+    fin = ~np.isnan(want)
+    assert ok and np.array_equal(out[fin].view(np.uint32), want[fin].view(np.uint32))
+    nan_bits = out[~fin].view(np.uint32)
+    hb = allh[~fin].astype(np.uint32)
+    assert np.array_equal(nan_bits, ((hb & 0x8000) << 16) | 0x7F800000 | ((hb & 0x3FF) << 13))
+    # Unknown types, partial blocks and short input leave dst untouched.
+    for ty, nbytes, n in [(9, 64, 32), (10, 128, 32), (8, 33, 32), (8, 68, 33)]:
+        ok, out = oracle.dequantize_to_f32(ty, np.zeros(nbytes, np.uint8), n)
+        assert not ok and (out == 9.0).all()
