@@ -401,7 +401,7 @@ def gemma_decode(args, N, cpu: bool):
     tg, hg, tp, td = m.generate_device(prompt, n_gen)
     out = dict(config="gemma-3-1b architecture, Q8_0 weights 0.02*N(0,1), 32-token prompt, 128 greedy tokens",
                tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
-               prefill_s=round(tp, 4), kernels_per_token=5 * m.cfg.n_layer + 5)
+               prefill_s=round(tp, 4), kernels_per_token=5 * m.cfg.n_layer + 4)
     log(f"gemma3-1b device decode: {out['tok_s']} tok/s")
     if cpu:
         from oracle import oracle as O  # the CPU baseline leg only

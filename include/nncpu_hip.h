@@ -171,6 +171,17 @@ int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* 
  * Host x; synchronous. */
 int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int act);
 
+/* Device-resident form of nnh_model_argmax for f32 activations: x (cols
+ * floats), logits (rows floats, written: W x) and work
+ * (nnh_model_argmax_work_bytes(w) bytes) are device buffers, *out_row (a
+ * device u64) receives the row; asynchronous on `stream`. For the matrices
+ * of 16384 rows or more the first argmax stage runs inside the gemv (each
+ * workgroup's best row), so only a one-workgroup reduction follows it.
+ * Calls on different streams must not share `work`. */
+size_t nnh_model_argmax_work_bytes(const nnh_weight* w);
+int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, void* work, uint64_t* out_row,
+                         void* stream);
+
 /* Device-resident form of nnh_gemv_batch: x and y are device pointers, the
  * call is asynchronous on `stream` (a hipStream_t; NULL = the null stream).
  * Uses a library-owned scratch buffer for the Q4 block sums / quantized

@@ -26,7 +26,7 @@ ACT_I8 = NNH_ACT_I8
 
 __all__ = [
     "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
-    "gemv_batch_dev", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
+    "gemv_batch_dev", "model_argmax_dev", "model_argmax_work_bytes", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
 
@@ -191,6 +191,15 @@ def model_argmax(w: Weight, x: np.ndarray, act: int = ACT_F32) -> int:
 def gemv_batch_dev(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,
                    act: int = ACT_F32, stream: int = 0) -> None:
     check(lib().nnh_gemv_batch_dev(w.handle, x_ptr, x_stride, y_ptr, y_stride, n_tok, act, stream or None))
+
+
+def model_argmax_work_bytes(w: Weight) -> int:
+    return int(lib().nnh_model_argmax_work_bytes(w.handle))
+
+
+def model_argmax_dev(w: Weight, x_ptr: int, logits_ptr: int, work_ptr: int, out_ptr: int, stream: int = 0) -> None:
+    """model_argmax on device buffers (f32 activations); the row lands in the u64 at out_ptr."""
+    check(lib().nnh_model_argmax_dev(w.handle, x_ptr, logits_ptr, work_ptr, out_ptr, stream or None))
 
 
 def act_layout(cols: int, n_tok: int) -> tuple[int, int, int]:

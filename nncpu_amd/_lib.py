@@ -66,6 +66,8 @@ def _declare(L):
     L.nnh_upload_q8_0.argtypes, L.nnh_upload_q8_0.restype = [vp, vp, sz, sz, P(vp)], i32
     L.nnh_upload_q4.argtypes, L.nnh_upload_q4.restype = [vp, vp, vp, sz, sz, P(vp)], i32
     L.nnh_upload_bf16.argtypes, L.nnh_upload_bf16.restype = [vp, sz, sz, P(vp)], i32
+    L.nnh_model_argmax_work_bytes.argtypes, L.nnh_model_argmax_work_bytes.restype = [vp], sz
+    L.nnh_model_argmax_dev.argtypes, L.nnh_model_argmax_dev.restype = [vp, vp, vp, vp, vp, vp], i32
     L.nnh_dequantize_dev.argtypes, L.nnh_dequantize_dev.restype = [C.c_uint32, vp, sz, vp, sz, vp], i32
     L.nnh_upload_gguf.argtypes, L.nnh_upload_gguf.restype = [C.c_uint32, vp, sz, sz, sz, i32, P(vp)], i32
     L.nnh_upload.argtypes, L.nnh_upload.restype = [i32, vp, sz, sz, P(vp)], i32

@@ -190,6 +190,39 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
     return NNH_OK;
 }
 
+// Work of the device argmax: the partial keys, then (Q4, fused path) the
+// block sums of x.
+bool argmax_fused(const nnh_weight* w, int act) { return act == NNH_ACT_F32 && w->dtype != NNH_BF16 && w->f32v2; }
+size_t argmax_parts(const nnh_weight* w, int act) {
+    return argmax_fused(w, act) ? (size_t)nnh::f32_v2_parts((int)w->rows) : nnh::argmax_partial_words(w->rows);
+}
+
+// Queue y = W x and the row of its first largest value into *out (device
+// pointers; `work` holds argmax_parts words and, fused Q4, nb floats).
+// Through the 8-lane kernel the first argmax stage is fused into the gemv.
+int run_argmax(const nnh_weight* w, const float* x, float* y, uint8_t* work, uint64_t* out, int act,
+               uint8_t* scratch, hipStream_t st) {
+    uint64_t* part = (uint64_t*)work;
+    if (argmax_fused(w, act)) {
+        float* xsum = (float*)(work + align_up(argmax_parts(w, act) * 8));
+        nnh::launch_gemv_f32_v2_argmax(w->dtype, w->fq, w->fs, w->bi, x, xsum, (int)w->rows, (int)w->nb,
+                                       (int)w->nbp, y, part, st);
+        nnh::launch_argmax_final(y, part, (int)argmax_parts(w, act), out, st, 0);
+    } else {
+        int rc = run_gemv(w, x, w->cols, y, w->rows, 1, act, scratch, st);
+        if (rc) return rc;
+        // BF16 with the 4-row kernel streams a running best from -inf
+        // (kernels/mod.rs:384-406), the rest take the first-max argmax.
+        nnh::launch_argmax(y, w->rows, part, out, st, w->dtype == NNH_BF16 && w->bpath == nnh::BF16_PATH_QUAD ? 1 : 0);
+    }
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+size_t argmax_work_bytes(const nnh_weight* w, int act) {
+    return align_up(argmax_parts(w, act) * 8) + (argmax_fused(w, act) && w->dtype == NNH_Q4S ? w->nb * 4 : 0);
+}
+
 size_t gemv_scratch_bytes(const nnh_weight* w, size_t n_tok, int act) {
     if (w->dtype == NNH_BF16) return 0;
     if (act == NNH_ACT_F32) return w->dtype == NNH_Q4S ? align_up(n_tok * w->nb * 4) : 0;
@@ -557,7 +590,7 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
     if (w->rows >= ((size_t)1 << 32)) return fail(NNH_E_INVALID, "argmax: too many rows");
     const size_t off_y = align_up(w->cols * 4);
     const size_t off_p = off_y + align_up(w->rows * 4);
-    const size_t off_o = off_p + align_up(nnh::argmax_partial_words(w->rows) * 8);
+    const size_t off_o = off_p + align_up(argmax_work_bytes(w, act));
     const size_t off_s = off_o + ALIGN;
     uint8_t *s, *h;
     if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, 1, act), &s))) return rc;
@@ -567,17 +600,28 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
     uint64_t* dout = (uint64_t*)(s + off_o);
     std::memcpy(h, x, w->cols * 4);
     NNH_HIP(hipMemcpyAsync(dx, h, w->cols * 4, hipMemcpyHostToDevice, g_stream));
-    if ((rc = run_gemv(w, dx, w->cols, dy, w->rows, 1, act, s + off_s, g_stream))) return rc;
-    // BF16 with the 4-row kernel streams a running best from -inf
-    // (kernels/mod.rs:384-406), the rest take the first-max argmax.
-    nnh::launch_argmax(dy, w->rows, (uint64_t*)(s + off_p), dout, g_stream,
-                       w->dtype == NNH_BF16 && w->bpath == nnh::BF16_PATH_QUAD ? 1 : 0);
-    NNH_HIP(hipGetLastError());
+    if ((rc = run_argmax(w, dx, dy, s + off_p, dout, act, s + off_s, g_stream))) return rc;
     uint64_t* hidx = (uint64_t*)(h + off_y);
     NNH_HIP(hipMemcpyAsync(hidx, dout, 8, hipMemcpyDeviceToHost, g_stream));
     NNH_HIP(hipStreamSynchronize(g_stream));
     *out_row = (size_t)*hidx;
     return NNH_OK;
+}
+
+size_t nnh_model_argmax_work_bytes(const nnh_weight* w) { return w ? argmax_work_bytes(w, NNH_ACT_F32) : 0; }
+
+int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, void* work, uint64_t* out_row,
+                         void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, 0, 0, 1, NNH_ACT_F32))) return rc;
+    if (w->rows >= ((size_t)1 << 32)) return fail(NNH_E_INVALID, "argmax: too many rows");
+    if (!x || !logits || !work || !out_row) return fail(NNH_E_INVALID, "argmax: null pointer");
+    uint8_t* s = nullptr;
+    const size_t need = argmax_fused(w, NNH_ACT_F32) ? 0 : gemv_scratch_bytes(w, 1, NNH_ACT_F32);
+    if (need && (rc = scratch_locked(need, &s))) return rc;
+    return run_argmax(w, x, logits, (uint8_t*)work, out_row, NNH_ACT_F32, s, (hipStream_t)stream);
 }
 
 int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,

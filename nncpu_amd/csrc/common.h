@@ -89,6 +89,12 @@ void launch_relayout_f32(int dtype, const uint8_t* raw_qs, const uint16_t* raw_s
 void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float* xsum, hipStream_t st);
 // Bit-exact f32 gemv for n_tok <= 16 vectors; for Q4, xsum is scratch of
 // n_tok * nb floats (the block sums of x).
+// One vector through the 8-lane (tall) kernel, y written and each
+// workgroup's largest argmax key into part[0..f32_v2_parts(rows)).
+int f32_v2_parts(int rows);
+void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
+                               const float* x, float* xsum, int rows, int nb, int nbp, float* y, uint64_t* part,
+                               hipStream_t st);
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
                      size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st);
@@ -129,6 +135,22 @@ void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows,
                        hipStream_t st);
 
 // argmax over n logits (kernels_misc.hip); partial holds 2*ceil(n/2048) words.
+// The argmax key of value v at row idx: an order-preserving image of v in
+// the high word (-0 folded onto +0, which compare equal), the complement of
+// the index in the low word, so the largest key is the largest value at its
+// lowest row; NaN gets key 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    if (!(v == v)) return 0;
+    if (v == 0.0f) v = 0.0f;
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+// The largest key of each part -> the row (v: the values, read for row 0's
+// NaN rule in mode 0).
+void launch_argmax_final(const float* v, const uint64_t* partial, int nparts, uint64_t* out, hipStream_t st,
+                         int mode);
 // mode 0: the first largest value, a NaN in row 0 keeping row 0
 // (forward.rs:1003-1011); mode 1: the BF16 4-row kernel's running best from
 // -inf (scalar.rs:612-628): NaN and -inf never taken, none taken gives 0.

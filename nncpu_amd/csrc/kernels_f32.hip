@@ -780,7 +780,8 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
                                                           const uint16_t* __restrict__ biases,
                                                           const float* __restrict__ x, size_t x_stride,
                                                           const float* __restrict__ xsum, int rows, int nb, int nbp,
-                                                          float* __restrict__ y, size_t y_stride) {
+                                                          float* __restrict__ y, size_t y_stride,
+                                                          uint64_t* __restrict__ part) {
     constexpr int G = DT == 1 ? 4 : 8;
     const int j = threadIdx.x & 7, lg = threadIdx.x >> 3;
     const int ng = (nb + G - 1) / G;
@@ -825,6 +826,7 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
         v2_group<DT, M>(acc, gb, g + 1, nb, xl, j);
     }
 
+    uint64_t key = 0;  // this lane's largest argmax key (M = 1, part != nullptr)
 #pragma unroll
     for (int r = 0; r < V2_R; ++r) {
         const bool valid = (blockIdx.x * V2_R + r) * 32 + lg < rows;
@@ -863,6 +865,27 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
             float res = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
             if (DT == 2) res = __fadd_rn(res, bdot[m]);
             if (valid && j == 0) y[(size_t)m * y_stride + row[r]] = res;
+            if (M == 1 && valid && j == 0) {
+                const uint64_t k = argmax_key(res, (uint32_t)row[r]);
+                key = k > key ? k : key;
+            }
+        }
+    }
+    if (M == 1 && part) {
+        // The workgroup's largest key (the argmax's first stage, fused).
+        __shared__ uint64_t red[4];
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)key, s, 64), hi = __shfl_xor((uint32_t)(key >> 32), s, 64);
+            const uint64_t o = ((uint64_t)hi << 32) | lo;
+            key = o > key ? o : key;
+        }
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = key;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t k = red[0];
+            for (int w = 1; w < 4; ++w) k = red[w] > k ? red[w] : k;
+            part[blockIdx.x] = k;
         }
     }
 }
@@ -873,10 +896,10 @@ void launch_dt_v2(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* 
     dim3 grid(ceil_div(rows, 32 * V2_R)), block(256);
     const size_t lds = (size_t)M * nb * 32 * sizeof(float);
     switch (M) {
-        case 1: gemv_f32_v2_kernel<DT, 1><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
-        case 2: gemv_f32_v2_kernel<DT, 2><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
-        case 3: gemv_f32_v2_kernel<DT, 3><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
-        default: gemv_f32_v2_kernel<DT, 4><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys); break;
+        case 1: gemv_f32_v2_kernel<DT, 1><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
+        case 2: gemv_f32_v2_kernel<DT, 2><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
+        case 3: gemv_f32_v2_kernel<DT, 3><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
+        default: gemv_f32_v2_kernel<DT, 4><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
     }
 }
 
@@ -928,6 +951,22 @@ void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float
 
 // Tokens in chunks of up to four per launch: every token's chains are
 // independent, so the chunking never changes a bit.
+int f32_v2_parts(int rows) { return ceil_div(rows, 32 * V2_R); }
+
+void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
+                               const float* x, float* xsum, int rows, int nb, int nbp, float* y, uint64_t* part,
+                               hipStream_t st) {
+    if (dtype == 2) launch_block_sums(x, (size_t)nb * 32, nb, 1, xsum, st);
+    const dim3 grid(f32_v2_parts(rows)), block(256);
+    const size_t lds = (size_t)nb * 32 * sizeof(float);
+    if (dtype == 1)
+        gemv_f32_v2_kernel<1, 1><<<grid, block, lds, st>>>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y,
+                                                           rows, part);
+    else
+        gemv_f32_v2_kernel<2, 1><<<grid, block, lds, st>>>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y,
+                                                           rows, part);
+}
+
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
                      size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st) {

@@ -17,14 +17,6 @@ namespace {
 
 constexpr int PER_BLOCK = 2048;
 
-__device__ __forceinline__ uint64_t key_of(float v, uint32_t idx) {
-    if (!(v == v)) return 0;
-    if (v == 0.0f) v = 0.0f;
-    uint32_t u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - idx);
-}
-
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ uint64_t block_max(uint64_t k) {
@@ -46,7 +38,7 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     uint64_t k = 0;
     for (int i = threadIdx.x; i < PER_BLOCK; i += 256) {
         size_t e = base + i;
-        if (e < n) k = umax64(k, key_of(v[e], (uint32_t)e));
+        if (e < n) k = umax64(k, argmax_key(v[e], (uint32_t)e));
     }
     k = block_max(k);
     if (threadIdx.x == 0) partial[blockIdx.x] = k;
@@ -83,6 +75,11 @@ int cu_count() {
 }
 
 size_t argmax_partial_words(size_t n) { return (n + PER_BLOCK - 1) / PER_BLOCK; }
+
+void launch_argmax_final(const float* v, const uint64_t* partial, int nparts, uint64_t* out, hipStream_t st,
+                         int mode) {
+    argmax_final_kernel<<<1, 256, 0, st>>>(v, partial, nparts, out, mode);
+}
 
 void launch_argmax(const float* v, size_t n, uint64_t* partial, uint64_t* out, hipStream_t st, int mode) {
     int nparts = (int)argmax_partial_words(n);

@@ -24,8 +24,8 @@
 // The residual stream alternates between two buffers, so no kernel reads the
 // buffer it writes. The matmuls are the library's bit-exact f32 path: its
 // one-vector core (f32_m1.h) on the 16-lane weight layout that
-// nnh_weight_f32_layout exposes, and nnh_gemv_batch_dev / nnh_argmax_dev for
-// the lm_head.
+// nnh_weight_f32_layout exposes, and nnh_model_argmax_dev for the lm_head
+// (its first argmax stage fused into the gemv).
 //
 // What is taken from the host: RoPE's cos / sin per position (computed with
 // the CPU restatement's own libm calls, uploaded once) and the embedding
@@ -846,7 +846,7 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     GD_HIP(hipMalloc((void**)&m->h, (size_t)c.n_ff * 4));
     GD_HIP(hipMalloc((void**)&m->logits, (size_t)c.n_vocab * 4));
     GD_HIP(hipMalloc((void**)&m->record, (size_t)n_gen_max * c.n_layer * E * 4));
-    GD_HIP(hipMalloc(&m->work, nnh_argmax_work_bytes((size_t)c.n_vocab)));
+    GD_HIP(hipMalloc(&m->work, nnh_model_argmax_work_bytes(m->w.back())));
     GD_HIP(hipMalloc((void**)&m->tok, 8));
     GD_HIP(hipMalloc((void**)&m->pos, 4));
     GD_HIP(hipMalloc((void**)&m->step, 4));
@@ -922,8 +922,7 @@ static int queue_step(nngd_model* m) {
                   m->xa,   m->y,    m->record + (size_t)(c.n_layer - 1) * E,          m->step,
                   rs,      E,       eps};
     final_kernel<<<1, WG, 0, st>>>(fin);
-    if (nnh_gemv_batch_dev(m->w.back(), m->y, E, m->logits, c.n_vocab, 1, NNH_ACT_F32, st) ||
-        nnh_argmax_dev(m->logits, (size_t)c.n_vocab, m->work, m->tok, st)) {
+    if (nnh_model_argmax_dev(m->w.back(), m->y, m->logits, m->work, m->tok, st)) {
         m->err = std::string("lm_head: ") + nnh_last_error();
         return 1;
     }

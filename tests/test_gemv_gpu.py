@@ -449,3 +449,51 @@ def test_device_encoded_weight_matmul(oracle, dtype):
     m = oracle.QMatrix.from_f32(dtype, w)
     x = rng.normals(cols, 1.0)
     assert np.array_equal(bits(N.model_gemv(dev, x)), bits(oracle.gemv_batch(m, x)))
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+@pytest.mark.parametrize("rows,cols", [(16384, 1152), (20000, 64), (3000, 1152)])
+def test_model_argmax_dev(oracle, dtype, rows, cols):
+    # model_argmax (forward.rs:989-1011) on device buffers: tall matrices take
+    # the gemv with the argmax's first stage fused in, the rest the two-kernel
+    # argmax; both the first largest logit (ties to the lower row, a NaN in
+    # row 0 keeps row 0). The logits are written either way.
+    import torch
+    say("argmax_dev", dtype, rows, cols)
+    rng = oracle.Rng(0xA5 + rows + dtype)
+    w = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+    m = oracle.QMatrix.from_f32(dtype, w)
+    wt = upload(m)
+    work = torch.zeros(N.model_argmax_work_bytes(wt), dtype=torch.uint8, device="cuda")
+    logits = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    out = torch.zeros(1, dtype=torch.int64, device="cuda")
+    for case in ("plain", "nan0"):
+        x = rng.normals(cols, 1.0)
+        if case == "nan0":
+            x[0] = np.nan  # every logit NaN: row 0
+        want_y = oracle.gemv_batch(m, x)
+        xd = torch.from_numpy(x).cuda()
+        N.model_argmax_dev(wt, xd.data_ptr(), logits.data_ptr(), work.data_ptr(), out.data_ptr())
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(logits.cpu().numpy()), bits(want_y)), case
+        assert int(out.item()) == oracle.argmax(want_y), case
+        assert N.model_argmax(wt, x) == oracle.argmax(want_y), case
+
+
+def test_model_argmax_dev_ties(oracle):
+    # Equal maxima in several rows of a tall Q8 matrix: the lowest row.
+    import torch
+    rows, cols = 16384, 64
+    w = np.zeros((rows, cols), np.float32)
+    for r in (7000, 300, 16000):
+        w[r, 0] = 1.0
+    m = oracle.QMatrix.from_f32(1, w)
+    wt = upload(m)
+    x = np.zeros(cols, np.float32)
+    x[0] = 2.0
+    work = torch.zeros(N.model_argmax_work_bytes(wt), dtype=torch.uint8, device="cuda")
+    logits = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    out = torch.zeros(1, dtype=torch.int64, device="cuda")
+    N.model_argmax_dev(wt, torch.from_numpy(x).cuda().data_ptr(), logits.data_ptr(), work.data_ptr(), out.data_ptr())
+    torch.cuda.synchronize()
+    assert int(out.item()) == 300 == oracle.argmax(oracle.gemv_batch(m, x))
