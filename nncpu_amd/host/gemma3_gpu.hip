@@ -123,27 +123,28 @@ __device__ __forceinline__ void tput4(float* xt, int S, int piece, float4 v) {
 }
 
 // hsum8 of the eight FMA lanes' sums of squares of a transposed dim-vector
-// (dim % 32 == 0), run by lanes 0..7 of the calling wave; valid at lane 0.
-// dim % 128 == 0. The LDS reads run four ahead of the FMAs, with no branch
-// between them (left to itself the compiler, short of registers, waits out
-// each read's latency in turn).
+// (dim % 128 == 0), run by lanes 0..7 of the calling wave; valid at lane 0.
+// A lane's values are read from LDS 12 float4s at a time, all issued before
+// that chunk's FMAs (a buffer rotated across loop iterations instead makes
+// the compiler wait for every read at the loop head).
 __device__ __forceinline__ float chain_sumsq(const float* xt, int dim, int lane) {
+    constexpr int CH = 12;
     float a = 0.0f;
     if (lane < 8) {
         const float4* p = (const float4*)(xt + lane * tstride(dim));
         const int n = dim / 32;
-        float4 b[4];
+        for (int m = 0; m < n; m += CH) {
+            float4 b[CH];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) b[k] = p[k];
-        for (int m = 0; m < n; m += 4) {
+            for (int k = 0; k < CH; ++k) b[k] = p[min(m + k, n - 1)];  // past the end: a spare read
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 v = b[k];
-                b[k] = p[min(m + k + 4, n - 1)];  // past the end: a spare read
-                a = __fmaf_rn(v.x, v.x, a);
-                a = __fmaf_rn(v.y, v.y, a);
-                a = __fmaf_rn(v.z, v.z, a);
-                a = __fmaf_rn(v.w, v.w, a);
+            for (int k = 0; k < CH; ++k) {
+                if (m + k < n) {
+                    a = __fmaf_rn(b[k].x, b[k].x, a);
+                    a = __fmaf_rn(b[k].y, b[k].y, a);
+                    a = __fmaf_rn(b[k].z, b[k].z, a);
+                    a = __fmaf_rn(b[k].w, b[k].w, a);
+                }
             }
         }
     }
@@ -358,6 +359,7 @@ __global__ __launch_bounds__(QKV_NT) void qkv_kernel(QkvArgs a) {
     // ahead of other workgroups' prologue loads).
     ss.store(sl);
     if (!FIRST) res_stage<NT>(r, a.E, xs);
+    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));  // every prologue load has landed
     __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
@@ -404,6 +406,7 @@ __global__ __launch_bounds__(FFN_NT) void ffn_kernel(FfnArgs a) {
     sg.store(sl);
     su.store(sl + HR * a.gate.nbp);
     res_stage<NT>(r, a.E, xs);
+    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));  // every prologue load has landed
     __builtin_amdgcn_sched_barrier(0);
     L.prefetch();
     __builtin_amdgcn_sched_barrier(0);
