@@ -64,10 +64,6 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
     const uint32_t u = __float_as_uint(f);
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
-__device__ __forceinline__ float hsum8(const float* v) {
-    return __fadd_rn(__fadd_rn(__fadd_rn(v[0], v[4]), __fadd_rn(v[1], v[5])),
-                     __fadd_rn(__fadd_rn(v[2], v[6]), __fadd_rn(v[3], v[7])));
-}
 // hsum8 of lanes 0..7's values, by lane exchanges (valid at lane 0):
 // xor-4 gives v_l + v_{l+4}, xor-1 and xor-2 then add those pairs as hsum8 does.
 __device__ __forceinline__ float hsum8_lanes(float a) {
@@ -479,11 +475,13 @@ __global__ __launch_bounds__(ATTN_NT) void attn_kernel(AttnArgs a) {
     constexpr int ST = ATTN_BLOCK / 8 + 4;  // transposed weights: lane l's run at l * ST
     constexpr int VS = ATTN_BLOCK + 8;  // transposed value rows: element e's keys at e * VS
     constexpr int VL = (ATTN_BLOCK * VCH + ATTN_NT - 1) / ATTN_NT;  // value pieces per thread
+    constexpr int QS = CH + 4;  // qe row stride: 16-byte rows, the pad spreads the four lanes' reads
     __shared__ __attribute__((aligned(16))) uint16_t ks_lds[ATTN_BLOCK * HD];
     __shared__ __attribute__((aligned(16))) uint16_t vt[EW * VS];
     __shared__ __attribute__((aligned(16))) float qs[HD];
     __shared__ __attribute__((aligned(16))) float ks[HD];
     __shared__ __attribute__((aligned(16))) float qt[HD + 32];
+    __shared__ __attribute__((aligned(16))) float qe[8 * QS];  // rotated q by element of chunk: qe[e * QS + c] = q[8c + e]
     __shared__ __attribute__((aligned(16))) float kt[HD + 32];
     __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
     __shared__ __attribute__((aligned(16))) float sc[ATTN_BLOCK];
@@ -546,8 +544,10 @@ __global__ __launch_bounds__(ATTN_NT) void attn_kernel(AttnArgs a) {
     // RoPE: threads 0..HALF-1 rotate q's pairs (j, j + HALF), HALF..HD-1 k's.
     if (tid < HALF) {
         const float x0 = qs[tid], x1 = qs[tid + HALF];
-        qs[tid] = __fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1));
-        qs[tid + HALF] = __fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1));
+        const float r0 = __fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1));
+        const float r1 = __fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1));
+        qe[(tid & 7) * QS + (tid >> 3)] = r0;
+        qe[((tid + HALF) & 7) * QS + ((tid + HALF) >> 3)] = r1;
     } else if (tid < HD) {
         const int j = tid - HALF;
         const float x0 = ks[j], x1 = ks[j + HALF];
@@ -572,52 +572,41 @@ __global__ __launch_bounds__(ATTN_NT) void attn_kernel(AttnArgs a) {
         if (es == 0) a.kc[(size_t)pos * kv_dim + kvh * HD + tid] = kn[tid];
         if (tid < EW) a.vc[(size_t)pos * kv_dim + kvh * HD + es * EW + tid] = vt[tid * VS + n - 1];
     }
-    // Scores: chunks of 8 elements in batches of SB, the next batch's LDS
-    // reads issued before this batch's FMAs.
-    float s_t = -INFINITY;
-    if (tid < n) {
-        constexpr int SB = 2;
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        const bool last = tid == n - 1;
-        const uint16_t* krow = last ? kn : ks_lds + tid * HD;
-        const int sw = last ? 0 : tid % CH;
-        uint4 ka[SB], kb[SB];
-        float4 qa[2 * SB], qb[2 * SB];
-        auto fetch = [&](uint4 (&kk)[SB], float4 (&qq)[2 * SB], int c0) {
+    // Scores: four lanes per key (key tid / 4), lane u running the dot's
+    // chains u and u + 4 (elements 8c + u and 8c + u + 4, c in order), then
+    // (a_u + a_{u+4}), xor-1, xor-2: hsum8's additions in its order. Each
+    // lane's q values are contiguous in qe; a key chunk's two values are two
+    // 32-bit LDS reads.
+    {
+        const int t = tid >> 2, u = tid & 3;
+        float a0 = 0.0f, a1 = 0.0f;
+        if (t < n) {
+            const bool last = t == n - 1;
+            const uint16_t* krow = last ? kn : ks_lds + t * HD;
+            const int sw = last ? 0 : t % CH;
+            const float* q0 = qe + u * QS;
+            const float* q1 = qe + (u + 4) * QS;
+            const int hs = 16 * (u & 1);
 #pragma unroll
-            for (int u = 0; u < SB; ++u) {
-                kk[u] = *(const uint4*)(krow + 8 * ((c0 + u) ^ sw));
-                qq[2 * u] = *(const float4*)(qs + 8 * (c0 + u));
-                qq[2 * u + 1] = *(const float4*)(qs + 8 * (c0 + u) + 4);
+            for (int c0 = 0; c0 < CH; c0 += 4) {
+                const float4 qa = *(const float4*)(q0 + c0), qb = *(const float4*)(q1 + c0);
+                const float qav[4] = {qa.x, qa.y, qa.z, qa.w}, qbv[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    const uint32_t* kc = (const uint32_t*)(krow + 8 * ((c0 + cc) ^ sw));
+                    const uint32_t klo = kc[u >> 1], khi = kc[2 + (u >> 1)];
+                    a0 = __fmaf_rn(qav[cc], bf16f((klo >> hs) & 0xffffu), a0);
+                    a1 = __fmaf_rn(qbv[cc], bf16f((khi >> hs) & 0xffffu), a1);
+                }
             }
-        };
-        auto dot = [&](const uint4 (&kk)[SB], const float4 (&qq)[2 * SB]) {
-#pragma unroll
-            for (int u = 0; u < SB; ++u) {
-                const uint4 k4 = kk[u];
-                const float4 q0 = qq[2 * u], q1 = qq[2 * u + 1];
-                acc[0] = __fmaf_rn(q0.x, bf16f(k4.x & 0xffffu), acc[0]);
-                acc[1] = __fmaf_rn(q0.y, bf16f(k4.x >> 16), acc[1]);
-                acc[2] = __fmaf_rn(q0.z, bf16f(k4.y & 0xffffu), acc[2]);
-                acc[3] = __fmaf_rn(q0.w, bf16f(k4.y >> 16), acc[3]);
-                acc[4] = __fmaf_rn(q1.x, bf16f(k4.z & 0xffffu), acc[4]);
-                acc[5] = __fmaf_rn(q1.y, bf16f(k4.z >> 16), acc[5]);
-                acc[6] = __fmaf_rn(q1.z, bf16f(k4.w & 0xffffu), acc[6]);
-                acc[7] = __fmaf_rn(q1.w, bf16f(k4.w >> 16), acc[7]);
-            }
-        };
-        fetch(ka, qa, 0);
-#pragma unroll
-        for (int c0 = 0; c0 < CH; c0 += 2 * SB) {
-            fetch(kb, qb, c0 + SB);
-            __builtin_amdgcn_sched_barrier(0);
-            dot(ka, qa);
-            if (c0 + 2 * SB < CH) fetch(ka, qa, c0 + 2 * SB);
-            __builtin_amdgcn_sched_barrier(0);
-            dot(kb, qb);
         }
-        s_t = __fmul_rn(hsum8(acc), a.scale);
+        float p = __fadd_rn(a0, a1);
+        p = __fadd_rn(p, __shfl_xor(p, 1, 64));
+        p = __fadd_rn(p, __shfl_xor(p, 2, 64));
+        if (t < n && u == 0) sc[t] = __fmul_rn(p, a.scale);
     }
+    lds_barrier();
+    const float s_t = tid < n ? sc[tid] : -INFINITY;
     // The first maximum over keys in order: a leftmost-maximum tree, with a
     // NaN after key 0 never taken (as the scan's comparison never takes one)
     // and a NaN at key 0 kept (it is never replaced).
