@@ -36,7 +36,7 @@ namespace {
 
 constexpr int BF16_NT = 128;                // threads per workgroup
 constexpr int BF16_D = 8;                   // 16-byte weight pieces in flight per lane
-constexpr int BF16_X_LDS = 64 * 1024;       // LDS for staged x (all vectors of a pass)
+constexpr int BF16_X_LDS = 72 * 1024;       // LDS for staged x (all vectors of a pass)
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
