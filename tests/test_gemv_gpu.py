@@ -403,6 +403,53 @@ def test_i8_gemm_bit_exact_sums(oracle, dtype, rows, cols, n_tok):
         assert np.linalg.norm(got - r) <= 1e-3 * np.linalg.norm(r)
 
 
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_i8_few_token_split_repeated_and_graph(oracle, dtype):
+    # With K split, the few-token kernel's partials meet in the workspace and
+    # a second kernel adds them: calls in a row on one weight (different token
+    # counts) and replays of a captured graph, with eager work between them,
+    # each keep one ulp of the exact sum, and the replays the eager bits.
+    import torch
+    rows, cols = 1536, 6144
+    say("split repeat", dtype, rows, cols)
+    rng = oracle.Rng(0x5C17 + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+
+    def check(x, n_tok, y):
+        for t in range(n_tok):
+            qx, sx = oracle.quantize_act(x[t * cols:(t + 1) * cols])
+            exact = oracle.gemv_i8_exact(m, qx, sx)
+            assert np.all(np.abs(y[t * rows:(t + 1) * rows] - exact) <= np.spacing(np.abs(exact))), (n_tok, t)
+
+    for n_tok in (8, 4, 16, 5, 8):
+        x = rng.normals(n_tok * cols, 1.0)
+        y = np.zeros(n_tok * rows, np.float32)
+        N.gemv_batch(w, x, cols, y, rows, n_tok, N.ACT_I8)
+        check(x, n_tok, y)
+    n_tok = 8
+    x = rng.normals(n_tok * cols, 1.0)
+    dx = torch_dev(x)
+    dy = torch.zeros(n_tok * rows, device="cuda")
+    st = torch.cuda.Stream()
+    N.gemv_batch_dev(w, dx.data_ptr(), cols, dy.data_ptr(), rows, n_tok, N.ACT_I8, st.cuda_stream)
+    torch.cuda.synchronize()
+    ref = dy.cpu().numpy().copy()
+    check(x, n_tok, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        N.gemv_batch_dev(w, dx.data_ptr(), cols, dy.data_ptr(), rows, n_tok, N.ACT_I8, st.cuda_stream)
+    for _ in range(3):
+        dy.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dy.cpu().numpy(), ref)
+        y2 = np.zeros(4 * rows, np.float32)  # eager work between replays
+        N.gemv_batch(w, x[:4 * cols], cols, y2, rows, 4, N.ACT_I8)
+        assert np.array_equal(y2, ref[:4 * rows])
+
+
 # ---- device re-encoder (kernels/quant.rs:31-95 on the GPU) ----------------------------
 
 def encode_on_device(dtype, w, rows, cols):
