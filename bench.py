@@ -193,7 +193,8 @@ BF16_SHAPES = [(1536, 1536), (2048, 1536), (6144, 1536), (4096, 4096), (14336, 4
 def measure_cases(args, N, cases, act_mode, label):
     """Time each (dtype, n, k, m) case alone: `args.steps` launches captured in
     a graph over rotating weight copies (>= 512 MB), inputs resident in HBM.
-    act_mode: ACT_I8 times the int8 matmul on pre-quantized activations;
+    act_mode: ACT_I8 / ACT_MXI8 time the int8 matmul on activations
+    quantized beforehand (nncpu's Q8_0 encoder / power-of-two MX blocks);
     ACT_F32 times the bit-exact f32 path (block sums included for Q4)."""
     import torch
     st = Stream()
@@ -204,16 +205,17 @@ def measure_cases(args, N, cases, act_mode, label):
         ws = make_weights(N, dtype, n, k, 0x5EED10 + 7 * ci + dtype, copies)
         x = make_x(k, m, 0xA11 + ci)
         y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
-        _, _, abytes = N.act_layout(k, m)
+        qmode = act_mode if act_mode != N.ACT_F32 else N.ACT_I8
+        _, _, abytes = N.act_layout_ex(qmode, k, m)
         act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
-        N.quantize_act_dev(x.data_ptr(), k, k, m, act.data_ptr(), st.handle)
+        N.quantize_act_ex_dev(qmode, x.data_ptr(), k, k, m, act.data_ptr(), st.handle)
         state = {"i": 0}
 
         def launch(ws=ws, state=state, act=act, x=x, y=y, n=n, k=k, m=m):
             w = ws[state["i"] % len(ws)]
             state["i"] += 1
-            if act_mode == N.ACT_I8:
-                N.gemv_i8_dev(w, act.data_ptr(), m, y.data_ptr(), n, st.handle)
+            if act_mode != N.ACT_F32:
+                N.gemv_act_dev(w, act_mode, act.data_ptr(), m, y.data_ptr(), n, st.handle)
             else:
                 N.gemv_batch_dev(w, x.data_ptr(), k, y.data_ptr(), n, m, N.ACT_F32, st.handle)
 
@@ -449,6 +451,8 @@ def main():
     torch.cuda.set_device(0)
     extra = {}
     if args.workload in ("prefill", "all"):
+        extra["prefill_m512_mx"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
+                                                 N.ACT_MXI8, "prefill_mx")
         extra["prefill_m512"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
                                               N.ACT_I8, "prefill")
     if args.workload in ("qwen_prefill", "all"):

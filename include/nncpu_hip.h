@@ -60,10 +60,21 @@ enum {
  *     nncpu's own Q8_0 encoder (kernels/quant.rs:31-60) to int8 blocks of 32
  *     with a BF16 scale; the kernels form the exact int32 block dot products
  *     and scale them in f64. The result is the f32 rounding of the exact
- *     product of the dequantized weights and activations. */
+ *     product of the dequantized weights and activations (from 17 vectors:
+ *     within the f32 roundings of 8-block chunks of it, see the GEMM).
+ *   NNH_ACT_MXI8: int8 blocks of 32 with a power-of-two scale (the OCP
+ *     MXINT8 block; the scale still stored as BF16 bits): the least 2^E
+ *     with 127 * 2^E >= max |x| of the block, q = rint(x / 2^E). Same exact
+ *     block dots and f64 scaling as NNH_ACT_I8 (same buffer layout, plus
+ *     BF16 operands), with which 17 or more vectors run on the BF16 matrix
+ *     unit exactly: q_x 2^E and every weight quant are BF16 values, so each
+ *     block dot comes out of the MFMA exact and the scaling costs one FMA
+ *     per output and block. No counterpart in the reference, which never
+ *     quantizes activations; an extension of the int8 path for prefill. */
 enum {
     NNH_ACT_F32 = 0,
-    NNH_ACT_I8 = 1
+    NNH_ACT_I8 = 1,
+    NNH_ACT_MXI8 = 2
 };
 
 typedef struct nnh_weight nnh_weight;
@@ -218,6 +229,19 @@ int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_
  * small matrices keep split-K partial sums in the library's scratch buffer:
  * calls on different streams must not overlap. */
 int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream);
+
+/* The same for either int8 mode (act = NNH_ACT_I8 or NNH_ACT_MXI8): the
+ * buffer's layout (the MXI8 buffer is the NNH_ACT_I8 layout followed by the
+ * GEMM's BF16 operands xb[n_tok][cols] = q 2^E and xl[P][nbp8][2] = the two
+ * BF16 limbs of 2^E sum(q) per block, nbp8 = cols/32 rounded up to a
+ * multiple of 8), the quantizer, and y = W x from a quantized buffer. The
+ * act-less functions above are these with NNH_ACT_I8. No counterpart in the
+ * reference (see NNH_ACT_MXI8). */
+int nnh_act_layout_ex(int act, size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes);
+int nnh_quantize_act_ex_dev(int act, const float* x, size_t x_stride, size_t cols, size_t n_tok, void* buf,
+                            void* stream);
+int nnh_gemv_act_dev(const nnh_weight* w, int act, const void* buf, size_t n_tok, float* y, size_t y_stride,
+                     void* stream);
 
 /* Diagnostics: the exact int32 block dot products P[n][r][b] =
  * sum_k q_w[r, 32b+k] * q_x[n, 32b+k] (device output, rows*cols/32 per

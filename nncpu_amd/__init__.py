@@ -15,7 +15,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (NNH_ACT_F32, NNH_ACT_I8, NNH_BF16, NNH_Q4S, NNH_Q8_0, DeviceOutOfMemory, InvalidArgument,
+from ._lib import (NNH_ACT_F32, NNH_ACT_I8, NNH_ACT_MXI8, NNH_BF16, NNH_Q4S, NNH_Q8_0, DeviceOutOfMemory, InvalidArgument,
                    NnhError, build, check, declared_functions, lib)
 
 Q8_0 = NNH_Q8_0
@@ -23,10 +23,12 @@ Q4S = NNH_Q4S
 BF16 = NNH_BF16
 ACT_F32 = NNH_ACT_F32
 ACT_I8 = NNH_ACT_I8
+ACT_MXI8 = NNH_ACT_MXI8
 
 __all__ = [
-    "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
+    "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "ACT_MXI8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
     "gemv_batch_dev", "model_argmax_dev", "model_argmax_work_bytes", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
+    "act_layout_ex", "quantize_act_ex_dev", "gemv_act_dev",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
 
@@ -207,6 +209,22 @@ def act_layout(cols: int, n_tok: int) -> tuple[int, int, int]:
     a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
     check(lib().nnh_act_layout(cols, n_tok, C.byref(a), C.byref(b), C.byref(c)))
     return a.value, b.value, c.value
+
+
+def act_layout_ex(act: int, cols: int, n_tok: int) -> tuple[int, int, int]:
+    """act_layout for either int8 mode (ACT_I8, ACT_MXI8)."""
+    a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    check(lib().nnh_act_layout_ex(act, cols, n_tok, C.byref(a), C.byref(b), C.byref(c)))
+    return a.value, b.value, c.value
+
+
+def quantize_act_ex_dev(act: int, x_ptr: int, x_stride: int, cols: int, n_tok: int, buf_ptr: int,
+                        stream: int = 0) -> None:
+    check(lib().nnh_quantize_act_ex_dev(act, x_ptr, x_stride, cols, n_tok, buf_ptr, stream or None))
+
+
+def gemv_act_dev(w: Weight, act: int, buf_ptr: int, n_tok: int, y_ptr: int, y_stride: int, stream: int = 0) -> None:
+    check(lib().nnh_gemv_act_dev(w.handle, act, buf_ptr, n_tok, y_ptr, y_stride, stream or None))
 
 
 def quantize_act_dev(x_ptr: int, x_stride: int, cols: int, n_tok: int, act_ptr: int, stream: int = 0) -> None:

@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "nncpu_hip.h")
 
 NNH_OK, NNH_E_INVALID, NNH_E_OOM, NNH_E_DEVICE, NNH_E_STATE = 0, 1, 2, 3, 4
 NNH_Q8_0, NNH_Q4S, NNH_BF16 = 1, 2, 3
-NNH_ACT_F32, NNH_ACT_I8 = 0, 1
+NNH_ACT_F32, NNH_ACT_I8, NNH_ACT_MXI8 = 0, 1, 2
 
 
 class NnhError(RuntimeError):
@@ -82,6 +82,9 @@ def _declare(L):
     L.nnh_act_layout.argtypes, L.nnh_act_layout.restype = [sz, sz, P(sz), P(sz), P(sz)], i32
     L.nnh_quantize_act_dev.argtypes, L.nnh_quantize_act_dev.restype = [vp, sz, sz, sz, vp, vp], i32
     L.nnh_gemv_i8_dev.argtypes, L.nnh_gemv_i8_dev.restype = [vp, vp, sz, vp, sz, vp], i32
+    L.nnh_act_layout_ex.argtypes, L.nnh_act_layout_ex.restype = [i32, sz, sz, P(sz), P(sz), P(sz)], i32
+    L.nnh_quantize_act_ex_dev.argtypes, L.nnh_quantize_act_ex_dev.restype = [i32, vp, sz, sz, sz, vp, vp], i32
+    L.nnh_gemv_act_dev.argtypes, L.nnh_gemv_act_dev.restype = [vp, i32, vp, sz, vp, sz, vp], i32
     L.nnh_block_dots_dev.argtypes, L.nnh_block_dots_dev.restype = [vp, vp, sz, vp, vp], i32
     L.nnh_sync.argtypes, L.nnh_sync.restype = [vp], i32
     L.nnh_weight_device_data.argtypes, L.nnh_weight_device_data.restype = [vp], vp

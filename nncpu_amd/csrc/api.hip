@@ -29,6 +29,8 @@ struct nnh_weight {
     float* swT;           // device: [nb][rows padded] f32 scales, Q4 biases after (MFMA GEMM)
     int bpath;            // BF16 only: the reference kernel this shape takes (nnh::BF16_PATH_*)
     uint16_t* bl;         // device: BF16 only, the chain layout (none on the f64 path)
+    uint16_t* wbf;        // device: BF16 copies of the quants, rows padded (MX GEMM)
+    uint16_t* wbi;        // device: Q4 biases twice per block, rows padded (MX GEMM)
 };
 
 namespace {
@@ -116,19 +118,38 @@ int pinned_locked(size_t bytes, uint8_t** out) {
 }
 
 struct ActLayout {
-    size_t off_s, off_sx, off_sxT, bytes;
+    size_t off_s, off_sx, off_sxT, off_xb, off_xl, bytes;
 };
 
 // q[n_tok][cols] i8, s[n_tok][nb] bf16, sx[n_tok][nb][2] f64, then the
-// GEMM's block-major copies sxT[2][nb][tok_pad] f32.
-ActLayout act_layout(size_t cols, size_t n_tok) {
+// GEMM's block-major copies sxT[2][nb][tok_pad] f32; MX adds the BF16
+// operands of its GEMM, xb[n_tok][cols] and xl[tok_pad][nbp8][2].
+ActLayout act_layout(size_t cols, size_t n_tok, int act = NNH_ACT_I8) {
     size_t nb = cols / 32;
     ActLayout l;
     l.off_s = align_up(n_tok * cols);
     l.off_sx = l.off_s + align_up(n_tok * nb * 2);
     l.off_sxT = l.off_sx + align_up(n_tok * nb * 16);
-    l.bytes = l.off_sxT + align_up(2 * nb * (size_t)nnh::gemm_tok_pad((int)n_tok) * 4);
+    l.off_xb = l.off_sxT + align_up(2 * nb * (size_t)nnh::gemm_tok_pad((int)n_tok) * 4);
+    l.off_xl = l.off_xb;
+    l.bytes = l.off_xb;
+    if (act == NNH_ACT_MXI8) {
+        l.off_xl = l.off_xb + align_up(n_tok * cols * 2);
+        l.bytes = l.off_xl + align_up(nnh::mx_xl_bytes((int)n_tok, (int)nb));
+    }
     return l;
+}
+
+void launch_quantize(int act, const float* x, size_t x_stride, size_t cols, size_t n_tok, uint8_t* a,
+                     hipStream_t st) {
+    const ActLayout l = act_layout(cols, n_tok, act);
+    if (act == NNH_ACT_MXI8)
+        nnh::launch_quantize_mx(x, x_stride, (int)cols, (int)n_tok, (int8_t*)a, (uint16_t*)(a + l.off_s),
+                                (double*)(a + l.off_sx), (float*)(a + l.off_sxT), nnh::gemm_tok_pad((int)n_tok),
+                                (uint16_t*)(a + l.off_xb), (uint16_t*)(a + l.off_xl), st);
+    else
+        nnh::launch_quantize_act(x, x_stride, (int)cols, (int)n_tok, (int8_t*)a, (uint16_t*)(a + l.off_s),
+                                 (double*)(a + l.off_sx), (float*)(a + l.off_sxT), nnh::gemm_tok_pad((int)n_tok), st);
 }
 
 int check_weight(const nnh_weight* w) {
@@ -145,19 +166,28 @@ constexpr size_t SKINNY_MIN_TOKENS = 4;
 constexpr size_t GEMM_MIN_TOKENS = 17;
 
 // Device workspace the int8 matmul needs beyond the activation buffer.
-size_t i8_workspace_bytes(const nnh_weight* w, size_t n_tok) {
+size_t i8_workspace_bytes(const nnh_weight* w, size_t n_tok, int act) {
+    if (n_tok >= GEMM_MIN_TOKENS && act == NNH_ACT_MXI8)
+        return nnh::gemm_mx_workspace_bytes((int)w->rows, (int)w->nb, (int)n_tok);
     if (n_tok >= GEMM_MIN_TOKENS) return nnh::gemm_workspace_bytes((int)w->rows, (int)w->nb, (int)n_tok);
     if (n_tok >= SKINNY_MIN_TOKENS) return nnh::skinny_workspace_bytes((int)w->rows, (int)w->nb);
     return 0;
 }
 
-void launch_i8(const nnh_weight* w, const uint8_t* act, size_t n_tok, float* y, size_t y_stride, uint8_t* ws,
-               hipStream_t st) {
-    const ActLayout l = act_layout(w->cols, n_tok);
+// `mode`: NNH_ACT_I8 or NNH_ACT_MXI8, the quantizer `act` came from. Both
+// buffers start with the same q / s / sx / sxT, so every kernel but the MX
+// GEMM reads either.
+void launch_i8(const nnh_weight* w, int mode, const uint8_t* act, size_t n_tok, float* y, size_t y_stride,
+               uint8_t* ws, hipStream_t st) {
+    const ActLayout l = act_layout(w->cols, n_tok, mode);
     const int8_t* q = (const int8_t*)act;
     const double* sx = (const double*)(act + l.off_sx);
     const float* sxT = (const float*)(act + l.off_sxT);
-    if (n_tok >= GEMM_MIN_TOKENS)
+    if (n_tok >= GEMM_MIN_TOKENS && mode == NNH_ACT_MXI8)
+        nnh::launch_gemm_mx(w->dtype, w->wbf, w->swT, w->wbi, (const uint16_t*)(act + l.off_xb),
+                            (const uint16_t*)(act + l.off_xl), (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride,
+                            (float*)ws, st);
+    else if (n_tok >= GEMM_MIN_TOKENS)
         nnh::launch_gemm_i8(w->dtype, w->qs, w->swT, q, sxT, (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride,
                             (double*)ws, st);
     else if (n_tok >= SKINNY_MIN_TOKENS)
@@ -180,11 +210,9 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
                              y, y_stride, w->f32v2, st);
     } else {
-        const ActLayout l = act_layout(w->cols, n_tok);
-        nnh::launch_quantize_act(x, x_stride, (int)w->cols, (int)n_tok, (int8_t*)scratch, (uint16_t*)(scratch + l.off_s),
-                                 (double*)(scratch + l.off_sx), (float*)(scratch + l.off_sxT),
-                                 nnh::gemm_tok_pad((int)n_tok), st);
-        launch_i8(w, scratch, n_tok, y, y_stride, scratch + l.bytes, st);
+        const ActLayout l = act_layout(w->cols, n_tok, act);
+        launch_quantize(act, x, x_stride, w->cols, n_tok, scratch, st);
+        launch_i8(w, act, scratch, n_tok, y, y_stride, scratch + l.bytes, st);
     }
     NNH_HIP(hipGetLastError());
     return NNH_OK;
@@ -226,17 +254,20 @@ size_t argmax_work_bytes(const nnh_weight* w, int act) {
 size_t gemv_scratch_bytes(const nnh_weight* w, size_t n_tok, int act) {
     if (w->dtype == NNH_BF16) return 0;
     if (act == NNH_ACT_F32) return w->dtype == NNH_Q4S ? align_up(n_tok * w->nb * 4) : 0;
-    return act_layout(w->cols, n_tok).bytes + i8_workspace_bytes(w, n_tok);
+    return act_layout(w->cols, n_tok, act).bytes + i8_workspace_bytes(w, n_tok, act);
 }
 
 int check_call(const nnh_weight* w, size_t x_stride, size_t y_stride, size_t n_tok, int act) {
     int rc = check_weight(w);
     if (rc) return rc;
-    if (act != NNH_ACT_F32 && act != NNH_ACT_I8) return fail(NNH_E_INVALID, "unknown activation mode");
+    if (act != NNH_ACT_F32 && act != NNH_ACT_I8 && act != NNH_ACT_MXI8)
+        return fail(NNH_E_INVALID, "unknown activation mode");
     if (w->dtype == NNH_BF16 && act != NNH_ACT_F32)
         return fail(NNH_E_INVALID, "BF16 weights take f32 activations (the int8 path is for Q8_0 / Q4)");
     if (n_tok > 1 && y_stride < w->rows) return fail(NNH_E_INVALID, "gemv batch: y_stride < rows");
     if (n_tok > (size_t)1 << 20) return fail(NNH_E_INVALID, "gemv batch: too many vectors");
+    if (act != NNH_ACT_F32 && n_tok * w->cols >= ((size_t)1 << 30))
+        return fail(NNH_E_INVALID, "gemv batch: activations too large for the int8 path (n_tok * cols >= 2^30)");
     (void)x_stride;
     return NNH_OK;
 }
@@ -263,6 +294,8 @@ void release(nnh_weight* w) {
     if (w->sb) (void)hipFree(w->sb);
     if (w->swT) (void)hipFree(w->swT);
     if (w->bl) (void)hipFree(w->bl);
+    if (w->wbf) (void)hipFree(w->wbf);
+    if (w->wbi) (void)hipFree(w->wbi);
     delete w;
 }
 
@@ -310,8 +343,13 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
             hipSuccess ||
         (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
         (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||
-        (e = hipMalloc((void**)&w->swT, align_up((size_t)nnh::gemm_rows_pad((int)rows) * nb * 4 *
-                                                  (dtype == NNH_Q4S ? 2 : 1)))) != hipSuccess) {
+        // swT: Q8 one spare block row (the MX GEMM loads scales in pairs of
+        // blocks); for Q4 the bias table follows the scales.
+        (e = hipMalloc((void**)&w->swT, align_up((size_t)nnh::gemm_rows_pad((int)rows) * 4 *
+                                                  (dtype == NNH_Q4S ? 2 * nb : nb + 1)))) != hipSuccess ||
+        (e = hipMalloc((void**)&w->wbf, align_up(nnh::mx_weight_bytes((int)rows, (int)nb)))) != hipSuccess ||
+        (dtype == NNH_Q4S &&
+         (e = hipMalloc((void**)&w->wbi, align_up(nnh::mx_bias_bytes((int)rows, (int)nb)))) != hipSuccess)) {
         release(w);
         return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE, std::string("weight alloc: ") + hipGetErrorString(e));
     }
@@ -335,6 +373,7 @@ int finalize_weight(nnh_weight* w) {
                              g_stream);
     if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
     nnh::launch_gemm_scales(w->sc, w->bi, w->swT, (int)w->rows, (int)w->nb, g_stream);
+    nnh::launch_mx_weights(w->dtype, w->qs, w->bi, (int)w->rows, (int)w->nb, w->wbf, w->wbi, g_stream);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
         return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
@@ -640,46 +679,58 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
     return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
 }
 
-int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes) {
+int nnh_act_layout_ex(int act, size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes) {
+    if (act != NNH_ACT_I8 && act != NNH_ACT_MXI8) return fail(NNH_E_INVALID, "act layout: not an int8 mode");
     if (cols % 32 != 0) return fail(NNH_E_INVALID, "act layout: cols is not a multiple of 32");
-    ActLayout l = act_layout(cols, n_tok);
+    ActLayout l = act_layout(cols, n_tok, act);
     if (off_s) *off_s = l.off_s;
     if (off_sx) *off_sx = l.off_sx;
     if (bytes) *bytes = l.bytes;
     return NNH_OK;
 }
 
-int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream) {
+int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes) {
+    return nnh_act_layout_ex(NNH_ACT_I8, cols, n_tok, off_s, off_sx, bytes);
+}
+
+int nnh_quantize_act_ex_dev(int act, const float* x, size_t x_stride, size_t cols, size_t n_tok, void* buf,
+                            void* stream) {
     std::lock_guard<std::mutex> g(g_mu);
     int rc = ensure_locked();
     if (rc) return rc;
+    if (act != NNH_ACT_I8 && act != NNH_ACT_MXI8) return fail(NNH_E_INVALID, "quantize: not an int8 mode");
     if (cols == 0 || cols % 32 != 0) return fail(NNH_E_INVALID, "quantize: cols is not a positive multiple of 32");
     if (n_tok == 0) return NNH_OK;
-    if (!x || !act) return fail(NNH_E_INVALID, "quantize: null pointer");
-    if (cols >= ((size_t)1 << 31) || n_tok * (cols / 32) >= ((size_t)1 << 31))
-        return fail(NNH_E_INVALID, "quantize: too large");
-    ActLayout l = act_layout(cols, n_tok);
-    uint8_t* a = (uint8_t*)act;
-    nnh::launch_quantize_act(x, n_tok > 1 ? x_stride : cols, (int)cols, (int)n_tok, (int8_t*)a,
-                             (uint16_t*)(a + l.off_s), (double*)(a + l.off_sx), (float*)(a + l.off_sxT),
-                             nnh::gemm_tok_pad((int)n_tok), (hipStream_t)stream);
+    if (!x || !buf) return fail(NNH_E_INVALID, "quantize: null pointer");
+    if (cols >= ((size_t)1 << 31) || n_tok * cols >= ((size_t)1 << 30)) return fail(NNH_E_INVALID, "quantize: too large");
+    launch_quantize(act, x, n_tok > 1 ? x_stride : cols, cols, n_tok, (uint8_t*)buf, (hipStream_t)stream);
+    NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream) {
+    return nnh_quantize_act_ex_dev(NNH_ACT_I8, x, x_stride, cols, n_tok, act, stream);
+}
+
+int nnh_gemv_act_dev(const nnh_weight* w, int act, const void* buf, size_t n_tok, float* y, size_t y_stride,
+                     void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if (act != NNH_ACT_I8 && act != NNH_ACT_MXI8) return fail(NNH_E_INVALID, "gemv_act: not an int8 mode");
+    if ((rc = check_call(w, 0, y_stride, n_tok, act))) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!buf || !y) return fail(NNH_E_INVALID, "gemv_act: null pointer");
+    uint8_t* ws = nullptr;
+    const size_t wsb = i8_workspace_bytes(w, n_tok, act);
+    if (wsb && (rc = scratch_locked(wsb, &ws))) return rc;
+    launch_i8(w, act, (const uint8_t*)buf, n_tok, y, n_tok > 1 ? y_stride : w->rows, ws, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;
 }
 
 int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream) {
-    std::lock_guard<std::mutex> g(g_mu);
-    int rc = ensure_locked();
-    if (rc) return rc;
-    if ((rc = check_call(w, 0, y_stride, n_tok, NNH_ACT_I8))) return rc;
-    if (n_tok == 0) return NNH_OK;
-    if (!act || !y) return fail(NNH_E_INVALID, "gemv_i8: null pointer");
-    uint8_t* ws = nullptr;
-    const size_t wsb = i8_workspace_bytes(w, n_tok);
-    if (wsb && (rc = scratch_locked(wsb, &ws))) return rc;
-    launch_i8(w, (const uint8_t*)act, n_tok, y, n_tok > 1 ? y_stride : w->rows, ws, (hipStream_t)stream);
-    NNH_HIP(hipGetLastError());
-    return NNH_OK;
+    return nnh_gemv_act_dev(w, NNH_ACT_I8, act, n_tok, y, y_stride, stream);
 }
 
 int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32_t* P, void* stream) {

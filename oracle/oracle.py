@@ -175,6 +175,14 @@ class QMatrix:
                      buf[n // 2 + n // 16:n // 2 + n // 8].view(np.uint16))
         return QMatrix(dtype, rows, cols, parts)
 
+    def dequant_quants(self) -> np.ndarray:
+        """The integer quants in element order, [rows][cols] (Q4: byte i of a
+        block holds element i low, element i + 16 high; runtime.rs:58-62)."""
+        if self.dtype == Q8_0:
+            return self.parts[0].astype(np.int32).reshape(self.rows, self.cols)
+        blk = self.parts[0].reshape(-1, 16)
+        return np.concatenate([blk & 15, blk >> 4], axis=1).astype(np.int32).reshape(self.rows, self.cols)
+
     def dequant(self) -> np.ndarray:
         """f32 weights the kernels multiply by (kernels/tests.rs:380-397)."""
         if self.dtype == Q8_0:
@@ -270,6 +278,76 @@ def gemv_bf16_argmax(w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> int:
 def quantize_act(x: np.ndarray):
     """The int8-block activation quantizer: nncpu's own Q8_0 encoder on x."""
     return quantize_q8_0(x)
+
+
+def mx_exponent(amax: np.ndarray) -> np.ndarray:
+    """Exponent of the MX block scale (the library's NNH_ACT_MXI8; no
+    counterpart in nncpu, which never quantizes activations): the least E
+    with 127 * 2^E >= amax, clamped to [-126, 127], read off the f32 bits.
+    amax = (1 + f) 2^e: 127 * 2^(e-6) = 1.984375 * 2^e covers it unless
+    f > 0.984375 (mantissa field above 0x7E0000). Pinned against a direct
+    search over E by tests/test_mx.py."""
+    u = np.ascontiguousarray(amax, np.float32).view(np.uint32).astype(np.int64)
+    be = u >> 23
+    e = be - 127 - 6 + ((u & 0x7FFFFF) > 0x7E0000)
+    e = np.where(be == 0, -126, e)
+    return np.clip(e, -126, 127)
+
+
+def quantize_act_mx(x: np.ndarray):
+    """MX int8 activation blocks: per block of 32, scale 2^E (mx_exponent of
+    the block's largest |x|, NaNs skipped), q = rint(x / 2^E) ties to even,
+    NaN -> 0, clamped to +-127; an all-zero (or all-NaN) block gets scale 0
+    and q = 0. Returns (q int8, scales as BF16 bits)."""
+    xb = np.ascontiguousarray(x, np.float32).reshape(-1, 32)
+    a = np.abs(xb)
+    a = np.where(np.isnan(a), np.float32(0), a)
+    amax = a.max(axis=1)
+    E = mx_exponent(amax)
+    zero = ~(amax > 0)
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = np.ldexp(xb.astype(np.float64), -E[:, None])  # exact: a power-of-two scaling
+        r = np.rint(v)
+    r = np.where(np.isnan(r), 0.0, r)
+    q = np.clip(r, -127, 127).astype(np.int8)
+    q[zero] = 0
+    scale = np.where(zero, np.float32(0), np.ldexp(np.float32(1), E).astype(np.float32)).astype(np.float32)
+    return q.reshape(-1), (scale.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def mx_limbs(X: np.ndarray):
+    """X = hi + lo as two BF16 values: hi = X's top 8 significant bits (its f32
+    bits with the low half cleared), lo = X - hi (exact for X of at most 16
+    significant bits). Returns both as BF16 bits."""
+    X = np.ascontiguousarray(X, np.float32)
+    hb = X.view(np.uint32) & np.uint32(0xFFFF0000)
+    lo = (X - hb.view(np.float32)).astype(np.float32)
+    return (hb >> 16).astype(np.uint16), (lo.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def gemm_exact(m: "QMatrix", qx: np.ndarray, sx: np.ndarray, n_tok: int):
+    """Batched restatement of or_gemv_i8_exact in numpy for many vectors:
+    y[t][r] = sum_b s_w[r,b] s_x[t,b] P_b[t][r] (+ Q4: bias[r,b] s_x[t,b]
+    sum_k q_x[t,32b+k]), each block term exact in f64 (integer block dots by
+    f64 matmuls of integers below 2^53), summed in f64. Returns (y as f64,
+    sum of |terms| as f64), both [n_tok][rows]."""
+    rows, cols = m.rows, m.cols
+    nb = cols // 32
+    wq = m.dequant_quants().astype(np.float64).reshape(rows, nb, 32)
+    sw = bf16_array_to_f32(m.parts[1]).astype(np.float64).reshape(rows, nb)
+    q = np.asarray(qx, np.int8).astype(np.float64).reshape(n_tok, nb, 32)
+    s = bf16_array_to_f32(np.asarray(sx, np.uint16)).astype(np.float64).reshape(n_tok, nb)
+    y = np.zeros((n_tok, rows))
+    mag = np.zeros((n_tok, rows))
+    for b in range(nb):
+        P = q[:, b, :] @ wq[:, b, :].T  # exact integers
+        t = P * (s[:, b][:, None] * sw[:, b][None, :])
+        if m.dtype == Q4S:
+            bi = bf16_array_to_f32(m.parts[2]).astype(np.float64).reshape(rows, nb)
+            t = t + (s[:, b] * q[:, b, :].sum(axis=1))[:, None] * bi[:, b][None, :]
+        y += t
+        mag += np.abs(t)
+    return y, mag
 
 
 def dequant_act(qx: np.ndarray, sx: np.ndarray) -> np.ndarray:
