@@ -235,14 +235,15 @@ def measure_cases(args, N, cases, act_mode, label):
     return out
 
 
-def qwen_prefill(args, N, dtype: int, n_tok: int = 512, n_layer: int = 28):
+def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int = 28):
     """BASELINE configs[4], end to end: a Qwen2.5-7B-shaped model (d 3584,
     FFN 18944, 28 query / 4 KV heads of 128, RoPE base 1e6, RMSNorm, SwiGLU,
     q/k/v biases) with random weights 0.02*N(0,1) encoded by the library's
     device encoder (nncpu Q8_0 / Q4), prefilling 512 tokens of random
     embeddings through all 28 layers and the last token's lm_head row
-    (152064 x 3584). Every weight matmul is the library's int8 path
-    (activations quantized on the device, MFMA GEMM); q/k/v and gate/up are
+    (152064 x 3584). Every weight matmul is the library's int8 path in mode
+    `act` (activations quantized on the device: nncpu's Q8_0 encoder and the
+    int8 MFMA GEMM, or MX blocks and the BF16-MFMA GEMM); q/k/v and gate/up are
     uploaded as one concatenated matrix each, as serving engines load them.
     The rest of the layer (norms, RoPE, causal GQA attention, SiLU) is torch
     float32 on the GPU: harness, not the measured path. One step = one full
@@ -283,7 +284,7 @@ def qwen_prefill(args, N, dtype: int, n_tok: int = 512, n_layer: int = 28):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(st.s)
-        N.gemv_batch_dev(w, x.data_ptr(), x.shape[1], y.data_ptr(), rows, x.shape[0], N.ACT_I8, st.handle)
+        N.gemv_batch_dev(w, x.data_ptr(), x.shape[1], y.data_ptr(), rows, x.shape[0], act, st.handle)
         e1.record(st.s)
         mm_events.append((e0, e1))
         return y
@@ -333,6 +334,7 @@ def qwen_prefill(args, N, dtype: int, n_tok: int = 512, n_layer: int = 28):
     ops = n_layer * per_layer + 2 * d * vocab
     assert torch.isfinite(logits).all()
     res = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} Qwen2.5-7B-shaped prefill, {n_layer} layers, {n_tok} tokens",
+               activations="MX int8 blocks (power-of-two scales)" if act == N.ACT_MXI8 else "int8 blocks (nncpu Q8_0)",
                ms=round(ms, 3), tokens_per_s=round(n_tok / ms * 1e3, 1), matmul_ms=round(mm_ms, 3),
                matmul_tops=round(ops / mm_ms / 1e9, 1), steps=steps)
     log(f"qwen_prefill: {res}")
@@ -456,7 +458,7 @@ def main():
         extra["prefill_m512"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
                                               N.ACT_I8, "prefill")
     if args.workload in ("qwen_prefill", "all"):
-        extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d) for d in (1, 2)]
+        extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d, a) for d in (1, 2) for a in (N.ACT_MXI8, N.ACT_I8)]
     if args.workload in ("q8_vocab", "all"):
         extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
     if args.workload in ("verify", "all"):

@@ -29,13 +29,16 @@
 // one rounding per fold of its exact value; split tiles' partial totals are
 // added in f64 and rounded once.
 //
-// Work split (stream-K): the output is cut into 128-row x 256-token tiles
-// and K into groups of 8 blocks. A "team" of workgroups, one per token tile,
-// walks a contiguous range of (row tile, group) units in the same order, so
-// the team shares every weight stage through the L2 of its XCD. Ranges are
-// equal, so every workgroup gets the same work; a tile whose groups span two
-// teams' ranges gets f64 partial tiles in a workspace, added in team order by
-// gemm_mx_fixup_kernel (deterministic).
+// Work split: the output is cut into 128-row x 256-token tiles and K into
+// groups of 8 blocks. A "team" of workgroups, one per token tile, walks the
+// same (row tile, group) units in the same order, so the team shares every
+// weight stage through the L2 of its XCD. Whole row tiles go round-robin to
+// the teams first (data-parallel rounds: every team at the same K group at
+// about the same time, so the activations are shared in L2 too); the
+// remaining row tiles' units are split evenly over the teams (stream-K), and
+// a tile whose groups span two teams' shares gets partial tiles in a
+// workspace, added in team order in f64 by gemm_mx_fixup_kernel
+// (deterministic).
 //
 // Workgroup: 8 waves (2 per SIMD), wave (wm, wn) owns tokens 64 wm .. +63
 // and rows 64 wn .. +63: 2 x 2 tiles of 32 x 32, each operand read from LDS
@@ -215,7 +218,8 @@ struct MxArgs {
     float* y;
     size_t y_stride, cols;
     int rows, rows_pad, nb, nbp8, ng, n_tok, mtiles, teams, rtiles;
-    long units;  // row tiles x groups
+    int rounds;  // whole row tiles per team (data-parallel rounds): team t takes row tiles t, t + teams, ..
+    long tail;   // the remaining (rtiles - rounds * teams) row tiles' units, split evenly over the teams
 };
 
 __device__ __forceinline__ long team_start(long team, long units, int teams) { return team * units / teams; }
@@ -399,15 +403,35 @@ __device__ __forceinline__ void mx_store(const MxArgs& g, MxTiles& tot, bool who
             for (int r = 0; r < 16; ++r) tot[ti][ri][r] = 0.0f;
 }
 
+// A team's units: its data-parallel row tiles (team, team + teams, .., each
+// over all its groups), then its share of the tail, a contiguous range of
+// the remaining row tiles' units that may start and end inside a tile.
+struct MxCursor {
+    int k, rt, gi;  // unit index within the team's work, its row tile and group
+};
+
 struct MxLoop {
     int nst;           // stages: 4 per unit
-    int rt0, gi0;      // the first unit's row tile and group
-    int crt, cgi;      // compute cursor: the group of the stage being computed
-    int irt, igi;      // issue cursor: the group of the stage being issued
+    int nk, dp;        // the team's units, of them data-parallel
+    int trt, tgi;      // the first tail unit's row tile and group
+    MxCursor cc, ic;   // compute cursor (the stage being computed), issue cursor (the stage being issued)
+    int seg_k0, seg_gi0;  // unit index and group the current segment began at
     int lid, wave, lane, c, h, rw, rm, m0;
     int chunk;         // groups in the current f32 chunk
     MxLane o;
 };
+
+__device__ __forceinline__ void mx_advance(MxCursor& c, const MxLoop& L, const MxArgs& g) {
+    ++c.k;
+    ++c.gi;
+    if (c.k == L.dp) {  // the data-parallel tiles are done: the tail share
+        c.rt = L.trt;
+        c.gi = L.tgi;
+    } else if (c.gi == g.ng) {
+        c.gi = 0;
+        c.rt += c.k < L.dp ? g.teams : 1;
+    }
+}
 
 // One step of the ring of three buffers: stage s (J = s % 4) is in `cur`;
 // stage s + 2 goes into `nxt`, the buffer stage s - 1 was computed from.
@@ -424,15 +448,10 @@ __device__ __forceinline__ void mx_step(MxStage& cur, MxStage& nxt, MxBias& bias
     // loads still in flight; the memory clobber keeps the LDS reads after it).
     asm volatile("s_barrier" ::: "memory");
     if (s + 2 < L.nst) {
-        if (J == 2) {  // stage s + 2 opens the next group
-            if (++L.igi == g.ng) {
-                L.igi = 0;
-                ++L.irt;
-            }
-        }
-        mx_issue<DT>(nxt, bias, g, L.o, L.irt, L.igi, (J + 2) & 3, L.wave, L.m0);
+        if (J == 2) mx_advance(L.ic, L, g);  // stage s + 2 opens the next group
+        mx_issue<DT>(nxt, bias, g, L.o, L.ic.rt, L.ic.gi, (J + 2) & 3, L.wave, L.m0);
     }
-    const int nblk = g.nb - (L.cgi * MX_GRP + J * MX_KS);
+    const int nblk = g.nb - (L.cc.gi * MX_GRP + J * MX_KS);
     mx_compute(cur, nblk, L.rw, L.rm, L.c, L.h, acc);
     if (J != 3) return;
     if (DT == 2) {
@@ -448,7 +467,7 @@ __device__ __forceinline__ void mx_step(MxStage& cur, MxStage& nxt, MxBias& bias
             }
         }
     }
-    const bool seg_end = s + 1 == L.nst || L.cgi + 1 == g.ng;
+    const bool seg_end = s + 1 == L.nst || L.cc.gi + 1 == g.ng;
     if (++L.chunk == MX_FOLD_GROUPS || seg_end) {
 #pragma unroll
         for (int ti = 0; ti < 2; ++ti)
@@ -462,15 +481,16 @@ __device__ __forceinline__ void mx_step(MxStage& cur, MxStage& nxt, MxBias& bias
         L.chunk = 0;
     }
     if (seg_end) {
-        // The segment is whole iff it opened the tile; the WG's first
-        // segment goes to slot 0, its last (partial) one to slot 1.
-        const bool first = L.crt == L.rt0;
-        const bool whole = L.cgi + 1 == g.ng && (!first || L.gi0 == 0);
-        mx_store(g, tot, whole, first ? 0 : 1, L.lid, L.wave, L.lane, L.crt * MX_TN, L.m0, L.rw, L.rm, L.c, L.h);
+        // The segment is whole iff it spans its tile's groups; a partial one
+        // is the team's first tail segment (slot 0) or its last (slot 1).
+        const bool whole = L.seg_gi0 == 0 && L.cc.gi + 1 == g.ng;
+        mx_store(g, tot, whole, L.seg_k0 == L.dp ? 0 : 1, L.lid, L.wave, L.lane, L.cc.rt * MX_TN, L.m0, L.rw, L.rm,
+                 L.c, L.h);
     }
-    if (++L.cgi == g.ng) {
-        L.cgi = 0;
-        ++L.crt;
+    mx_advance(L.cc, L, g);
+    if (seg_end) {
+        L.seg_k0 = L.cc.k;
+        L.seg_gi0 = L.cc.gi;
     }
 }
 
@@ -495,12 +515,19 @@ __global__ __launch_bounds__(MX_NW * 64) void gemm_mx_kernel(MxArgs g) {
     L.lid = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
     const int team = L.lid / g.mtiles, mt = L.lid - team * g.mtiles;
     L.m0 = mt * MX_TM;
-    const long u0 = team_start(team, g.units, g.teams), u1 = team_start(team + 1, g.units, g.teams);
-    L.nst = (int)(u1 - u0) * MX_NS;
-    L.rt0 = (int)(u0 / g.ng);
-    L.gi0 = (int)(u0 - (long)L.rt0 * g.ng);
-    L.crt = L.irt = L.rt0;
-    L.cgi = L.igi = L.gi0;
+    const long t0 = team_start(team, g.tail, g.teams), t1 = team_start(team + 1, g.tail, g.teams);
+    const long ut = (long)g.rounds * g.teams * g.ng + t0;  // the first tail unit
+    L.dp = g.rounds * g.ng;
+    L.nk = L.dp + (int)(t1 - t0);
+    L.nst = L.nk * MX_NS;
+    L.trt = (int)(ut / g.ng);
+    L.tgi = (int)(ut - (long)L.trt * g.ng);
+    L.cc.k = 0;
+    L.cc.rt = L.dp > 0 ? team : L.trt;
+    L.cc.gi = L.dp > 0 ? 0 : L.tgi;
+    L.ic = L.cc;
+    L.seg_k0 = 0;
+    L.seg_gi0 = L.cc.gi;
     L.chunk = 0;
     L.o = mx_lane(g, L.wave, L.lane, L.m0);
 
@@ -517,8 +544,8 @@ __global__ __launch_bounds__(MX_NW * 64) void gemm_mx_kernel(MxArgs g) {
 
     // Stages 0 and 1 (the first group's blocks 0..3), then the ring: step
     // k of 12 computes buffer k % 3 and refills buffer (k + 2) % 3.
-    mx_issue<DT>(s0, bias, g, L.o, L.irt, L.igi, 0, L.wave, L.m0);
-    mx_issue<DT>(s1, bias, g, L.o, L.irt, L.igi, 1, L.wave, L.m0);
+    mx_issue<DT>(s0, bias, g, L.o, L.ic.rt, L.ic.gi, 0, L.wave, L.m0);
+    mx_issue<DT>(s1, bias, g, L.o, L.ic.rt, L.ic.gi, 1, L.wave, L.m0);
     for (int s = 0; s < L.nst; s += 12) {
         mx_step<DT, 0>(s0, s2, bias, g, L, s, acc, tot);
         mx_step<DT, 1>(s1, s0, bias, g, L, s + 1, acc, tot);
@@ -543,15 +570,16 @@ __device__ __forceinline__ int team_of(long u, long units, int teams) {
     return t;
 }
 
-// y of every tile split between teams = its partial tiles added in team
-// order, in f64, rounded once. One workgroup of 256 threads per (tile,
-// wave region); thread (tt, lane) takes MFMA tile tt = 2 ti + ri of that
-// wave's region, 16 results. Whole tiles exit at once.
+// y of every tail tile split between teams = its partial tiles added in
+// team order, in f64, rounded once. One workgroup of 256 threads per (tail
+// tile, wave region); thread (tt, lane) takes MFMA tile tt = 2 ti + ri of
+// that wave's region, 16 results. Whole tiles exit at once.
 __global__ __launch_bounds__(256) void gemm_mx_fixup_kernel(MxArgs g) {
     const int tile = blockIdx.x / MX_NW, wave = blockIdx.x % MX_NW;
-    const int rt = tile / g.mtiles, mt = tile - rt * g.mtiles;
-    const long ua = (long)rt * g.ng, ub = ua + g.ng;
-    const int t0 = team_of(ua, g.units, g.teams), t1 = team_of(ub - 1, g.units, g.teams);
+    const int tr = tile / g.mtiles, mt = tile - tr * g.mtiles;
+    const int rt = g.rounds * g.teams + tr;
+    const long ua = (long)tr * g.ng, ub = ua + g.ng;  // tail units of the tile
+    const int t0 = team_of(ua, g.tail, g.teams), t1 = team_of(ub - 1, g.tail, g.teams);
     if (t0 == t1) return;
     const int lane = threadIdx.x & 63, tt = threadIdx.x >> 6;
     const int ti = tt >> 1, ri = tt & 1, h = lane >> 5, c = lane & 31;
@@ -560,7 +588,9 @@ __global__ __launch_bounds__(256) void gemm_mx_fixup_kernel(MxArgs g) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sum[r] = 0.0;
     for (int tm = t0; tm <= t1; ++tm) {
-        const int slot = team_start(tm, g.units, g.teams) >= ua ? 0 : 1;
+        const long ts = team_start(tm, g.tail, g.teams);
+        if (team_start(tm + 1, g.tail, g.teams) == ts) continue;  // an empty tail share (tail < teams)
+        const int slot = ts >= ua ? 0 : 1;
         const int lid = tm * g.mtiles + mt;
         const float* p = g.ws + (((size_t)lid * 2 + slot) * MX_NW + wave) * 4096 + (size_t)tt * 1024 + lane;
         float v[16];
@@ -579,8 +609,8 @@ __global__ __launch_bounds__(256) void gemm_mx_fixup_kernel(MxArgs g) {
 }
 
 struct MxSched {
-    int mtiles, rtiles, ng, teams;
-    long units;
+    int mtiles, rtiles, ng, teams, rounds;
+    long units, tail;
 };
 
 MxSched mx_sched(int rows, int nb, int n_tok) {
@@ -593,6 +623,8 @@ MxSched mx_sched(int rows, int nb, int n_tok) {
     const long most = s.units / MX_MIN_UNITS;
     if (teams > most) teams = most;
     s.teams = teams < 1 ? 1 : (int)teams;
+    s.rounds = s.rtiles / s.teams;
+    s.tail = (long)(s.rtiles - s.rounds * s.teams) * s.ng;
     return s;
 }
 
@@ -652,16 +684,18 @@ void launch_gemm_mx(int dtype, const uint16_t* wbf, const float* swT, const uint
     g.mtiles = s.mtiles;
     g.teams = s.teams;
     g.rtiles = s.rtiles;
-    g.units = s.units;
+    g.rounds = s.rounds;
+    g.tail = s.tail;
     const dim3 grid(s.teams * s.mtiles), block(MX_NW * 64);
     if (dtype == 1)
         gemm_mx_kernel<1><<<grid, block, 0, st>>>(g);
     else
         gemm_mx_kernel<2><<<grid, block, 0, st>>>(g);
-    // Some tile is split iff some team's range starts inside a row tile.
+    // A tail tile is split iff some team's tail share starts inside it.
     bool split = false;
-    for (long t = 1; t < s.teams && !split; ++t) split = (t * s.units / s.teams) % s.ng != 0;
-    if (split) gemm_mx_fixup_kernel<<<s.rtiles * s.mtiles * MX_NW, 256, 0, st>>>(g);
+    for (long t = 1; t < s.teams && !split; ++t) split = (t * s.tail / s.teams) % s.ng != 0;
+    const int tail_tiles = s.rtiles - s.rounds * s.teams;
+    if (split) gemm_mx_fixup_kernel<<<tail_tiles * s.mtiles * MX_NW, 256, 0, st>>>(g);
 }
 
 }  // namespace nnh

@@ -180,6 +180,8 @@ def check_gemm(oracle, m, y, ys, x, xs, n_tok, sample_ref=True):
     (1536, 64, 2048),    # nb = 2, sixteen token tiles
     (4100, 1536, 300),   # ragged row tile, three token tiles
     (1536, 1536, 17),    # the smallest GEMM batch at a Gemma-4-E2B-like shape (config 4)
+    (18944, 3584, 512),  # Qwen2.5-7B gate/up, M = 512: a data-parallel round, then a stream-K tail
+    (18944, 512, 300),   # a tail of fewer units than teams: empty tail shares, tiles split in two
 ])
 def test_mx_gemm_exact_bound_and_tolerance(oracle, dtype, rows, cols, n_tok):
     say("mx gemm", dtype, rows, cols, n_tok)
