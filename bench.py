@@ -472,6 +472,11 @@ def main():
                                                 N.ACT_F32, "bf16")
     if args.workload in ("gemma_decode", "q4_sweep", "all"):
         extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
+    if args.workload == "q4_sweep":
+        # The metric's GEMM part: M = 512 prefill at the
+        # Qwen2.5-7B shapes, MX int8 activations, both weight formats.
+        extra["prefill_m512_mx"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
+                                                 N.ACT_MXI8, "prefill_mx")
     if args.workload not in ("q4_sweep", "all"):
         print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
         return

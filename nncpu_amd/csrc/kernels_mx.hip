@@ -220,6 +220,7 @@ struct MxArgs {
     int rows, rows_pad, nb, nbp8, ng, n_tok, mtiles, teams, rtiles;
     int rounds;  // whole row tiles per team (data-parallel rounds): team t takes row tiles t, t + teams, ..
     long tail;   // the remaining (rtiles - rounds * teams) row tiles' units, split evenly over the teams
+    long tail_q, tail_r;  // tail / teams, tail % teams
 };
 
 __device__ __forceinline__ long team_start(long team, long units, int teams) { return team * units / teams; }
@@ -587,17 +588,43 @@ __global__ __launch_bounds__(256) void gemm_mx_fixup_kernel(MxArgs g) {
     double sum[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sum[r] = 0.0;
-    for (int tm = t0; tm <= t1; ++tm) {
-        const long ts = team_start(tm, g.tail, g.teams);
-        if (team_start(tm + 1, g.tail, g.teams) == ts) continue;  // an empty tail share (tail < teams)
-        const int slot = ts >= ua ? 0 : 1;
-        const int lid = tm * g.mtiles + mt;
-        const float* p = g.ws + (((size_t)lid * 2 + slot) * MX_NW + wave) * 4096 + (size_t)tt * 1024 + lane;
-        float v[16];
+    // Partials are loaded 8 teams at a time before any is added (one round
+    // trip per 8, not per team), then added in team order. The teams' tail
+    // starts team_start(tm) = floor(tm tail / teams) are walked by quotient
+    // and remainder (no division per team).
+    constexpr int BATCH = 8;
+    long ts = team_start(t0, g.tail, g.teams);
+    long rem = (long)t0 * g.tail - ts * g.teams;
+    for (int tb = t0; tb <= t1; tb += BATCH) {
+        float v[BATCH][16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = p[r * 64];
+        for (int i = 0; i < BATCH; ++i) {
+            const int tm = tb + i;
+            long te = ts + g.tail_q;
+            long rn = rem + g.tail_r;
+            if (rn >= g.teams) {
+                ++te;
+                rn -= g.teams;
+            }
+            // Teams past t1 and empty tail shares (tail < teams) contribute
+            // nothing: they load team t0's slot (a valid address, so the
+            // load needs no branch) and the value is dropped by a select.
+            const bool use = tm <= t1 && te > ts;
+            const int slot = use && ts < ua ? 1 : 0;
+            const float* p = g.ws + (((size_t)(use ? tm : t0) * g.mtiles + mt) * 2 + (use ? slot : 0)) * MX_NW * 4096 +
+                             (size_t)wave * 4096 + (size_t)tt * 1024 + lane;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sum[r] += (double)v[r];
+            for (int r = 0; r < 16; ++r) {
+                const float x = p[r * 64];
+                v[i][r] = use ? x : 0.0f;
+            }
+            ts = te;
+            rem = rn;
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sum[r] += (double)v[i][r];
     }
     const int n = rt * MX_TN + rw + 32 * ri + c;
     if (n >= g.rows) return;
@@ -686,6 +713,8 @@ void launch_gemm_mx(int dtype, const uint16_t* wbf, const float* swT, const uint
     g.rtiles = s.rtiles;
     g.rounds = s.rounds;
     g.tail = s.tail;
+    g.tail_q = s.tail / s.teams;
+    g.tail_r = s.tail % s.teams;
     const dim3 grid(s.teams * s.mtiles), block(MX_NW * 64);
     if (dtype == 1)
         gemm_mx_kernel<1><<<grid, block, 0, st>>>(g);
