@@ -445,7 +445,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by rows across GPUs by design, see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the path shards by rows: each GPU a row slice of every matrix, then an all-gather of y)", file=sys.stderr)
         sys.exit(2)
     import torch
     import nncpu_amd as N
