@@ -259,3 +259,21 @@ def test_mx_argmax_and_model_gemv(oracle):
     exact = oracle.gemv_i8_exact(m, q, s)
     assert np.all(np.abs(y - exact) <= np.spacing(np.abs(exact)))
     assert N.model_argmax(w, x, act=N.ACT_MXI8) == oracle.argmax(y)
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_mx_gemm_edge_blocks(oracle, dtype):
+    # Activations with zero, NaN, subnormal, mantissa-boundary and ~1e30
+    # blocks (scales from 2^-126 to about 2^96, X limbs at both ends) through the
+    # BF16 GEMM: within the exact-sum bound like any other input.
+    rows, cols, n_tok = 200, 1152, 20
+    rng = oracle.Rng(0x4D5C + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = special_x(rng, n_tok, cols, cols)
+    for t in range(1, n_tok, 3):  # the edge blocks in other tokens too, shifted
+        x[t * cols:(t + 1) * cols] = np.roll(x[:cols], 32 * t)
+    y = np.zeros(n_tok * rows, np.float32)
+    N.gemv_batch(w, x, cols, y, rows, n_tok, N.ACT_MXI8)
+    assert np.all(np.isfinite(y))
+    check_gemm(oracle, m, y, rows, x, cols, n_tok, sample_ref=False)
