@@ -8,19 +8,28 @@ encoder). One step = one GEMV per shape. Inputs are resident in HBM; each
 shape cycles through enough uploaded weight copies (>= 512 MB, twice the
 MI355X Infinity Cache) that every launch streams its weights from HBM.
 
-value = algorithmic bytes of the timed steps / wall time between the two
-synchronised events (GB/s); bytes per GEMV = N*K/2 + N*K/16 (quants, BF16
-scales and biases) + 4K + 4N (f32 x in, f32 y out), the reference's own
-byte accounting plus the vectors.
+value = algorithmic bytes of exactly --steps timed steps / the time between
+two events on the launch stream, synchronised on both sides (GB/s); bytes
+per GEMV = N*K/2 + N*K/16 (quants, BF16 scales and biases) + 4K + 4N (f32 x
+in, f32 y out), the reference's own byte accounting plus the vectors.
 
-    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--workload q4_sweep]
+roofline: the same kernel timed per shape over a HIP graph of
+max(copies, 200, steps) launches, so every launch reads a copy no earlier
+launch of the graph has left in a cache and the graph's start-up is spread
+over many launches; achieved = mean algorithmic bytes / mean per-launch
+time. The measured peaks (calibration kernels, include/nncpu_calib.h) go
+beside the datasheet's.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload q4_sweep]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -31,12 +40,18 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 512 << 20
+MIN_LAUNCHES = 200
 
 Q4_SWEEP = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
-# HBM bytes per launch of the sweep's GEMVs, from rocprofv3 --pmc FETCH_SIZE
-# (x2.0, the factor a 64 MiB device copy gives) + WRITE_SIZE, in the order of
-# Q4_SWEEP; the runs are in profiles/gemv_i8_q4_llama3_8b_sweep.md.
+# Llama-3-8B's gate and up projections as one matrix: what a decode step
+# streams in one launch when the two are loaded concatenated.
+FUSED_GATE_UP = (28672, 4096)
+# HBM bytes per launch of the sweep's GEMVs, in the order of Q4_SWEEP: the
+# rocprofv3 --pmc FETCH_SIZE (scaled by 2.0, the factor a 64 MiB device copy
+# gives in the same run) + WRITE_SIZE readings of `bench.py --workload traffic`.
+TRAFFIC_SOURCE = "profiles/gemv_i8_q4_llama3_8b_sweep.md (rocprofv3 --pmc over bench.py --workload traffic)"
 Q4_SWEEP_TRAFFIC = [10_603_212, 2_713_600, 36_853_350, 36_929_126]
 Q8_VOCAB = [(262144, 1152), (151936, 3584)]
 
@@ -91,11 +106,12 @@ class Stream:
         return e
 
 
-def time_gemv_set(N, st, launches, steps, warmup):
-    """Run `launches` (a list of callables, one step) `warmup` times eagerly,
-    then capture `steps` steps in one HIP graph (host launch cost would
-    otherwise exceed these microsecond kernels) and time its replay between
-    two events on the launch stream, synchronised on both sides."""
+def time_graph(st, launches, reps, warmup):
+    """Run the step `launches` (a list of callables) `warmup` times eagerly,
+    capture `reps` steps in one HIP graph (host launch cost would otherwise
+    exceed these microsecond kernels), replay it once untimed (the first
+    replay uploads the graph) and time a second replay between two events on
+    the launch stream, synchronised on both sides. Returns seconds."""
     torch = st.torch
     for _ in range(warmup):
         for f in launches:
@@ -103,67 +119,113 @@ def time_gemv_set(N, st, launches, steps, warmup):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=st.s):
-        for _ in range(steps):
+        for _ in range(reps):
             for f in launches:
                 f()
     torch.cuda.synchronize()
-    g.replay()  # first replay uploads the graph
+    g.replay()
     torch.cuda.synchronize()
     e0 = st.event()
     with torch.cuda.stream(st.s):
         g.replay()
     e1 = st.event()
     torch.cuda.synchronize()
+    del g
     return e0.elapsed_time(e1) / 1e3
 
 
-def q4_sweep(args, N):
+def rotating(N, st, dtype, n, k, m, act, seed, rot_bytes=ROTATE_BYTES):
+    """A launch callable over >= rot_bytes of weight copies (each call takes
+    the next copy), its inputs resident in HBM. act: ACT_I8 / ACT_MXI8 launch
+    the int8 matmul on activations quantized beforehand (nncpu's Q8_0 encoder
+    / power-of-two MX blocks); ACT_F32 the bit-exact f32 path (Q4 block sums
+    included)."""
+    import torch
+    wb = weight_bytes(dtype, n, k)
+    copies = max(2, math.ceil(rot_bytes / wb))
+    ws = make_weights(N, dtype, n, k, seed, copies)
+    x = make_x(k, m, seed ^ 0xA11)
+    y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+    qmode = act if act != N.ACT_F32 else N.ACT_I8
+    _, _, abytes = N.act_layout_ex(qmode, k, m)
+    buf = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
+    N.quantize_act_ex_dev(qmode, x.data_ptr(), k, k, m, buf.data_ptr(), st.handle)
+    for w in ws:
+        w.prepare(act, m)
+    state = {"i": 0}
+
+    def launch():
+        w = ws[state["i"] % len(ws)]
+        state["i"] += 1
+        if act != N.ACT_F32:
+            N.gemv_act_dev(w, act, buf.data_ptr(), m, y.data_ptr(), n, st.handle)
+        else:
+            N.gemv_batch_dev(w, x.data_ptr(), k, y.data_ptr(), n, m, N.ACT_F32, st.handle)
+
+    launch.keep = (ws, x, y, buf)
+    launch.copies = copies
+    return launch
+
+
+def per_launch(st, launch, steps, warmup):
+    """Seconds per launch over a graph of max(copies, MIN_LAUNCHES, steps)."""
+    reps = max(launch.copies, MIN_LAUNCHES, steps)
+    return time_graph(st, [launch], reps, min(warmup, 5)) / reps, reps
+
+
+def case_name(dtype, n, k, m):
+    return f"{ {1: 'Q8', 2: 'Q4', 3: 'BF16'}[dtype]} {n}x{k} M={m}"
+
+
+def measure_cases(args, N, cases, act, label):
+    """Each (dtype, n, k, m) case alone, per launch (see per_launch)."""
     import torch
     st = Stream()
-    shapes = Q4_SWEEP
-    per_shape = []
-    inputs = []
-    all_launch = []
-    keep = []
-    total_bytes_step = 0
-    for i, (n, k) in enumerate(shapes):
-        wb = weight_bytes(2, n, k)
-        copies = max(2, math.ceil(ROTATE_BYTES / wb))
-        ws = make_weights(N, 2, n, k, 0x5EED01 + i, copies)
-        x = make_x(k, 1, 0xA11 + i)
-        _, _, abytes = N.act_layout(k, 1)
-        act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
-        N.quantize_act_dev(x.data_ptr(), k, k, 1, act.data_ptr(), st.handle)
-        y = torch.zeros(n, dtype=torch.float32, device="cuda")
-        keep += [ws, x, act, y]
-        state = {"i": 0}
+    out = []
+    for ci, (dtype, n, k, m) in enumerate(cases):
+        launch = rotating(N, st, dtype, n, k, m, act, 0x5EED10 + 7 * ci + dtype)
+        torch.cuda.synchronize()
+        secs, reps = per_launch(st, launch, args.steps, args.warmup)
+        us = secs * 1e6
+        byts = gemv_bytes(dtype, n, k, m)
+        ops = 2.0 * m * n * k
+        e = dict(case=case_name(dtype, n, k, m), us=round(us, 3), gbs=round(byts / us / 1e3, 1),
+                 hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4), tops=round(ops / us / 1e6, 2),
+                 int8_frac=round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), launches=reps)
+        log(f"{label}: {e}")
+        out.append(e)
+        del launch
+        torch.cuda.synchronize()
+    return out
 
-        def launch(ws=ws, act=act, y=y, state=state):
-            w = ws[state["i"] % len(ws)]
-            state["i"] += 1
-            N.gemv_i8_dev(w, act.data_ptr(), 1, y.data_ptr(), n, st.handle)
 
-        all_launch.append(launch)
-        total_bytes_step += gemv_bytes(2, n, k)
-        per_shape.append(dict(shape=f"{n}x{k}", copies=copies, bytes=gemv_bytes(2, n, k), launch=launch))
-        inputs.append((ws[0], act, k))
-        log(f"shape {n}x{k}: {copies} copies of {wb / 1e6:.1f} MB")
+def q4_sweep(args, N):
+    """The headline: exactly args.steps timed steps of the four GEMVs, plus
+    each shape's per-launch time for the roofline."""
+    import torch
+    st = Stream()
+    per_shape, inputs, launches = [], [], []
+    for i, (n, k) in enumerate(Q4_SWEEP):
+        launch = rotating(N, st, 2, n, k, 1, N.ACT_I8, 0x5EED01 + i)
+        launches.append(launch)
+        ws, x, _, buf = launch.keep
+        inputs.append((ws[0], buf, k))
+        log(f"shape {n}x{k}: {launch.copies} copies of {weight_bytes(2, n, k) / 1e6:.1f} MB")
     torch.cuda.synchronize()
-
-    # Per-shape timing (each shape alone, back to back).
-    for p in per_shape:
-        secs = time_gemv_set(N, st, [p["launch"]], args.steps, args.warmup)
-        p["us"] = secs / args.steps * 1e6
-        p["gbs"] = p["bytes"] / (secs / args.steps) / 1e9
-        p["hbm_frac"] = p["gbs"] / HBM_PEAK_GBS
-        log(f"{p['shape']}: {p['us']:.2f} us/launch, {p['gbs']:.0f} GB/s ({100 * p['hbm_frac']:.1f}% of HBM)")
-        del p["launch"]
-
-    # The sweep: one step = the four GEMVs; barrier + sync on both sides.
-    secs = time_gemv_set(N, st, all_launch, args.steps, args.warmup)
-    value = total_bytes_step * args.steps / secs / 1e9
+    for (n, k), launch in zip(Q4_SWEEP, launches):
+        secs, reps = per_launch(st, launch, args.steps, args.warmup)
+        b = gemv_bytes(2, n, k)
+        p = dict(shape=f"{n}x{k}", copies=launch.copies, launches=reps, bytes=b, us=round(secs * 1e6, 4),
+                 gbs=round(b / secs / 1e9, 1), hbm_frac=round(b / secs / 1e9 / HBM_PEAK_GBS, 4))
+        log(f"{p['shape']}: {p['us']:.2f} us/launch over {reps} launches, {p['gbs']:.0f} GB/s "
+            f"({100 * p['hbm_frac']:.1f}% of HBM)")
+        per_shape.append(p)
+    # The sweep: exactly `steps` steps of the four GEMVs.
+    secs = time_graph(st, launches, args.steps, args.warmup)
+    step_bytes = sum(gemv_bytes(2, n, k) for n, k in Q4_SWEEP)
+    value = step_bytes * args.steps / secs / 1e9
     kernel_us = sum(p["us"] for p in per_shape) / len(per_shape)
-    bytes_per_launch = total_bytes_step / len(shapes)
+    bytes_per_launch = step_bytes / len(Q4_SWEEP)
     achieved = bytes_per_launch / (kernel_us * 1e-6) / 1e9
     result = dict(
         metric="quantized GEMV GB/s (% HBM peak); int8 GEMM TOPS; batch-1 decode tok/s",
@@ -174,12 +236,106 @@ def q4_sweep(args, N):
                     rotate_mb=ROTATE_BYTES >> 20),
         roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                       frac=round(achieved / HBM_PEAK_GBS, 4),
-                      traffic=round(sum(Q4_SWEEP_TRAFFIC) / len(Q4_SWEEP_TRAFFIC)),
+                      traffic=round(sum(Q4_SWEEP_TRAFFIC) / len(Q4_SWEEP_TRAFFIC)), traffic_source=TRAFFIC_SOURCE,
                       kernel="gemv_i8_v2_kernel (Q4, M=1)", bytes_per_launch=bytes_per_launch,
-                      avg_launch_us=round(kernel_us, 3)),
-        per_shape=[{k: (round(v, 4) if isinstance(v, float) else v) for k, v in p.items()} for p in per_shape],
+                      avg_launch_us=round(kernel_us, 3),
+                      timing=f"HIP events over a graph of max(copies, {MIN_LAUNCHES}, steps) launches per shape"),
+        per_shape=per_shape,
     )
-    return result, inputs
+    return result, inputs, launches
+
+
+def traffic_run(N):
+    """For `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`: a 64 MiB device
+    copy (the counter's calibration: 64 MiB read, 64 MiB written), then each
+    sweep shape launched eagerly five times over two weight copies."""
+    import torch
+    a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    st = Stream()
+    for i, (n, k) in enumerate(Q4_SWEEP):
+        launch = rotating(N, st, 2, n, k, 1, N.ACT_I8, 0x5EED01 + i, rot_bytes=1)
+        for _ in range(5):
+            launch()
+        torch.cuda.synchronize()
+        log(f"traffic: {n}x{k} x5")
+        del launch
+
+
+# ---- measured peaks (the roofline denominators on this box) ------------------------
+
+def _calib():
+    L = C.CDLL(os.path.join(ROOT, "nncpu_amd", "lib", "libnncpu_calib.so"))
+    L.nnc_read_stream.argtypes, L.nnc_read_stream.restype = [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p], C.c_int
+    L.nnc_mfma_loop.argtypes, L.nnc_mfma_loop.restype = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p], C.c_int
+    L.nnc_mfma_ops.argtypes, L.nnc_mfma_ops.restype = [C.c_int, C.c_int, C.c_int], C.c_longlong
+    return L
+
+
+def peaks(args):
+    """HBM: a read stream over 1 GiB (cold, four times the Infinity Cache)
+    and a device copy; per-launch read-stream ceilings at the sweep's weight
+    sizes, timed like the sweep (a graph of launches over >= 512 MB of
+    rotating slices); the matrix unit: dense int8 and BF16 MFMA loops over
+    every CU."""
+    import torch
+    L = _calib()
+    st = Stream()
+    out = torch.zeros(256, dtype=torch.int32, device="cuda")
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    big.fill_(1)
+    res = {}
+    best = {}
+    for unroll in (4, 16):
+        def f(unroll=unroll):
+            assert L.nnc_read_stream(big.data_ptr(), big.numel(), unroll, out.data_ptr(), st.handle) == 0
+        secs = time_graph(st, [f], 5, 1) / 5
+        best[unroll] = big.numel() / secs / 1e9
+    res["hbm_read_1gib_gbs"] = round(max(best.values()), 1)
+    dst = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    src = big[:256 << 20]
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0 = st.event()
+    with torch.cuda.stream(st.s):
+        for _ in range(10):
+            dst.copy_(src)
+    e1 = st.event()
+    torch.cuda.synchronize()
+    res["copy_256mib_gbs"] = round(2 * dst.numel() * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9, 1)
+    ceil = []
+    for size in sorted({weight_bytes(2, n, k) for n, k in Q4_SWEEP + [FUSED_GATE_UP]}):
+        sz = (size + 4095) // 4096 * 4096
+        slices = max(2, (512 << 20) // sz)
+        state = {"i": 0}
+
+        def f(sz=sz, slices=slices, state=state):
+            off = (state["i"] % slices) * sz
+            state["i"] += 1
+            assert L.nnc_read_stream(big.data_ptr() + off, sz, 4, out.data_ptr(), st.handle) == 0
+        reps = max(slices, MIN_LAUNCHES)
+        secs = time_graph(st, [f], reps, 2) / reps
+        ceil.append(dict(bytes=sz, us=round(secs * 1e6, 3), gbs=round(sz / secs / 1e9, 1)))
+    res["read_stream_per_launch"] = ceil
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for kind, name, peak in ((1, "mfma_i8_tops", INT8_PEAK_TOPS), (2, "mfma_bf16_tflops", BF16_PEAK_TFLOPS)):
+        blocks, iters = cus * 2, 4096
+
+        def f(kind=kind, blocks=blocks, iters=iters):
+            assert L.nnc_mfma_loop(kind, iters, blocks, out.data_ptr(), st.handle) == 0
+        secs = time_graph(st, [f], 5, 1) / 5
+        v = L.nnc_mfma_ops(kind, iters, blocks) / secs / 1e12
+        res[name] = round(v, 1)
+        res[name.replace("_tops", "_frac").replace("_tflops", "_frac")] = round(v / peak, 4)
+    res["datasheet"] = dict(hbm_gbs=HBM_PEAK_GBS, int8_tops=INT8_PEAK_TOPS, bf16_tflops=BF16_PEAK_TFLOPS)
+    del big, dst
+    torch.cuda.synchronize()
+    log(f"peaks: {res}")
+    return res
 
 
 QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
@@ -188,51 +344,6 @@ GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 69
 # BF16 weights: the reference's own BF16 test shapes (Gemma E2B/E4B, kernels/tests.rs:435-447) and
 # Llama-3-8B projections.
 BF16_SHAPES = [(1536, 1536), (2048, 1536), (6144, 1536), (4096, 4096), (14336, 4096)]
-
-
-def measure_cases(args, N, cases, act_mode, label):
-    """Time each (dtype, n, k, m) case alone: `args.steps` launches captured in
-    a graph over rotating weight copies (>= 512 MB), inputs resident in HBM.
-    act_mode: ACT_I8 / ACT_MXI8 time the int8 matmul on activations
-    quantized beforehand (nncpu's Q8_0 encoder / power-of-two MX blocks);
-    ACT_F32 times the bit-exact f32 path (block sums included for Q4)."""
-    import torch
-    st = Stream()
-    out = []
-    for ci, (dtype, n, k, m) in enumerate(cases):
-        wb = weight_bytes(dtype, n, k)
-        copies = max(2, math.ceil(ROTATE_BYTES / wb))
-        ws = make_weights(N, dtype, n, k, 0x5EED10 + 7 * ci + dtype, copies)
-        x = make_x(k, m, 0xA11 + ci)
-        y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
-        qmode = act_mode if act_mode != N.ACT_F32 else N.ACT_I8
-        _, _, abytes = N.act_layout_ex(qmode, k, m)
-        act = torch.zeros(abytes, dtype=torch.uint8, device="cuda")
-        N.quantize_act_ex_dev(qmode, x.data_ptr(), k, k, m, act.data_ptr(), st.handle)
-        state = {"i": 0}
-
-        def launch(ws=ws, state=state, act=act, x=x, y=y, n=n, k=k, m=m):
-            w = ws[state["i"] % len(ws)]
-            state["i"] += 1
-            if act_mode != N.ACT_F32:
-                N.gemv_act_dev(w, act_mode, act.data_ptr(), m, y.data_ptr(), n, st.handle)
-            else:
-                N.gemv_batch_dev(w, x.data_ptr(), k, y.data_ptr(), n, m, N.ACT_F32, st.handle)
-
-        torch.cuda.synchronize()
-        steps = max(10, min(args.steps, int(2e5 / max(1.0, wb / 1e6))))  # bound the timed work
-        secs = time_gemv_set(N, st, [launch], steps, min(args.warmup, 10))
-        us = secs / steps * 1e6
-        byts = gemv_bytes(dtype, n, k, m)
-        ops = 2.0 * m * n * k
-        e = dict(case=f"{ {1: 'Q8', 2: 'Q4', 3: 'BF16'}[dtype]} {n}x{k} M={m}", us=round(us, 3),
-                 gbs=round(byts / us / 1e3, 1), hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
-                 tops=round(ops / us / 1e6, 2), int8_frac=round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), steps=steps)
-        log(f"{label}: {e}")
-        out.append(e)
-        del ws
-        torch.cuda.synchronize()
-    return out
 
 
 def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int = 28):
@@ -345,46 +456,137 @@ def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int =
     return res
 
 
-def cpu_baseline_q4(N, O, inputs, budget_s=12.0):
+def host_info():
+    """nproc, the CPU model and the physical cores this process may use (the
+    box's CPU share: OMP_NUM_THREADS when the environment sets it)."""
+    model = ""
+    try:
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    avail = len(os.sched_getaffinity(0))
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=10).stdout
+        phys = len({ln for ln in out.splitlines() if ln and not ln.startswith("#")})
+    except Exception:
+        phys = avail
+    share = int(os.environ.get("OMP_NUM_THREADS") or 0) or phys
+    return dict(nproc=avail, model=model, physical_cores=phys, all_cores=max(1, min(share, phys, avail)))
+
+
+def cpu_time(f, budget_s, min_reps=2):
+    """Best time of f() over repeats after one warm-up, within a budget."""
+    f()
+    best, t_end, reps = float("inf"), time.time() + budget_s, 0
+    while reps < min_reps or (time.time() < t_end and reps < 3):
+        t0 = time.perf_counter()
+        f()
+        best = min(best, time.perf_counter() - t0)
+        reps += 1
+    return best
+
+
+def cpu_baseline(N, O, inputs):
     """nncpu's AVX2 kernels (restated, oracle/avx2.cpp) on this host's cores,
-    on the same weights (downloaded from the GPU) and the same quantized
-    activations (dequantized: the values nncpu's f32 kernel would be fed),
-    rotating >= 256 MB of weight copies as the reference's bench_gemv does;
-    best of 3 passes after a warm-up."""
+    as the reference's bench_gemv (kernels/tests.rs:1295-1416) times them:
+    the same weights (downloaded from the GPU), the same quantized
+    activations dequantized (the values nncpu's f32 kernel would be fed),
+    >= 256 MB of weight copies rotated so they stream from DRAM, best of
+    passes after a warm-up; rows split over threads as pool::for_rows does.
+    value: the Q4 sweep at nncpu's default min(8, CPUs) threads; beside it
+    the same at 1 thread and at all cores (14336x4096 only), the Q8 vocab
+    GEMV, speculative verify at M = 2..16 and the M = 512 prefill as nncpu
+    runs it (32 batches of 16 tokens, session/engine.rs:362-380)."""
     if not O.avx_available():
         return None
-    threads = min(8, os.cpu_count() or 1)
-    O.avx_set_threads(threads)
-    tot_bytes, tot_secs, sample = 0, 0.0, []
+    host = host_info()
+    threads = min(8, host["nproc"])
     t_start = time.time()
-    for w, act, k in inputs:
+    mats = {}
+
+    def rotation(w, k, dtype):
         n = w.rows()
-        m = O.QMatrix.from_split(2, n, k, w.download())
-        copies = max(2, math.ceil((256 << 20) / weight_bytes(2, n, k)))
-        mats = [m] + [O.QMatrix(2, n, k, tuple(p.copy() for p in m.parts)) for _ in range(copies - 1)]
-        off_s, _, _ = N.act_layout(k, 1)
-        a = act.cpu().numpy()
-        xd = O.dequant_act(a[:k].view(np.int8), a[off_s:off_s + k // 16].view(np.uint16))
-        best = float("inf")
-        for rep in range(4):
-            t0 = time.perf_counter()
-            for mm in mats:
-                O.gemv_batch(mm, xd, backend="avx2")
-            dt = (time.perf_counter() - t0) / len(mats)
-            if rep > 0:
-                best = min(best, dt)
-        tot_bytes += gemv_bytes(2, n, k)
-        tot_secs += best
-        sample.append(f"{n}x{k}:{gemv_bytes(2, n, k) / best / 1e9:.1f}GB/s")
-        del mats
-        if time.time() - t_start > budget_s:
-            break
-    gbs = tot_bytes / tot_secs / 1e9
-    return dict(value=round(gbs, 2), unit="GB/s", cores=threads, kind="port",
-                sample="Q4 GEMV M=1 at " + ", ".join(sample) + f"; {threads} threads (nncpu default min(8, CPUs)), "
-                "AVX2 restatement of q4_rows_raw on the same weights and dequantized int8 activations, "
-                ">=256 MB rotation, best of 3",
-                host_stream_gbs_1thread=round(O.avx_stream_gbs(256 << 20, 2), 1))
+        m = O.QMatrix.from_split(dtype, n, k, w.download())
+        copies = max(2, math.ceil((256 << 20) / weight_bytes(dtype, n, k)))
+        return [m] + [O.QMatrix(dtype, n, k, tuple(p.copy() for p in m.parts)) for _ in range(copies - 1)]
+
+    def xdeq(buf, k, m=1):
+        off_s, _, _ = N.act_layout(k, m)
+        a = buf.cpu().numpy()
+        return O.dequant_act(a[:m * k].view(np.int8), a[off_s:off_s + m * k // 16].view(np.uint16))
+
+    def sweep_rate(th, sel, budget):
+        O.avx_set_threads(th)
+        tot_b, tot_s, parts = 0, 0.0, []
+        for i in sel:
+            w, buf, k = inputs[i]
+            n = w.rows()
+            if i not in mats:
+                mats[i] = (rotation(w, k, 2), xdeq(buf, k))
+            ms, xd = mats[i]
+
+            def one_pass(ms=ms, xd=xd):
+                for mm in ms:
+                    O.gemv_batch(mm, xd, backend="avx2")
+            dt = cpu_time(one_pass, budget) / len(ms)
+            tot_b += gemv_bytes(2, n, k)
+            tot_s += dt
+            parts.append(f"{n}x{k}:{gemv_bytes(2, n, k) / dt / 1e9:.1f}GB/s")
+        return tot_b / tot_s / 1e9, parts
+
+    gbs, parts = sweep_rate(threads, range(len(inputs)), 2.0)
+    g1, _ = sweep_rate(1, [2], 2.0)
+    gall, _ = sweep_rate(host["all_cores"], [2], 1.0)
+    res = dict(value=round(gbs, 2), unit="GB/s", cores=threads, kind="port",
+               sample="Q4 GEMV M=1 at " + ", ".join(parts) + f"; {threads} threads (nncpu default min(8, CPUs)), "
+               "AVX2 restatement of q4_rows_raw on the same weights and dequantized int8 activations, "
+               ">=256 MB rotation, best of passes",
+               host=host, threads_1_gbs=round(g1, 2), threads_all_gbs=round(gall, 2),
+               threads_all=host["all_cores"], per_thread_shape="14336x4096",
+               host_stream_gbs_1thread=round(O.avx_stream_gbs(256 << 20, 2), 1))
+    mats.clear()
+    O.avx_set_threads(threads)
+    import torch
+    rng = O.Rng(0xC9B)
+    other = {}
+    # Config 3: Gemma-3 vocab lm_head, Q8, M = 1.
+    n, k = Q8_VOCAB[0]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED03)
+    wt = torch.randn(n * k, generator=g, device="cuda").mul_(0.02)
+    torch.cuda.synchronize()
+    dev = N.Weight.encode_dev(1, wt.data_ptr(), n, k)
+    del wt
+    m = O.QMatrix.from_split(1, n, k, dev.download())
+    dev.free()
+    x = rng.normals(k, 1.0)
+    dt = cpu_time(lambda: O.gemv_batch(m, x, backend="avx2"), 1.0)
+    other["q8_vocab_262144x1152_m1"] = dict(gbs=round(gemv_bytes(1, n, k) / dt / 1e9, 2), ms=round(dt * 1e3, 3))
+    del m
+    # Config 4: verify at M = 2..16, Q8 6144x1536.
+    n, k = VERIFY_SHAPES[0]
+    m = O.QMatrix.from_f32(1, rng.normals(n * k, 0.02).reshape(n, k))
+    ver = {}
+    for mt in (2, 4, 8, 16):
+        x = rng.normals(mt * k, 1.0)
+        dt = cpu_time(lambda: O.gemv_batch(m, x, mt, backend="avx2"), 0.5)
+        ver[f"M={mt}"] = dict(us=round(dt * 1e6, 1), gflops=round(2 * mt * n * k / dt / 1e9, 1))
+    other["verify_q8_6144x1536"] = ver
+    # Config 5: the gate projection at M = 512 as 32 calls of 16 tokens.
+    n, k = QWEN_PREFILL[2]
+    m = O.QMatrix.from_f32(1, rng.normals(n * k, 0.02).reshape(n, k))
+    x = rng.normals(16 * k, 1.0)
+    dt = cpu_time(lambda: O.gemv_batch(m, x, 16, backend="avx2"), 0.5, min_reps=1)
+    other["prefill_q8_18944x3584_m512"] = dict(ms=round(32 * dt * 1e3, 1),
+                                               gops=round(2 * 512 * n * k / (32 * dt) / 1e9, 1),
+                                               how="32 x gemv_batch(16 tokens), timed one, times 32")
+    del m
+    res["configs"] = other
+    res["wall_s"] = round(time.time() - t_start, 1)
+    log(f"cpu baseline: {res}")
+    return res
 
 
 def gemma_decode(args, N, cpu: bool):
@@ -436,11 +638,11 @@ def gemma_decode(args, N, cpu: bool):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "bf16", "all"])
+                             "bf16", "peaks", "traffic", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -451,19 +653,37 @@ def main():
     import nncpu_amd as N
     N.init(0)
     torch.cuda.set_device(0)
+    if args.workload == "traffic":
+        traffic_run(N)
+        return
     extra = {}
-    if args.workload in ("prefill", "all"):
-        extra["prefill_m512_mx"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
-                                                 N.ACT_MXI8, "prefill_mx")
-        extra["prefill_m512"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
-                                              N.ACT_I8, "prefill")
+    prefill_cases = [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL]
+    if args.workload in ("peaks", "q4_sweep", "all"):
+        extra["peaks"] = peaks(args)
+    result = inputs = None
+    if args.workload in ("q4_sweep", "all"):
+        result, inputs, _ = q4_sweep(args, N)
+        # Llama-3-8B's gate and up as one launch (a decode step's largest
+        # weight read), and the bit-exact f32 path (the drop-in mode) at the
+        # sweep's shapes.
+        extra["q4_fused_gate_up_m1"] = measure_cases(args, N, [(2, *FUSED_GATE_UP, 1)], N.ACT_I8, "fused_gate_up")
+        extra["q4_sweep_f32_bit_exact"] = measure_cases(args, N, [(2, n, k, 1) for n, k in Q4_SWEEP], N.ACT_F32,
+                                                        "q4_f32")
+    if args.workload in ("prefill", "q4_sweep", "all"):
+        # The metric's GEMM part: M = 512 at the
+        # Qwen2.5-7B shapes, both weight formats, both int8 modes (nncpu's
+        # Q8_0 activation encoder, and power-of-two MX blocks).
+        extra["prefill_m512_i8"] = measure_cases(args, N, prefill_cases, N.ACT_I8, "prefill_i8")
+        extra["prefill_m512_mx"] = measure_cases(args, N, prefill_cases, N.ACT_MXI8, "prefill_mx")
     if args.workload in ("qwen_prefill", "all"):
         extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d, a) for d in (1, 2) for a in (N.ACT_MXI8, N.ACT_I8)]
     if args.workload in ("q8_vocab", "all"):
         extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
+        extra["q8_vocab_m1_f32_bit_exact"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_F32,
+                                                           "q8_vocab_f32")
     if args.workload in ("verify", "all"):
         extra["verify"] = measure_cases(args, N, [(d, n, k, m) for d in (1, 2) for n, k in VERIFY_SHAPES[:2]
-                                                     for m in (2, 4, 8, 16)], N.ACT_I8, "verify")
+                                                  for m in (2, 4, 8, 16)], N.ACT_I8, "verify")
     if args.workload in ("decode_f32", "all"):
         extra["decode_f32_bit_exact"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
                                                       N.ACT_F32, "decode_f32")
@@ -472,24 +692,22 @@ def main():
                                                 N.ACT_F32, "bf16")
     if args.workload in ("gemma_decode", "q4_sweep", "all"):
         extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
-    if args.workload == "q4_sweep":
-        # The metric's GEMM part: M = 512 prefill at the
-        # Qwen2.5-7B shapes, MX int8 activations, both weight formats.
-        extra["prefill_m512_mx"] = measure_cases(args, N, [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL],
-                                                 N.ACT_MXI8, "prefill_mx")
-    if args.workload not in ("q4_sweep", "all"):
+    if result is None:
         print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
         return
-    result, inputs = q4_sweep(args, N)
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import oracle as O  # the CPU baseline leg only
-        cpu = cpu_baseline_q4(N, O, inputs)
+        cpu = cpu_baseline(N, O, inputs)
     line = dict(metric=result["metric"], value=result["value"], unit=result["unit"], n_gpus=1, steps=args.steps,
                 warmup=args.warmup, ms_per_step=round(result["ms_per_step"], 5), higher_is_better=True,
                 scaling="weak", vs_baseline=None, dtype=result["dtype"], data="synthetic (seeded)",
                 config=result["config"], roofline=result["roofline"], cpu_baseline=cpu,
                 per_shape=result["per_shape"])
+    pk = extra.get("peaks")
+    if pk:
+        line["roofline"]["measured_peak"] = pk["hbm_read_1gib_gbs"]
+        line["roofline"]["frac_of_measured"] = round(result["roofline"]["achieved"] / pk["hbm_read_1gib_gbs"], 4)
     if extra:
         line["extra"] = extra
     print(json.dumps(line), flush=True)

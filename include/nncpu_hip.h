@@ -137,6 +137,25 @@ void nnh_free(nnh_weight* w);
 /* Shape and format of an uploaded weight. */
 int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols);
 
+/* Device memory of a weight. An upload holds nncpu's split layout only
+ * (Q8_0 1.0625 B per weight, Q4 0.625; BF16 2 B plus its chain layout);
+ * each activation mode builds the layouts its kernels read on the first call
+ * that needs them, once (the upload's owner pays for the modes it uses):
+ *   NNH_ACT_F32            Q8_0 +1.0625 B, Q4 +0.5625 B (per-lane quant groups,
+ *                          padded scales)
+ *   int8, 1..3 vectors     Q4 +0.125 B (packed scale | bias), Q8_0 nothing
+ *   int8, 4 and more       +0.125 B Q8_0, +0.25 B Q4 (block-major f32 scales,
+ *                          Q4 biases)
+ *   NNH_ACT_MXI8, 17 and more vectors: +2 B (BF16 quants), Q4 +0.125 B more
+ *                          (BF16 biases)
+ * nnh_weight_prepare builds those of a call (act, n_tok) ahead of time, for
+ * callers that capture calls into HIP graphs (a first call inside a capture
+ * would allocate and synchronise the library's own stream there) or that
+ * must not allocate later. nnh_weight_device_bytes gives the bytes held now.
+ * No counterpart in the reference, whose kernels read the split layout. */
+int nnh_weight_prepare(const nnh_weight* w, int act, size_t n_tok);
+size_t nnh_weight_device_bytes(const nnh_weight* w);
+
 /* Device address of the weight's split layout as uploaded (runtime.rs:136-164:
  * quants, then BF16 scales, then Q4 biases), read-only, valid until
  * nnh_free: the device form of Tensor::data, for callers that read rows
@@ -188,15 +207,21 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
  * device u64) receives the row; asynchronous on `stream`. For the matrices
  * of 16384 rows or more the first argmax stage runs inside the gemv (each
  * workgroup's best row), so only a one-workgroup reduction follows it.
- * Calls on different streams must not share `work`. */
+ * Calls on different streams must not share `work`; a Q4 matrix under 16384
+ * rows also uses the scratch of `stream` (as nnh_gemv_batch_dev). */
 size_t nnh_model_argmax_work_bytes(const nnh_weight* w);
 int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, void* work, uint64_t* out_row,
                          void* stream);
 
 /* Device-resident form of nnh_gemv_batch: x and y are device pointers, the
  * call is asynchronous on `stream` (a hipStream_t; NULL = the null stream).
- * Uses a library-owned scratch buffer for the Q4 block sums / quantized
- * activations: calls on different streams must not overlap. */
+ * The Q4 block sums / quantized activations / partial sums live in a
+ * library-owned scratch buffer of that stream: calls on different streams
+ * may overlap, as the reference's Model is shared by sessions on many
+ * threads (lib.rs:36-41). A buffer that has to grow is replaced, and the old
+ * one is kept until the process ends, so a call captured in a HIP graph stays
+ * valid after larger calls; replays of graphs captured on the same stream
+ * share that stream's scratch, so they must not overlap each other. */
 int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
                        size_t n_tok, int act, void* stream);
 
@@ -225,9 +250,8 @@ int nnh_act_layout(size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, siz
 int nnh_quantize_act_dev(const float* x, size_t x_stride, size_t cols, size_t n_tok, void* act, void* stream);
 
 /* y (device, y_stride apart) = W x for activations already in `act`: the
- * int8 path without the quantization step. Batches of 5 or more vectors on
- * small matrices keep split-K partial sums in the library's scratch buffer:
- * calls on different streams must not overlap. */
+ * int8 path without the quantization step. Batches of 4 or more vectors keep
+ * split-K partial sums in the scratch of `stream` (as nnh_gemv_batch_dev). */
 int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y, size_t y_stride, void* stream);
 
 /* The same for either int8 mode (act = NNH_ACT_I8 or NNH_ACT_MXI8): the

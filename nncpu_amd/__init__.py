@@ -124,6 +124,16 @@ class Weight:
         check(lib().nnh_weight_download(self.handle, _ptr(out), out.size))
         return out
 
+    def prepare(self, act: int = ACT_F32, n_tok: int = 1) -> "Weight":
+        """Build the device layouts a call with ``act`` over ``n_tok`` vectors
+        reads (otherwise built on the first such call)."""
+        check(lib().nnh_weight_prepare(self.handle, act, n_tok))
+        return self
+
+    def device_bytes(self) -> int:
+        """Device memory this weight holds now."""
+        return int(lib().nnh_weight_device_bytes(self.handle))
+
     def rows(self) -> int:
         """Rows: the output length of a gemv over this matrix (runtime.rs:103-107)."""
         return self._rows

@@ -4,12 +4,20 @@
 // 989-1011), and the device-resident entry points.
 //
 // One process-wide context (device, one non-blocking stream at default
-// priority, a growable device scratch buffer and pinned staging) guarded by
-// a mutex, as the reference's pool serialises dispatch (pool.rs:7-9,253).
+// priority, a device scratch buffer per calling stream and pinned staging)
+// guarded by a mutex, as the reference's pool serialises dispatch
+// (pool.rs:7-9,253).
+//
+// Device memory per weight: nncpu's split layout as uploaded, plus derived
+// layouts built on the first call that reads them (each one once, under the
+// mutex, synchronised), so a weight used in one mode holds only that mode's
+// copies.
 
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "common.h"
 #include "nncpu_hip.h"
@@ -31,6 +39,8 @@ struct nnh_weight {
     uint16_t* bl;         // device: BF16 only, the chain layout (none on the f64 path)
     uint16_t* wbf;        // device: BF16 copies of the quants, rows padded (MX GEMM)
     uint16_t* wbi;        // device: Q4 biases twice per block, rows padded (MX GEMM)
+    unsigned ready;       // derived layouts built so far (LAY_* bits)
+    size_t dev_bytes;     // device bytes held (split layout + derived layouts)
 };
 
 namespace {
@@ -39,8 +49,15 @@ thread_local std::string t_err;
 std::mutex g_mu;
 int g_device = -1;
 hipStream_t g_stream = nullptr;
-uint8_t* g_scratch = nullptr;
-size_t g_scratch_bytes = 0;
+// Device scratch per calling stream (the host-buffer calls use g_stream's),
+// so calls on different streams never share one. A buffer that grows is
+// retired, not freed: a HIP graph that captured a call keeps its address.
+struct Scratch {
+    uint8_t* p = nullptr;
+    size_t bytes = 0;
+};
+std::unordered_map<hipStream_t, Scratch> g_scratch;
+std::vector<uint8_t*> g_retired;
 uint8_t* g_pinned = nullptr;  // pinned host staging for the host-buffer calls
 size_t g_pinned_bytes = 0;
 
@@ -82,21 +99,21 @@ int init_locked(int device) {
 
 int ensure_locked() { return init_locked(g_device >= 0 ? g_device : 0); }
 
-// Grow the scratch to `bytes`; caller holds g_mu. The old buffer may still
-// be read by queued work, so the device is drained first.
-int scratch_locked(size_t bytes, uint8_t** out) {
-    if (bytes > g_scratch_bytes) {
-        if (g_scratch) {
-            NNH_HIP(hipDeviceSynchronize());
-            NNH_HIP(hipFree(g_scratch));
-            g_scratch = nullptr;
-            g_scratch_bytes = 0;
-        }
-        size_t want = align_up(bytes + bytes / 4);
-        NNH_HIP(hipMalloc((void**)&g_scratch, want));
-        g_scratch_bytes = want;
+// The scratch of calls on `st`, at least `bytes`; caller holds g_mu. Work
+// queued on `st` (or replays of graphs captured on it) may still use the
+// old buffer, so a grown buffer keeps the old one alive until the process
+// ends; doubling bounds the retired total by the live size.
+int scratch_locked(hipStream_t st, size_t bytes, uint8_t** out) {
+    Scratch& s = g_scratch[st];
+    if (bytes > s.bytes) {
+        const size_t want = align_up(bytes > 2 * s.bytes ? bytes : 2 * s.bytes);
+        uint8_t* p = nullptr;
+        NNH_HIP(hipMalloc((void**)&p, want));
+        if (s.p) g_retired.push_back(s.p);
+        s.p = p;
+        s.bytes = want;
     }
-    *out = g_scratch;
+    *out = s.p;
     return NNH_OK;
 }
 
@@ -306,77 +323,120 @@ void release(nnh_weight* w) {
 #endif
 constexpr size_t F32_V2_MIN_ROWS = NNH_F32_V2_MIN_ROWS;
 
-// Allocate a weight's device buffers; caller holds g_mu.
+// Derived layouts, built on the first call that reads them.
+enum : unsigned {
+    LAY_F32 = 1,  // fq + fs: the bit-exact f32 path
+    LAY_SB = 2,   // Q4 sb: the int8 GEMV
+    LAY_SWT = 4,  // swT: the MFMA kernels (few-token, GEMM)
+    LAY_MX = 8,   // wbf (+ Q4 wbi): the MX GEMM
+};
+
+// What a call with activation mode `act` over n_tok vectors reads.
+unsigned layouts_for(const nnh_weight* w, int act, size_t n_tok) {
+    if (w->dtype == NNH_BF16) return 0;
+    if (act == NNH_ACT_F32) return LAY_F32;
+    if (n_tok >= GEMM_MIN_TOKENS && act == NNH_ACT_MXI8) return LAY_SWT | LAY_MX;
+    if (n_tok >= SKINNY_MIN_TOKENS) return LAY_SWT;
+    return w->dtype == NNH_Q4S ? LAY_SB : 0;
+}
+
+// Allocate a weight's split layout (BF16: and its chain layout); caller
+// holds g_mu.
 int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
-    if (dtype == NNH_BF16) {
-        nnh_weight* w = new nnh_weight();
-        w->dtype = dtype;
-        w->device = g_device;
-        w->rows = rows;
-        w->cols = cols;
-        w->bpath = nnh::bf16_path(rows, cols);
-        const size_t lb = nnh::bf16_layout_bytes(w->bpath, rows, cols);
-        hipError_t e;
-        if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
-            (lb && (e = hipMalloc((void**)&w->bl, align_up(lb))) != hipSuccess)) {
-            release(w);
-            return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
-                        std::string("weight alloc: ") + hipGetErrorString(e));
-        }
-        *out = w;
-        return NNH_OK;
-    }
-    const size_t n = rows * cols, nb = cols / 32;
-    const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2;
-    const size_t group = dtype == NNH_Q8_0 ? 8 : 16;
     nnh_weight* w = new nnh_weight();
     w->dtype = dtype;
     w->device = g_device;
     w->rows = rows;
     w->cols = cols;
-    w->nb = nb;
-    w->nbp = (nb + group - 1) / group * group;
-    w->f32v2 = rows >= F32_V2_MIN_ROWS && cols * 4 <= (size_t)nnh::F32_V2_MAX_LDS;
-    hipError_t e;
-    if ((e = hipMalloc((void**)&w->raw, align_up(raw_bytes_of(dtype, rows, cols)))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->fq, align_up(nnh::f32_quant_bytes(dtype, (int)rows, (int)nb, w->f32v2)))) !=
-            hipSuccess ||
-        (e = hipMalloc((void**)&w->fs, align_up(rows * w->nbp * 2))) != hipSuccess ||
-        (dtype == NNH_Q4S && (e = hipMalloc((void**)&w->sb, align_up(rows * nb * 4))) != hipSuccess) ||
-        // swT: Q8 one spare block row (the MX GEMM loads scales in pairs of
-        // blocks); for Q4 the bias table follows the scales.
-        (e = hipMalloc((void**)&w->swT, align_up((size_t)nnh::gemm_rows_pad((int)rows) * 4 *
-                                                  (dtype == NNH_Q4S ? 2 * nb : nb + 1)))) != hipSuccess ||
-        (e = hipMalloc((void**)&w->wbf, align_up(nnh::mx_weight_bytes((int)rows, (int)nb)))) != hipSuccess ||
-        (dtype == NNH_Q4S &&
-         (e = hipMalloc((void**)&w->wbi, align_up(nnh::mx_bias_bytes((int)rows, (int)nb)))) != hipSuccess)) {
-        release(w);
-        return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE, std::string("weight alloc: ") + hipGetErrorString(e));
+    const size_t rb = align_up(raw_bytes_of(dtype, rows, cols));
+    hipError_t e = hipMalloc((void**)&w->raw, rb);
+    w->dev_bytes = rb;
+    if (e == hipSuccess && dtype == NNH_BF16) {
+        w->bpath = nnh::bf16_path(rows, cols);
+        const size_t lb = nnh::bf16_layout_bytes(w->bpath, rows, cols);
+        if (lb) {
+            e = hipMalloc((void**)&w->bl, align_up(lb));
+            w->dev_bytes += align_up(lb);
+        }
     }
-    w->qs = w->raw;
-    w->sc = (const uint16_t*)(w->raw + qbytes);
-    w->bi = dtype == NNH_Q4S ? (const uint16_t*)(w->raw + qbytes + (n / 32) * 2) : nullptr;
+    if (e != hipSuccess) {
+        release(w);
+        return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
+                    std::string("weight alloc: ") + hipGetErrorString(e));
+    }
+    if (dtype != NNH_BF16) {
+        const size_t n = rows * cols, nb = cols / 32;
+        const size_t qbytes = dtype == NNH_Q8_0 ? n : n / 2;
+        const size_t group = dtype == NNH_Q8_0 ? 8 : 16;
+        w->nb = nb;
+        w->nbp = (nb + group - 1) / group * group;
+        w->f32v2 = rows >= F32_V2_MIN_ROWS && cols * 4 <= (size_t)nnh::F32_V2_MAX_LDS;
+        w->qs = w->raw;
+        w->sc = (const uint16_t*)(w->raw + qbytes);
+        w->bi = dtype == NNH_Q4S ? (const uint16_t*)(w->raw + qbytes + (n / 32) * 2) : nullptr;
+    }
     *out = w;
     return NNH_OK;
 }
 
-// Build the derived layouts from `raw` and wait; caller holds g_mu.
+// Build the BF16 chain layout from `raw` and wait; caller holds g_mu. (Q8_0
+// and Q4 layouts are built by prepare_locked when a call first needs them.)
 int finalize_weight(nnh_weight* w) {
-    if (w->dtype == NNH_BF16) {
-        nnh::launch_relayout_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, (int)w->rows, (int)w->cols, g_stream);
-        hipError_t e;
-        if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
-            return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
-        return NNH_OK;
-    }
-    nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, (int)w->rows, (int)w->nb, (int)w->nbp, w->f32v2,
-                             g_stream);
-    if (w->dtype == NNH_Q4S) nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
-    nnh::launch_gemm_scales(w->sc, w->bi, w->swT, (int)w->rows, (int)w->nb, g_stream);
-    nnh::launch_mx_weights(w->dtype, w->qs, w->bi, (int)w->rows, (int)w->nb, w->wbf, w->wbi, g_stream);
+    if (w->dtype != NNH_BF16) return NNH_OK;
+    nnh::launch_relayout_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, (int)w->rows, (int)w->cols, g_stream);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
         return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
+    return NNH_OK;
+}
+
+int dev_alloc(nnh_weight* w, void** p, size_t bytes) {
+    const size_t b = align_up(bytes);
+    hipError_t e = hipMalloc(p, b);
+    if (e != hipSuccess)
+        return fail(e == hipErrorOutOfMemory ? NNH_E_OOM : NNH_E_DEVICE,
+                    std::string("weight layout alloc: ") + hipGetErrorString(e));
+    w->dev_bytes += b;
+    return NNH_OK;
+}
+
+// Build the derived layouts in `need` that `w` lacks, from its split layout
+// (read-only since upload), on the library stream, and wait for them; caller
+// holds g_mu. Nothing queued on any caller stream can read a layout before
+// it exists, since the calls that read it are queued after this returns.
+int prepare_locked(const nnh_weight* cw, unsigned need) {
+    nnh_weight* w = const_cast<nnh_weight*>(cw);
+    need &= ~w->ready;
+    if (!need) return NNH_OK;
+    int rc;
+    const int rows = (int)w->rows, nb = (int)w->nb;
+    if (need & LAY_F32) {
+        if ((rc = dev_alloc(w, (void**)&w->fq, nnh::f32_quant_bytes(w->dtype, rows, nb, w->f32v2))) ||
+            (rc = dev_alloc(w, (void**)&w->fs, w->rows * w->nbp * 2)))
+            return rc;
+        nnh::launch_relayout_f32(w->dtype, w->qs, w->sc, w->fq, w->fs, rows, nb, (int)w->nbp, w->f32v2, g_stream);
+    }
+    if ((need & LAY_SB) && w->dtype == NNH_Q4S) {
+        if ((rc = dev_alloc(w, (void**)&w->sb, w->rows * w->nb * 4))) return rc;
+        nnh::launch_pack_sb(w->sc, w->bi, w->sb, w->rows * w->nb, g_stream);
+    }
+    if (need & LAY_SWT) {
+        // Q8 one spare block row (the MX GEMM loads scales in pairs of
+        // blocks); for Q4 the bias table follows the scales.
+        const size_t bytes = (size_t)nnh::gemm_rows_pad(rows) * 4 * (w->dtype == NNH_Q4S ? 2 * w->nb : w->nb + 1);
+        if ((rc = dev_alloc(w, (void**)&w->swT, bytes))) return rc;
+        nnh::launch_gemm_scales(w->sc, w->bi, w->swT, rows, nb, g_stream);
+    }
+    if (need & LAY_MX) {
+        if ((rc = dev_alloc(w, (void**)&w->wbf, nnh::mx_weight_bytes(rows, nb))) ||
+            (w->dtype == NNH_Q4S && (rc = dev_alloc(w, (void**)&w->wbi, nnh::mx_bias_bytes(rows, nb)))))
+            return rc;
+        nnh::launch_mx_weights(w->dtype, w->qs, w->bi, rows, nb, w->wbf, w->wbi, g_stream);
+    }
+    hipError_t e;
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
+        return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
+    w->ready |= need;
     return NNH_OK;
 }
 
@@ -567,13 +627,30 @@ int nnh_argmax_dev(const float* v, size_t n, void* work, uint64_t* out_row, void
 }
 
 int nnh_weight_f32_layout(const nnh_weight* w, nnh_f32_layout* out) {
-    int rc = check_weight(w);
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
     if (rc) return rc;
+    if ((rc = check_weight(w))) return rc;
     if (!out) return fail(NNH_E_INVALID, "f32 layout: null output");
     if (w->dtype == NNH_BF16) return fail(NNH_E_INVALID, "f32 layout: BF16 weight (no quant layout)");
     if (w->f32v2) return fail(NNH_E_INVALID, "f32 layout: tall weight (8-lane layout)");
+    if ((rc = prepare_locked(w, LAY_F32))) return rc;
     *out = nnh_f32_layout{w->fq, w->fs, w->bi, w->rows, w->cols, w->nb, w->nbp, w->dtype};
     return NNH_OK;
+}
+
+int nnh_weight_prepare(const nnh_weight* w, int act, size_t n_tok) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, 0, w ? w->rows : 0, n_tok, act))) return rc;
+    return prepare_locked(w, layouts_for(w, act, n_tok));
+}
+
+size_t nnh_weight_device_bytes(const nnh_weight* w) {
+    if (!w) return 0;
+    std::lock_guard<std::mutex> g(g_mu);
+    return w->dev_bytes;
 }
 
 int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols) {
@@ -599,7 +676,8 @@ int nnh_gemv_batch(const nnh_weight* w, const float* x, size_t x_stride, float* 
     const size_t off_y = align_up(x_elems * 4);
     const size_t off_s = off_y + align_up(y_elems * 4);
     uint8_t *s, *h;
-    if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, n_tok, act), &s))) return rc;
+    if ((rc = prepare_locked(w, layouts_for(w, act, n_tok)))) return rc;
+    if ((rc = scratch_locked(g_stream, off_s + gemv_scratch_bytes(w, n_tok, act), &s))) return rc;
     if ((rc = pinned_locked(off_s, &h))) return rc;
     float* dx = (float*)s;
     float* dy = (float*)(s + off_y);
@@ -632,7 +710,8 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
     const size_t off_o = off_p + align_up(argmax_work_bytes(w, act));
     const size_t off_s = off_o + ALIGN;
     uint8_t *s, *h;
-    if ((rc = scratch_locked(off_s + gemv_scratch_bytes(w, 1, act), &s))) return rc;
+    if ((rc = prepare_locked(w, layouts_for(w, act, 1)))) return rc;
+    if ((rc = scratch_locked(g_stream, off_s + gemv_scratch_bytes(w, 1, act), &s))) return rc;
     if ((rc = pinned_locked(off_y + ALIGN, &h))) return rc;
     float* dx = (float*)s;
     float* dy = (float*)(s + off_y);
@@ -658,8 +737,9 @@ int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, voi
     if (w->rows >= ((size_t)1 << 32)) return fail(NNH_E_INVALID, "argmax: too many rows");
     if (!x || !logits || !work || !out_row) return fail(NNH_E_INVALID, "argmax: null pointer");
     uint8_t* s = nullptr;
+    if ((rc = prepare_locked(w, layouts_for(w, NNH_ACT_F32, 1)))) return rc;
     const size_t need = argmax_fused(w, NNH_ACT_F32) ? 0 : gemv_scratch_bytes(w, 1, NNH_ACT_F32);
-    if (need && (rc = scratch_locked(need, &s))) return rc;
+    if (need && (rc = scratch_locked((hipStream_t)stream, need, &s))) return rc;
     return run_argmax(w, x, logits, (uint8_t*)work, out_row, NNH_ACT_F32, s, (hipStream_t)stream);
 }
 
@@ -672,8 +752,9 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
     if (n_tok == 0) return NNH_OK;
     if (!x || !y) return fail(NNH_E_INVALID, "gemv: null x or y");
     uint8_t* s = nullptr;
+    if ((rc = prepare_locked(w, layouts_for(w, act, n_tok)))) return rc;
     size_t need = gemv_scratch_bytes(w, n_tok, act);
-    if (need && (rc = scratch_locked(need, &s))) return rc;
+    if (need && (rc = scratch_locked((hipStream_t)stream, need, &s))) return rc;
     const size_t xs = n_tok > 1 ? x_stride : w->cols;
     const size_t ys = n_tok > 1 ? y_stride : w->rows;
     return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
@@ -722,8 +803,9 @@ int nnh_gemv_act_dev(const nnh_weight* w, int act, const void* buf, size_t n_tok
     if (n_tok == 0) return NNH_OK;
     if (!buf || !y) return fail(NNH_E_INVALID, "gemv_act: null pointer");
     uint8_t* ws = nullptr;
+    if ((rc = prepare_locked(w, layouts_for(w, act, n_tok)))) return rc;
     const size_t wsb = i8_workspace_bytes(w, n_tok, act);
-    if (wsb && (rc = scratch_locked(wsb, &ws))) return rc;
+    if (wsb && (rc = scratch_locked((hipStream_t)stream, wsb, &ws))) return rc;
     launch_i8(w, act, (const uint8_t*)buf, n_tok, y, n_tok > 1 ? y_stride : w->rows, ws, (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
     return NNH_OK;

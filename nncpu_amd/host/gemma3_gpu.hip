@@ -812,6 +812,11 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
         }
         m->f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, l.biases, (int)l.rows, (int)l.nb, (int)l.nbp});
     }
+    // The lm_head's layouts too, before any step is captured.
+    if (nnh_weight_prepare(m->w.back(), NNH_ACT_F32, 1)) {
+        m->err = std::string("lm_head layout: ") + nnh_last_error();
+        return 1;
+    }
     m->n_gen_max = n_gen_max;
     const size_t E = c.n_embd, hd = c.head_dim, qd = (size_t)c.n_head * hd, kvd = (size_t)c.n_kv * hd;
     const size_t nn = norm_stride(c) * c.n_layer + E, half = hd / 2;

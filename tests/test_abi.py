@@ -77,3 +77,22 @@ def test_act_modes_are_checked_without_a_device():
     assert L.nnh_act_layout_ex(7, 64, 1, None, None, C.byref(sz)) == _lib.NNH_E_INVALID
     assert L.nnh_act_layout_ex(N.ACT_MXI8, 100, 1, None, None, C.byref(sz)) == _lib.NNH_E_INVALID
     assert b"multiple of 32" in L.nnh_last_error()
+
+
+def test_calibration_library_exports_its_header():
+    # libnncpu_calib.so (the benchmark's peak calibration) exports exactly
+    # what include/nncpu_calib.h declares, for gfx950 only.
+    import os
+    import re
+    root = os.path.dirname(_lib.HEADER)
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(root, "nncpu_calib.h")).read(), flags=re.S)
+    names = set(re.findall(r"^\s*(?:long long|int)\s+(nnc_\w+)\s*\(", text, flags=re.M))
+    assert names == {"nnc_read_stream", "nnc_mfma_loop", "nnc_mfma_ops"}
+    path = os.path.join(os.path.dirname(_lib.LIB_PATH), "libnncpu_calib.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True)
+    assert {line.split()[-1] for line in out.stdout.splitlines() if " T nnc_" in line} == names
+    L = C.CDLL(path)
+    L.nnc_mfma_ops.restype = C.c_longlong
+    assert L.nnc_mfma_ops(1, 10, 3) == 2 * 32 * 32 * 32 * 4 * 10 * 3 * 4
+    assert L.nnc_read_stream(None, 16, 4, None, None) == 1
+    assert set(re.findall(rb"amdgcn-amd-amdhsa--(gfx[0-9a-z]+)", open(path, "rb").read())) == {b"gfx950"}

@@ -1,0 +1,144 @@
+"""Parity at the full BASELINE shapes of configs 3 and 5, through the C-ABI
+(needs an MI355X).
+
+Config 5 (Qwen2.5-7B prefill, M = 512): every projection shape in both int8
+modes and both weight formats. Each output is checked against the exact sum
+of its block terms (integer block dots, f64) within the kernel's stated f32
+rounding bound, and 8 sampled tokens x all rows against nncpu's own kernel
+(the oracle's restatement of kernels/scalar.rs:626-742) fed the dequantized
+activations, at the north-star tolerance: 1e-5 absolute per element and
+1e-3 relative L2 (kernels/tests.rs:555-639 compare against an f64 gemv the
+same way).
+
+Config 3 (Qwen2.5-7B vocab, 151936 x 3584, M = 1): the f32 path bit for bit
+against the oracle, the int8 path within 1e-5 of the oracle fed x'.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import bits
+
+pytestmark = pytest.mark.gpu
+
+N = pytest.importorskip("nncpu_amd")
+
+U32 = 2.0 ** -24
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    N.init(0)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def device_weight(oracle, dtype, rows, cols, seed):
+    """0.02 N(0,1) weights drawn on the GPU and encoded there (nncpu's encoder
+    bit for bit, pinned in test_gemv_gpu.py), and the same weight on the host
+    for the oracle."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    w = torch.randn(rows * cols, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+    torch.cuda.synchronize()
+    dev = N.Weight.encode_dev(dtype, w.data_ptr(), rows, cols)
+    del w
+    return dev, oracle.QMatrix.from_split(dtype, rows, cols, dev.download())
+
+
+def quantize(oracle, act, x, n_tok, xs, cols):
+    f = oracle.quantize_act_mx if act == N.ACT_MXI8 else oracle.quantize_act
+    qs, ss = zip(*[f(x[t * xs:t * xs + cols]) for t in range(n_tok)])
+    return qs, ss
+
+
+def gemm_bound(dtype, act, cols):
+    """The f32 rounding allowance (in units of u * sum|terms|) of the GEMM
+    each int8 mode takes from 17 vectors: MX sums 16-block chunks in f32
+    (Q4: plus the bias MFMAs) into f32 totals, one rounding per 8-block group
+    at most; the int8 GEMM sums 8-block chunks in f32 and the chunks in f64."""
+    if act == N.ACT_MXI8:
+        return (16 if dtype == 1 else 64) + (cols // 32 + 7) // 8
+    return 16
+
+
+SAMPLED = 8
+
+
+def check_batch(oracle, m, act, x, xs, y, ys, n_tok):
+    rows, cols = m.rows, m.cols
+    qs, ss = quantize(oracle, act, x, n_tok, xs, cols)
+    exact, mag = oracle.gemm_exact(m, np.concatenate(qs), np.concatenate(ss), n_tok)
+    got = np.stack([y[t * ys:t * ys + rows] for t in range(n_tok)]).astype(np.float64)
+    k = gemm_bound(m.dtype, act, cols)
+    bound = k * U32 * mag + np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    bad = np.abs(got - exact) > bound
+    assert not bad.any(), (np.argwhere(bad)[:5], (got - exact)[bad][:5], bound[bad][:5])
+    sample = sorted(set([0, n_tok - 1] + list(range(0, n_tok, max(1, n_tok // (SAMPLED - 1))))))[:SAMPLED + 1]
+    xd = np.concatenate([oracle.dequant_act(qs[t], ss[t]) for t in sample])
+    ref = oracle.gemv_batch(m, xd, len(sample), cols, rows)
+    worst = 0.0
+    for i, t in enumerate(sample):
+        r = ref[i * rows:(i + 1) * rows]
+        err = np.abs(got[t] - r).max()
+        worst = max(worst, err)
+        assert err <= 1e-5, (t, err)
+        assert np.linalg.norm(got[t] - r) <= 1e-3 * np.linalg.norm(r), t
+    say(f"  max |y - nncpu(x')| over {len(sample)} tokens: {worst:.3g}")
+
+
+QWEN_M512 = [
+    (3584, 3584),    # q / o projections
+    (512, 3584),     # k / v projections
+    (18944, 3584),   # gate / up projections
+    (3584, 18944),   # down projection (K = 18944: the tightest absolute margin)
+]
+
+
+@pytest.mark.parametrize("act", [1, 2], ids=["I8", "MXI8"])
+@pytest.mark.parametrize("dtype", [1, 2], ids=["Q8", "Q4"])
+@pytest.mark.parametrize("rows,cols", QWEN_M512, ids=["qo", "kv", "gate_up", "down"])
+def test_qwen_prefill_m512(oracle, dtype, act, rows, cols):
+    import torch
+    n_tok = 512
+    say("config5", {1: "Q8", 2: "Q4"}[dtype], {1: "I8", 2: "MXI8"}[act], rows, cols, n_tok)
+    w, m = device_weight(oracle, dtype, rows, cols, 0x5EED05 + rows + 7 * cols + dtype)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11 + rows + cols)
+    dx = torch.randn(n_tok * cols, generator=g, device="cuda", dtype=torch.float32)
+    dy = torch.full((n_tok * rows,), 7.0, device="cuda")
+    N.gemv_batch_dev(w, dx.data_ptr(), cols, dy.data_ptr(), rows, n_tok, act)
+    N.sync()
+    check_batch(oracle, m, act, dx.cpu().numpy(), cols, dy.cpu().numpy(), rows, n_tok)
+    w.free()
+
+
+def test_qwen_vocab_m1(oracle):
+    # Config 3's larger lm_head, 151936 x 3584 Q8_0 (578 MB), one vector.
+    import torch
+    rows, cols = 151936, 3584
+    say("config3 vocab", rows, cols)
+    w, m = device_weight(oracle, 1, rows, cols, 0x5EED03)
+    rng = oracle.Rng(0x7A11)
+    x = rng.normals(cols, 1.0)
+    want = oracle.gemv_batch(m, x)
+    got = N.model_gemv(w, x)
+    assert np.array_equal(bits(got), bits(want))
+    assert N.model_argmax(w, x) == oracle.argmax(want)
+    qx, sx = oracle.quantize_act(x)
+    ref = oracle.gemv_batch(m, oracle.dequant_act(qx, sx))
+    yi = N.model_gemv(w, x, act=N.ACT_I8)
+    assert np.abs(yi - ref).max() <= 1e-5
+    assert np.linalg.norm(yi - ref) <= 1e-3 * np.linalg.norm(ref)
+    exact = oracle.gemv_i8_exact(m, qx, sx)
+    assert np.all(np.abs(yi - exact) <= np.spacing(np.abs(exact)))
+    del torch
+    w.free()
