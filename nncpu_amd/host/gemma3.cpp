@@ -482,4 +482,46 @@ int nng_gpu_argmax(void* ctx, const float* x, size_t* row) {
     return nnh_model_argmax(g->w[g->n - 1], x, row, g->act) != NNH_OK;
 }
 
+// ---- the forward's non-matmul ops, one by one ------------------------------------------
+// The functions the forward above calls (and the device decode step repeats
+// operation for operation), exported so the reference's own op tests can be
+// run against them (crates/nncpu/src/kernels/tests.rs:105-147, 242-293,
+// 938-992, 1133-1217, 1263).
+
+void nng_op_exp(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = exp_lane(x[i]);
+}
+
+void nng_op_gelu(float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = gelu_lane(x[i]);
+}
+
+// gelu(gate) * up, in place in gate (the forward's MLP step).
+void nng_op_gelu_mul(float* gate, const float* up, size_t n) {
+    for (size_t i = 0; i < n; ++i) gate[i] = gelu_lane(gate[i]) * up[i];
+}
+
+void nng_op_rmsnorm_gamma(float* y, const float* x, size_t total, size_t dim, const float* gamma, float eps) {
+    rmsnorm_gamma_multi(y, x, total, dim, gamma, eps);
+}
+
+void nng_op_rope_neox(float* x, size_t n_heads, size_t head_dim, size_t n_rot, float pos, float freq_base) {
+    rope_neox(x, n_heads, head_dim, n_rot, pos, freq_base);
+}
+
+// n_keys <= 256 (one block); scores holds n_heads * n_keys floats, part
+// n_heads * (hd + 2).
+void nng_op_attn_block(const float* q, size_t q_stride, const uint16_t* kr, const uint16_t* vr, size_t kv_stride,
+                       size_t n_keys, size_t hd, size_t n_heads, float scale, float* scores, float* part) {
+    attn_block(q, q_stride, kr, vr, kv_stride, n_keys, hd, n_heads, scale, scores, part);
+}
+
+void nng_op_attn_merge(float* acc, const float* part, size_t hd, size_t n_heads) {
+    attn_merge(acc, part, hd, n_heads);
+}
+
+void nng_op_attn_finish(float* out, size_t out_stride, const float* acc, size_t hd, size_t n_heads) {
+    attn_finish(out, out_stride, acc, hd, n_heads);
+}
+
 }  // extern "C"
