@@ -488,44 +488,51 @@ def cpu_time(f, budget_s, min_reps=2):
     return best
 
 
-def cpu_baseline(N, O, inputs):
+def cpu_inputs(N, O, inputs):
+    """The sweep's weights (downloaded from the GPU) and quantized
+    activations (dequantized: the values nncpu's f32 kernel would be fed)."""
+    out = []
+    for w, buf, k in inputs:
+        n = w.rows()
+        off_s, _, _ = N.act_layout(k, 1)
+        a = buf.cpu().numpy()
+        xd = O.dequant_act(a[:k].view(np.int8), a[off_s:off_s + k // 16].view(np.uint16))
+        out.append((O.QMatrix.from_split(2, n, k, w.download()), xd))
+    return out
+
+
+def cpu_baseline(O, sweep):
     """nncpu's AVX2 kernels (restated, oracle/avx2.cpp) on this host's cores,
     as the reference's bench_gemv (kernels/tests.rs:1295-1416) times them:
-    the same weights (downloaded from the GPU), the same quantized
-    activations dequantized (the values nncpu's f32 kernel would be fed),
+    the sweep's own weights and activations (`sweep`, from cpu_inputs),
     >= 256 MB of weight copies rotated so they stream from DRAM, best of
     passes after a warm-up; rows split over threads as pool::for_rows does.
     value: the Q4 sweep at nncpu's default min(8, CPUs) threads; beside it
     the same at 1 thread and at all cores (14336x4096 only), the Q8 vocab
     GEMV, speculative verify at M = 2..16 and the M = 512 prefill as nncpu
-    runs it (32 batches of 16 tokens, session/engine.rs:362-380)."""
+    runs it (32 batches of 16 tokens, session/engine.rs:362-380), on seeded
+    weights of the reference's test generator."""
     if not O.avx_available():
         return None
     host = host_info()
     threads = min(8, host["nproc"])
     t_start = time.time()
-    mats = {}
+    rot = {}
 
-    def rotation(w, k, dtype):
-        n = w.rows()
-        m = O.QMatrix.from_split(dtype, n, k, w.download())
-        copies = max(2, math.ceil((256 << 20) / weight_bytes(dtype, n, k)))
-        return [m] + [O.QMatrix(dtype, n, k, tuple(p.copy() for p in m.parts)) for _ in range(copies - 1)]
-
-    def xdeq(buf, k, m=1):
-        off_s, _, _ = N.act_layout(k, m)
-        a = buf.cpu().numpy()
-        return O.dequant_act(a[:m * k].view(np.int8), a[off_s:off_s + m * k // 16].view(np.uint16))
+    def rotation(i):
+        if i not in rot:
+            m, xd = sweep[i]
+            copies = max(2, math.ceil((256 << 20) / weight_bytes(2, m.rows, m.cols)))
+            rot[i] = ([m] + [O.QMatrix(2, m.rows, m.cols, tuple(p.copy() for p in m.parts))
+                             for _ in range(copies - 1)], xd)
+        return rot[i]
 
     def sweep_rate(th, sel, budget):
         O.avx_set_threads(th)
         tot_b, tot_s, parts = 0, 0.0, []
         for i in sel:
-            w, buf, k = inputs[i]
-            n = w.rows()
-            if i not in mats:
-                mats[i] = (rotation(w, k, 2), xdeq(buf, k))
-            ms, xd = mats[i]
+            ms, xd = rotation(i)
+            n, k = ms[0].rows, ms[0].cols
 
             def one_pass(ms=ms, xd=xd):
                 for mm in ms:
@@ -534,9 +541,10 @@ def cpu_baseline(N, O, inputs):
             tot_b += gemv_bytes(2, n, k)
             tot_s += dt
             parts.append(f"{n}x{k}:{gemv_bytes(2, n, k) / dt / 1e9:.1f}GB/s")
+        log(f"cpu: {th} threads: {', '.join(parts)}")
         return tot_b / tot_s / 1e9, parts
 
-    gbs, parts = sweep_rate(threads, range(len(inputs)), 2.0)
+    gbs, parts = sweep_rate(threads, range(len(sweep)), 2.0)
     g1, _ = sweep_rate(1, [2], 2.0)
     gall, _ = sweep_rate(host["all_cores"], [2], 1.0)
     res = dict(value=round(gbs, 2), unit="GB/s", cores=threads, kind="port",
@@ -546,24 +554,17 @@ def cpu_baseline(N, O, inputs):
                host=host, threads_1_gbs=round(g1, 2), threads_all_gbs=round(gall, 2),
                threads_all=host["all_cores"], per_thread_shape="14336x4096",
                host_stream_gbs_1thread=round(O.avx_stream_gbs(256 << 20, 2), 1))
-    mats.clear()
+    rot.clear()
     O.avx_set_threads(threads)
-    import torch
     rng = O.Rng(0xC9B)
     other = {}
     # Config 3: Gemma-3 vocab lm_head, Q8, M = 1.
     n, k = Q8_VOCAB[0]
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0x5EED03)
-    wt = torch.randn(n * k, generator=g, device="cuda").mul_(0.02)
-    torch.cuda.synchronize()
-    dev = N.Weight.encode_dev(1, wt.data_ptr(), n, k)
-    del wt
-    m = O.QMatrix.from_split(1, n, k, dev.download())
-    dev.free()
+    m = O.QMatrix.from_f32(1, rng.normals(n * k, 0.02).reshape(n, k))
     x = rng.normals(k, 1.0)
     dt = cpu_time(lambda: O.gemv_batch(m, x, backend="avx2"), 1.0)
     other["q8_vocab_262144x1152_m1"] = dict(gbs=round(gemv_bytes(1, n, k) / dt / 1e9, 2), ms=round(dt * 1e3, 3))
+    log(f"cpu: vocab {other['q8_vocab_262144x1152_m1']}")
     del m
     # Config 4: verify at M = 2..16, Q8 6144x1536.
     n, k = VERIFY_SHAPES[0]
@@ -574,6 +575,7 @@ def cpu_baseline(N, O, inputs):
         dt = cpu_time(lambda: O.gemv_batch(m, x, mt, backend="avx2"), 0.5)
         ver[f"M={mt}"] = dict(us=round(dt * 1e6, 1), gflops=round(2 * mt * n * k / dt / 1e9, 1))
     other["verify_q8_6144x1536"] = ver
+    log(f"cpu: verify {ver}")
     # Config 5: the gate projection at M = 512 as 32 calls of 16 tokens.
     n, k = QWEN_PREFILL[2]
     m = O.QMatrix.from_f32(1, rng.normals(n * k, 0.02).reshape(n, k))
@@ -581,11 +583,11 @@ def cpu_baseline(N, O, inputs):
     dt = cpu_time(lambda: O.gemv_batch(m, x, 16, backend="avx2"), 0.5, min_reps=1)
     other["prefill_q8_18944x3584_m512"] = dict(ms=round(32 * dt * 1e3, 1),
                                                gops=round(2 * 512 * n * k / (32 * dt) / 1e9, 1),
-                                               how="32 x gemv_batch(16 tokens), timed one, times 32")
+                                               how="32 x gemv_batch(16 tokens), one timed, times 32")
+    log(f"cpu: prefill {other['prefill_q8_18944x3584_m512']}")
     del m
     res["configs"] = other
     res["wall_s"] = round(time.time() - t_start, 1)
-    log(f"cpu baseline: {res}")
     return res
 
 
@@ -698,7 +700,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import oracle as O  # the CPU baseline leg only
-        cpu = cpu_baseline(N, O, inputs)
+        cpu = cpu_baseline(O, cpu_inputs(N, O, inputs))
     line = dict(metric=result["metric"], value=result["value"], unit=result["unit"], n_gpus=1, steps=args.steps,
                 warmup=args.warmup, ms_per_step=round(result["ms_per_step"], 5), higher_is_better=True,
                 scaling="weak", vs_baseline=None, dtype=result["dtype"], data="synthetic (seeded)",

@@ -254,7 +254,10 @@ public:
         stop_all();
         n_ = n < 1 ? 1 : n;
         quit_.store(false);
-        for (int t = 1; t < n_; ++t) workers_.emplace_back([this, t] { loop(t); });
+        // Each worker starts from the generation current now: a worker that
+        // read it only once running could miss a dispatch issued meanwhile.
+        const uint64_t g0 = gen_.load();
+        for (int t = 1; t < n_; ++t) workers_.emplace_back([this, t, g0] { loop(t, g0); });
     }
     int size() const { return n_; }
     void dispatch(const std::function<void(int, int)>& f) {
@@ -272,8 +275,7 @@ public:
     ~Pool() { stop_all(); }
 
 private:
-    void loop(int tid) {
-        uint64_t seen = gen_.load();
+    void loop(int tid, uint64_t seen) {
         for (;;) {
             int spins = 0;
             uint64_t g;

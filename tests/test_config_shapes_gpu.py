@@ -6,9 +6,10 @@ modes and both weight formats. Each output is checked against the exact sum
 of its block terms (integer block dots, f64) within the kernel's stated f32
 rounding bound, and 8 sampled tokens x all rows against nncpu's own kernel
 (the oracle's restatement of kernels/scalar.rs:626-742) fed the dequantized
-activations, at the north-star tolerance: 1e-5 absolute per element and
-1e-3 relative L2 (kernels/tests.rs:555-639 compare against an f64 gemv the
-same way).
+activations, at the north-star tolerance: 1e-5 absolute per element (against
+the exact value, and against nncpu's kernel up to that kernel's own rounding
+error, which reaches 1.2e-5 for Q4 at K = 18944) and 1e-3 relative L2
+(kernels/tests.rs:555-639 compare against an f64 gemv the same way).
 
 Config 3 (Qwen2.5-7B vocab, 151936 x 3584, M = 1): the f32 path bit for bit
 against the oracle, the int8 path within 1e-5 of the oracle fed x'.
@@ -84,15 +85,24 @@ def check_batch(oracle, m, act, x, xs, y, ys, n_tok):
     assert not bad.any(), (np.argwhere(bad)[:5], (got - exact)[bad][:5], bound[bad][:5])
     sample = sorted(set([0, n_tok - 1] + list(range(0, n_tok, max(1, n_tok // (SAMPLED - 1))))))[:SAMPLED + 1]
     xd = np.concatenate([oracle.dequant_act(qs[t], ss[t]) for t in sample])
-    ref = oracle.gemv_batch(m, xd, len(sample), cols, rows)
-    worst = 0.0
+    ref = oracle.gemv_batch(m, xd, len(sample), cols, rows).astype(np.float64)
+    worst = worst_ref = 0.0
     for i, t in enumerate(sample):
         r = ref[i * rows:(i + 1) * rows]
-        err = np.abs(got[t] - r).max()
-        worst = max(worst, err)
-        assert err <= 1e-5, (t, err)
+        # nncpu's own f32 chains are |r - exact[t]| from the exact product of
+        # the same quantized operands: up to ~1.2e-5 for Q4 at K = 18944, so
+        # there no result but nncpu's own bits is within 1e-5 of r
+        # everywhere. The tolerance is then taken against the exact value,
+        # and against r up to nncpu's own deviation; where nncpu is within
+        # 5e-6 of exact, within 1e-5 of r outright.
+        own = np.abs(r - exact[t])
+        assert np.all(np.abs(got[t] - exact[t]) <= 1e-5), t
+        assert np.all(np.abs(got[t] - r) <= 1e-5 + own), t
+        assert np.all(np.abs(got[t] - r)[own <= 5e-6] <= 1e-5), t
         assert np.linalg.norm(got[t] - r) <= 1e-3 * np.linalg.norm(r), t
-    say(f"  max |y - nncpu(x')| over {len(sample)} tokens: {worst:.3g}")
+        worst = max(worst, np.abs(got[t] - r).max())
+        worst_ref = max(worst_ref, own.max())
+    say(f"  over {len(sample)} tokens: max |y - nncpu(x')| {worst:.3g}, max |nncpu(x') - exact| {worst_ref:.3g}")
 
 
 QWEN_M512 = [
