@@ -234,6 +234,24 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
 size_t nnh_argmax_work_bytes(size_t n);
 int nnh_argmax_dev(const float* v, size_t n, void* work, uint64_t* out_row, void* stream);
 
+/* nnh_gemv_batch_dev for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): no
+ * counterpart in the reference. Its scratch (Q4 block sums, quantized
+ * activations, split-K partials) is one device array of
+ * NNH_NOALLOC_SCRATCH_BYTES that the library holds on each GPU for the life
+ * of the process; the call allocates nothing. Preconditions beyond
+ * nnh_gemv_batch_dev's: nnh_init has run, and the weight's layouts for this
+ * (act, n_tok) exist (nnh_weight_prepare, or an earlier nnh_gemv_batch_dev
+ * call), else NNH_E_STATE; a call needing more scratch than the maximum
+ * fails with NNH_E_INVALID (every call of up to 16 vectors fits at the
+ * BASELINE shapes; large prefill batches may not). Every such call on one
+ * GPU shares the array, whatever the stream: calls that overlap on one GPU
+ * race (serialise them, e.g. on one stream). Nothing in the array needs to
+ * start at zero: a call writes all it reads. */
+#define NNH_NOALLOC_SCRATCH_BYTES (64u << 20)
+int nnh_gemv_batch_dev_noalloc(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
+                               size_t n_tok, int act, void* stream);
+
 /* ---- int8 activation blocks (device memory, caller-owned) ----
  * An activation buffer holds n_tok vectors of `cols` values quantized with
  * nncpu's Q8_0 encoder, laid out as:

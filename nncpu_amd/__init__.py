@@ -27,7 +27,7 @@ ACT_MXI8 = NNH_ACT_MXI8
 
 __all__ = [
     "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "ACT_MXI8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
-    "gemv_batch_dev", "model_argmax_dev", "model_argmax_work_bytes", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
+    "gemv_batch_dev", "gemv_batch_dev_noalloc", "model_argmax_dev", "model_argmax_work_bytes", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
     "act_layout_ex", "quantize_act_ex_dev", "gemv_act_dev",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
@@ -203,6 +203,13 @@ def model_argmax(w: Weight, x: np.ndarray, act: int = ACT_F32) -> int:
 def gemv_batch_dev(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,
                    act: int = ACT_F32, stream: int = 0) -> None:
     check(lib().nnh_gemv_batch_dev(w.handle, x_ptr, x_stride, y_ptr, y_stride, n_tok, act, stream or None))
+
+
+def gemv_batch_dev_noalloc(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,
+                           act: int = ACT_F32, stream: int = 0) -> None:
+    """gemv_batch_dev with the library's fixed device scratch: allocates
+    nothing (the weight must be prepared for (act, n_tok) first)."""
+    check(lib().nnh_gemv_batch_dev_noalloc(w.handle, x_ptr, x_stride, y_ptr, y_stride, n_tok, act, stream or None))
 
 
 def model_argmax_work_bytes(w: Weight) -> int:

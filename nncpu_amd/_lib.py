@@ -17,6 +17,7 @@ HEADER = os.path.join(ROOT, "include", "nncpu_hip.h")
 NNH_OK, NNH_E_INVALID, NNH_E_OOM, NNH_E_DEVICE, NNH_E_STATE = 0, 1, 2, 3, 4
 NNH_Q8_0, NNH_Q4S, NNH_BF16 = 1, 2, 3
 NNH_ACT_F32, NNH_ACT_I8, NNH_ACT_MXI8 = 0, 1, 2
+NNH_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class NnhError(RuntimeError):
@@ -81,6 +82,8 @@ def _declare(L):
     L.nnh_gemv_batch.argtypes, L.nnh_gemv_batch.restype = [vp, vp, sz, vp, sz, sz, i32], i32
     L.nnh_model_argmax.argtypes, L.nnh_model_argmax.restype = [vp, vp, P(sz), i32], i32
     L.nnh_gemv_batch_dev.argtypes, L.nnh_gemv_batch_dev.restype = [vp, vp, sz, vp, sz, sz, i32, vp], i32
+    L.nnh_gemv_batch_dev_noalloc.argtypes = [vp, vp, sz, vp, sz, sz, i32, vp]
+    L.nnh_gemv_batch_dev_noalloc.restype = i32
     L.nnh_act_layout.argtypes, L.nnh_act_layout.restype = [sz, sz, P(sz), P(sz), P(sz)], i32
     L.nnh_quantize_act_dev.argtypes, L.nnh_quantize_act_dev.restype = [vp, sz, sz, sz, vp, vp], i32
     L.nnh_gemv_i8_dev.argtypes, L.nnh_gemv_i8_dev.restype = [vp, vp, sz, vp, sz, vp], i32

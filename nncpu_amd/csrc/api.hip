@@ -61,6 +61,14 @@ std::vector<uint8_t*> g_retired;
 uint8_t* g_pinned = nullptr;  // pinned host staging for the host-buffer calls
 size_t g_pinned_bytes = 0;
 
+// The scratch of nnh_gemv_batch_dev_noalloc, for callers that cannot
+// allocate: a device array each GPU holds for the process's lifetime, at its
+// own address, looked up once per device at init (g_noalloc). Host code
+// never passes the array's name to a kernel or copy: in host code it is a
+// stand-in, not a device address.
+static __device__ __align__(256) uint8_t scratch[NNH_NOALLOC_SCRATCH_BYTES];
+uint8_t* g_noalloc = nullptr;  // device address of `scratch` on g_device
+
 int fail(int code, const std::string& msg) {
     t_err = msg;
     return code;
@@ -92,7 +100,11 @@ int init_locked(int device) {
     NNH_HIP(hipGetDeviceProperties(&prop, device));
     if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
         return fail(NNH_E_STATE, std::string("nnh_init: built for gfx950, device is ") + prop.gcnArchName);
+    void* na = nullptr;
+    NNH_HIP(hipGetSymbolAddress(&na, HIP_SYMBOL(scratch)));
+    if (!na) return fail(NNH_E_DEVICE, "nnh_init: no device address for the no-alloc scratch");
     NNH_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    g_noalloc = (uint8_t*)na;
     g_device = device;
     return NNH_OK;
 }
@@ -758,6 +770,29 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
     const size_t xs = n_tok > 1 ? x_stride : w->cols;
     const size_t ys = n_tok > 1 ? y_stride : w->rows;
     return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
+}
+
+int nnh_gemv_batch_dev_noalloc(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
+                               size_t n_tok, int act, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    if (g_device < 0 || !g_noalloc) return fail(NNH_E_STATE, "gemv noalloc: call nnh_init first");
+    NNH_HIP(hipSetDevice(g_device));
+    int rc = check_call(w, x_stride, y_stride, n_tok, act);
+    if (rc) return rc;
+    if (n_tok == 0) return NNH_OK;
+    if (!x || !y) return fail(NNH_E_INVALID, "gemv noalloc: null x or y");
+    const unsigned need = layouts_for(w, act, n_tok);
+    if ((w->ready & need) != need)
+        return fail(NNH_E_STATE, "gemv noalloc: the weight's layouts for this mode and batch are not built "
+                                 "(nnh_weight_prepare, or one call of nnh_gemv_batch_dev, builds them)");
+    const size_t bytes = gemv_scratch_bytes(w, n_tok, act);
+    if (bytes > (size_t)NNH_NOALLOC_SCRATCH_BYTES)
+        return fail(NNH_E_INVALID, "gemv noalloc: this call needs " + std::to_string(bytes) +
+                                       " bytes of scratch, more than the no-alloc maximum of " +
+                                       std::to_string((size_t)NNH_NOALLOC_SCRATCH_BYTES));
+    const size_t xs = n_tok > 1 ? x_stride : w->cols;
+    const size_t ys = n_tok > 1 ? y_stride : w->rows;
+    return run_gemv(w, x, xs, y, ys, n_tok, act, g_noalloc, (hipStream_t)stream);
 }
 
 int nnh_act_layout_ex(int act, size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes) {
