@@ -1,9 +1,10 @@
 """Gemma-3 decode through the GPU matmul.
 
-A Gemma-3-architecture model with seeded random weights: every weight matrix
-is 0.02*N(0,1) (a seeded torch generator on the GPU), re-encoded to nncpu's
-Q8_0 layout by the library's device encoder (nncpu's load-time encoder, bit
-for bit), norms 1 + 0.1*N(0,1). The forward pass is nncpu's
+A Gemma-3-architecture model loaded from a GGUF file (nncpu_amd.gguf writes
+the seeded random-init one: matrices 0.02*N(0,1) as BF16, norms
+1 + 0.1*N(0,1)), every matrix decoded and re-encoded to nncpu's Q8_0 layout
+on the device (nncpu's load-time decode and encoder, bit for bit). The
+forward pass is nncpu's
 (nncpu_amd/host/gemma3.cpp, restating crates/nncpu/src/model/forward.rs) on
 the CPU; its weight matmuls run through `nnh_gemv_batch` in the bit-exact
 f32 mode and the greedy lm_head through `nnh_model_argmax`. The prompt is
@@ -80,27 +81,60 @@ def _gemma_lib():
 
 
 class Gemma3:
-    """Device weights of a seeded random Gemma-3 model, plus the host copies
-    (norms, the Q8_0 embedding table) the CPU forward reads."""
+    """Device weights of a Gemma-3 model (nncpu's Q8_0 layout), plus the
+    host copies (norms, the Q8_0 embedding table) the CPU forward reads."""
 
-    def __init__(self, cfg: NngConfig, seed: int = 0x6E33A):
-        import torch
+    def __init__(self, cfg: NngConfig, weights: list[Weight], norms: np.ndarray):
         self.cfg = cfg
         self.shapes = matrix_shapes(cfg)
-        self.weights: list[Weight] = []
-        g = torch.Generator(device="cuda")
-        for i, (r, c) in enumerate(self.shapes):
-            g.manual_seed(seed + i)
-            w = torch.randn(r * c, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
-            torch.cuda.synchronize()
-            self.weights.append(Weight.encode_dev(Q8_0, w.data_ptr(), r, c))
-            del w
-        rng = np.random.default_rng(seed)
-        E, hd = cfg.n_embd, cfg.head_dim
-        n_norm = (4 * E + 2 * hd) * cfg.n_layer + E
-        self.norms = (1.0 + 0.1 * rng.standard_normal(n_norm)).astype(np.float32)
+        self.weights = weights
+        self.norms = np.ascontiguousarray(norms, np.float32)
         self.token_embd = self.weights[-1].download()  # the tied embedding / lm_head table
         self._lib = _gemma_lib()
+
+    @classmethod
+    def from_gguf(cls, path: str, n_ctx: int = 256, dtype: int = Q8_0) -> "Gemma3":
+        """Load a Gemma-3 GGUF as nncpu's loader does (model/load.rs:881-1288
+        for the hyperparameters and names): every matrix decoded from its
+        ggml type to f32 and re-encoded to `dtype` on the device
+        (nnh_upload_gguf: load.rs:182-243 on the GPU), the norm vectors as
+        f32, the lm_head tied to token_embd (model/mod.rs:366-372)."""
+        from .gguf import GgufFile
+        f = GgufFile(path)
+        kv = f.kv
+        if kv.get("general.architecture") != "gemma3":
+            raise ValueError(f"{path}: not a gemma3 model")
+        a = "gemma3."
+        E, nh = int(kv[a + "embedding_length"]), int(kv[a + "attention.head_count"])
+        hd = int(kv.get(a + "attention.key_length", E // nh))
+        cfg = NngConfig(n_layer=int(kv[a + "block_count"]), n_embd=E, n_head=nh,
+                        n_kv=int(kv.get(a + "attention.head_count_kv", nh)), head_dim=hd,
+                        n_ff=int(kv[a + "feed_forward_length"]), n_vocab=len(kv["tokenizer.ggml.tokens"]),
+                        n_ctx=n_ctx, rms_eps=float(kv.get(a + "attention.layer_norm_rms_epsilon", 1e-6)),
+                        rope_base=float(kv.get(a + "rope.freq_base", 10000.0)), rope_base_swa=10000.0,
+                        attn_scale=float(kv.get(a + "attention.scale", 1.0 / hd ** 0.5)),
+                        window=int(kv.get(a + "attention.sliding_window", 0)), swa_period=6)
+
+        def mat(name):
+            t = f.tensors[name]
+            return Weight.from_gguf(t.ggml_type, t.data, t.rows, t.cols, dtype)
+
+        def vec(name):
+            t = f.tensors[name]
+            if t.ggml_type != 0:
+                raise ValueError(f"{name}: norm vectors are read as F32")
+            return np.asarray(t.data).view(np.float32)
+
+        weights, norms = [], []
+        for li in range(cfg.n_layer):
+            b = f"blk.{li}."
+            weights += [mat(b + n) for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                                              "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight")]
+            norms += [vec(b + n) for n in ("attn_norm.weight", "attn_q_norm.weight", "attn_k_norm.weight",
+                                            "post_attention_norm.weight", "ffn_norm.weight", "post_ffw_norm.weight")]
+        weights.append(mat("token_embd.weight"))
+        norms.append(vec("output_norm.weight"))
+        return cls(cfg, weights, np.concatenate(norms))
 
     def generate(self, prompt: np.ndarray, n_gen: int, gemv_ptr: int, argmax_ptr: int | None, ctx,
                  batch: int = 16):
@@ -187,6 +221,22 @@ class Gemma3:
         if getattr(self, "_dev", None) is not None:
             self._lib.nngd_free(self._dev)
             self._dev = None
+
+
+def gemma3_1b_gguf(path: str | None = None, seed: int = 0x6E33A, n_ctx: int = 256, n_layer: int = 26,
+                   n_vocab: int = 262144) -> str:
+    """BASELINE config 1's model file: the Gemma-3-1B-architecture random-init
+    GGUF from `seed` (nncpu_amd.gguf.write_gemma3, BF16 matrices), written to
+    `path` (default: the temp directory) unless a file of that name exists."""
+    import tempfile
+    from .gguf import write_gemma3
+    if path is None:
+        path = os.path.join(tempfile.gettempdir(), f"nncpu-amd-gemma3-{n_layer}x{n_vocab}-{seed:x}.gguf")
+    if not os.path.exists(path):
+        tmp = path + f".tmp{os.getpid()}"
+        write_gemma3(tmp, gemma3_1b_config(n_ctx=n_ctx, n_layer=n_layer, n_vocab=n_vocab), seed)
+        os.replace(tmp, path)
+    return path
 
 
 def random_prompt(n: int, n_vocab: int, seed: int = 0x9A0) -> np.ndarray:

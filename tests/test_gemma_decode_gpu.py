@@ -1,9 +1,13 @@
 """Gemma-3-1B-architecture greedy decode with the GPU matmul
 is token-identical to the same decode with nncpu's CPU gemv.
 
-Random Gemma-3-1B-shaped weights (26 layers, d 1152, FFN 6912, 4 / 1 heads,
-head_dim 256, vocab 262144) in nncpu's Q8_0 layout; a 32-token uniform-random
-prompt evaluated in 16-token batches, then 128 greedy tokens. The CPU run
+The model is the random-init GGUF from a seed (nncpu_amd.gguf.write_gemma3:
+26 layers, d 1152, FFN 6912, 4 / 1 heads, head_dim 256, vocab 262144, BF16
+matrices drawn from the reference's test generator), loaded as nncpu loads
+it: each matrix decoded and re-encoded to Q8_0 (on the device, through
+nnh_upload_gguf; checked bit for bit against the oracle's encoder below); a
+32-token uniform-random prompt evaluated in 16-token batches, then 128
+greedy tokens. The CPU run
 uses the AVX2 restatement of nncpu's gemv (bit-equal to the scalar oracle,
 tests/test_oracle.py) on the same weight bytes; both runs share the CPU
 forward (nncpu_amd/host/gemma3.cpp). Tokens and the per-layer residual
@@ -29,9 +33,23 @@ def model():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     import nncpu_amd as N
-    from nncpu_amd.gemma import Gemma3, gemma3_1b_config
+    from nncpu_amd.gemma import Gemma3, gemma3_1b_gguf
     N.init(0)
-    return Gemma3(gemma3_1b_config(n_ctx=256))
+    print("writing / loading the GGUF", flush=True)
+    return Gemma3.from_gguf(gemma3_1b_gguf(), n_ctx=256)
+
+
+def test_gguf_load_reencodes_like_nncpu(oracle, model):
+    # The device decode + re-encode of a BF16 GGUF matrix (load.rs:182-243)
+    # gives the oracle encoder's bytes for the same decoded values.
+    from nncpu_amd.gemma import gemma3_1b_gguf
+    from nncpu_amd.gguf import GgufFile
+    f = GgufFile(gemma3_1b_gguf())
+    for idx, name in ((0, "blk.0.attn_q.weight"), (7 * 3 + 6, "blk.3.ffn_down.weight")):
+        t = f.tensors[name]
+        vals = oracle.bf16_array_to_f32(np.asarray(t.data).view(np.uint16)).reshape(t.rows, t.cols)
+        want = oracle.QMatrix.from_f32(1, vals).buf
+        assert np.array_equal(model.weights[idx].download(), want), name
 
 
 def cpu_generate(oracle, model, prompt, n_gen):
