@@ -274,10 +274,13 @@ int nnh_gemv_i8_dev(const nnh_weight* w, const void* act, size_t n_tok, float* y
 
 /* The same for either int8 mode (act = NNH_ACT_I8 or NNH_ACT_MXI8): the
  * buffer's layout (the MXI8 buffer is the NNH_ACT_I8 layout followed by the
- * GEMM's BF16 operands xb[n_tok][cols] = q 2^E and xl[P][nbp8][2] = the two
- * BF16 limbs of 2^E sum(q) per block, nbp8 = cols/32 rounded up to a
- * multiple of 8), the quantizer, and y = W x from a quantized buffer. The
- * act-less functions above are these with NNH_ACT_I8. No counterpart in the
+ * GEMM's BF16 operands: xb = q 2^E in tiles of 256 tokens,
+ * xb[T][cols/32][256][32] for T = n_tok rounded up to whole tiles, zero for
+ * tokens past n_tok, the 16-byte chunk c of each 32-value row stored at
+ * position c ^ ((t % 256 >> 2) & 3); and xl[P][nbp8][2] = the two BF16 limbs
+ * of 2^E sum(q) per block, nbp8 = cols/32 rounded up to a multiple of 8),
+ * the quantizer, and y = W x from a quantized buffer. The act-less
+ * functions above are these with NNH_ACT_I8. No counterpart in the
  * reference (see NNH_ACT_MXI8). */
 int nnh_act_layout_ex(int act, size_t cols, size_t n_tok, size_t* off_s, size_t* off_sx, size_t* bytes);
 int nnh_quantize_act_ex_dev(int act, const float* x, size_t x_stride, size_t cols, size_t n_tok, void* buf,

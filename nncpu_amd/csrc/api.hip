@@ -163,7 +163,7 @@ ActLayout act_layout(size_t cols, size_t n_tok, int act = NNH_ACT_I8) {
     l.off_xl = l.off_xb;
     l.bytes = l.off_xb;
     if (act == NNH_ACT_MXI8) {
-        l.off_xl = l.off_xb + align_up(n_tok * cols * 2);
+        l.off_xl = l.off_xb + align_up((size_t)nnh::mx_xl_tok((int)n_tok) * cols * 2);
         l.bytes = l.off_xl + align_up(nnh::mx_xl_bytes((int)n_tok, (int)nb));
     }
     return l;

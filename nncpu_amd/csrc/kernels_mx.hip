@@ -61,6 +61,7 @@ constexpr int MX_KS = 2;           // blocks per ring stage
 constexpr int MX_NS = 4;           // stages per 8-block group
 constexpr int MX_GRP = 8;          // blocks per group
 constexpr int MX_FOLD_GROUPS = 2;  // groups per f32 chunk before the f64 fold
+constexpr int MX_TM_Q = 256;       // tokens per GEMM tile (the quantizer's xb tiles, = MX_TM)
 constexpr int MX_MIN_UNITS = 2;    // groups per workgroup at least
 static_assert(MX_KS * MX_NS == MX_GRP, "whole stages per group");
 
@@ -89,7 +90,8 @@ __device__ __forceinline__ int mx_exponent(float amax) {
 
 // One 32-lane half-wave per block of 32 values; blocks past nb (up to the
 // group-padded nbp8) and tokens past n_tok (up to xl_tok, whole GEMM token
-// tiles) only write the zero limbs of xl.
+// tiles) only write zeros: the limbs of xl, and for tokens past n_tok the
+// xb values.
 __global__ __launch_bounds__(256) void quantize_mx_kernel(const float* __restrict__ x, size_t x_stride, int cols,
                                                           int n_tok, int nbp8, int8_t* __restrict__ q,
                                                           uint16_t* __restrict__ s, double* __restrict__ sx,
@@ -100,8 +102,13 @@ __global__ __launch_bounds__(256) void quantize_mx_kernel(const float* __restric
     const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
     if (blk >= nbp8 * xl_tok) return;  // uniform per half-wave
     const int t = blk / nbp8, b = blk - t * nbp8;
+    // xb tiled: [token tile][block][token in tile][32], 16-byte chunks of a
+    // row swizzled as the GEMM's LDS rows are (chunk c at c ^ ((row >> 2) & 3)).
+    const int tt = t / MX_TM_Q, tr = t % MX_TM_Q;
+    const size_t xe = (((size_t)tt * nb + b) * MX_TM_Q + tr) * 32 + (((k >> 3) ^ ((tr >> 2) & 3)) << 3) + (k & 7);
     if (b >= nb || t >= n_tok) {
         if (k < 2) xl[((size_t)t * nbp8 + b) * 2 + k] = 0;
+        if (b < nb) xb[xe] = 0;
         return;
     }
     const float v = x[(size_t)t * x_stride + 32 * (size_t)b + k];
@@ -121,7 +128,7 @@ __global__ __launch_bounds__(256) void quantize_mx_kernel(const float* __restric
     const size_t e = (size_t)t * cols + 32 * (size_t)b + k;
     q[e] = (int8_t)qi;
     // q 2^E as BF16: at most 7 significant bits, so the f32's low half is zero.
-    xb[e] = (uint16_t)(__float_as_uint((float)qi * scale) >> 16);
+    xb[xe] = (uint16_t)(__float_as_uint((float)qi * scale) >> 16);
     if (k == 0) {
         const float X = scale * (float)qsum;  // exact: <= 12 significant bits
         s[(size_t)t * nb + b] = (uint16_t)(__float_as_uint(scale) >> 16);
@@ -139,13 +146,19 @@ __global__ __launch_bounds__(256) void quantize_mx_kernel(const float* __restric
 
 // ---- upload-time weight copies -------------------------------------------------
 
-// wbf[n][32b + k] = BF16 of quant k of block b (exact: Q8 -127..127, Q4
-// 0..15, nncpu's nibble order: byte i low = element i, high = element i+16);
-// zero in the pad rows (n up to the next multiple of 128).
+// BF16 of quant k of block b of row n (exact: Q8 -127..127, Q4 0..15,
+// nncpu's nibble order: byte i low = element i, high = element i+16), zero
+// in the pad rows (n up to the next multiple of 128), stored tiled as the
+// GEMM loads it: [n / 128][b][n % 128][32], the 16-byte chunk c of a row at
+// position c ^ ((n % 128 >> 2) & 3).
 __global__ void mx_weights_kernel(int dtype, const uint8_t* __restrict__ qs, uint16_t* __restrict__ wbf, size_t n,
-                                  size_t n_pad) {
+                                  size_t n_pad, int nb) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_pad) return;
+    const size_t row = i / ((size_t)nb * 32), rb = i - row * nb * 32;
+    const size_t bb = rb >> 5;
+    const int kk = (int)(rb & 31), rt = (int)(row / 128), rr = (int)(row % 128);
+    const size_t dst = (((size_t)rt * nb + bb) * 128 + rr) * 32 + (((kk >> 3) ^ ((rr >> 2) & 3)) << 3) + (kk & 7);
     int v;
     if (i >= n) {
         v = 0;
@@ -157,7 +170,7 @@ __global__ void mx_weights_kernel(int dtype, const uint8_t* __restrict__ qs, uin
         const uint8_t byte = qs[blk * 16 + (k & 15)];
         v = k < 16 ? (byte & 15) : (byte >> 4);
     }
-    wbf[i] = (uint16_t)(__float_as_uint((float)v) >> 16);
+    wbf[dst] = (uint16_t)(__float_as_uint((float)v) >> 16);
 }
 
 // Q4 biases twice per block, [rows_pad][nbp8][2], zero past nb and in the pad
@@ -209,10 +222,10 @@ struct MxPlan {
 static_assert(sizeof(MxStage) * 3 + sizeof(MxBias) <= 160 * 1024, "three stages and the bias operands fit the LDS");
 
 struct MxArgs {
-    const uint16_t* wbf;  // [rows_pad][cols] BF16 quants
+    const uint16_t* wbf;  // [row tile][nb][128][32] BF16 quants (chunks swizzled)
     const float* swT;     // [nb + 1][rows_pad] f32 weight scales
     const uint16_t* wbi;  // Q4: [rows_pad][nbp8][2] BF16 biases, twice
-    const uint16_t* xb;   // [n_tok][cols] BF16 q_x 2^E
+    const uint16_t* xb;   // [token tile][nb][256][32] BF16 q_x 2^E (chunks swizzled)
     const uint16_t* xl;   // [xl_tok][nbp8][2] BF16 limbs of X
     float* ws;            // [team * mtiles + mt][2][8 waves][4 tiles][16][64] partial tiles
     float* y;
@@ -232,23 +245,23 @@ __device__ __forceinline__ long team_start(long team, long units, int teams) { r
 __device__ __forceinline__ int mx_swz(int c, int r) { return c ^ ((r >> 2) & 3); }
 
 // A lane's byte offsets for its loads, fixed for the kernel: each load is a
-// uniform (scalar) base plus one of these. Wave w's A instructions cover
-// token rows 16 w + lane / 4 (a0) and 128 + 16 w + lane / 4 (a1) of each
-// block, its B instructions weight rows 16 w + lane / 4; chunk
-// mx_swz(lane % 4, row) of each.
+// uniform (scalar) base plus one of these. The operands are stored tiled
+// (xb [token tile][block][256 tokens][32], wbf [row tile][block][128 rows]
+// [32], chunks already swizzled), so each 1 KB load is 1 KB of consecutive
+// bytes: wave w's A instructions cover token rows 16 w .. 16 w + 15 (a0)
+// and 128 + 16 w .. (a1) of a block, its B instructions weight rows
+// 16 w .. 16 w + 15; lane l's 16 bytes are row l / 4's chunk position l % 4,
+// which holds chunk mx_swz(l % 4, row) of the row.
 struct MxLane {
     uint32_t a0, a1, b, bias, sw;
 };
 
 __device__ __forceinline__ MxLane mx_lane(const MxArgs& g, int wave, int lane, int m0) {
     MxLane o;
-    const int r = wave * 16 + (lane >> 2);
-    const int c0 = mx_swz(lane & 3, r), c1 = mx_swz(lane & 3, r + 128);
-    const int t0 = m0 + r < g.n_tok ? m0 + r : g.n_tok - 1;
-    const int t1 = m0 + 128 + r < g.n_tok ? m0 + 128 + r : g.n_tok - 1;
-    o.a0 = (uint32_t)((size_t)t0 * g.cols * 2 + 16 * c0);
-    o.a1 = (uint32_t)((size_t)t1 * g.cols * 2 + 16 * c1);
-    o.b = (uint32_t)((size_t)r * g.cols * 2 + 16 * c0);
+    (void)m0;
+    o.a0 = (uint32_t)(wave * 1024 + lane * 16);
+    o.a1 = (uint32_t)(8192 + wave * 1024 + lane * 16);
+    o.b = (uint32_t)(wave * 1024 + lane * 16);
     o.bias = (uint32_t)((lane >> 1) * g.nbp8 * 4 + 16 * (lane & 1));
     o.sw = (uint32_t)((lane >> 5) * g.rows_pad * 4 + 16 * (lane & 31));
     return o;
@@ -266,26 +279,25 @@ __device__ __forceinline__ void lds_load(const void* base, uint32_t voff, void* 
 }
 
 // Issue this wave's loads of the stage holding blocks 2 j, 2 j + 1 of group
-// gi of row tile rt. Tokens past the end are clamped to the last one and
-// blocks past nb to the last block (never computed); weight rows and X
-// limbs are padded to whole tiles with zeros; the scale table has a spare
-// block row past nb.
+// gi of row tile rt. Blocks past nb are clamped to the last block (never
+// computed); tokens, weight rows and X limbs are padded to whole tiles with
+// zeros; the scale table has a spare block row past nb.
 template <int DT>
 __device__ __forceinline__ void mx_issue(MxStage& st, MxBias& bias, const MxArgs& g, const MxLane& o, int rt, int gi,
                                          int j, int wave, int m0) {
     const int n0 = rt * MX_TN;
     const int b0 = gi * MX_GRP + j * MX_KS;
     const int bA = b0 < g.nb ? b0 : g.nb - 1, bB = b0 + 1 < g.nb ? b0 + 1 : g.nb - 1;
-    const uint8_t* xb = (const uint8_t*)g.xb;
-    const uint8_t* wb = (const uint8_t*)g.wbf + (size_t)n0 * g.cols * 2;
+    const uint8_t* xb = (const uint8_t*)g.xb + (size_t)(m0 / MX_TM) * g.nb * (MX_TM * 64);
+    const uint8_t* wb = (const uint8_t*)g.wbf + (size_t)rt * g.nb * (MX_TN * 64);
     uint8_t* A = (uint8_t*)&st.A[0][0][0];
     uint8_t* B = (uint8_t*)&st.B[0][0][0];
-    lds_load(xb + (size_t)bA * 64, o.a0, A + wave * 1024);
-    lds_load(xb + (size_t)bA * 64, o.a1, A + (wave + 8) * 1024);
-    lds_load(xb + (size_t)bB * 64, o.a0, A + (wave + 16) * 1024);
-    lds_load(xb + (size_t)bB * 64, o.a1, A + (wave + 24) * 1024);
-    lds_load(wb + (size_t)bA * 64, o.b, B + wave * 1024);
-    lds_load(wb + (size_t)bB * 64, o.b, B + (wave + 8) * 1024);
+    lds_load(xb + (size_t)bA * (MX_TM * 64), o.a0, A + wave * 1024);
+    lds_load(xb + (size_t)bA * (MX_TM * 64), o.a1, A + (wave + 8) * 1024);
+    lds_load(xb + (size_t)bB * (MX_TM * 64), o.a0, A + (wave + 16) * 1024);
+    lds_load(xb + (size_t)bB * (MX_TM * 64), o.a1, A + (wave + 24) * 1024);
+    lds_load(wb + (size_t)bA * (MX_TN * 64), o.b, B + wave * 1024);
+    lds_load(wb + (size_t)bB * (MX_TN * 64), o.b, B + (wave + 8) * 1024);
     if (wave == 0) lds_load((const uint8_t*)g.swT + ((size_t)bA * g.rows_pad + n0) * 4, o.sw, &st.SW[0][0]);
     if (DT == 2 && j == 3) {
         // Bias pieces 0..11 are instructions 49..60: waves 1..7 take pieces
@@ -676,7 +688,7 @@ void launch_mx_weights(int dtype, const uint8_t* qs, const uint16_t* bi, int row
                        uint16_t* wbi, hipStream_t st) {
     const int rp = gemm_rows_pad(rows);
     const size_t n = (size_t)rows * nb * 32, n_pad = (size_t)rp * nb * 32;
-    mx_weights_kernel<<<(unsigned)((n_pad + 255) / 256), 256, 0, st>>>(dtype, qs, wbf, n, n_pad);
+    mx_weights_kernel<<<(unsigned)((n_pad + 255) / 256), 256, 0, st>>>(dtype, qs, wbf, n, n_pad, nb);
     if (dtype == 2) {
         const size_t m = (size_t)rp * mx_nbp8(nb);
         mx_bias_kernel<<<(unsigned)((m + 255) / 256), 256, 0, st>>>(bi, wbi, rows, rp, nb, mx_nbp8(nb));

@@ -56,15 +56,15 @@ def test_init_without_gpu_fails_cleanly():
 
 
 def test_mx_act_layout_extends_the_int8_layout():
-    # The MX buffer is the NNH_ACT_I8 layout followed by xb[n_tok][cols] BF16
-    # and xl[n_tok rounded up to 256][cols/32 rounded up to 8][2] BF16
+    # The MX buffer is the NNH_ACT_I8 layout followed by xb (BF16, tokens in
+    # tiles of 256) and xl[n_tok rounded up to 256][cols/32 rounded up to 8][2] BF16
     # (include/nncpu_hip.h); the int8 kernels read its prefix unchanged.
     for cols, n_tok in [(32, 1), (1152, 3), (4096, 17), (18944, 512), (96, 300)]:
         s8, sx8, b8 = N.act_layout_ex(N.ACT_I8, cols, n_tok)
         assert (s8, sx8, b8) == N.act_layout(cols, n_tok)
         s, sx, b = N.act_layout_ex(N.ACT_MXI8, cols, n_tok)
         assert (s, sx) == (s8, sx8)
-        xb = (n_tok * cols * 2 + 255) // 256 * 256
+        xb = ((n_tok + 255) // 256 * 256) * cols * 2
         nbp8 = (cols // 32 + 7) // 8 * 8
         xl = (((n_tok + 255) // 256 * 256) * nbp8 * 4 + 255) // 256 * 256
         assert b == b8 + xb + xl

@@ -67,12 +67,19 @@ def mx_buffer(x, cols, n_tok, xs):
     nbp8 = (nb + 7) // 8 * 8
     tok_pad = (n_tok + 127) // 128 * 128
     off_xb = i8_bytes
-    off_xl = off_xb + align(n_tok * cols * 2)
+    off_xl = off_xb + align((n_tok + 255) // 256 * 256 * cols * 2)
+    tiles = (n_tok + 255) // 256
+    # xb: [tile][block][256 tokens][32], chunk c of a row at c ^ ((row >> 2) & 3)
+    xt = a[off_xb:off_xb + tiles * 256 * cols * 2].view(np.uint16).reshape(tiles, nb, 256, 4, 8)
+    rows = np.arange(256)
+    unswz = np.stack([xt[:, :, rows, c ^ ((rows >> 2) & 3), :] for c in range(4)], axis=3)  # [tile][b][row][c][8]
+    xb_all = unswz.transpose(0, 2, 1, 3, 4).reshape(tiles * 256, cols)
     f = dict(
         q=a[:n_tok * cols].view(np.int8).reshape(n_tok, cols),
         s=a[off_s:off_s + n_tok * nb * 2].view(np.uint16).reshape(n_tok, nb),
         sx=a[off_sx:off_sx + n_tok * nb * 16].view(np.float64).reshape(n_tok, nb, 2),
-        xb=a[off_xb:off_xb + n_tok * cols * 2].view(np.uint16).reshape(n_tok, cols),
+        xb=xb_all[:n_tok],
+        xb_pad=xb_all[n_tok:],
         xl=a[off_xl:off_xl + tok_pad * nbp8 * 4].view(np.uint16).reshape(tok_pad, nbp8, 2),
     )
     return buf, f
@@ -119,6 +126,7 @@ def test_mx_quantizer_buffer_bit_exact(oracle, cols, n_tok):
         assert np.array_equal(f["xl"][t][:nb, 0], hi) and np.array_equal(f["xl"][t][:nb, 1], lo)
         assert np.all(f["xl"][t][nb:] == 0)
     assert np.all(f["xl"][n_tok:] == 0)  # pad tokens
+    assert np.all(f["xb_pad"] == 0)
     assert nbp8 % 8 == 0
 
 
