@@ -614,7 +614,7 @@ def gemma_decode(args, N, cpu: bool):
     out = dict(config="gemma-3-1b architecture, random-init GGUF from seed (BF16 matrices 0.02*N(0,1) from the "
                       "reference's test generator) re-encoded to Q8_0 on load, 32-token prompt, 128 greedy tokens",
                tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
-               prefill_s=round(tp, 4), kernels_per_token=5 * m.cfg.n_layer + 4)
+               prefill_s=round(tp, 4), kernels_per_token=4)
     log(f"gemma3-1b device decode: {out['tok_s']} tok/s")
     if cpu:
         from oracle import oracle as O  # the CPU baseline leg only

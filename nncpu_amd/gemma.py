@@ -11,9 +11,9 @@ f32 mode and the greedy lm_head through `nnh_model_argmax`. The prompt is
 evaluated in 16-token batches (session/engine.rs:362-380, PREFILL_BATCH).
 
 `Gemma3.generate_device` runs the same prefill, then decodes on the GPU
-alone (nncpu_amd/host/gemma3_gpu.hip): the forward's non-matmul steps as
-HIP kernels with the CPU restatement's arithmetic, one step captured in a
-HIP graph and replayed per token.
+alone (nncpu_amd/host/gemma3_gpu.hip): one persistent kernel runs every
+layer of a step with the CPU restatement's arithmetic, then the lm_head
+argmax; the step is captured in a HIP graph and replayed per token.
 """
 from __future__ import annotations
 

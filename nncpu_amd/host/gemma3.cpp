@@ -488,6 +488,11 @@ int nng_gpu_argmax(void* ctx, const float* x, size_t* row) {
 // run against them (crates/nncpu/src/kernels/tests.rs:105-147, 242-293,
 // 938-992, 1133-1217, 1263).
 
+// std::exp of floats, as attn_merge takes it (the platform libm's expf).
+void nng_op_libm_expf(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = std::exp(x[i]);
+}
+
 void nng_op_exp(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; ++i) y[i] = exp_lane(x[i]);
 }

@@ -1,38 +1,59 @@
 // The Gemma-3 decode step resident on the GPU: the forward of gemma3.cpp
 // (crates/nncpu/src/model/forward.rs:197-439, 719-965 with the scalar.rs
-// non-matmul kernels) for one token, with every operation in the same order
-// and rounding as that CPU restatement, so a decode gives the same tokens and
-// the same per-layer hidden states bit for bit. The token and the position
-// live in device memory, and one step is captured once in a HIP graph and
-// replayed per generated token: no host round trip inside the decode loop.
+// non-matmul kernels) for one token, every operation in the same order and
+// rounding as that CPU restatement, so a decode gives the same tokens and
+// the same per-layer hidden states bit for bit.
 //
-// Five kernels per layer. Every kernel boundary costs a few microseconds on
-// this GPU, so the non-matmul work rides on the matmul kernels around it:
-//   qkv   the previous layer's post-FFW RMSNorm and residual add (or, in
-//         layer 0, the embedding row), the attention RMSNorm, then the q, k
-//         and v matmuls (one launch over the three matrices);
-//   attn  the q / k RMSNorms, NeoX RoPE, the K/V append and the attention,
-//         one workgroup per query head;
-//   o     the output projection (the library's one-vector kernel);
-//   ffn   the post-attention RMSNorm and residual, the FFN RMSNorm, then the
-//         gate and up matmuls with GELU(gate) * up in the epilogue (a
-//         workgroup runs eight rows of each);
-//   down  the down projection (the library's one-vector kernel).
-// The residual and norm prologue is recomputed by every workgroup of its
-// kernel (the same operations, so the same bits), while the weight loads of
-// the matmul are already in flight; workgroup 0 stores the new residual.
-// The residual stream alternates between two buffers, so no kernel reads the
-// buffer it writes. The matmuls are the library's bit-exact f32 path: its
-// one-vector core (f32_m1.h) on the 16-lane weight layout that
-// nnh_weight_f32_layout exposes, and nnh_model_argmax_dev for the lm_head
-// (its first argmax stage fused into the gemv).
+// One persistent kernel runs every layer of a step; the lm_head argmax (the
+// library's nnh_model_argmax_dev) and a one-thread step end follow. The
+// three are captured once in a HIP graph and replayed per token: no host
+// round trip inside the decode loop.
 //
-// What is taken from the host: RoPE's cos / sin per position (computed with
-// the CPU restatement's own libm calls, uploaded once) and the embedding
-// scale sqrt(n_embd). The attention runs in one key block (n_ctx <= 256, the
-// reference's ATTN_BLOCK), so the block merge, whose exp is libm's, never
-// runs; longer contexts are refused. Compiled with -ffp-contract=off;
-// __fmaf_rn / __fma_rn exactly where the CPU code calls std::fma.
+// The step kernel: one workgroup of 1024 threads per CU, launched
+// cooperatively (every workgroup resident at once). Workgroups 0 .. A-1
+// run the attention, PK_S per query head (each computes all of its head's
+// scores and HD / PK_S output elements); the others, the matmul workgroups,
+// each run a share of the rows of every matmul. Per layer:
+//   P0  the previous layer's post-FFW RMSNorm and residual add (layer 0:
+//       the embedding row), the attention RMSNorm, q / k / v rows;
+//   P1  (attention workgroups) q / k RMSNorm, NeoX RoPE, the K/V append,
+//       the attention over the cached keys block by block;
+//   P2  rows of the output projection;
+//   P3  the post-attention RMSNorm and residual add, the FFN RMSNorm,
+//       gate and up rows, GELU(gate) * up;
+//   P4  rows of the down projection.
+// Every matmul workgroup computes the norms itself (the same operations, so
+// the same bits) and keeps the residual stream in registers.
+//
+// Hand-offs: every value a phase produces is stored as 64 bits, the float
+// and a tag naming the step and the layer, by a relaxed device-scope atomic
+// store; its consumers poll the tagged values until every tag is current.
+// A value is visible exactly when its tag is: no barrier, no fence. Each
+// buffer is written once per layer; before a phase of layer l + 1 can
+// overwrite a buffer, every reader of layer l's values has produced an
+// output that the writer transitively waited for (every matmul workgroup
+// has rows in every phase, which nngd_create checks). Every poll is
+// bounded: a wait that runs out sets the error flag, which ends every other
+// wait too, so every wave exits.
+//
+// Weights: a matmul workgroup's rows of each matrix (the 16-lane quant
+// layout of the library's f32 path and the BF16 scale rows) are copied into
+// LDS by direct global->LDS loads one layer ahead: layer l + 1's q / k / v
+// rows as soon as layer l's are consumed, and so on, so a phase finds its
+// weights in LDS. Waves 4-15 issue the copies and wait for them by count
+// (vector loads complete in order); waves 0-3 poll and never issue a copy,
+// so a poll never waits behind one.
+//
+// Attention: keys are cached chain-major per key (the 64 values score lane
+// u of 4 multiplies are contiguous), so the score lanes load them straight
+// into registers before the q / k / v poll. A context longer than one
+// 256-key block (the reference's ATTN_BLOCK) runs block by block, merging
+// the partials as scalar.rs attn_merge does, with glibc's expf restated.
+//
+// Compiled with -ffp-contract=off; __fmaf_rn / __fma_rn exactly where the
+// CPU code calls std::fma. What comes from the host: RoPE's cos / sin per
+// position (the CPU restatement's own libm calls), sqrt(n_embd), and the
+// expf table (2^(i/32), i < 32, rounded to double).
 
 #include <hip/hip_runtime.h>
 
@@ -50,14 +71,19 @@ namespace {
 
 using nnh::F32Mat;
 using nnh::lds_barrier;
-using nnh::ScaleStage;
-using nnh::M1Lane;
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+using nnh::xor_get;
 
 constexpr int ATTN_BLOCK = 256;  // model/mod.rs:84-87
-constexpr int WG = 256;          // threads per workgroup
 constexpr int E_MAX = 2048;      // residual width
+constexpr int PK_NT = 1024;      // threads per workgroup
+constexpr int PK_POLL = 512;     // threads 0..511 (waves 0-7) poll
+constexpr int PK_LOADERS = 4;    // waves 8-11 copy weights into LDS, on their own schedule
+constexpr int PK_CW = PK_POLL;   // threads 0..511 compute (the pollers); waves 12-15 idle in matmul workgroups
+constexpr int PK_S = 4;          // attention workgroups per query head
+constexpr int PK_KE = E_MAX / PK_POLL;  // residual values per poller thread
+constexpr int PK_KF = 16;        // tagged values per poller thread, longest vector (8192)
+constexpr int PK_LDS = 156 * 1024;
+constexpr long PK_SPIN = 1L << 21;  // poll rounds (each ~1 us) before a wait gives up
 
 __device__ __forceinline__ float bf16f(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ uint16_t to_bf16(float f) {
@@ -71,7 +97,6 @@ __device__ __forceinline__ float hsum8_lanes(float a) {
     const float q = __fadd_rn(p, __shfl_xor(p, 1, 64));
     return __fadd_rn(q, __shfl_xor(q, 2, 64));
 }
-__device__ __forceinline__ float4 ld4(const float* p) { return __builtin_bit_cast(float4, *(const f4u*)p); }
 
 // scalar.rs:19-84 (gemma3.cpp exp_lane).
 __device__ float exp_lane(float x) {
@@ -105,24 +130,59 @@ __device__ float gelu_lane(float v) {
     return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, t));
 }
 
+}  // namespace
+
+// ---- expf as glibc computes it ----------------------------------------------------------
+// scalar.rs attn_merge (gemma3.cpp attn_merge) scales the partials by
+// std::exp of a float: glibc's expf, the published algorithm of ARM's
+// optimized-routines (glibc >= 2.28): z = x * 32 / ln2 in double, k = z
+// rounded to an integer (by adding and subtracting 1.5 * 2^52), r = z - k,
+// s = 2^(k / 32) from a 32-entry table of 2^(i / 32) with k's integer part
+// added to the exponent, exp2(r / 32) by a degree-3 polynomial, one rounding
+// to float. glibc's x86-64 FMA build contracts r = z - k into one fma of
+// x * (32 / ln2) - k, so this does too. T[i] = bits of 2^(i / 32) rounded
+// to double, minus i << 47. The CPU test runs every float through this and
+// glibc's expf.
+__host__ __device__ inline float glibc_expf(float x, const uint64_t* T) {
+    uint32_t ux;
+    memcpy(&ux, &x, 4);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42bu) {  // |x| >= 88
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double InvLn2N = 0x1.71547652b82fep+5, SHIFT = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-20, C1 = 0x1.ebfce50fac4f3p-13, C2 = 0x1.62e42ff0c52d6p-6;
+    const double xd = (double)x, z = InvLn2N * xd;
+    double kd = z + SHIFT;
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= SHIFT;
+    const double r = fma(InvLn2N, xd, -kd);
+    const uint64_t t = T[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double zz = fma(C0, r, C1), r2 = r * r;
+    double y = fma(C2, r, 1.0);
+    y = fma(zz, r2, y);
+    return (float)(y * s);
+}
+
+namespace {
+
 // A chain input in LDS, transposed: element e of a dim-vector (dim a
 // multiple of 128) at (e % 8) * S + e / 8, S = dim / 8 + 4, so FMA lane l's
 // values are contiguous (16-byte reads) and the 4-float pad spreads the eight
 // lanes' reads over the banks.
-__device__ __forceinline__ int tstride(int dim) { return dim / 8 + 4; }
-__device__ __forceinline__ void tput4(float* xt, int S, int piece, float4 v) {
-    float* p = xt + 4 * (piece & 1) * S + (piece >> 1);
-    p[0] = v.x;
-    p[S] = v.y;
-    p[2 * S] = v.z;
-    p[3 * S] = v.w;
-}
+__host__ __device__ __forceinline__ int tstride(int dim) { return dim / 8 + 4; }
+__device__ __forceinline__ void tput(float* xt, int S, int e, float v) { xt[(e & 7) * S + (e >> 3)] = v; }
 
 // hsum8 of the eight FMA lanes' sums of squares of a transposed dim-vector
 // (dim % 128 == 0), run by lanes 0..7 of the calling wave; valid at lane 0.
 // A lane's values are read from LDS 12 float4s at a time, all issued before
-// that chunk's FMAs (a buffer rotated across loop iterations instead makes
-// the compiler wait for every read at the loop head).
+// that chunk's FMAs.
 __device__ __forceinline__ float chain_sumsq(const float* xt, int dim, int lane) {
     constexpr int CH = 12;
     float a = 0.0f;
@@ -147,602 +207,949 @@ __device__ __forceinline__ float chain_sumsq(const float* xt, int dim, int lane)
     return hsum8_lanes(a);
 }
 
-// The RMSNorm scale of a transposed dim-vector xt (scalar.rs:232-292,
-// gemma3.cpp sum_sq / rmsnorm_gamma_multi): lanes 0..7 of wave 0 run the
-// eight FMA lanes over the chunks of 8 in order, hsum8, lane 0 forms
-// (float)(1 / sqrt(ss * inv_dim + eps)) in f64 (dim % 8 == 0: no tail).
-// xt written before a barrier; every thread gets the scale (bc: one LDS float).
-__device__ float wg_rms_scale(const float* xt, int dim, float eps, float* bc) {
-    const int tid = threadIdx.x;
-    if (tid < 64) {
-        const float r = chain_sumsq(xt, dim, tid);
-        if (tid == 0) {
-            const float inv_dim = __fdiv_rn(1.0f, (float)dim);
-            bc[0] = (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn((double)r, (double)inv_dim), (double)eps)));
-        }
-    }
-    lds_barrier();
-    return bc[0];
+// (float)(1 / sqrt(ss / dim + eps)) in f64 (scalar.rs:232-292, gemma3.cpp
+// rmsnorm_gamma_multi; dim % 8 == 0: no tail).
+__device__ __forceinline__ float rms_of(float ss, int dim, float eps) {
+    const float inv_dim = __fdiv_rn(1.0f, (float)dim);
+    return (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn((double)ss, (double)inv_dim), (double)eps)));
 }
 
-// ---- the matmul kernels' prologues --------------------------------------------------------
-// NT threads per workgroup; a thread holds pieces (4 floats) tid + NT k of
-// an E-vector.
+// ---- tagged hand-offs ----------------------------------------------------------------------
 
-template <int NT>
-struct Pieces {
-    static constexpr int K = (E_MAX / 4 + NT - 1) / NT;
-};
+__device__ __forceinline__ void tstore(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tload(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int flag_load(const int* p) {
+    return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void flag_raise(int* p) {
+    __hip_atomic_fetch_or(p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-// A prologue's inputs: the block output o, the residual x, two gammas.
-template <int NT>
-struct ResIn {
-    static constexpr int K = Pieces<NT>::K;
-    float4 o[K], x[K], g1[K], g2[K];
-    __device__ __forceinline__ void load(const float* po, const float* px, const float* pg1, const float* pg2, int E) {
+// Thread t of nt polls values t, t + nt, ... (< n, K per thread) of src
+// until each carries `tag`, then stores the floats to dst[i] (LDS). False
+// when the wait runs out (the error flag is raised) or another workgroup
+// raised it.
+template <int K>
+__device__ bool poll_tagged(const uint64_t* src, int n, int t, int nt, uint32_t tag, int* err, float* dst) {
+    uint64_t w[K];
+    for (long r = 0; r < PK_SPIN; ++r) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) w[k] = tload(src + min(t + nt * k, n - 1));
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < K; ++k) ok = ok && (uint32_t)(w[k] >> 32) == tag;
+        if (ok) {
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+                if (t + nt * k < n) dst[t + nt * k] = __uint_as_float((uint32_t)w[k]);
+            return true;
+        }
+        if ((r & 63) == 63 && flag_load(err)) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    flag_raise(err);
+    return false;
+}
+
+// Poller thread t reads values t, t + PK_POLL, ... (< n, K per thread) into
+// dst (LDS), waiting for any whose tag is not yet current.
+template <int K>
+__device__ bool read_tagged(const uint64_t* src, int n, int t, uint32_t tag, int* err, float* dst) {
+    uint32_t stale = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if (t + PK_POLL * k < n) stale |= 1u << k;
+    for (long r = 0; stale; ++r) {
+        // Every stale value re-read at once: one round trip per round.
+        uint64_t w[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (stale & (1u << k)) w[k] = tload(src + t + PK_POLL * k);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const int i = 4 * min((int)threadIdx.x + NT * k, E / 4 - 1);
-            o[k] = ld4(po + i);
-            x[k] = ld4(px + i);
-            g1[k] = ld4(pg1 + i);
-            g2[k] = ld4(pg2 + i);
+            if ((stale & (1u << k)) && (uint32_t)(w[k] >> 32) == tag) {
+                dst[t + PK_POLL * k] = __uint_as_float((uint32_t)w[k]);
+                stale &= ~(1u << k);
+            }
         }
+        if (!stale) break;
+        if (r >= PK_SPIN || ((r & 63) == 63 && flag_load(err))) {
+            flag_raise(err);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
     }
+    return true;
+}
+
+constexpr long PK_LSPIN = 1L << 24;  // LDS-wait rounds before a wait gives up
+
+// A barrier of `waves` waves on an LDS counter, for a subset of the
+// workgroup (the loader waves never join one). gen: arrivals expected so
+// far, kept by the caller.
+__device__ __forceinline__ bool lbar(int* ctr, int& gen, int waves) {
+    gen += waves;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (long r = 0; r < PK_LSPIN; ++r) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= gen) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+// The poller waves' barrier.
+__device__ __forceinline__ bool pbar(int* ctr, int& gen) { return lbar(ctr, gen, PK_POLL / 64); }
+
+// Wait until the LDS counter *p >= v; false on a timeout or an abort.
+__device__ __forceinline__ bool lds_wait_ge(int* p, int v, int* abort_flag) {
+    for (long r = 0; r < PK_LSPIN; ++r) {
+        if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return true;
+        if (__hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// ---- weight copies into LDS ------------------------------------------------------------
+
+// Producer i of `parts` owns rows [i * total / parts, (i + 1) * total /
+// parts) (32-bit: total * parts < 2^31, which nngd_create checks).
+__host__ __device__ __forceinline__ int row_first(int total, int parts, int i) {
+    return (int)((uint32_t)(i * total) / (uint32_t)parts);
+}
+__host__ __device__ __forceinline__ void row_range(int total, int parts, int i, int* r0, int* r1) {
+    *r0 = row_first(total, parts, i);
+    *r1 = row_first(total, parts, i + 1);
+}
+
+// A matmul workgroup's rows of each phase's matrices.
+struct Rows {
+    int q0, q1, o0, o1, f0, f1, d0, d1;
 };
 
-__device__ __forceinline__ float4 add_normed(float4 x, float4 o, float s, float4 g) {
-    return make_float4(__fadd_rn(x.x, __fmul_rn(__fmul_rn(o.x, s), g.x)),
-                       __fadd_rn(x.y, __fmul_rn(__fmul_rn(o.y, s), g.y)),
-                       __fadd_rn(x.z, __fmul_rn(__fmul_rn(o.z, s), g.z)),
-                       __fadd_rn(x.w, __fmul_rn(__fmul_rn(o.w, s), g.w)));
-}
-__device__ __forceinline__ float4 normed(float4 x, float s, float4 g) {
-    return make_float4(__fmul_rn(__fmul_rn(x.x, s), g.x), __fmul_rn(__fmul_rn(x.y, s), g.y),
-                       __fmul_rn(__fmul_rn(x.z, s), g.z), __fmul_rn(__fmul_rn(x.w, s), g.w));
-}
+// Bytes of a row in the 16-lane layout (Q8 groups of 8 blocks) and of its
+// padded scale row.
+__host__ __device__ __forceinline__ uint32_t qrow_bytes(const F32Mat& m) { return (uint32_t)((m.nb + 7) / 8) * 256; }
+__host__ __device__ __forceinline__ uint32_t srow_bytes(const F32Mat& m) { return (uint32_t)m.nbp * 2; }
 
-// Piece index of thread slot k, and whether it is one of the vector's own
-// (slots past the end repeat the last piece: stores of it write its own
-// values again, so they need no condition).
-template <int NT>
-__device__ __forceinline__ int piece(int k, int E) { return min((int)threadIdx.x + NT * k, E / 4 - 1); }
-
-// y = RMSNorm(x, g) into LDS yl, x already in LDS xs (transposed) and in the
-// thread's registers; ends with a barrier.
-template <int NT, int K>
-__device__ __forceinline__ void norm_to(const float4 (&xn)[K], const float4 (&g)[K], int E, float eps,
-                                        const float* xs, float* yl, float* bc) {
-    const float s = wg_rms_scale(xs, E, eps, bc);
-#pragma unroll
-    for (int k = 0; k < K; ++k) *(float4*)(yl + 4 * piece<NT>(k, E)) = normed(xn[k], s, g[k]);
-    lds_barrier();
+// Rows [lo, hi) of m into LDS row slots slot0..: v(src, bytes, LDS offset)
+// for the quants, then for the scales.
+template <class V>
+__host__ __device__ __forceinline__ void visit_rows(V&& v, const F32Mat& m, int lo, int hi, int slot0, uint32_t wdst,
+                                                    uint32_t sdst) {
+    if (hi <= lo) return;
+    const uint32_t qb = qrow_bytes(m), sb = srow_bytes(m);
+    v(m.fq + (size_t)lo * qb, (uint32_t)(hi - lo) * qb, wdst + (uint32_t)slot0 * qb);
+    v((const uint8_t*)(m.fs + (size_t)lo * m.nbp), (uint32_t)(hi - lo) * sb, sdst + (uint32_t)slot0 * sb);
 }
 
-// Keep x (the new residual) in xs (transposed) and, from workgroup 0, in
-// x_out and rec.
-template <int NT, int K>
-__device__ __forceinline__ void keep_residual(const float4 (&xn)[K], int E, float* xs, float* x_out, float* rec) {
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int i = piece<NT>(k, E);
-        tput4(xs, tstride(E), i, xn[k]);
-        if (blockIdx.x == 0) {
-            *(float4*)(x_out + 4 * i) = xn[k];
-            if (rec) *(float4*)(rec + 4 * i) = xn[k];
-        }
-    }
-    lds_barrier();
-}
+}  // namespace
 
-// x_new = x + RMSNorm(o, g1), y = RMSNorm(x_new, g2) (forward.rs:749-803):
-// a block's post-norm and residual add, then the next pre-norm. y goes to
-// LDS yl (the matmul's x). xs: LDS scratch of E + 32 floats. In two parts:
-// res_stage puts o in LDS (so every input load has landed when it returns),
-// res_norm does the rest.
-template <int NT>
-__device__ __forceinline__ void res_stage(const ResIn<NT>& r, int E, float* xs) {
-#pragma unroll
-    for (int k = 0; k < Pieces<NT>::K; ++k) tput4(xs, tstride(E), piece<NT>(k, E), r.o[k]);
-    lds_barrier();
-}
-
-template <int NT>
-__device__ void res_norm(const ResIn<NT>& r, int E, float eps, float* xs, float* yl, float* bc, float* x_out,
-                         float* rec) {
-    constexpr int K = Pieces<NT>::K;
-    const float s1 = wg_rms_scale(xs, E, eps, bc);
-    float4 xn[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) xn[k] = add_normed(r.x[k], r.o[k], s1, r.g1[k]);
-    keep_residual<NT>(xn, E, xs, x_out, rec);
-    norm_to<NT>(xn, r.g2, E, eps, xs, yl, bc);
-}
-
-// Layer 0's input: the token's Q8_0 row of the tied token_embd times
-// sqrt(n_embd) (kernels/mod.rs:917-929: f32(q) * (bf16(s) * scale)).
-template <int NT>
-struct EmbIn {
-    static constexpr int K = Pieces<NT>::K;
-    uint32_t q[K], s[K];  // four quants, their block's BF16 scale
-    float4 g[K];
-    __device__ __forceinline__ void load(const uint64_t* tok, const int8_t* tq, const uint16_t* ts, const float* pg,
-                                         int E) {
-        const size_t t = (size_t)*tok;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int i = 4 * piece<NT>(k, E);
-            q[k] = *(const uint32_t*)(tq + t * E + i);
-            s[k] = ts[t * (E / 32) + i / 32];
-            g[k] = ld4(pg + i);
-        }
-    }
+// LDS byte offsets of a matmul workgroup, and the copy instructions each
+// loader wave issues per phase (the most any workgroup needs).
+struct PkGeom {
+    uint32_t qw, qs, ow, os, fw, fs, dw, ds, y, in, xt, res, bc, h, wtab, bytes;
+    int kq, ko, kf, kd;
 };
 
-template <int NT>
-__device__ void emb_norm(const EmbIn<NT>& r, int E, float eps, float embd_scale, float* xs, float* yl, float* bc,
-                         float* x_out) {
-    constexpr int K = Pieces<NT>::K;
-    float4 xn[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const float vs = __fmul_rn(bf16f(r.s[k]), embd_scale);
-        xn[k] = make_float4(__fmul_rn((float)(int8_t)(r.q[k] & 0xffu), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 8), vs),
-                            __fmul_rn((float)(int8_t)(r.q[k] >> 16), vs), __fmul_rn((float)(int8_t)(r.q[k] >> 24), vs));
-    }
-    keep_residual<NT>(xn, E, xs, x_out, nullptr);
-    norm_to<NT>(xn, r.g, E, eps, xs, yl, bc);
-}
-
-// ---- the step's kernels -----------------------------------------------------------------
-// One workgroup per CU for the matmul kernels (the grids stay under 256
-// workgroups), so the wave that runs a norm's FMA chain has its SIMD to
-// itself while the others wait at the barrier.
-
-constexpr int QKV_NT = 512;   // 32 rows of one matrix per workgroup
-constexpr int FFN_NT = 1024;  // 32 gate rows and the same 32 up rows
-constexpr int MAX_NBP = E_MAX / 32;
-
-struct QkvArgs {
-    F32Mat m[3];  // q, k, v
-    float* y[3];
-    int wg[3];  // workgroups per matrix
-    const float *o, *x_in, *post, *norm;  // post: the previous layer's post-FFW gamma; norm: attention's
-    float* x_out;
-    float* rec;  // this layer's slot of the step-0 record (advanced by *step_p * rec_stride), or null
-    const int* step_p;
-    size_t rec_stride;
-    const uint64_t* tok;  // layer 0: the token and the embedding table
+struct PkArgs {
+    int n_layer, E, F, H, KV, QD, KVD, A, M;
+    float eps, attn_scale, embd_scale;
+    PkGeom g;
+    F32Mat geo[4];              // geometry (no pointers) of q / k / v, o, gate / up, down
+    const uint64_t* wptr;       // [n_layer][7] x (quants, scales) of q k v o gate up down
+    const float* norms;         // per layer, ns apart: attn, q, k, post_attn, ffn, post_ffw
+    size_t ns;
+    uint16_t *kc, *vc;          // caches [n_layer][n_ctx][n_kv * HD]: K chain-major per key, V natural
+    size_t kv_layer;
+    const float *cos_t, *sin_t; // RoPE tables [2][n_ctx][HD / 2]: sliding (local) base, then global
+    int n_ctx, window, swa_period;
+    const uint64_t* tok;  // the token; the embedding table (the tied lm_head, Q8_0)
     const int8_t* tq;
     const uint16_t* ts;
-    float embd_scale;
-    int E;
-    float eps;
+    const float* out_norm;
+    const int *pos_p, *step_p;
+    const uint32_t* seq_p;  // steps run on this model so far: the tags' base
+    uint64_t *t_qkv, *t_attn, *t_o, *t_h, *t_down;
+    float *record, *y;
+    size_t rec_stride;
+    const uint64_t* expt;  // glibc_expf's table
+    int* err;
 };
 
-template <int D, bool FIRST>
-__global__ __launch_bounds__(QKV_NT) void qkv_kernel(QkvArgs a) {
-    constexpr int NT = QKV_NT, R = NT / 16;
-    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
-    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
-    __shared__ __attribute__((aligned(16))) uint16_t sl[R * MAX_NBP];
-    __shared__ float bc[4];
-    const int tid = threadIdx.x;
-    ResIn<NT> r;
-    EmbIn<NT> e;
-    if (FIRST)
-        e.load(a.tok, a.tq, a.ts, a.norm, a.E);
-    else
-        r.load(a.o, a.x_in, a.post, a.norm, a.E);
-    int b = blockIdx.x, seg = 0;
-    if (b >= a.wg[0]) {
-        b -= a.wg[0];
-        seg = 1;
-        if (b >= a.wg[1]) {
-            b -= a.wg[1];
-            seg = 2;
+namespace {
+
+// A matmul workgroup's rows (workgroup mw of a.M).
+__host__ __device__ inline Rows rows_of(const PkArgs& a, int mw) {
+    Rows r;
+    row_range(a.QD + 2 * a.KVD, a.M, mw, &r.q0, &r.q1);
+    row_range(a.E, a.M, mw, &r.o0, &r.o1);
+    row_range(a.F, a.M, mw, &r.f0, &r.f1);
+    row_range(a.E, a.M, mw, &r.d0, &r.d1);
+    return r;
+}
+
+// The contiguous runs of bytes a matmul workgroup (rows rw) copies into LDS
+// for a phase of layer Ly, in order: v(src, bytes, LDS offset) for each.
+// mat(j): matrix j (q k v o gate up down) of the layer.
+template <class Mat, class V>
+__host__ __device__ __forceinline__ void visit_phase(const PkArgs& a, Mat&& mat, int phase, const Rows& rw, V&& v) {
+    const PkGeom& g = a.g;
+    if (phase == 0) {
+        const int r0 = rw.q0, r1 = rw.q1, kb = a.QD, vb = a.QD + a.KVD, ve = a.QD + 2 * a.KVD;
+        visit_rows(v, mat(0), r0, min(r1, kb), 0, g.qw, g.qs);
+        visit_rows(v, mat(1), max(r0, kb) - kb, min(r1, vb) - kb, max(r0, kb) - r0, g.qw, g.qs);
+        visit_rows(v, mat(2), max(r0, vb) - vb, min(r1, ve) - vb, max(r0, vb) - r0, g.qw, g.qs);
+    } else if (phase == 2) {
+        visit_rows(v, mat(3), rw.o0, rw.o1, 0, g.ow, g.os);
+    } else if (phase == 3) {
+        visit_rows(v, mat(4), rw.f0, rw.f1, 0, g.fw, g.fs);
+        visit_rows(v, mat(5), rw.f0, rw.f1, rw.f1 - rw.f0, g.fw, g.fs);
+    } else {
+        visit_rows(v, mat(6), rw.d0, rw.d1, 0, g.dw, g.ds);
+    }
+}
+
+// Which geometry matrix j (q k v o gate up down) has.
+__host__ __device__ __forceinline__ int geo_of(int j) { return j < 3 ? 0 : j == 3 ? 1 : j < 6 ? 2 : 3; }
+
+__host__ __device__ __forceinline__ int chunks_of(uint32_t len) { return (int)((len + 1023) >> 10); }
+
+__host__ int phase_chunks(const PkArgs& a, const F32Mat* w7, int phase, int mw) {
+    int c = 0;
+    visit_phase(a, [&](int j) { return w7[j]; }, phase, rows_of(a, mw), [&](const uint8_t*, uint32_t len, uint32_t) { c += chunks_of(len); });
+    return c;
+}
+
+// One 16-byte piece global -> LDS (lane l's bytes at LDS address dst + 16 l,
+// dst uniform). As asm, so the compiler neither waits for it nor reorders
+// LDS reads around it; the waits are explicit.
+__device__ __forceinline__ void copy16(const uint8_t* src, uint32_t dst) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(dst) : "memory");
+}
+
+// Loader wave lw issues exactly k copy instructions for a phase's runs
+// (1 KB chunks lw, lw + PK_LOADERS, ...; past the last chunk it copies the
+// last one again, the same bytes to the same place), so every loader wave's
+// count per phase is the same known number. Lanes past a run's end are
+// masked off.
+// The pointers of a layer's matrices from the LDS table (uniform values,
+// moved to scalar registers).
+__device__ __forceinline__ const void* lds_ptr(const uint64_t* p) {
+    const uint64_t v = *p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(((uint64_t)hi << 32) | lo);
+}
+struct LdsMats {
+    const PkArgs* a;
+    const uint64_t* tab;  // this layer's 7 x (quants, scales) in LDS
+    __device__ __forceinline__ F32Mat operator()(int j) const {
+        F32Mat m = a->geo[geo_of(j)];
+        m.fq = (const uint8_t*)lds_ptr(tab + 2 * j);
+        m.fs = (const uint16_t*)lds_ptr(tab + 2 * j + 1);
+        return m;
+    }
+};
+
+__device__ void issue(const PkArgs& a, const LdsMats& mats, int phase, const Rows& rw, int k, int lw, int lane,
+                      uint32_t lds) {
+    int total = 0;
+    visit_phase(a, mats, phase, rw, [&](const uint8_t*, uint32_t len, uint32_t) { total += chunks_of(len); });
+    for (int i = 0; i < k; ++i) {
+        const int c = min(lw + PK_LOADERS * i, total - 1);
+        const uint8_t* src = nullptr;
+        uint32_t len = 0, dst = 0;
+        int cs = 0, c0 = 0;
+        visit_phase(a, mats, phase, rw, [&](const uint8_t* s_, uint32_t l_, uint32_t d_) {
+            if (c >= cs) {  // the last run starting at or before chunk c
+                src = s_;
+                len = l_;
+                dst = d_;
+                c0 = cs;
+            }
+            cs += chunks_of(l_);
+        });
+        const uint32_t off = (uint32_t)(c - c0) * 1024, o = off + (uint32_t)lane * 16;
+        if (o < len) copy16(src + o, lds + dst + off);
+    }
+}
+
+// ---- the bit-exact row sums, weights in LDS ----------------------------------------------
+// gemv_f32_kernel's arithmetic (scalar.rs:626-649): chain j of a row
+// (element j of every 32-block) over the blocks in order, acc = fma(f32(q) *
+// bf16(s), x, acc), then v[l] = (acc_l + acc_{8+l}) + (acc_{16+l} +
+// acc_{24+l}), hsum8. w: the row's 16-lane groups (lane j's 16 bytes of
+// group g at g * 256 + 16 j: byte 2i element j of block 8g + i, byte 2i + 1
+// element j + 16); s: its BF16 scales; x: the input, natural order.
+
+// One 8-block group of a lane's chains, read from LDS: the 16-byte piece,
+// the 8 BF16 scales, and x for chain j (and, 16 lanes per row, j + 16).
+template <bool TWO>
+struct Grp {
+    uint4 q, s;
+    float x0[8], x1[TWO ? 8 : 1];
+    __device__ __forceinline__ void read(const uint8_t* w, const uint16_t* sc, const float* x, int g, int j) {
+        q = *(const uint4*)(w + g * 256 + (TWO ? j : (j & 15)) * 16);
+        s = *(const uint4*)(sc + g * 8);
+        const float* xb = x + 256 * g + j;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x0[i] = xb[32 * i];
+            if (TWO) x1[i] = xb[32 * i + 16];
         }
     }
-    const F32Mat m = a.m[seg];
-    const int row0 = b * R, row_raw = row0 + (tid >> 4);
-    const int row = row_raw < m.rows ? row_raw : m.rows - 1;  // keep loads in bounds; the store is skipped
-    ScaleStage<NT, R * MAX_NBP * 2> ss;
-    ss.load(m, row0, min(R, m.rows - row0));
-    M1Lane<1, D> L;
-    L.init(m, row, tid & 15);
-    // The prologue's inputs land first; the weight loads then stream while
-    // the prologue's norm chains run (issued earlier, they would queue
-    // ahead of other workgroups' prologue loads).
-    ss.store(sl);
-    if (!FIRST) res_stage<NT>(r, a.E, xs);
-    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));  // every prologue load has landed
-    __builtin_amdgcn_sched_barrier(0);
-    L.prefetch();
-    __builtin_amdgcn_sched_barrier(0);
-    if (FIRST)
-        emb_norm<NT>(e, a.E, a.eps, a.embd_scale, xs, yl, bc, a.x_out);
-    else
-        res_norm<NT>(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec ? a.rec + (size_t)*a.step_p * a.rec_stride : nullptr);
-    L.run(yl, sl + (row - row0) * m.nbp);
-    const float v = L.reduce();
-    if (row_raw < m.rows && (tid & 15) == 0) a.y[seg][row_raw] = v;
-}
-
-struct FfnArgs {
-    F32Mat gate, up;
-    float* h;  // GELU(gate) * up
-    int F;
-    const float *o, *x_in, *post, *norm;  // post_attention_norm, ffn_norm
-    float* x_out;
-    int E;
-    float eps;
+    // Blocks i < nblk (all 8 when FULL) into the chains; hs: the byte of a
+    // pair a one-chain lane takes (0 or 8), applied to the piece once so the
+    // per-block byte selects are constants.
+    template <bool FULL>
+    __device__ __forceinline__ void run(float& a0, float& a1, int nblk, int hs) const {
+        uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t sw[4] = {s.x, s.y, s.z, s.w};
+        if (!TWO) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qw[k] >>= hs;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (FULL || i < nblk) {
+                const float sb = bf16f((sw[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+                const uint32_t qq = qw[i >> 1] >> (16 * (i & 1));
+                if (TWO) {
+                    a0 = __fmaf_rn((float)(int8_t)(qq & 0xffu) * sb, x0[i], a0);
+                    a1 = __fmaf_rn((float)(int8_t)((qq >> 8) & 0xffu) * sb, x1[TWO ? i : 0], a1);
+                } else {
+                    a0 = __fmaf_rn((float)(int8_t)(qq & 0xffu) * sb, x0[i], a0);
+                }
+            }
+        }
+    }
 };
 
-// Workgroup g runs gate rows 32g..32g+31 (row slots 0..31) and the same up
-// rows (slots 32..63); h = GELU(gate) * up (forward.rs:771-777).
-template <int D>
-__global__ __launch_bounds__(FFN_NT) void ffn_kernel(FfnArgs a) {
-    constexpr int NT = FFN_NT, R = NT / 16, HR = R / 2;
-    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
-    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
-    __shared__ __attribute__((aligned(16))) uint16_t sl[R * MAX_NBP];
-    __shared__ float bc[4], res[R];
-    const int tid = threadIdx.x, slot = tid >> 4, r0 = blockIdx.x * HR;
-    ResIn<NT> r;
-    r.load(a.o, a.x_in, a.post, a.norm, a.E);
-    const int nr = min(HR, a.F - r0);
-    ScaleStage<NT, HR * MAX_NBP * 2> sg, su;
-    sg.load(a.gate, r0, nr);
-    su.load(a.up, r0, nr);
-    const int row = r0 + (slot % HR) < a.F ? r0 + (slot % HR) : a.F - 1;
-    M1Lane<1, D> L;
-    L.init(slot < HR ? a.gate : a.up, row, tid & 15);
-    // The prologue's inputs land first; the weight loads then stream while
-    // the norm chains run.
-    sg.store(sl);
-    su.store(sl + HR * a.gate.nbp);
-    res_stage<NT>(r, a.E, xs);
-    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));  // every prologue load has landed
-    __builtin_amdgcn_sched_barrier(0);
-    L.prefetch();
-    __builtin_amdgcn_sched_barrier(0);
-    res_norm<NT>(r, a.E, a.eps, xs, yl, bc, a.x_out, nullptr);
-    L.run(yl, sl + (slot < HR ? row - r0 : HR + row - r0) * a.gate.nbp);
-    const float v = L.reduce();
-    if ((tid & 15) == 0) res[slot] = v;
-    lds_barrier();
-    if (tid < HR && r0 + tid < a.F) a.h[r0 + tid] = __fmul_rn(gelu_lane(res[tid]), res[HR + tid]);
+// The chains of one row over its groups in order, the next group's LDS
+// reads issued before the current group's arithmetic.
+template <bool TWO>
+__device__ __forceinline__ void row_chains(const uint8_t* w, const uint16_t* sc, const float* x, int nb, int j,
+                                           float& a0, float& a1) {
+    const int ng = nb / 8, hs = TWO ? 0 : 8 * (j >> 4);
+    Grp<TWO> A, B;
+    int g = 0;
+    if (ng > 0) A.read(w, sc, x, 0, j);
+    for (; g + 1 < ng; g += 2) {
+        B.read(w, sc, x, g + 1, j);
+        A.template run<true>(a0, a1, 8, hs);
+        if (g + 2 < ng) A.read(w, sc, x, g + 2, j);
+        B.template run<true>(a0, a1, 8, hs);
+    }
+    if (g < ng) A.template run<true>(a0, a1, 8, hs);
+    if (nb % 8) {
+        B.read(w, sc, x, ng, j);
+        B.template run<false>(a0, a1, nb % 8, hs);
+    }
 }
 
-struct FinalArgs {
-    const float *o, *x_in, *post, *norm;  // the last post-FFW gamma, output_norm
-    float *x_out, *y, *rec;
-    const int* step_p;
-    size_t rec_stride;
-    int E;
-    float eps;
-};
-
-// After the last layer: its residual, then y = RMSNorm(x, output_norm).
-__global__ __launch_bounds__(WG) void final_kernel(FinalArgs a) {
-    __shared__ __attribute__((aligned(16))) float xs[E_MAX + 32];
-    __shared__ __attribute__((aligned(16))) float yl[E_MAX];
-    __shared__ float bc[4];
-    ResIn<WG> r;
-    r.load(a.o, a.x_in, a.post, a.norm, a.E);
-    res_stage<WG>(r, a.E, xs);
-    res_norm<WG>(r, a.E, a.eps, xs, yl, bc, a.x_out, a.rec + (size_t)*a.step_p * a.rec_stride);
-    for (int i = threadIdx.x; i < a.E / 4; i += WG) *(float4*)(a.y + 4 * i) = *(const float4*)(yl + 4 * i);
+// 16 lanes per row, lane j (0..15) running chains j and j + 16; the sum is
+// valid at j == 0.
+__device__ float row16(const uint8_t* w, const uint16_t* s, const float* x, int nb, int j) {
+    float a0 = 0.0f, a1 = 0.0f;
+    row_chains<true>(w, s, x, nb, j, a0, a1);
+    const float u = __fadd_rn(a0, xor_get(a0, 8));
+    const float v = __fadd_rn(a1, xor_get(a1, 8));
+    const float uv = __fadd_rn(u, v);
+    const float p = __fadd_rn(uv, xor_get(uv, 4));
+    const float q = __fadd_rn(p, xor_get(p, 1));
+    return __fadd_rn(q, xor_get(q, 2));
 }
 
-struct AttnArgs {
-    const float *q, *k, *v;  // the projections
-    const float *q_norm, *k_norm, *cos_t, *sin_t;
-    const int* pos_p;
-    uint16_t *kc, *vc;  // this layer's caches [n_ctx][n_kv * HD]
-    int group, KV, window;
-    float scale, eps;
-    float* out;
-};
+// 32 lanes per row, lane j (0..31) running chain j alone: lanes j and j + 16
+// read the same piece and take its even / odd bytes. Valid at j == 0.
+__device__ float row32(const uint8_t* w, const uint16_t* s, const float* x, int nb, int j) {
+    float a = 0.0f, unused = 0.0f;
+    row_chains<false>(w, s, x, nb, j, a, unused);
+    const float u = __fadd_rn(a, xor_get(a, 8));
+    const float v = __fadd_rn(u, xor_get(u, 16));
+    const float p = __fadd_rn(v, xor_get(v, 4));
+    const float q = __fadd_rn(p, xor_get(p, 1));
+    return __fadd_rn(q, xor_get(q, 2));
+}
+
+// ---- matmul workgroups -----------------------------------------------------------------
+
+// The pollers' part of P0 / P3, among the poller waves only: x +=
+// RMSNorm(in) * g1 (in: the polled vector in LDS, natural order), then y =
+// RMSNorm(x) * g2 into Y. Wave 0's lanes 0..7 run the norm chains. g1v /
+// g2v: the thread's elements of the gammas, loaded at the start of the pass
+// (their loads overlap the wait for the input).
+__device__ bool residual_norms(const PkArgs& a, int tid, const float* in, float (&xr)[PK_KE], const float (&g1v)[PK_KE],
+                               const float (&g2v)[PK_KE], float* xt, float* Y, float* bc, int* pctr, int& pgen,
+                               float* rec, bool add) {
+    const int E = a.E, S = tstride(E);
+    bool ok = true;
+    if (add) {
+#pragma unroll
+        for (int k = 0; k < PK_KE; ++k) {
+            const int i = tid + PK_POLL * k;
+            if (i < E) tput(xt, S, i, in[i]);
+        }
+        ok = pbar(pctr, pgen) && ok;
+        if (tid < 64) {
+            const float r = chain_sumsq(xt, E, tid);
+            if (tid == 0) bc[0] = rms_of(r, E, a.eps);
+        }
+        ok = pbar(pctr, pgen) && ok;
+        const float s1 = bc[0];
+#pragma unroll
+        for (int k = 0; k < PK_KE; ++k) {
+            const int i = tid + PK_POLL * k;
+            if (i < E) {
+                xr[k] = __fadd_rn(xr[k], __fmul_rn(__fmul_rn(in[i], s1), g1v[k]));
+                if (rec) rec[i] = xr[k];
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PK_KE; ++k) {
+        const int i = tid + PK_POLL * k;
+        if (i < E) tput(xt, S, i, xr[k]);
+    }
+    ok = pbar(pctr, pgen) && ok;
+    if (tid < 64) {
+        const float r = chain_sumsq(xt, E, tid);
+        if (tid == 0) bc[0] = rms_of(r, E, a.eps);
+    }
+    ok = pbar(pctr, pgen) && ok;
+    const float s2 = bc[0];
+#pragma unroll
+    for (int k = 0; k < PK_KE; ++k) {
+        const int i = tid + PK_POLL * k;
+        if (i < E) Y[i] = __fmul_rn(__fmul_rn(xr[k], s2), g2v[k]);
+    }
+    return ok;
+}
+
+// A phase's rows (nrows of matrix geometry m, weights w / scales sc in LDS,
+// input x in LDS), NB: the rows' block count when known at compile time.
+template <int NB>
+__device__ __forceinline__ void rows32(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const float* x, int nrows,
+                                       uint64_t* out, uint32_t tag, int tid) {
+    const int nb = NB ? NB : m.nb;
+    const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
+    for (int slot = tid >> 5; slot < nrows; slot += PK_CW / 32) {
+        const float v = row32(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 31);
+        if ((tid & 31) == 0) tstore(out + slot, v, tag);
+    }
+}
+template <int NB>
+__device__ __forceinline__ void rows16(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const float* x, int nrows,
+                                       float* res, int tid) {
+    const int nb = NB ? NB : m.nb;
+    const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
+    for (int slot = tid >> 4; slot < nrows; slot += PK_CW / 16) {
+        const float v = row16(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 15);
+        if ((tid & 15) == 0) res[slot] = v;
+    }
+}
+
+// The matmul workgroups. Waves 8-11 (loaders) copy each layer's rows of
+// each matrix into its LDS region as soon as the region's previous layer is
+// consumed, wait for the copies and count them landed; they never meet the
+// other waves at a barrier, so a slow copy never holds up a phase that does
+// not need it. Waves 0-7 poll the inputs, run the norms and compute,
+// running the layers as a loop over phases, ph = 0 (q / k / v), 1 (o), 2
+// (gate / up), 3 (down), with one copy of each piece of code (the step's
+// code stays small enough for the instruction cache). Waves 12-15 have no
+// work here. A last pass (mw 0 only) forms the final norm.
+template <int NBE, int NBQ, int NBF>
+__device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_t base) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, mw = blockIdx.x - a.A;
+    const bool poller = (int)threadIdx.x < PK_POLL;
+    const PkGeom& g = a.g;
+    const uint32_t lbase = (uint32_t)(uintptr_t)lds;
+    float* Y = (float*)(lds + g.y);
+    float* XT = (float*)(lds + g.xt);
+    float* RES = (float*)(lds + g.res);
+    float* BC = (float*)(lds + g.bc);
+    int* ABORT = (int*)(BC + 1);
+    int* PCTR = (int*)(BC + 2);    // the compute waves' barrier
+    int* FREED = (int*)(BC + 4);   // [3] layers consumed of the q / k / v, o, gate / up + down regions
+    int* LANDED = (int*)(BC + 8);  // [4] loader-wave copies landed of q / k / v, o, gate / up, down
+    float* H = (float*)(lds + g.h);
+    float* IN = (float*)(lds + g.in);
+    const int E = a.E, L = a.n_layer;
+    const Rows rw = rows_of(a, mw);
+    const int q0 = rw.q0, q1 = rw.q1, o0 = rw.o0, o1 = rw.o1, f0 = rw.f0, f1 = rw.f1, d0 = rw.d0, d1 = rw.d1;
+    const int nf = f1 - f0;
+    if (threadIdx.x < 16) ((int*)BC)[threadIdx.x] = 0;
+    // The layers' matrix pointers into LDS (scalar loads of a table read
+    // once per layer would each wait a memory round trip).
+    uint64_t* WT = (uint64_t*)(lds + g.wtab);
+    for (int i = threadIdx.x; i < 14 * L; i += PK_NT) WT[i] = a.wptr[i];
+    lds_barrier();  // the last barrier of the whole workgroup
+    if ((int)threadIdx.x >= PK_CW + 64 * PK_LOADERS) return;
+    if ((int)threadIdx.x >= PK_CW) {
+        // ---- loader waves
+        const int lw = wave - PK_CW / 64;
+        for (int l = 0; l < L; ++l) {
+            const LdsMats mats{&a, WT + 14 * l};
+#pragma unroll 1
+            for (int q = 0; q < 4; ++q) {
+                // Region free: its previous layer's phase is done.
+                if (!lds_wait_ge(FREED + (q == 3 ? 2 : q), l, ABORT)) {
+                    flag_raise(a.err);
+                    *ABORT = 1;
+                    l = L;
+                    break;
+                }
+                issue(a, mats, q == 0 ? 0 : q + 1, rw, q == 0 ? g.kq : q == 1 ? g.ko : q == 2 ? g.kf : g.kd, lw, lane,
+                      lbase);
+                __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
+                if (lane == 0) __hip_atomic_fetch_add(LANDED + q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
+        return;
+    }
+    // ---- compute waves
+    int pgen = 0;  // barrier arrivals so far
+    float* rec = (mw == 0) ? a.record + (size_t)(*a.step_p) * a.rec_stride : nullptr;
+    float xr[PK_KE];
+#pragma unroll
+    for (int k = 0; k < PK_KE; ++k) xr[k] = 0.0f;
+    const int passes = 4 * L + (mw == 0 ? 1 : 0);
+    for (int it = 0; it < passes; ++it) {
+        const int l = it >> 2, ph = it & 3;
+        const bool fin = l == L;  // the final norm
+        const int lv = fin ? L - 1 : l;
+        const float* nrm = a.norms + a.ns * lv;  // this layer's norms
+        const uint32_t tag = base + (uint32_t)l + 1;
+        // The thread index through an empty asm: addresses derived from it
+        // are recomputed per pass instead of being held in registers.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        // ---- the input, among the poller waves
+        if (poller) {
+            bool ok = true;
+            // The norms' gammas first (attn +0, post_attn +E+2hd, ffn +2E+2hd,
+            // post_ffw +3E+2hd): their loads overlap the wait for the input.
+            float g1v[PK_KE], g2v[PK_KE];
+            const bool norms = ph == 0 || ph == 2;
+            if (norms) {
+                const int hd2 = 2 * (a.QD / a.H);
+                const float* g1 = ph == 2 ? nrm + E + hd2 : a.norms + a.ns * (l - 1) + 3 * E + hd2;  // ph 0: layer l - 1's
+                const float* g2 = fin ? a.out_norm : ph == 2 ? nrm + 2 * E + hd2 : nrm;
+#pragma unroll
+                for (int k = 0; k < PK_KE; ++k) {
+                    const int i = tid + PK_POLL * k;
+                    g1v[k] = (i < E && it > 0) ? g1[i] : 0.0f;
+                    g2v[k] = i < E ? g2[i] : 0.0f;
+                }
+            }
+            if (it == 0) {
+                // The token's Q8_0 row times sqrt(n_embd) (kernels/mod.rs:917-929).
+                const size_t t = (size_t)*a.tok;
+#pragma unroll
+                for (int k = 0; k < PK_KE; ++k) {
+                    const int i = tid + PK_POLL * k;
+                    if (i < E) {
+                        const float vs = __fmul_rn(bf16f(a.ts[t * (E / 32) + i / 32]), a.embd_scale);
+                        xr[k] = __fmul_rn((float)a.tq[t * E + i], vs);
+                    }
+                }
+            } else {
+                const uint64_t* src = ph == 0 ? a.t_down : ph == 1 ? a.t_attn : ph == 2 ? a.t_o : a.t_h;
+                const int n = ph == 1 ? a.QD : ph == 3 ? a.F : E;
+                float* dst = ph == 1 ? Y : ph == 3 ? H : IN;
+                if (!read_tagged<PK_KF>(src, n, tid, ph == 0 ? tag - 1 : tag, a.err, dst)) *ABORT = 1;
+            }
+            if (norms) {
+                // x += RMSNorm(in) * g1, y = RMSNorm(x) * g2 (forward.rs:749-803).
+                float* r = (rec && ph == 0 && l > 0) ? rec + (size_t)(l - 1) * E : nullptr;
+                ok = pbar(PCTR, pgen) && !*ABORT;
+                if (ok && !residual_norms(a, tid, IN, xr, g1v, g2v, XT, Y, BC, PCTR, pgen, r, it > 0)) *ABORT = 1;
+            }
+            // This phase's weights have landed (all four loader waves).
+            if (tid == 0 && !fin && !lds_wait_ge(LANDED + ph, PK_LOADERS * (l + 1), ABORT)) {
+                flag_raise(a.err);
+                *ABORT = 1;
+            }
+        }
+        if (!pbar(PCTR, pgen)) *ABORT = 1;
+        if (*ABORT) break;
+        if (fin) {
+            for (int i = tid; i < E; i += PK_CW) a.y[i] = Y[i];
+            break;
+        }
+        // ---- the rows: 32 lanes per row (one chain each) where there are
+        // few rows, 16 lanes (two chains each) for gate / up; one call site
+        // per matrix shape, so a known block count unrolls.
+        {
+            const int nrows = ph == 0 ? q1 - q0 : ph == 1 ? o1 - o0 : ph == 2 ? 2 * nf : d1 - d0;
+            if (ph == 2)
+                rows16<NBE>(a.geo[2], lds + g.fw, lds + g.fs, Y, nrows, RES, tid);
+            else if (ph == 0)
+                rows32<NBE>(a.geo[0], lds + g.qw, lds + g.qs, Y, nrows, a.t_qkv + q0, tag, tid);
+            else if (ph == 1)
+                rows32<NBQ>(a.geo[1], lds + g.ow, lds + g.os, Y, nrows, a.t_o + o0, tag, tid);
+            else
+                rows32<NBF>(a.geo[3], lds + g.dw, lds + g.ds, H, nrows, a.t_down + d0, tag, tid);
+        }
+        if (!pbar(PCTR, pgen)) *ABORT = 1;
+        // The region is free for the next layer's copies (gate / up only
+        // after down: the down input H lives there).
+        if (tid == 0 && ph != 2)
+            __hip_atomic_store(FREED + (ph == 3 ? 2 : ph), l + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (ph == 2 && tid < nf) tstore(a.t_h + f0 + tid, __fmul_rn(gelu_lane(RES[tid]), RES[nf + tid]), tag);
+    }
+}
+
+// ---- attention workgroups --------------------------------------------------------------
 
 // The first-maximum scan's step (scalar.rs attn_block): b follows a.
 __device__ __forceinline__ float first_max(float a, float b) { return a < b ? b : a; }
 
-// Attention workgroups per query head: each runs every score of its head
-// and the V chains of HD / ATTN_SPLIT output elements.
-constexpr int ATTN_SPLIT = 8;
-// Threads per attention workgroup: all 16 waves issue the cache loads (a
-// wave keeps only a few loads in flight), the first 4 do the rest.
-constexpr int ATTN_NT = 1024;
+// Position of element e in a chain-major key row: score lane u = e % 4
+// multiplies elements 8c + u (c = 0 .. HD/8 - 1), then 8c + u + 4.
+__host__ __device__ __forceinline__ int kperm(int e, int hd) { return (e & 3) * (hd / 4) + ((e >> 2) & 1) * (hd / 8) + (e >> 3); }
 
-// One query head, one key block (forward.rs:326-351 and attn_block /
-// attn_finish, scalar.rs:444-548): q / k RMSNorm, NeoX RoPE at the current
-// position, the K/V append (by one workgroup per KV head), scores by 8-lane
-// FMA dots and hsum8 times the scale, the first maximum, exp_lane, the
-// 8-lane sum of the weights over whole chunks then the tail in order, and
-// the V sum as one FMA chain per output element over the keys in order,
-// / sum. Workgroup (h, e) of ATTN_SPLIT per head computes all of head h's
-// scores (thread t scores key t) and output elements e * EW .. e * EW + EW - 1.
-// The cached keys 0..n-2 and the workgroup's slice of their values are
-// copied into LDS at the start by coalesced direct loads; a key row's
-// 16-byte chunks are stored XOR-swizzled by the row index, so the score
-// threads (one row each) read different banks. The new key and value come
-// from LDS.
 template <int HD>
-__global__ __launch_bounds__(ATTN_NT) void attn_kernel(AttnArgs a) {
-    static_assert(HD % 64 == 0 && HD <= WG && ATTN_BLOCK <= WG, "head size, key block");
-    constexpr int HALF = HD / 2, CH = HD / 8, EW = HD / ATTN_SPLIT, VCH = EW / 8;
-    constexpr int ST = ATTN_BLOCK / 8 + 4;  // transposed weights: lane l's run at l * ST
-    constexpr int VS = ATTN_BLOCK + 8;  // transposed value rows: element e's keys at e * VS
-    constexpr int VL = (ATTN_BLOCK * VCH + ATTN_NT - 1) / ATTN_NT;  // value pieces per thread
-    constexpr int QS = CH + 4;  // qe row stride: 16-byte rows, the pad spreads the four lanes' reads
-    __shared__ __attribute__((aligned(16))) uint16_t ks_lds[ATTN_BLOCK * HD];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[EW * VS];
-    __shared__ __attribute__((aligned(16))) float qs[HD];
-    __shared__ __attribute__((aligned(16))) float ks[HD];
-    __shared__ __attribute__((aligned(16))) float qt[HD + 32];
-    __shared__ __attribute__((aligned(16))) float qe[8 * QS];  // rotated q by element of chunk: qe[e * QS + c] = q[8c + e]
-    __shared__ __attribute__((aligned(16))) float kt[HD + 32];
-    __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
-    __shared__ __attribute__((aligned(16))) float sc[ATTN_BLOCK];
-    __shared__ __attribute__((aligned(16))) float sct[8 * ST];
-    __shared__ float red[2 + ATTN_NT / 64 + 1];
+struct AttnLds {
+    static constexpr int EW = HD / PK_S, VCH = EW / 8, ST = ATTN_BLOCK / 8 + 4, VS = ATTN_BLOCK + 8, QS = HD / 8 + 4;
+    static constexpr int vt = 0;                                      // uint16 [EW][VS]
+    static constexpr int pq = ((EW * VS * 2 + 255) / 256) * 256;      // polled q, k, v: float [3][HD]
+    static constexpr int qt = pq + 3 * HD * 4;                        // float [8 * tstride(HD)]
+    static constexpr int kt = qt + 8 * (HD / 8 + 4) * 4;
+    static constexpr int qs = kt + 8 * (HD / 8 + 4) * 4;              // float [HD]
+    static constexpr int ks = qs + HD * 4;
+    static constexpr int qe = ks + HD * 4;                            // float [8][QS]
+    static constexpr int knp = qe + 8 * QS * 4;                       // uint16 [HD], chain-major
+    static constexpr int sc = knp + HD * 2;                           // float [ATTN_BLOCK]
+    static constexpr int sct = sc + ATTN_BLOCK * 4;                   // float [8][ST]
+    static constexpr int red = sct + 8 * ST * 4;                      // float [32]
+    static constexpr int bytes = red + 32 * 4;
+};
+
+// A key block [k0, k1] (k1 <= pos): the cached keys (positions < pos) into
+// registers, chain-major (lane u of key t: 16-byte pieces u * HD/4 ..), and
+// this workgroup's slice of the cached values.
+template <int HD>
+struct KvRegs {
+    using Lay = AttnLds<HD>;
+    static constexpr int KR = HD / 32;  // 16-byte pieces of a lane's key values
+    static constexpr int VL = (ATTN_BLOCK * Lay::VCH + PK_NT - 1) / PK_NT;
+    uint4 kr[KR], vr[VL];
+    __device__ __forceinline__ void load(const uint16_t* kc, const uint16_t* vc, size_t kv_dim, int kvh, int es, int k0,
+                                         int k1, int pos) {
+        const int tid = threadIdx.x, t = tid >> 2, u = tid & 3;
+        const int last_cached = min(k1, pos - 1);
+        if (k0 + t <= last_cached) {
+            const uint16_t* p = kc + (size_t)(k0 + t) * kv_dim + kvh * HD + u * (HD / 4);
+#pragma unroll
+            for (int c = 0; c < KR; ++c) kr[c] = *(const uint4*)(p + 8 * c);
+        }
+        const int nv = (last_cached - k0 + 1) * Lay::VCH;
+        const uint16_t* vb = vc + (size_t)k0 * kv_dim + kvh * HD + es * Lay::EW;
+#pragma unroll
+        for (int k = 0; k < VL; ++k) {
+            const int q = tid + PK_NT * k;
+            if (q < nv) vr[k] = *(const uint4*)(vb + (size_t)(q / Lay::VCH) * kv_dim + 8 * (q % Lay::VCH));
+        }
+    }
+};
+
+// One query head, every layer (forward.rs:326-351 and attn_block /
+// attn_merge / attn_finish, scalar.rs:444-548): q / k RMSNorm, NeoX RoPE at
+// the current position, the K/V append (by the head of each KV group),
+// then per key block: scores by 8-lane FMA dots and hsum8 times the scale,
+// the first maximum, exp_lane, the 8-lane sum of the weights over whole
+// chunks then the tail in order, the V sum as one FMA chain per output
+// element over the keys in order; blocks merged in order; / sum.
+template <int HD>
+__device__ __forceinline__ void attn_wg(const PkArgs& a, uint8_t* lds, uint32_t base) {
+    using Lay = AttnLds<HD>;
+    constexpr int HALF = HD / 2, CH = HD / 8, EW = Lay::EW, VCH = Lay::VCH, ST = Lay::ST, VS = Lay::VS, QS = Lay::QS;
+    constexpr int KR = KvRegs<HD>::KR, VL = KvRegs<HD>::VL;
+    uint16_t* vt = (uint16_t*)(lds + Lay::vt);
+    float* pq = (float*)(lds + Lay::pq);
+    float* qt = (float*)(lds + Lay::qt);
+    float* kt = (float*)(lds + Lay::kt);
+    float* qs = (float*)(lds + Lay::qs);
+    float* ks = (float*)(lds + Lay::ks);
+    float* qe = (float*)(lds + Lay::qe);
+    uint16_t* knp = (uint16_t*)(lds + Lay::knp);
+    float* sc = (float*)(lds + Lay::sc);
+    float* sct = (float*)(lds + Lay::sct);
+    float* red = (float*)(lds + Lay::red);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = *a.pos_p, h = blockIdx.x / ATTN_SPLIT, es = blockIdx.x % ATTN_SPLIT, kvh = h / a.group;
-    const int first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-    const int n = pos + 1 - first;  // keys; the last is the new one
-    const size_t kv_dim = (size_t)a.KV * HD;
-    const int i = tid < HD ? tid : HD - 1;
-    const float qv = a.q[h * HD + i], kv = a.k[kvh * HD + i];
-    const float vv = a.v[kvh * HD + es * EW + (tid < EW ? tid : EW - 1)];
-    const float qg = a.q_norm[i], kg = a.k_norm[i];
-    const float cs = a.cos_t[(size_t)pos * HALF + i % HALF], sn = a.sin_t[(size_t)pos * HALF + i % HALF];
-    // This slice of the cached values (keys first .. pos - 1), 16-byte pieces
-    // into registers (a fixed count per thread, clamped), stored transposed
-    // into LDS once they land.
-    const uint16_t* vbase = a.vc + kvh * HD + es * EW + (size_t)first * kv_dim;
-    const int nv = max((n - 1) * VCH, 1);
-    uint4 vr[VL];
-#pragma unroll
-    for (int k = 0; k < VL; ++k) {
-        const int u = min(tid + ATTN_NT * k, nv - 1);
-        vr[k] = *(const uint4*)(vbase + (size_t)(u / VCH) * kv_dim + 8 * (u % VCH));
-    }
-    // Cached keys, 16 bytes per lane straight into LDS, 1 KB per wave
-    // instruction; pieces past the end repeat the last one (their LDS slots
-    // are never read).
-    {
-        const uint16_t* kbase = a.kc + kvh * HD + (size_t)first * kv_dim;
-        const int nk = (n - 1) * CH, nik = (nk + 63) / 64;
-        for (int k = wave; k < nik; k += ATTN_NT / 64) {
-            const int u = min(64 * k + lane, nk - 1);
-            const int t = u / CH, c = u % CH;  // LDS chunk c of row t holds key chunk c ^ (t % CH)
-            __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)t * kv_dim + 8 * (c ^ (t % CH))),
-                                             (lds_ptr_t)(ks_lds + 512 * k), 16, 0, 0);
+    const int h = blockIdx.x / PK_S, es = blockIdx.x % PK_S, group = a.H / a.KV, kvh = h / group;
+    const size_t kv_dim = (size_t)a.KVD;
+    const int pos = *a.pos_p;
+    for (int l = 0; l < a.n_layer; ++l) {
+        const uint32_t tag = base + (uint32_t)l + 1;
+        const bool sliding = a.swa_period > 0 && (l + 1) % a.swa_period != 0;  // load.rs:1156-1160
+        const int window = sliding ? a.window : 0;
+        uint16_t* kc = a.kc + a.kv_layer * l;
+        uint16_t* vc = a.vc + a.kv_layer * l;
+        const float* q_norm = a.norms + a.ns * l + a.E;
+        const float* k_norm = q_norm + HD;
+        const size_t tab = sliding ? 0 : (size_t)a.n_ctx * HALF;
+        const int first = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+        const int bf = first / ATTN_BLOCK, bl = pos / ATTN_BLOCK;
+        KvRegs<HD> kv;
+        {
+            const int k0 = max(first, bf * ATTN_BLOCK), k1 = min(pos, bf * ATTN_BLOCK + ATTN_BLOCK - 1);
+            kv.load(kc, vc, kv_dim, kvh, es, k0, k1, pos);
         }
-    }
-    // q and k RMSNorm: wave 0 runs q's chains, wave 1 k's (transposed copies).
-    if (tid < HD) {
-        qt[(tid & 7) * tstride(HD) + (tid >> 3)] = qv;
-        kt[(tid & 7) * tstride(HD) + (tid >> 3)] = kv;
-    }
-    lds_barrier();
-    if (wave < 2) {
-        const float ss = chain_sumsq(wave == 0 ? qt : kt, HD, lane);
-        if (lane == 0) {
-            const float inv_dim = __fdiv_rn(1.0f, (float)HD);
-            red[wave] = (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn((double)ss, (double)inv_dim), (double)a.eps)));
+        // The norm gammas and RoPE's cos / sin, loaded before the wait.
+        const int e = tid < HD ? tid : HD - 1, jr = e % HALF;
+        const float qg = q_norm[e], kg = k_norm[e];
+        const float cs = a.cos_t[tab + (size_t)pos * HALF + jr], sn = a.sin_t[tab + (size_t)pos * HALF + jr];
+        // q of head h, k and v of its KV head.
+        if (tid == 0) red[30] = 0.0f;
+        lds_barrier();
+        if (tid < 3 * HD) {
+            const int part = tid / HD, e = tid % HD;
+            const int src = part == 0 ? h * HD + e : a.QD + (part - 1) * a.KVD + kvh * HD + e;
+            if (!poll_tagged<1>(a.t_qkv + src, 1, 0, 1, tag, a.err, pq + tid)) red[30] = 1.0f;
         }
-    }
-    lds_barrier();
-    if (tid < HD) {
-        qs[tid] = __fmul_rn(__fmul_rn(qv, red[0]), qg);
-        ks[tid] = __fmul_rn(__fmul_rn(kv, red[1]), kg);
-    }
-    if (tid < EW) vt[tid * VS + n - 1] = to_bf16(vv);  // the new value: key n - 1
-    lds_barrier();
-    // RoPE: threads 0..HALF-1 rotate q's pairs (j, j + HALF), HALF..HD-1 k's.
-    if (tid < HALF) {
-        const float x0 = qs[tid], x1 = qs[tid + HALF];
-        const float r0 = __fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1));
-        const float r1 = __fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1));
-        qe[(tid & 7) * QS + (tid >> 3)] = r0;
-        qe[((tid + HALF) & 7) * QS + ((tid + HALF) >> 3)] = r1;
-    } else if (tid < HD) {
-        const int j = tid - HALF;
-        const float x0 = ks[j], x1 = ks[j + HALF];
-        kn[j] = to_bf16(__fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1)));
-        kn[j + HALF] = to_bf16(__fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1)));
-    }
-    // The cached keys and values have landed (each wave its own copies,
-    // then the barrier for the others').
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int k = 0; k < VL; ++k) {
-        const int u = tid + ATTN_NT * k;
-        if (u < (n - 1) * VCH) {
-            const int t = u / VCH, e0 = 8 * (u % VCH);
-            const uint32_t w[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-#pragma unroll
-            for (int q = 0; q < 8; ++q) vt[(e0 + q) * VS + t] = (uint16_t)(w[q / 2] >> (16 * (q & 1)));
+        lds_barrier();
+        if (red[30] != 0.0f) break;
+        // q and k RMSNorm: wave 0 runs q's chain, wave 1 k's (transposed copies).
+        if (tid < HD) {
+            tput(qt, tstride(HD), tid, pq[tid]);
+            tput(kt, tstride(HD), tid, pq[HD + tid]);
         }
-    }
-    lds_barrier();
-    if (h % a.group == 0 && tid < HD) {
-        if (es == 0) a.kc[(size_t)pos * kv_dim + kvh * HD + tid] = kn[tid];
-        if (tid < EW) a.vc[(size_t)pos * kv_dim + kvh * HD + es * EW + tid] = vt[tid * VS + n - 1];
-    }
-    // Scores: four lanes per key (key tid / 4), lane u running the dot's
-    // chains u and u + 4 (elements 8c + u and 8c + u + 4, c in order), then
-    // (a_u + a_{u+4}), xor-1, xor-2: hsum8's additions in its order. Each
-    // lane's q values are contiguous in qe; a key chunk's two values are two
-    // 32-bit LDS reads.
-    {
-        const int t = tid >> 2, u = tid & 3;
-        float a0 = 0.0f, a1 = 0.0f;
-        if (t < n) {
-            const bool last = t == n - 1;
-            const uint16_t* krow = last ? kn : ks_lds + t * HD;
-            const int sw = last ? 0 : t % CH;
-            const float* q0 = qe + u * QS;
-            const float* q1 = qe + (u + 4) * QS;
-            const int hs = 16 * (u & 1);
-#pragma unroll
-            for (int c0 = 0; c0 < CH; c0 += 4) {
-                const float4 qa = *(const float4*)(q0 + c0), qb = *(const float4*)(q1 + c0);
-                const float qav[4] = {qa.x, qa.y, qa.z, qa.w}, qbv[4] = {qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    const uint32_t* kc = (const uint32_t*)(krow + 8 * ((c0 + cc) ^ sw));
-                    const uint32_t klo = kc[u >> 1], khi = kc[2 + (u >> 1)];
-                    a0 = __fmaf_rn(qav[cc], bf16f((klo >> hs) & 0xffffu), a0);
-                    a1 = __fmaf_rn(qbv[cc], bf16f((khi >> hs) & 0xffffu), a1);
-                }
-            }
+        lds_barrier();
+        if (wave < 2) {
+            const float ss = chain_sumsq(wave == 0 ? qt : kt, HD, lane);
+            if (lane == 0) red[wave] = rms_of(ss, HD, a.eps);
         }
-        float p = __fadd_rn(a0, a1);
-        p = __fadd_rn(p, __shfl_xor(p, 1, 64));
-        p = __fadd_rn(p, __shfl_xor(p, 2, 64));
-        if (t < n && u == 0) sc[t] = __fmul_rn(p, a.scale);
-    }
-    lds_barrier();
-    const float s_t = tid < n ? sc[tid] : -INFINITY;
-    // The first maximum over keys in order: a leftmost-maximum tree, with a
-    // NaN after key 0 never taken (as the scan's comparison never takes one)
-    // and a NaN at key 0 kept (it is never replaced).
-    float mv = (tid > 0 && s_t != s_t) ? -INFINITY : s_t;
-#pragma unroll
-    for (int k = 1; k < 64; k <<= 1) {
-        const float o = __shfl_xor(mv, k, 64);
-        mv = (lane & k) ? first_max(o, mv) : first_max(mv, o);
-    }
-    if (lane == 0) red[2 + wave] = mv;
-    lds_barrier();
-    float m = red[2];
-#pragma unroll
-    for (int w = 1; w < ATTN_NT / 64; ++w) m = first_max(m, red[2 + w]);
-    if (tid < n) {
-        const float pw = exp_lane(__fsub_rn(s_t, m));
-        sc[tid] = pw;
-        sct[(tid & 7) * ST + (tid >> 3)] = pw;
-    }
-    lds_barrier();
-    if (tid < 64) {
-        // The eight add lanes over the whole chunks of 8, in order.
-        const int body = n & ~7, K = body / 8;
-        float acc = 0.0f;
-        if (tid < 8) {
-            const float* p = sct + tid * ST;
-            int k = 0;
-            for (; k + 4 <= K; k += 4) {
-                const float4 v = *(const float4*)(p + k);
-                acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, v.x), v.y), v.z), v.w);
-            }
-            for (; k < K; ++k) acc = __fadd_rn(acc, p[k]);
+        lds_barrier();
+        if (tid < HD) {
+            qs[tid] = __fmul_rn(__fmul_rn(pq[tid], red[0]), qg);
+            ks[tid] = __fmul_rn(__fmul_rn(pq[HD + tid], red[1]), kg);
         }
-        float l = hsum8_lanes(acc);
-        if (tid == 0) {
-            for (int j = body; j < n; ++j) l = __fadd_rn(l, sc[j]);
-            red[2 + ATTN_NT / 64] = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
-        }
-    }
-    lds_barrier();
-    if (tid < EW) {
-        // V: one FMA chain per element over the keys in order, 8 keys per
-        // 16-byte read of the transposed values (and two of the weights),
-        // the next batch's reads issued before this batch's FMAs.
-        const uint16_t* vrow = vt + tid * VS;
-        const int nbat = (n + 7) / 8;
-        float o = 0.0f;
-        uint4 va, vb;
-        float4 pa0, pa1, pb0, pb1;
-        auto fetch = [&](uint4& v, float4& p0, float4& p1, int b) {
-            v = *(const uint4*)(vrow + 8 * b);
-            p0 = *(const float4*)(sc + 8 * b);
-            p1 = *(const float4*)(sc + 8 * b + 4);
-        };
-        auto batch = [&](const uint4& v, const float4& p0, const float4& p1, int b) {
-            const float vv[8] = {bf16f(v.x & 0xffffu), bf16f(v.x >> 16), bf16f(v.y & 0xffffu), bf16f(v.y >> 16),
-                                 bf16f(v.z & 0xffffu), bf16f(v.z >> 16), bf16f(v.w & 0xffffu), bf16f(v.w >> 16)};
-            const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-            if (b > 0 && 8 * b + 8 <= n) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o = __fmaf_rn(pp[j], vv[j], o);
+        lds_barrier();
+        // RoPE: threads 0..HALF-1 rotate q's pairs (j, j + HALF), HALF..HD-1 k's.
+        if (tid < HD) {
+            const int j = jr;
+            const float* src = tid < HALF ? qs : ks;
+            const float x0 = src[j], x1 = src[j + HALF];
+            const float r0 = __fsub_rn(__fmul_rn(cs, x0), __fmul_rn(sn, x1));
+            const float r1 = __fadd_rn(__fmul_rn(sn, x0), __fmul_rn(cs, x1));
+            if (tid < HALF) {
+                qe[(j & 7) * QS + (j >> 3)] = r0;
+                qe[((j + HALF) & 7) * QS + ((j + HALF) >> 3)] = r1;
             } else {
+                knp[kperm(j, HD)] = to_bf16(r0);
+                knp[kperm(j + HALF, HD)] = to_bf16(r1);
+            }
+        }
+        lds_barrier();
+        // The K/V append (forward.rs:326-351): the head of each KV group.
+        if (h % group == 0) {
+            if (es == 0 && tid < HD) kc[(size_t)pos * kv_dim + kvh * HD + tid] = knp[tid];
+            if (tid < EW)
+                vc[(size_t)pos * kv_dim + kvh * HD + es * EW + tid] = to_bf16(pq[2 * HD + es * EW + tid]);
+        }
+        float acc_o = 0.0f, acc_m = 0.0f, acc_l = 0.0f;
+        for (int b = bf; b <= bl; ++b) {
+            const int k0 = max(first, b * ATTN_BLOCK), k1 = min(pos, b * ATTN_BLOCK + ATTN_BLOCK - 1);
+            const int n = k1 - k0 + 1;
+            if (b > bf) kv.load(kc, vc, kv_dim, kvh, es, k0, k1, pos);
+            // This slice of the values, transposed into LDS (the new one from q/k/v).
+            {
+                const int nv = (min(k1, pos - 1) - k0 + 1) * VCH;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int t = 8 * b + j;
-                    if (t < n) o = t == 0 ? __fmul_rn(pp[j], vv[j]) : __fmaf_rn(pp[j], vv[j], o);
+                for (int k = 0; k < VL; ++k) {
+                    const int q = tid + PK_NT * k;
+                    if (q < nv) {
+                        const int t = q / VCH, e0 = 8 * (q % VCH);
+                        const uint32_t w[4] = {kv.vr[k].x, kv.vr[k].y, kv.vr[k].z, kv.vr[k].w};
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) vt[(e0 + i) * VS + t] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
+                    }
+                }
+                if (k1 == pos && tid < EW) vt[tid * VS + (pos - k0)] = to_bf16(pq[2 * HD + es * EW + tid]);
+            }
+            // Scores: four lanes per key (key tid / 4), lane u running the
+            // dot's chains u and u + 4 (elements 8c + u and 8c + u + 4, c in
+            // order), then (a_u + a_{u+4}), xor-1, xor-2: hsum8's additions
+            // in its order.
+            {
+                const int t = tid >> 2, u = tid & 3;
+                float a0 = 0.0f, a1 = 0.0f;
+                if (t < n) {
+                    uint4* kk = kv.kr;
+                    if (k0 + t == pos) {  // the new key, from LDS
+#pragma unroll
+                        for (int c = 0; c < KR; ++c) kk[c] = *(const uint4*)(knp + u * (HD / 4) + 8 * c);
+                    }
+                    const float* q0 = qe + u * QS;
+                    const float* q1 = qe + (u + 4) * QS;
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) {
+                        const uint4 lo = kk[c / 8], hi = kk[KR / 2 + c / 8];
+                        const uint32_t wl[4] = {lo.x, lo.y, lo.z, lo.w}, wh[4] = {hi.x, hi.y, hi.z, hi.w};
+                        const int i = c % 8;
+                        a0 = __fmaf_rn(q0[c], bf16f((wl[i >> 1] >> (16 * (i & 1))) & 0xffffu), a0);
+                        a1 = __fmaf_rn(q1[c], bf16f((wh[i >> 1] >> (16 * (i & 1))) & 0xffffu), a1);
+                    }
+                }
+                float p = __fadd_rn(a0, a1);
+                p = __fadd_rn(p, __shfl_xor(p, 1, 64));
+                p = __fadd_rn(p, __shfl_xor(p, 2, 64));
+                if (t < n && u == 0) sc[t] = __fmul_rn(p, a.attn_scale);
+            }
+            lds_barrier();
+            const float s_t = tid < n ? sc[tid] : -INFINITY;
+            // The first maximum over keys in order: a leftmost-maximum tree,
+            // with a NaN after key 0 never taken (as the scan's comparison
+            // never takes one) and a NaN at key 0 kept (it is never replaced).
+            float mv = (tid > 0 && s_t != s_t) ? -INFINITY : s_t;
+#pragma unroll
+            for (int k = 1; k < 64; k <<= 1) {
+                const float o = __shfl_xor(mv, k, 64);
+                mv = (lane & k) ? first_max(o, mv) : first_max(mv, o);
+            }
+            if (lane == 0) red[2 + wave] = mv;
+            lds_barrier();
+            float m = red[2];
+#pragma unroll
+            for (int w = 1; w < PK_NT / 64; ++w) m = first_max(m, red[2 + w]);
+            if (tid < n) {
+                const float pw = exp_lane(__fsub_rn(s_t, m));
+                sc[tid] = pw;
+                sct[(tid & 7) * ST + (tid >> 3)] = pw;
+            }
+            lds_barrier();
+            if (tid < 64) {
+                // The eight add lanes over the whole chunks of 8, in order.
+                const int body = n & ~7, K = body / 8;
+                float acc = 0.0f;
+                if (tid < 8) {
+                    const float* p = sct + tid * ST;
+                    int k = 0;
+                    for (; k + 4 <= K; k += 4) {
+                        const float4 v = *(const float4*)(p + k);
+                        acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, v.x), v.y), v.z), v.w);
+                    }
+                    for (; k < K; ++k) acc = __fadd_rn(acc, p[k]);
+                }
+                float ls = hsum8_lanes(acc);
+                if (tid == 0) {
+                    for (int j = body; j < n; ++j) ls = __fadd_rn(ls, sc[j]);
+                    red[2 + PK_NT / 64] = ls;
                 }
             }
-        };
-        fetch(va, pa0, pa1, 0);
-        for (int b = 0; b < nbat; b += 2) {
-            fetch(vb, pb0, pb1, min(b + 1, nbat - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            batch(va, pa0, pa1, b);
-            fetch(va, pa0, pa1, min(b + 2, nbat - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 1 < nbat) batch(vb, pb0, pb1, b + 1);
+            lds_barrier();
+            const float lsum = red[2 + PK_NT / 64];
+            float o = 0.0f;
+            if (tid < EW) {
+                // V: one FMA chain per element over the keys in order, 8 keys
+                // per 16-byte read of the transposed values.
+                const uint16_t* vrow = vt + tid * VS;
+                const int nbat = (n + 7) / 8;
+                for (int bb = 0; bb < nbat; ++bb) {
+                    const uint4 v = *(const uint4*)(vrow + 8 * bb);
+                    const float4 p0 = *(const float4*)(sc + 8 * bb), p1 = *(const float4*)(sc + 8 * bb + 4);
+                    const float vv[8] = {bf16f(v.x & 0xffffu), bf16f(v.x >> 16), bf16f(v.y & 0xffffu), bf16f(v.y >> 16),
+                                         bf16f(v.z & 0xffffu), bf16f(v.z >> 16), bf16f(v.w & 0xffffu), bf16f(v.w >> 16)};
+                    const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int t = 8 * bb + j;
+                        if (t < n) o = t == 0 ? __fmul_rn(pp[j], vv[j]) : __fmaf_rn(pp[j], vv[j], o);
+                    }
+                }
+            }
+            if (b == bf) {
+                acc_o = o;
+                acc_m = m;
+                acc_l = lsum;
+            } else {
+                // scalar.rs:521-537 (gemma3.cpp attn_merge).
+                const float mm = acc_m < m ? m : acc_m;
+                const float ca = glibc_expf(__fsub_rn(acc_m, mm), a.expt), cb = glibc_expf(__fsub_rn(m, mm), a.expt);
+                acc_o = __fmaf_rn(o, cb, __fmul_rn(acc_o, ca));
+                acc_m = mm;
+                acc_l = __fadd_rn(__fmul_rn(acc_l, ca), __fmul_rn(lsum, cb));
+            }
+            lds_barrier();  // sc, vt and red are rewritten by the next block
         }
-        a.out[h * HD + es * EW + tid] = __fmul_rn(o, red[2 + ATTN_NT / 64]);
+        if (tid < EW) {
+            const float inv = acc_l > 0.0f ? __fdiv_rn(1.0f, acc_l) : 0.0f;
+            tstore(a.t_attn + h * HD + es * EW + tid, __fmul_rn(acc_o, inv), tag);
+        }
+
     }
+}
+
+// The arguments live in device memory (a by-value struct whose address the
+// workgroup code takes would be copied to the stack).
+// NBE, NBQ, NBF: the block counts of the n_embd-, q-dim- and n_ff-column
+// matrices when compiled for them (Gemma-3-1B's), else 0.
+template <int HD, int NBE, int NBQ, int NBF>
+__global__ __launch_bounds__(PK_NT) void step_kernel(const PkArgs* __restrict__ ap) {
+    __shared__ __attribute__((aligned(256))) uint8_t lds[PK_LDS];
+    const PkArgs& a = *ap;
+    const uint32_t base = *a.seq_p * (uint32_t)a.n_layer;
+    if ((int)blockIdx.x < a.A)
+        attn_wg<HD>(a, lds, base);
+    else
+        matmul_wg<NBE, NBQ, NBF>(a, lds, base);
 }
 
 // End of a step: the greedy token is recorded, the position advances.
-__global__ void step_end_kernel(const uint64_t* tok, int* tokens_out, int* pos_p, int* step_p) {
+__global__ void step_end_kernel(const uint64_t* tok, int* tokens_out, int* pos_p, int* step_p, uint32_t* seq_p) {
     tokens_out[*step_p] = (int)*tok;
     *pos_p += 1;
     *step_p += 1;
+    *seq_p += 1;
 }
 
-#define GD_HIP(expr)                                                                       \
-    do {                                                                                   \
-        hipError_t e_ = (expr);                                                            \
-        if (e_ != hipSuccess) {                                                            \
-            m->err = std::string(#expr) + ": " + hipGetErrorString(e_);                    \
-            return 1;                                                                      \
-        }                                                                                  \
-    } while (0)
-
-// Weight-load slots of the fused matmuls: at least the rows' groups.
-template <bool FIRST>
-static void launch_qkv(const QkvArgs& a, int ngp, int wgs, hipStream_t st) {
-    if (ngp <= 4)
-        qkv_kernel<4, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
-    else if (ngp <= 6)
-        qkv_kernel<6, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
-    else
-        qkv_kernel<8, FIRST><<<wgs, QKV_NT, 0, st>>>(a);
-}
-
-static void launch_ffn(const FfnArgs& a, int ngp, int wgs, hipStream_t st) {
-    if (ngp <= 4)
-        ffn_kernel<4><<<wgs, FFN_NT, 0, st>>>(a);
-    else if (ngp <= 6)
-        ffn_kernel<6><<<wgs, FFN_NT, 0, st>>>(a);
-    else
-        ffn_kernel<8><<<wgs, FFN_NT, 0, st>>>(a);
+// The CPU harness's K cache (natural order) into the chain-major layout.
+__global__ void kperm_kernel(const uint16_t* src, uint16_t* dst, size_t rows, int hd) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * hd) return;
+    const size_t r = i / hd;
+    const int e = (int)(i % hd);
+    dst[r * hd + kperm(e, hd)] = src[i];
 }
 
 }  // namespace
+
+#define GD_HIP(expr)                                                    \
+    do {                                                                \
+        hipError_t e_ = (expr);                                         \
+        if (e_ != hipSuccess) {                                         \
+            m->err = std::string(#expr) + ": " + hipGetErrorString(e_); \
+            return 1;                                                   \
+        }                                                               \
+    } while (0)
 
 extern "C" {
 
 struct nngd_model {
     nng_config c;
     std::vector<nnh_weight*> w;  // 7 * n_layer + 1, lm_head (the tied token_embd) last
-    std::vector<F32Mat> f;       // the 16-lane layouts of the 7 * n_layer layer weights
-    float* norms = nullptr;      // device copy, layout of nng_create
-    uint16_t *kc = nullptr, *vc = nullptr;
+    PkArgs args{};
+    PkArgs* args_dev = nullptr;
+    uint64_t* wptr = nullptr;
+    float* norms = nullptr;  // device copy, layout of nng_create
+    uint16_t *kc = nullptr, *vc = nullptr, *kstage = nullptr;
     float *cos_t = nullptr, *sin_t = nullptr;  // [2][n_ctx][hd/2]: sliding (local) base, then global
-    float *xa = nullptr, *xb = nullptr;        // the residual stream, alternating
-    float *y = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *o = nullptr;
-    float *h = nullptr, *logits = nullptr, *record = nullptr;
+    uint64_t* tagged = nullptr;
+    float *y = nullptr, *logits = nullptr, *record = nullptr;
+    uint64_t* expt = nullptr;
     void* work = nullptr;
     uint64_t* tok = nullptr;
-    int *pos = nullptr, *step = nullptr, *tokens = nullptr;
-    int n_gen_max = 0;
+    int *pos = nullptr, *step = nullptr, *tokens = nullptr, *errf = nullptr;
+    uint32_t* seq = nullptr;
+    int n_gen_max = 0, grid = 0;
+    const void* kernel = nullptr;  // the step kernel instance for this model's shapes
     hipStream_t st = nullptr;
     hipGraphExec_t exec = nullptr;
     std::string err;
@@ -755,12 +1162,31 @@ const char* nngd_error(nngd_model* m) { return m->err.c_str(); }
 void nngd_free(nngd_model* m) {
     if (!m) return;
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    void* bufs[] = {m->norms, m->kc, m->vc, m->cos_t, m->sin_t, m->xa, m->xb, m->y, m->q, m->k, m->v, m->attn, m->o,
-                    m->h, m->logits, m->record, m->work, m->tok, m->pos, m->step, m->tokens};
+    void* bufs[] = {m->args_dev, m->wptr, m->norms, m->kc,   m->vc,  m->kstage, m->cos_t, m->sin_t, m->tagged, m->y,
+                    m->logits, m->record, m->expt, m->work, m->tok,    m->pos,   m->step,  m->tokens, m->errf,
+                    m->seq};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
+}
+
+// The table of glibc_expf: bits of 2^(i / 32) rounded to double, minus i << 47.
+static void expf_table(uint64_t* T) {
+    for (int i = 0; i < 32; ++i) {
+        const double v = (double)exp2l((long double)i / 32);
+        uint64_t u;
+        memcpy(&u, &v, 8);
+        T[i] = u - ((uint64_t)i << 47);
+    }
+}
+
+// glibc_expf on the host (the function the device runs), for the CPU test
+// against the platform's expf.
+void nngd_expf_batch(const float* x, float* y, size_t n) {
+    uint64_t T[32];
+    expf_table(T);
+    for (size_t i = 0; i < n; ++i) y[i] = glibc_expf(x[i], T);
 }
 
 // RoPE tables exactly as gemma3.cpp's rope_neox forms them: ratio =
@@ -779,151 +1205,215 @@ static void rope_table(float base, int n_ctx, int hd, float* cs, float* sn) {
     }
 }
 
+static uint32_t align256(size_t v) { return (uint32_t)((v + 255) & ~(size_t)255); }
+
 int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* weights, int n_weights, int n_gen_max,
                 nngd_model** out) {
     nngd_model* m = new nngd_model();
     *out = m;
     m->c = *cfg;
     const nng_config& c = m->c;
-    if (c.n_ctx > ATTN_BLOCK) {
-        m->err = "the device decode holds one attention block: n_ctx <= 256";
-        return 1;
-    }
     if (n_weights != 7 * c.n_layer + 1 || c.n_head % c.n_kv != 0) {
         m->err = "bad weight count or head grouping";
         return 1;
     }
-    if (c.n_embd % 128 || c.n_embd > E_MAX || (c.head_dim != 128 && c.head_dim != 256) || c.n_ff % 32) {
-        m->err = "the fused step needs n_embd a multiple of 128 up to 2048, head_dim 128 or 256";
+    if (c.n_embd % 128 || c.n_embd > E_MAX || (c.head_dim != 128 && c.head_dim != 256) || c.n_ff % 32 ||
+        c.n_ff > PK_POLL * PK_KF) {
+        m->err = "the device step needs n_embd a multiple of 128 up to 2048, head_dim 128 or 256, n_ff up to 8192";
         return 1;
     }
     m->w.assign(weights, weights + n_weights);
-    // The fused kernels read q, k, v, gate and up in the 16-lane Q8_0 layout.
+    std::vector<F32Mat> f;
     for (int i = 0; i < 7 * c.n_layer; ++i) {
         nnh_f32_layout l;
         if (nnh_weight_f32_layout(weights[i], &l)) {
             m->err = std::string("weight layout: ") + nnh_last_error();
             return 1;
         }
-        const int kind = i % 7;
-        if (kind != 3 && kind != 6 && (l.dtype != NNH_Q8_0 || l.cols != (size_t)c.n_embd)) {
-            m->err = "the fused q, k, v, gate and up matmuls take Q8_0 weights of n_embd columns";
+        if (l.dtype != NNH_Q8_0) {
+            m->err = "the device step takes Q8_0 layer weights";
             return 1;
         }
-        m->f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, l.biases, (int)l.rows, (int)l.nb, (int)l.nbp});
+        f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, l.biases, (int)l.rows, (int)l.nb, (int)l.nbp});
     }
     // The lm_head's layouts too, before any step is captured.
     if (nnh_weight_prepare(m->w.back(), NNH_ACT_F32, 1)) {
         m->err = std::string("lm_head layout: ") + nnh_last_error();
         return 1;
     }
-    m->n_gen_max = n_gen_max;
-    const size_t E = c.n_embd, hd = c.head_dim, qd = (size_t)c.n_head * hd, kvd = (size_t)c.n_kv * hd;
+    int dev = 0, cus = 0;
+    GD_HIP(hipGetDevice(&dev));
+    GD_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int E = c.n_embd, hd = c.head_dim, QD = c.n_head * hd, KVD = c.n_kv * hd, F = c.n_ff;
+    PkArgs& a = m->args;
+    a.n_layer = c.n_layer;
+    a.E = E;
+    a.F = F;
+    a.H = c.n_head;
+    a.KV = c.n_kv;
+    a.QD = QD;
+    a.KVD = KVD;
+    a.A = c.n_head * PK_S;
+    a.M = cus - a.A;
+    a.eps = c.rms_eps;
+    a.attn_scale = c.attn_scale;
+    a.embd_scale = std::sqrt((float)E);
+    if (a.M < 1 || QD + 2 * KVD < a.M || E < a.M || F < a.M || (long)(QD + 2 * KVD + F) * cus >= (1L << 31)) {
+        m->err = "the device step needs every matmul workgroup to own rows of every matrix";
+        return 1;
+    }
+    // LDS of a matmul workgroup: the largest share of each phase's rows.
+    auto most = [&](int total) { return (total + a.M - 1) / a.M; };
+    const F32Mat &mq = f[0], &mo = f[3], &mf = f[4], &md = f[6];
+    PkGeom& g = a.g;
+    size_t o = 0;
+    g.qw = (uint32_t)o, o = align256(o + (size_t)most(QD + 2 * KVD) * qrow_bytes(mq));
+    g.qs = (uint32_t)o, o = align256(o + (size_t)most(QD + 2 * KVD) * srow_bytes(mq));
+    g.ow = (uint32_t)o, o = align256(o + (size_t)most(E) * qrow_bytes(mo));
+    g.os = (uint32_t)o, o = align256(o + (size_t)most(E) * srow_bytes(mo));
+    g.fw = (uint32_t)o;
+    const size_t fw_bytes = (size_t)2 * most(F) * qrow_bytes(mf);
+    o = align256(o + std::max(fw_bytes, (size_t)F * 4));  // H (the down input) aliases the FFN weights
+    g.h = g.fw;
+    g.fs = (uint32_t)o, o = align256(o + (size_t)2 * most(F) * srow_bytes(mf));
+    g.dw = (uint32_t)o, o = align256(o + (size_t)most(E) * qrow_bytes(md));
+    g.ds = (uint32_t)o, o = align256(o + (size_t)most(E) * srow_bytes(md));
+    g.y = (uint32_t)o, o = align256(o + (size_t)std::max(E, QD) * 4);
+    g.in = (uint32_t)o, o = align256(o + (size_t)E * 4);
+    g.xt = (uint32_t)o, o = align256(o + (size_t)8 * tstride(E) * 4);
+    g.res = (uint32_t)o, o = align256(o + (size_t)2 * most(F) * 4);
+    g.bc = (uint32_t)o, o = align256(o + 64);
+    g.wtab = (uint32_t)o, o = align256(o + (size_t)14 * c.n_layer * 8);
+    g.bytes = (uint32_t)o;
+    if (o > (size_t)PK_LDS || (hd == 256 ? AttnLds<256>::bytes : AttnLds<128>::bytes) > PK_LDS) {
+        m->err = "the device step's LDS share exceeds the workgroup's LDS";
+        return 1;
+    }
+    // The layer table.
     const size_t nn = norm_stride(c) * c.n_layer + E, half = hd / 2;
     GD_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
     GD_HIP(hipMalloc((void**)&m->norms, nn * 4));
     GD_HIP(hipMemcpy(m->norms, norms, nn * 4, hipMemcpyHostToDevice));
-    GD_HIP(hipMalloc((void**)&m->kc, (size_t)c.n_layer * c.n_ctx * kvd * 2));
-    GD_HIP(hipMalloc((void**)&m->vc, (size_t)c.n_layer * c.n_ctx * kvd * 2));
+    GD_HIP(hipMalloc((void**)&m->kc, (size_t)c.n_layer * c.n_ctx * KVD * 2));
+    GD_HIP(hipMalloc((void**)&m->vc, (size_t)c.n_layer * c.n_ctx * KVD * 2));
+    GD_HIP(hipMalloc((void**)&m->kstage, (size_t)c.n_layer * c.n_ctx * KVD * 2));
     std::vector<float> cs(2 * (size_t)c.n_ctx * half), sn(2 * (size_t)c.n_ctx * half);
-    rope_table(c.rope_base_swa, c.n_ctx, (int)hd, cs.data(), sn.data());
-    rope_table(c.rope_base, c.n_ctx, (int)hd, cs.data() + (size_t)c.n_ctx * half, sn.data() + (size_t)c.n_ctx * half);
+    rope_table(c.rope_base_swa, c.n_ctx, hd, cs.data(), sn.data());
+    rope_table(c.rope_base, c.n_ctx, hd, cs.data() + (size_t)c.n_ctx * half, sn.data() + (size_t)c.n_ctx * half);
     GD_HIP(hipMalloc((void**)&m->cos_t, cs.size() * 4));
     GD_HIP(hipMalloc((void**)&m->sin_t, sn.size() * 4));
     GD_HIP(hipMemcpy(m->cos_t, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
     GD_HIP(hipMemcpy(m->sin_t, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-    GD_HIP(hipMalloc((void**)&m->xa, E * 4));
-    GD_HIP(hipMalloc((void**)&m->xb, E * 4));
-    GD_HIP(hipMalloc((void**)&m->y, E * 4));
-    GD_HIP(hipMalloc((void**)&m->o, E * 4));
-    GD_HIP(hipMalloc((void**)&m->q, qd * 4));
-    GD_HIP(hipMalloc((void**)&m->k, kvd * 4));
-    GD_HIP(hipMalloc((void**)&m->v, kvd * 4));
-    GD_HIP(hipMalloc((void**)&m->attn, qd * 4));
-    GD_HIP(hipMalloc((void**)&m->h, (size_t)c.n_ff * 4));
+    const size_t ns = norm_stride(c);
+    a.geo[0] = f[0], a.geo[1] = f[3], a.geo[2] = f[4], a.geo[3] = f[6];
+    for (F32Mat& gm : a.geo) gm.fq = nullptr, gm.fs = nullptr, gm.bi = nullptr;
+    for (int li = 0; li < c.n_layer; ++li)
+        for (int j = 0; j < 7; ++j) {
+            const F32Mat& w = f[7 * li + j], &gw = a.geo[geo_of(j)];
+            if (w.nb != gw.nb || w.nbp != gw.nbp) {
+                m->err = "every layer's matrices must share the first layer's column counts";
+                return 1;
+            }
+        }
+    std::vector<uint64_t> wp(14 * (size_t)c.n_layer);
+    for (int li = 0; li < c.n_layer; ++li)
+        for (int j = 0; j < 7; ++j) {
+            wp[14 * li + 2 * j] = (uint64_t)(uintptr_t)f[7 * li + j].fq;
+            wp[14 * li + 2 * j + 1] = (uint64_t)(uintptr_t)f[7 * li + j].fs;
+        }
+    GD_HIP(hipMalloc((void**)&m->wptr, wp.size() * 8));
+    GD_HIP(hipMemcpy(m->wptr, wp.data(), wp.size() * 8, hipMemcpyHostToDevice));
+    a.wptr = m->wptr;
+    a.norms = m->norms;
+    a.ns = ns;
+    a.kc = m->kc;
+    a.vc = m->vc;
+    a.kv_layer = (size_t)c.n_ctx * KVD;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.n_ctx = c.n_ctx;
+    a.window = c.window;
+    a.swa_period = c.swa_period;
+    // Copy counts per loader wave: the most chunks any workgroup copies.
+    int kmax[5] = {0, 0, 0, 0, 0};
+    for (int li = 0; li < c.n_layer; ++li)
+        for (int mw = 0; mw < a.M; ++mw)
+            for (int ph : {0, 2, 3, 4}) {
+                const int ch = phase_chunks(a, f.data() + 7 * li, ph, mw);
+                kmax[ph] = std::max(kmax[ph], (ch + PK_LOADERS - 1) / PK_LOADERS);
+            }
+    g.kq = kmax[0], g.ko = kmax[2], g.kf = kmax[3], g.kd = kmax[4];
+    if (g.kq + g.ko + g.kf + g.kd > 63) {
+        m->err = "the device step's weight copies exceed the load counter";
+        return 1;
+    }
+    // Tagged hand-off buffers, zero (tag 0 is never current).
+    const size_t nt = (size_t)(QD + 2 * KVD) + QD + E + F + E;
+    GD_HIP(hipMalloc((void**)&m->tagged, nt * 8));
+    GD_HIP(hipMemset(m->tagged, 0, nt * 8));
+    a.t_qkv = m->tagged;
+    a.t_attn = a.t_qkv + QD + 2 * KVD;
+    a.t_o = a.t_attn + QD;
+    a.t_h = a.t_o + E;
+    a.t_down = a.t_h + F;
+    // glibc_expf's table.
+    uint64_t T[32];
+    expf_table(T);
+    GD_HIP(hipMalloc((void**)&m->expt, sizeof T));
+    GD_HIP(hipMemcpy(m->expt, T, sizeof T, hipMemcpyHostToDevice));
+    m->n_gen_max = n_gen_max;
+    GD_HIP(hipMalloc((void**)&m->y, (size_t)E * 4));
     GD_HIP(hipMalloc((void**)&m->logits, (size_t)c.n_vocab * 4));
-    GD_HIP(hipMalloc((void**)&m->record, (size_t)n_gen_max * c.n_layer * E * 4));
+    GD_HIP(hipMalloc((void**)&m->record, (size_t)std::max(n_gen_max, 1) * c.n_layer * E * 4));
     GD_HIP(hipMalloc(&m->work, nnh_model_argmax_work_bytes(m->w.back())));
     GD_HIP(hipMalloc((void**)&m->tok, 8));
     GD_HIP(hipMalloc((void**)&m->pos, 4));
     GD_HIP(hipMalloc((void**)&m->step, 4));
-    GD_HIP(hipMalloc((void**)&m->tokens, (size_t)n_gen_max * 4));
+    GD_HIP(hipMalloc((void**)&m->seq, 4));
+    GD_HIP(hipMalloc((void**)&m->errf, 4));
+    GD_HIP(hipMemset(m->seq, 0, 4));
+    GD_HIP(hipMemset(m->errf, 0, 4));
+    GD_HIP(hipMalloc((void**)&m->tokens, (size_t)std::max(n_gen_max, 1) * 4));
+    const uint8_t* te = (const uint8_t*)nnh_weight_device_data(m->w.back());
+    a.tok = m->tok;
+    a.tq = (const int8_t*)te;
+    a.ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
+    a.out_norm = m->norms + ns * c.n_layer;
+    a.pos_p = m->pos;
+    a.step_p = m->step;
+    a.seq_p = m->seq;
+    a.record = m->record;
+    a.y = m->y;
+    a.rec_stride = (size_t)c.n_layer * E;
+    a.expt = m->expt;
+    a.err = m->errf;
+    m->grid = a.A + a.M;
+    GD_HIP(hipMalloc((void**)&m->args_dev, sizeof(PkArgs)));
+    GD_HIP(hipMemcpy(m->args_dev, &a, sizeof(PkArgs), hipMemcpyHostToDevice));
+    // Gemma-3-1B's shapes have an instance of their own (its row loops unroll).
+    if (hd == 256 && E == 1152 && QD == 1024 && F == 6912)
+        m->kernel = (const void*)step_kernel<256, 36, 32, 216>;
+    else
+        m->kernel = hd == 256 ? (const void*)step_kernel<256, 0, 0, 0> : (const void*)step_kernel<128, 0, 0, 0>;
+    // Every workgroup must be resident at once.
+    int per_cu = 0;
+    GD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, m->kernel, PK_NT, 0));
+    if (per_cu < 1) {
+        m->err = "the device step kernel does not fit a CU";
+        return 1;
+    }
     return 0;
 }
 
 // Queue one decode step on m->st (eagerly, or into a graph being captured).
 static int queue_step(nngd_model* m) {
-    const nng_config& c = m->c;
-    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, F = c.n_ff, ngp = (E / 32 + 7) / 8;
-    const size_t ns = norm_stride(c), rs = (size_t)c.n_layer * E;
-    hipStream_t st = m->st;
-    const uint8_t* te = (const uint8_t*)nnh_weight_device_data(m->w.back());
-    const float eps = c.rms_eps;
-    for (int li = 0; li < c.n_layer; ++li) {
-        const float* nr = m->norms + ns * li;
-        const float *attn_norm = nr, *q_norm = nr + E, *k_norm = nr + E + hd, *post_attn = nr + E + 2 * hd,
-                    *ffn_norm = nr + 2 * E + 2 * hd;
-        const bool sliding = c.swa_period > 0 && (li + 1) % c.swa_period != 0;  // load.rs:1156-1160
-        const size_t half = hd / 2, tab = sliding ? 0 : (size_t)c.n_ctx * half;
-        const F32Mat* f = m->f.data() + 7 * li;
-        nnh_weight* const* w = m->w.data() + 7 * li;
-        const size_t kvd = (size_t)KV * hd, cache = (size_t)li * c.n_ctx * kvd;
-        // The previous layer's post-FFW residual (or the embedding), attention's norm, q / k / v.
-        QkvArgs qa{};
-        int wgs = 0;
-        float* outs[3] = {m->q, m->k, m->v};
-        for (int j = 0; j < 3; ++j) {
-            qa.m[j] = f[j];
-            qa.y[j] = outs[j];
-            qa.wg[j] = (f[j].rows + QKV_NT / 16 - 1) / (QKV_NT / 16);
-            wgs += qa.wg[j];
-        }
-        qa.norm = attn_norm;
-        qa.x_out = m->xa;
-        qa.E = E;
-        qa.eps = eps;
-        if (li == 0) {
-            qa.tok = m->tok;
-            qa.tq = (const int8_t*)te;
-            qa.ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
-            qa.embd_scale = std::sqrt((float)E);
-            launch_qkv<true>(qa, ngp, wgs, st);
-        } else {
-            qa.o = m->o;
-            qa.x_in = m->xb;
-            qa.post = m->norms + ns * (li - 1) + 3 * E + 2 * hd;
-            qa.rec = m->record + (size_t)(li - 1) * E;
-            qa.step_p = m->step;
-            qa.rec_stride = rs;
-            launch_qkv<false>(qa, ngp, wgs, st);
-        }
-        AttnArgs aa{m->q,  m->k,         m->v,         q_norm, k_norm, m->cos_t + tab, m->sin_t + tab, m->pos,
-                    m->kc + cache, m->vc + cache, H / KV, KV, sliding ? c.window : 0, c.attn_scale, eps, m->attn};
-        if (hd == 256)
-            attn_kernel<256><<<H * ATTN_SPLIT, ATTN_NT, 0, st>>>(aa);
-        else
-            attn_kernel<128><<<H * ATTN_SPLIT, ATTN_NT, 0, st>>>(aa);
-        if (nnh_gemv_batch_dev(w[3], m->attn, H * hd, m->o, E, 1, NNH_ACT_F32, st)) {
-            m->err = std::string("gemv: ") + nnh_last_error();
-            return 1;
-        }
-        FfnArgs fa{f[4], f[5], m->h, F, m->o, m->xa, post_attn, ffn_norm, m->xb, E, eps};
-        launch_ffn(fa, ngp, (F + FFN_NT / 32 - 1) / (FFN_NT / 32), st);
-        if (nnh_gemv_batch_dev(w[6], m->h, F, m->o, E, 1, NNH_ACT_F32, st)) {
-            m->err = std::string("gemv: ") + nnh_last_error();
-            return 1;
-        }
-    }
-    // The last residual and y = RMSNorm(x, output_norm); the greedy token is the lm_head argmax of y.
-    FinalArgs fin{m->o,    m->xb,   m->norms + ns * (c.n_layer - 1) + 3 * E + 2 * hd, m->norms + ns * c.n_layer,
-                  m->xa,   m->y,    m->record + (size_t)(c.n_layer - 1) * E,          m->step,
-                  rs,      E,       eps};
-    final_kernel<<<1, WG, 0, st>>>(fin);
-    if (nnh_model_argmax_dev(m->w.back(), m->y, m->logits, m->work, m->tok, st)) {
+    void* args[] = {&m->args_dev};
+    GD_HIP(hipLaunchCooperativeKernel(m->kernel, dim3(m->grid), dim3(PK_NT), args, 0, m->st));
+    if (nnh_model_argmax_dev(m->w.back(), m->y, m->logits, m->work, m->tok, m->st)) {
         m->err = std::string("lm_head: ") + nnh_last_error();
         return 1;
     }
-    step_end_kernel<<<1, 1, 0, st>>>(m->tok, m->tokens, m->pos, m->step);
+    step_end_kernel<<<1, 1, 0, m->st>>>(m->tok, m->tokens, m->pos, m->step, m->seq);
     GD_HIP(hipGetLastError());
     return 0;
 }
@@ -947,8 +1437,11 @@ int nngd_decode(nngd_model* m, nng_model* cpu, int32_t first_token, int n_gen, i
         m->err = "context full";
         return 1;
     }
-    const size_t cache = (size_t)c.n_layer * c.n_ctx * c.n_kv * c.head_dim * 2;
-    GD_HIP(hipMemcpy(m->kc, kc, cache, hipMemcpyHostToDevice));
+    const size_t rows = (size_t)c.n_layer * c.n_ctx * c.n_kv, cache = rows * c.head_dim * 2;
+    GD_HIP(hipMemcpy(m->kstage, kc, cache, hipMemcpyHostToDevice));
+    kperm_kernel<<<(unsigned)((rows * c.head_dim + 255) / 256), 256, 0, m->st>>>(m->kstage, m->kc, rows, c.head_dim);
+    GD_HIP(hipGetLastError());
+    GD_HIP(hipStreamSynchronize(m->st));
     GD_HIP(hipMemcpy(m->vc, vc, cache, hipMemcpyHostToDevice));
     const uint64_t tok = (uint64_t)first_token;
     const int p = (int)pos, zero = 0;
@@ -979,6 +1472,12 @@ int nngd_decode(nngd_model* m, nng_model* cpu, int32_t first_token, int n_gen, i
     }
     auto t1 = std::chrono::steady_clock::now();
     if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+    int ef = 0;
+    GD_HIP(hipMemcpy(&ef, m->errf, 4, hipMemcpyDeviceToHost));
+    if (ef) {
+        m->err = "the device step's hand-off waits ran out";
+        return 1;
+    }
     if (steps > 0) {
         GD_HIP(hipMemcpy(out_tokens + 1, m->tokens, (size_t)steps * 4, hipMemcpyDeviceToHost));
         if (record)

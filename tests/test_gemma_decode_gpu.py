@@ -79,8 +79,8 @@ def cpu_run(oracle, model):
     return prompt, tc, hc
 
 
-def check_same(model, tg, hg, tc, hc):
-    assert len(hg) == len(hc) == (2 + N_GEN - 1) * model.cfg.n_layer
+def check_same(model, tg, hg, tc, hc, n_fwd=2 + N_GEN - 1):
+    assert len(hg) == len(hc) == n_fwd * model.cfg.n_layer
     assert np.array_equal(tg, tc), np.nonzero(tg != tc)[0][:5]
     assert np.array_equal(hg, hc), np.nonzero(hg != hc)[0][:5]
     # Random weights settle greedy decoding on few tokens, but every step's
@@ -113,3 +113,31 @@ def test_gemma3_1b_device_decode_token_identical(model, cpu_run):
     print(f"device (graph reused): decode {tdg2:.3f}s ({(N_GEN - 1) / tdg2:.1f} tok/s)", flush=True)
     check_same(model, tg2, hg2, tc, hc)
     sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def long_model():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import nncpu_amd as N
+    from nncpu_amd.gemma import Gemma3, gemma3_1b_gguf
+    N.init(0)
+    return Gemma3.from_gguf(gemma3_1b_gguf(), n_ctx=768)
+
+
+def test_device_decode_past_one_block_and_the_window(oracle, long_model):
+    # A 500-token prompt, then 40 tokens: positions 500..539. Every layer
+    # attends over two or three 256-key blocks, merged as attn_merge does
+    # (kernels/mod.rs:765-800, forward.rs:387-414), and from position 512 on
+    # the sliding layers' 512-key window starts past key 0, so their first
+    # block is partial (model/embed.rs:14-30).
+    from nncpu_amd.gemma import random_prompt
+    n_prompt, n_gen = 500, 40
+    prompt = random_prompt(n_prompt, long_model.cfg.n_vocab, seed=0x1B0C)
+    print("cpu decode, long context", flush=True)
+    tc, hc, _, _ = cpu_generate(oracle, long_model, prompt, n_gen)
+    print("device decode, long context", flush=True)
+    tg, hg, _, tdg = long_model.generate_device(prompt, n_gen)
+    print(f"device: {(n_gen - 1) / tdg:.1f} tok/s at positions {n_prompt}..{n_prompt + n_gen - 1}", flush=True)
+    check_same(long_model, tg, hg, tc, hc, n_fwd=(n_prompt + 15) // 16 + n_gen - 1)

@@ -266,3 +266,28 @@ def test_attn_block_softmax_known_values(ops, oracle):
         else:
             assert np.all(np.abs(got - want) <= 2e-6 * want + 1e-12), np.max(np.abs(got - want) / want)
         assert np.all(out[n:] == 0.0)
+
+
+def test_merge_expf_restatement_is_glibc_expf(ops):
+    # attn_merge scales the block partials by std::exp of a float (scalar.rs:
+    # 521-537, the platform's expf). The device step restates glibc's expf
+    # (glibc_expf in gemma3_gpu.hip); every one of the 2^32 float inputs
+    # gives the same bits as the harness's own std::exp.
+    from concurrent.futures import ThreadPoolExecutor
+    L = ops
+    L.nng_op_libm_expf.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    L.nngd_expf_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    chunk = 1 << 24
+
+    def run(c):
+        x = (np.arange(chunk, dtype=np.uint64) + c * chunk).astype(np.uint32).view(np.float32)
+        a = np.empty_like(x)
+        b = np.empty_like(x)
+        L.nng_op_libm_expf(x.ctypes.data, a.ctypes.data, chunk)
+        L.nngd_expf_batch(x.ctypes.data, b.ctypes.data, chunk)
+        same = (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+        return int(chunk - np.count_nonzero(same))
+
+    with ThreadPoolExecutor(8) as pool:
+        bad = sum(pool.map(run, range((1 << 32) // chunk)))
+    assert bad == 0
