@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
 // loop has no tail (nb is a multiple of LPR*BPL, checked by the launcher),
 // Q4 scale and bias come as one packed 32-bit word per block (`sb`,
 // scale | bias << 16, built at upload), and the lane sum uses DPP.
-template <int DT, int M, int R, int LPR, int BPL>
+template <int DT, int M, int R, int LPR, int BPL, bool PF>
 __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restrict__ qs,
                                                          const uint16_t* __restrict__ sc,
                                                          const uint32_t* __restrict__ sb,
@@ -231,11 +231,15 @@ __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restri
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0;
 
-    for (int c0 = 0; c0 < nb; c0 += LPR * BPL) {
+    // One chunk's operands; with PF (rows of several chunks per lane) the
+    // next chunk's loads are issued before the current chunk's arithmetic.
+    struct Chunk {
         int4 w[R][BPL][QV];
         uint32_t s[R][BPL];
         int4 x0[M][BPL], x1[M][BPL];
         double2 sx[M][BPL];
+    };
+    auto load = [&](Chunk& k, int c0) {
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             const size_t b = c0 + lane + i * LPR;
@@ -243,32 +247,90 @@ __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restri
             for (int r = 0; r < R; ++r) {
                 const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + (DT == 1 ? 32 : 16) * b);
 #pragma unroll
-                for (int v = 0; v < QV; ++v) w[r][i][v] = load_nt16(wp + v);
-                s[r][i] = DT == 1 ? (uint32_t)sc[(size_t)rr[r] * nb + b] : sb[(size_t)rr[r] * nb + b];
+                for (int v = 0; v < QV; ++v) k.w[r][i][v] = load_nt16(wp + v);
+                k.s[r][i] = DT == 1 ? (uint32_t)sc[(size_t)rr[r] * nb + b] : sb[(size_t)rr[r] * nb + b];
             }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * b);
-                x0[m][i] = xp[0];
-                x1[m][i] = xp[1];
-                sx[m][i] = ((const double2*)asx)[(size_t)m * nb + b];
+                k.x0[m][i] = xp[0];
+                k.x1[m][i] = xp[1];
+                k.sx[m][i] = ((const double2*)asx)[(size_t)m * nb + b];
             }
         }
+    };
+    auto run = [&](const Chunk& k) {
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const double sw = (double)bf16f(s[r][i] & 0xffffu);
+                const double sw = (double)bf16f(k.s[r][i] & 0xffffu);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const int P = DT == 1 ? dot_q8(w[r][i][0], w[r][i][QV - 1], x0[m][i], x1[m][i])
-                                          : dot_q4(w[r][i][0], x0[m][i], x1[m][i]);
-                    acc[r][m] = __builtin_fma(sw * sx[m][i].x, (double)P, acc[r][m]);
+                    const int P = DT == 1 ? dot_q8(k.w[r][i][0], k.w[r][i][QV - 1], k.x0[m][i], k.x1[m][i])
+                                          : dot_q4(k.w[r][i][0], k.x0[m][i], k.x1[m][i]);
+                    acc[r][m] = __builtin_fma(sw * k.sx[m][i].x, (double)P, acc[r][m]);
                 }
                 if (DT == 2) {
-                    const double bw = (double)bf16f(s[r][i] >> 16);
+                    const double bw = (double)bf16f(k.s[r][i] >> 16);
 #pragma unroll
-                    for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sx[m][i].y, acc[r][m]);
+                    for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, k.sx[m][i].y, acc[r][m]);
+                }
+            }
+        }
+    };
+    constexpr int STEP = LPR * BPL;
+    if (PF) {
+        Chunk A, B;
+        load(A, 0);
+        int c0 = 0;
+        for (; c0 + STEP < nb; c0 += 2 * STEP) {
+            load(B, c0 + STEP);
+            run(A);
+            if (c0 + 2 * STEP < nb) load(A, c0 + 2 * STEP);
+            run(B);
+        }
+        if (c0 < nb) run(A);
+    } else {
+        for (int c0 = 0; c0 < nb; c0 += STEP) {
+            int4 w[R][BPL][QV];
+            uint32_t s[R][BPL];
+            int4 x0[M][BPL], x1[M][BPL];
+            double2 sx[M][BPL];
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+                const size_t b = c0 + lane + i * LPR;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + (DT == 1 ? 32 : 16) * b);
+#pragma unroll
+                    for (int v = 0; v < QV; ++v) w[r][i][v] = load_nt16(wp + v);
+                    s[r][i] = DT == 1 ? (uint32_t)sc[(size_t)rr[r] * nb + b] : sb[(size_t)rr[r] * nb + b];
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const int4* xp = (const int4*)(aq + (size_t)m * cols + 32 * b);
+                    x0[m][i] = xp[0];
+                    x1[m][i] = xp[1];
+                    sx[m][i] = ((const double2*)asx)[(size_t)m * nb + b];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const double sw = (double)bf16f(s[r][i] & 0xffffu);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const int P = DT == 1 ? dot_q8(w[r][i][0], w[r][i][QV - 1], x0[m][i], x1[m][i])
+                                              : dot_q4(w[r][i][0], x0[m][i], x1[m][i]);
+                        acc[r][m] = __builtin_fma(sw * sx[m][i].x, (double)P, acc[r][m]);
+                    }
+                    if (DT == 2) {
+                        const double bw = (double)bf16f(s[r][i] >> 16);
+#pragma unroll
+                        for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fma(bw, sx[m][i].y, acc[r][m]);
+                    }
                 }
             }
         }
@@ -352,8 +414,12 @@ template <int DT, int M, int R, int LPR, int BPL>
 void launch_v2(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
                int rows, int nb, float* y, size_t ys, hipStream_t st) {
     constexpr int rows_per_wg = 4 * (64 / LPR) * R;
-    gemv_i8_v2_kernel<DT, M, R, LPR, BPL>
-        <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
+    if (nb > LPR * BPL)
+        gemv_i8_v2_kernel<DT, M, R, LPR, BPL, true>
+            <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
+    else
+        gemv_i8_v2_kernel<DT, M, R, LPR, BPL, false>
+            <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
 }
 
 // Launch shape from the measured sweep (Llama-3-8B and vocab shapes): 64
