@@ -594,28 +594,36 @@ def cpu_baseline(O, sweep):
 def gemma_decode(args, N, cpu: bool):
     """Gemma-3-1B-shaped greedy decode of 128 tokens from a
     32-token prompt, on the device-resident step, the model loaded from the
-    seeded random-init GGUF (nncpu_amd.gguf) and re-encoded to Q8_0.
-    tok/s counts the 127 decode forwards after the prompt; the timed run is
-    the second one (the first captures the step's graph). With `cpu`, the CPU
-    baseline leg: the same decode with nncpu's CPU gemv (the oracle's AVX2
-    restatement, 8 threads) in the shared C++ forward, timed, and its tokens
-    compared with the device run's."""
-    import ctypes as C
-    from nncpu_amd.gemma import Gemma3, gemma3_1b_gguf, random_prompt
+    seeded random-init GGUF (nncpu_amd.gguf) and re-encoded to Q8_0 (and, in
+    `q4`, to nncpu's Q4). tok/s counts the 127 decode forwards after the
+    prompt; the timed run is the second one (the first captures the step's
+    graph). With `cpu`, the CPU baseline leg: the same decode with nncpu's CPU
+    gemv (the oracle's AVX2 restatement, 8 threads) in the shared C++
+    forward, timed, and its tokens compared with the device run's."""
+    from nncpu_amd.gemma import gemma3_1b_gguf
     t0 = time.perf_counter()
     path = gemma3_1b_gguf()
+    log(f"gemma3-1b GGUF written in {time.perf_counter() - t0:.1f}s")
+    out = decode_leg(N, path, N.Q8_0, cpu)
+    out["q4"] = decode_leg(N, path, N.Q4S, cpu)
+    return out
+
+
+def decode_leg(N, path, dtype, cpu: bool):
+    import ctypes as C
+    from nncpu_amd.gemma import Gemma3, random_prompt
+    fmt = "Q8_0" if dtype == N.Q8_0 else "Q4"
     t1 = time.perf_counter()
-    m = Gemma3.from_gguf(path, n_ctx=256)
-    log(f"gemma3-1b GGUF written in {t1 - t0:.1f}s, loaded (device decode + Q8_0 re-encode) in "
-        f"{time.perf_counter() - t1:.1f}s")
+    m = Gemma3.from_gguf(path, n_ctx=256, dtype=dtype)
+    log(f"gemma3-1b loaded (device decode + {fmt} re-encode) in {time.perf_counter() - t1:.1f}s")
     prompt, n_gen = random_prompt(32, m.cfg.n_vocab), 128
     m.generate_device(prompt, n_gen)
     tg, hg, tp, td = m.generate_device(prompt, n_gen)
     out = dict(config="gemma-3-1b architecture, random-init GGUF from seed (BF16 matrices 0.02*N(0,1) from the "
-                      "reference's test generator) re-encoded to Q8_0 on load, 32-token prompt, 128 greedy tokens",
+                      f"reference's test generator) re-encoded to {fmt} on load, 32-token prompt, 128 greedy tokens",
                tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
                prefill_s=round(tp, 4), kernels_per_token=4)
-    log(f"gemma3-1b device decode: {out['tok_s']} tok/s")
+    log(f"gemma3-1b device decode ({fmt}): {out['tok_s']} tok/s")
     if cpu:
         from oracle import oracle as O  # the CPU baseline leg only
 
@@ -626,7 +634,7 @@ def gemma_decode(args, N, cpu: bool):
         arr = (C.c_void_p * len(bufs))(*[b.ctypes.data for b in bufs])
         rows = (C.c_size_t * len(bufs))(*[r for r, _ in m.shapes])
         cols = (C.c_size_t * len(bufs))(*[c for _, c in m.shapes])
-        table = Table(n=len(bufs), dtype=1, bufs=C.cast(arr, C.POINTER(C.c_void_p)),
+        table = Table(n=len(bufs), dtype=dtype, bufs=C.cast(arr, C.POINTER(C.c_void_p)),
                       rows=C.cast(rows, C.POINTER(C.c_size_t)), cols=C.cast(cols, C.POINTER(C.c_size_t)))
         threads = 8
         O.avx_set_threads(threads)
@@ -637,7 +645,7 @@ def gemma_decode(args, N, cpu: bool):
                                           "C++ forward",
                                    tokens_identical=bool(np.array_equal(tg, tc)),
                                    layer_states_identical=bool(np.array_equal(hg, hc)))
-        log(f"gemma3-1b cpu decode: {out['cpu_baseline']}")
+        log(f"gemma3-1b cpu decode ({fmt}): {out['cpu_baseline']}")
     m.free()
     return out
 

@@ -2,8 +2,8 @@
 
 A Gemma-3-architecture model loaded from a GGUF file (nncpu_amd.gguf writes
 the seeded random-init one: matrices 0.02*N(0,1) as BF16, norms
-1 + 0.1*N(0,1)), every matrix decoded and re-encoded to nncpu's Q8_0 layout
-on the device (nncpu's load-time decode and encoder, bit for bit). The
+1 + 0.1*N(0,1)), every matrix decoded and re-encoded to nncpu's Q8_0 (or Q4)
+layout on the device (nncpu's load-time decode and encoder, bit for bit). The
 forward pass is nncpu's
 (nncpu_amd/host/gemma3.cpp, restating crates/nncpu/src/model/forward.rs) on
 the CPU; its weight matmuls run through `nnh_gemv_batch` in the bit-exact
@@ -32,7 +32,7 @@ class NngConfig(C.Structure):
     _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int), ("n_kv", C.c_int),
                 ("head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
                 ("rms_eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
-                ("attn_scale", C.c_float), ("window", C.c_int), ("swa_period", C.c_int)]
+                ("attn_scale", C.c_float), ("window", C.c_int), ("swa_period", C.c_int), ("wtype", C.c_int)]
 
 
 class NngGpuCtx(C.Structure):
@@ -45,7 +45,7 @@ def gemma3_1b_config(n_ctx: int = 256, n_layer: int = 26, n_vocab: int = 262144)
     layer global, RoPE bases 1e6 / 1e4, attention scale 1/16)."""
     return NngConfig(n_layer=n_layer, n_embd=1152, n_head=4, n_kv=1, head_dim=256, n_ff=6912, n_vocab=n_vocab,
                      n_ctx=n_ctx, rms_eps=1e-6, rope_base=1e6, rope_base_swa=1e4, attn_scale=1.0 / 16.0,
-                     window=512, swa_period=6)
+                     window=512, swa_period=6, wtype=Q8_0)
 
 
 def matrix_shapes(cfg: NngConfig) -> list[tuple[int, int]]:
@@ -81,8 +81,8 @@ def _gemma_lib():
 
 
 class Gemma3:
-    """Device weights of a Gemma-3 model (nncpu's Q8_0 layout), plus the
-    host copies (norms, the Q8_0 embedding table) the CPU forward reads."""
+    """Device weights of a Gemma-3 model (nncpu's Q8_0 or Q4 layout), plus
+    the host copies (norms, the embedding table) the CPU forward reads."""
 
     def __init__(self, cfg: NngConfig, weights: list[Weight], norms: np.ndarray):
         self.cfg = cfg
@@ -113,7 +113,7 @@ class Gemma3:
                         n_ctx=n_ctx, rms_eps=float(kv.get(a + "attention.layer_norm_rms_epsilon", 1e-6)),
                         rope_base=float(kv.get(a + "rope.freq_base", 10000.0)), rope_base_swa=10000.0,
                         attn_scale=float(kv.get(a + "attention.scale", 1.0 / hd ** 0.5)),
-                        window=int(kv.get(a + "attention.sliding_window", 0)), swa_period=6)
+                        window=int(kv.get(a + "attention.sliding_window", 0)), swa_period=6, wtype=dtype)
 
         def mat(name):
             t = f.tensors[name]

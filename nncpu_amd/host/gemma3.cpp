@@ -228,7 +228,7 @@ typedef int (*nng_argmax_fn)(void* ctx, const float* x, size_t* row);
 struct nng_model {
     nng_config c;
     std::vector<float> norms;          // per layer: attn, q, k, post_attn, ffn, post_ffw; then output
-    std::vector<uint8_t> token_embd;   // Q8_0 split layout [n_vocab x n_embd] (the embedding table)
+    std::vector<uint8_t> token_embd;   // Q8_0 or Q4 split layout [n_vocab x n_embd] (the embedding table)
     nng_gemv_fn gemv;
     nng_argmax_fn argmax;
     void* ctx;
@@ -243,7 +243,8 @@ struct nng_model {
 static size_t norm_stride(const nng_config& c) { return 4 * (size_t)c.n_embd + 2 * (size_t)c.head_dim; }
 
 // norms: per layer [attn n_embd][q_norm hd][k_norm hd][post_attn n_embd][ffn n_embd][post_ffw n_embd],
-// then output_norm [n_embd]. token_embd: the Q8_0 split layout of the embedding / lm_head table.
+// then output_norm [n_embd]. token_embd: the split layout of the embedding / lm_head table (Q4 when
+// cfg->wtype is 2, else Q8_0).
 nng_model* nng_create(const nng_config* cfg, const float* norms, const void* token_embd, nng_gemv_fn gemv,
                       nng_argmax_fn argmax, void* ctx) {
     nng_model* m = new nng_model();
@@ -252,7 +253,8 @@ nng_model* nng_create(const nng_config* cfg, const float* norms, const void* tok
     size_t nn = norm_stride(c) * c.n_layer + c.n_embd;
     m->norms.assign(norms, norms + nn);
     size_t te = (size_t)c.n_vocab * c.n_embd;
-    m->token_embd.assign((const uint8_t*)token_embd, (const uint8_t*)token_embd + te + te / 16);
+    const size_t tbytes = c.wtype == 2 ? te / 2 + te / 8 : te + te / 16;
+    m->token_embd.assign((const uint8_t*)token_embd, (const uint8_t*)token_embd + tbytes);
     m->gemv = gemv;
     m->argmax = argmax;
     m->ctx = ctx;
@@ -278,6 +280,34 @@ void nng_fnv_many(const float* v, size_t n, size_t count, uint64_t* out) {
     for (size_t i = 0; i < count; ++i) out[i] = fnv(v + i * n, n);
 }
 
+// Row `tok` of a split-layout embedding table times `scale` into y[0..E)
+// (model/mod.rs:447-460): Q8_0 f32(q) * (s * scale) (kernels/mod.rs:917-930);
+// Q4 (wtype 2) (s * scale) * q + bias * scale, unfused, byte k of a block
+// holding elements k (low nibble) and k + 16 (kernels/mod.rs:934-954).
+static void embed_row(int wtype, const uint8_t* table, size_t n_vocab, size_t E, size_t tok, float scale, float* y) {
+    const size_t te = n_vocab * E, nbe = E / 32;
+    if (wtype == 2) {
+        const uint8_t* tq = table + tok * (E / 2);
+        const uint16_t* ts = (const uint16_t*)(table + te / 2) + tok * nbe;
+        const uint16_t* tb = (const uint16_t*)(table + te / 2 + te / 16) + tok * nbe;
+        for (size_t b = 0; b < nbe; ++b) {
+            const float s = bf16f(ts[b]) * scale, bias = bf16f(tb[b]) * scale;
+            for (int k = 0; k < 16; ++k) {
+                const uint8_t q = tq[16 * b + k];
+                y[32 * b + k] = s * (float)(q & 15) + bias;
+                y[32 * b + k + 16] = s * (float)(q >> 4) + bias;
+            }
+        }
+    } else {
+        const int8_t* tq = (const int8_t*)table + tok * E;
+        const uint16_t* ts = (const uint16_t*)(table + te) + tok * nbe;
+        for (size_t b = 0; b < nbe; ++b) {
+            const float vs = bf16f(ts[b]) * scale;
+            for (int i = 0; i < 32; ++i) y[32 * b + i] = (float)tq[32 * b + i] * vs;
+        }
+    }
+}
+
 // model_forward (forward.rs:848-965) for n_tok tokens at cur_pos.
 int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
     const nng_config& c = m->c;
@@ -300,20 +330,15 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
     m->part.assign(group * pw, 0.0f);
     m->acc.assign(group * pw, 0.0f);
 
-    // Embedding rows times sqrt(n_embd) (kernels/mod.rs:917-929, load.rs:565-566).
+    // Embedding rows times sqrt(n_embd) (load.rs:565-566).
     const float embd_scale = std::sqrt((float)E);
-    const int8_t* tq = (const int8_t*)m->token_embd.data();
-    const uint16_t* ts = (const uint16_t*)(m->token_embd.data() + (size_t)c.n_vocab * E);
     for (size_t t = 0; t < n_tok; ++t) {
         if (tokens[t] < 0 || tokens[t] >= c.n_vocab) {
             m->err = "token outside the vocabulary";
             return 1;
         }
-        size_t tok = (size_t)tokens[t];
-        for (size_t b = 0; b < E / 32; ++b) {
-            float vs = bf16f(ts[tok * (E / 32) + b]) * embd_scale;
-            for (int i = 0; i < 32; ++i) m->x[t * E + 32 * b + i] = (float)tq[tok * E + 32 * b + i] * vs;
-        }
+        embed_row(c.wtype, m->token_embd.data(), (size_t)c.n_vocab, E, (size_t)tokens[t], embd_scale,
+                  m->x.data() + t * E);
     }
 
     const size_t ns = norm_stride(c);
@@ -489,6 +514,11 @@ int nng_gpu_argmax(void* ctx, const float* x, size_t* row) {
 // 938-992, 1133-1217, 1263).
 
 // std::exp of floats, as attn_merge takes it (the platform libm's expf).
+void nng_op_embed_row(int wtype, const void* table, size_t n_vocab, size_t n_embd, size_t token, float scale,
+                      float* y) {
+    embed_row(wtype, (const uint8_t*)table, n_vocab, n_embd, token, scale, y);
+}
+
 void nng_op_libm_expf(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; ++i) y[i] = std::exp(x[i]);
 }

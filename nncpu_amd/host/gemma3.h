@@ -12,6 +12,7 @@ struct nng_config {
     int n_layer, n_embd, n_head, n_kv, head_dim, n_ff, n_vocab, n_ctx;
     float rms_eps, rope_base, rope_base_swa, attn_scale;
     int window, swa_period;
+    int wtype;  // the matrices' format (the embedding table's too): 2 = Q4, else Q8_0
 };
 
 struct nng_model;

@@ -37,12 +37,16 @@
 // wait too, so every wave exits.
 //
 // Weights: a matmul workgroup's rows of each matrix (the 16-lane quant
-// layout of the library's f32 path and the BF16 scale rows) are copied into
-// LDS by direct global->LDS loads one layer ahead: layer l + 1's q / k / v
-// rows as soon as layer l's are consumed, and so on, so a phase finds its
-// weights in LDS. Waves 4-15 issue the copies and wait for them by count
-// (vector loads complete in order); waves 0-3 poll and never issue a copy,
-// so a poll never waits behind one.
+// layout of the library's Q8_0 f32 path, the BF16 scale rows and, for Q4,
+// the bias rows) are copied into LDS by direct global->LDS loads one layer
+// ahead: layer l + 1's q / k / v rows as soon as layer l's are consumed, and
+// so on, so a phase finds its weights in LDS. Waves 8-11 issue the copies
+// and wait for them by count (vector loads complete in order); waves 0-7
+// poll and compute and never issue a copy, so a poll never waits behind
+// one. Q4 matrices run as Q8_0 rows of their nibble values (q4_row's chains
+// are q8_row's with q = 0..15: the same products in the same order) plus the
+// bias term dot_bf16_f32(bias row, block_sums(x)) (scalar.rs:334-359,
+// 654-674, 708-740), the block sums formed once per phase.
 //
 // Attention: keys are cached chain-major per key (the 64 values score lane
 // u of 4 multiplies are contiguous), so the score lanes load them straight
@@ -335,16 +339,23 @@ struct Rows {
 // padded scale row.
 __host__ __device__ __forceinline__ uint32_t qrow_bytes(const F32Mat& m) { return (uint32_t)((m.nb + 7) / 8) * 256; }
 __host__ __device__ __forceinline__ uint32_t srow_bytes(const F32Mat& m) { return (uint32_t)m.nbp * 2; }
+// A Q4 bias row: nb BF16 values, zero-padded to whole 16-byte pieces (so a
+// copy's last piece never spills into the next run's slots).
+__host__ __device__ __forceinline__ uint32_t brow_elems(int nb) { return (uint32_t)((nb + 7) / 8) * 8; }
 
 // Rows [lo, hi) of m into LDS row slots slot0..: v(src, bytes, LDS offset)
-// for the quants, then for the scales.
+// for the quants, then the scales, then (Q4) the bias rows.
 template <class V>
 __host__ __device__ __forceinline__ void visit_rows(V&& v, const F32Mat& m, int lo, int hi, int slot0, uint32_t wdst,
-                                                    uint32_t sdst) {
+                                                    uint32_t sdst, uint32_t bdst) {
     if (hi <= lo) return;
     const uint32_t qb = qrow_bytes(m), sb = srow_bytes(m);
     v(m.fq + (size_t)lo * qb, (uint32_t)(hi - lo) * qb, wdst + (uint32_t)slot0 * qb);
     v((const uint8_t*)(m.fs + (size_t)lo * m.nbp), (uint32_t)(hi - lo) * sb, sdst + (uint32_t)slot0 * sb);
+    if (m.bi) {
+        const uint32_t bb = 2 * brow_elems(m.nb);
+        v((const uint8_t*)m.bi + (size_t)lo * bb, (uint32_t)(hi - lo) * bb, bdst + (uint32_t)slot0 * bb);
+    }
 }
 
 }  // namespace
@@ -352,7 +363,7 @@ __host__ __device__ __forceinline__ void visit_rows(V&& v, const F32Mat& m, int 
 // LDS byte offsets of a matmul workgroup, and the copy instructions each
 // loader wave issues per phase (the most any workgroup needs).
 struct PkGeom {
-    uint32_t qw, qs, ow, os, fw, fs, dw, ds, y, in, xt, res, bc, h, wtab, bytes;
+    uint32_t qw, qs, ow, os, fw, fs, dw, ds, qb, ob, fb, db, xs, y, in, xt, res, bc, h, wtab, bytes;
     int kq, ko, kf, kd;
 };
 
@@ -361,16 +372,18 @@ struct PkArgs {
     float eps, attn_scale, embd_scale;
     PkGeom g;
     F32Mat geo[4];              // geometry (no pointers) of q / k / v, o, gate / up, down
-    const uint64_t* wptr;       // [n_layer][7] x (quants, scales) of q k v o gate up down
+    const uint64_t* wptr;       // [n_layer][7] x (quants, scales, Q4 bias rows or 0) of q k v o gate up down
+    int q4;                     // the layer matrices are Q4 (bias rows, block sums)
     const float* norms;         // per layer, ns apart: attn, q, k, post_attn, ffn, post_ffw
     size_t ns;
     uint16_t *kc, *vc;          // caches [n_layer][n_ctx][n_kv * HD]: K chain-major per key, V natural
     size_t kv_layer;
     const float *cos_t, *sin_t; // RoPE tables [2][n_ctx][HD / 2]: sliding (local) base, then global
     int n_ctx, window, swa_period;
-    const uint64_t* tok;  // the token; the embedding table (the tied lm_head, Q8_0)
+    const uint64_t* tok;  // the token; the embedding table (the tied lm_head): quants, scales, Q4 biases
     const int8_t* tq;
     const uint16_t* ts;
+    const uint16_t* tb;   // null: Q8_0
     const float* out_norm;
     const int *pos_p, *step_p;
     const uint32_t* seq_p;  // steps run on this model so far: the tags' base
@@ -401,16 +414,16 @@ __host__ __device__ __forceinline__ void visit_phase(const PkArgs& a, Mat&& mat,
     const PkGeom& g = a.g;
     if (phase == 0) {
         const int r0 = rw.q0, r1 = rw.q1, kb = a.QD, vb = a.QD + a.KVD, ve = a.QD + 2 * a.KVD;
-        visit_rows(v, mat(0), r0, min(r1, kb), 0, g.qw, g.qs);
-        visit_rows(v, mat(1), max(r0, kb) - kb, min(r1, vb) - kb, max(r0, kb) - r0, g.qw, g.qs);
-        visit_rows(v, mat(2), max(r0, vb) - vb, min(r1, ve) - vb, max(r0, vb) - r0, g.qw, g.qs);
+        visit_rows(v, mat(0), r0, min(r1, kb), 0, g.qw, g.qs, g.qb);
+        visit_rows(v, mat(1), max(r0, kb) - kb, min(r1, vb) - kb, max(r0, kb) - r0, g.qw, g.qs, g.qb);
+        visit_rows(v, mat(2), max(r0, vb) - vb, min(r1, ve) - vb, max(r0, vb) - r0, g.qw, g.qs, g.qb);
     } else if (phase == 2) {
-        visit_rows(v, mat(3), rw.o0, rw.o1, 0, g.ow, g.os);
+        visit_rows(v, mat(3), rw.o0, rw.o1, 0, g.ow, g.os, g.ob);
     } else if (phase == 3) {
-        visit_rows(v, mat(4), rw.f0, rw.f1, 0, g.fw, g.fs);
-        visit_rows(v, mat(5), rw.f0, rw.f1, rw.f1 - rw.f0, g.fw, g.fs);
+        visit_rows(v, mat(4), rw.f0, rw.f1, 0, g.fw, g.fs, g.fb);
+        visit_rows(v, mat(5), rw.f0, rw.f1, rw.f1 - rw.f0, g.fw, g.fs, g.fb);
     } else {
-        visit_rows(v, mat(6), rw.d0, rw.d1, 0, g.dw, g.ds);
+        visit_rows(v, mat(6), rw.d0, rw.d1, 0, g.dw, g.ds, g.db);
     }
 }
 
@@ -446,11 +459,12 @@ __device__ __forceinline__ const void* lds_ptr(const uint64_t* p) {
 }
 struct LdsMats {
     const PkArgs* a;
-    const uint64_t* tab;  // this layer's 7 x (quants, scales) in LDS
+    const uint64_t* tab;  // this layer's 7 x (quants, scales, bias rows) in LDS
     __device__ __forceinline__ F32Mat operator()(int j) const {
         F32Mat m = a->geo[geo_of(j)];
-        m.fq = (const uint8_t*)lds_ptr(tab + 2 * j);
-        m.fs = (const uint16_t*)lds_ptr(tab + 2 * j + 1);
+        m.fq = (const uint8_t*)lds_ptr(tab + 3 * j);
+        m.fs = (const uint16_t*)lds_ptr(tab + 3 * j + 1);
+        m.bi = a->q4 ? (const uint16_t*)lds_ptr(tab + 3 * j + 2) : nullptr;
         return m;
     }
 };
@@ -576,6 +590,37 @@ __device__ float row32(const uint8_t* w, const uint16_t* s, const float* x, int 
     return __fadd_rn(q, xor_get(q, 2));
 }
 
+// The Q4 bias term dot_bf16_f32(bias row, xs) (scalar.rs:334-347): lane l
+// of an 8-lane group accumulates elements 8c + l (fused), hsum8 across the
+// group, then the tail in order (unfused). b: the row's biases, xs: the
+// block sums, both in LDS. Valid at l == 0.
+__device__ __forceinline__ float bias_dot(const uint16_t* b, const float* xs, int nb, int l) {
+    const int body = nb & ~7;
+    float acc = 0.0f;
+    for (int c = 0; c < body; c += 8) acc = __fmaf_rn(bf16f(b[c + l]), xs[c + l], acc);
+    float s = hsum8_lanes(acc);
+    for (int i = body; i < nb; ++i) s = __fadd_rn(s, __fmul_rn(bf16f(b[i]), xs[i]));
+    return s;
+}
+
+// block_sums (scalar.rs:355-359) of x (LDS) into xs, a thread per block.
+__device__ __forceinline__ void block_sums_lds(const float* x, int nb, float* xs, int tid) {
+    for (int b = tid; b < nb; b += PK_CW) {
+        const float4* c = (const float4*)(x + 32 * b);
+        float e[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 f = c[i];
+            e[4 * i] = f.x, e[4 * i + 1] = f.y, e[4 * i + 2] = f.z, e[4 * i + 3] = f.w;
+        }
+        float v[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) v[l] = __fadd_rn(__fadd_rn(__fadd_rn(e[l], e[8 + l]), e[16 + l]), e[24 + l]);
+        xs[b] = __fadd_rn(__fadd_rn(__fadd_rn(v[0], v[4]), __fadd_rn(v[1], v[5])),
+                          __fadd_rn(__fadd_rn(v[2], v[6]), __fadd_rn(v[3], v[7])));
+    }
+}
+
 // ---- matmul workgroups -----------------------------------------------------------------
 
 // The pollers' part of P0 / P3, among the poller waves only: x +=
@@ -630,25 +675,30 @@ __device__ bool residual_norms(const PkArgs& a, int tid, const float* in, float 
     return ok;
 }
 
-// A phase's rows (nrows of matrix geometry m, weights w / scales sc in LDS,
-// input x in LDS), NB: the rows' block count when known at compile time.
+// A phase's rows (nrows of matrix geometry m, weights w / scales sc / Q4
+// bias rows bi (null: Q8_0) in LDS, input x and its block sums xs in LDS),
+// NB: the rows' block count when known at compile time. A Q4 row is
+// q4_row's sum plus its bias term (gemv_q4_rows: y + bias).
 template <int NB>
-__device__ __forceinline__ void rows32(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const float* x, int nrows,
-                                       uint64_t* out, uint32_t tag, int tid) {
+__device__ __forceinline__ void rows32(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const uint16_t* bi,
+                                       const float* xs, const float* x, int nrows, uint64_t* out, uint32_t tag,
+                                       int tid) {
     const int nb = NB ? NB : m.nb;
     const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
     for (int slot = tid >> 5; slot < nrows; slot += PK_CW / 32) {
-        const float v = row32(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 31);
+        float v = row32(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 31);
+        if (bi) v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
         if ((tid & 31) == 0) tstore(out + slot, v, tag);
     }
 }
 template <int NB>
-__device__ __forceinline__ void rows16(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const float* x, int nrows,
-                                       float* res, int tid) {
+__device__ __forceinline__ void rows16(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const uint16_t* bi,
+                                       const float* xs, const float* x, int nrows, float* res, int tid) {
     const int nb = NB ? NB : m.nb;
     const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
     for (int slot = tid >> 4; slot < nrows; slot += PK_CW / 16) {
-        const float v = row16(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 15);
+        float v = row16(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 15);
+        if (bi) v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
         if ((tid & 15) == 0) res[slot] = v;
     }
 }
@@ -662,7 +712,7 @@ __device__ __forceinline__ void rows16(const F32Mat& m, const uint8_t* w, const 
 // (gate / up), 3 (down), with one copy of each piece of code (the step's
 // code stays small enough for the instruction cache). Waves 12-15 have no
 // work here. A last pass (mw 0 only) forms the final norm.
-template <int NBE, int NBQ, int NBF>
+template <int NBE, int NBQ, int NBF, bool Q4>
 __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_t base) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, mw = blockIdx.x - a.A;
     const bool poller = (int)threadIdx.x < PK_POLL;
@@ -678,6 +728,7 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
     int* LANDED = (int*)(BC + 8);  // [4] loader-wave copies landed of q / k / v, o, gate / up, down
     float* H = (float*)(lds + g.h);
     float* IN = (float*)(lds + g.in);
+    float* XS = (float*)(lds + g.xs);  // Q4: the block sums of the phase's input
     const int E = a.E, L = a.n_layer;
     const Rows rw = rows_of(a, mw);
     const int q0 = rw.q0, q1 = rw.q1, o0 = rw.o0, o1 = rw.o1, f0 = rw.f0, f1 = rw.f1, d0 = rw.d0, d1 = rw.d1;
@@ -686,14 +737,14 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
     // The layers' matrix pointers into LDS (scalar loads of a table read
     // once per layer would each wait a memory round trip).
     uint64_t* WT = (uint64_t*)(lds + g.wtab);
-    for (int i = threadIdx.x; i < 14 * L; i += PK_NT) WT[i] = a.wptr[i];
+    for (int i = threadIdx.x; i < 21 * L; i += PK_NT) WT[i] = a.wptr[i];
     lds_barrier();  // the last barrier of the whole workgroup
     if ((int)threadIdx.x >= PK_CW + 64 * PK_LOADERS) return;
     if ((int)threadIdx.x >= PK_CW) {
         // ---- loader waves
         const int lw = wave - PK_CW / 64;
         for (int l = 0; l < L; ++l) {
-            const LdsMats mats{&a, WT + 14 * l};
+            const LdsMats mats{&a, WT + 21 * l};
 #pragma unroll 1
             for (int q = 0; q < 4; ++q) {
                 // Region free: its previous layer's phase is done.
@@ -748,14 +799,23 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
                 }
             }
             if (it == 0) {
-                // The token's Q8_0 row times sqrt(n_embd) (kernels/mod.rs:917-929).
+                // The token's row times sqrt(n_embd) (kernels/mod.rs:917-954):
+                // Q8_0 q * s; Q4 s * q + bias (byte k of a block: elements k,
+                // low nibble, and k + 16).
                 const size_t t = (size_t)*a.tok;
 #pragma unroll
                 for (int k = 0; k < PK_KE; ++k) {
                     const int i = tid + PK_POLL * k;
                     if (i < E) {
                         const float vs = __fmul_rn(bf16f(a.ts[t * (E / 32) + i / 32]), a.embd_scale);
-                        xr[k] = __fmul_rn((float)a.tq[t * E + i], vs);
+                        if (Q4) {
+                            const int e = i & 31;
+                            const uint8_t byte = ((const uint8_t*)a.tq)[t * (E / 2) + 16 * (i >> 5) + (e & 15)];
+                            const float bs = __fmul_rn(bf16f(a.tb[t * (E / 32) + i / 32]), a.embd_scale);
+                            xr[k] = __fadd_rn(__fmul_rn(vs, (float)(e < 16 ? (byte & 15) : (byte >> 4))), bs);
+                        } else {
+                            xr[k] = __fmul_rn((float)a.tq[t * E + i], vs);
+                        }
                     }
                 }
             } else {
@@ -782,19 +842,28 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
             for (int i = tid; i < E; i += PK_CW) a.y[i] = Y[i];
             break;
         }
+        if (Q4) {
+            block_sums_lds(ph == 3 ? H : Y, (ph == 1 ? a.QD : ph == 3 ? a.F : E) / 32, XS, tid);
+            if (!pbar(PCTR, pgen)) *ABORT = 1;
+        }
         // ---- the rows: 32 lanes per row (one chain each) where there are
         // few rows, 16 lanes (two chains each) for gate / up; one call site
         // per matrix shape, so a known block count unrolls.
         {
             const int nrows = ph == 0 ? q1 - q0 : ph == 1 ? o1 - o0 : ph == 2 ? 2 * nf : d1 - d0;
+            const uint16_t* bi = Q4 ? (const uint16_t*)(lds + (ph == 0   ? g.qb
+                                                               : ph == 1 ? g.ob
+                                                               : ph == 2 ? g.fb
+                                                                         : g.db))
+                                      : nullptr;
             if (ph == 2)
-                rows16<NBE>(a.geo[2], lds + g.fw, lds + g.fs, Y, nrows, RES, tid);
+                rows16<NBE>(a.geo[2], lds + g.fw, lds + g.fs, bi, XS, Y, nrows, RES, tid);
             else if (ph == 0)
-                rows32<NBE>(a.geo[0], lds + g.qw, lds + g.qs, Y, nrows, a.t_qkv + q0, tag, tid);
+                rows32<NBE>(a.geo[0], lds + g.qw, lds + g.qs, bi, XS, Y, nrows, a.t_qkv + q0, tag, tid);
             else if (ph == 1)
-                rows32<NBQ>(a.geo[1], lds + g.ow, lds + g.os, Y, nrows, a.t_o + o0, tag, tid);
+                rows32<NBQ>(a.geo[1], lds + g.ow, lds + g.os, bi, XS, Y, nrows, a.t_o + o0, tag, tid);
             else
-                rows32<NBF>(a.geo[3], lds + g.dw, lds + g.ds, H, nrows, a.t_down + d0, tag, tid);
+                rows32<NBF>(a.geo[3], lds + g.dw, lds + g.ds, bi, XS, H, nrows, a.t_down + d0, tag, tid);
         }
         if (!pbar(PCTR, pgen)) *ABORT = 1;
         // The region is free for the next layer's copies (gate / up only
@@ -1091,7 +1160,7 @@ __device__ __forceinline__ void attn_wg(const PkArgs& a, uint8_t* lds, uint32_t 
 // workgroup code takes would be copied to the stack).
 // NBE, NBQ, NBF: the block counts of the n_embd-, q-dim- and n_ff-column
 // matrices when compiled for them (Gemma-3-1B's), else 0.
-template <int HD, int NBE, int NBQ, int NBF>
+template <int HD, int NBE, int NBQ, int NBF, bool Q4>
 __global__ __launch_bounds__(PK_NT) void step_kernel(const PkArgs* __restrict__ ap) {
     __shared__ __attribute__((aligned(256))) uint8_t lds[PK_LDS];
     const PkArgs& a = *ap;
@@ -1099,7 +1168,7 @@ __global__ __launch_bounds__(PK_NT) void step_kernel(const PkArgs* __restrict__ 
     if ((int)blockIdx.x < a.A)
         attn_wg<HD>(a, lds, base);
     else
-        matmul_wg<NBE, NBQ, NBF>(a, lds, base);
+        matmul_wg<NBE, NBQ, NBF, Q4>(a, lds, base);
 }
 
 // End of a step: the greedy token is recorded, the position advances.
@@ -1148,6 +1217,8 @@ struct nngd_model {
     uint64_t* tok = nullptr;
     int *pos = nullptr, *step = nullptr, *tokens = nullptr, *errf = nullptr;
     uint32_t* seq = nullptr;
+    uint16_t* bias = nullptr;           // Q4: every layer matrix's bias rows, padded
+    std::vector<nnh_weight*> shadow;    // Q4: Q8_0 copies of the layer matrices' nibble values
     int n_gen_max = 0, grid = 0;
     const void* kernel = nullptr;  // the step kernel instance for this model's shapes
     hipStream_t st = nullptr;
@@ -1167,6 +1238,8 @@ void nngd_free(nngd_model* m) {
                     m->seq};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    if (m->bias) (void)hipFree(m->bias);
+    for (nnh_weight* w : m->shadow) nnh_free(w);
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
 }
@@ -1223,18 +1296,68 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
         return 1;
     }
     m->w.assign(weights, weights + n_weights);
+    // Layer matrices: Q8_0 as uploaded; Q4 as a Q8_0 copy of the nibble
+    // values (the same chains: f32(q) * s with q = 0..15) through the
+    // library, whose f32 layout the step reads, plus the bias rows, each
+    // zero-padded to whole 16-byte pieces.
     std::vector<F32Mat> f;
+    std::vector<uint16_t> bias_host;
+    std::vector<size_t> bias_at;
+    int wdt = 0;
     for (int i = 0; i < 7 * c.n_layer; ++i) {
+        int dt = 0;
+        size_t rows = 0, cols = 0;
+        if (nnh_weight_info(weights[i], &dt, &rows, &cols)) {
+            m->err = std::string("weight info: ") + nnh_last_error();
+            return 1;
+        }
+        if ((dt != NNH_Q8_0 && dt != NNH_Q4S) || (i > 0 && dt != wdt)) {
+            m->err = "the device step takes layer matrices all Q8_0 or all Q4";
+            return 1;
+        }
+        wdt = dt;
+        const nnh_weight* src = weights[i];
+        if (dt == NNH_Q4S) {
+            const size_t n = rows * cols, nb = cols / 32, be = brow_elems((int)nb);
+            std::vector<uint8_t> raw(n / 2 + n / 8);
+            std::vector<int8_t> q8(n);
+            nnh_weight* sh = nullptr;
+            if (nnh_weight_download(weights[i], raw.data(), raw.size())) {
+                m->err = std::string("Q4 download: ") + nnh_last_error();
+                return 1;
+            }
+            for (size_t r = 0; r < rows; ++r)
+                for (size_t b = 0; b < nb; ++b)
+                    for (int k = 0; k < 16; ++k) {
+                        const uint8_t byte = raw[r * cols / 2 + 16 * b + k];
+                        q8[r * cols + 32 * b + k] = (int8_t)(byte & 15);
+                        q8[r * cols + 32 * b + k + 16] = (int8_t)(byte >> 4);
+                    }
+            const uint16_t* sc = (const uint16_t*)(raw.data() + n / 2);
+            const uint16_t* bi = sc + n / 32;
+            if (nnh_upload_q8_0(q8.data(), sc, rows, cols, &sh)) {
+                m->err = std::string("Q4 rows as Q8_0: ") + nnh_last_error();
+                return 1;
+            }
+            m->shadow.push_back(sh);
+            src = sh;
+            bias_at.push_back(bias_host.size());
+            for (size_t r = 0; r < rows; ++r) {
+                bias_host.insert(bias_host.end(), bi + r * nb, bi + (r + 1) * nb);
+                bias_host.insert(bias_host.end(), be - nb, (uint16_t)0);
+            }
+        }
         nnh_f32_layout l;
-        if (nnh_weight_f32_layout(weights[i], &l)) {
+        if (nnh_weight_f32_layout(src, &l)) {
             m->err = std::string("weight layout: ") + nnh_last_error();
             return 1;
         }
-        if (l.dtype != NNH_Q8_0) {
-            m->err = "the device step takes Q8_0 layer weights";
-            return 1;
-        }
-        f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, l.biases, (int)l.rows, (int)l.nb, (int)l.nbp});
+        f.push_back(F32Mat{(const uint8_t*)l.quants, l.scales, nullptr, (int)l.rows, (int)l.nb, (int)l.nbp});
+    }
+    if (wdt == NNH_Q4S) {
+        GD_HIP(hipMalloc((void**)&m->bias, bias_host.size() * 2));
+        GD_HIP(hipMemcpy(m->bias, bias_host.data(), bias_host.size() * 2, hipMemcpyHostToDevice));
+        for (int i = 0; i < 7 * c.n_layer; ++i) f[i].bi = m->bias + bias_at[i];
     }
     // The lm_head's layouts too, before any step is captured.
     if (nnh_weight_prepare(m->w.back(), NNH_ACT_F32, 1)) {
@@ -1278,12 +1401,21 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     g.fs = (uint32_t)o, o = align256(o + (size_t)2 * most(F) * srow_bytes(mf));
     g.dw = (uint32_t)o, o = align256(o + (size_t)most(E) * qrow_bytes(md));
     g.ds = (uint32_t)o, o = align256(o + (size_t)most(E) * srow_bytes(md));
+    const bool q4 = wdt == NNH_Q4S;
+    auto bbytes = [&](int rows, const F32Mat& mm) { return q4 ? (size_t)rows * 2 * brow_elems(mm.nb) : 0; };
+    g.qb = (uint32_t)o, o = align256(o + bbytes(most(QD + 2 * KVD), mq));
+    g.ob = (uint32_t)o, o = align256(o + bbytes(most(E), mo));
+    g.fb = (uint32_t)o, o = align256(o + bbytes(2 * most(F), mf));
+    g.db = (uint32_t)o, o = align256(o + bbytes(most(E), md));
     g.y = (uint32_t)o, o = align256(o + (size_t)std::max(E, QD) * 4);
-    g.in = (uint32_t)o, o = align256(o + (size_t)E * 4);
+    // The Q4 block sums alias the polled input: formed after the norms have
+    // read it, dead before the next phase polls into it.
+    g.in = (uint32_t)o, o = align256(o + std::max((size_t)E * 4, q4 ? (size_t)std::max(std::max(E, QD), F) / 32 * 4 : 0));
+    g.xs = g.in;
     g.xt = (uint32_t)o, o = align256(o + (size_t)8 * tstride(E) * 4);
     g.res = (uint32_t)o, o = align256(o + (size_t)2 * most(F) * 4);
     g.bc = (uint32_t)o, o = align256(o + 64);
-    g.wtab = (uint32_t)o, o = align256(o + (size_t)14 * c.n_layer * 8);
+    g.wtab = (uint32_t)o, o = align256(o + (size_t)21 * c.n_layer * 8);
     g.bytes = (uint32_t)o;
     if (o > (size_t)PK_LDS || (hd == 256 ? AttnLds<256>::bytes : AttnLds<128>::bytes) > PK_LDS) {
         m->err = "the device step's LDS share exceeds the workgroup's LDS";
@@ -1306,6 +1438,7 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     GD_HIP(hipMemcpy(m->sin_t, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     const size_t ns = norm_stride(c);
     a.geo[0] = f[0], a.geo[1] = f[3], a.geo[2] = f[4], a.geo[3] = f[6];
+    a.q4 = q4 ? 1 : 0;
     for (F32Mat& gm : a.geo) gm.fq = nullptr, gm.fs = nullptr, gm.bi = nullptr;
     for (int li = 0; li < c.n_layer; ++li)
         for (int j = 0; j < 7; ++j) {
@@ -1315,11 +1448,12 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
                 return 1;
             }
         }
-    std::vector<uint64_t> wp(14 * (size_t)c.n_layer);
+    std::vector<uint64_t> wp(21 * (size_t)c.n_layer);
     for (int li = 0; li < c.n_layer; ++li)
         for (int j = 0; j < 7; ++j) {
-            wp[14 * li + 2 * j] = (uint64_t)(uintptr_t)f[7 * li + j].fq;
-            wp[14 * li + 2 * j + 1] = (uint64_t)(uintptr_t)f[7 * li + j].fs;
+            wp[21 * li + 3 * j] = (uint64_t)(uintptr_t)f[7 * li + j].fq;
+            wp[21 * li + 3 * j + 1] = (uint64_t)(uintptr_t)f[7 * li + j].fs;
+            wp[21 * li + 3 * j + 2] = (uint64_t)(uintptr_t)f[7 * li + j].bi;
         }
     GD_HIP(hipMalloc((void**)&m->wptr, wp.size() * 8));
     GD_HIP(hipMemcpy(m->wptr, wp.data(), wp.size() * 8, hipMemcpyHostToDevice));
@@ -1375,9 +1509,18 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     GD_HIP(hipMemset(m->errf, 0, 4));
     GD_HIP(hipMalloc((void**)&m->tokens, (size_t)std::max(n_gen_max, 1) * 4));
     const uint8_t* te = (const uint8_t*)nnh_weight_device_data(m->w.back());
+    int edt = 0;
+    size_t er = 0, ec = 0;
+    if (nnh_weight_info(m->w.back(), &edt, &er, &ec) || er != (size_t)c.n_vocab || ec != (size_t)E ||
+        edt != wdt) {
+        m->err = "the embedding table must be n_vocab x n_embd, in the layer matrices' format";
+        return 1;
+    }
+    const size_t tn = (size_t)c.n_vocab * E;
     a.tok = m->tok;
     a.tq = (const int8_t*)te;
-    a.ts = (const uint16_t*)(te + (size_t)c.n_vocab * E);
+    a.ts = (const uint16_t*)(te + (edt == NNH_Q4S ? tn / 2 : tn));
+    a.tb = edt == NNH_Q4S ? (const uint16_t*)(te + tn / 2 + tn / 16) : nullptr;
     a.out_norm = m->norms + ns * c.n_layer;
     a.pos_p = m->pos;
     a.step_p = m->step;
@@ -1390,11 +1533,17 @@ int nngd_create(const nng_config* cfg, const float* norms, nnh_weight* const* we
     m->grid = a.A + a.M;
     GD_HIP(hipMalloc((void**)&m->args_dev, sizeof(PkArgs)));
     GD_HIP(hipMemcpy(m->args_dev, &a, sizeof(PkArgs), hipMemcpyHostToDevice));
-    // Gemma-3-1B's shapes have an instance of their own (its row loops unroll).
-    if (hd == 256 && E == 1152 && QD == 1024 && F == 6912)
-        m->kernel = (const void*)step_kernel<256, 36, 32, 216>;
+    // Gemma-3-1B's shapes have an instance of their own (its row loops
+    // unroll); Q4 layer matrices one of their own (the bias term).
+    const bool g1b = hd == 256 && E == 1152 && QD == 1024 && F == 6912;
+    if (q4)
+        m->kernel = g1b ? (const void*)step_kernel<256, 36, 32, 216, true>
+                        : hd == 256 ? (const void*)step_kernel<256, 0, 0, 0, true>
+                                    : (const void*)step_kernel<128, 0, 0, 0, true>;
     else
-        m->kernel = hd == 256 ? (const void*)step_kernel<256, 0, 0, 0> : (const void*)step_kernel<128, 0, 0, 0>;
+        m->kernel = g1b ? (const void*)step_kernel<256, 36, 32, 216, false>
+                        : hd == 256 ? (const void*)step_kernel<256, 0, 0, 0, false>
+                                    : (const void*)step_kernel<128, 0, 0, 0, false>;
     // Every workgroup must be resident at once.
     int per_cu = 0;
     GD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, m->kernel, PK_NT, 0));

@@ -57,7 +57,7 @@ def cpu_generate(oracle, model, prompt, n_gen):
     arr = (C.c_void_p * len(bufs))(*[b.ctypes.data for b in bufs])
     rows = (C.c_size_t * len(bufs))(*[r for r, _ in model.shapes])
     cols = (C.c_size_t * len(bufs))(*[c for _, c in model.shapes])
-    table = OrModelTable(n=len(bufs), dtype=1, bufs=C.cast(arr, C.POINTER(C.c_void_p)),
+    table = OrModelTable(n=len(bufs), dtype=model.cfg.wtype, bufs=C.cast(arr, C.POINTER(C.c_void_p)),
                          rows=C.cast(rows, C.POINTER(C.c_size_t)), cols=C.cast(cols, C.POINTER(C.c_size_t)))
     oracle.avx_set_threads(8)
     gemv = C.cast(oracle.lib().or_model_gemv_cb, C.c_void_p).value
@@ -141,3 +141,34 @@ def test_device_decode_past_one_block_and_the_window(oracle, long_model):
     tg, hg, _, tdg = long_model.generate_device(prompt, n_gen)
     print(f"device: {(n_gen - 1) / tdg:.1f} tok/s at positions {n_prompt}..{n_prompt + n_gen - 1}", flush=True)
     check_same(long_model, tg, hg, tc, hc, n_fwd=(n_prompt + 15) // 16 + n_gen - 1)
+
+
+@pytest.fixture(scope="module")
+def q4_model():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import nncpu_amd as N
+    from nncpu_amd.gemma import Gemma3, gemma3_1b_gguf
+    N.init(0)
+    return Gemma3.from_gguf(gemma3_1b_gguf(), n_ctx=256, dtype=N.Q4S)
+
+
+def test_gemma3_1b_q4_device_decode_token_identical(oracle, q4_model):
+    # The same GGUF re-encoded to nncpu's Q4 (every matrix and the tied
+    # embedding, as load.rs:186-197 does for WeightFormat::Q4): the embedding
+    # row is embed_row_q4 (kernels/mod.rs:934-954), every matmul q4_row plus
+    # the bias term (scalar.rs:654-674, 708-740). The device decode against
+    # the CPU forward with the AVX2 restatement of nncpu's Q4 gemv.
+    from nncpu_amd.gemma import random_prompt
+    n_gen = 64
+    prompt = random_prompt(PROMPT_LEN, q4_model.cfg.n_vocab, seed=0x4B17)
+    print("cpu decode, Q4", flush=True)
+    tc, hc, _, _ = cpu_generate(oracle, q4_model, prompt, n_gen)
+    print("device decode, Q4", flush=True)
+    tg, hg, _, tdg = q4_model.generate_device(prompt, n_gen)
+    print(f"device, Q4: {(n_gen - 1) / tdg:.1f} tok/s", flush=True)
+    check_same(q4_model, tg, hg, tc, hc, n_fwd=2 + n_gen - 1)
+    # The matmuls through the library's Q4 path (host round trips) agree too.
+    tg2, hg2, _, _ = q4_model.generate_gpu(prompt, n_gen)
+    check_same(q4_model, tg2, hg2, tc, hc, n_fwd=2 + n_gen - 1)

@@ -291,3 +291,62 @@ def test_merge_expf_restatement_is_glibc_expf(ops):
     with ThreadPoolExecutor(8) as pool:
         bad = sum(pool.map(run, range((1 << 32) // chunk)))
     assert bad == 0
+
+
+# ---- embedding rows (kernels/tests.rs:992-1032) ------------------------------------------------
+
+def embed(ops, wtype, table, n_vocab, n_embd, tok, scale):
+    ops.nng_op_embed_row.argtypes = [C.c_int, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p]
+    ops.nng_op_embed_row.restype = None
+    y = np.zeros(n_embd, np.float32)
+    ops.nng_op_embed_row(wtype, p(table), n_vocab, n_embd, tok, scale, p(y))
+    return y
+
+
+def test_embed_rows_match_dequantized_tables(ops, oracle):
+    # The scaled dequantized row, within quantization error of the source.
+    rng = oracle.Rng(0xE3B0)
+    rng.vec(17 * 5, -2.0, 2.0)  # the reference's BF16 case draws first (no BF16 tables here)
+    n_embd, n_vocab, tok, scale = 64, 7, 5, 0.75
+    src = rng.vec(n_vocab * n_embd, -2.0, 2.0)
+    row = tok * n_embd
+    qs, sc = oracle.quantize_q8_0(src)
+    y = embed(ops, 1, oracle.pack_q8(qs, sc), n_vocab, n_embd, tok, scale)
+    want = np.array([float(np.float32(qs[row + i]) * np.float32(oracle.bf16_to_f32(int(sc[(row + i) // 32])))
+                           * np.float32(scale)) for i in range(n_embd)])
+    assert close(y, want, 1e-5).all()
+    assert (np.abs(y - src[row:row + n_embd] * scale) <= 0.05).all()
+    q4, s4, b4 = oracle.quantize_q4(src)
+    y = embed(ops, 2, oracle.pack_q4(q4, s4, b4), n_vocab, n_embd, tok, scale)
+    # q4_dequant (kernels/tests.rs:387-397): sc * q + bi per element.
+    want = np.zeros(n_embd, np.float32)
+    for b in range(n_embd // 32):
+        s_ = np.float32(oracle.bf16_to_f32(int(s4[row // 32 + b])))
+        b_ = np.float32(oracle.bf16_to_f32(int(b4[row // 32 + b])))
+        for k in range(16):
+            byte = int(q4[row // 2 + 16 * b + k])
+            want[32 * b + k] = s_ * np.float32(byte & 15) + b_
+            want[32 * b + k + 16] = s_ * np.float32(byte >> 4) + b_
+    assert close(y, want * np.float32(scale), 1e-5).all()
+    assert (np.abs(y - src[row:row + n_embd] * scale) <= 0.2).all()
+
+
+def test_embed_row_q4_nibble_order(ops):
+    # Known answers: byte k of a block holds element k in its low nibble and
+    # element k + 16 in its high one (kernels/mod.rs:948-951); scale 1 and
+    # bias 0 make every output the nibble itself, times the row scale.
+    n_vocab, n_embd = 2, 64
+    q = np.zeros(n_vocab * n_embd // 2, np.uint8)
+    for t in range(n_vocab):
+        for b in range(2):
+            for k in range(16):
+                q[t * 32 + 16 * b + k] = ((k + b + t) & 15) | (((15 - k) & 15) << 4)
+    one = 0x3F80
+    table = np.concatenate([q, np.full(n_vocab * 2, one, np.uint16).view(np.uint8),
+                            np.zeros(n_vocab * 2, np.uint16).view(np.uint8)])
+    for t in range(n_vocab):
+        y = embed(ops, 2, table, n_vocab, n_embd, t, 2.0)
+        for b in range(2):
+            for k in range(16):
+                assert y[32 * b + k] == 2.0 * ((k + b + t) & 15)
+                assert y[32 * b + k + 16] == 2.0 * (15 - k)
