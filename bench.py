@@ -52,7 +52,7 @@ FUSED_GATE_UP = (28672, 4096)
 # rocprofv3 --pmc FETCH_SIZE (scaled by 2.0, the factor a 64 MiB device copy
 # gives in the same run) + WRITE_SIZE readings of `bench.py --workload traffic`.
 TRAFFIC_SOURCE = "profiles/gemv_i8_q4_llama3_8b_sweep.md (rocprofv3 --pmc over bench.py --workload traffic)"
-Q4_SWEEP_TRAFFIC = [10_603_212, 2_713_600, 36_853_350, 36_929_126]
+Q4_SWEEP_TRAFFIC = [10_597_376, 2_708_480, 36_837_325, 36_943_872]
 Q8_VOCAB = [(262144, 1152), (151936, 3584)]
 
 
@@ -333,6 +333,26 @@ def peaks(args):
         res[name.replace("_tops", "_frac").replace("_tflops", "_frac")] = round(v / peak, 4)
     res["datasheet"] = dict(hbm_gbs=HBM_PEAK_GBS, int8_tops=INT8_PEAK_TOPS, bf16_tflops=BF16_PEAK_TFLOPS)
     del big, dst
+    # A reference point for the M = 512 GEMMs: the platform library's plain
+    # BF16 GEMM (torch.matmul -> hipBLASLt) at the prefill's gate / down
+    # shapes, no block scales, four rotating weight copies.
+    lib_gemm = []
+    for n, k in ((18944, 3584), (3584, 18944)):
+        a = torch.randn(512, k, device="cuda", dtype=torch.bfloat16)
+        ws = [torch.randn(k, n, device="cuda", dtype=torch.bfloat16) for _ in range(4)]
+        for i in range(4):
+            torch.matmul(a, ws[i])
+        torch.cuda.synchronize()
+        e0 = st.event()
+        with torch.cuda.stream(st.s):
+            for i in range(40):
+                torch.matmul(a, ws[i % 4])
+        e1 = st.event()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 40
+        lib_gemm.append(dict(case=f"BF16 512x{n}x{k}", us=round(us, 2), tflops=round(2 * 512 * n * k / us / 1e6, 1)))
+        del a, ws
+    res["hipblaslt_bf16_m512"] = lib_gemm
     torch.cuda.synchronize()
     log(f"peaks: {res}")
     return res
