@@ -37,7 +37,6 @@ struct nnh_weight {
     float* swT;           // device: [nb][rows padded] f32 scales, Q4 biases after (MFMA GEMM)
     int bpath;            // BF16 only: the reference kernel this shape takes (nnh::BF16_PATH_*)
     uint16_t* bl;         // device: BF16 only, the chain layout (none on the f64 path)
-    uint16_t* wbf;        // device: BF16 copies of the quants, rows padded (MX GEMM)
     uint16_t* wbi;        // device: Q4 biases twice per block, rows padded (MX GEMM)
     unsigned ready;       // derived layouts built so far (LAY_* bits)
     size_t dev_bytes;     // device bytes held (split layout + derived layouts)
@@ -213,7 +212,7 @@ void launch_i8(const nnh_weight* w, int mode, const uint8_t* act, size_t n_tok, 
     const double* sx = (const double*)(act + l.off_sx);
     const float* sxT = (const float*)(act + l.off_sxT);
     if (n_tok >= GEMM_MIN_TOKENS && mode == NNH_ACT_MXI8)
-        nnh::launch_gemm_mx(w->dtype, w->wbf, w->swT, w->wbi, (const uint16_t*)(act + l.off_xb),
+        nnh::launch_gemm_mx(w->dtype, w->qs, w->swT, w->wbi, (const uint16_t*)(act + l.off_xb),
                             (const uint16_t*)(act + l.off_xl), (int)w->rows, (int)w->nb, (int)n_tok, y, y_stride,
                             (float*)ws, st);
     else if (n_tok >= GEMM_MIN_TOKENS)
@@ -323,7 +322,6 @@ void release(nnh_weight* w) {
     if (w->sb) (void)hipFree(w->sb);
     if (w->swT) (void)hipFree(w->swT);
     if (w->bl) (void)hipFree(w->bl);
-    if (w->wbf) (void)hipFree(w->wbf);
     if (w->wbi) (void)hipFree(w->wbi);
     delete w;
 }
@@ -340,7 +338,7 @@ enum : unsigned {
     LAY_F32 = 1,  // fq + fs: the bit-exact f32 path
     LAY_SB = 2,   // Q4 sb: the int8 GEMV
     LAY_SWT = 4,  // swT: the MFMA kernels (few-token, GEMM)
-    LAY_MX = 8,   // wbf (+ Q4 wbi): the MX GEMM
+    LAY_MX = 8,   // Q4 wbi: the MX GEMM's bias operand
 };
 
 // What a call with activation mode `act` over n_tok vectors reads.
@@ -439,11 +437,9 @@ int prepare_locked(const nnh_weight* cw, unsigned need) {
         if ((rc = dev_alloc(w, (void**)&w->swT, bytes))) return rc;
         nnh::launch_gemm_scales(w->sc, w->bi, w->swT, rows, nb, g_stream);
     }
-    if (need & LAY_MX) {
-        if ((rc = dev_alloc(w, (void**)&w->wbf, nnh::mx_weight_bytes(rows, nb))) ||
-            (w->dtype == NNH_Q4S && (rc = dev_alloc(w, (void**)&w->wbi, nnh::mx_bias_bytes(rows, nb)))))
-            return rc;
-        nnh::launch_mx_weights(w->dtype, w->qs, w->bi, rows, nb, w->wbf, w->wbi, g_stream);
+    if ((need & LAY_MX) && w->dtype == NNH_Q4S) {
+        if ((rc = dev_alloc(w, (void**)&w->wbi, nnh::mx_bias_bytes(rows, nb)))) return rc;
+        nnh::launch_mx_bias(w->bi, rows, nb, w->wbi, g_stream);
     }
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)

@@ -138,14 +138,12 @@ void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows,
 int mx_nbp8(int nb);
 void launch_quantize_mx(const float* x, size_t x_stride, int cols, int n_tok, int8_t* q, uint16_t* s, double* sx,
                         float* sxT, int tok_pad, uint16_t* xb, uint16_t* xl, hipStream_t st);
-size_t mx_weight_bytes(int rows, int nb);  // BF16 quants, rows padded to whole tiles
 size_t mx_bias_bytes(int rows, int nb);    // Q4 biases twice, rows padded
 int mx_xl_tok(int n_tok);                  // GEMM token tiles' worth of tokens
 size_t mx_xl_bytes(int n_tok, int nb);     // X limbs, tokens padded to mx_xl_tok
-void launch_mx_weights(int dtype, const uint8_t* qs, const uint16_t* bi, int rows, int nb, uint16_t* wbf,
-                       uint16_t* wbi, hipStream_t st);
+void launch_mx_bias(const uint16_t* bi, int rows, int nb, uint16_t* wbi, hipStream_t st);
 size_t gemm_mx_workspace_bytes(int rows, int nb, int n_tok);  // f32 partial tiles
-void launch_gemm_mx(int dtype, const uint16_t* wbf, const float* swT, const uint16_t* wbi, const uint16_t* xb,
+void launch_gemm_mx(int dtype, const uint8_t* qs, const float* swT, const uint16_t* wbi, const uint16_t* xb,
                     const uint16_t* xl, int rows, int nb, int n_tok, float* y, size_t y_stride, float* ws,
                     hipStream_t st);
 

@@ -45,8 +45,15 @@
 // serving two MFMAs. Operands stream through a ring of three LDS stages of
 // 2 blocks (two in flight while one is computed), filled by direct
 // global -> LDS loads (no staging registers) whose addresses are a scalar
-// base plus a fixed per-lane offset; 16-byte chunks of each 64-byte row are
-// XOR-swizzled against bank conflicts.
+// base plus a per-lane offset; 16-byte chunks of each 64-byte row are
+// XOR-swizzled against bank conflicts. The weights arrive as nncpu's own
+// quant bytes (Q8 1 byte, Q4 half a byte per weight, read in place from the
+// uploaded split layout): each wave's direct load lands in a staging slice
+// of the stage, and at the stage's turn the wave converts its slice to BF16
+// (exact: the quants are small integers) into the stage's operand rows. A
+// weight tile is reused by 256 tokens, so the conversion is a small VALU
+// cost per MFMA, while the bytes streamed per weight are a half (Q8) or a
+// quarter (Q4) of a BF16 copy's, and no such copy is kept.
 
 #include "common.h"
 
@@ -144,34 +151,7 @@ __global__ __launch_bounds__(256) void quantize_mx_kernel(const float* __restric
     }
 }
 
-// ---- upload-time weight copies -------------------------------------------------
-
-// BF16 of quant k of block b of row n (exact: Q8 -127..127, Q4 0..15,
-// nncpu's nibble order: byte i low = element i, high = element i+16), zero
-// in the pad rows (n up to the next multiple of 128), stored tiled as the
-// GEMM loads it: [n / 128][b][n % 128][32], the 16-byte chunk c of a row at
-// position c ^ ((n % 128 >> 2) & 3).
-__global__ void mx_weights_kernel(int dtype, const uint8_t* __restrict__ qs, uint16_t* __restrict__ wbf, size_t n,
-                                  size_t n_pad, int nb) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_pad) return;
-    const size_t row = i / ((size_t)nb * 32), rb = i - row * nb * 32;
-    const size_t bb = rb >> 5;
-    const int kk = (int)(rb & 31), rt = (int)(row / 128), rr = (int)(row % 128);
-    const size_t dst = (((size_t)rt * nb + bb) * 128 + rr) * 32 + (((kk >> 3) ^ ((rr >> 2) & 3)) << 3) + (kk & 7);
-    int v;
-    if (i >= n) {
-        v = 0;
-    } else if (dtype == 1) {
-        v = (int)(int8_t)qs[i];
-    } else {
-        const size_t blk = i >> 5;
-        const int k = (int)(i & 31);
-        const uint8_t byte = qs[blk * 16 + (k & 15)];
-        v = k < 16 ? (byte & 15) : (byte >> 4);
-    }
-    wbf[dst] = (uint16_t)(__float_as_uint((float)v) >> 16);
-}
+// ---- upload-time weight tables -------------------------------------------------
 
 // Q4 biases twice per block, [rows_pad][nbp8][2], zero past nb and in the pad
 // rows: the B operand of the bias MFMA, whose A operand holds X's limbs.
@@ -208,11 +188,12 @@ struct MxBias {
 template <int DT>
 struct MxPlan {
     static constexpr int I_A = MX_KS * MX_TM * 64 / 1024;
-    static constexpr int I_B = MX_KS * MX_TN * 64 / 1024;
+    static constexpr int I_B = MX_NW;  // one quant-byte load per wave (Q4: half a wave's lanes)
     static constexpr int I_S = MX_KS * MX_TN * 4 / 1024;
     static constexpr int I_MAIN = I_A + I_B + I_S;
     static constexpr int I_BIAS = DT == 2 ? (int)sizeof(MxBias) / 1024 : 0;
-    static_assert(I_A == 4 * MX_NW && I_B == 2 * MX_NW && I_S == 1, "the issue code below hard-codes this split");
+    static_assert(I_A == 4 * MX_NW && I_S == 1, "the issue code below hard-codes this split");
+    static_assert(MX_KS * MX_TN * 32 == I_B * 1024, "Q8: a wave's slice is 16 rows x 2 blocks x 32 bytes");
     static_assert(I_BIAS == 0 || I_BIAS == 12, "bias pieces: 8 of X, 4 of W");
     __device__ static int count(int wave, bool last) {
         const int tot = I_MAIN + (last ? I_BIAS : 0);
@@ -222,7 +203,7 @@ struct MxPlan {
 static_assert(sizeof(MxStage) * 3 + sizeof(MxBias) <= 160 * 1024, "three stages and the bias operands fit the LDS");
 
 struct MxArgs {
-    const uint16_t* wbf;  // [row tile][nb][128][32] BF16 quants (chunks swizzled)
+    const uint8_t* qs;    // nncpu's quants, row-major: Q8 32 bytes, Q4 16 bytes per block
     const float* swT;     // [nb + 1][rows_pad] f32 weight scales
     const uint16_t* wbi;  // Q4: [rows_pad][nbp8][2] BF16 biases, twice
     const uint16_t* xb;   // [token tile][nb][256][32] BF16 q_x 2^E (chunks swizzled)
@@ -230,6 +211,7 @@ struct MxArgs {
     float* ws;            // [team * mtiles + mt][2][8 waves][4 tiles][16][64] partial tiles
     float* y;
     size_t y_stride, cols;
+    uint32_t qrow;  // bytes per weight row of qs
     int rows, rows_pad, nb, nbp8, ng, n_tok, mtiles, teams, rtiles;
     int rounds;  // whole row tiles per team (data-parallel rounds): team t takes row tiles t, t + teams, ..
     long tail;   // the remaining (rtiles - rounds * teams) row tiles' units, split evenly over the teams
@@ -245,25 +227,35 @@ __device__ __forceinline__ long team_start(long team, long units, int teams) { r
 __device__ __forceinline__ int mx_swz(int c, int r) { return c ^ ((r >> 2) & 3); }
 
 // A lane's byte offsets for its loads, fixed for the kernel: each load is a
-// uniform (scalar) base plus one of these. The operands are stored tiled
-// (xb [token tile][block][256 tokens][32], wbf [row tile][block][128 rows]
-// [32], chunks already swizzled), so each 1 KB load is 1 KB of consecutive
-// bytes: wave w's A instructions cover token rows 16 w .. 16 w + 15 (a0)
-// and 128 + 16 w .. (a1) of a block, its B instructions weight rows
-// 16 w .. 16 w + 15; lane l's 16 bytes are row l / 4's chunk position l % 4,
-// which holds chunk mx_swz(l % 4, row) of the row.
+// uniform (scalar) base plus one of these. The activations are stored tiled
+// (xb [token tile][block][256 tokens][32], chunks already swizzled), so each
+// 1 KB load is 1 KB of consecutive bytes: wave w's A instructions cover
+// token rows 16 w .. 16 w + 15 (a0) and 128 + 16 w .. (a1) of a block; lane
+// l's 16 bytes are row l / 4's chunk position l % 4, which holds chunk
+// mx_swz(l % 4, row) of the row. The weight quants are read from the split
+// layout: wave w's slice is weight rows 16 w .. 16 w + 15 of the stage's two
+// blocks, Q8 lane l row 16 w + l / 4, block (l / 2) % 2, bytes 16 (l % 2)
+// .. + 15 of it; Q4 lane l < 32 row 16 w + l / 2, block l % 2, all 16
+// bytes (brow, the row in the tile; bcol, the byte offset in the row when
+// the stage's two blocks are consecutive).
 struct MxLane {
-    uint32_t a0, a1, b, bias, sw;
+    uint32_t a0, a1, bias, sw, brow, bcol;
 };
 
-__device__ __forceinline__ MxLane mx_lane(const MxArgs& g, int wave, int lane, int m0) {
+template <int DT>
+__device__ __forceinline__ MxLane mx_lane(const MxArgs& g, int wave, int lane) {
     MxLane o;
-    (void)m0;
     o.a0 = (uint32_t)(wave * 1024 + lane * 16);
     o.a1 = (uint32_t)(8192 + wave * 1024 + lane * 16);
-    o.b = (uint32_t)(wave * 1024 + lane * 16);
     o.bias = (uint32_t)((lane >> 1) * g.nbp8 * 4 + 16 * (lane & 1));
     o.sw = (uint32_t)((lane >> 5) * g.rows_pad * 4 + 16 * (lane & 31));
+    if (DT == 1) {
+        o.brow = (uint32_t)(16 * wave + (lane >> 2));
+        o.bcol = (uint32_t)(16 * (lane & 1) + 32 * ((lane >> 1) & 1));
+    } else {
+        o.brow = (uint32_t)(16 * wave + ((lane >> 1) & 15));
+        o.bcol = (uint32_t)(16 * (lane & 1));
+    }
     return o;
 }
 
@@ -278,10 +270,18 @@ __device__ __forceinline__ void lds_load(const void* base, uint32_t voff, void* 
                  : "memory");
 }
 
+// Wave w's staging slice of a stage's weight quants: 1 KB at B[1] + 1 KB w,
+// inside the BF16 rows 16 w .. 16 w + 15 of block 1 that the wave's own
+// conversion writes (so no other wave's slice is overwritten).
+__device__ __forceinline__ uint8_t* mx_stage_slice(MxStage& st, int wave) {
+    return (uint8_t*)&st.B[1][0][0] + 1024 * wave;
+}
+
 // Issue this wave's loads of the stage holding blocks 2 j, 2 j + 1 of group
 // gi of row tile rt. Blocks past nb are clamped to the last block (never
-// computed); tokens, weight rows and X limbs are padded to whole tiles with
-// zeros; the scale table has a spare block row past nb.
+// computed); tokens and X limbs are padded to whole tiles with zeros, weight
+// rows past the matrix read its last row (their scales are zero and their
+// outputs are never stored); the scale table has a spare block row past nb.
 template <int DT>
 __device__ __forceinline__ void mx_issue(MxStage& st, MxBias& bias, const MxArgs& g, const MxLane& o, int rt, int gi,
                                          int j, int wave, int m0) {
@@ -289,18 +289,24 @@ __device__ __forceinline__ void mx_issue(MxStage& st, MxBias& bias, const MxArgs
     const int b0 = gi * MX_GRP + j * MX_KS;
     const int bA = b0 < g.nb ? b0 : g.nb - 1, bB = b0 + 1 < g.nb ? b0 + 1 : g.nb - 1;
     const uint8_t* xb = (const uint8_t*)g.xb + (size_t)(m0 / MX_TM) * g.nb * (MX_TM * 64);
-    const uint8_t* wb = (const uint8_t*)g.wbf + (size_t)rt * g.nb * (MX_TN * 64);
     uint8_t* A = (uint8_t*)&st.A[0][0][0];
-    uint8_t* B = (uint8_t*)&st.B[0][0][0];
     lds_load(xb + (size_t)bA * (MX_TM * 64), o.a0, A + wave * 1024);
     lds_load(xb + (size_t)bA * (MX_TM * 64), o.a1, A + (wave + 8) * 1024);
     lds_load(xb + (size_t)bB * (MX_TM * 64), o.a0, A + (wave + 16) * 1024);
     lds_load(xb + (size_t)bB * (MX_TM * 64), o.a1, A + (wave + 24) * 1024);
-    lds_load(wb + (size_t)bA * (MX_TN * 64), o.b, B + wave * 1024);
-    lds_load(wb + (size_t)bB * (MX_TN * 64), o.b, B + (wave + 8) * 1024);
+    {
+        constexpr int BLK = DT == 1 ? 32 : 16;  // quant bytes per block
+        const uint8_t* wq = g.qs + (size_t)n0 * g.qrow + (size_t)bA * BLK;
+        const int last = g.rows - 1 - n0;  // rows past the matrix read its last row
+        const uint32_t r = (int)o.brow < last ? o.brow : (uint32_t)last;
+        // bB == bA when the second block is past nb: both halves then read bA.
+        const uint32_t col = bB > bA ? o.bcol : (DT == 1 ? (o.bcol & 16u) : 0u);
+        const uint32_t voff = r * g.qrow + col;
+        if (DT == 1 || (__lane_id() < 32)) lds_load(wq, voff, mx_stage_slice(st, wave));
+    }
     if (wave == 0) lds_load((const uint8_t*)g.swT + ((size_t)bA * g.rows_pad + n0) * 4, o.sw, &st.SW[0][0]);
     if (DT == 2 && j == 3) {
-        // Bias pieces 0..11 are instructions 49..60: waves 1..7 take pieces
+        // Bias pieces 0..11 are instructions 41..52: waves 1..7 take pieces
         // 0..6, waves 0..4 pieces 7..11. Piece p < 8: X of tokens 32 p ..,
         // else the biases of rows 32 (p - 8) ..
         const uint8_t* xl = (const uint8_t*)g.xl + ((size_t)m0 * g.nbp8 + (size_t)gi * MX_GRP) * 4;
@@ -323,6 +329,51 @@ __device__ __forceinline__ void wait_vm(int n) {
 #undef NNH_W
         default: __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0)); break;
     }
+}
+
+// The high halves of two f32 values (exact BF16 values) as one BF16 pair.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// This wave's staged quants of the stage to BF16 operand rows (exact: Q8
+// -127..127 and Q4 0..15 are small integers), written into rows
+// 16 wave .. + 15 of both blocks, chunks swizzled as the reads expect. The
+// slice is read before any of it is overwritten (each lane's writes depend
+// on its read, and the slice lies inside the rows the wave writes).
+template <int DT>
+__device__ __forceinline__ void mx_convert(MxStage& st, int wave, int lane) {
+    const int row = 16 * wave + (lane >> 2), bsel = (lane >> 1) & 1;
+    uint16_t* dst = &st.B[bsel][row][0];
+    uint32_t o[8];
+    int c0, c1;
+    if (DT == 1) {
+        // 16 signed quants: elements 16 (lane % 2) .. + 15 of the block.
+        const int4 v = *(const int4*)(mx_stage_slice(st, wave) + 16 * lane);
+        const int w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            o[2 * d] = bf16_pair((float)(int8_t)w[d], (float)(int8_t)(w[d] >> 8));
+            o[2 * d + 1] = bf16_pair((float)(int8_t)(w[d] >> 16), (float)(w[d] >> 24));
+        }
+        c0 = 2 * (lane & 1);
+        c1 = c0 + 1;
+    } else {
+        // 8 bytes of the block: elements 8 p .. 8 p + 7 in the low nibbles,
+        // 16 + 8 p .. in the high ones (nncpu's order), p = lane % 2.
+        const uint2 v = *(const uint2*)(mx_stage_slice(st, wave) + 8 * lane);
+        const uint32_t w[4] = {v.x & 0x0F0F0F0Fu, v.y & 0x0F0F0F0Fu, (v.x >> 4) & 0x0F0F0F0Fu,
+                               (v.y >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            o[2 * d] = bf16_pair((float)(w[d] & 255u), (float)((w[d] >> 8) & 255u));
+            o[2 * d + 1] = bf16_pair((float)((w[d] >> 16) & 255u), (float)(w[d] >> 24));
+        }
+        c0 = lane & 1;
+        c1 = c0 + 2;
+    }
+    *(uint4*)(dst + 8 * mx_swz(c0, row)) = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4*)(dst + 8 * mx_swz(c1, row)) = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
 __device__ __forceinline__ v8bf lds_bf8(const uint16_t* row, int chunk, int r) {
@@ -456,9 +507,13 @@ __device__ __forceinline__ void mx_step(MxStage& cur, MxStage& nxt, MxBias& bias
     // This wave's loads of stage s are done once at most those of s + 1 are
     // outstanding (vmcnt counts down in issue order).
     wait_vm(s + 1 < L.nst ? P::count(L.wave, ((J + 1) & 3) == 3) : 0);
-    // Every wave's loads of stage s have landed and every wave is done with
-    // stage s - 1 (a bare barrier: __syncthreads would also wait for the
+    asm volatile("" ::: "memory");
+    mx_convert<DT>(cur, L.wave, L.lane);
+    // Every wave's loads of stage s have landed, its quants are converted,
+    // and every wave is done with stage s - 1 (the wave's own LDS writes
+    // first, then a bare barrier: __syncthreads would also wait for the
     // loads still in flight; the memory clobber keeps the LDS reads after it).
+    __builtin_amdgcn_s_waitcnt(NNH_LGKMCNT0);
     asm volatile("s_barrier" ::: "memory");
     if (s + 2 < L.nst) {
         if (J == 2) mx_advance(L.ic, L, g);  // stage s + 2 opens the next group
@@ -542,7 +597,7 @@ __global__ __launch_bounds__(MX_NW * 64) void gemm_mx_kernel(MxArgs g) {
     L.seg_k0 = 0;
     L.seg_gi0 = L.cc.gi;
     L.chunk = 0;
-    L.o = mx_lane(g, L.wave, L.lane, L.m0);
+    L.o = mx_lane<DT>(g, L.wave, L.lane);
 
     MxTiles tot, acc;
 #pragma unroll
@@ -680,19 +735,13 @@ void launch_quantize_mx(const float* x, size_t x_stride, int cols, int n_tok, in
                                                             xl_tok, xb, xl);
 }
 
-size_t mx_weight_bytes(int rows, int nb) { return (size_t)gemm_rows_pad(rows) * nb * 32 * 2; }
 size_t mx_bias_bytes(int rows, int nb) { return (size_t)gemm_rows_pad(rows) * mx_nbp8(nb) * 4; }
 size_t mx_xl_bytes(int n_tok, int nb) { return (size_t)mx_xl_tok(n_tok) * mx_nbp8(nb) * 4; }
 
-void launch_mx_weights(int dtype, const uint8_t* qs, const uint16_t* bi, int rows, int nb, uint16_t* wbf,
-                       uint16_t* wbi, hipStream_t st) {
+void launch_mx_bias(const uint16_t* bi, int rows, int nb, uint16_t* wbi, hipStream_t st) {
     const int rp = gemm_rows_pad(rows);
-    const size_t n = (size_t)rows * nb * 32, n_pad = (size_t)rp * nb * 32;
-    mx_weights_kernel<<<(unsigned)((n_pad + 255) / 256), 256, 0, st>>>(dtype, qs, wbf, n, n_pad, nb);
-    if (dtype == 2) {
-        const size_t m = (size_t)rp * mx_nbp8(nb);
-        mx_bias_kernel<<<(unsigned)((m + 255) / 256), 256, 0, st>>>(bi, wbi, rows, rp, nb, mx_nbp8(nb));
-    }
+    const size_t m = (size_t)rp * mx_nbp8(nb);
+    mx_bias_kernel<<<(unsigned)((m + 255) / 256), 256, 0, st>>>(bi, wbi, rows, rp, nb, mx_nbp8(nb));
 }
 
 size_t gemm_mx_workspace_bytes(int rows, int nb, int n_tok) {
@@ -700,12 +749,13 @@ size_t gemm_mx_workspace_bytes(int rows, int nb, int n_tok) {
     return (size_t)s.teams * s.mtiles * 2 * MX_TM * MX_TN * sizeof(float);
 }
 
-void launch_gemm_mx(int dtype, const uint16_t* wbf, const float* swT, const uint16_t* wbi, const uint16_t* xb,
+void launch_gemm_mx(int dtype, const uint8_t* qs, const float* swT, const uint16_t* wbi, const uint16_t* xb,
                     const uint16_t* xl, int rows, int nb, int n_tok, float* y, size_t y_stride, float* ws,
                     hipStream_t st) {
     const MxSched s = mx_sched(rows, nb, n_tok);
     MxArgs g;
-    g.wbf = wbf;
+    g.qs = qs;
+    g.qrow = (uint32_t)(dtype == 1 ? (size_t)nb * 32 : (size_t)nb * 16);
     g.swT = swT;
     g.wbi = wbi;
     g.xb = xb;
