@@ -146,8 +146,8 @@ int nnh_weight_info(const nnh_weight* w, int* dtype, size_t* rows, size_t* cols)
  *   int8, 1..3 vectors     Q4 +0.125 B (packed scale | bias), Q8_0 nothing
  *   int8, 4 and more       +0.125 B Q8_0, +0.25 B Q4 (block-major f32 scales,
  *                          Q4 biases)
- *   NNH_ACT_MXI8, 17 and more vectors: +2 B (BF16 quants), Q4 +0.125 B more
- *                          (BF16 biases)
+ *   NNH_ACT_MXI8, 17 and more vectors: as int8 with 4 and more, Q4 +0.125 B
+ *                          more (BF16 biases); the quants are read in place
  * nnh_weight_prepare builds those of a call (act, n_tok) ahead of time, for
  * callers that capture calls into HIP graphs (a first call inside a capture
  * would allocate and synchronise the library's own stream there) or that

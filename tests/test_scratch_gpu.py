@@ -61,8 +61,13 @@ def test_layouts_are_built_on_first_use(oracle, dtype):
     y20 = np.zeros(20 * rows, np.float32)
     N.gemv_batch(w, x, cols, y20, rows, 20, N.ACT_MXI8)
     after_mx = w.device_bytes()
-    # The MX GEMM's BF16 quants are the bulk of its layouts.
-    assert after_mx - after_gemv >= 2 * n
+    # The MX GEMM reads the quants in place: it adds the block-major f32
+    # scales (Q8 one spare block row; Q4 the biases too) and Q4's BF16 bias
+    # table, rows padded to whole 128-row tiles, and no copy of the quants.
+    rows_pad, nb = (rows + 127) // 128 * 128, cols // 32
+    swt = rows_pad * 4 * (nb + 1 if dtype == 1 else 2 * nb)
+    wbi = rows_pad * ((nb + 7) // 8 * 8) * 4 if dtype == 2 else 0
+    assert after_mx - after_gemv == align(swt) + (align(wbi) if wbi else 0)
     qx, sx = oracle.quantize_act(x[:cols])
     exact = oracle.gemv_i8_exact(m, qx, sx)
     assert np.all(np.abs(y1 - exact) <= np.spacing(np.abs(exact)))
