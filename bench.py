@@ -248,7 +248,8 @@ def q4_sweep(args, N):
 def traffic_run(N):
     """For `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`: a 64 MiB device
     copy (the counter's calibration: 64 MiB read, 64 MiB written), then each
-    sweep shape launched eagerly five times over two weight copies."""
+    sweep shape launched eagerly five times over two weight copies, then the
+    M = 512 MX GEMM at the Q8 gate and down shapes three times each."""
     import torch
     a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
@@ -262,6 +263,13 @@ def traffic_run(N):
             launch()
         torch.cuda.synchronize()
         log(f"traffic: {n}x{k} x5")
+        del launch
+    for i, (n, k) in enumerate([(18944, 3584), (3584, 18944)]):
+        launch = rotating(N, st, 1, n, k, 512, N.ACT_MXI8, 0x5EED20 + i, rot_bytes=1)
+        for _ in range(3):
+            launch()
+        torch.cuda.synchronize()
+        log(f"traffic: MX Q8 {n}x{k} M=512 x3")
         del launch
 
 
