@@ -190,6 +190,7 @@ def measure_cases(args, N, cases, act, label):
         byts = gemv_bytes(dtype, n, k, m)
         ops = 2.0 * m * n * k
         e = dict(case=case_name(dtype, n, k, m), us=round(us, 3), gbs=round(byts / us / 1e3, 1),
+                 weights_gbs=round(weight_bytes(dtype, n, k) / us / 1e3, 1),
                  hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4), tops=round(ops / us / 1e6, 2),
                  int8_frac=round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), launches=reps)
         log(f"{label}: {e}")
@@ -216,7 +217,8 @@ def q4_sweep(args, N):
         secs, reps = per_launch(st, launch, args.steps, args.warmup)
         b = gemv_bytes(2, n, k)
         p = dict(shape=f"{n}x{k}", copies=launch.copies, launches=reps, bytes=b, us=round(secs * 1e6, 4),
-                 gbs=round(b / secs / 1e9, 1), hbm_frac=round(b / secs / 1e9 / HBM_PEAK_GBS, 4))
+                 gbs=round(b / secs / 1e9, 1), weights_gbs=round(weight_bytes(2, n, k) / secs / 1e9, 1),
+                 hbm_frac=round(b / secs / 1e9 / HBM_PEAK_GBS, 4))
         log(f"{p['shape']}: {p['us']:.2f} us/launch over {reps} launches, {p['gbs']:.0f} GB/s "
             f"({100 * p['hbm_frac']:.1f}% of HBM)")
         per_shape.append(p)
@@ -680,6 +682,11 @@ def decode_leg(N, path, dtype, cpu: bool):
                       f"reference's test generator) re-encoded to {fmt} on load, 32-token prompt, 128 greedy tokens",
                tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
                prefill_s=round(tp, 4), kernels_per_token=4)
+    # The matmul-only ceiling: every weight read once per token at the HBM
+    # datasheet rate (the layers' matrices and the tied lm_head).
+    wpt = sum(weight_bytes(dtype, r, c) for r, c in m.shapes)
+    out.update(weight_bytes_per_token=wpt, matmul_ceiling_tok_s=round(HBM_PEAK_GBS * 1e9 / wpt, 1),
+               frac_of_ceiling=round(out["tok_s"] * wpt / (HBM_PEAK_GBS * 1e9), 4))
     log(f"gemma3-1b device decode ({fmt}): {out['tok_s']} tok/s")
     if cpu:
         from oracle import oracle as O  # the CPU baseline leg only
