@@ -675,6 +675,21 @@ __device__ bool residual_norms(const PkArgs& a, int tid, const float* in, float 
     return ok;
 }
 
+// The Q4 block sums of a phase's input are formed by the compute waves
+// right before their rows, each wave announcing its share on an LDS counter
+// (`bs.ctr`); a row waits for all of them only before its bias term, so the
+// row chains run while the other waves finish the sums (no barrier between).
+struct BsumWait {
+    int* ctr;   // arrivals of the compute waves so far (all passes)
+    int want;   // arrivals that complete this pass's sums
+    int* abort;
+};
+__device__ __forceinline__ void bsum_wait(const BsumWait& bs, bool& ready) {
+    if (ready) return;
+    if (!lds_wait_ge(bs.ctr, bs.want, bs.abort)) *bs.abort = 1;
+    ready = true;
+}
+
 // A phase's rows (nrows of matrix geometry m, weights w / scales sc / Q4
 // bias rows bi (null: Q8_0) in LDS, input x and its block sums xs in LDS),
 // NB: the rows' block count when known at compile time. A Q4 row is
@@ -682,23 +697,32 @@ __device__ bool residual_norms(const PkArgs& a, int tid, const float* in, float 
 template <int NB>
 __device__ __forceinline__ void rows32(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const uint16_t* bi,
                                        const float* xs, const float* x, int nrows, uint64_t* out, uint32_t tag,
-                                       int tid) {
+                                       int tid, const BsumWait& bs) {
     const int nb = NB ? NB : m.nb;
     const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
+    bool ready = false;
     for (int slot = tid >> 5; slot < nrows; slot += PK_CW / 32) {
         float v = row32(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 31);
-        if (bi) v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
+        if (bi) {
+            bsum_wait(bs, ready);
+            v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
+        }
         if ((tid & 31) == 0) tstore(out + slot, v, tag);
     }
 }
 template <int NB>
 __device__ __forceinline__ void rows16(const F32Mat& m, const uint8_t* w, const uint8_t* sc, const uint16_t* bi,
-                                       const float* xs, const float* x, int nrows, float* res, int tid) {
+                                       const float* xs, const float* x, int nrows, float* res, int tid,
+                                       const BsumWait& bs) {
     const int nb = NB ? NB : m.nb;
     const uint32_t qb = NB ? (uint32_t)((NB + 7) / 8) * 256 : qrow_bytes(m), sb = srow_bytes(m);
+    bool ready = false;
     for (int slot = tid >> 4; slot < nrows; slot += PK_CW / 16) {
         float v = row16(w + slot * qb, (const uint16_t*)(sc + slot * sb), x, nb, tid & 15);
-        if (bi) v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
+        if (bi) {
+            bsum_wait(bs, ready);
+            v = __fadd_rn(v, bias_dot(bi + slot * brow_elems(nb), xs, nb, tid & 7));
+        }
         if ((tid & 15) == 0) res[slot] = v;
     }
 }
@@ -726,6 +750,7 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
     int* PCTR = (int*)(BC + 2);    // the compute waves' barrier
     int* FREED = (int*)(BC + 4);   // [3] layers consumed of the q / k / v, o, gate / up + down regions
     int* LANDED = (int*)(BC + 8);  // [4] loader-wave copies landed of q / k / v, o, gate / up, down
+    int* BSUM = (int*)(BC + 12);   // Q4: compute waves done with the pass's block sums
     float* H = (float*)(lds + g.h);
     float* IN = (float*)(lds + g.in);
     float* XS = (float*)(lds + g.xs);  // Q4: the block sums of the phase's input
@@ -844,8 +869,10 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
         }
         if (Q4) {
             block_sums_lds(ph == 3 ? H : Y, (ph == 1 ? a.QD : ph == 3 ? a.F : E) / 32, XS, tid);
-            if (!pbar(PCTR, pgen)) *ABORT = 1;
+            __builtin_amdgcn_s_waitcnt(NNH_LGKMCNT0);
+            if (lane == 0) __hip_atomic_fetch_add(BSUM, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+        const BsumWait bs{BSUM, (PK_CW / 64) * (it + 1), ABORT};
         // ---- the rows: 32 lanes per row (one chain each) where there are
         // few rows, 16 lanes (two chains each) for gate / up; one call site
         // per matrix shape, so a known block count unrolls.
@@ -857,13 +884,13 @@ __device__ __forceinline__ void matmul_wg(const PkArgs& a, uint8_t* lds, uint32_
                                                                          : g.db))
                                       : nullptr;
             if (ph == 2)
-                rows16<NBE>(a.geo[2], lds + g.fw, lds + g.fs, bi, XS, Y, nrows, RES, tid);
+                rows16<NBE>(a.geo[2], lds + g.fw, lds + g.fs, bi, XS, Y, nrows, RES, tid, bs);
             else if (ph == 0)
-                rows32<NBE>(a.geo[0], lds + g.qw, lds + g.qs, bi, XS, Y, nrows, a.t_qkv + q0, tag, tid);
+                rows32<NBE>(a.geo[0], lds + g.qw, lds + g.qs, bi, XS, Y, nrows, a.t_qkv + q0, tag, tid, bs);
             else if (ph == 1)
-                rows32<NBQ>(a.geo[1], lds + g.ow, lds + g.os, bi, XS, Y, nrows, a.t_o + o0, tag, tid);
+                rows32<NBQ>(a.geo[1], lds + g.ow, lds + g.os, bi, XS, Y, nrows, a.t_o + o0, tag, tid, bs);
             else
-                rows32<NBF>(a.geo[3], lds + g.dw, lds + g.ds, bi, XS, H, nrows, a.t_down + d0, tag, tid);
+                rows32<NBF>(a.geo[3], lds + g.dw, lds + g.ds, bi, XS, H, nrows, a.t_down + d0, tag, tid, bs);
         }
         if (!pbar(PCTR, pgen)) *ABORT = 1;
         // The region is free for the next layer's copies (gate / up only
