@@ -171,6 +171,10 @@ __device__ __forceinline__ int m1w_stride(int nb) {
     const int s = (nb + 3) & ~3;  // 16-byte rows; an odd number of 16-byte units spreads the banks
     return (s & 4) ? s : s + 4;
 }
+inline int m1w_stride_host(int nb) {
+    const int s = (nb + 3) & ~3;
+    return (s & 4) ? s : s + 4;
+}
 // Position of x[32 b + c] in the transposed copy.
 __device__ __forceinline__ int m1w_xpos(int b, int c, int S) { return c * S + b; }
 

@@ -639,6 +639,168 @@ __global__ __launch_bounds__(M1S_NT) void gemv_f32_m1s_kernel(F32Mat m, const fl
     if (2 * wave + (lane >> 5) < nr && j == 0) y[row0 + 2 * wave + (lane >> 5)] = res;
 }
 
+// The streamed kernel (long rows, many of them): 32 lanes per row, lane j
+// running chain j alone (M1Wide's arithmetic on the same 16-lane layout),
+// every wave computing two rows; a workgroup takes NT / 32 consecutive rows.
+// x is staged once per workgroup, transposed (m1w_xpos: a lane's x values
+// for 4 consecutive blocks are one 16-byte LDS read), with the Q4 block sums
+// of x. Each lane streams its row's groups straight from global memory into
+// a ring of PF register slots (the quant piece and the group's BF16 scales,
+// the scale loads the same address across the row's 32 lanes), so PF
+// groups are always in flight behind the arithmetic; the staged kernel's
+// LDS copies of every row are not needed. The lane's byte (Q8) or nibble
+// (Q4) of each pair is brought to fixed positions once per group.
+constexpr int M1R_MIN_ROWS = 2048;  // fills the GPU at 32 lanes per row
+
+template <int DT>
+struct M1rSlot {  // one group in flight
+    static constexpr int G = DT == 1 ? 8 : 16;
+    uint4 q;          // the lane's 16-byte piece of the group
+    uint4 s[G / 8];   // the group's BF16 scales
+};
+
+// One group of the lane's chain: blocks 0 .. nblk - 1 (all G when FULL) of
+// the slot, x from the transposed LDS copy (xg: the lane's x at the group's
+// first block). The lane's byte (Q8) / nibble (Q4) of each pair is brought
+// to fixed byte positions once per group.
+template <int DT, bool FULL>
+__device__ __forceinline__ void m1r_group(const M1rSlot<DT>& sl, const float* xg, int h, int nblk, float& a) {
+    constexpr int G = DT == 1 ? 8 : 16;
+    uint32_t qd[4] = {sl.q.x, sl.q.y, sl.q.z, sl.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        qd[k] = DT == 1 ? qd[k] >> (8 * h) : (qd[k] >> (4 * h)) & 0x0f0f0f0fu;
+        // Opaque to the compiler: it would fold the mask into a bit-field
+        // extract per block instead of converting the bytes directly.
+        if (DT == 2) asm volatile("" : "+v"(qd[k]));
+    }
+    float xv[G];
+#pragma unroll
+    for (int i = 0; i < G; i += 4) {
+        if (FULL || i < nblk) {
+            const float4 v = *(const float4*)(xg + i);
+            xv[i] = v.x, xv[i + 1] = v.y, xv[i + 2] = v.z, xv[i + 3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        if (FULL || i < nblk) {
+            const float sb = bf16f(half_of(sl.s[i / 8], i % 8));
+            float w;
+            if (DT == 1)
+                w = (float)(int8_t)((qd[i >> 1] >> (16 * (i & 1))) & 0xffu);
+            else
+                w = (float)((qd[i >> 2] >> (8 * (i & 3))) & 0xffu);
+            a = __builtin_fmaf(w * sb, xv[i], a);
+        }
+    }
+}
+
+template <int DT, int NT, int M1R_PF>
+__global__ __launch_bounds__(NT) void gemv_f32_m1r_kernel(F32Mat m, const float* __restrict__ x,
+                                                         float* __restrict__ y) {
+    constexpr int G = DT == 1 ? 8 : 16;
+    constexpr int RPW = NT / 32;  // rows per workgroup
+    extern __shared__ __align__(16) float xw[];
+    const int tid = threadIdx.x, nb = m.nb, S = m1w_stride(nb);
+    const int ngp = m1_groups(DT, nb), ng = nb / G;
+    float* xs = xw + 32 * S;
+    const int row0 = blockIdx.x * RPW;
+    const int rraw = row0 + (tid >> 5);
+    const int row = rraw < m.rows ? rraw : m.rows - 1;
+    const int j = tid & 31, h = j >> 4;
+
+    // The first PF groups of the row first, so they are in flight while x
+    // is staged.
+    const uint8_t* qrow = m.fq + (size_t)row * ngp * 256 + (j & 15) * 16;
+    const uint16_t* srow = m.fs + (size_t)row * m.nbp;
+    M1rSlot<DT> slot[M1R_PF];
+#pragma unroll
+    for (int d = 0; d < M1R_PF; ++d) {
+        const int g = d < ngp ? d : ngp - 1;
+        slot[d].q = load_nt16u(qrow + (size_t)g * 256);
+#pragma unroll
+        for (int k = 0; k < G / 8; ++k) slot[d].s[k] = *(const uint4*)(srow + g * G + 8 * k);
+    }
+    // x in 16-byte pieces, four pieces' loads in flight per thread before
+    // their LDS stores (x is 16-byte aligned: checked by the launcher).
+    const float4* x4 = (const float4*)x;
+    const int nf = nb * 8;
+    for (int f0 = tid; f0 < nf; f0 += 4 * NT) {
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int f = f0 + k * NT;
+            v[k] = x4[f < nf ? f : nf - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int f = f0 + k * NT;
+            if (f < nf) {
+                const int b = f >> 3, c = 4 * (f & 7);
+                xw[m1w_xpos(b, c, S)] = v[k].x;
+                xw[m1w_xpos(b, c + 1, S)] = v[k].y;
+                xw[m1w_xpos(b, c + 2, S)] = v[k].z;
+                xw[m1w_xpos(b, c + 3, S)] = v[k].w;
+            }
+        }
+    }
+    if (DT == 2) {
+        for (int b = tid; b < nb; b += NT) {
+            float c[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 v = x4[8 * b + k];
+                c[4 * k] = v.x, c[4 * k + 1] = v.y, c[4 * k + 2] = v.z, c[4 * k + 3] = v.w;
+            }
+            xs[b] = m1_block_sum(c);
+        }
+    }
+    __syncthreads();
+
+    const float* xp = xw + j * S;
+    float a = 0.0f;
+    // Groups in order, group g in slot g % PF. Whole rounds of PF whole
+    // groups run straight-line, each slot refilled with the group PF ahead
+    // right after its arithmetic (clamped to the row's last group, so the
+    // refill needs no branch; a few repeated loads at the row's end are never
+    // used); the rest of the row follows from the slots as they are.
+    int g = 0;
+    for (; g + M1R_PF <= ng; g += M1R_PF) {
+#pragma unroll
+        for (int d = 0; d < M1R_PF; ++d) {
+            m1r_group<DT, true>(slot[d], xp + (g + d) * G, h, G, a);
+            const int gn = min(g + d + M1R_PF, ngp - 1);
+            slot[d].q = load_nt16u(qrow + (size_t)gn * 256);
+#pragma unroll
+            for (int k = 0; k < G / 8; ++k) slot[d].s[k] = *(const uint4*)(srow + gn * G + 8 * k);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < M1R_PF; ++d) {
+        if (g + d < ng)
+            m1r_group<DT, true>(slot[d], xp + (g + d) * G, h, G, a);
+        else if (g + d == ng && ng < ngp)
+            m1r_group<DT, false>(slot[d], xp + (g + d) * G, h, nb - ng * G, a);
+    }
+    // v[l] = (acc_l + acc_{8+l}) + (acc_{16+l} + acc_{24+l}) by xor-8, xor-16,
+    // then hsum8 by xor-4, xor-1, xor-2 (valid at lane 0 of the row).
+    const float u = __fadd_rn(a, xor_get(a, 8));
+    const float v = __fadd_rn(u, xor_get(u, 16));
+    const float p = __fadd_rn(v, xor_get(v, 4));
+    const float q = __fadd_rn(p, xor_get(p, 1));
+    float res = __fadd_rn(q, xor_get(q, 2));
+    if (DT == 2) res = __fadd_rn(res, m1_bias_dot(m.bi + (size_t)row * nb, xs, nb, j));
+    if (rraw < m.rows && j == 0) y[rraw] = res;
+}
+
+// The streamed kernel's conditions: enough rows to fill the GPU at 32 lanes
+// per row, x (staged whole in LDS) at most 64 KB and 16-byte aligned.
+static bool m1r_fits(int rows, int nb, const float* x) {
+    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && (size_t)nb * 32 * 4 <= (size_t)F32_V2_MAX_LDS &&
+           ((uintptr_t)x & 15) == 0;
+}
+
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
 // 16-lane kernel, 8, 16 or 32 (Q4: up to 16) for the wide one.
 template <int DT>
@@ -648,6 +810,19 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
     const int ngp = DT == 1 ? (nb + 7) / 8 : (nb + 15) / 16;
     const size_t q4 = DT == 2 ? (size_t)nb * 4 : 0;
     const dim3 block(256);
+    if (m1r_fits(rows, nb, x)) {
+        // Many long rows: the streamed kernel, 16 rows per workgroup (8
+        // waves) when that still gives a workgroup per CU, else 8.
+        const size_t lds = (size_t)32 * m1w_stride_host(nb) * 4 + (DT == 2 ? (size_t)nb * 4 : 0);
+        // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8,
+        // the fastest of 2..8 at Llama's shapes.
+        constexpr int PF = DT == 1 ? 6 : 3;
+        if (rows >= 16 * cu_count())
+            gemv_f32_m1r_kernel<DT, 512, PF><<<dim3(ceil_div(rows, 16)), dim3(512), lds, st>>>(m, x, y);
+        else
+            gemv_f32_m1r_kernel<DT, 256, PF><<<dim3(ceil_div(rows, 8)), dim3(256), lds, st>>>(m, x, y);
+        return;
+    }
     if (nb >= M1W_MIN_NB) {
         // About one workgroup per CU, at most M1S_ROWS rows each.
         const int nwg = std::max(std::min(rows, cu_count()), ceil_div(rows, M1S_ROWS));
@@ -971,7 +1146,8 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
                      size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st) {
     // Q4 block sums, except for the one-vector kernel, which forms its own.
-    if (dtype == 2 && !(n_tok == 1 && !v2 && nb <= M1_MAX_NB)) launch_block_sums(x, x_stride, nb, n_tok, xsum, st);
+    const auto one = [&](const float* xt) { return !v2 && (nb <= M1_MAX_NB || m1r_fits(rows, nb, xt)); };
+    if (dtype == 2 && !(n_tok == 1 && one(x))) launch_block_sums(x, x_stride, nb, n_tok, xsum, st);
     // The 8-lane kernel keeps x in LDS: at most 64 KB of it per launch.
     int per = 4;
     if (v2 && per * nb * 32 * 4 > F32_V2_MAX_LDS) per = F32_V2_MAX_LDS / (nb * 32 * 4);
@@ -980,7 +1156,7 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
         const float* xt = x + (size_t)t0 * x_stride;
         const float* st_xsum = xsum ? xsum + (size_t)t0 * nb : nullptr;
         float* yt = y + (size_t)t0 * y_stride;
-        if (m == 1 && !v2 && nb <= M1_MAX_NB) {
+        if (m == 1 && one(xt)) {
             if (dtype == 1)
                 launch_m1<1>(fq, fs, biases, xt, rows, nb, nbp, yt, st);
             else
