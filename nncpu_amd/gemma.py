@@ -32,7 +32,8 @@ class NngConfig(C.Structure):
     _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int), ("n_kv", C.c_int),
                 ("head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
                 ("rms_eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
-                ("attn_scale", C.c_float), ("window", C.c_int), ("swa_period", C.c_int), ("wtype", C.c_int)]
+                ("attn_scale", C.c_float), ("window", C.c_int), ("swa_period", C.c_int), ("wtype", C.c_int),
+                ("arch", C.c_int), ("rope_mode", C.c_int)]  # arch 0 Gemma-3, 1 Llama, 2 Qwen2; rope_mode 0 NeoX, 1 Norm
 
 
 class NngGpuCtx(C.Structure):

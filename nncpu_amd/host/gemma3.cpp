@@ -1,5 +1,6 @@
-// A Gemma-3 forward pass on the CPU whose every weight matmul goes through
-// a pluggable gemv (the reference's `gemv_batch` / `model_gemv` dispatch):
+// A Gemma-3 / Llama / Qwen2 forward pass on the CPU whose every weight
+// matmul goes through a pluggable gemv (the reference's `gemv_batch` /
+// `model_gemv` dispatch):
 // the decode and prefill caller of the quantized matmul, restated from
 // crates/nncpu/src/model/forward.rs:197-439 (attention), 719-841 (layer),
 // 848-965 (model_forward), 989-1011 (argmax), with the scalar non-matmul
@@ -80,6 +81,14 @@ float gelu_lane(float v) {
     return (0.5f * v) * (1.0f + t);
 }
 
+// scalar.rs:104-106: 1 / (1 + exp(0 - g)), a true divide.
+float sigmoid_lane(float g) { return 1.0f / (1.0f + exp_lane(0.0f - g)); }
+
+// scalar.rs:146-150: SiLU(gate) * up, in place in gate.
+void swiglu(float* gate, const float* up, size_t n) {
+    for (size_t i = 0; i < n; ++i) gate[i] = (gate[i] * sigmoid_lane(gate[i])) * up[i];
+}
+
 // scalar.rs:232-250: sum of squares, FMA lanes over whole 8-chunks, tail in f64.
 double sum_sq(const float* x, size_t n) {
     size_t body = n & ~(size_t)7;
@@ -103,24 +112,32 @@ void rmsnorm_gamma_multi(float* y, const float* x, size_t total, size_t dim, con
     }
 }
 
-// kernels/mod.rs:687-737: RoPE, NeoX pairing (lane i with i + n_rot/2).
-void rope_neox(float* x, size_t n_heads, size_t head_dim, size_t n_rot, float pos, float freq_base) {
+// kernels/mod.rs:687-737: RoPE over the first n_rot lanes of each head,
+// pairing lane i with i + n_rot/2 (NeoX) or lane 2i with 2i + 1 (Norm); the
+// angles pos * base^(-2i/n_rot) (the ratio accumulated in f32), divided by
+// the frequency factors ff when given; lanes past n_rot pass through.
+void rope(float* x, size_t n_heads, size_t head_dim, size_t n_rot, float pos, float freq_base, int mode,
+          const float* ff) {
+    if (n_rot == 0) return;
     size_t half = n_rot / 2;
     std::vector<float> cs(half), sn(half);
     float ratio = std::pow(freq_base, -2.0f / (float)n_rot);
     float inv = 1.0f;
     for (size_t i = 0; i < half; ++i) {
         float theta = pos * inv;
+        if (ff) theta /= ff[i];
         cs[i] = std::cos(theta);
         sn[i] = std::sin(theta);
         inv *= ratio;
     }
+    const size_t stride = mode == NNG_ROPE_NORM ? 2 : 1, partner = mode == NNG_ROPE_NORM ? 1 : half;
     for (size_t h = 0; h < n_heads; ++h) {
         float* xh = x + h * head_dim;
         for (size_t i = 0; i < half; ++i) {
-            float a = xh[i], b = xh[i + half];
-            xh[i] = cs[i] * a - sn[i] * b;
-            xh[i + half] = sn[i] * a + cs[i] * b;
+            const size_t p = i * stride;
+            float a = xh[p], b = xh[p + partner];
+            xh[p] = cs[i] * a - sn[i] * b;
+            xh[p + partner] = sn[i] * a + cs[i] * b;
         }
     }
 }
@@ -228,6 +245,8 @@ typedef int (*nng_argmax_fn)(void* ctx, const float* x, size_t* row);
 struct nng_model {
     nng_config c;
     std::vector<float> norms;          // per layer: attn, q, k, post_attn, ffn, post_ffw; then output
+    std::vector<float> bias;           // per layer: q, k, v projection biases (Qwen2), or empty
+    std::vector<float> rope_ff;        // RoPE frequency factors (head_dim / 2), or empty
     std::vector<uint8_t> token_embd;   // Q8_0 or Q4 split layout [n_vocab x n_embd] (the embedding table)
     nng_gemv_fn gemv;
     nng_argmax_fn argmax;
@@ -265,6 +284,24 @@ nng_model* nng_create(const nng_config* cfg, const float* norms, const void* tok
 }
 
 void nng_free(nng_model* m) { delete m; }
+
+// The q / k / v projection biases (Qwen2, forward.rs:255-272): per layer
+// [q_dim][kv_dim][kv_dim] floats, added to the projections before the
+// norms and RoPE.
+void nng_set_biases(nng_model* m, const float* b) {
+    const nng_config& c = m->c;
+    const size_t per = (size_t)(c.n_head + 2 * c.n_kv) * c.head_dim;
+    m->bias.assign(b, b + per * c.n_layer);
+}
+
+// RoPE frequency factors (head_dim / 2 floats; Llama 3's long-context
+// scaling, load.rs:760-769), or NULL for none.
+void nng_set_rope_freqs(nng_model* m, const float* ff) {
+    if (ff)
+        m->rope_ff.assign(ff, ff + m->c.head_dim / 2);
+    else
+        m->rope_ff.clear();
+}
 const char* nng_error(nng_model* m) { return m->err.c_str(); }
 
 static uint64_t fnv(const float* v, size_t n) {
@@ -330,8 +367,10 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
     m->part.assign(group * pw, 0.0f);
     m->acc.assign(group * pw, 0.0f);
 
-    // Embedding rows times sqrt(n_embd) (load.rs:565-566).
-    const float embd_scale = std::sqrt((float)E);
+    // Embedding rows times sqrt(n_embd) for Gemma, else 1 (load.rs:565-566).
+    const bool gemma = c.arch == NNG_GEMMA3;
+    const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
+    const float* ff = m->rope_ff.empty() ? nullptr : m->rope_ff.data();
     for (size_t t = 0; t < n_tok; ++t) {
         if (tokens[t] < 0 || tokens[t] >= c.n_vocab) {
             m->err = "token outside the vocabulary";
@@ -356,13 +395,23 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
             m->err = "gemv failed";
             return 1;
         }
-        rmsnorm_gamma_multi(m->q.data(), m->q.data(), n_tok * q_dim, hd, q_norm, c.rms_eps);
-        rmsnorm_gamma_multi(m->k.data(), m->k.data(), n_tok * kv_dim, hd, k_norm, c.rms_eps);
+        if (!m->bias.empty()) {  // forward.rs:255-272
+            const float* bl = m->bias.data() + (q_dim + 2 * kv_dim) * li;
+            for (size_t t = 0; t < n_tok; ++t) {
+                for (size_t i = 0; i < q_dim; ++i) m->q[t * q_dim + i] += bl[i];
+                for (size_t i = 0; i < kv_dim; ++i) m->k[t * kv_dim + i] += bl[q_dim + i];
+                for (size_t i = 0; i < kv_dim; ++i) m->v[t * kv_dim + i] += bl[q_dim + kv_dim + i];
+            }
+        }
+        if (gemma) {
+            rmsnorm_gamma_multi(m->q.data(), m->q.data(), n_tok * q_dim, hd, q_norm, c.rms_eps);
+            rmsnorm_gamma_multi(m->k.data(), m->k.data(), n_tok * kv_dim, hd, k_norm, c.rms_eps);
+        }
         const float freq = sliding ? c.rope_base_swa : c.rope_base;
         for (size_t t = 0; t < n_tok; ++t) {
             float rpos = (float)(pos0 + t);
-            rope_neox(m->q.data() + t * q_dim, H, hd, hd, rpos, freq);
-            rope_neox(m->k.data() + t * kv_dim, KV, hd, hd, rpos, freq);
+            rope(m->q.data() + t * q_dim, H, hd, hd, rpos, freq, c.rope_mode, ff);
+            rope(m->k.data() + t * kv_dim, KV, hd, hd, rpos, freq, c.rope_mode, ff);
         }
         // Append K/V as BF16 (forward.rs:326-351); rows = n_ctx, no ring wrap below n_ctx.
         uint16_t* kc = m->kcache.data() + (size_t)li * c.n_ctx * kv_dim;
@@ -394,21 +443,25 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
             m->err = "gemv failed";
             return 1;
         }
-        rmsnorm_gamma_multi(m->normed.data(), m->normed.data(), n_tok * E, E, post_attn, c.rms_eps);
+        if (gemma) rmsnorm_gamma_multi(m->normed.data(), m->normed.data(), n_tok * E, E, post_attn, c.rms_eps);
         for (size_t i = 0; i < n_tok * E; ++i) m->x[i] += m->normed[i];
-        // MLP block: gelu(gate) * up, then down (forward.rs:755-803).
+        // MLP block: gelu(gate) * up (Gemma) or silu(gate) * up, then down
+        // (forward.rs:755-803).
         rmsnorm_gamma_multi(m->normed.data(), m->x.data(), n_tok * E, E, ffn_norm, c.rms_eps);
         if (m->gemv(m->ctx, id + 4, m->normed.data(), E, m->gate.data(), F, n_tok) ||
             m->gemv(m->ctx, id + 5, m->normed.data(), E, m->up.data(), F, n_tok)) {
             m->err = "gemv failed";
             return 1;
         }
-        for (size_t i = 0; i < n_tok * F; ++i) m->gate[i] = gelu_lane(m->gate[i]) * m->up[i];
+        if (gemma)
+            for (size_t i = 0; i < n_tok * F; ++i) m->gate[i] = gelu_lane(m->gate[i]) * m->up[i];
+        else
+            swiglu(m->gate.data(), m->up.data(), n_tok * F);
         if (m->gemv(m->ctx, id + 6, m->gate.data(), F, m->normed.data(), E, n_tok)) {
             m->err = "gemv failed";
             return 1;
         }
-        rmsnorm_gamma_multi(m->normed.data(), m->normed.data(), n_tok * E, E, post_ffw, c.rms_eps);
+        if (gemma) rmsnorm_gamma_multi(m->normed.data(), m->normed.data(), n_tok * E, E, post_ffw, c.rms_eps);
         for (size_t i = 0; i < n_tok * E; ++i) m->x[i] += m->normed[i];
         m->layer_hash.push_back(fnv(m->x.data() + (n_tok - 1) * E, E));
     }
@@ -541,8 +594,17 @@ void nng_op_rmsnorm_gamma(float* y, const float* x, size_t total, size_t dim, co
 }
 
 void nng_op_rope_neox(float* x, size_t n_heads, size_t head_dim, size_t n_rot, float pos, float freq_base) {
-    rope_neox(x, n_heads, head_dim, n_rot, pos, freq_base);
+    rope(x, n_heads, head_dim, n_rot, pos, freq_base, NNG_ROPE_NEOX, nullptr);
 }
+
+// mode: NNG_ROPE_NEOX or NNG_ROPE_NORM; ff: n_rot / 2 frequency factors or NULL.
+void nng_op_rope(float* x, size_t n_heads, size_t head_dim, size_t n_rot, float pos, float freq_base, int mode,
+                 const float* ff) {
+    rope(x, n_heads, head_dim, n_rot, pos, freq_base, mode, ff);
+}
+
+// SiLU(gate) * up, in place in gate (the Llama / Qwen MLP step).
+void nng_op_swiglu(float* gate, const float* up, size_t n) { swiglu(gate, up, n); }
 
 // n_keys <= 256 (one block); scores holds n_heads * n_keys floats, part
 // n_heads * (hd + 2).

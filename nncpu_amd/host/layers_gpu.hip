@@ -1,0 +1,767 @@
+// The forward of gemma3.cpp (nng_forward: crates/nncpu/src/model/forward.rs
+// 197-439 attention, 719-841 layer, 848-965 model_forward) on the GPU, for
+// any number of tokens and any of its architectures (Gemma-3, Llama,
+// Qwen2): every weight matmul through the library (nnh_gemv_batch_dev, in
+// any activation mode), everything between the matmuls as the kernels
+// below, each value computed by the CPU restatement's operations in its
+// order and rounding (-ffp-contract=off; __f*_rn where it matters). With
+// the bit-exact f32 matmul the hidden states, the K/V cache and the tokens
+// equal the CPU forward's bit for bit; with an int8 mode the matmuls carry
+// that mode's tolerance and the rest is still the CPU's arithmetic.
+//
+// Per layer, on one stream (activations [token][dim], f32):
+//   qkv         = W_qkv normed (one fused matrix, or q, k, v into column
+//                 ranges of one buffer)
+//   qkv_post    biases (Qwen2), per-head q / k RMSNorm (Gemma), RoPE from a
+//               host table per position, K / V rows appended to the BF16
+//               cache, q kept in place
+//   attn_part   a partial (o, m, l) per (token, KV head, 256-key block): the
+//               scores as 8-lane FMA chains, the block's first maximum,
+//               exp_lane weights and their 8-lane sum, the V rows' weighted
+//               sum (scalar.rs:444-519)
+//   attn_merge  the partials merged in block order with glibc's expf, each
+//               head's output divided by its weight sum (scalar.rs:521-548)
+//   r           = W_o attn
+//   resid_norm  x += post_attention_norm(r) (Gemma) or r; normed = ffn_norm(x)
+//   gu          = [W_gate; W_up] normed (fused, or gate and up into halves)
+//   act         gate = gelu(gate) * up (Gemma) or silu(gate) * up, in place
+//   r           = W_down gate
+//   resid_norm  x += post_ffw_norm(r) or r, the last token's x recorded as
+//               the layer's state; normed = the next layer's attn_norm(x),
+//               after the last layer x = output_norm(x)
+// The sums of squares of the norms are the CPU's 8 FMA lanes over whole
+// 8-chunks (one lane each), hsum8 and an f64 tail; the norm scale is f64.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gemma3.h"
+#include "nncpu_hip.h"
+#include "ops_dev.h"
+
+namespace {
+
+constexpr int ATTN_BLOCK = 256;  // model/mod.rs:84-87
+constexpr int LDS_MAX = 160 * 1024;
+
+// hsum8 of lanes 0..7's values (valid at lane 0 of each aligned group of 8):
+// xor-4 gives v_l + v_{l+4}, xor-1 and xor-2 then add those pairs as hsum8 does.
+__device__ __forceinline__ float hsum8_lanes(float a) {
+    const float p = __fadd_rn(a, __shfl_xor(a, 4, 64));
+    const float q = __fadd_rn(p, __shfl_xor(p, 1, 64));
+    return __fadd_rn(q, __shfl_xor(q, 2, 64));
+}
+
+__device__ __forceinline__ float hsum8(const float* a) {
+    return __fadd_rn(__fadd_rn(__fadd_rn(a[0], a[4]), __fadd_rn(a[1], a[5])),
+                     __fadd_rn(__fadd_rn(a[2], a[6]), __fadd_rn(a[3], a[7])));
+}
+
+// sum_sq (scalar.rs:232-250) of v[0..dim) (LDS), run by one wave: lanes
+// 0..7 each run FMA lane l over the whole 8-chunks in order, hsum8, then
+// the tail in f64. The result (a double) is returned to every lane.
+__device__ double row_sumsq(const float* v, int dim, int lane) {
+    const int body = dim & ~7;
+    float a = 0.0f;
+    if (lane < 8) {
+        int i = lane;
+        for (; i + 56 < body; i += 64) {
+            float t[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t[k] = v[i + 8 * k];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) a = __fmaf_rn(t[k], t[k], a);
+        }
+        for (; i < body; i += 8) a = __fmaf_rn(v[i], v[i], a);
+    }
+    const float h = hsum8_lanes(a);
+    double s = dim >= 8 ? (double)__shfl(h, 0, 64) : 0.0;
+    for (int i = body; i < dim; ++i) s = __dadd_rn(s, __dmul_rn((double)v[i], (double)v[i]));
+    return s;
+}
+
+// Embedding rows (gemma3.cpp embed_row, kernels/mod.rs:917-954): token t's
+// row of the split-layout table times `scale` into x[t].
+__global__ void embed_kernel(const int32_t* __restrict__ tok, const uint8_t* __restrict__ table, int wtype,
+                             int n_vocab, int E, float scale, float* __restrict__ x) {
+    const int t = blockIdx.x;
+    int id = tok[t];
+    id = id < 0 ? 0 : (id >= n_vocab ? n_vocab - 1 : id);  // the host checks; a device caller gets a clamp
+    const size_t te = (size_t)n_vocab * E, nbe = E / 32;
+    float* y = x + (size_t)t * E;
+    for (int i = threadIdx.x; i < E; i += blockDim.x) {
+        const int b = i >> 5, k = i & 31;
+        if (wtype == 2) {
+            const uint8_t* tq = table + (size_t)id * (E / 2);
+            const uint16_t* ts = (const uint16_t*)(table + te / 2) + (size_t)id * nbe;
+            const uint16_t* tb = (const uint16_t*)(table + te / 2 + te / 16) + (size_t)id * nbe;
+            const float s = __fmul_rn(bf16f(ts[b]), scale), bias = __fmul_rn(bf16f(tb[b]), scale);
+            const uint8_t q = tq[16 * b + (k & 15)];
+            y[i] = __fadd_rn(__fmul_rn(s, (float)(k < 16 ? q & 15 : q >> 4)), bias);
+        } else {
+            const int8_t* tq = (const int8_t*)table + (size_t)id * E;
+            const uint16_t* ts = (const uint16_t*)(table + te) + (size_t)id * nbe;
+            y[i] = __fmul_rn((float)tq[i], __fmul_rn(bf16f(ts[b]), scale));
+        }
+    }
+}
+
+// One wave per row (dim <= 8192):
+//   r == NULL: y = rmsnorm(x) * gamma (y may be x);
+//   else: x += (post ? rmsnorm(r) * post : r), written back, the last row's
+//   new x copied to rec (if not NULL), then y = rmsnorm(x) * gamma (y may be x).
+// rmsnorm_gamma_multi (scalar.rs:270-292): y = (x * scale) * gamma.
+__global__ __launch_bounds__(64) void resid_norm_kernel(float* x, const float* __restrict__ r,
+                                                        const float* __restrict__ post, const float* gamma,
+                                                        float* y, float* __restrict__ rec, int n_rows, int dim,
+                                                        float eps) {
+    extern __shared__ float lds[];
+    float* v = lds;         // the row being normed
+    float* w = lds + dim;   // r, when it is normed first
+    const int row = blockIdx.x, lane = threadIdx.x;
+    float* xr = x + (size_t)row * dim;
+    if (r) {
+        const float* rr = r + (size_t)row * dim;
+        if (post) {
+            for (int i = lane; i < dim; i += 64) w[i] = rr[i];
+            __syncthreads();
+            const float sc = rms_of_d(row_sumsq(w, dim, lane), dim, eps);
+            for (int i = lane; i < dim; i += 64) {
+                const float nv = __fadd_rn(xr[i], __fmul_rn(__fmul_rn(w[i], sc), post[i]));
+                v[i] = nv;
+                xr[i] = nv;
+            }
+        } else {
+            for (int i = lane; i < dim; i += 64) {
+                const float nv = __fadd_rn(xr[i], rr[i]);
+                v[i] = nv;
+                xr[i] = nv;
+            }
+        }
+        if (rec && row == n_rows - 1)
+            for (int i = lane; i < dim; i += 64) rec[i] = v[i];
+    } else {
+        for (int i = lane; i < dim; i += 64) v[i] = xr[i];
+    }
+    __syncthreads();
+    const float sc = rms_of_d(row_sumsq(v, dim, lane), dim, eps);
+    float* yr = y + (size_t)row * dim;
+    for (int i = lane; i < dim; i += 64) yr[i] = __fmul_rn(__fmul_rn(v[i], sc), gamma[i]);
+}
+
+struct QkvArgs {
+    float* qkv;              // [n_tok][QKV]: q, k, v
+    const float* bias;       // [QKV] of this layer, or NULL
+    const float* qn;         // per-head q / k RMSNorm gammas (Gemma), or NULL
+    const float* kn;
+    const float* cs;         // RoPE table of this layer's base: [n_ctx][hd / 2]
+    const float* sn;
+    uint16_t* kc;            // this layer's cache rows: [n_ctx][KVD]
+    uint16_t* vc;
+    int H, KV, hd, QKV, pos0, rope_mode;
+    float eps;
+};
+
+// One wave per (token, head slot): q heads, then k heads, then v heads
+// (forward.rs:255-351 for one head's values, in the CPU restatement's order:
+// bias, norm, RoPE, then the BF16 append).
+__global__ __launch_bounds__(64) void qkv_post_kernel(QkvArgs a) {
+    extern __shared__ float v[];
+    const int t = blockIdx.x, s = blockIdx.y, lane = threadIdx.x, hd = a.hd;
+    const int kind = s < a.H ? 0 : (s < a.H + a.KV ? 1 : 2), head = kind == 0 ? s : (kind == 1 ? s - a.H : s - a.H - a.KV);
+    const int off = kind == 0 ? head * hd : a.H * hd + (kind - 1) * a.KV * hd + head * hd;
+    float* src = a.qkv + (size_t)t * a.QKV + off;
+    for (int i = lane; i < hd; i += 64) v[i] = a.bias ? __fadd_rn(src[i], a.bias[off + i]) : src[i];
+    __syncthreads();
+    if (kind < 2) {
+        const float* g = kind == 0 ? a.qn : a.kn;
+        if (g) {
+            const float sc = rms_of_d(row_sumsq(v, hd, lane), hd, a.eps);
+            __syncthreads();
+            for (int i = lane; i < hd; i += 64) v[i] = __fmul_rn(__fmul_rn(v[i], sc), g[i]);
+            __syncthreads();
+        }
+        const int half = hd / 2, pos = a.pos0 + t;
+        const int stride = a.rope_mode == NNG_ROPE_NORM ? 2 : 1, partner = a.rope_mode == NNG_ROPE_NORM ? 1 : half;
+        const float* cs = a.cs + (size_t)pos * half;
+        const float* sn = a.sn + (size_t)pos * half;
+        for (int i = lane; i < half; i += 64) {
+            const int p = i * stride;
+            const float x0 = v[p], x1 = v[p + partner], c = cs[i], sv = sn[i];
+            v[p] = __fsub_rn(__fmul_rn(c, x0), __fmul_rn(sv, x1));
+            v[p + partner] = __fadd_rn(__fmul_rn(sv, x0), __fmul_rn(c, x1));
+        }
+        __syncthreads();
+    }
+    if (kind == 0) {
+        for (int i = lane; i < hd; i += 64) src[i] = v[i];
+    } else {
+        uint16_t* dst = (kind == 1 ? a.kc : a.vc) + (size_t)(a.pos0 + t) * a.KV * hd + head * hd;
+        for (int i = lane; i < hd; i += 64) dst[i] = to_bf16(v[i]);
+    }
+}
+
+struct AttnArgs {
+    const float* qkv;        // q of every token at [t][QKV]
+    const uint16_t* kc;      // this layer's cache: [n_ctx][KVD] BF16
+    const uint16_t* vc;
+    float* parts;            // [n_tok][KV][nblk][G][hd + 2]
+    float* out;              // [n_tok][H * hd]
+    const uint64_t* expt;    // glibc_expf's table
+    int KV, G, hd, QKV, nblk, pos0, n_seq, window;
+    float scale;
+};
+
+// model/embed.rs:14-30, the causal branch (gemma3.cpp attn_span).
+__device__ __forceinline__ void attn_span(int window, int pos, int n_seq, int& first, int& last) {
+    const int end = n_seq ? n_seq - 1 : 0;
+    first = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+    last = pos < end ? pos : end;
+}
+
+// A partial of the heads sharing KV head y over block b0 + x of token z's
+// span (scalar.rs:444-519, gemma3.cpp attn_block). 256 threads; LDS: the
+// heads' queries, the block's K (then V) rows padded to hd + 8, the scores.
+__global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int t = blockIdx.z, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hd = a.hd, G = a.G, pw = hd + 2, KS = hd + 8, KVD = a.KV * hd, hd8 = hd & ~7;
+    int first, last;
+    attn_span(a.window, a.pos0 + t, a.n_seq, first, last);
+    const int b = first / ATTN_BLOCK + (int)blockIdx.x;
+    if (b > last / ATTN_BLOCK) return;
+    const int k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
+    const int k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
+    const int nk = k1 + 1 - k0;
+    float* qs = lds;                                  // [G][hd]
+    float* sc = qs + G * hd;                          // [G][256]
+    float* mh = sc + G * ATTN_BLOCK;                  // [G]
+    uint16_t* kv = (uint16_t*)(mh + ((G + 3) & ~3));  // [256][KS]
+    float* part = a.parts + ((((size_t)t * a.KV + kvh) * a.nblk) + blockIdx.x) * G * pw;
+
+    const float* q = a.qkv + (size_t)t * a.QKV + (size_t)kvh * G * hd;
+    for (int i = tid; i < G * hd; i += 256) qs[i] = q[i];
+    // K rows in 16-byte pieces (hd % 8 == 0).
+    const int pr = hd / 8;
+    for (int i = tid; i < nk * pr; i += 256) {
+        const int j = i / pr, c = i - j * pr;
+        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.kc + (size_t)(k0 + j) * KVD + kvh * hd + 8 * c);
+    }
+    __syncthreads();
+    // Scores: head h, key j; FMA lanes l = i % 8 over the whole 8-chunks,
+    // hsum8, the tail, times the scale.
+    for (int i = tid; i < G * nk; i += 256) {
+        const int h = i / nk, j = i - h * nk;
+        const float* qh = qs + h * hd;
+        const uint16_t* kr = kv + j * KS;
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < hd8; c += 8) {
+            const uint4 k8 = *(const uint4*)(kr + c);
+            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l)
+                acc[l] = __fmaf_rn(qh[c + l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
+        }
+        float s = hsum8(acc);
+        for (int c = hd8; c < hd; ++c) s = __fadd_rn(s, __fmul_rn(qh[c], bf16f(kr[c])));
+        sc[h * ATTN_BLOCK + j] = __fmul_rn(s, a.scale);
+    }
+    __syncthreads();
+    // Each head's maximum as `if m < v { m = v }` from s[0] finds it: the
+    // first largest, NaN never taken unless s[0] is NaN. Lane l scans keys
+    // 4l .. 4l + 3 from -inf, then the lanes' results combine in key order.
+    for (int h = wave; h < G; h += 4) {
+        const float* s = sc + h * ATTN_BLOCK;
+        float m = -INFINITY;
+        for (int j = 4 * lane; j < 4 * lane + 4 && j < nk; ++j)
+            if (m < s[j]) m = s[j];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float other = __shfl_xor(m, o, 64);
+            const float lo = (lane & o) ? other : m, hi = (lane & o) ? m : other;
+            m = lo < hi ? hi : lo;
+        }
+        if (lane == 0) mh[h] = s[0] != s[0] ? s[0] : m;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * nk; i += 256) {
+        const int h = i / nk, j = i - h * nk;
+        sc[h * ATTN_BLOCK + j] = exp_lane(__fsub_rn(sc[h * ATTN_BLOCK + j], mh[h]));
+    }
+    __syncthreads();
+    // The weights' sum: lane l of head h's group of 8 adds weights 8c + l
+    // over the whole 8-chunks, hsum8, then the tail in order.
+    {
+        const int h = tid >> 3, l = tid & 7, body = nk & ~7;
+        float vs = 0.0f;
+        if (h < G)
+            for (int j = l; j < body; j += 8) vs = __fadd_rn(vs, sc[h * ATTN_BLOCK + j]);
+        float ls = hsum8_lanes(vs);
+        if (h < G && l == 0) {
+            for (int j = body; j < nk; ++j) ls = __fadd_rn(ls, sc[h * ATTN_BLOCK + j]);
+            part[h * pw + hd] = mh[h];
+            part[h * pw + hd + 1] = ls;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < nk * pr; i += 256) {
+        const int j = i / pr, c = i - j * pr;
+        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.vc + (size_t)(k0 + j) * KVD + kvh * hd + 8 * c);
+    }
+    __syncthreads();
+    // o[h][i] over the keys in order: the first writes w * v, the rest FMA
+    // (the tail lanes past hd8: o + w * v). Four outputs per thread at once.
+    for (int base = tid; base < G * hd; base += 1024) {
+        float o[4];
+        int hh[4], ii[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = base + 256 * k < G * hd ? base + 256 * k : base;
+            hh[k] = idx / hd;
+            ii[k] = idx - hh[k] * hd;
+            o[k] = __fmul_rn(sc[hh[k] * ATTN_BLOCK], bf16f(kv[ii[k]]));
+        }
+        for (int j = 1; j < nk; ++j) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float wv = sc[hh[k] * ATTN_BLOCK + j], vv = bf16f(kv[j * KS + ii[k]]);
+                o[k] = ii[k] < hd8 ? __fmaf_rn(wv, vv, o[k]) : __fadd_rn(o[k], __fmul_rn(wv, vv));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (base + 256 * k < G * hd) part[hh[k] * pw + ii[k]] = o[k];
+    }
+}
+
+// The partials of token y's heads sharing KV head x merged in block order
+// (scalar.rs:521-537, with glibc's expf), then each head's o / l
+// (scalar.rs:539-548) into out[t][head * hd ..].
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    const int t = blockIdx.y, kvh = blockIdx.x, hd = a.hd, G = a.G, pw = hd + 2, hd8 = hd & ~7;
+    int first, last;
+    attn_span(a.window, a.pos0 + t, a.n_seq, first, last);
+    const int nb = last / ATTN_BLOCK - first / ATTN_BLOCK + 1;
+    const float* P = a.parts + ((size_t)t * a.KV + kvh) * a.nblk * G * pw;
+    for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
+        const int h = idx / hd, i = idx - h * hd;
+        float o = P[h * pw + i], am = P[h * pw + hd], al = P[h * pw + hd + 1];
+        for (int bi = 1; bi < nb; ++bi) {
+            const float* B = P + (size_t)bi * G * pw + h * pw;
+            const float bm = B[hd], bl = B[hd + 1];
+            const float m = am < bm ? bm : am;
+            const float ca = glibc_expf(__fsub_rn(am, m), a.expt), cb = glibc_expf(__fsub_rn(bm, m), a.expt);
+            o = i < hd8 ? __fmaf_rn(B[i], cb, __fmul_rn(o, ca)) : __fadd_rn(__fmul_rn(o, ca), __fmul_rn(B[i], cb));
+            am = m;
+            al = __fadd_rn(__fmul_rn(al, ca), __fmul_rn(bl, cb));
+        }
+        const float inv = al > 0.0f ? __fdiv_rn(1.0f, al) : 0.0f;
+        a.out[(size_t)t * (a.KV * G * hd) + (size_t)(kvh * G + h) * hd + i] = __fmul_rn(o, inv);
+    }
+}
+
+// gate = gelu(gate) * up (Gemma) or (gate * sigmoid(gate)) * up, gate and up
+// the halves of each token's row of gu [n_tok][2F] (scalar.rs:140-150).
+__global__ void act_kernel(float* __restrict__ gu, int F, int n_tok, int gelu) {
+    const size_t n = (size_t)n_tok * F;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = e / F, i = e - t * F;
+        float* g = gu + t * 2 * F + i;
+        const float u = g[F], gv = *g;
+        *g = gelu ? __fmul_rn(gelu_lane(gv), u) : __fmul_rn(__fmul_rn(gv, sigmoid_lane(gv)), u);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+struct nngl_model {
+    nng_config c;
+    std::vector<nnh_weight*> w;  // 7 * n_layer + 1, as nng_gemv_fn's ids; lm_head last
+    const nnh_weight* embd = nullptr;
+    const uint8_t* table = nullptr;  // the embedding table's split layout (device)
+    bool fused_qkv = false, fused_gu = false;
+    int act = NNH_ACT_F32, n_batch = 0, nblk = 0;
+    size_t pos = 0;
+    hipStream_t st = nullptr;
+    bool own_stream = false;
+    float *norms = nullptr, *bias = nullptr, *cs = nullptr, *sn = nullptr;
+    uint64_t* expt = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    float *x = nullptr, *normed = nullptr, *r = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr,
+          *parts = nullptr, *states = nullptr, *logits = nullptr;
+    int32_t* tok = nullptr;
+    int32_t* tok_host = nullptr;  // pinned staging of the host forward's token ids
+    void* work = nullptr;
+    uint64_t* row = nullptr;
+    size_t lds_attn = 0;
+    std::string err;
+};
+
+const char* nngl_error(nngl_model* m) { return m ? m->err.c_str() : "no model"; }
+
+void nngl_free(nngl_model* m) {
+    if (!m) return;
+    void* bufs[] = {m->norms, m->bias, m->cs,    m->sn,     m->expt,   m->kc,     m->vc,   m->x,   m->normed,
+                    m->r,     m->qkv,  m->attn, m->gu,     m->parts,  m->states, m->logits, m->tok, m->work, m->row};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->tok_host) (void)hipHostFree(m->tok_host);
+    if (m->own_stream && m->st) (void)hipStreamDestroy(m->st);
+    delete m;
+}
+
+static size_t norm_stride_l(const nng_config& c) { return 4 * (size_t)c.n_embd + 2 * (size_t)c.head_dim; }
+
+#define NNGL_CHECK(expr)                                                   \
+    do {                                                                   \
+        hipError_t e_ = (expr);                                            \
+        if (e_ != hipSuccess) {                                            \
+            m->err = std::string(#expr) + ": " + hipGetErrorString(e_);    \
+            return 1;                                                      \
+        }                                                                  \
+    } while (0)
+
+// RoPE tables as gemma3.cpp's rope forms the angles: ratio = pow(base,
+// -2 / n_rot) and inv *= ratio in f32, theta = pos * inv (/ ff[i]), then the
+// platform's cosf / sinf.
+static void rope_table_l(float base, int n_ctx, int hd, const float* ff, float* cs, float* sn) {
+    const int half = hd / 2;
+    const float ratio = std::pow(base, -2.0f / (float)hd);
+    for (int p = 0; p < n_ctx; ++p) {
+        float inv = 1.0f;
+        for (int i = 0; i < half; ++i) {
+            float theta = (float)p * inv;
+            if (ff) theta /= ff[i];
+            cs[(size_t)p * half + i] = std::cos(theta);
+            sn[(size_t)p * half + i] = std::sin(theta);
+            inv *= ratio;
+        }
+    }
+}
+
+// weights: 7 * n_layer + 1 handles with nng_gemv_fn's ids (7 l + {q, k, v,
+// o, gate, up, down}, the lm_head last); k and v NULL when q is the fused
+// [q; k; v] matrix, up NULL when gate is the fused [gate; up] matrix.
+// norms: nng_create's layout; biases: per layer [q_dim][kv_dim][kv_dim] or
+// NULL; rope_ff: head_dim / 2 RoPE frequency factors or NULL; token_embd:
+// the embedding table (may be the lm_head). n_batch: most tokens per
+// forward. act: the matmuls' activation mode. stream: a hipStream_t, or
+// NULL for a stream of the model's own.
+int nngl_create(const nng_config* cfg, const float* norms, const float* biases, const float* rope_ff,
+                nnh_weight* const* weights, int n_weights, const nnh_weight* token_embd, int n_batch, int act,
+                void* stream, nngl_model** out) {
+    nngl_model* m = new nngl_model();
+    *out = m;
+    m->c = *cfg;
+    const nng_config& c = m->c;
+    if (n_weights != 7 * c.n_layer + 1 || c.n_layer < 1 || c.n_kv < 1 || c.n_head % c.n_kv != 0 || n_batch < 1 ||
+        n_batch > c.n_ctx) {
+        m->err = "bad weight count, head grouping or batch";
+        return 1;
+    }
+    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, G = H / KV, F = c.n_ff;
+    if (E % 32 || E > 8192 || hd % 8 || hd > 512 || F % 32 || G > 32 || c.n_vocab < 1 || c.arch < NNG_GEMMA3 ||
+        c.arch > NNG_QWEN2) {
+        m->err = "n_embd and n_ff must be multiples of 32 (n_embd at most 8192), head_dim a multiple of 8 up to "
+                 "512, at most 32 query heads per KV head";
+        return 1;
+    }
+    const int QD = H * hd, KVD = KV * hd, QKV = QD + 2 * KVD;
+    m->w.assign(weights, weights + n_weights);
+    m->fused_qkv = !m->w[1] && !m->w[2];
+    m->fused_gu = !m->w[5];
+    for (int l = 0; l < c.n_layer; ++l) {
+        const bool fq = !m->w[7 * l + 1] && !m->w[7 * l + 2], fg = !m->w[7 * l + 5];
+        if (fq != m->fused_qkv || fg != m->fused_gu) {
+            m->err = "every layer must fuse q / k / v and gate / up alike";
+            return 1;
+        }
+        const int want[7][2] = {{m->fused_qkv ? QKV : QD, E}, {KVD, E}, {KVD, E}, {E, QD},
+                                {m->fused_gu ? 2 * F : F, E}, {F, E}, {E, F}};
+        for (int k = 0; k < 7; ++k) {
+            const nnh_weight* wk = m->w[7 * l + k];
+            if (!wk) {
+                if ((k == 1 || k == 2) && m->fused_qkv) continue;
+                if (k == 5 && m->fused_gu) continue;
+                m->err = "missing weight";
+                return 1;
+            }
+            int dt;
+            size_t rows, cols;
+            if (nnh_weight_info(wk, &dt, &rows, &cols) != NNH_OK || (int)rows != want[k][0] || (int)cols != want[k][1]) {
+                m->err = "layer " + std::to_string(l) + " matrix " + std::to_string(k) + ": shape mismatch";
+                return 1;
+            }
+        }
+    }
+    {
+        int dt;
+        size_t rows, cols;
+        if (nnh_weight_info(m->w.back(), &dt, &rows, &cols) != NNH_OK || (int)rows != c.n_vocab || (int)cols != E) {
+            m->err = "lm_head must be n_vocab x n_embd";
+            return 1;
+        }
+        if (!token_embd || nnh_weight_info(token_embd, &dt, &rows, &cols) != NNH_OK || (int)rows != c.n_vocab ||
+            (int)cols != E || (dt != NNH_Q8_0 && dt != NNH_Q4S) || (dt == NNH_Q4S) != (c.wtype == 2)) {
+            m->err = "the embedding table must be n_vocab x n_embd, Q4 when wtype is 2, else Q8_0";
+            return 1;
+        }
+    }
+    m->embd = token_embd;
+    m->table = (const uint8_t*)nnh_weight_device_data(token_embd);
+    m->act = act;
+    m->n_batch = n_batch;
+    m->nblk = (c.n_ctx + ATTN_BLOCK - 1) / ATTN_BLOCK;
+    m->lds_attn = (size_t)G * hd * 4 + (size_t)G * ATTN_BLOCK * 4 + (size_t)((G + 3) & ~3) * 4 +
+                  (size_t)ATTN_BLOCK * (hd + 8) * 2;
+    if (m->lds_attn > (size_t)LDS_MAX) {
+        m->err = "a 256-key block of K rows and the group's queries exceed the LDS";
+        return 1;
+    }
+    if (stream) {
+        m->st = (hipStream_t)stream;
+    } else {
+        NNGL_CHECK(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
+        m->own_stream = true;
+    }
+    const size_t nn = norm_stride_l(c) * c.n_layer + E;
+    NNGL_CHECK(hipMalloc(&m->norms, nn * 4));
+    NNGL_CHECK(hipMemcpy(m->norms, norms, nn * 4, hipMemcpyHostToDevice));
+    if (biases) {
+        NNGL_CHECK(hipMalloc(&m->bias, (size_t)c.n_layer * QKV * 4));
+        NNGL_CHECK(hipMemcpy(m->bias, biases, (size_t)c.n_layer * QKV * 4, hipMemcpyHostToDevice));
+    }
+    const size_t half = hd / 2, tab = (size_t)c.n_ctx * half;
+    std::vector<float> cs(2 * tab), sn(2 * tab);
+    rope_table_l(c.rope_base_swa, c.n_ctx, hd, rope_ff, cs.data(), sn.data());
+    rope_table_l(c.rope_base, c.n_ctx, hd, rope_ff, cs.data() + tab, sn.data() + tab);
+    NNGL_CHECK(hipMalloc(&m->cs, 2 * tab * 4));
+    NNGL_CHECK(hipMalloc(&m->sn, 2 * tab * 4));
+    NNGL_CHECK(hipMemcpy(m->cs, cs.data(), 2 * tab * 4, hipMemcpyHostToDevice));
+    NNGL_CHECK(hipMemcpy(m->sn, sn.data(), 2 * tab * 4, hipMemcpyHostToDevice));
+    uint64_t T[32];
+    expf_table(T);
+    NNGL_CHECK(hipMalloc(&m->expt, sizeof(T)));
+    NNGL_CHECK(hipMemcpy(m->expt, T, sizeof(T), hipMemcpyHostToDevice));
+    const size_t cache = (size_t)c.n_layer * c.n_ctx * KVD * 2;
+    NNGL_CHECK(hipMalloc(&m->kc, cache));
+    NNGL_CHECK(hipMalloc(&m->vc, cache));
+    NNGL_CHECK(hipMemset(m->kc, 0, cache));
+    NNGL_CHECK(hipMemset(m->vc, 0, cache));
+    const size_t nb = n_batch;
+    NNGL_CHECK(hipMalloc(&m->x, nb * E * 4));
+    NNGL_CHECK(hipMalloc(&m->normed, nb * E * 4));
+    NNGL_CHECK(hipMalloc(&m->r, nb * E * 4));
+    NNGL_CHECK(hipMalloc(&m->qkv, nb * QKV * 4));
+    NNGL_CHECK(hipMalloc(&m->attn, nb * QD * 4));
+    NNGL_CHECK(hipMalloc(&m->gu, nb * 2 * F * 4));
+    NNGL_CHECK(hipMalloc(&m->parts, nb * KV * m->nblk * G * (hd + 2) * 4));
+    NNGL_CHECK(hipMalloc(&m->states, (size_t)c.n_layer * E * 4));
+    NNGL_CHECK(hipMalloc(&m->logits, (size_t)c.n_vocab * 4));
+    NNGL_CHECK(hipMalloc(&m->tok, nb * 4));
+    NNGL_CHECK(hipHostMalloc(&m->tok_host, nb * 4));
+    NNGL_CHECK(hipMalloc(&m->row, 8));
+    const size_t wb = nnh_model_argmax_work_bytes(m->w.back()), ab = nnh_argmax_work_bytes(c.n_vocab);
+    NNGL_CHECK(hipMalloc(&m->work, wb > ab ? wb : ab));
+    NNGL_CHECK(hipFuncSetAttribute((const void*)attn_part_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)m->lds_attn));
+    // The weights' layouts for this mode and batch, so no forward allocates
+    // (and a forward can be captured into a graph).
+    for (nnh_weight* wk : m->w)
+        if (wk && (nnh_weight_prepare(wk, act, nb) != NNH_OK || (nb > 1 && nnh_weight_prepare(wk, act, 1) != NNH_OK))) {
+            m->err = std::string("weight layouts: ") + nnh_last_error();
+            return 1;
+        }
+    return 0;
+}
+
+static int gemv(nngl_model* m, const nnh_weight* w, const float* x, size_t xs, float* y, size_t ys, size_t n) {
+    if (nnh_gemv_batch_dev(w, x, xs, y, ys, n, m->act, m->st) != NNH_OK) {
+        m->err = std::string("gemv: ") + nnh_last_error();
+        return 1;
+    }
+    return 0;
+}
+
+// The forward of n_tok tokens (device ids at tokens_dev) at positions pos0
+// .. pos0 + n_tok - 1 (forward.rs:848-965): every layer, the final hidden
+// states in the model's x (after the output norm), the K/V rows appended,
+// the last token's state after each layer kept. Asynchronous on the model's
+// stream; allocates nothing, so it can be captured into a HIP graph. The
+// caller keeps positions in order (earlier positions' K/V written first).
+int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, size_t pos0) {
+    const nng_config& c = m->c;
+    if (n_tok == 0 || n_tok > (size_t)m->n_batch || pos0 + n_tok > (size_t)c.n_ctx) {
+        m->err = "n_tok out of range or context full";
+        return 1;
+    }
+    const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, G = H / KV, F = c.n_ff;
+    const int QD = H * hd, KVD = KV * hd, QKV = QD + 2 * KVD, n = (int)n_tok;
+    const bool gemma = c.arch == NNG_GEMMA3;
+    const size_t ns = norm_stride_l(c), half = hd / 2, tab = (size_t)c.n_ctx * half;
+    const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
+    hipStream_t st = m->st;
+    embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
+    resid_norm_kernel<<<n, 64, (size_t)E * 4, st>>>(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E,
+                                                    c.rms_eps);
+    NNGL_CHECK(hipGetLastError());
+    const int n_seq = (int)(pos0 + n_tok);
+    const int nblk = (n_seq - 1) / ATTN_BLOCK + 1;
+    for (int li = 0; li < c.n_layer; ++li) {
+        const float* nr = m->norms + ns * li;
+        const float *q_norm = nr + E, *k_norm = nr + E + hd, *post_attn = nr + E + 2 * hd,
+                    *ffn_norm = nr + 2 * E + 2 * hd, *post_ffw = nr + 3 * E + 2 * hd;
+        const bool sliding = c.swa_period > 0 && (li + 1) % c.swa_period != 0;  // load.rs:1156-1160
+        nnh_weight* const* W = m->w.data() + 7 * li;
+        if (m->fused_qkv) {
+            if (gemv(m, W[0], m->normed, E, m->qkv, QKV, n_tok)) return 1;
+        } else if (gemv(m, W[0], m->normed, E, m->qkv, QKV, n_tok) ||
+                   gemv(m, W[1], m->normed, E, m->qkv + QD, QKV, n_tok) ||
+                   gemv(m, W[2], m->normed, E, m->qkv + QD + KVD, QKV, n_tok)) {
+            return 1;
+        }
+        uint16_t* kcl = m->kc + (size_t)li * c.n_ctx * KVD;
+        uint16_t* vcl = m->vc + (size_t)li * c.n_ctx * KVD;
+        QkvArgs qa{m->qkv,
+                   m->bias ? m->bias + (size_t)li * QKV : nullptr,
+                   gemma ? q_norm : nullptr,
+                   gemma ? k_norm : nullptr,
+                   m->cs + (sliding ? 0 : tab),
+                   m->sn + (sliding ? 0 : tab),
+                   kcl,
+                   vcl,
+                   H,
+                   KV,
+                   hd,
+                   QKV,
+                   (int)pos0,
+                   c.rope_mode,
+                   c.rms_eps};
+        qkv_post_kernel<<<dim3(n, H + 2 * KV), 64, (size_t)hd * 4, st>>>(qa);
+        AttnArgs aa{m->qkv, kcl, vcl, m->parts, m->attn, m->expt, KV, G, hd, QKV, m->nblk, (int)pos0, n_seq,
+                    sliding ? c.window : 0, c.attn_scale};
+        attn_part_kernel<<<dim3(nblk, KV, n), 256, m->lds_attn, st>>>(aa);
+        attn_merge_kernel<<<dim3(KV, n), 256, 0, st>>>(aa);
+        NNGL_CHECK(hipGetLastError());
+        if (gemv(m, W[3], m->attn, QD, m->r, E, n_tok)) return 1;
+        resid_norm_kernel<<<n, 64, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed,
+                                                        nullptr, n, E, c.rms_eps);
+        if (m->fused_gu) {
+            if (gemv(m, W[4], m->normed, E, m->gu, 2 * F, n_tok)) return 1;
+        } else if (gemv(m, W[4], m->normed, E, m->gu, 2 * F, n_tok) ||
+                   gemv(m, W[5], m->normed, E, m->gu + F, 2 * F, n_tok)) {
+            return 1;
+        }
+        const size_t ne = (size_t)n * F;
+        act_kernel<<<(unsigned)std::min<size_t>((ne + 255) / 256, 65536), 256, 0, st>>>(m->gu, F, n, gemma ? 1 : 0);
+        NNGL_CHECK(hipGetLastError());
+        if (gemv(m, W[6], m->gu, 2 * F, m->r, E, n_tok)) return 1;
+        const bool last = li + 1 == c.n_layer;
+        const float* next = last ? m->norms + ns * c.n_layer : m->norms + ns * (li + 1);
+        resid_norm_kernel<<<n, 64, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_ffw : nullptr, next,
+                                                        last ? m->x : m->normed, m->states + (size_t)li * E, n, E,
+                                                        c.rms_eps);
+        NNGL_CHECK(hipGetLastError());
+    }
+    return 0;
+}
+
+// nngl_forward_dev for host token ids at the model's position, which it
+// then advances (the ids are checked against the vocabulary first).
+int nngl_forward(nngl_model* m, const int32_t* tokens, size_t n_tok) {
+    if (n_tok == 0 || n_tok > (size_t)m->n_batch || m->pos + n_tok > (size_t)m->c.n_ctx) {
+        m->err = "n_tok out of range or context full";
+        return 1;
+    }
+    for (size_t i = 0; i < n_tok; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->c.n_vocab) {
+            m->err = "token outside the vocabulary";
+            return 1;
+        }
+    // The staging buffer is rewritten only once the stream's earlier copies are done.
+    NNGL_CHECK(hipStreamSynchronize(m->st));
+    memcpy(m->tok_host, tokens, n_tok * 4);
+    NNGL_CHECK(hipMemcpyAsync(m->tok, m->tok_host, n_tok * 4, hipMemcpyHostToDevice, m->st));
+    if (nngl_forward_dev(m, m->tok, n_tok, m->pos)) return 1;
+    m->pos += n_tok;
+    return 0;
+}
+
+// The greedy token after the last forward of n_tok tokens: model_argmax of
+// its last hidden state (forward.rs:989-1011); synchronous.
+int nngl_argmax_last(nngl_model* m, size_t n_tok, int32_t* out) {
+    if (n_tok == 0 || n_tok > (size_t)m->n_batch) {
+        m->err = "n_tok out of range";
+        return 1;
+    }
+    const float* h = m->x + (n_tok - 1) * m->c.n_embd;
+    int rc;
+    if (m->act == NNH_ACT_F32) {
+        rc = nnh_model_argmax_dev(m->w.back(), h, m->logits, m->work, m->row, m->st);
+    } else {
+        rc = nnh_gemv_batch_dev(m->w.back(), h, m->c.n_embd, m->logits, m->c.n_vocab, 1, m->act, m->st);
+        if (rc == NNH_OK) rc = nnh_argmax_dev(m->logits, m->c.n_vocab, m->work, m->row, m->st);
+    }
+    if (rc != NNH_OK) {
+        m->err = std::string("argmax: ") + nnh_last_error();
+        return 1;
+    }
+    uint64_t r = 0;
+    NNGL_CHECK(hipMemcpyAsync(&r, m->row, 8, hipMemcpyDeviceToHost, m->st));
+    NNGL_CHECK(hipStreamSynchronize(m->st));
+    *out = (int32_t)r;
+    return 0;
+}
+
+// The lm_head row of the last token of a forward of n_tok tokens into
+// logits (device, n_vocab floats): model_logits for that token, in the
+// model's mode; asynchronous, allocates nothing.
+int nngl_logits_last_dev(nngl_model* m, size_t n_tok, float* logits) {
+    if (n_tok == 0 || n_tok > (size_t)m->n_batch) {
+        m->err = "n_tok out of range";
+        return 1;
+    }
+    return gemv(m, m->w.back(), m->x + (n_tok - 1) * m->c.n_embd, m->c.n_embd, logits, m->c.n_vocab, 1);
+}
+
+// Copies out (synchronous; any pointer may be NULL): the final hidden
+// states of the last forward (n_tok x n_embd), the last token's state after
+// each layer (n_layer x n_embd), the K/V caches (n_layer x n_ctx x kv_dim
+// BF16 each).
+int nngl_read(nngl_model* m, size_t n_tok, float* hidden, float* states, uint16_t* kcache, uint16_t* vcache) {
+    const nng_config& c = m->c;
+    if (n_tok > (size_t)m->n_batch) {
+        m->err = "n_tok out of range";
+        return 1;
+    }
+    const size_t cache = (size_t)c.n_layer * c.n_ctx * c.n_kv * c.head_dim * 2;
+    if (hidden) NNGL_CHECK(hipMemcpyAsync(hidden, m->x, n_tok * c.n_embd * 4, hipMemcpyDeviceToHost, m->st));
+    if (states)
+        NNGL_CHECK(hipMemcpyAsync(states, m->states, (size_t)c.n_layer * c.n_embd * 4, hipMemcpyDeviceToHost, m->st));
+    if (kcache) NNGL_CHECK(hipMemcpyAsync(kcache, m->kc, cache, hipMemcpyDeviceToHost, m->st));
+    if (vcache) NNGL_CHECK(hipMemcpyAsync(vcache, m->vc, cache, hipMemcpyDeviceToHost, m->st));
+    NNGL_CHECK(hipStreamSynchronize(m->st));
+    return 0;
+}
+
+size_t nngl_pos(nngl_model* m) { return m->pos; }
+
+// Start the sequence again at position `pos` (0: a new sequence; the
+// cache rows past it are overwritten as the forwards reach them).
+int nngl_set_pos(nngl_model* m, size_t pos) {
+    if (pos > (size_t)m->c.n_ctx) {
+        m->err = "position past the context";
+        return 1;
+    }
+    m->pos = pos;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,4 +1,4 @@
-"""The Gemma-3 harness's non-matmul ops against the reference's own op tests
+"""The model harness's non-matmul ops against the reference's own op tests
 (CPU only).
 
 nncpu_amd/host/gemma3.cpp restates the forward's non-matmul kernels of
@@ -35,11 +35,13 @@ def ops():
     L.nng_op_gelu_mul.argtypes = [vp, vp, sz]
     L.nng_op_rmsnorm_gamma.argtypes = [vp, vp, sz, sz, vp, f]
     L.nng_op_rope_neox.argtypes = [vp, sz, sz, sz, f, f]
+    L.nng_op_rope.argtypes = [vp, sz, sz, sz, f, f, C.c_int, vp]
+    L.nng_op_swiglu.argtypes = [vp, vp, sz]
     L.nng_op_attn_block.argtypes = [vp, sz, vp, vp, sz, sz, sz, sz, f, vp, vp]
     L.nng_op_attn_merge.argtypes = [vp, vp, sz, sz]
     L.nng_op_attn_finish.argtypes = [vp, sz, vp, sz, sz]
     for fn in (L.nng_op_exp, L.nng_op_gelu, L.nng_op_gelu_mul, L.nng_op_rmsnorm_gamma, L.nng_op_rope_neox,
-               L.nng_op_attn_block, L.nng_op_attn_merge, L.nng_op_attn_finish):
+               L.nng_op_rope, L.nng_op_swiglu, L.nng_op_attn_block, L.nng_op_attn_merge, L.nng_op_attn_finish):
         fn.restype = None
     return L
 
@@ -180,6 +182,64 @@ def test_rope_matches_reference(ops, oracle):
             m0 = a[i] * a[i] + a[i + 8] * a[i + 8]
             m1 = b[i] * b[i] + b[i + 8] * b[i + 8]
             assert abs(m0 - m1) <= 1e-4 * max(m0, 1e-6)
+
+
+def test_rope_both_pairings_and_frequency_factors(ops, oracle):
+    # kernels/tests.rs:947-983: NeoX (Gemma, Qwen) and Norm (Llama's
+    # adjacent pairs), n_rot < head_dim, with and without frequency factors
+    # (1e30 switches a pair off), against a direct evaluation; the lanes past
+    # n_rot pass through unchanged. The generator continues as the
+    # reference's does after its pos-0 vector.
+    rng = oracle.Rng(0x5051)
+    rng.vec(8 * 64, -1.0, 1.0)
+    h, d, r, pos, base = 4, 64, 32, 17.0, 1e6
+    half = r // 2
+    ff = f32([1e30 if i == 3 else 1.0 + i * 0.25 for i in range(half)])
+    for mode in (0, 1):  # NNG_ROPE_NEOX, NNG_ROPE_NORM
+        for factors in (None, ff):
+            x0 = rng.vec(h * d, -1.0, 1.0)
+            want = x0.copy().reshape(h, d)
+            for i in range(half):
+                inv = np.float32(base) ** np.float32(-(2 * i) / r)
+                theta = np.float32(pos) * inv / (np.float32(1.0) if factors is None else factors[i])
+                c, s = np.cos(theta, dtype=np.float32), np.sin(theta, dtype=np.float32)
+                pa, pb = (i, i + half) if mode == 0 else (2 * i, 2 * i + 1)
+                a, b = want[:, pa].copy(), want[:, pb].copy()
+                want[:, pa] = c * a - s * b
+                want[:, pb] = s * a + c * b
+            x = x0.copy()
+            ops.nng_op_rope(p(x), h, d, r, pos, base, mode, None if factors is None else p(factors))
+            assert_close(x, want.ravel(), 1e-5, f"rope mode {mode} factors {factors is not None}")
+            xr, x0r = x.reshape(h, d), x0.reshape(h, d)
+            assert np.array_equal(bits(xr[:, r:]), bits(x0r[:, r:])), "pass-through lanes"
+    # A switched-off pair (factor 1e30: theta 0) is unchanged; the Norm
+    # pairing rotates lanes 2i, 2i + 1 and leaves the half-split partner alone.
+    x0 = rng.vec(d, -1.0, 1.0)
+    x = x0.copy()
+    ops.nng_op_rope(p(x), 1, d, r, pos, base, 0, p(ff))
+    assert x[3] == x0[3] and x[3 + half] == x0[3 + half]
+    x = x0.copy()
+    ops.nng_op_rope(p(x), 1, d, r, 0.0, base, 1, None)
+    assert np.array_equal(bits(x), bits(x0)), "pos 0 is the identity in the Norm pairing too"
+
+
+# ---- gated activations (kernels/tests.rs:120-146): SiLU(gate) * up ---------------------------
+
+def test_swiglu_matches_reference(ops, oracle):
+    rng = oracle.Rng(0x5167)
+    for n in (257, 8, 5):
+        g, u = rng.vec(n, -3.0, 3.0), rng.vec(n, -3.0, 3.0)
+        sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-g.astype(np.float64)).astype(np.float32))
+        want = (g * sig * u).astype(np.float32)
+        y = g.copy()
+        ops.nng_op_swiglu(p(y), p(f32(u)), n)
+        assert_close(y, want, 1e-5, f"swiglu n={n}")
+    # Known values: silu(0) = 0, silu(x) -> x for large x, -> -0 for very negative x.
+    g = f32([0.0, 20.0, -100.0, 1.0])
+    u = f32([1.0, 1.0, 1.0, 2.0])
+    ops.nng_op_swiglu(p(g), p(u), 4)
+    assert g[0] == 0.0 and abs(g[1] - 20.0) < 1e-5 and g[2] == 0.0
+    assert abs(g[3] - 2.0 * 0.7310585786) < 1e-6
 
 
 # ---- attention blocks (kernels/tests.rs:1099-1217), BF16 K/V as Gemma's cache ----------------

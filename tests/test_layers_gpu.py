@@ -1,0 +1,130 @@
+"""The device forward (nncpu_amd/host/layers_gpu.hip) against the CPU forward
+(nncpu_amd/host/gemma3.cpp, crates/nncpu/src/model/forward.rs restated) for
+Qwen2, Llama and Gemma-3 layers.
+
+Both runs use the library's bit-exact f32 matmul (nncpu's own kernel, bit for
+bit), so everything between the matmuls on the device must reproduce the CPU
+forward exactly: the greedy tokens, the last token's residual after every
+layer of every forward (hashed), and the whole BF16 K/V cache. Prompts run in
+16-token batches (session/engine.rs:362-380), then one token per forward;
+contexts past 256 keys exercise the blockwise attention merge
+(kernels/mod.rs:765-800), a short sliding window a partial first block
+(model/embed.rs:14-30).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def N():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import nncpu_amd as N
+    N.init(0)
+    return N
+
+
+def run_both(model, prompt, n_gen, fused=False, batch=16):
+    print(f"arch {model.cfg.arch} dtype {model.cfg.wtype} prompt {len(prompt)} gen {n_gen} fused {fused}", flush=True)
+    tc, hc, kc, vc = model.cpu_generate(prompt, n_gen, batch=batch)
+    dev = model.device(n_batch=batch, fused=fused)
+    try:
+        tg, hg, kg, vg = dev.generate(prompt, n_gen, batch=batch)
+    finally:
+        dev.free()
+    assert np.array_equal(tg, tc), (tg, tc)
+    assert np.array_equal(hg, hc), np.argwhere(hg != hc)[:5]
+    assert np.array_equal(kg, kc), np.argwhere(kg != kc)[:5]
+    assert np.array_equal(vg, vc), np.argwhere(vg != vc)[:5]
+    return tc
+
+
+def test_qwen2_layers_match_cpu_forward(N):
+    # Qwen2: q / k / v biases, NeoX RoPE, SiLU(gate) * up, GQA 2 query heads
+    # per KV head; 270 prompt tokens, so the later tokens attend over two
+    # 256-key blocks merged with glibc's expf.
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=256, n_head=4, n_kv=2, n_ff=512, n_vocab=1024, n_ctx=320)
+    model = Model.random(cfg, seed=0x0E2)
+    prompt = np.random.default_rng(1).integers(0, cfg.n_vocab, 270).astype(np.int32)
+    run_both(model, prompt, 6)
+
+
+def test_llama_layers_match_cpu_forward(N):
+    # Llama: adjacent-pair RoPE, no biases, 3 query heads per KV head, an
+    # untied embedding table.
+    from nncpu_amd.models import Model, llama_config
+    cfg = llama_config(n_layer=2, n_embd=384, n_head=6, n_kv=2, n_ff=1024, n_vocab=2048, n_ctx=64)
+    model = Model.random(cfg, seed=0x11A, tied=False)
+    prompt = np.random.default_rng(2).integers(0, cfg.n_vocab, 21).astype(np.int32)
+    run_both(model, prompt, 8)
+
+
+def test_llama_rope_frequency_factors(N):
+    # Llama 3's RoPE frequency factors divide each pair's angle (kernels/mod.rs
+    # 712-716), in both forwards' tables.
+    from nncpu_amd.models import Model, llama_config
+    cfg = llama_config(n_layer=1, n_embd=256, n_head=4, n_kv=4, n_ff=512, n_vocab=512, n_ctx=48)
+    model = Model.random(cfg, seed=0x3F)
+    model.rope_ff = np.linspace(1.0, 8.0, cfg.head_dim // 2).astype(np.float32)
+    prompt = np.random.default_rng(3).integers(0, cfg.n_vocab, 17).astype(np.int32)
+    run_both(model, prompt, 4)
+
+
+def test_gemma3_layers_match_cpu_forward(N):
+    # Gemma-3 through the generic kernels: embedding scale, per-head q / k
+    # RMSNorm, post-attention and post-FFW norms, GELU(gate) * up, head_dim 256,
+    # and a 24-key sliding window on every layer but each second one, so
+    # from position 24 the sliding layers' spans start past key 0.
+    from nncpu_amd.gemma import gemma3_1b_config
+    from nncpu_amd.models import Model
+    cfg = gemma3_1b_config(n_ctx=64, n_layer=2, n_vocab=1024)
+    cfg.window, cfg.swa_period = 24, 2
+    model = Model.random(cfg, seed=0x6E3)
+    prompt = np.random.default_rng(4).integers(0, cfg.n_vocab, 40).astype(np.int32)
+    run_both(model, prompt, 6)
+
+
+def test_qwen2_q4_and_fused_matrices(N):
+    # Q4 weights and embedding table; q / k / v and gate / up uploaded as one
+    # matrix each (concat_rows): the same rows, so the same bits.
+    from nncpu_amd import Q4S
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=256, n_head=4, n_kv=1, n_ff=768, n_vocab=640, n_ctx=48)
+    model = Model.random(cfg, seed=0x44, dtype=Q4S)
+    prompt = np.random.default_rng(5).integers(0, cfg.n_vocab, 19).astype(np.int32)
+    t = run_both(model, prompt, 5)
+    t2 = run_both(model, prompt, 5, fused=True)
+    assert np.array_equal(t, t2)
+
+
+def test_forward_dev_graph_replay(N):
+    # nngl_forward_dev allocates nothing: one prefill captured in a HIP graph
+    # and replayed (eager work between replays) gives the eager hidden states.
+    import torch
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=256, n_head=4, n_kv=2, n_ff=512, n_vocab=512, n_ctx=64)
+    model = Model.random(cfg, seed=0x6A)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=32, stream=s.cuda_stream)
+    try:
+        tok = torch.randint(0, cfg.n_vocab, (32,), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        dev.forward_dev(tok.data_ptr(), 32, 0)
+        want, want_st = dev.read(32)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            dev.forward_dev(tok.data_ptr(), 32, 0)
+        for i in range(3):
+            junk = torch.randn(1 << 20, device="cuda")
+            (junk * 2).sum().item()
+            g.replay()
+            torch.cuda.synchronize()
+            got, got_st = dev.read(32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
+            assert np.array_equal(got_st.view(np.uint32), want_st.view(np.uint32)), i
+    finally:
+        dev.free()
