@@ -380,18 +380,23 @@ def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int =
     """BASELINE configs[4], end to end: a Qwen2.5-7B-shaped model (d 3584,
     FFN 18944, 28 query / 4 KV heads of 128, RoPE base 1e6, RMSNorm, SwiGLU,
     q/k/v biases) with random weights 0.02*N(0,1) encoded by the library's
-    device encoder (nncpu Q8_0 / Q4), prefilling 512 tokens of random
-    embeddings through all 28 layers and the last token's lm_head row
-    (152064 x 3584). Every weight matmul is the library's int8 path in mode
-    `act` (activations quantized on the device: nncpu's Q8_0 encoder and the
-    int8 MFMA GEMM, or MX blocks and the BF16-MFMA GEMM); q/k/v and gate/up are
-    uploaded as one concatenated matrix each, as serving engines load them.
-    The rest of the layer (norms, RoPE, causal GQA attention, SiLU) is torch
-    float32 on the GPU: harness, not the measured path. One step = one full
-    prefill; returns ms and tokens/s, plus the matmul share from HIP events."""
+    device encoder (nncpu Q8_0 / Q4), prefilling 512 random tokens through
+    all 28 layers and the last token's lm_head row (152064 x 3584, tied to
+    the embedding table). Every weight matmul is the library's int8 path in
+    mode `act` (activations quantized on the device: nncpu's Q8_0 encoder and
+    the int8 MFMA GEMM, or MX blocks and the BF16-MFMA GEMM); q/k/v and
+    gate/up are one concatenated matrix each, as serving engines load them.
+    Everything between the matmuls is the device forward
+    (nncpu_amd/host/layers_gpu.hip: embedding rows, RMSNorm, biases, RoPE, the
+    BF16 K/V cache, blockwise causal GQA attention, SiLU(gate) * up, with the
+    CPU forward's arithmetic). One step = one full prefill, captured in a HIP
+    graph; `matmul_ms` is a graph of the same matmul calls alone on the same
+    shapes, `layer_ops_ms` the difference."""
     import torch
-    import torch.nn.functional as F
-    d, ff, nh, nkv, hd, vocab = 3584, 18944, 28, 4, 128, 152064
+    from nncpu_amd.models import DeviceForward, norm_stride, qwen25_7b_config
+    cfg = qwen25_7b_config(n_ctx=n_tok, n_layer=n_layer, wtype=2 if dtype == 2 else 1)
+    d, ff, nkv, hd, vocab = cfg.n_embd, cfg.n_ff, cfg.n_kv, cfg.head_dim, cfg.n_vocab
+    qkv = d + 2 * nkv * hd
     dev = "cuda"
     st = Stream()
     g = torch.Generator(device=dev)
@@ -404,114 +409,89 @@ def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int =
         del w
         return out
 
-    layers = []
+    weights = []
     for _ in range(n_layer):
-        layers.append(dict(
-            qkv=weight(d + 2 * nkv * hd, d), o=weight(d, d), gu=weight(2 * ff, d), down=weight(d, ff),
-            bqkv=torch.randn(d + 2 * nkv * hd, generator=g, device=dev).mul_(0.02),
-            n1=1.0 + 0.1 * torch.randn(d, generator=g, device=dev),
-            n2=1.0 + 0.1 * torch.randn(d, generator=g, device=dev)))
+        weights += [weight(qkv, d), None, None, weight(d, d), weight(2 * ff, d), None, weight(d, ff)]
     lm_head = weight(vocab, d)
-    norm_f = 1.0 + 0.1 * torch.randn(d, generator=g, device=dev)
-    x0 = torch.randn(n_tok, d, generator=g, device=dev)
-    pos = torch.arange(n_tok, device=dev, dtype=torch.float32)
-    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
-    ang = pos[:, None] * inv[None, :]
-    cos, sin = torch.cos(ang), torch.sin(ang)
-    mm_events = []
-    timed = {"on": True}
-
-    def mm(w, x, rows):
-        y = torch.empty(x.shape[0], rows, device=dev)
-        if not timed["on"]:  # inside a graph capture: no event records
-            N.gemv_batch_dev(w, x.data_ptr(), x.shape[1], y.data_ptr(), rows, x.shape[0], act, st.handle)
-            return y
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(st.s)
-        N.gemv_batch_dev(w, x.data_ptr(), x.shape[1], y.data_ptr(), rows, x.shape[0], act, st.handle)
-        e1.record(st.s)
-        mm_events.append((e0, e1))
-        return y
-
-    def rms(x, wgt):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * wgt
-
-    def rope(t):  # t [tokens, heads, hd], NeoX halves
-        a, b = t[..., :hd // 2], t[..., hd // 2:]
-        c, s_ = cos[:, None, :], sin[:, None, :]
-        return torch.cat([a * c - b * s_, b * c + a * s_], dim=-1)
+    weights.append(lm_head)
+    rng = np.random.default_rng(0x9E11 + dtype)
+    norms = (1.0 + 0.1 * rng.standard_normal(norm_stride(cfg) * n_layer + d)).astype(np.float32)
+    biases = (0.02 * rng.standard_normal(n_layer * qkv)).astype(np.float32)
+    fwd = DeviceForward(cfg, weights, norms, biases, lm_head, n_batch=n_tok, act=act, stream=st.handle)
+    tok = torch.randint(0, vocab, (n_tok,), generator=g, device=dev, dtype=torch.int32)
+    logits = torch.empty(vocab, device=dev)
 
     def forward():
-        x = x0.clone()
-        for L in layers:
-            h = rms(x, L["n1"]).contiguous()
-            qkv = mm(L["qkv"], h, d + 2 * nkv * hd) + L["bqkv"]
-            q = rope(qkv[:, :d].view(n_tok, nh, hd))
-            k = rope(qkv[:, d:d + nkv * hd].view(n_tok, nkv, hd))
-            v = qkv[:, d + nkv * hd:].view(n_tok, nkv, hd)
-            k = k.repeat_interleave(nh // nkv, dim=1)
-            v = v.repeat_interleave(nh // nkv, dim=1)
-            a = F.scaled_dot_product_attention(q.transpose(0, 1).contiguous(), k.transpose(0, 1).contiguous(),
-                                               v.transpose(0, 1).contiguous(), is_causal=True)
-            a = a.transpose(0, 1).reshape(n_tok, d).contiguous()
-            x = x + mm(L["o"], a, d)
-            h = rms(x, L["n2"]).contiguous()
-            gu = mm(L["gu"], h, 2 * ff)
-            x = x + mm(L["down"], (F.silu(gu[:, :ff]) * gu[:, ff:]).contiguous(), d)
-        last = rms(x[-1:], norm_f).contiguous()
-        return mm(lm_head, last, vocab)
+        fwd.forward_dev(tok.data_ptr(), n_tok, 0)
+        fwd.logits_last_dev(n_tok, logits.data_ptr())
+
+    # The matmuls alone, the same calls on buffers of the same shapes.
+    xa = torch.randn(n_tok, 2 * ff, device=dev)
+    ya = torch.empty(n_tok, 2 * ff, device=dev)
+
+    def matmuls():
+        for li in range(n_layer):
+            W = weights[7 * li:7 * li + 7]
+            N.gemv_batch_dev(W[0], xa.data_ptr(), d, ya.data_ptr(), qkv, n_tok, act, st.handle)
+            N.gemv_batch_dev(W[3], xa.data_ptr(), d, ya.data_ptr(), d, n_tok, act, st.handle)
+            N.gemv_batch_dev(W[4], xa.data_ptr(), d, ya.data_ptr(), 2 * ff, n_tok, act, st.handle)
+            N.gemv_batch_dev(W[6], xa.data_ptr(), 2 * ff, ya.data_ptr(), d, n_tok, act, st.handle)
+        N.gemv_batch_dev(lm_head, xa.data_ptr(), d, ya.data_ptr(), vocab, 1, act, st.handle)
 
     with torch.cuda.stream(st.s):
         for _ in range(2):
             forward()
+            matmuls()
         torch.cuda.synchronize()
-        mm_events.clear()
         steps = max(1, min(args.steps, 5))
         e0 = st.event()
         for _ in range(steps):
-            logits = forward()
+            forward()
         e1 = st.event()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    mm_ms = sum(a.elapsed_time(b) for a, b in mm_events) / steps
-    per_layer = 2 * n_tok * d * ((d + 2 * nkv * hd) + d + 2 * ff + ff)
+    eager_logits = logits.clone()
+    assert torch.isfinite(eager_logits).all()
+    per_layer = 2 * n_tok * d * (qkv + d + 2 * ff + ff)
     ops = n_layer * per_layer + 2 * d * vocab
-    assert torch.isfinite(logits).all()
-    # The same prefill captured once in a HIP graph (the library's kernels and
-    # the harness's; the library's per-stream scratch is sized by the eager
-    # runs above) and replayed: the end-to-end time without the host's
-    # per-kernel launch cost. Each replay, with eager work between them, must
-    # give the eager logits.
-    timed["on"] = False
-    graph = torch.cuda.CUDAGraph()
+    # One prefill captured in a HIP graph and replayed; each replay, with
+    # eager work between them, must give the eager logits.
+    graph, mgraph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=st.s):
-        glogits = forward()
-    timed["on"] = True
+        forward()
+    with torch.cuda.graph(mgraph, stream=st.s):
+        matmuls()
     for _ in range(3):
+        logits.zero_()
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(glogits, logits), "graph replay differs from the eager prefill"
+        assert torch.equal(logits, eager_logits), "graph replay differs from the eager prefill"
         torch.ones(256, device=dev).sum().item()  # eager work between replays
-    with torch.cuda.stream(st.s):
-        g0 = st.event()
-        for _ in range(steps):
-            graph.replay()
-        g1 = st.event()
-    torch.cuda.synchronize()
-    gms = g0.elapsed_time(g1) / steps
-    del graph
+
+    def timed(gr):
+        with torch.cuda.stream(st.s):
+            g0 = st.event()
+            for _ in range(steps):
+                gr.replay()
+            g1 = st.event()
+        torch.cuda.synchronize()
+        return g0.elapsed_time(g1) / steps
+
+    gms, mm_ms = timed(graph), timed(mgraph)
+    del graph, mgraph
     res = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} Qwen2.5-7B-shaped prefill, {n_layer} layers, {n_tok} tokens",
                activations="MX int8 blocks (power-of-two scales)" if act == N.ACT_MXI8 else "int8 blocks (nncpu Q8_0)",
                ms=round(gms, 3), tokens_per_s=round(n_tok / gms * 1e3, 1), eager_ms=round(ms, 3),
-               matmul_ms=round(mm_ms, 3), matmul_tops=round(ops / mm_ms / 1e9, 1), steps=steps,
-               timing="ms: one prefill replayed from a HIP graph; eager_ms: launched from the host; matmul_ms: "
-                      "the library's calls in the eager runs (HIP events)")
+               matmul_ms=round(mm_ms, 3), layer_ops_ms=round(gms - mm_ms, 3),
+               matmul_tops=round(ops / mm_ms / 1e9, 1), steps=steps,
+               timing="ms: one prefill replayed from a HIP graph (embedding, 28 layers of the device forward, "
+                      "lm_head row); eager_ms: launched from the host; matmul_ms: a graph of the same matmul calls "
+                      "alone; layer_ops_ms = ms - matmul_ms")
     log(f"qwen_prefill: {res}")
-    for L in layers:
-        for key in ("qkv", "o", "gu", "down"):
-            L[key].free()
-    lm_head.free()
+    fwd.free()
+    for w in weights:
+        if w is not None:
+            w.free()
     return res
 
 

@@ -111,47 +111,94 @@ __global__ void embed_kernel(const int32_t* __restrict__ tok, const uint8_t* __r
     }
 }
 
-// One wave per row (dim <= 8192):
+// One workgroup of 256 threads per row (dim a multiple of 4, at most 8192):
 //   r == NULL: y = rmsnorm(x) * gamma (y may be x);
 //   else: x += (post ? rmsnorm(r) * post : r), written back, the last row's
 //   new x copied to rec (if not NULL), then y = rmsnorm(x) * gamma (y may be x).
-// rmsnorm_gamma_multi (scalar.rs:270-292): y = (x * scale) * gamma.
-__global__ __launch_bounds__(64) void resid_norm_kernel(float* x, const float* __restrict__ r,
-                                                        const float* __restrict__ post, const float* gamma,
-                                                        float* y, float* __restrict__ rec, int n_rows, int dim,
-                                                        float eps) {
-    extern __shared__ float lds[];
-    float* v = lds;         // the row being normed
-    float* w = lds + dim;   // r, when it is normed first
-    const int row = blockIdx.x, lane = threadIdx.x;
-    float* xr = x + (size_t)row * dim;
+// rmsnorm_gamma_multi (scalar.rs:270-292): y = (x * scale) * gamma. Every
+// thread loads its 16-byte pieces at once; the sums of squares are the 8
+// FMA lanes of wave 0 over the row in LDS.
+constexpr int RN_T = 256, RN_K = 8;  // threads; 16-byte pieces per thread (8192 floats)
+__global__ __launch_bounds__(RN_T) void resid_norm_kernel(float* x, const float* __restrict__ r,
+                                                          const float* __restrict__ post, const float* gamma,
+                                                          float* y, float* __restrict__ rec, int n_rows, int dim,
+                                                          float eps) {
+    extern __shared__ __align__(16) float lds[];
+    __shared__ float scale_s;
+    float* v = lds;        // the row being normed
+    float* w = lds + dim;  // r, when it is normed first
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, n4 = dim / 4;
+    float4* xr = (float4*)(x + (size_t)row * dim);
+    float4 xv[RN_K], rv[RN_K], pv[RN_K], gv[RN_K];
+#pragma unroll
+    for (int k = 0; k < RN_K; ++k) {
+        const int i = tid + k * RN_T;
+        if (i < n4) {
+            xv[k] = xr[i];
+            gv[k] = ((const float4*)gamma)[i];
+            if (r) rv[k] = ((const float4*)(r + (size_t)row * dim))[i];
+            if (post) pv[k] = ((const float4*)post)[i];
+        }
+    }
     if (r) {
-        const float* rr = r + (size_t)row * dim;
+        float sc = 1.0f;
         if (post) {
-            for (int i = lane; i < dim; i += 64) w[i] = rr[i];
+#pragma unroll
+            for (int k = 0; k < RN_K; ++k)
+                if (tid + k * RN_T < n4) ((float4*)w)[tid + k * RN_T] = rv[k];
             __syncthreads();
-            const float sc = rms_of_d(row_sumsq(w, dim, lane), dim, eps);
-            for (int i = lane; i < dim; i += 64) {
-                const float nv = __fadd_rn(xr[i], __fmul_rn(__fmul_rn(w[i], sc), post[i]));
-                v[i] = nv;
-                xr[i] = nv;
+            if (tid < 64) {
+                const double ss = row_sumsq(w, dim, lane);
+                if (lane == 0) scale_s = rms_of_d(ss, dim, eps);
             }
-        } else {
-            for (int i = lane; i < dim; i += 64) {
-                const float nv = __fadd_rn(xr[i], rr[i]);
-                v[i] = nv;
+            __syncthreads();
+            sc = scale_s;
+        }
+#pragma unroll
+        for (int k = 0; k < RN_K; ++k) {
+            const int i = tid + k * RN_T;
+            if (i < n4) {
+                float4 nv;
+                if (post) {
+                    nv.x = __fadd_rn(xv[k].x, __fmul_rn(__fmul_rn(rv[k].x, sc), pv[k].x));
+                    nv.y = __fadd_rn(xv[k].y, __fmul_rn(__fmul_rn(rv[k].y, sc), pv[k].y));
+                    nv.z = __fadd_rn(xv[k].z, __fmul_rn(__fmul_rn(rv[k].z, sc), pv[k].z));
+                    nv.w = __fadd_rn(xv[k].w, __fmul_rn(__fmul_rn(rv[k].w, sc), pv[k].w));
+                } else {
+                    nv.x = __fadd_rn(xv[k].x, rv[k].x);
+                    nv.y = __fadd_rn(xv[k].y, rv[k].y);
+                    nv.z = __fadd_rn(xv[k].z, rv[k].z);
+                    nv.w = __fadd_rn(xv[k].w, rv[k].w);
+                }
+                xv[k] = nv;
                 xr[i] = nv;
+                if (rec && row == n_rows - 1) ((float4*)rec)[i] = nv;
             }
         }
-        if (rec && row == n_rows - 1)
-            for (int i = lane; i < dim; i += 64) rec[i] = v[i];
-    } else {
-        for (int i = lane; i < dim; i += 64) v[i] = xr[i];
+    }
+#pragma unroll
+    for (int k = 0; k < RN_K; ++k)
+        if (tid + k * RN_T < n4) ((float4*)v)[tid + k * RN_T] = xv[k];
+    __syncthreads();
+    if (tid < 64) {
+        const double ss = row_sumsq(v, dim, lane);
+        if (lane == 0) scale_s = rms_of_d(ss, dim, eps);
     }
     __syncthreads();
-    const float sc = rms_of_d(row_sumsq(v, dim, lane), dim, eps);
-    float* yr = y + (size_t)row * dim;
-    for (int i = lane; i < dim; i += 64) yr[i] = __fmul_rn(__fmul_rn(v[i], sc), gamma[i]);
+    const float sc = scale_s;
+    float4* yr = (float4*)(y + (size_t)row * dim);
+#pragma unroll
+    for (int k = 0; k < RN_K; ++k) {
+        const int i = tid + k * RN_T;
+        if (i < n4) {
+            float4 o;
+            o.x = __fmul_rn(__fmul_rn(xv[k].x, sc), gv[k].x);
+            o.y = __fmul_rn(__fmul_rn(xv[k].y, sc), gv[k].y);
+            o.z = __fmul_rn(__fmul_rn(xv[k].z, sc), gv[k].z);
+            o.w = __fmul_rn(__fmul_rn(xv[k].w, sc), gv[k].w);
+            yr[i] = o;
+        }
+    }
 }
 
 struct QkvArgs {
@@ -213,7 +260,7 @@ struct AttnArgs {
     float* parts;            // [n_tok][KV][nblk][G][hd + 2]
     float* out;              // [n_tok][H * hd]
     const uint64_t* expt;    // glibc_expf's table
-    int KV, G, hd, QKV, nblk, pos0, n_seq, window;
+    int KV, G, hd, QKV, nblk, pos0, n_seq, window, n_tok, tq;
     float scale;
 };
 
@@ -224,118 +271,236 @@ __device__ __forceinline__ void attn_span(int window, int pos, int n_seq, int& f
     last = pos < end ? pos : end;
 }
 
-// A partial of the heads sharing KV head y over block b0 + x of token z's
-// span (scalar.rs:444-519, gemma3.cpp attn_block). 256 threads; LDS: the
-// heads' queries, the block's K (then V) rows padded to hd + 8, the scores.
-__global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs a) {
-    extern __shared__ __align__(16) float lds[];
-    const int t = blockIdx.z, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int hd = a.hd, G = a.G, pw = hd + 2, KS = hd + 8, KVD = a.KV * hd, hd8 = hd & ~7;
+// Token t's keys in 256-key block b (false when its span has none), and
+// the index of b among its span's blocks.
+__device__ __forceinline__ bool tok_block(const AttnArgs& a, int t, int b, int& k0, int& k1, int& bi) {
+    if (t >= a.n_tok) return false;
     int first, last;
     attn_span(a.window, a.pos0 + t, a.n_seq, first, last);
-    const int b = first / ATTN_BLOCK + (int)blockIdx.x;
-    if (b > last / ATTN_BLOCK) return;
-    const int k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
-    const int k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
-    const int nk = k1 + 1 - k0;
-    float* qs = lds;                                  // [G][hd]
-    float* sc = qs + G * hd;                          // [G][256]
-    float* mh = sc + G * ATTN_BLOCK;                  // [G]
-    uint16_t* kv = (uint16_t*)(mh + ((G + 3) & ~3));  // [256][KS]
-    float* part = a.parts + ((((size_t)t * a.KV + kvh) * a.nblk) + blockIdx.x) * G * pw;
+    if (b < first / ATTN_BLOCK || b > last / ATTN_BLOCK) return false;
+    k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
+    k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
+    bi = b - first / ATTN_BLOCK;
+    return true;
+}
 
-    const float* q = a.qkv + (size_t)t * a.QKV + (size_t)kvh * G * hd;
-    for (int i = tid; i < G * hd; i += 256) qs[i] = q[i];
-    // K rows in 16-byte pieces (hd % 8 == 0).
-    const int pr = hd / 8;
-    for (int i = tid; i < nk * pr; i += 256) {
-        const int j = i / pr, c = i - j * pr;
-        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.kc + (size_t)(k0 + j) * KVD + kvh * hd + 8 * c);
-    }
-    __syncthreads();
-    // Scores: head h, key j; FMA lanes l = i % 8 over the whole 8-chunks,
-    // hsum8, the tail, times the scale.
-    for (int i = tid; i < G * nk; i += 256) {
-        const int h = i / nk, j = i - h * nk;
-        const float* qh = qs + h * hd;
-        const uint16_t* kr = kv + j * KS;
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < hd8; c += 8) {
-            const uint4 k8 = *(const uint4*)(kr + c);
-            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
-#pragma unroll
-            for (int l = 0; l < 8; ++l)
-                acc[l] = __fmaf_rn(qh[c + l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
+// The partials (scalar.rs:444-519, gemma3.cpp attn_block) of tokens
+// x * tq .. + tq - 1, heads of KV head y, over 256-key block z: rows
+// r = s * G + h (token slot s, head h), at most AT_NQ. Every row's values
+// are the CPU's: its scores, first maximum, weights, weight sum and V sum
+// over the token's own keys of the block, in key order. The workgroup stages
+// the block's K rows (then V rows) AT_KC at a time in LDS for all its rows.
+// Scores: thread (key j, half) holds K row j in registers and runs the
+// 8-lane FMA chains of rows half, half + 2, ... against the queries in LDS
+// (broadcast reads). V sums: thread (lane i of the head, group) keeps the
+// chains o[r][i] of its rows across the chunks, each V value read once.
+constexpr int AT_KC = 128;  // keys per LDS chunk
+constexpr int AT_NQ = 32;   // rows per workgroup at most
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
+    constexpr int KS = HD + 8, NG = 256 / HD, RM = AT_NQ / NG;
+    static_assert(HD % 8 == 0 && 256 % HD == 0, "head_dim divides 256");
+    extern __shared__ __align__(16) float lds[];
+    __shared__ int tk0[AT_NQ], tk1[AT_NQ], tbi[AT_NQ], rk0[AT_NQ], rk1[AT_NQ];
+    const int kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.G, TQ = a.tq, NQ = TQ * G, t0 = blockIdx.x * TQ, pw = HD + 2, KVD = a.KV * HD;
+    // The tile's key range in the block (every thread computes it).
+    int K0 = 1 << 30, K1 = -1;
+    for (int s = 0; s < TQ; ++s) {
+        int k0, k1, bi;
+        const bool on = tok_block(a, t0 + s, b, k0, k1, bi);
+        if (tid == 0) {
+            tk0[s] = on ? k0 : 1;
+            tk1[s] = on ? k1 : 0;
+            tbi[s] = bi;
         }
-        float s = hsum8(acc);
-        for (int c = hd8; c < hd; ++c) s = __fadd_rn(s, __fmul_rn(qh[c], bf16f(kr[c])));
-        sc[h * ATTN_BLOCK + j] = __fmul_rn(s, a.scale);
+        if (on) {
+            K0 = k0 < K0 ? k0 : K0;
+            K1 = k1 > K1 ? k1 : K1;
+        }
+    }
+    if (K1 < 0) return;
+    __syncthreads();
+    if (tid < NQ) {  // each row's key range: its token's
+        rk0[tid] = tk0[tid / G];
+        rk1[tid] = tk1[tid / G];
+    }
+    float* qs = lds;                              // [NQ][HD]
+    float* sc = qs + NQ * HD;                     // [NQ][256], key k at k - K0
+    float* mh = sc + NQ * ATTN_BLOCK;             // [AT_NQ]
+    uint16_t* kv = (uint16_t*)(mh + AT_NQ);       // [AT_KC][KS]
+    for (int i = tid; i < NQ * HD; i += 256) {
+        const int r = i / HD, s = r / G, h = r - s * G, e = i - r * HD;
+        if (t0 + s < a.n_tok) qs[i] = a.qkv[(size_t)(t0 + s) * a.QKV + (size_t)(kvh * G + h) * HD + e];
     }
     __syncthreads();
-    // Each head's maximum as `if m < v { m = v }` from s[0] finds it: the
-    // first largest, NaN never taken unless s[0] is NaN. Lane l scans keys
-    // 4l .. 4l + 3 from -inf, then the lanes' results combine in key order.
-    for (int h = wave; h < G; h += 4) {
-        const float* s = sc + h * ATTN_BLOCK;
+    // Scores, chunk by chunk.
+    constexpr int PR = HD / 8;  // 16-byte pieces per row
+    for (int c0 = K0; c0 <= K1; c0 += AT_KC) {
+        const int nkc = K1 + 1 - c0 < AT_KC ? K1 + 1 - c0 : AT_KC;
+        for (int i = tid; i < nkc * PR; i += 256) {
+            const int j = i / PR, c = i - j * PR;
+            *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.kc + (size_t)(c0 + j) * KVD + kvh * HD + 8 * c);
+        }
+        __syncthreads();
+        const int j = tid & (AT_KC - 1), half = tid >> 7;
+        if (j < nkc) {
+            const int key = c0 + j;
+            // The key's row in registers: as f32 up to head_dim 128 (converted
+            // once for all rows), else as BF16 pairs.
+            constexpr bool F32ROW = HD <= 128;
+            float kf[F32ROW ? HD : 1];
+            uint4 kr[F32ROW ? 1 : PR];
+#pragma unroll
+            for (int c = 0; c < PR; ++c) {
+                const uint4 k8 = *(const uint4*)(kv + j * KS + 8 * c);
+                if (F32ROW) {
+                    const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) kf[F32ROW ? 8 * c + l : 0] = bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu);
+                } else {
+                    kr[F32ROW ? 0 : c] = k8;
+                }
+            }
+            for (int r = half; r < NQ; r += 2) {
+                if (key < rk0[r] || key > rk1[r]) continue;
+                const float* qh = qs + r * HD;
+                float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c = 0; c < PR; ++c) {
+                    const float4 qa = *(const float4*)(qh + 8 * c), qb = *(const float4*)(qh + 8 * c + 4);
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                    if (F32ROW) {
+#pragma unroll
+                        for (int l = 0; l < 8; ++l) acc[l] = __fmaf_rn(qv[l], kf[F32ROW ? 8 * c + l : 0], acc[l]);
+                    } else {
+                        const uint32_t kw[4] = {kr[F32ROW ? 0 : c].x, kr[F32ROW ? 0 : c].y, kr[F32ROW ? 0 : c].z,
+                                                kr[F32ROW ? 0 : c].w};
+#pragma unroll
+                        for (int l = 0; l < 8; ++l)
+                            acc[l] = __fmaf_rn(qv[l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
+                    }
+                }
+                sc[r * ATTN_BLOCK + key - K0] = __fmul_rn(hsum8(acc), a.scale);
+            }
+        }
+        __syncthreads();
+    }
+    // Each row's maximum as `if m < v { m = v }` from its first key finds it:
+    // the first largest, NaN never taken unless the first score is NaN.
+    // Lane l scans keys 4l .. 4l + 3 of the row from -inf, then the lanes'
+    // results combine in key order.
+    for (int r = wave; r < NQ; r += 4) {
+        const int n = rk1[r] + 1 - rk0[r];
+        if (n <= 0) continue;
+        const float* sr = sc + r * ATTN_BLOCK + (rk0[r] - K0);
         float m = -INFINITY;
-        for (int j = 4 * lane; j < 4 * lane + 4 && j < nk; ++j)
-            if (m < s[j]) m = s[j];
+        for (int j = 4 * lane; j < 4 * lane + 4 && j < n; ++j)
+            if (m < sr[j]) m = sr[j];
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float other = __shfl_xor(m, o, 64);
             const float lo = (lane & o) ? other : m, hi = (lane & o) ? m : other;
             m = lo < hi ? hi : lo;
         }
-        if (lane == 0) mh[h] = s[0] != s[0] ? s[0] : m;
+        if (lane == 0) mh[r] = sr[0] != sr[0] ? sr[0] : m;
     }
     __syncthreads();
-    for (int i = tid; i < G * nk; i += 256) {
-        const int h = i / nk, j = i - h * nk;
-        sc[h * ATTN_BLOCK + j] = exp_lane(__fsub_rn(sc[h * ATTN_BLOCK + j], mh[h]));
+    for (int i = tid; i < NQ * ATTN_BLOCK; i += 256) {
+        const int r = i >> 8, k = K0 + (i & (ATTN_BLOCK - 1));
+        if (k >= rk0[r] && k <= rk1[r]) sc[i] = exp_lane(__fsub_rn(sc[i], mh[r]));
     }
     __syncthreads();
-    // The weights' sum: lane l of head h's group of 8 adds weights 8c + l
-    // over the whole 8-chunks, hsum8, then the tail in order.
+    // The weight sums: lane l of row r's group of 8 adds weights l, l + 8, ..
+    // of the row's whole 8-chunks, hsum8, then the tail in order.
     {
-        const int h = tid >> 3, l = tid & 7, body = nk & ~7;
+        const int r = tid >> 3, l = tid & 7, s = r / G;
+        const int n = r < NQ ? rk1[r] + 1 - rk0[r] : 0, body = n & ~7;
+        const float* sr = sc + r * ATTN_BLOCK + (r < NQ ? rk0[r] - K0 : 0);
         float vs = 0.0f;
-        if (h < G)
-            for (int j = l; j < body; j += 8) vs = __fadd_rn(vs, sc[h * ATTN_BLOCK + j]);
+        for (int j = l; j < body; j += 8) vs = __fadd_rn(vs, sr[j]);
         float ls = hsum8_lanes(vs);
-        if (h < G && l == 0) {
-            for (int j = body; j < nk; ++j) ls = __fadd_rn(ls, sc[h * ATTN_BLOCK + j]);
-            part[h * pw + hd] = mh[h];
-            part[h * pw + hd + 1] = ls;
+        if (n > 0 && l == 0) {
+            for (int j = body; j < n; ++j) ls = __fadd_rn(ls, sr[j]);
+            const int h = r - s * G;
+            float* part = a.parts + ((((size_t)(t0 + s) * a.KV + kvh) * a.nblk) + tbi[s]) * G * pw + h * pw;
+            part[HD] = mh[r];
+            part[HD + 1] = ls;
         }
     }
-    __syncthreads();
-    for (int i = tid; i < nk * pr; i += 256) {
-        const int j = i / pr, c = i - j * pr;
-        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.vc + (size_t)(k0 + j) * KVD + kvh * hd + 8 * c);
+    // V sums, chunk by chunk: the first key of a row writes w * v, the rest
+    // FMA. Each chain starts at -0, so the first key's FMA is exactly w * v
+    // (x + -0 = x for every x, signed zeros included). Keys every active row
+    // of the tile has ([kf0, kf1]) run without masks, four per step (each
+    // row's four weights one 16-byte read, all the step's reads issued
+    // before its FMAs); the keys at the edges only some rows have run masked.
+    const int ie = tid % HD, grp = tid / HD;
+    float o[RM];
+    int lo[RM], hi[RM];  // the key range of each of the thread's rows (empty past NQ)
+    int kf0 = K0, kf1 = K1;
+#pragma unroll
+    for (int k = 0; k < RM; ++k) {
+        const int r = grp + NG * k;
+        o[k] = -0.0f;
+        lo[k] = r < NQ ? rk0[r] : 1;
+        hi[k] = r < NQ ? rk1[r] : 0;
     }
-    __syncthreads();
-    // o[h][i] over the keys in order: the first writes w * v, the rest FMA
-    // (the tail lanes past hd8: o + w * v). Four outputs per thread at once.
-    for (int base = tid; base < G * hd; base += 1024) {
-        float o[4];
-        int hh[4], ii[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int idx = base + 256 * k < G * hd ? base + 256 * k : base;
-            hh[k] = idx / hd;
-            ii[k] = idx - hh[k] * hd;
-            o[k] = __fmul_rn(sc[hh[k] * ATTN_BLOCK], bf16f(kv[ii[k]]));
+    for (int r = 0; r < NQ; ++r)
+        if (rk1[r] >= rk0[r]) {
+            kf0 = rk0[r] > kf0 ? rk0[r] : kf0;
+            kf1 = rk1[r] < kf1 ? rk1[r] : kf1;
         }
-        for (int j = 1; j < nk; ++j) {
+    for (int c0 = K0; c0 <= K1; c0 += AT_KC) {
+        const int nkc = K1 + 1 - c0 < AT_KC ? K1 + 1 - c0 : AT_KC, c1 = c0 + nkc;
+        __syncthreads();  // the previous chunk's (or the scores') reads are done
+        for (int i = tid; i < nkc * PR; i += 256) {
+            const int j = i / PR, c = i - j * PR;
+            *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.vc + (size_t)(c0 + j) * KVD + kvh * HD + 8 * c);
+        }
+        __syncthreads();
+        // The unmasked keys of this chunk, from a multiple of 4 past K0.
+        int f0 = kf0 > c0 ? kf0 : c0, f1 = kf1 + 1 < c1 ? kf1 + 1 : c1;
+        f0 = K0 + ((f0 - K0 + 3) & ~3);
+        if (f1 < f0) f1 = f0;
+        f1 = f0 + ((f1 - f0) & ~3);
+        auto masked = [&](int key) {
+            const float vv = bf16f(kv[(key - c0) * KS + ie]);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float wv = sc[hh[k] * ATTN_BLOCK + j], vv = bf16f(kv[j * KS + ii[k]]);
-                o[k] = ii[k] < hd8 ? __fmaf_rn(wv, vv, o[k]) : __fadd_rn(o[k], __fmul_rn(wv, vv));
+            for (int k = 0; k < RM; ++k) {
+                const int r = grp + NG * k < NQ ? grp + NG * k : NQ - 1;
+                const float nv = __fmaf_rn(sc[r * ATTN_BLOCK + key - K0], vv, o[k]);
+                o[k] = (key >= lo[k] && key <= hi[k]) ? nv : o[k];
+            }
+        };
+        for (int key = c0; key < f0 && key < c1; ++key) masked(key);
+        for (int key = f0; key < f1; key += 4) {
+            float vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vv[u] = bf16f(kv[(key - c0 + u) * KS + ie]);
+            float4 wv[RM];
+#pragma unroll
+            for (int k = 0; k < RM; ++k) {
+                const int r = grp + NG * k < NQ ? grp + NG * k : NQ - 1;
+                wv[k] = *(const float4*)(sc + r * ATTN_BLOCK + key - K0);
+            }
+#pragma unroll
+            for (int k = 0; k < RM; ++k) {
+                o[k] = __fmaf_rn(wv[k].x, vv[0], o[k]);
+                o[k] = __fmaf_rn(wv[k].y, vv[1], o[k]);
+                o[k] = __fmaf_rn(wv[k].z, vv[2], o[k]);
+                o[k] = __fmaf_rn(wv[k].w, vv[3], o[k]);
             }
         }
+        for (int key = f1 > f0 ? f1 : f0; key < c1; ++key)
+            if (key >= c0) masked(key);
+    }
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (base + 256 * k < G * hd) part[hh[k] * pw + ii[k]] = o[k];
+    for (int k = 0; k < RM; ++k) {
+        const int r = grp + NG * k;
+        if (hi[k] < lo[k]) continue;
+        const int s = r / G, h = r - s * G;
+        a.parts[((((size_t)(t0 + s) * a.KV + kvh) * a.nblk) + tbi[s]) * G * pw + h * pw + ie] = o[k];
     }
 }
 
@@ -366,14 +531,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
 }
 
 // gate = gelu(gate) * up (Gemma) or (gate * sigmoid(gate)) * up, gate and up
-// the halves of each token's row of gu [n_tok][2F] (scalar.rs:140-150).
-__global__ void act_kernel(float* __restrict__ gu, int F, int n_tok, int gelu) {
-    const size_t n = (size_t)n_tok * F;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
-        const size_t t = e / F, i = e - t * F;
-        float* g = gu + t * 2 * F + i;
-        const float u = g[F], gv = *g;
-        *g = gelu ? __fmul_rn(gelu_lane(gv), u) : __fmul_rn(__fmul_rn(gv, sigmoid_lane(gv)), u);
+// the halves of token y's row of gu [n_tok][2F] (scalar.rs:140-150).
+__global__ void act_kernel(float* __restrict__ gu, int F, int gelu) {
+    float* g = gu + (size_t)blockIdx.y * 2 * F;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
+        const float u = g[F + i], gv = g[i];
+        g[i] = gelu ? __fmul_rn(gelu_lane(gv), u) : __fmul_rn(__fmul_rn(gv, sigmoid_lane(gv)), u);
     }
 }
 
@@ -401,6 +564,7 @@ struct nngl_model {
     void* work = nullptr;
     uint64_t* row = nullptr;
     size_t lds_attn = 0;
+    int tq = 1;  // tokens per attention tile
     std::string err;
 };
 
@@ -519,10 +683,15 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     m->act = act;
     m->n_batch = n_batch;
     m->nblk = (c.n_ctx + ATTN_BLOCK - 1) / ATTN_BLOCK;
-    m->lds_attn = (size_t)G * hd * 4 + (size_t)G * ATTN_BLOCK * 4 + (size_t)((G + 3) & ~3) * 4 +
-                  (size_t)ATTN_BLOCK * (hd + 8) * 2;
+    if (hd != 32 && hd != 64 && hd != 128 && hd != 256) {
+        m->err = "the attention kernels take head_dim 32, 64, 128 or 256";
+        return 1;
+    }
+    m->tq = G >= AT_NQ ? 1 : AT_NQ / G;
+    const size_t nq = (size_t)m->tq * G;
+    m->lds_attn = nq * hd * 4 + nq * ATTN_BLOCK * 4 + AT_NQ * 4 + (size_t)AT_KC * (hd + 8) * 2;
     if (m->lds_attn > (size_t)LDS_MAX) {
-        m->err = "a 256-key block of K rows and the group's queries exceed the LDS";
+        m->err = "the attention tile exceeds the LDS";
         return 1;
     }
     if (stream) {
@@ -570,8 +739,10 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     NNGL_CHECK(hipMalloc(&m->row, 8));
     const size_t wb = nnh_model_argmax_work_bytes(m->w.back()), ab = nnh_argmax_work_bytes(c.n_vocab);
     NNGL_CHECK(hipMalloc(&m->work, wb > ab ? wb : ab));
-    NNGL_CHECK(hipFuncSetAttribute((const void*)attn_part_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)m->lds_attn));
+    const void* ak = hd == 32 ? (const void*)attn_tile_kernel<32>
+                     : hd == 64 ? (const void*)attn_tile_kernel<64>
+                     : hd == 128 ? (const void*)attn_tile_kernel<128> : (const void*)attn_tile_kernel<256>;
+    NNGL_CHECK(hipFuncSetAttribute(ak, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn));
     // The weights' layouts for this mode and batch, so no forward allocates
     // (and a forward can be captured into a graph).
     for (nnh_weight* wk : m->w)
@@ -609,7 +780,7 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
     const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
     hipStream_t st = m->st;
     embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
-    resid_norm_kernel<<<n, 64, (size_t)E * 4, st>>>(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E,
+    resid_norm_kernel<<<n, RN_T, (size_t)E * 4, st>>>(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E,
                                                     c.rms_eps);
     NNGL_CHECK(hipGetLastError());
     const int n_seq = (int)(pos0 + n_tok);
@@ -646,12 +817,20 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
                    c.rms_eps};
         qkv_post_kernel<<<dim3(n, H + 2 * KV), 64, (size_t)hd * 4, st>>>(qa);
         AttnArgs aa{m->qkv, kcl, vcl, m->parts, m->attn, m->expt, KV, G, hd, QKV, m->nblk, (int)pos0, n_seq,
-                    sliding ? c.window : 0, c.attn_scale};
-        attn_part_kernel<<<dim3(nblk, KV, n), 256, m->lds_attn, st>>>(aa);
+                    sliding ? c.window : 0, n, m->tq, c.attn_scale};
+        const dim3 ag((n + m->tq - 1) / m->tq, KV, nblk);
+        if (hd == 32)
+            attn_tile_kernel<32><<<ag, 256, m->lds_attn, st>>>(aa);
+        else if (hd == 64)
+            attn_tile_kernel<64><<<ag, 256, m->lds_attn, st>>>(aa);
+        else if (hd == 128)
+            attn_tile_kernel<128><<<ag, 256, m->lds_attn, st>>>(aa);
+        else
+            attn_tile_kernel<256><<<ag, 256, m->lds_attn, st>>>(aa);
         attn_merge_kernel<<<dim3(KV, n), 256, 0, st>>>(aa);
         NNGL_CHECK(hipGetLastError());
         if (gemv(m, W[3], m->attn, QD, m->r, E, n_tok)) return 1;
-        resid_norm_kernel<<<n, 64, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed,
+        resid_norm_kernel<<<n, RN_T, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed,
                                                         nullptr, n, E, c.rms_eps);
         if (m->fused_gu) {
             if (gemv(m, W[4], m->normed, E, m->gu, 2 * F, n_tok)) return 1;
@@ -659,13 +838,12 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
                    gemv(m, W[5], m->normed, E, m->gu + F, 2 * F, n_tok)) {
             return 1;
         }
-        const size_t ne = (size_t)n * F;
-        act_kernel<<<(unsigned)std::min<size_t>((ne + 255) / 256, 65536), 256, 0, st>>>(m->gu, F, n, gemma ? 1 : 0);
+        act_kernel<<<dim3((F + 1023) / 1024, n), 256, 0, st>>>(m->gu, F, gemma ? 1 : 0);
         NNGL_CHECK(hipGetLastError());
         if (gemv(m, W[6], m->gu, 2 * F, m->r, E, n_tok)) return 1;
         const bool last = li + 1 == c.n_layer;
         const float* next = last ? m->norms + ns * c.n_layer : m->norms + ns * (li + 1);
-        resid_norm_kernel<<<n, 64, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_ffw : nullptr, next,
+        resid_norm_kernel<<<n, RN_T, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_ffw : nullptr, next,
                                                         last ? m->x : m->normed, m->states + (size_t)li * E, n, E,
                                                         c.rms_eps);
         NNGL_CHECK(hipGetLastError());
