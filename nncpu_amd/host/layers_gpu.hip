@@ -291,16 +291,20 @@ __device__ __forceinline__ bool tok_block(const AttnArgs& a, int t, int b, int& 
 // over the token's own keys of the block, in key order. The workgroup stages
 // the block's K rows (then V rows) AT_KC at a time in LDS for all its rows.
 // Scores: thread (key j, half) holds K row j in registers and runs the
-// 8-lane FMA chains of rows half, half + 2, ... against the queries in LDS
-// (broadcast reads). V sums: thread (lane i of the head, group) keeps the
-// chains o[r][i] of its rows across the chunks, each V value read once.
+// 8-lane FMA chains of its half's rows, the queries (the same for the whole
+// wave) read by scalar loads. V sums: thread (columns, row group) keeps the
+// chains o[r][i] of its rows and columns across the chunks. The LDS moves
+// about 4 bytes per FMA lane when the wave-uniform operand comes from LDS
+// (a broadcast read still returns 64 lanes' data), half the VALU's rate:
+// hence scalar queries, and several columns per weight read.
 constexpr int AT_KC = 128;  // keys per LDS chunk
-constexpr int AT_NQ = 32;   // rows per workgroup at most
+constexpr int AT_NQ = 32;   // rows per workgroup at most (16 at head_dim 256: registers)
+__host__ __device__ constexpr int at_nq(int hd) { return hd >= 256 ? 16 : AT_NQ; }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
-    constexpr int KS = HD + 8, NG = 256 / HD, RM = AT_NQ / NG;
-    static_assert(HD % 8 == 0 && 256 % HD == 0, "head_dim divides 256");
+    constexpr int KS = HD + 8;
+    static_assert(HD % 8 == 0 && 256 % HD == 0 && HD >= 32, "head_dim 32, 64, 128 or 256");
     extern __shared__ __align__(16) float lds[];
     __shared__ int tk0[AT_NQ], tk1[AT_NQ], tbi[AT_NQ], rk0[AT_NQ], rk1[AT_NQ];
     const int kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -326,14 +330,9 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
         rk0[tid] = tk0[tid / G];
         rk1[tid] = tk1[tid / G];
     }
-    float* qs = lds;                              // [NQ][HD]
-    float* sc = qs + NQ * HD;                     // [NQ][256], key k at k - K0
+    float* sc = lds;                              // [NQ][256], key k at k - K0
     float* mh = sc + NQ * ATTN_BLOCK;             // [AT_NQ]
     uint16_t* kv = (uint16_t*)(mh + AT_NQ);       // [AT_KC][KS]
-    for (int i = tid; i < NQ * HD; i += 256) {
-        const int r = i / HD, s = r / G, h = r - s * G, e = i - r * HD;
-        if (t0 + s < a.n_tok) qs[i] = a.qkv[(size_t)(t0 + s) * a.QKV + (size_t)(kvh * G + h) * HD + e];
-    }
     __syncthreads();
     // Scores, chunk by chunk.
     constexpr int PR = HD / 8;  // 16-byte pieces per row
@@ -347,42 +346,54 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
         const int j = tid & (AT_KC - 1), half = tid >> 7;
         if (j < nkc) {
             const int key = c0 + j;
-            // The key's row in registers: as f32 up to head_dim 128 (converted
-            // once for all rows), else as BF16 pairs.
+            // The key's row in registers as f32 up to head_dim 128 (converted
+            // once for all rows); at 256 it is read from LDS with the queries.
             constexpr bool F32ROW = HD <= 128;
+            const uint16_t* krow = kv + j * KS;
             float kf[F32ROW ? HD : 1];
-            uint4 kr[F32ROW ? 1 : PR];
-#pragma unroll
-            for (int c = 0; c < PR; ++c) {
-                const uint4 k8 = *(const uint4*)(kv + j * KS + 8 * c);
-                if (F32ROW) {
-                    const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
-#pragma unroll
-                    for (int l = 0; l < 8; ++l) kf[F32ROW ? 8 * c + l : 0] = bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu);
-                } else {
-                    kr[F32ROW ? 0 : c] = k8;
-                }
-            }
-            for (int r = half; r < NQ; r += 2) {
-                if (key < rk0[r] || key > rk1[r]) continue;
-                const float* qh = qs + r * HD;
-                float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            if (F32ROW) {
 #pragma unroll
                 for (int c = 0; c < PR; ++c) {
-                    const float4 qa = *(const float4*)(qh + 8 * c), qb = *(const float4*)(qh + 8 * c + 4);
-                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-                    if (F32ROW) {
+                    const uint4 k8 = *(const uint4*)(krow + 8 * c);
+                    const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
 #pragma unroll
-                        for (int l = 0; l < 8; ++l) acc[l] = __fmaf_rn(qv[l], kf[F32ROW ? 8 * c + l : 0], acc[l]);
-                    } else {
-                        const uint32_t kw[4] = {kr[F32ROW ? 0 : c].x, kr[F32ROW ? 0 : c].y, kr[F32ROW ? 0 : c].z,
-                                                kr[F32ROW ? 0 : c].w};
-#pragma unroll
-                        for (int l = 0; l < 8; ++l)
-                            acc[l] = __fmaf_rn(qv[l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
-                    }
+                    for (int l = 0; l < 8; ++l)
+                        kf[F32ROW ? 8 * c + l : 0] = bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu);
                 }
-                sc[r * ATTN_BLOCK + key - K0] = __fmul_rn(hsum8(acc), a.scale);
+            }
+            // The two halves take token slots (or, with one token per tile,
+            // alternate heads). A row's queries are the same for the whole
+            // wave: read from global memory at a wave-uniform address (scalar
+            // loads; nothing in this kernel writes them), so the FMAs take
+            // them as scalar operands and only the K rows come from LDS.
+            const int hs = (TQ + 1) / 2;
+            const int ts0 = TQ >= 2 ? half * hs : 0, ts1 = TQ >= 2 ? (half + 1) * hs < TQ ? (half + 1) * hs : TQ : 1;
+            const int h0 = TQ >= 2 ? 0 : half, hstep = TQ >= 2 ? 1 : 2;
+            for (int ts = ts0; ts < ts1; ++ts) {
+                if (key < tk0[ts] || key > tk1[ts]) continue;
+                for (int h = h0; h < G; h += hstep) {
+                    const int r = ts * G + h;
+                    const float* __restrict__ qg =
+                        a.qkv + (size_t)__builtin_amdgcn_readfirstlane((t0 + ts) * a.QKV + (kvh * G + h) * HD);
+                    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int c = 0; c < PR; ++c) {
+                        float qv[8];
+#pragma unroll
+                        for (int l = 0; l < 8; ++l) qv[l] = qg[8 * c + l];
+                        if (F32ROW) {
+#pragma unroll
+                            for (int l = 0; l < 8; ++l) acc[l] = __fmaf_rn(qv[l], kf[F32ROW ? 8 * c + l : 0], acc[l]);
+                        } else {
+                            const uint4 k8 = *(const uint4*)(krow + 8 * c);
+                            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+#pragma unroll
+                            for (int l = 0; l < 8; ++l)
+                                acc[l] = __fmaf_rn(qv[l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
+                        }
+                    }
+                    sc[r * ATTN_BLOCK + key - K0] = __fmul_rn(hsum8(acc), a.scale);
+                }
             }
         }
         __syncthreads();
@@ -431,26 +442,46 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
     }
     // V sums, chunk by chunk: the first key of a row writes w * v, the rest
     // FMA. Each chain starts at -0, so the first key's FMA is exactly w * v
-    // (x + -0 = x for every x, signed zeros included). Keys every active row
-    // of the tile has ([kf0, kf1]) run without masks, four per step (each
-    // row's four weights one 16-byte read, all the step's reads issued
-    // before its FMAs); the keys at the edges only some rows have run masked.
-    const int ie = tid % HD, grp = tid / HD;
-    float o[RM];
-    int lo[RM], hi[RM];  // the key range of each of the thread's rows (empty past NQ)
-    int kf0 = K0, kf1 = K1;
+    // (x + -0 = x for every x, signed zeros included). Thread (row group,
+    // column group) runs the chains of CPT adjacent columns of its rows, so
+    // each weight read (the same for the whole wave: one row group per wave
+    // from head_dim 64) feeds CPT FMAs. Keys every active row of the tile has
+    // ([kf0, kf1]) run without masks, four per step, the next step's reads
+    // issued before this step's FMAs; keys only some rows have run masked.
+    constexpr int CPT = HD >= 64 ? HD / 64 : 1, CG = HD / CPT, RG = 256 / CG;
+    constexpr int RPT = (at_nq(HD) + RG - 1) / RG;
+    const int cg = tid % CG, rg = tid / CG, ie = cg * CPT;
+    float o[RPT][CPT];
 #pragma unroll
-    for (int k = 0; k < RM; ++k) {
-        const int r = grp + NG * k;
-        o[k] = -0.0f;
-        lo[k] = r < NQ ? rk0[r] : 1;
-        hi[k] = r < NQ ? rk1[r] : 0;
-    }
+    for (int k = 0; k < RPT; ++k)
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) o[k][c] = -0.0f;
+    int kf0 = K0, kf1 = K1;
     for (int r = 0; r < NQ; ++r)
         if (rk1[r] >= rk0[r]) {
             kf0 = rk0[r] > kf0 ? rk0[r] : kf0;
             kf1 = rk1[r] < kf1 ? rk1[r] : kf1;
         }
+    const float* wrow[RPT];  // each row's weights, indexed by key (rows past NQ read row NQ - 1)
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) wrow[k] = sc + (rg + RG * k < NQ ? rg + RG * k : NQ - 1) * ATTN_BLOCK - K0;
+    // CPT BF16 values of one V row at the thread's columns.
+    auto vload = [&](int j, float* v) {
+        const uint16_t* p = kv + j * KS + ie;
+        if (CPT == 1) {
+            v[0] = bf16f(p[0]);
+        } else if (CPT == 2) {
+            const uint32_t u = *(const uint32_t*)p;
+            v[0] = bf16f(u & 0xffffu);
+            v[CPT > 1 ? 1 : 0] = bf16f(u >> 16);
+        } else {
+            const uint2 u = *(const uint2*)p;
+            v[0] = bf16f(u.x & 0xffffu);
+            v[CPT > 1 ? 1 : 0] = bf16f(u.x >> 16);
+            v[CPT > 2 ? 2 : 0] = bf16f(u.y & 0xffffu);
+            v[CPT > 3 ? 3 : 0] = bf16f(u.y >> 16);
+        }
+    };
     for (int c0 = K0; c0 <= K1; c0 += AT_KC) {
         const int nkc = K1 + 1 - c0 < AT_KC ? K1 + 1 - c0 : AT_KC, c1 = c0 + nkc;
         __syncthreads();  // the previous chunk's (or the scores') reads are done
@@ -465,42 +496,63 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
         if (f1 < f0) f1 = f0;
         f1 = f0 + ((f1 - f0) & ~3);
         auto masked = [&](int key) {
-            const float vv = bf16f(kv[(key - c0) * KS + ie]);
+            float v[CPT];
+            vload(key - c0, v);
 #pragma unroll
-            for (int k = 0; k < RM; ++k) {
-                const int r = grp + NG * k < NQ ? grp + NG * k : NQ - 1;
-                const float nv = __fmaf_rn(sc[r * ATTN_BLOCK + key - K0], vv, o[k]);
-                o[k] = (key >= lo[k] && key <= hi[k]) ? nv : o[k];
+            for (int k = 0; k < RPT; ++k) {
+                const int r = rg + RG * k < NQ ? rg + RG * k : NQ - 1;
+                const bool on = rg + RG * k < NQ && key >= rk0[r] && key <= rk1[r];
+                const float w = wrow[k][key];
+#pragma unroll
+                for (int c = 0; c < CPT; ++c) {
+                    const float nv = __fmaf_rn(w, v[c], o[k][c]);
+                    o[k][c] = on ? nv : o[k][c];
+                }
             }
         };
         for (int key = c0; key < f0 && key < c1; ++key) masked(key);
-        for (int key = f0; key < f1; key += 4) {
-            float vv[4];
+        if (f0 < f1) {
+            // Two register sets used in turn (no copies): a step's FMAs run
+            // on one while the next step's reads fill the other.
+            float4 wa[RPT], wb[RPT];
+            float va[4][CPT], vb[4][CPT];
+            auto fetch = [&](int key, float4* w, float (*v)[CPT]) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) vv[u] = bf16f(kv[(key - c0 + u) * KS + ie]);
-            float4 wv[RM];
+                for (int k = 0; k < RPT; ++k) w[k] = *(const float4*)(wrow[k] + key);
 #pragma unroll
-            for (int k = 0; k < RM; ++k) {
-                const int r = grp + NG * k < NQ ? grp + NG * k : NQ - 1;
-                wv[k] = *(const float4*)(sc + r * ATTN_BLOCK + key - K0);
+                for (int u = 0; u < 4; ++u) vload(key - c0 + u, v[u]);
+            };
+            auto step = [&](const float4* w, const float (*v)[CPT]) {
+#pragma unroll
+                for (int k = 0; k < RPT; ++k) {
+                    const float w4[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+#pragma unroll
+                        for (int c = 0; c < CPT; ++c) o[k][c] = __fmaf_rn(w4[u], v[u][c], o[k][c]);
+                }
+            };
+            fetch(f0, wa, va);
+            int key = f0;
+            for (; key + 8 <= f1; key += 8) {
+                fetch(key + 4, wb, vb);
+                step(wa, va);
+                if (key + 8 < f1) fetch(key + 8, wa, va);
+                step(wb, vb);
             }
-#pragma unroll
-            for (int k = 0; k < RM; ++k) {
-                o[k] = __fmaf_rn(wv[k].x, vv[0], o[k]);
-                o[k] = __fmaf_rn(wv[k].y, vv[1], o[k]);
-                o[k] = __fmaf_rn(wv[k].z, vv[2], o[k]);
-                o[k] = __fmaf_rn(wv[k].w, vv[3], o[k]);
-            }
+            if (key < f1) step(wa, va);
         }
         for (int key = f1 > f0 ? f1 : f0; key < c1; ++key)
             if (key >= c0) masked(key);
     }
 #pragma unroll
-    for (int k = 0; k < RM; ++k) {
-        const int r = grp + NG * k;
-        if (hi[k] < lo[k]) continue;
+    for (int k = 0; k < RPT; ++k) {
+        const int r = rg + RG * k;
+        if (r >= NQ || rk1[r] < rk0[r]) continue;
         const int s = r / G, h = r - s * G;
-        a.parts[((((size_t)(t0 + s) * a.KV + kvh) * a.nblk) + tbi[s]) * G * pw + h * pw + ie] = o[k];
+        float* dst = a.parts + ((((size_t)(t0 + s) * a.KV + kvh) * a.nblk) + tbi[s]) * G * pw + h * pw + ie;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) dst[c] = o[k][c];
     }
 }
 
@@ -631,10 +683,10 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
         return 1;
     }
     const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, G = H / KV, F = c.n_ff;
-    if (E % 32 || E > 8192 || hd % 8 || hd > 512 || F % 32 || G > 32 || c.n_vocab < 1 || c.arch < NNG_GEMMA3 ||
+    if (E % 32 || E > 8192 || hd % 8 || hd > 512 || F % 32 || G > at_nq(hd) || c.n_vocab < 1 || c.arch < NNG_GEMMA3 ||
         c.arch > NNG_QWEN2) {
         m->err = "n_embd and n_ff must be multiples of 32 (n_embd at most 8192), head_dim a multiple of 8 up to "
-                 "512, at most 32 query heads per KV head";
+                 "512, at most 32 query heads per KV head (16 at head_dim 256)";
         return 1;
     }
     const int QD = H * hd, KVD = KV * hd, QKV = QD + 2 * KVD;
@@ -687,9 +739,9 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
         m->err = "the attention kernels take head_dim 32, 64, 128 or 256";
         return 1;
     }
-    m->tq = G >= AT_NQ ? 1 : AT_NQ / G;
+    m->tq = G >= at_nq(hd) ? 1 : at_nq(hd) / G;
     const size_t nq = (size_t)m->tq * G;
-    m->lds_attn = nq * hd * 4 + nq * ATTN_BLOCK * 4 + AT_NQ * 4 + (size_t)AT_KC * (hd + 8) * 2;
+    m->lds_attn = nq * ATTN_BLOCK * 4 + AT_NQ * 4 + (size_t)AT_KC * (hd + 8) * 2;
     if (m->lds_attn > (size_t)LDS_MAX) {
         m->err = "the attention tile exceeds the LDS";
         return 1;
