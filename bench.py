@@ -495,6 +495,63 @@ def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int =
     return res
 
 
+def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128, n_layer: int = 28):
+    """Batch-1 greedy decode of the Qwen2.5-7B shape (config 5's model) on the
+    device forward: the prompt in 16-token batches, then one decode step per
+    token (nngl_decode_step_dev + nngl_greedy_next_dev, captured once in a
+    HIP graph and replayed; no host round trip per token). Random weights as
+    qwen_prefill's; every matmul in each activation mode of `acts`. tok/s
+    beside the weight bytes a token streams and the matmul-only ceiling at
+    the measured HBM read rate."""
+    import torch
+    from nncpu_amd.models import DeviceForward, norm_stride, qwen25_7b_config
+    cfg = qwen25_7b_config(n_ctx=n_prompt + n_gen, n_layer=n_layer, wtype=2 if dtype == 2 else 1)
+    d, ff, nkv, hd, vocab = cfg.n_embd, cfg.n_ff, cfg.n_kv, cfg.head_dim, cfg.n_vocab
+    qkv = d + 2 * nkv * hd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xDEC0 + dtype)
+
+    def weight(rows, cols):
+        w = torch.randn(rows * cols, generator=g, device="cuda").mul_(0.02)
+        torch.cuda.synchronize()
+        out = N.Weight.encode_dev(dtype, w.data_ptr(), rows, cols)
+        del w
+        return out
+
+    weights = []
+    for _ in range(n_layer):
+        weights += [weight(qkv, d), None, None, weight(d, d), weight(2 * ff, d), None, weight(d, ff)]
+    lm_head = weight(vocab, d)
+    weights.append(lm_head)
+    rng = np.random.default_rng(0xDEC0 + dtype)
+    norms = (1.0 + 0.1 * rng.standard_normal(norm_stride(cfg) * n_layer + d)).astype(np.float32)
+    biases = (0.02 * rng.standard_normal(n_layer * qkv)).astype(np.float32)
+    prompt = rng.integers(0, vocab, n_prompt).astype(np.int32)
+    wbytes = sum(w.split_bytes() for w in weights if w is not None)
+    out = []
+    for act in acts:
+        s = torch.cuda.Stream()
+        fwd = DeviceForward(cfg, weights, norms, biases, lm_head, n_batch=16, act=act, stream=s.cuda_stream)
+        fwd.generate_graph(prompt, 8, stream=s)  # warm-up: layouts, scratch, clocks
+        toks, secs, _, _ = fwd.generate_graph(prompt, n_gen, stream=s)
+        fwd.free()
+        tok_s = (n_gen - 1) / secs
+        res = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} Qwen2.5-7B-shaped decode, {n_layer} layers",
+                   activations={N.ACT_F32: "f32 (bit-exact drop-in)", N.ACT_I8: "int8 blocks (nncpu Q8_0)",
+                                N.ACT_MXI8: "MX int8 blocks"}[act],
+                   prompt=n_prompt, generated=n_gen, tok_s=round(tok_s, 1), ms_per_token=round(1e3 / tok_s, 3),
+                   weight_bytes_per_token=wbytes, weights_gbs=round(wbytes * tok_s / 1e9, 1),
+                   timing="graph replays of one decode step per token, host clock around the replays")
+        res["matmul_ceiling_tok_s"] = round(HBM_PEAK_GBS * 1e9 / wbytes, 1)
+        res["frac_of_ceiling"] = round(tok_s / res["matmul_ceiling_tok_s"], 3)
+        log(f"qwen_decode: {res}")
+        out.append(res)
+    for w in weights:
+        if w is not None:
+            w.free()
+    return out
+
+
 def host_info():
     """nproc, the CPU model and the physical cores this process may use (the
     box's CPU share: OMP_NUM_THREADS when the environment sets it)."""
@@ -700,7 +757,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
-                    choices=["q4_sweep", "prefill", "qwen_prefill", "q8_vocab", "verify", "decode_f32", "gemma_decode",
+                    choices=["q4_sweep", "prefill", "qwen_prefill", "qwen_decode", "q8_vocab", "verify", "decode_f32", "gemma_decode",
                              "bf16", "peaks", "traffic", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -736,6 +793,8 @@ def main():
         extra["prefill_m512_mx"] = measure_cases(args, N, prefill_cases, N.ACT_MXI8, "prefill_mx")
     if args.workload in ("qwen_prefill", "all"):
         extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d, a) for d in (1, 2) for a in (N.ACT_MXI8, N.ACT_I8)]
+    if args.workload in ("qwen_decode", "all"):
+        extra["qwen_decode"] = [r for d in (1, 2) for r in qwen_decode(args, N, d, (N.ACT_F32, N.ACT_I8))]
     if args.workload in ("q8_vocab", "all"):
         extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
         extra["q8_vocab_m1_f32_bit_exact"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_F32,

@@ -796,9 +796,21 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1r_kernel(F32Mat m, const float*
 
 // The streamed kernel's conditions: enough rows to fill the GPU at 32 lanes
 // per row, x (staged whole in LDS) at most 64 KB and 16-byte aligned.
-static bool m1r_fits(int rows, int nb, const float* x) {
-    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && (size_t)nb * 32 * 4 <= (size_t)F32_V2_MAX_LDS &&
-           ((uintptr_t)x & 15) == 0;
+// x staged whole: up to 150 KB of LDS (rows of about 37000 columns).
+constexpr size_t M1R_MAX_LDS = 150 * 1024;
+static size_t m1r_lds(int dt, int nb) { return (size_t)32 * m1w_stride_host(nb) * 4 + (dt == 2 ? (size_t)nb * 4 : 0); }
+static bool m1r_fits(int dt, int rows, int nb, const float* x) {
+    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && m1r_lds(dt, nb) <= M1R_MAX_LDS && ((uintptr_t)x & 15) == 0;
+}
+// The streamed kernel's instances may take more than the default 64 KB of
+// dynamic LDS (set once per instance).
+template <int DT, int NT, int PF>
+static void m1r_allow_lds() {
+    static const bool once = [] {
+        return hipFuncSetAttribute((const void*)gemv_f32_m1r_kernel<DT, NT, PF>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)M1R_MAX_LDS) == hipSuccess;
+    }();
+    (void)once;
 }
 
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
@@ -810,17 +822,20 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
     const int ngp = DT == 1 ? (nb + 7) / 8 : (nb + 15) / 16;
     const size_t q4 = DT == 2 ? (size_t)nb * 4 : 0;
     const dim3 block(256);
-    if (m1r_fits(rows, nb, x)) {
+    if (m1r_fits(DT, rows, nb, x)) {
         // Many long rows: the streamed kernel, 16 rows per workgroup (8
         // waves) when that still gives a workgroup per CU, else 8.
-        const size_t lds = (size_t)32 * m1w_stride_host(nb) * 4 + (DT == 2 ? (size_t)nb * 4 : 0);
+        const size_t lds = m1r_lds(DT, nb);
         // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8,
         // the fastest of 2..8 at Llama's shapes.
         constexpr int PF = DT == 1 ? 6 : 3;
-        if (rows >= 16 * cu_count())
+        if (rows >= 16 * cu_count()) {
+            m1r_allow_lds<DT, 512, PF>();
             gemv_f32_m1r_kernel<DT, 512, PF><<<dim3(ceil_div(rows, 16)), dim3(512), lds, st>>>(m, x, y);
-        else
+        } else {
+            m1r_allow_lds<DT, 256, PF>();
             gemv_f32_m1r_kernel<DT, 256, PF><<<dim3(ceil_div(rows, 8)), dim3(256), lds, st>>>(m, x, y);
+        }
         return;
     }
     if (nb >= M1W_MIN_NB) {
@@ -1146,7 +1161,7 @@ void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uin
                      size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st) {
     // Q4 block sums, except for the one-vector kernel, which forms its own.
-    const auto one = [&](const float* xt) { return !v2 && (nb <= M1_MAX_NB || m1r_fits(rows, nb, xt)); };
+    const auto one = [&](const float* xt) { return !v2 && (nb <= M1_MAX_NB || m1r_fits(dtype, rows, nb, xt)); };
     if (dtype == 2 && !(n_tok == 1 && one(x))) launch_block_sums(x, x_stride, nb, n_tok, xsum, st);
     // The 8-lane kernel keeps x in LDS: at most 64 KB of it per launch.
     int per = 4;

@@ -69,13 +69,36 @@ __device__ double row_sumsq(const float* v, int dim, int lane) {
     const int body = dim & ~7;
     float a = 0.0f;
     if (lane < 8) {
+        // The lane's values 32 at a time, each batch read while the previous
+        // batch's FMAs run (the chain itself is sequential); two named
+        // buffers in turn, so no register array is indexed at run time.
+        constexpr int B = 32;
         int i = lane;
-        for (; i + 56 < body; i += 64) {
-            float t[8];
+        float ta[B], tb[B];
+        auto full = [&](int at) { return at + 8 * (B - 1) < body; };
+        if (full(i)) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) t[k] = v[i + 8 * k];
+            for (int k = 0; k < B; ++k) ta[k] = v[i + 8 * k];
+            while (true) {
+                const bool nb = full(i + 8 * B);
+                if (nb) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) a = __fmaf_rn(t[k], t[k], a);
+                    for (int k = 0; k < B; ++k) tb[k] = v[i + 8 * B + 8 * k];
+                }
+#pragma unroll
+                for (int k = 0; k < B; ++k) a = __fmaf_rn(ta[k], ta[k], a);
+                i += 8 * B;
+                if (!nb) break;
+                const bool na = full(i + 8 * B);
+                if (na) {
+#pragma unroll
+                    for (int k = 0; k < B; ++k) ta[k] = v[i + 8 * B + 8 * k];
+                }
+#pragma unroll
+                for (int k = 0; k < B; ++k) a = __fmaf_rn(tb[k], tb[k], a);
+                i += 8 * B;
+                if (!na) break;
+            }
         }
         for (; i < body; i += 8) a = __fmaf_rn(v[i], v[i], a);
     }
@@ -210,7 +233,8 @@ struct QkvArgs {
     const float* sn;
     uint16_t* kc;            // this layer's cache rows: [n_ctx][KVD]
     uint16_t* vc;
-    int H, KV, hd, QKV, pos0, rope_mode;
+    const int* posp;         // the first token's position in device memory, or NULL: pos0
+    int H, KV, hd, QKV, pos0, rope_mode, n_ctx;
     float eps;
 };
 
@@ -233,10 +257,11 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvArgs a) {
             for (int i = lane; i < hd; i += 64) v[i] = __fmul_rn(__fmul_rn(v[i], sc), g[i]);
             __syncthreads();
         }
-        const int half = hd / 2, pos = a.pos0 + t;
+        const int half = hd / 2, pos = (a.posp ? *a.posp : a.pos0) + t;
         const int stride = a.rope_mode == NNG_ROPE_NORM ? 2 : 1, partner = a.rope_mode == NNG_ROPE_NORM ? 1 : half;
-        const float* cs = a.cs + (size_t)pos * half;
-        const float* sn = a.sn + (size_t)pos * half;
+        const int pr = pos < a.n_ctx ? pos : a.n_ctx - 1;
+        const float* cs = a.cs + (size_t)pr * half;
+        const float* sn = a.sn + (size_t)pr * half;
         for (int i = lane; i < half; i += 64) {
             const int p = i * stride;
             const float x0 = v[p], x1 = v[p + partner], c = cs[i], sv = sn[i];
@@ -245,10 +270,11 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvArgs a) {
         }
         __syncthreads();
     }
+    const int pos = (a.posp ? *a.posp : a.pos0) + t;
     if (kind == 0) {
         for (int i = lane; i < hd; i += 64) src[i] = v[i];
-    } else {
-        uint16_t* dst = (kind == 1 ? a.kc : a.vc) + (size_t)(a.pos0 + t) * a.KV * hd + head * hd;
+    } else if (pos < a.n_ctx) {  // a device position past the context writes nothing
+        uint16_t* dst = (kind == 1 ? a.kc : a.vc) + (size_t)pos * a.KV * hd + head * hd;
         for (int i = lane; i < hd; i += 64) dst[i] = to_bf16(v[i]);
     }
 }
@@ -260,9 +286,19 @@ struct AttnArgs {
     float* parts;            // [n_tok][KV][nblk][G][hd + 2]
     float* out;              // [n_tok][H * hd]
     const uint64_t* expt;    // glibc_expf's table
-    int KV, G, hd, QKV, nblk, pos0, n_seq, window, n_tok, tq;
+    const int* posp;         // the first token's position in device memory, or NULL: pos0
+    int KV, G, hd, QKV, nblk, pos0, n_seq, window, n_tok, tq, n_ctx;
     float scale;
 };
+
+// The batch's first position and the sequence length after it (both from
+// device memory for a replayed decode step), the length capped at the
+// context so no read leaves the cache.
+__device__ __forceinline__ void attn_pos(const AttnArgs& a, int& p0, int& n_seq) {
+    p0 = a.posp ? *a.posp : a.pos0;
+    n_seq = a.posp ? p0 + a.n_tok : a.n_seq;
+    n_seq = n_seq < a.n_ctx ? n_seq : a.n_ctx;
+}
 
 // model/embed.rs:14-30, the causal branch (gemma3.cpp attn_span).
 __device__ __forceinline__ void attn_span(int window, int pos, int n_seq, int& first, int& last) {
@@ -273,10 +309,11 @@ __device__ __forceinline__ void attn_span(int window, int pos, int n_seq, int& f
 
 // Token t's keys in 256-key block b (false when its span has none), and
 // the index of b among its span's blocks.
-__device__ __forceinline__ bool tok_block(const AttnArgs& a, int t, int b, int& k0, int& k1, int& bi) {
+__device__ __forceinline__ bool tok_block(const AttnArgs& a, int p0, int n_seq, int t, int b, int& k0, int& k1,
+                                          int& bi) {
     if (t >= a.n_tok) return false;
     int first, last;
-    attn_span(a.window, a.pos0 + t, a.n_seq, first, last);
+    attn_span(a.window, p0 + t, n_seq, first, last);
     if (b < first / ATTN_BLOCK || b > last / ATTN_BLOCK) return false;
     k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
     k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
@@ -310,10 +347,12 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
     const int kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.G, TQ = a.tq, NQ = TQ * G, t0 = blockIdx.x * TQ, pw = HD + 2, KVD = a.KV * HD;
     // The tile's key range in the block (every thread computes it).
+    int p0, n_seq;
+    attn_pos(a, p0, n_seq);
     int K0 = 1 << 30, K1 = -1;
     for (int s = 0; s < TQ; ++s) {
         int k0, k1, bi;
-        const bool on = tok_block(a, t0 + s, b, k0, k1, bi);
+        const bool on = tok_block(a, p0, n_seq, t0 + s, b, k0, k1, bi);
         if (tid == 0) {
             tk0[s] = on ? k0 : 1;
             tk1[s] = on ? k1 : 0;
@@ -556,13 +595,107 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
     }
 }
 
+// One token's partial (decode) for query head x of KV head y over its block
+// b0 + z: attn_tile_kernel's arithmetic for a single row, spread over more
+// workgroups (one per head and block) for latency: the block's K rows, then
+// its V rows, staged whole in LDS; thread j the score of key j (query by
+// scalar loads), the first maximum and weight sum as there, thread i the V
+// chain of column i (from -0, so the first key's FMA is w * v exactly).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+    constexpr int KS = HD + 8, PR = HD / 8;
+    extern __shared__ __align__(16) float lds[];
+    float* sc = lds;                                   // [256]
+    uint16_t* kv = (uint16_t*)(lds + ATTN_BLOCK + 4);  // [256][KS]
+    __shared__ float mh;
+    const int hh = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.G, pw = HD + 2, KVD = a.KV * HD;
+    int p0, n_seq, first, last;
+    attn_pos(a, p0, n_seq);
+    attn_span(a.window, p0, n_seq, first, last);
+    const int b = first / ATTN_BLOCK + (int)blockIdx.z;
+    if (b > last / ATTN_BLOCK) return;
+    const int k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
+    const int k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
+    const int nk = k1 + 1 - k0;
+    for (int i = tid; i < nk * PR; i += 256) {
+        const int j = i / PR, c = i - j * PR;
+        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.kc + (size_t)(k0 + j) * KVD + kvh * HD + 8 * c);
+    }
+    __syncthreads();
+    if (tid < nk) {
+        const float* __restrict__ qg = a.qkv + (size_t)__builtin_amdgcn_readfirstlane((kvh * G + hh) * HD);
+        const uint16_t* kr = kv + tid * KS;
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < PR; ++c) {
+            const uint4 k8 = *(const uint4*)(kr + 8 * c);
+            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l)
+                acc[l] = __fmaf_rn(qg[8 * c + l], bf16f((kw[l >> 1] >> (16 * (l & 1))) & 0xffffu), acc[l]);
+        }
+        sc[tid] = __fmul_rn(hsum8(acc), a.scale);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float m = -INFINITY;
+        for (int j = 4 * lane; j < 4 * lane + 4 && j < nk; ++j)
+            if (m < sc[j]) m = sc[j];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float other = __shfl_xor(m, o, 64);
+            const float lo = (lane & o) ? other : m, hi = (lane & o) ? m : other;
+            m = lo < hi ? hi : lo;
+        }
+        if (lane == 0) mh = sc[0] != sc[0] ? sc[0] : m;
+    }
+    __syncthreads();
+    if (tid < nk) sc[tid] = exp_lane(__fsub_rn(sc[tid], mh));
+    __syncthreads();
+    float* part = a.parts + ((size_t)kvh * a.nblk + blockIdx.z) * G * pw + hh * pw;
+    if (wave == 0) {
+        const int body = nk & ~7;
+        float vs = 0.0f;
+        if (lane < 8)
+            for (int j = lane; j < body; j += 8) vs = __fadd_rn(vs, sc[j]);
+        float ls = hsum8_lanes(vs);
+        if (lane == 0) {
+            for (int j = body; j < nk; ++j) ls = __fadd_rn(ls, sc[j]);
+            part[HD] = mh;
+            part[HD + 1] = ls;
+        }
+    }
+    for (int i = tid; i < nk * PR; i += 256) {
+        const int j = i / PR, c = i - j * PR;
+        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.vc + (size_t)(k0 + j) * KVD + kvh * HD + 8 * c);
+    }
+    __syncthreads();
+    if (tid < HD) {
+        float o = -0.0f;
+        int j = 0;
+        for (; j + 4 <= nk; j += 4) {
+            const float4 w = *(const float4*)(sc + j);
+            const float v0 = bf16f(kv[j * KS + tid]), v1 = bf16f(kv[(j + 1) * KS + tid]);
+            const float v2 = bf16f(kv[(j + 2) * KS + tid]), v3 = bf16f(kv[(j + 3) * KS + tid]);
+            o = __fmaf_rn(w.x, v0, o);
+            o = __fmaf_rn(w.y, v1, o);
+            o = __fmaf_rn(w.z, v2, o);
+            o = __fmaf_rn(w.w, v3, o);
+        }
+        for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(kv[j * KS + tid]), o);
+        part[tid] = o;
+    }
+}
+
 // The partials of token y's heads sharing KV head x merged in block order
 // (scalar.rs:521-537, with glibc's expf), then each head's o / l
 // (scalar.rs:539-548) into out[t][head * hd ..].
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const int t = blockIdx.y, kvh = blockIdx.x, hd = a.hd, G = a.G, pw = hd + 2, hd8 = hd & ~7;
-    int first, last;
-    attn_span(a.window, a.pos0 + t, a.n_seq, first, last);
+    int p0, n_seq, first, last;
+    attn_pos(a, p0, n_seq);
+    attn_span(a.window, p0 + t, n_seq, first, last);
     const int nb = last / ATTN_BLOCK - first / ATTN_BLOCK + 1;
     const float* P = a.parts + ((size_t)t * a.KV + kvh) * a.nblk * G * pw;
     for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
@@ -592,6 +725,15 @@ __global__ void act_kernel(float* __restrict__ gu, int F, int gelu) {
     }
 }
 
+// The argmax row as the next token, recorded, and the position advanced.
+__global__ void next_token_kernel(const uint64_t* row, int32_t* tok, int* pos, int32_t* out, int* step) {
+    const int32_t t = (int32_t)*row;
+    *tok = t;
+    out[*step] = t;
+    *step += 1;
+    *pos += 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -615,7 +757,7 @@ struct nngl_model {
     int32_t* tok_host = nullptr;  // pinned staging of the host forward's token ids
     void* work = nullptr;
     uint64_t* row = nullptr;
-    size_t lds_attn = 0;
+    size_t lds_attn = 0, lds_dec = 0;
     int tq = 1;  // tokens per attention tile
     std::string err;
 };
@@ -795,6 +937,11 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
                      : hd == 64 ? (const void*)attn_tile_kernel<64>
                      : hd == 128 ? (const void*)attn_tile_kernel<128> : (const void*)attn_tile_kernel<256>;
     NNGL_CHECK(hipFuncSetAttribute(ak, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn));
+    m->lds_dec = (size_t)(ATTN_BLOCK + 4) * 4 + (size_t)ATTN_BLOCK * (hd + 8) * 2;
+    const void* dk = hd == 32 ? (const void*)attn_decode_kernel<32>
+                     : hd == 64 ? (const void*)attn_decode_kernel<64>
+                     : hd == 128 ? (const void*)attn_decode_kernel<128> : (const void*)attn_decode_kernel<256>;
+    NNGL_CHECK(hipFuncSetAttribute(dk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_dec));
     // The weights' layouts for this mode and batch, so no forward allocates
     // (and a forward can be captured into a graph).
     for (nnh_weight* wk : m->w)
@@ -819,9 +966,12 @@ static int gemv(nngl_model* m, const nnh_weight* w, const float* x, size_t xs, f
 // the last token's state after each layer kept. Asynchronous on the model's
 // stream; allocates nothing, so it can be captured into a HIP graph. The
 // caller keeps positions in order (earlier positions' K/V written first).
-int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, size_t pos0) {
+// posp (device, or NULL): the first position read by the kernels at run
+// time, so one captured step replays at successive positions; the attention
+// grid then covers the whole context and the blocks past the span exit.
+static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, size_t pos0, const int* posp) {
     const nng_config& c = m->c;
-    if (n_tok == 0 || n_tok > (size_t)m->n_batch || pos0 + n_tok > (size_t)c.n_ctx) {
+    if (n_tok == 0 || n_tok > (size_t)m->n_batch || (!posp && pos0 + n_tok > (size_t)c.n_ctx)) {
         m->err = "n_tok out of range or context full";
         return 1;
     }
@@ -835,7 +985,7 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
     resid_norm_kernel<<<n, RN_T, (size_t)E * 4, st>>>(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E,
                                                     c.rms_eps);
     NNGL_CHECK(hipGetLastError());
-    const int n_seq = (int)(pos0 + n_tok);
+    const int n_seq = posp ? c.n_ctx : (int)(pos0 + n_tok);
     const int nblk = (n_seq - 1) / ATTN_BLOCK + 1;
     for (int li = 0; li < c.n_layer; ++li) {
         const float* nr = m->norms + ns * li;
@@ -860,18 +1010,30 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
                    m->sn + (sliding ? 0 : tab),
                    kcl,
                    vcl,
+                   posp,
                    H,
                    KV,
                    hd,
                    QKV,
                    (int)pos0,
                    c.rope_mode,
+                   c.n_ctx,
                    c.rms_eps};
         qkv_post_kernel<<<dim3(n, H + 2 * KV), 64, (size_t)hd * 4, st>>>(qa);
-        AttnArgs aa{m->qkv, kcl, vcl, m->parts, m->attn, m->expt, KV, G, hd, QKV, m->nblk, (int)pos0, n_seq,
-                    sliding ? c.window : 0, n, m->tq, c.attn_scale};
+        AttnArgs aa{m->qkv, kcl, vcl, m->parts, m->attn, m->expt, posp, KV, G, hd, QKV, m->nblk, (int)pos0,
+                    n_seq, sliding ? c.window : 0, n, m->tq, c.n_ctx, c.attn_scale};
         const dim3 ag((n + m->tq - 1) / m->tq, KV, nblk);
-        if (hd == 32)
+        if (n == 1) {
+            const dim3 dg(G, KV, nblk);
+            if (hd == 32)
+                attn_decode_kernel<32><<<dg, 256, m->lds_dec, st>>>(aa);
+            else if (hd == 64)
+                attn_decode_kernel<64><<<dg, 256, m->lds_dec, st>>>(aa);
+            else if (hd == 128)
+                attn_decode_kernel<128><<<dg, 256, m->lds_dec, st>>>(aa);
+            else
+                attn_decode_kernel<256><<<dg, 256, m->lds_dec, st>>>(aa);
+        } else if (hd == 32)
             attn_tile_kernel<32><<<ag, 256, m->lds_attn, st>>>(aa);
         else if (hd == 64)
             attn_tile_kernel<64><<<ag, 256, m->lds_attn, st>>>(aa);
@@ -900,6 +1062,39 @@ int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, siz
                                                         c.rms_eps);
         NNGL_CHECK(hipGetLastError());
     }
+    return 0;
+}
+
+int nngl_forward_dev(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, size_t pos0) {
+    return forward_impl(m, tokens_dev, n_tok, pos0, nullptr);
+}
+
+// One decode step for replay from a HIP graph: the token at tok_dev (device)
+// at the position *pos_dev (device), read when the kernels run. A position
+// at or past the context writes nothing and reads no key past it; the caller
+// bounds its replays.
+int nngl_decode_step_dev(nngl_model* m, const int32_t* tok_dev, const int* pos_dev) {
+    return forward_impl(m, tok_dev, 1, 0, pos_dev);
+}
+
+// The greedy token after a decode step, on the device: model_argmax of the
+// step's hidden state (forward.rs:989-1011) into *tok_dev, out[*step_dev]
+// = that token, then *step_dev and *pos_dev advanced. Asynchronous, allocates
+// nothing (capturable with the step).
+int nngl_greedy_next_dev(nngl_model* m, int32_t* tok_dev, int* pos_dev, int32_t* out, int* step_dev) {
+    int rc;
+    if (m->act == NNH_ACT_F32) {
+        rc = nnh_model_argmax_dev(m->w.back(), m->x, m->logits, m->work, m->row, m->st);
+    } else {
+        rc = nnh_gemv_batch_dev(m->w.back(), m->x, m->c.n_embd, m->logits, m->c.n_vocab, 1, m->act, m->st);
+        if (rc == NNH_OK) rc = nnh_argmax_dev(m->logits, m->c.n_vocab, m->work, m->row, m->st);
+    }
+    if (rc != NNH_OK) {
+        m->err = std::string("argmax: ") + nnh_last_error();
+        return 1;
+    }
+    next_token_kernel<<<1, 1, 0, m->st>>>(m->row, tok_dev, pos_dev, out, step_dev);
+    NNGL_CHECK(hipGetLastError());
     return 0;
 }
 

@@ -70,6 +70,8 @@ def _lib():
     L.nngl_read.argtypes, L.nngl_read.restype = [vp, sz, vp, vp, vp, vp], i32
     L.nngl_pos.argtypes, L.nngl_pos.restype = [vp], sz
     L.nngl_set_pos.argtypes, L.nngl_set_pos.restype = [vp, sz], i32
+    L.nngl_decode_step_dev.argtypes, L.nngl_decode_step_dev.restype = [vp, vp, vp], i32
+    L.nngl_greedy_next_dev.argtypes, L.nngl_greedy_next_dev.restype = [vp, vp, vp, vp, vp], i32
     return L
 
 
@@ -280,6 +282,55 @@ class DeviceForward:
             tok = self.argmax_last(1)
         _, _, kc, vc = self.read(0, caches=True)
         return out, np.concatenate(hashes) if hashes else np.zeros(0, np.uint64), kc, vc
+
+    def generate_graph(self, prompt: np.ndarray, n_gen: int, batch: int = 16, stream=None):
+        """The prompt as in `generate`, then the greedy decode with one step
+        (nngl_decode_step_dev + nngl_greedy_next_dev: the token, position and
+        step counter in device memory) captured in a HIP graph on the model's
+        stream (`stream`, the torch stream it was created on) and replayed per
+        token. (tokens, decode seconds, K cache, V cache)."""
+        import time
+
+        import torch
+        self.set_pos(0)
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        if len(prompt) + n_gen > self.cfg.n_ctx:
+            raise ValueError("the prompt and the generated tokens exceed the context")
+        last = 0
+        for p in range(0, len(prompt), batch):
+            chunk = prompt[p:p + batch]
+            self.forward(chunk)
+            last = len(chunk)
+        first = self.argmax_last(last)
+        dev = "cuda"
+        tok = torch.tensor([first], dtype=torch.int32, device=dev)
+        pos = torch.tensor([len(prompt)], dtype=torch.int32, device=dev)
+        step = torch.tensor([1], dtype=torch.int32, device=dev)
+        out = torch.zeros(n_gen, dtype=torch.int32, device=dev)
+        out[0] = first
+        torch.cuda.synchronize()
+        L = self._lib
+
+        def one():
+            self._check(L.nngl_decode_step_dev(self._h, tok.data_ptr(), pos.data_ptr()))
+            self._check(L.nngl_greedy_next_dev(self._h, tok.data_ptr(), pos.data_ptr(), out.data_ptr(),
+                                               step.data_ptr()))
+
+        secs = 0.0
+        if n_gen > 1:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                one()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(n_gen - 1):
+                g.replay()
+            torch.cuda.synchronize()
+            secs = time.perf_counter() - t0
+            del g
+        toks = out.cpu().numpy()
+        _, _, kc, vc = self.read(0, caches=True)
+        return toks, secs, kc, vc
 
     def free(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:

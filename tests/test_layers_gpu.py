@@ -128,3 +128,27 @@ def test_forward_dev_graph_replay(N):
             assert np.array_equal(got_st.view(np.uint32), want_st.view(np.uint32)), i
     finally:
         dev.free()
+
+
+def test_decode_graph_matches_eager(N):
+    # One decode step (the token, position and step counter in device memory)
+    # captured in a HIP graph and replayed per token: the same tokens and the
+    # same K/V cache as the eager decode, across a 256-key block boundary.
+    import torch
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=256, n_head=4, n_kv=2, n_ff=512, n_vocab=1024, n_ctx=300)
+    model = Model.random(cfg, seed=0x5D)
+    prompt = np.random.default_rng(7).integers(0, cfg.n_vocab, 250).astype(np.int32)
+    n_gen = 20
+    print("decode graph vs eager", flush=True)
+    tc, _, kc, vc = model.cpu_generate(prompt, n_gen)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=16, stream=s.cuda_stream)
+    try:
+        tg, _, kg, vg = dev.generate_graph(prompt, n_gen, stream=s)
+        te, _, ke, ve = dev.generate(prompt, n_gen)
+    finally:
+        dev.free()
+    assert np.array_equal(te, tc) and np.array_equal(ke, kc) and np.array_equal(ve, vc)
+    assert np.array_equal(tg, tc), (tg, tc)
+    assert np.array_equal(kg, kc) and np.array_equal(vg, vc)
