@@ -1,4 +1,4 @@
-// A Gemma-3 / Llama / Qwen2 forward pass on the CPU whose every weight
+// A Gemma-3 / Llama / Qwen2 / Qwen3 forward pass on the CPU whose every weight
 // matmul goes through a pluggable gemv (the reference's `gemv_batch` /
 // `model_gemv` dispatch):
 // the decode and prefill caller of the quantized matmul, restated from
@@ -368,7 +368,7 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
     m->acc.assign(group * pw, 0.0f);
 
     // Embedding rows times sqrt(n_embd) for Gemma, else 1 (load.rs:565-566).
-    const bool gemma = c.arch == NNG_GEMMA3;
+    const bool gemma = c.arch == NNG_GEMMA3, qk_norm = gemma || c.arch == NNG_QWEN3;
     const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
     const float* ff = m->rope_ff.empty() ? nullptr : m->rope_ff.data();
     for (size_t t = 0; t < n_tok; ++t) {
@@ -403,7 +403,7 @@ int nng_forward(nng_model* m, const int32_t* tokens, size_t n_tok) {
                 for (size_t i = 0; i < kv_dim; ++i) m->v[t * kv_dim + i] += bl[q_dim + kv_dim + i];
             }
         }
-        if (gemma) {
+        if (qk_norm) {  // forward.rs:274-290: Gemma, Qwen3
             rmsnorm_gamma_multi(m->q.data(), m->q.data(), n_tok * q_dim, hd, q_norm, c.rms_eps);
             rmsnorm_gamma_multi(m->k.data(), m->k.data(), n_tok * kv_dim, hd, k_norm, c.rms_eps);
         }

@@ -15,13 +15,13 @@ struct nng_config {
     int wtype;  // the matrices' format (the embedding table's too): 2 = Q4, else Q8_0
     // NNG_GEMMA3: embedding rows times sqrt(n_embd), per-head q / k RMSNorm,
     // post-attention and post-FFW RMSNorm, GELU(gate) * up. NNG_LLAMA,
-    // NNG_QWEN2: none of those, SiLU(gate) * up; Qwen2 adds the q / k / v
-    // projection biases (nng_set_biases). (load.rs:538-566, forward.rs:255-
-    // 290, 742-809.)
+    // NNG_QWEN2, NNG_QWEN3: none of those, SiLU(gate) * up; Qwen2 adds the
+    // q / k / v projection biases (nng_set_biases), Qwen3 the per-head q / k
+    // RMSNorm. (load.rs:538-566, forward.rs:255-290, 742-809.)
     int arch;
     int rope_mode;  // NNG_ROPE_NEOX (lane i with i + n_rot/2) or NNG_ROPE_NORM (2i with 2i + 1)
 };
-enum { NNG_GEMMA3 = 0, NNG_LLAMA = 1, NNG_QWEN2 = 2 };
+enum { NNG_GEMMA3 = 0, NNG_LLAMA = 1, NNG_QWEN2 = 2, NNG_QWEN3 = 3 };
 enum { NNG_ROPE_NEOX = 0, NNG_ROPE_NORM = 1 };
 
 struct nng_model;

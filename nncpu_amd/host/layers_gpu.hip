@@ -1,7 +1,7 @@
 // The forward of gemma3.cpp (nng_forward: crates/nncpu/src/model/forward.rs
 // 197-439 attention, 719-841 layer, 848-965 model_forward) on the GPU, for
 // any number of tokens and any of its architectures (Gemma-3, Llama,
-// Qwen2): every weight matmul through the library (nnh_gemv_batch_dev, in
+// Qwen2, Qwen3): every weight matmul through the library (nnh_gemv_batch_dev, in
 // any activation mode), everything between the matmuls as the kernels
 // below, each value computed by the CPU restatement's operations in its
 // order and rounding (-ffp-contract=off; __f*_rn where it matters). With
@@ -826,7 +826,7 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     }
     const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, G = H / KV, F = c.n_ff;
     if (E % 32 || E > 8192 || hd % 8 || hd > 512 || F % 32 || G > at_nq(hd) || c.n_vocab < 1 || c.arch < NNG_GEMMA3 ||
-        c.arch > NNG_QWEN2) {
+        c.arch > NNG_QWEN3) {
         m->err = "n_embd and n_ff must be multiples of 32 (n_embd at most 8192), head_dim a multiple of 8 up to "
                  "512, at most 32 query heads per KV head (16 at head_dim 256)";
         return 1;
@@ -977,7 +977,7 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
     }
     const int E = c.n_embd, hd = c.head_dim, H = c.n_head, KV = c.n_kv, G = H / KV, F = c.n_ff;
     const int QD = H * hd, KVD = KV * hd, QKV = QD + 2 * KVD, n = (int)n_tok;
-    const bool gemma = c.arch == NNG_GEMMA3;
+    const bool gemma = c.arch == NNG_GEMMA3, qk_norm = gemma || c.arch == NNG_QWEN3;
     const size_t ns = norm_stride_l(c), half = hd / 2, tab = (size_t)c.n_ctx * half;
     const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
     hipStream_t st = m->st;
@@ -1004,8 +1004,8 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
         uint16_t* vcl = m->vc + (size_t)li * c.n_ctx * KVD;
         QkvArgs qa{m->qkv,
                    m->bias ? m->bias + (size_t)li * QKV : nullptr,
-                   gemma ? q_norm : nullptr,
-                   gemma ? k_norm : nullptr,
+                   qk_norm ? q_norm : nullptr,
+                   qk_norm ? k_norm : nullptr,
                    m->cs + (sliding ? 0 : tab),
                    m->sn + (sliding ? 0 : tab),
                    kcl,

@@ -1,10 +1,11 @@
-"""Gemma-3, Llama and Qwen2 forward passes around the GPU matmul.
+"""Gemma-3, Llama, Qwen2 and Qwen3 forward passes around the GPU matmul.
 
 One model, two runs:
 
 * `Model.cpu_generate`: the CPU forward of nncpu_amd/host/gemma3.cpp
-  (crates/nncpu/src/model/forward.rs restated, for the three
-  architectures: Qwen2's q/k/v biases, SwiGLU, Llama's adjacent-pair RoPE)
+  (crates/nncpu/src/model/forward.rs restated, for the four
+  architectures: Qwen2's q/k/v biases, Qwen3's per-head q/k norms, SwiGLU,
+  Llama's adjacent-pair RoPE)
   with every weight matmul through `nnh_gemv_batch`, the prompt in 16-token
   batches (session/engine.rs:362-380) and then greedy tokens;
 * `DeviceForward`: the same forward resident on the GPU
@@ -23,7 +24,7 @@ import numpy as np
 from . import ACT_F32, Q4S, Q8_0, Weight
 from .gemma import NngConfig, NngGpuCtx, _gemma_lib, matrix_shapes
 
-ARCH_GEMMA3, ARCH_LLAMA, ARCH_QWEN2 = 0, 1, 2
+ARCH_GEMMA3, ARCH_LLAMA, ARCH_QWEN2, ARCH_QWEN3 = 0, 1, 2, 3
 ROPE_NEOX, ROPE_NORM = 0, 1
 
 
@@ -45,6 +46,15 @@ def qwen2_config(n_layer: int, n_embd: int, n_head: int, n_kv: int, n_ff: int, n
     """A Qwen2 architecture (NeoX RoPE, q/k/v projection biases)."""
     cfg = llama_config(n_layer, n_embd, n_head, n_kv, n_ff, n_vocab, n_ctx, head_dim, rope_base, rms_eps, wtype)
     cfg.arch, cfg.rope_mode = ARCH_QWEN2, ROPE_NEOX
+    return cfg
+
+
+def qwen3_config(n_layer: int, n_embd: int, n_head: int, n_kv: int, n_ff: int, n_vocab: int, n_ctx: int,
+                 head_dim: int | None = None, rope_base: float = 1e6, rms_eps: float = 1e-6,
+                 wtype: int = Q8_0) -> NngConfig:
+    """A Qwen3 architecture (NeoX RoPE, per-head q/k RMSNorm, no biases)."""
+    cfg = llama_config(n_layer, n_embd, n_head, n_kv, n_ff, n_vocab, n_ctx, head_dim, rope_base, rms_eps, wtype)
+    cfg.arch, cfg.rope_mode = ARCH_QWEN3, ROPE_NEOX
     return cfg
 
 

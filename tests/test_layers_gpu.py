@@ -63,6 +63,16 @@ def test_llama_layers_match_cpu_forward(N):
     run_both(model, prompt, 8)
 
 
+def test_qwen3_layers_match_cpu_forward(N):
+    # Qwen3: per-head q / k RMSNorm (forward.rs:274-290) with NeoX RoPE, no
+    # biases, head_dim 128 (past n_embd / n_head).
+    from nncpu_amd.models import Model, qwen3_config
+    cfg = qwen3_config(n_layer=2, n_embd=256, n_head=4, n_kv=2, n_ff=512, n_vocab=768, n_ctx=48, head_dim=128)
+    model = Model.random(cfg, seed=0x03)
+    prompt = np.random.default_rng(6).integers(0, cfg.n_vocab, 18).astype(np.int32)
+    run_both(model, prompt, 5)
+
+
 def test_llama_rope_frequency_factors(N):
     # Llama 3's RoPE frequency factors divide each pair's angle (kernels/mod.rs
     # 712-716), in both forwards' tables.
