@@ -13,20 +13,12 @@
 // dequantized operands, to within f64 rounding.
 
 #include "common.h"
+#include "q8_act.h"
 
 namespace nnh {
 namespace {
 
 // ---- activation quantizer: quant.rs:31-60 on the device ----------------------
-
-// Round half to even, then Rust's saturating `as i32` (quant.rs:18-29).
-__device__ __forceinline__ int rint_sat(float v) {
-    float r = __builtin_rintf(v);
-    if (!(r == r)) return 0;
-    if (r >= 2147483648.0f) return 2147483647;
-    if (r <= -2147483648.0f) return (int)0x80000000;
-    return (int)r;
-}
 
 // One 32-lane half-wave per block of 32 values.
 __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, size_t x_stride, int cols,
@@ -40,18 +32,13 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restri
     const int bb = valid ? blk : 0;
     const int t = bb / nb, b = bb - t * nb;
     float v = x[(size_t)t * x_stride + 32 * (size_t)b + k];
-    // amax: the reference skips NaNs (`v.abs() > amax` is false for them);
-    // fmaxf does too, and max is order-free over the rest.
-    float a = fabsf(v);
-    a = (a == a) ? a : 0.0f;
+    float a = q8_abs(v);
 #pragma unroll
     for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
-    // Times the reciprocal of 127, rounded to BF16 (quant.rs:49-53).
-    uint32_t sbits = f32_to_bf16(__fmul_rn(a, 1.0f / 127.0f));
-    float scale = bf16f(sbits);
-    float inv = scale > 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
-    int qi = rint_sat(__fmul_rn(v, inv));
-    qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+    const Q8Scale qs = q8_scale(a);
+    const uint32_t sbits = qs.bits;
+    const float scale = qs.scale;
+    const int qi = q8_quant(v, qs.inv);
     int qsum = qi;
 #pragma unroll
     for (int m = 16; m >= 1; m >>= 1) qsum += __shfl_xor(qsum, m, 32);

@@ -43,6 +43,7 @@
 #include "gemma3.h"
 #include "nncpu_hip.h"
 #include "ops_dev.h"
+#include "q8_act.h"
 
 namespace {
 
@@ -108,6 +109,101 @@ __device__ double row_sumsq(const float* v, int dim, int lane) {
     return s;
 }
 
+// A matmul's one-row input written by the kernel that produces it, in the
+// library's int8 activation layout (nnh_act_layout_ex, NNH_ACT_I8, one row):
+// quants [cols], BF16 block scales [cols / 32], then (scale, scale * sum of
+// the block's quants) per block as f64. The values are nncpu's Q8_0 encoder
+// (q8_act.h, the library quantizer's own steps), so the bits are those of
+// quantizing the f32 row afterwards. q == NULL: nothing is written.
+struct QOut {
+    int8_t* q;
+    uint16_t* s;
+    double* sx;
+};
+
+// Lane exchanges by DPP (a VALU operand modifier, no LDS round trip): 0xB1
+// quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141 row_half_mirror (lane
+// i <-> 7 - i within 8), 0x140 row_mirror (i <-> 15 - i within 16). After
+// the first k of them every lane holds the max / sum over its aligned group
+// of 2, 4, 8, 16 lanes (max and integer sums do not depend on the order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float max8(float a) {
+    a = fmaxf(a, dpp_f<0xB1>(a));
+    a = fmaxf(a, dpp_f<0x4E>(a));
+    return fmaxf(a, dpp_f<0x141>(a));
+}
+__device__ __forceinline__ int sum8(int a) {
+    a += dpp_i<0xB1>(a);
+    a += dpp_i<0x4E>(a);
+    return a + dpp_i<0x141>(a);
+}
+
+// A thread's pieces k = 0 .. K-1, piece k being values 4i .. 4i+3 of the row
+// with i = i0 + k * stride (i0 & 7 == lane & 7, stride a multiple of 8), so a
+// block is one piece of each of 8 consecutive lanes. Every lane of the wave
+// calls it, pieces at i >= n4 holding zeros (a whole block is in range or
+// not); each step runs over all pieces before the next, so the pieces'
+// chains overlap, and only the stores are conditional.
+template <int K>
+__device__ __forceinline__ void q8_pieces(const float4 (&p)[K], int i0, int stride, int n4, const QOut& qo) {
+    float a[K];
+    nnh::Q8Scale s[K];
+    int q[K][4], qs[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        a[k] = max8(fmaxf(fmaxf(nnh::q8_abs(p[k].x), nnh::q8_abs(p[k].y)),
+                          fmaxf(nnh::q8_abs(p[k].z), nnh::q8_abs(p[k].w))));
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        s[k] = nnh::q8_scale(a[k]);
+        q[k][0] = nnh::q8_quant(p[k].x, s[k].inv);
+        q[k][1] = nnh::q8_quant(p[k].y, s[k].inv);
+        q[k][2] = nnh::q8_quant(p[k].z, s[k].inv);
+        q[k][3] = nnh::q8_quant(p[k].w, s[k].inv);
+        qs[k] = sum8(q[k][0] + q[k][1] + q[k][2] + q[k][3]);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = i0 + k * stride;
+        if (i >= n4) continue;
+        ((uint32_t*)qo.q)[i] = (uint32_t)(q[k][0] & 255) | (uint32_t)(q[k][1] & 255) << 8 |
+                               (uint32_t)(q[k][2] & 255) << 16 | (uint32_t)(q[k][3] & 255) << 24;
+        if ((i & 7) == 0) {
+            const int b = i >> 3;
+            qo.s[b] = (uint16_t)s[k].bits;
+            qo.sx[2 * b] = (double)s[k].scale;
+            qo.sx[2 * b + 1] = (double)s[k].scale * (double)qs[k];  // exact: s_x * sum(q_x)
+        }
+    }
+}
+
+// Value j of the row, a block being one half-wave (j & 31 == lane & 31, all
+// 32 lanes active).
+__device__ __forceinline__ void q8_value(float v, int j, const QOut& qo) {
+    float a = max8(nnh::q8_abs(v));
+    a = fmaxf(a, dpp_f<0x140>(a));
+    a = fmaxf(a, __shfl_xor(a, 16, 64));
+    const nnh::Q8Scale s = nnh::q8_scale(a);
+    const int q = nnh::q8_quant(v, s.inv);
+    int qs = sum8(q);
+    qs += dpp_i<0x140>(qs);
+    qs += __shfl_xor(qs, 16, 64);
+    qo.q[j] = (int8_t)q;
+    if ((j & 31) == 0) {
+        const int b = j >> 5;
+        qo.s[b] = (uint16_t)s.bits;
+        qo.sx[2 * b] = (double)s.scale;
+        qo.sx[2 * b + 1] = (double)s.scale * (double)qs;
+    }
+}
+
 // Embedding rows (gemma3.cpp embed_row, kernels/mod.rs:917-954): token t's
 // row of the split-layout table times `scale` into x[t].
 __global__ void embed_kernel(const int32_t* __restrict__ tok, const uint8_t* __restrict__ table, int wtype,
@@ -137,15 +233,20 @@ __global__ void embed_kernel(const int32_t* __restrict__ tok, const uint8_t* __r
 // One workgroup of 256 threads per row (dim a multiple of 4, at most 8192):
 //   r == NULL: y = rmsnorm(x) * gamma (y may be x);
 //   else: x += (post ? rmsnorm(r) * post : r), written back, the last row's
-//   new x copied to rec (if not NULL), then y = rmsnorm(x) * gamma (y may be x).
+//   new x copied to rec (if not NULL), then y = rmsnorm(x) * gamma (y may be x);
+//   qo.q != NULL (one row, dim a multiple of 32): y also quantized into qo.
 // rmsnorm_gamma_multi (scalar.rs:270-292): y = (x * scale) * gamma. Every
 // thread loads its 16-byte pieces at once; the sums of squares are the 8
 // FMA lanes of wave 0 over the row in LDS.
-constexpr int RN_T = 256, RN_K = 8;  // threads; 16-byte pieces per thread (8192 floats)
+// RN_K: 16-byte pieces per thread, the fewest of 1, 2, 4, 8 that cover the
+// row (launch_resid_norm), so no thread carries empty pieces through the
+// norm or the quantizer.
+constexpr int RN_T = 256;  // threads
+template <int RN_K>
 __global__ __launch_bounds__(RN_T) void resid_norm_kernel(float* x, const float* __restrict__ r,
                                                           const float* __restrict__ post, const float* gamma,
                                                           float* y, float* __restrict__ rec, int n_rows, int dim,
-                                                          float eps) {
+                                                          float eps, QOut qo) {
     extern __shared__ __align__(16) float lds[];
     __shared__ float scale_s;
     float* v = lds;        // the row being normed
@@ -210,18 +311,34 @@ __global__ __launch_bounds__(RN_T) void resid_norm_kernel(float* x, const float*
     __syncthreads();
     const float sc = scale_s;
     float4* yr = (float4*)(y + (size_t)row * dim);
+    float4 o[RN_K];
 #pragma unroll
     for (int k = 0; k < RN_K; ++k) {
         const int i = tid + k * RN_T;
+        o[k] = float4{0.0f, 0.0f, 0.0f, 0.0f};
         if (i < n4) {
-            float4 o;
-            o.x = __fmul_rn(__fmul_rn(xv[k].x, sc), gv[k].x);
-            o.y = __fmul_rn(__fmul_rn(xv[k].y, sc), gv[k].y);
-            o.z = __fmul_rn(__fmul_rn(xv[k].z, sc), gv[k].z);
-            o.w = __fmul_rn(__fmul_rn(xv[k].w, sc), gv[k].w);
-            yr[i] = o;
+            o[k].x = __fmul_rn(__fmul_rn(xv[k].x, sc), gv[k].x);
+            o[k].y = __fmul_rn(__fmul_rn(xv[k].y, sc), gv[k].y);
+            o[k].z = __fmul_rn(__fmul_rn(xv[k].z, sc), gv[k].z);
+            o[k].w = __fmul_rn(__fmul_rn(xv[k].w, sc), gv[k].w);
+            yr[i] = o[k];
         }
     }
+    if (qo.q) q8_pieces<RN_K>(o, tid, RN_T, n4, qo);
+}
+
+static void launch_resid_norm(float* x, const float* r, const float* post, const float* gamma, float* y,
+                              float* rec, int n_rows, int dim, float eps, QOut qo, hipStream_t st) {
+    const size_t lds = (size_t)dim * (r && post ? 8 : 4);
+    const int pieces = (dim / 4 + RN_T - 1) / RN_T;
+    if (pieces <= 1)
+        resid_norm_kernel<1><<<n_rows, RN_T, lds, st>>>(x, r, post, gamma, y, rec, n_rows, dim, eps, qo);
+    else if (pieces <= 2)
+        resid_norm_kernel<2><<<n_rows, RN_T, lds, st>>>(x, r, post, gamma, y, rec, n_rows, dim, eps, qo);
+    else if (pieces <= 4)
+        resid_norm_kernel<4><<<n_rows, RN_T, lds, st>>>(x, r, post, gamma, y, rec, n_rows, dim, eps, qo);
+    else
+        resid_norm_kernel<8><<<n_rows, RN_T, lds, st>>>(x, r, post, gamma, y, rec, n_rows, dim, eps, qo);
 }
 
 struct QkvArgs {
@@ -595,14 +712,69 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
     }
 }
 
+// Batch u0 .. u0 + U - 1 of a thread's 16-byte pieces of cache rows k0 ..
+// k0 + nk - 1 (KV head kvh's HD columns; nk >= 1): every load issued before
+// any is used, then stored into LDS rows of HD + 8 halves. Loads and stores
+// are unconditional (a conditional store lets the compiler sink its load
+// into the branch, one round trip per piece): LDS rows nk .. 255 get copies
+// of row nk - 1 and are never read.
+template <int HD, int U>
+__device__ __forceinline__ void kv_load(uint4 (&r)[U], const uint16_t* __restrict__ src, int k0, int nk, int KVD,
+                                        int kvh, int tid, int u0) {
+    constexpr int PR = HD / 8;
+    // A uniform base and 32-bit offsets: one address register per load.
+    const uint16_t* base = src + (size_t)k0 * KVD + kvh * HD;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = tid + 256 * (u0 + u), j = i / PR, c = i % PR;
+        r[u] = *(const uint4*)(base + (uint32_t)((j < nk ? j : nk - 1) * KVD + 8 * c));
+    }
+}
+template <int HD, int U>
+__device__ __forceinline__ void kv_store(const uint4 (&r)[U], uint16_t* kv, int tid, int u0) {
+    constexpr int PR = HD / 8, KS = HD + 8;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = tid + 256 * (u0 + u), j = i / PR, c = i % PR;
+        *(uint4*)(kv + j * KS + 8 * c) = r[u];
+    }
+}
+
+// Eight keys' weights and one V column's values (LDS rows of KS halves),
+// and their FMAs into a chain in key order.
+struct V8 {
+    float4 w0, w1;
+    float v[8];
+    template <int KS>
+    __device__ __forceinline__ void load(const float* sc, const uint16_t* col, int j) {
+        w0 = *(const float4*)(sc + j);
+        w1 = *(const float4*)(sc + j + 4);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = bf16f(col[(j + r) * KS]);
+    }
+    __device__ __forceinline__ float fma(float o) const {
+        o = __fmaf_rn(w0.x, v[0], o);
+        o = __fmaf_rn(w0.y, v[1], o);
+        o = __fmaf_rn(w0.z, v[2], o);
+        o = __fmaf_rn(w0.w, v[3], o);
+        o = __fmaf_rn(w1.x, v[4], o);
+        o = __fmaf_rn(w1.y, v[5], o);
+        o = __fmaf_rn(w1.z, v[6], o);
+        return __fmaf_rn(w1.w, v[7], o);
+    }
+};
+
 // One token's partial (decode) for query head x of KV head y over its block
 // b0 + z: attn_tile_kernel's arithmetic for a single row, spread over more
-// workgroups (one per head and block) for latency: the block's K rows, then
-// its V rows, staged whole in LDS; thread j the score of key j (query by
-// scalar loads), the first maximum and weight sum as there, thread i the V
-// chain of column i (from -0, so the first key's FMA is w * v exactly).
+// workgroups (one per head and block) for latency: the block's K and V rows
+// staged whole in LDS, together up to head_dim 128 (each thread's loads
+// issued at once: one round trip), at 256 V after the scores; thread j the
+// score of key j (query by scalar loads), the first maximum and weight sum
+// as there, thread i the V chain of column i (from -0, so the first key's
+// FMA is w * v exactly). Its LDS (the staged rows) allows at most two
+// workgroups per CU, so the registers are budgeted for two waves per SIMD.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(AttnArgs a) {
     constexpr int KS = HD + 8, PR = HD / 8;
     extern __shared__ __align__(16) float lds[];
     float* sc = lds;                                   // [256]
@@ -618,9 +790,25 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const int k0 = first > b * ATTN_BLOCK ? first : b * ATTN_BLOCK;
     const int k1 = last < b * ATTN_BLOCK + ATTN_BLOCK - 1 ? last : b * ATTN_BLOCK + ATTN_BLOCK - 1;
     const int nk = k1 + 1 - k0;
-    for (int i = tid; i < nk * PR; i += 256) {
-        const int j = i / PR, c = i - j * PR;
-        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.kc + (size_t)(k0 + j) * KVD + kvh * HD + 8 * c);
+    // Pieces per thread: PR (256 rows), in NB batches. Up to head_dim 128 the
+    // V rows have an LDS region of their own and are staged with the K rows;
+    // at 256 they replace the K rows after the scores.
+    constexpr int U = PR < 16 ? PR : 16, NB = PR / U;
+    constexpr bool KV2 = HD <= 128;
+    uint16_t* vv = KV2 ? kv + ATTN_BLOCK * KS : kv;
+    if constexpr (KV2) {
+        uint4 rk[U], rv[U];
+        kv_load<HD, U>(rk, a.kc, k0, nk, KVD, kvh, tid, 0);
+        kv_load<HD, U>(rv, a.vc, k0, nk, KVD, kvh, tid, 0);
+        kv_store<HD, U>(rk, kv, tid, 0);
+        kv_store<HD, U>(rv, vv, tid, 0);
+    } else {
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt) {
+            uint4 r[U];
+            kv_load<HD, U>(r, a.kc, k0, nk, KVD, kvh, tid, bt * U);
+            kv_store<HD, U>(r, kv, tid, bt * U);
+        }
     }
     __syncthreads();
     if (tid < nk) {
@@ -666,32 +854,48 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
             part[HD + 1] = ls;
         }
     }
-    for (int i = tid; i < nk * PR; i += 256) {
-        const int j = i / PR, c = i - j * PR;
-        *(uint4*)(kv + j * KS + 8 * c) = *(const uint4*)(a.vc + (size_t)(k0 + j) * KVD + kvh * HD + 8 * c);
+    if constexpr (!KV2) {
+        // The K rows were last read before the barrier after the scores.
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt) {
+            uint4 r[U];
+            kv_load<HD, U>(r, a.vc, k0, nk, KVD, kvh, tid, bt * U);
+            kv_store<HD, U>(r, kv, tid, bt * U);
+        }
     }
     __syncthreads();
     if (tid < HD) {
+        // Keys in order, 8 per step; the next step's LDS reads are issued
+        // before this step's FMAs (two named buffers, no copies).
         float o = -0.0f;
+        const int body = nk & ~7;
+        const uint16_t* vc = vv + tid;
         int j = 0;
-        for (; j + 4 <= nk; j += 4) {
-            const float4 w = *(const float4*)(sc + j);
-            const float v0 = bf16f(kv[j * KS + tid]), v1 = bf16f(kv[(j + 1) * KS + tid]);
-            const float v2 = bf16f(kv[(j + 2) * KS + tid]), v3 = bf16f(kv[(j + 3) * KS + tid]);
-            o = __fmaf_rn(w.x, v0, o);
-            o = __fmaf_rn(w.y, v1, o);
-            o = __fmaf_rn(w.z, v2, o);
-            o = __fmaf_rn(w.w, v3, o);
+        if (body) {
+            V8 a, b;
+            a.load<KS>(sc, vc, 0);
+            for (; j + 16 <= body; j += 16) {
+                b.load<KS>(sc, vc, j + 8);
+                o = a.fma(o);
+                if (j + 16 < body) a.load<KS>(sc, vc, j + 16);
+                o = b.fma(o);
+            }
+            if (j < body) {
+                o = a.fma(o);
+                j += 8;
+            }
         }
-        for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(kv[j * KS + tid]), o);
+        for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(vv[j * KS + tid]), o);
         part[tid] = o;
     }
 }
 
 // The partials of token y's heads sharing KV head x merged in block order
 // (scalar.rs:521-537, with glibc's expf), then each head's o / l
-// (scalar.rs:539-548) into out[t][head * hd ..].
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+// (scalar.rs:539-548) into out[t][head * hd ..]; qo.q != NULL (one token):
+// the output also quantized into qo (head_dim a multiple of 32, so every
+// half-wave of an iteration holds one block).
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, QOut qo) {
     const int t = blockIdx.y, kvh = blockIdx.x, hd = a.hd, G = a.G, pw = hd + 2, hd8 = hd & ~7;
     int p0, n_seq, first, last;
     attn_pos(a, p0, n_seq);
@@ -711,18 +915,33 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
             al = __fadd_rn(__fmul_rn(al, ca), __fmul_rn(bl, cb));
         }
         const float inv = al > 0.0f ? __fdiv_rn(1.0f, al) : 0.0f;
-        a.out[(size_t)t * (a.KV * G * hd) + (size_t)(kvh * G + h) * hd + i] = __fmul_rn(o, inv);
+        const float v = __fmul_rn(o, inv);
+        a.out[(size_t)t * (a.KV * G * hd) + (size_t)(kvh * G + h) * hd + i] = v;
+        if (qo.q) q8_value(v, kvh * G * hd + idx, qo);
     }
 }
 
 // gate = gelu(gate) * up (Gemma) or (gate * sigmoid(gate)) * up, gate and up
-// the halves of token y's row of gu [n_tok][2F] (scalar.rs:140-150).
-__global__ void act_kernel(float* __restrict__ gu, int F, int gelu) {
-    float* g = gu + (size_t)blockIdx.y * 2 * F;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
-        const float u = g[F + i], gv = g[i];
-        g[i] = gelu ? __fmul_rn(gelu_lane(gv), u) : __fmul_rn(__fmul_rn(gv, sigmoid_lane(gv)), u);
+// the halves of token y's row of gu [n_tok][2F] (scalar.rs:140-150); four
+// values per thread (F a multiple of 32); qo.q != NULL (one token): the
+// result also quantized into qo.
+__device__ __forceinline__ float act1(float g, float u, int gelu) {
+    return gelu ? __fmul_rn(gelu_lane(g), u) : __fmul_rn(__fmul_rn(g, sigmoid_lane(g)), u);
+}
+__global__ __launch_bounds__(256) void act_kernel(float* __restrict__ gu, int F, int gelu, QOut qo) {
+    float4* g = (float4*)(gu + (size_t)blockIdx.y * 2 * F);
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, F4 = F / 4;
+    const bool ok = i < F4;
+    float4 o[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+    if (ok) {
+        const float4 gv = g[i], u = g[F4 + i];
+        o[0].x = act1(gv.x, u.x, gelu);
+        o[0].y = act1(gv.y, u.y, gelu);
+        o[0].z = act1(gv.z, u.z, gelu);
+        o[0].w = act1(gv.w, u.w, gelu);
+        g[i] = o[0];
     }
+    if (qo.q) q8_pieces<1>(o, i, 0, F4, qo);
 }
 
 // The argmax row as the next token, recorded, and the position advanced.
@@ -759,6 +978,14 @@ struct nngl_model {
     uint64_t* row = nullptr;
     size_t lds_attn = 0, lds_dec = 0;
     int tq = 1;  // tokens per attention tile
+    // One-token forwards in NNH_ACT_I8: the int8 inputs of the matmuls
+    // written by their producer kernels (n_embd wide: q/k/v, gate/up and
+    // lm_head; the attention output; the FFN activation), one row each in
+    // the library's layout at these offsets (s, sx).
+    uint8_t *qa_e = nullptr, *qa_a = nullptr, *qa_f = nullptr;
+    size_t qo_e[2] = {}, qo_a[2] = {}, qo_f[2] = {};
+    bool qfuse = true;    // nngl_set_fused_quant
+    bool q_last = false;  // the last forward left the lm_head input in qa_e
     std::string err;
 };
 
@@ -767,7 +994,8 @@ const char* nngl_error(nngl_model* m) { return m ? m->err.c_str() : "no model"; 
 void nngl_free(nngl_model* m) {
     if (!m) return;
     void* bufs[] = {m->norms, m->bias, m->cs,    m->sn,     m->expt,   m->kc,     m->vc,   m->x,   m->normed,
-                    m->r,     m->qkv,  m->attn, m->gu,     m->parts,  m->states, m->logits, m->tok, m->work, m->row};
+                    m->r,     m->qkv,  m->attn, m->gu,     m->parts,  m->states, m->logits, m->tok, m->work, m->row,
+                    m->qa_e,  m->qa_a, m->qa_f};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->tok_host) (void)hipHostFree(m->tok_host);
@@ -931,13 +1159,26 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     NNGL_CHECK(hipMalloc(&m->tok, nb * 4));
     NNGL_CHECK(hipHostMalloc(&m->tok_host, nb * 4));
     NNGL_CHECK(hipMalloc(&m->row, 8));
+    if (act == NNH_ACT_I8) {
+        uint8_t** bufs[3] = {&m->qa_e, &m->qa_a, &m->qa_f};
+        size_t* offs[3] = {m->qo_e, m->qo_a, m->qo_f};
+        const int cols[3] = {E, QD, F};
+        for (int k = 0; k < 3; ++k) {
+            size_t bytes = 0;
+            if (nnh_act_layout_ex(NNH_ACT_I8, cols[k], 1, &offs[k][0], &offs[k][1], &bytes) != NNH_OK) {
+                m->err = std::string("act layout: ") + nnh_last_error();
+                return 1;
+            }
+            NNGL_CHECK(hipMalloc(bufs[k], bytes));
+        }
+    }
     const size_t wb = nnh_model_argmax_work_bytes(m->w.back()), ab = nnh_argmax_work_bytes(c.n_vocab);
     NNGL_CHECK(hipMalloc(&m->work, wb > ab ? wb : ab));
     const void* ak = hd == 32 ? (const void*)attn_tile_kernel<32>
                      : hd == 64 ? (const void*)attn_tile_kernel<64>
                      : hd == 128 ? (const void*)attn_tile_kernel<128> : (const void*)attn_tile_kernel<256>;
     NNGL_CHECK(hipFuncSetAttribute(ak, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn));
-    m->lds_dec = (size_t)(ATTN_BLOCK + 4) * 4 + (size_t)ATTN_BLOCK * (hd + 8) * 2;
+    m->lds_dec = (size_t)(ATTN_BLOCK + 4) * 4 + (size_t)(hd <= 128 ? 2 : 1) * ATTN_BLOCK * (hd + 8) * 2;
     const void* dk = hd == 32 ? (const void*)attn_decode_kernel<32>
                      : hd == 64 ? (const void*)attn_decode_kernel<64>
                      : hd == 128 ? (const void*)attn_decode_kernel<128> : (const void*)attn_decode_kernel<256>;
@@ -958,6 +1199,23 @@ static int gemv(nngl_model* m, const nnh_weight* w, const float* x, size_t xs, f
         return 1;
     }
     return 0;
+}
+
+// The matmul of a one-token forward: on the int8 row `qa` (written by the
+// producer kernel) when not NULL, else on the f32 row x.
+static int gemv_q(nngl_model* m, const nnh_weight* w, const uint8_t* qa, const float* x, size_t xs, float* y,
+                  size_t ys, size_t n) {
+    if (!qa) return gemv(m, w, x, xs, y, ys, n);
+    if (nnh_gemv_act_dev(w, NNH_ACT_I8, qa, 1, y, ys, m->st) != NNH_OK) {
+        m->err = std::string("gemv: ") + nnh_last_error();
+        return 1;
+    }
+    return 0;
+}
+
+static QOut qout(uint8_t* base, const size_t* off) {
+    return base ? QOut{(int8_t*)base, (uint16_t*)(base + off[0]), (double*)(base + off[1])}
+                : QOut{nullptr, nullptr, nullptr};
 }
 
 // The forward of n_tok tokens (device ids at tokens_dev) at positions pos0
@@ -981,9 +1239,13 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
     const size_t ns = norm_stride_l(c), half = hd / 2, tab = (size_t)c.n_ctx * half;
     const float embd_scale = gemma ? std::sqrt((float)E) : 1.0f;
     hipStream_t st = m->st;
+    // One token in NNH_ACT_I8: the producers quantize the matmul inputs.
+    const bool fq = m->qfuse && m->act == NNH_ACT_I8 && n == 1 && m->qa_e;
+    uint8_t *qe = fq ? m->qa_e : nullptr, *qt = fq ? m->qa_a : nullptr, *qf = fq ? m->qa_f : nullptr;
+    const QOut oe = qout(qe, m->qo_e), oa = qout(qt, m->qo_a), of = qout(qf, m->qo_f);
+    m->q_last = false;
     embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
-    resid_norm_kernel<<<n, RN_T, (size_t)E * 4, st>>>(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E,
-                                                    c.rms_eps);
+    launch_resid_norm(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E, c.rms_eps, oe, st);
     NNGL_CHECK(hipGetLastError());
     const int n_seq = posp ? c.n_ctx : (int)(pos0 + n_tok);
     const int nblk = (n_seq - 1) / ATTN_BLOCK + 1;
@@ -994,10 +1256,10 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
         const bool sliding = c.swa_period > 0 && (li + 1) % c.swa_period != 0;  // load.rs:1156-1160
         nnh_weight* const* W = m->w.data() + 7 * li;
         if (m->fused_qkv) {
-            if (gemv(m, W[0], m->normed, E, m->qkv, QKV, n_tok)) return 1;
-        } else if (gemv(m, W[0], m->normed, E, m->qkv, QKV, n_tok) ||
-                   gemv(m, W[1], m->normed, E, m->qkv + QD, QKV, n_tok) ||
-                   gemv(m, W[2], m->normed, E, m->qkv + QD + KVD, QKV, n_tok)) {
+            if (gemv_q(m, W[0], qe, m->normed, E, m->qkv, QKV, n_tok)) return 1;
+        } else if (gemv_q(m, W[0], qe, m->normed, E, m->qkv, QKV, n_tok) ||
+                   gemv_q(m, W[1], qe, m->normed, E, m->qkv + QD, QKV, n_tok) ||
+                   gemv_q(m, W[2], qe, m->normed, E, m->qkv + QD + KVD, QKV, n_tok)) {
             return 1;
         }
         uint16_t* kcl = m->kc + (size_t)li * c.n_ctx * KVD;
@@ -1041,27 +1303,27 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
             attn_tile_kernel<128><<<ag, 256, m->lds_attn, st>>>(aa);
         else
             attn_tile_kernel<256><<<ag, 256, m->lds_attn, st>>>(aa);
-        attn_merge_kernel<<<dim3(KV, n), 256, 0, st>>>(aa);
+        attn_merge_kernel<<<dim3(KV, n), 256, 0, st>>>(aa, oa);
         NNGL_CHECK(hipGetLastError());
-        if (gemv(m, W[3], m->attn, QD, m->r, E, n_tok)) return 1;
-        resid_norm_kernel<<<n, RN_T, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed,
-                                                        nullptr, n, E, c.rms_eps);
+        if (gemv_q(m, W[3], qt, m->attn, QD, m->r, E, n_tok)) return 1;
+        launch_resid_norm(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed, nullptr, n, E, c.rms_eps, oe,
+                          st);
         if (m->fused_gu) {
-            if (gemv(m, W[4], m->normed, E, m->gu, 2 * F, n_tok)) return 1;
-        } else if (gemv(m, W[4], m->normed, E, m->gu, 2 * F, n_tok) ||
-                   gemv(m, W[5], m->normed, E, m->gu + F, 2 * F, n_tok)) {
+            if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok)) return 1;
+        } else if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok) ||
+                   gemv_q(m, W[5], qe, m->normed, E, m->gu + F, 2 * F, n_tok)) {
             return 1;
         }
-        act_kernel<<<dim3((F + 1023) / 1024, n), 256, 0, st>>>(m->gu, F, gemma ? 1 : 0);
+        act_kernel<<<dim3((F + 1023) / 1024, n), 256, 0, st>>>(m->gu, F, gemma ? 1 : 0, of);
         NNGL_CHECK(hipGetLastError());
-        if (gemv(m, W[6], m->gu, 2 * F, m->r, E, n_tok)) return 1;
+        if (gemv_q(m, W[6], qf, m->gu, 2 * F, m->r, E, n_tok)) return 1;
         const bool last = li + 1 == c.n_layer;
         const float* next = last ? m->norms + ns * c.n_layer : m->norms + ns * (li + 1);
-        resid_norm_kernel<<<n, RN_T, (size_t)E * 8, st>>>(m->x, m->r, gemma ? post_ffw : nullptr, next,
-                                                        last ? m->x : m->normed, m->states + (size_t)li * E, n, E,
-                                                        c.rms_eps);
+        launch_resid_norm(m->x, m->r, gemma ? post_ffw : nullptr, next, last ? m->x : m->normed,
+                          m->states + (size_t)li * E, n, E, c.rms_eps, oe, st);
         NNGL_CHECK(hipGetLastError());
     }
+    m->q_last = fq;
     return 0;
 }
 
@@ -1086,7 +1348,8 @@ int nngl_greedy_next_dev(nngl_model* m, int32_t* tok_dev, int* pos_dev, int32_t*
     if (m->act == NNH_ACT_F32) {
         rc = nnh_model_argmax_dev(m->w.back(), m->x, m->logits, m->work, m->row, m->st);
     } else {
-        rc = nnh_gemv_batch_dev(m->w.back(), m->x, m->c.n_embd, m->logits, m->c.n_vocab, 1, m->act, m->st);
+        rc = m->q_last ? nnh_gemv_act_dev(m->w.back(), NNH_ACT_I8, m->qa_e, 1, m->logits, m->c.n_vocab, m->st)
+                       : nnh_gemv_batch_dev(m->w.back(), m->x, m->c.n_embd, m->logits, m->c.n_vocab, 1, m->act, m->st);
         if (rc == NNH_OK) rc = nnh_argmax_dev(m->logits, m->c.n_vocab, m->work, m->row, m->st);
     }
     if (rc != NNH_OK) {
@@ -1177,6 +1440,15 @@ int nngl_read(nngl_model* m, size_t n_tok, float* hidden, float* states, uint16_
 }
 
 size_t nngl_pos(nngl_model* m) { return m->pos; }
+
+// on != 0 (the default): one-token forwards in NNH_ACT_I8 have the kernels
+// that produce each matmul's input write it quantized (the same bits as
+// the library's quantizer on the f32 row, one launch fewer per matmul);
+// 0: every matmul quantizes its f32 input itself.
+int nngl_set_fused_quant(nngl_model* m, int on) {
+    m->qfuse = on != 0;
+    return 0;
+}
 
 // Start the sequence again at position `pos` (0: a new sequence; the
 // cache rows past it are overwritten as the forwards reach them).

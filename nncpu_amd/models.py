@@ -82,6 +82,7 @@ def _lib():
     L.nngl_set_pos.argtypes, L.nngl_set_pos.restype = [vp, sz], i32
     L.nngl_decode_step_dev.argtypes, L.nngl_decode_step_dev.restype = [vp, vp, vp], i32
     L.nngl_greedy_next_dev.argtypes, L.nngl_greedy_next_dev.restype = [vp, vp, vp, vp, vp], i32
+    L.nngl_set_fused_quant.argtypes, L.nngl_set_fused_quant.restype = [vp, i32], i32
     return L
 
 
@@ -257,6 +258,11 @@ class DeviceForward:
         p = lambda a: None if a is None else a.ctypes.data_as(C.c_void_p)  # noqa: E731
         self._check(self._lib.nngl_read(self._h, n_tok, p(hid) if n_tok else None, p(st), p(kc), p(vc)))
         return (hid, st, kc, vc) if caches else (hid, st)
+
+    def set_fused_quant(self, on: bool) -> None:
+        """One-token int8 forwards: the kernels producing each matmul input
+        write it quantized (default, same bits), or the matmuls quantize."""
+        self._check(self._lib.nngl_set_fused_quant(self._h, int(bool(on))))
 
     def set_pos(self, pos: int) -> None:
         self._check(self._lib.nngl_set_pos(self._h, pos))

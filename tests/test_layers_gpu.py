@@ -162,3 +162,48 @@ def test_decode_graph_matches_eager(N):
     assert np.array_equal(te, tc) and np.array_equal(ke, kc) and np.array_equal(ve, vc)
     assert np.array_equal(tg, tc), (tg, tc)
     assert np.array_equal(kg, kc) and np.array_equal(vg, vc)
+
+
+@pytest.mark.parametrize("case", ["qwen2_q4", "llama_q8", "gemma3_q8"])
+def test_i8_producer_quantization_matches_library_quantizer(N, case):
+    # One-token forwards in the int8 mode: the norm, attention-merge and
+    # activation kernels write each matmul's int8 input themselves
+    # (nngl_set_fused_quant). The library's quantizer on the same f32 rows
+    # gives the same bits, so the tokens, per-layer states and K/V caches
+    # equal the unfused run's, eagerly and from decode-graph replays (whose
+    # lm_head reads the final norm's int8 row). The 17- and 33-token prompts
+    # end in a one-token prompt batch.
+    import torch
+    from nncpu_amd import ACT_I8, Q4S
+    from nncpu_amd.gemma import gemma3_1b_config
+    from nncpu_amd.models import Model, llama_config, qwen2_config
+    if case == "qwen2_q4":
+        cfg = qwen2_config(n_layer=2, n_embd=256, n_head=4, n_kv=2, n_ff=512, n_vocab=768, n_ctx=300)
+        model, n_prompt = Model.random(cfg, seed=0x7A, dtype=Q4S), 257
+    elif case == "llama_q8":
+        cfg = llama_config(n_layer=2, n_embd=384, n_head=6, n_kv=2, n_ff=1024, n_vocab=1024, n_ctx=64)
+        model, n_prompt = Model.random(cfg, seed=0x7B, tied=False), 17
+    else:
+        cfg = gemma3_1b_config(n_ctx=64, n_layer=2, n_vocab=1024)
+        cfg.window, cfg.swa_period = 24, 2
+        model, n_prompt = Model.random(cfg, seed=0x7C), 33
+    prompt = np.random.default_rng(8).integers(0, cfg.n_vocab, n_prompt).astype(np.int32)
+    n_gen = 12
+    print(f"{case}: prompt {n_prompt} gen {n_gen}", flush=True)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=16, act=ACT_I8, stream=s.cuda_stream, fused=case == "qwen2_q4")
+    try:
+        dev.set_fused_quant(False)
+        t0, h0, k0, v0 = dev.generate(prompt, n_gen)
+        g0, _, gk0, gv0 = dev.generate_graph(prompt, n_gen, stream=s)
+        dev.set_fused_quant(True)
+        t1, h1, k1, v1 = dev.generate(prompt, n_gen)
+        g1, _, gk1, gv1 = dev.generate_graph(prompt, n_gen, stream=s)
+    finally:
+        dev.free()
+    assert np.array_equal(t1, t0), (t1, t0)
+    assert np.array_equal(h1, h0), np.argwhere(h1 != h0)[:5]
+    assert np.array_equal(k1, k0) and np.array_equal(v1, v0)
+    assert np.array_equal(g0, t0) and np.array_equal(gk0, k0) and np.array_equal(gv0, v0)
+    assert np.array_equal(g1, t0), (g1, t0)
+    assert np.array_equal(gk1, k0) and np.array_equal(gv1, v0)
