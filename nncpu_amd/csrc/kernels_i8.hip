@@ -369,10 +369,28 @@ void launch_cfg(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const
 // = ceil(nb / lanes) so no lane issues a load past the row (measured on the
 // 262144 x 1152 Q8 vocab GEMV, nb = 36: 3 blocks per lane 51.8 us against
 // 4 blocks 58.6 us). A lane's blocks and their order do not depend on the
-// chunking, so neither do the results.
+// chunking, so neither do the results. One vector with 97..127 blocks
+// (Qwen2.5-7B's 3584 columns) or Q8 rows past 256 blocks (its 18944-column
+// down projection): the best of 8 shapes measured at those matrices, Q8
+// 3584x3584 / 4608x3584 / 37888x3584 / 3584x18944 5.28 / 6.87 / 24.9 / 16.5
+// -> 4.86 / 5.38 / 23.7 / 15.6 us, Q4 3584x3584 / 37888x3584 4.36 / 16.4 ->
+// 4.17 / 16.2 us.
 template <int DT, int M>
 void launch_m(const uint8_t* qs, const uint16_t* sc, const uint16_t* bi, const int8_t* aq, const double* asx,
               int rows, int nb, float* y, size_t ys, hipStream_t st) {
+    if constexpr (M == 1) {
+        if (nb > 96 && nb <= 128) {
+            if (DT == 1)
+                launch_cfg<DT, M, 1, 64, 2>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+            else
+                launch_cfg<DT, M, 2, 64, 2>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+            return;
+        }
+        if (DT == 1 && nb > 256) {
+            launch_cfg<DT, M, 2, 64, 5>(qs, sc, bi, aq, asx, rows, nb, y, ys, st);
+            return;
+        }
+    }
     if (nb <= 64) {
         switch (ceil_div(nb, 16)) {
         case 1: launch_cfg<DT, M, 2, 16, 1>(qs, sc, bi, aq, asx, rows, nb, y, ys, st); break;

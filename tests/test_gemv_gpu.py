@@ -322,6 +322,7 @@ def test_i8_golden(oracle, case):
     (4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1), (4096, 14336, 1),
     (6144, 1536, 2), (1536, 6144, 4), (6144, 1536, 8), (1536, 6144, 16),
     (512, 3584, 3), (3584, 18944, 1),
+    (3584, 3584, 1), (4100, 3584, 1), (300, 8224, 1),  # one vector: 112 blocks, ragged rows; 257 blocks
 ])
 def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
     say("i8", dtype, rows, cols, n_tok)
