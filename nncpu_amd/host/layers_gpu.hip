@@ -895,7 +895,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // (scalar.rs:539-548) into out[t][head * hd ..]; qo.q != NULL (one token):
 // the output also quantized into qo (head_dim a multiple of 32, so every
 // half-wave of an iteration holds one block).
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, QOut qo) {
+__global__ __launch_bounds__(1024) void attn_merge_kernel(AttnArgs a, QOut qo) {
     const int t = blockIdx.y, kvh = blockIdx.x, hd = a.hd, G = a.G, pw = hd + 2, hd8 = hd & ~7;
     int p0, n_seq, first, last;
     attn_pos(a, p0, n_seq);
@@ -1247,6 +1247,9 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
     embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
     launch_resid_norm(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E, c.rms_eps, oe, st);
     NNGL_CHECK(hipGetLastError());
+    // One merged output per thread: G * head_dim threads (a multiple of 32)
+    // up to 1024, else 1024 threads looping.
+    const int merge_threads = G * hd <= 1024 ? G * hd : 1024;
     const int n_seq = posp ? c.n_ctx : (int)(pos0 + n_tok);
     const int nblk = (n_seq - 1) / ATTN_BLOCK + 1;
     for (int li = 0; li < c.n_layer; ++li) {
@@ -1303,7 +1306,7 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
             attn_tile_kernel<128><<<ag, 256, m->lds_attn, st>>>(aa);
         else
             attn_tile_kernel<256><<<ag, 256, m->lds_attn, st>>>(aa);
-        attn_merge_kernel<<<dim3(KV, n), 256, 0, st>>>(aa, oa);
+        attn_merge_kernel<<<dim3(KV, n), merge_threads, 0, st>>>(aa, oa);
         NNGL_CHECK(hipGetLastError());
         if (gemv_q(m, W[3], qt, m->attn, QD, m->r, E, n_tok)) return 1;
         launch_resid_norm(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed, nullptr, n, E, c.rms_eps, oe,
