@@ -794,8 +794,10 @@ def main():
     if args.workload in ("qwen_prefill", "all"):
         extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, d, a) for d in (1, 2) for a in (N.ACT_MXI8, N.ACT_I8)]
     elif args.workload == "q4_sweep":
-        # Config 5 end to end in the default run: Q8 weights, MX activations.
+        # Config 5 end to end in the default run: Q8 weights, MX activations;
+        # and its model's batch-1 decode, Q8 and Q4 weights, int8 activations.
         extra["qwen_prefill_e2e"] = [qwen_prefill(args, N, 1, N.ACT_MXI8)]
+        extra["qwen_decode_e2e"] = [r for d in (1, 2) for r in qwen_decode(args, N, d, (N.ACT_I8,))]
     if args.workload in ("qwen_decode", "all"):
         extra["qwen_decode"] = [r for d in (1, 2) for r in qwen_decode(args, N, d, (N.ACT_F32, N.ACT_I8))]
     if args.workload in ("q8_vocab", "all"):
