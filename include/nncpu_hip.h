@@ -293,6 +293,22 @@ int nnh_gemv_act_dev(const nnh_weight* w, int act, const void* buf, size_t n_tok
  * vector), as the int8 path forms them. */
 int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32_t* P, void* stream);
 
+/* Size the scratch of `stream` (and build the weight's layouts) for a call
+ * (w, act, n_tok) ahead of time, so that such calls on `stream` allocate
+ * nothing afterwards: for callers that capture them into a HIP graph, whose
+ * first call would otherwise grow the stream's scratch inside the capture.
+ * No counterpart in the reference, whose scratch is per session
+ * (model/kv.rs:324-332). */
+int nnh_stream_reserve(const nnh_weight* w, int act, size_t n_tok, void* stream);
+
+/* Free the scratch the library holds for `stream` (its current buffer and
+ * every outgrown one), after waiting for the work queued on it. For servers
+ * that create a stream per session and end it: the scratch otherwise lives
+ * until the process ends. Graphs captured on `stream` that used its scratch
+ * must not be replayed afterwards; the next call on `stream` allocates
+ * afresh. No counterpart in the reference. */
+int nnh_stream_release(void* stream);
+
 /* Block until all work the library queued on `stream` is done. */
 int nnh_sync(void* stream);
 

@@ -28,7 +28,7 @@ ACT_MXI8 = NNH_ACT_MXI8
 __all__ = [
     "Q8_0", "Q4S", "BF16", "ACT_F32", "ACT_I8", "ACT_MXI8", "Weight", "init", "model_gemv", "gemv_batch", "model_argmax",
     "gemv_batch_dev", "gemv_batch_dev_noalloc", "model_argmax_dev", "model_argmax_work_bytes", "dequantize_dev", "act_layout", "quantize_act_dev", "gemv_i8_dev", "block_dots_dev", "sync",
-    "act_layout_ex", "quantize_act_ex_dev", "gemv_act_dev",
+    "act_layout_ex", "quantize_act_ex_dev", "gemv_act_dev", "stream_reserve", "stream_release",
     "NnhError", "InvalidArgument", "DeviceOutOfMemory", "build", "declared_functions",
 ]
 
@@ -259,6 +259,17 @@ def block_dots_dev(w: Weight, act_ptr: int, n_tok: int, P_ptr: int, stream: int 
 def dequantize_dev(ggml_type: int, blocks_ptr: int, nbytes: int, dst_ptr: int, n: int, stream: int = 0) -> None:
     """kernels/quant.rs:107-156 on the device: n values of GGUF blocks into f32 dst."""
     check(lib().nnh_dequantize_dev(ggml_type, blocks_ptr, nbytes, dst_ptr, n, stream or None))
+
+
+def stream_reserve(w: Weight, act: int, n_tok: int, stream: int = 0) -> None:
+    """Build the layouts and size ``stream``'s scratch for a call (w, act, n_tok)
+    ahead of time, so such calls on ``stream`` allocate nothing (graph capture)."""
+    check(lib().nnh_stream_reserve(w.handle, act, n_tok, stream or None))
+
+
+def stream_release(stream: int = 0) -> None:
+    """Free the library's scratch for ``stream`` (waits for its queued work)."""
+    check(lib().nnh_stream_release(stream or None))
 
 
 def sync(stream: int = 0) -> None:

@@ -77,6 +77,8 @@ def _declare(L):
     L.nnh_weight_download.argtypes, L.nnh_weight_download.restype = [vp, vp, sz], i32
     L.nnh_weight_info.argtypes, L.nnh_weight_info.restype = [vp, P(i32), P(sz), P(sz)], i32
     L.nnh_weight_prepare.argtypes, L.nnh_weight_prepare.restype = [vp, i32, sz], i32
+    L.nnh_stream_reserve.argtypes, L.nnh_stream_reserve.restype = [vp, i32, sz, vp], i32
+    L.nnh_stream_release.argtypes, L.nnh_stream_release.restype = [vp], i32
     L.nnh_weight_device_bytes.argtypes, L.nnh_weight_device_bytes.restype = [vp], sz
     L.nnh_model_gemv.argtypes, L.nnh_model_gemv.restype = [vp, vp, vp, i32], i32
     L.nnh_gemv_batch.argtypes, L.nnh_gemv_batch.restype = [vp, vp, sz, vp, sz, sz, i32], i32

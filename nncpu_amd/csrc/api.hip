@@ -51,12 +51,13 @@ hipStream_t g_stream = nullptr;
 // Device scratch per calling stream (the host-buffer calls use g_stream's),
 // so calls on different streams never share one. A buffer that grows is
 // retired, not freed: a HIP graph that captured a call keeps its address.
+// nnh_stream_release frees a stream's buffers, retired ones included.
 struct Scratch {
     uint8_t* p = nullptr;
     size_t bytes = 0;
+    std::vector<uint8_t*> retired;  // outgrown buffers, freed by nnh_stream_release
 };
 std::unordered_map<hipStream_t, Scratch> g_scratch;
-std::vector<uint8_t*> g_retired;
 uint8_t* g_pinned = nullptr;  // pinned host staging for the host-buffer calls
 size_t g_pinned_bytes = 0;
 
@@ -112,15 +113,16 @@ int ensure_locked() { return init_locked(g_device >= 0 ? g_device : 0); }
 
 // The scratch of calls on `st`, at least `bytes`; caller holds g_mu. Work
 // queued on `st` (or replays of graphs captured on it) may still use the
-// old buffer, so a grown buffer keeps the old one alive until the process
-// ends; doubling bounds the retired total by the live size.
+// old buffer, so a grown buffer keeps the old one alive until
+// nnh_stream_release (or the process end); doubling bounds the retired
+// total by the live size.
 int scratch_locked(hipStream_t st, size_t bytes, uint8_t** out) {
     Scratch& s = g_scratch[st];
     if (bytes > s.bytes) {
         const size_t want = align_up(bytes > 2 * s.bytes ? bytes : 2 * s.bytes);
         uint8_t* p = nullptr;
         NNH_HIP(hipMalloc((void**)&p, want));
-        if (s.p) g_retired.push_back(s.p);
+        if (s.p) s.retired.push_back(s.p);
         s.p = p;
         s.bytes = want;
     }
@@ -389,18 +391,24 @@ int alloc_weight(int dtype, size_t rows, size_t cols, nnh_weight** out) {
     return NNH_OK;
 }
 
-// Build the BF16 chain layout from `raw` and wait; caller holds g_mu. (Q8_0
-// and Q4 layouts are built by prepare_locked when a call first needs them.)
+// Build the BF16 chain layout from `raw`, then wait for everything queued
+// on the library stream for this weight (the upload copies or the encode
+// kernel, every dtype); caller holds g_mu. On return the caller may free or
+// reuse the source, and any stream may read `raw` (Q8_0 and Q4 derived
+// layouts are built by prepare_locked when a call first needs them).
 int finalize_weight(nnh_weight* w) {
-    if (w->dtype != NNH_BF16) return NNH_OK;
-    nnh::launch_relayout_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, (int)w->rows, (int)w->cols, g_stream);
+    if (w->dtype == NNH_BF16)
+        nnh::launch_relayout_bf16(w->bpath, (const uint16_t*)w->raw, w->bl, (int)w->rows, (int)w->cols, g_stream);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(g_stream)) != hipSuccess)
         return fail(NNH_E_DEVICE, std::string("weight layouts: ") + hipGetErrorString(e));
     return NNH_OK;
 }
 
+// A derived layout's buffer; one left by an earlier call whose later
+// allocation failed is reused, so a retry neither leaks nor double-counts.
 int dev_alloc(nnh_weight* w, void** p, size_t bytes) {
+    if (*p) return NNH_OK;
     const size_t b = align_up(bytes);
     hipError_t e = hipMalloc(p, b);
     if (e != hipSuccess)
@@ -857,6 +865,31 @@ int nnh_block_dots_dev(const nnh_weight* w, const void* act, size_t n_tok, int32
     nnh::launch_block_dots(w->dtype, w->qs, (const int8_t*)act, (int)w->rows, (int)w->nb, (int)n_tok, P,
                            (hipStream_t)stream);
     NNH_HIP(hipGetLastError());
+    return NNH_OK;
+}
+
+int nnh_stream_reserve(const nnh_weight* w, int act, size_t n_tok, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, 0, w ? w->rows : 0, n_tok, act))) return rc;
+    if ((rc = prepare_locked(w, layouts_for(w, act, n_tok)))) return rc;
+    const size_t need = n_tok ? gemv_scratch_bytes(w, n_tok, act) : 0;
+    uint8_t* s = nullptr;
+    if (need && (rc = scratch_locked((hipStream_t)stream, need, &s))) return rc;
+    return NNH_OK;
+}
+
+int nnh_stream_release(void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    auto it = g_scratch.find((hipStream_t)stream);
+    if (it == g_scratch.end()) return NNH_OK;
+    NNH_HIP(hipStreamSynchronize((hipStream_t)stream));
+    for (uint8_t* p : it->second.retired) (void)hipFree(p);
+    if (it->second.p) (void)hipFree(it->second.p);
+    g_scratch.erase(it);
     return NNH_OK;
 }
 

@@ -1183,10 +1183,12 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
                      : hd == 64 ? (const void*)attn_decode_kernel<64>
                      : hd == 128 ? (const void*)attn_decode_kernel<128> : (const void*)attn_decode_kernel<256>;
     NNGL_CHECK(hipFuncSetAttribute(dk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_dec));
-    // The weights' layouts for this mode and batch, so no forward allocates
-    // (and a forward can be captured into a graph).
+    // The weights' layouts and the stream's scratch for this mode and batch
+    // (and for one token), so no forward allocates and a forward can be
+    // captured into a graph.
     for (nnh_weight* wk : m->w)
-        if (wk && (nnh_weight_prepare(wk, act, nb) != NNH_OK || (nb > 1 && nnh_weight_prepare(wk, act, 1) != NNH_OK))) {
+        if (wk && (nnh_stream_reserve(wk, act, nb, m->st) != NNH_OK ||
+                   (nb > 1 && nnh_stream_reserve(wk, act, 1, m->st) != NNH_OK))) {
             m->err = std::string("weight layouts: ") + nnh_last_error();
             return 1;
         }

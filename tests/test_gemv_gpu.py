@@ -493,6 +493,37 @@ def test_device_encoder_bit_exact(oracle, dtype):
     assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
 
 
+@pytest.mark.parametrize("dtype", [1, 2, 3])
+def test_encode_is_complete_when_it_returns(oracle, dtype):
+    # nnh_encode_dev (and the uploads) return only once the weight is written:
+    # the f32 source freed and its memory overwritten straight after the call
+    # must not reach the encoded weight. Then the split layout is read through
+    # the int8 GEMV of one vector (no derived layout for Q8_0) on torch's
+    # stream, with no other ordering.
+    import torch
+    rng = oracle.Rng(0xE7D0 + dtype)
+    rows, cols = 4096, 4096
+    w = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+    dw = torch_dev(np.ascontiguousarray(w, np.float32).ravel())
+    dev = N.Weight.encode_dev(dtype, dw.data_ptr(), rows, cols)
+    dw.fill_(1e6)
+    del dw
+    junk = torch.full((rows * cols,), -7.0, device="cuda")
+    torch.cuda.synchronize()
+    del junk
+    got = dev.download()
+    if dtype == 3:
+        want = oracle.f32_array_to_bf16(w.ravel()).view(np.uint8)
+    else:
+        want = oracle.QMatrix.from_f32(dtype, w).buf
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
+    if dtype != 3:
+        x = rng.normals(cols, 1.0)
+        assert np.abs(N.model_gemv(dev, x, act=N.ACT_I8) - oracle.gemv_batch(
+            oracle.QMatrix.from_f32(dtype, w), oracle.dequant_act(*oracle.quantize_act(x)))).max() <= 1e-5
+    dev.free()
+
+
 @pytest.mark.parametrize("dtype", [1, 2])
 def test_device_encoded_weight_matmul(oracle, dtype):
     # The encoded weight is a complete weight: its f32 matmul matches the

@@ -139,3 +139,45 @@ def test_streams_have_their_own_scratch(oracle):
             qx, sx = oracle.quantize_act(xh[t * cols:(t + 1) * cols])
             exact = oracle.gemv_i8_exact(m, qx, sx)
             assert np.all(np.abs(yh[t * rows:(t + 1) * rows] - exact) <= np.spacing(np.abs(exact))), t
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_reserved_stream_captures_without_allocating(oracle, act):
+    # nnh_stream_reserve sizes a fresh stream's scratch ahead of time: the
+    # first call on that stream may then be captured (no allocation inside the
+    # capture), and replays give the eager bits. nnh_stream_release frees the
+    # stream's scratch; the next call on it allocates afresh, same bits.
+    import torch
+    rows, cols, n_tok = 640, 2048, 24
+    say("reserve then capture", act)
+    rng = oracle.Rng(0x5E5 + act)
+    m = oracle.QMatrix.from_f32(2, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    st = torch.cuda.Stream()
+    x = torch.from_numpy(rng.normals(n_tok * cols, 1.0)).cuda()
+    y = torch.zeros(n_tok * rows, device="cuda")
+    N.stream_reserve(w, act, n_tok, st.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        N.gemv_batch_dev(w, x.data_ptr(), cols, y.data_ptr(), rows, n_tok, act, st.cuda_stream)
+    outs = []
+    for _ in range(3):
+        y.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy().copy())
+    del g
+    y.fill_(-1.0)
+    N.gemv_batch_dev(w, x.data_ptr(), cols, y.data_ptr(), rows, n_tok, act, st.cuda_stream)
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    for o in outs:
+        assert np.array_equal(bits(o), bits(eager))
+    N.stream_release(st.cuda_stream)
+    y.fill_(-1.0)
+    N.gemv_batch_dev(w, x.data_ptr(), cols, y.data_ptr(), rows, n_tok, act, st.cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(y.cpu().numpy()), bits(eager))
+    N.stream_release(st.cuda_stream)
