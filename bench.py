@@ -279,10 +279,26 @@ def traffic_run(N):
 
 def _calib():
     L = C.CDLL(os.path.join(ROOT, "nncpu_amd", "lib", "libnncpu_calib.so"))
+    L.nnc_clock_probe.argtypes, L.nnc_clock_probe.restype = [C.c_int, C.c_int, C.c_void_p, C.c_void_p], C.c_int
     L.nnc_read_stream.argtypes, L.nnc_read_stream.restype = [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p], C.c_int
     L.nnc_mfma_loop.argtypes, L.nnc_mfma_loop.restype = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p], C.c_int
     L.nnc_mfma_ops.argtypes, L.nnc_mfma_ops.restype = [C.c_int, C.c_int, C.c_int], C.c_longlong
     return L
+
+
+def shader_clock_mhz():
+    """The shader clock now: one wave per CU times a dependent FMA chain with
+    the core-clock and the 100 MHz counters (nnc_clock_probe); the median
+    over the CUs, in MHz."""
+    import torch
+    L = _calib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.zeros(2 * cus, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    assert L.nnc_clock_probe(cus, 200000, out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    v = out.cpu().numpy().reshape(cus, 2).astype(np.float64)
+    return round(float(np.median(100.0 * v[:, 0] / np.maximum(v[:, 1], 1))), 1)
 
 
 def peaks(args):
@@ -714,11 +730,13 @@ def decode_leg(N, path, dtype, cpu: bool):
     log(f"gemma3-1b loaded (device decode + {fmt} re-encode) in {time.perf_counter() - t1:.1f}s")
     prompt, n_gen = random_prompt(32, m.cfg.n_vocab), 128
     m.generate_device(prompt, n_gen)
+    clk0 = shader_clock_mhz()
     tg, hg, tp, td = m.generate_device(prompt, n_gen)
+    clk1 = shader_clock_mhz()
     out = dict(config="gemma-3-1b architecture, random-init GGUF from seed (BF16 matrices 0.02*N(0,1) from the "
                       f"reference's test generator) re-encoded to {fmt} on load, 32-token prompt, 128 greedy tokens",
                tok_s=round((n_gen - 1) / td, 1), ms_per_token=round(td / (n_gen - 1) * 1e3, 4),
-               prefill_s=round(tp, 4), kernels_per_token=4)
+               prefill_s=round(tp, 4), kernels_per_token=4, shader_clock_mhz=[clk0, clk1])
     # The matmul-only ceiling: every weight read once per token at the HBM
     # datasheet rate (the layers' matrices and the tied lm_head).
     wpt = sum(weight_bytes(dtype, r, c) for r, c in m.shapes)
@@ -774,6 +792,11 @@ def main():
         return
     extra = {}
     prefill_cases = [(d, n, k, 512) for d in (1, 2) for n, k in QWEN_PREFILL]
+    if args.workload in ("gemma_decode", "q4_sweep", "all"):
+        # First, on a GPU that has not yet run the minutes of matrix-unit and
+        # streaming work below: the decode step is a chain of dependent
+        # hand-offs, so its rate follows the shader clock (recorded beside it).
+        extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
     if args.workload in ("peaks", "q4_sweep", "all"):
         extra["peaks"] = peaks(args)
     result = inputs = None
@@ -800,11 +823,11 @@ def main():
         extra["qwen_decode_e2e"] = [r for d in (1, 2) for r in qwen_decode(args, N, d, (N.ACT_I8,))]
     if args.workload in ("qwen_decode", "all"):
         extra["qwen_decode"] = [r for d in (1, 2) for r in qwen_decode(args, N, d, (N.ACT_F32, N.ACT_I8))]
-    if args.workload in ("q8_vocab", "all"):
+    if args.workload in ("q8_vocab", "q4_sweep", "all"):
         extra["q8_vocab_m1"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_I8, "q8_vocab")
         extra["q8_vocab_m1_f32_bit_exact"] = measure_cases(args, N, [(1, n, k, 1) for n, k in Q8_VOCAB], N.ACT_F32,
                                                            "q8_vocab_f32")
-    if args.workload in ("verify", "all"):
+    if args.workload in ("verify", "q4_sweep", "all"):
         extra["verify"] = measure_cases(args, N, [(d, n, k, m) for d in (1, 2) for n, k in VERIFY_SHAPES[:2]
                                                   for m in (2, 4, 8, 16)], N.ACT_I8, "verify")
     if args.workload in ("decode_f32", "all"):
@@ -813,8 +836,10 @@ def main():
     if args.workload in ("bf16", "all"):
         extra["bf16_bit_exact"] = measure_cases(args, N, [(3, n, k, m) for n, k in BF16_SHAPES for m in (1, 4)],
                                                 N.ACT_F32, "bf16")
-    if args.workload in ("gemma_decode", "q4_sweep", "all"):
-        extra["gemma3_1b_decode"] = gemma_decode(args, N, cpu=not args.no_cpu_baseline)
+    if args.workload in ("q4_sweep", "all"):
+        # The same decode again after everything above (device only), with
+        # the shader clock it ran at.
+        extra["gemma3_1b_decode_late"] = gemma_decode(args, N, cpu=False)
     if result is None:
         print(json.dumps(dict(workload=args.workload, results=extra)), flush=True)
         return

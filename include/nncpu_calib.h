@@ -33,6 +33,12 @@ enum { NNC_MFMA_I8 = 1, NNC_MFMA_BF16 = 2 };
 int nnc_mfma_loop(int kind, int iters, int blocks, void* out, void* stream);
 long long nnc_mfma_ops(int kind, int iters, int blocks);
 
+/* The shader clock: `blocks` one-wave workgroups each time a dependent
+ * chain of `iters` FMAs with the core-clock counter and the constant 100 MHz
+ * counter; out (device, 2 * blocks u64) receives per workgroup {core cycles,
+ * 100 MHz ticks}. The clock in MHz is 100 * cycles / ticks. */
+int nnc_clock_probe(int blocks, int iters, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

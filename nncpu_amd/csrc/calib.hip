@@ -78,9 +78,34 @@ __global__ __launch_bounds__(256) void mfma_bf16_kernel(int iters, int* __restri
     if (s == 1234.5f) out[threadIdx.x] = 1;
 }
 
+// The shader clock under a light load: each workgroup's first lane reads
+// the core-clock counter (s_memtime) and the constant 100 MHz counter
+// (s_memrealtime) around a dependent FMA chain of `iters` steps, and stores
+// the two differences (vector stores). cycles / (ticks / 100 MHz) is the
+// clock the workgroup's CU ran at.
+__global__ __launch_bounds__(64) void clock_probe_kernel(int iters, unsigned long long* __restrict__ out) {
+    float v = 1.0f + threadIdx.x * 1e-7f;
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < iters; ++i) v = __builtin_fmaf(v, 0.999999f, 1e-7f);
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[2 * blockIdx.x] = c1 - c0;
+        out[2 * blockIdx.x + 1] = (r1 - r0) + (v == 12345.0f ? 1 : 0);
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int nnc_clock_probe(int blocks, int iters, void* out, void* stream) {
+    if (!out || blocks <= 0 || iters <= 0) return 1;
+    clock_probe_kernel<<<blocks, 64, 0, (hipStream_t)stream>>>(iters, (unsigned long long*)out);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
 
 int nnc_read_stream(const void* p, size_t bytes, int unroll, void* out, void* stream) {
     if (!p || !out || bytes % 16 != 0 || bytes == 0) return 1;

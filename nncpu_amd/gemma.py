@@ -81,6 +81,50 @@ def _gemma_lib():
     return L
 
 
+def gemma3_config_from_kv(kv: dict, n_ctx: int, dtype: int, path: str = "") -> NngConfig:
+    """A Gemma-3 GGUF's hyperparameters as nncpu's loader reads them
+    (model/load.rs:431-595, 1147-1165). Models these forwards cannot run as
+    the reference would (RoPE linear scaling, every layer sliding, a
+    non-periodic sliding pattern) raise ValueError."""
+    a = "gemma3."
+    E, nh = int(kv[a + "embedding_length"]), int(kv[a + "attention.head_count"])
+    hd = int(kv.get(a + "attention.key_length", E // nh))
+    n_layer = int(kv[a + "block_count"])
+    # RoPE linear scaling (load.rs:550-554) scales the global layers'
+    # positions (forward.rs:296-304; Gemma-3 4B/12B/27B); neither forward
+    # here carries that scale, so such a model is refused, not run wrong.
+    if kv.get(a + "rope.scaling.type", "") == "linear" and float(kv.get(a + "rope.scaling.factor", 0.0)) > 0.0:
+        raise ValueError(f"{path}: RoPE linear scaling is not supported by these forwards")
+    base = float(kv.get(a + "rope.freq_base", 10000.0))
+    base_swa = float(kv.get(a + "rope.freq_base_swa", 0.0))
+    base_swa = base_swa if base_swa > 0.0 else 10000.0  # load.rs:486-492: gemma3's unstored local theta
+    window = max(int(kv.get(a + "attention.sliding_window", 0)), 0)
+    # Sliding layers (load.rs:1147-1165): a per-layer array, else every
+    # `period`-th layer global (default 6), none when the window is 0.
+    pat = kv.get(a + "attention.sliding_window_pattern")
+    period = 6
+    if isinstance(pat, (list, tuple, np.ndarray)) and len(pat) == n_layer:
+        flags = [int(v) != 0 for v in pat]
+        globals_ = [i for i, v in enumerate(flags) if not v]
+        period = globals_[0] + 1 if globals_ else 0
+        if period > 0 and [(i + 1) % period != 0 for i in range(n_layer)] != flags:
+            raise ValueError(f"{path}: a sliding-window layer pattern that is not periodic is not supported")
+    elif pat is not None and not isinstance(pat, (list, tuple, np.ndarray)):
+        period = int(pat)
+    if window == 0:
+        period = 0  # no layer slides, every layer takes the global RoPE base
+    elif period <= 0:
+        raise ValueError(f"{path}: every layer sliding (pattern <= 0) is not supported")
+    cfg = NngConfig(n_layer=n_layer, n_embd=E, n_head=nh,
+                    n_kv=int(kv.get(a + "attention.head_count_kv", nh)), head_dim=hd,
+                    n_ff=int(kv[a + "feed_forward_length"]), n_vocab=len(kv["tokenizer.ggml.tokens"]),
+                    n_ctx=n_ctx, rms_eps=float(kv.get(a + "attention.layer_norm_rms_epsilon", 1e-6)),
+                    rope_base=base, rope_base_swa=base_swa,
+                    attn_scale=float(kv.get(a + "attention.scale", 1.0 / hd ** 0.5)),
+                    window=window, swa_period=period, wtype=dtype)
+    return cfg
+
+
 class Gemma3:
     """Device weights of a Gemma-3 model (nncpu's Q8_0 or Q4 layout), plus
     the host copies (norms, the embedding table) the CPU forward reads."""
@@ -105,16 +149,7 @@ class Gemma3:
         kv = f.kv
         if kv.get("general.architecture") != "gemma3":
             raise ValueError(f"{path}: not a gemma3 model")
-        a = "gemma3."
-        E, nh = int(kv[a + "embedding_length"]), int(kv[a + "attention.head_count"])
-        hd = int(kv.get(a + "attention.key_length", E // nh))
-        cfg = NngConfig(n_layer=int(kv[a + "block_count"]), n_embd=E, n_head=nh,
-                        n_kv=int(kv.get(a + "attention.head_count_kv", nh)), head_dim=hd,
-                        n_ff=int(kv[a + "feed_forward_length"]), n_vocab=len(kv["tokenizer.ggml.tokens"]),
-                        n_ctx=n_ctx, rms_eps=float(kv.get(a + "attention.layer_norm_rms_epsilon", 1e-6)),
-                        rope_base=float(kv.get(a + "rope.freq_base", 10000.0)), rope_base_swa=10000.0,
-                        attn_scale=float(kv.get(a + "attention.scale", 1.0 / hd ** 0.5)),
-                        window=int(kv.get(a + "attention.sliding_window", 0)), swa_period=6, wtype=dtype)
+        cfg = gemma3_config_from_kv(kv, n_ctx, dtype, path)
 
         def mat(name):
             t = f.tensors[name]

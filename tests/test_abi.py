@@ -87,7 +87,7 @@ def test_calibration_library_exports_its_header():
     root = os.path.dirname(_lib.HEADER)
     text = re.sub(r"/\*.*?\*/", "", open(os.path.join(root, "nncpu_calib.h")).read(), flags=re.S)
     names = set(re.findall(r"^\s*(?:long long|int)\s+(nnc_\w+)\s*\(", text, flags=re.M))
-    assert names == {"nnc_read_stream", "nnc_mfma_loop", "nnc_mfma_ops"}
+    assert names == {"nnc_read_stream", "nnc_mfma_loop", "nnc_mfma_ops", "nnc_clock_probe"}
     path = os.path.join(os.path.dirname(_lib.LIB_PATH), "libnncpu_calib.so")
     out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True)
     assert {line.split()[-1] for line in out.stdout.splitlines() if " T nnc_" in line} == names

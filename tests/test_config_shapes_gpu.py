@@ -6,14 +6,18 @@ modes and both weight formats. Each output is checked against the exact sum
 of its block terms (integer block dots, f64) within the kernel's stated f32
 rounding bound, and 8 sampled tokens x all rows against nncpu's own kernel
 (the oracle's restatement of kernels/scalar.rs:626-742) fed the dequantized
-activations, at the north-star tolerance: 1e-5 absolute per element (against
-the exact value, and against nncpu's kernel up to that kernel's own rounding
-error, which reaches 1.2e-5 for Q4 at K = 18944) and 1e-3 relative L2
-(kernels/tests.rs:555-639 compare against an f64 gemv the same way).
+activations: 1e-3 relative L2 (kernels/tests.rs:555-639 compare against an
+f64 gemv the same way), and 1e-5 absolute per element against the exact
+value. The literal 1e-5 against nncpu's kernel is counted per case (printed,
+and written to NNH_PARITY_RECORD when set); an element that misses it must
+be one where nncpu's own kernel is further from the exact value than this
+kernel is.
 
 Config 3 (Qwen2.5-7B vocab, 151936 x 3584, M = 1): the f32 path bit for bit
 against the oracle, the int8 path within 1e-5 of the oracle fed x'.
 """
+import json
+import os
 import sys
 
 import numpy as np
@@ -74,7 +78,15 @@ def gemm_bound(dtype, act, cols):
 SAMPLED = 8
 
 
-def check_batch(oracle, m, act, x, xs, y, ys, n_tok):
+def record(entry):
+    """Append one case's numbers to the JSON-lines file NNH_PARITY_RECORD names (if set)."""
+    path = os.environ.get("NNH_PARITY_RECORD")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(entry) + "\n")
+
+
+def check_batch(oracle, m, act, x, xs, y, ys, n_tok, label=""):
     rows, cols = m.rows, m.cols
     qs, ss = quantize(oracle, act, x, n_tok, xs, cols)
     exact, mag = oracle.gemm_exact(m, np.concatenate(qs), np.concatenate(ss), n_tok)
@@ -86,23 +98,35 @@ def check_batch(oracle, m, act, x, xs, y, ys, n_tok):
     sample = sorted(set([0, n_tok - 1] + list(range(0, n_tok, max(1, n_tok // (SAMPLED - 1))))))[:SAMPLED + 1]
     xd = np.concatenate([oracle.dequant_act(qs[t], ss[t]) for t in sample])
     ref = oracle.gemv_batch(m, xd, len(sample), cols, rows).astype(np.float64)
-    worst = worst_ref = 0.0
+    worst = worst_ref = worst_exact = 0.0
+    n_over = 0
     for i, t in enumerate(sample):
         r = ref[i * rows:(i + 1) * rows]
-        # nncpu's own f32 chains are |r - exact[t]| from the exact product of
-        # the same quantized operands: up to ~1.2e-5 for Q4 at K = 18944, so
-        # there no result but nncpu's own bits is within 1e-5 of r
-        # everywhere. The tolerance is then taken against the exact value,
-        # and against r up to nncpu's own deviation; where nncpu is within
-        # 5e-6 of exact, within 1e-5 of r outright.
+        # The north-star tolerance, literally: |y - nncpu(x')| <= 1e-5 per
+        # element. nncpu's own f32 chains lie |r - exact| from the exact
+        # product of the same quantized operands (up to ~1.2e-5 at K =
+        # 18944), so no other summation order meets it everywhere. Every
+        # element that misses it is counted and recorded, and must be one
+        # where this kernel is within 1e-5 of the exact value and closer to it
+        # than nncpu's own kernel is: the miss is nncpu's rounding, not ours.
         own = np.abs(r - exact[t])
-        assert np.all(np.abs(got[t] - exact[t]) <= 1e-5), t
-        assert np.all(np.abs(got[t] - r) <= 1e-5 + own), t
-        assert np.all(np.abs(got[t] - r)[own <= 5e-6] <= 1e-5), t
+        ours = np.abs(got[t] - exact[t])
+        diff = np.abs(got[t] - r)
+        over = diff > 1e-5
+        n_over += int(over.sum())
+        assert np.all(ours <= 1e-5), t
+        assert np.all(ours[over] < own[over]), (t, ours[over][:5], own[over][:5])
         assert np.linalg.norm(got[t] - r) <= 1e-3 * np.linalg.norm(r), t
-        worst = max(worst, np.abs(got[t] - r).max())
+        worst = max(worst, diff.max())
         worst_ref = max(worst_ref, own.max())
-    say(f"  over {len(sample)} tokens: max |y - nncpu(x')| {worst:.3g}, max |nncpu(x') - exact| {worst_ref:.3g}")
+        worst_exact = max(worst_exact, ours.max())
+    say(f"  over {len(sample)} tokens x {rows} rows: max |y - nncpu(x')| {worst:.3g}, "
+        f"max |nncpu(x') - exact| {worst_ref:.3g}, max |y - exact| {worst_exact:.3g}, above 1e-5: {n_over}")
+    record({"case": label, "rows": rows, "cols": cols, "n_tok": n_tok, "dtype": "Q8" if m.dtype == 1 else "Q4",
+            "act": {1: "I8", 2: "MXI8"}.get(act, act), "checked": len(sample) * rows,
+            "max_y_minus_nncpu": worst, "max_nncpu_minus_exact": worst_ref, "max_y_minus_exact": worst_exact,
+            "above_1e-5": n_over})
+    return n_over
 
 
 QWEN_M512 = [
@@ -127,7 +151,8 @@ def test_qwen_prefill_m512(oracle, dtype, act, rows, cols):
     dy = torch.full((n_tok * rows,), 7.0, device="cuda")
     N.gemv_batch_dev(w, dx.data_ptr(), cols, dy.data_ptr(), rows, n_tok, act)
     N.sync()
-    check_batch(oracle, m, act, dx.cpu().numpy(), cols, dy.cpu().numpy(), rows, n_tok)
+    check_batch(oracle, m, act, dx.cpu().numpy(), cols, dy.cpu().numpy(), rows, n_tok,
+                label=f"config5 {rows}x{cols}")
     w.free()
 
 
@@ -151,4 +176,26 @@ def test_qwen_vocab_m1(oracle):
     exact = oracle.gemv_i8_exact(m, qx, sx)
     assert np.all(np.abs(yi - exact) <= np.spacing(np.abs(exact)))
     del torch
+    w.free()
+
+
+def test_gemma_vocab_m1_i8(oracle):
+    # Config 3's Gemma-3 lm_head, 262144 x 1152 Q8_0 (302 MB + 19 MB of
+    # scales), one vector, at full size in both modes: the int8 GEMV's launch
+    # shape for this height, and the f32 path bit for bit.
+    rows, cols = 262144, 1152
+    say("config3 gemma vocab", rows, cols)
+    w, m = device_weight(oracle, 1, rows, cols, 0x5EED13)
+    rng = oracle.Rng(0x7A12)
+    x = rng.normals(cols, 1.0)
+    qx, sx = oracle.quantize_act(x)
+    ref = oracle.gemv_batch(m, oracle.dequant_act(qx, sx))
+    exact = oracle.gemv_i8_exact(m, qx, sx)
+    yi = N.model_gemv(w, x, act=N.ACT_I8)
+    assert np.all(np.abs(yi - exact) <= np.spacing(np.abs(exact)))
+    assert np.abs(yi - ref).max() <= 1e-5
+    assert np.linalg.norm(yi - ref) <= 1e-3 * np.linalg.norm(ref)
+    assert N.model_argmax(w, x, act=N.ACT_I8) == oracle.argmax(yi)
+    want = oracle.gemv_batch(m, x)
+    assert np.array_equal(bits(N.model_gemv(w, x)), bits(want))
     w.free()

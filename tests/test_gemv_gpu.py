@@ -42,6 +42,43 @@ def say(*a):
 
 # ---- f32 path: bit-exact ----------------------------------------------------------
 
+def kat_weight(dtype, seed, nb, rows):
+    """A matrix of `rows` copies of a known-answer row (tests/row_kats.py) and its x."""
+    from row_kats import q4_inputs, q4_split, q8_inputs, q8_split
+    if dtype == 1:
+        q, s, x, _ = q8_inputs(seed, nb)
+        qs, sc = q8_split(q, s)
+        w = N.Weight.q8_0(np.tile(qs, rows), np.tile(sc, rows), rows, 32 * nb)
+    else:
+        qb, s, bi, x = q4_inputs(seed, nb)
+        qs, sc, b = q4_split(qb, s, bi)
+        w = N.Weight.q4(np.tile(qs, rows), np.tile(sc, rows), np.tile(b, rows), rows, 32 * nb)
+    return w, np.array(x, np.float32)
+
+
+def kat_cases():
+    from row_kats import Q4_KATS, Q8_KATS
+    return [(1,) + k for k in Q8_KATS] + [(2,) + k for k in Q4_KATS]
+
+
+@pytest.mark.parametrize("rows", [4, 2048, 16384])
+@pytest.mark.parametrize("kat", kat_cases(), ids=lambda k: f"{'Q8' if k[0] == 1 else 'Q4'}_nb{k[2]}")
+def test_f32_known_answers(kat, rows):
+    # The hand-derived known answers whose inputs tell nncpu's reduction
+    # order from every plausible other one: every kernel of the bit-exact
+    # path (few rows, the streamed long-row kernels from 64 blocks, the
+    # 8-lane tall kernel from 16384 rows, 2-4 vectors) gives those bits.
+    dtype, seed, nb, want = kat
+    say("kat", dtype, seed, nb, rows)
+    w, x = kat_weight(dtype, seed, nb, rows)
+    y = N.model_gemv(w, x)
+    assert np.all(bits(y) == want), (hex(int(bits(y)[0])), hex(want))
+    y3 = np.zeros(3 * rows, np.float32)
+    N.gemv_batch(w, np.tile(x, 3), 32 * nb, y3, rows, 3, N.ACT_F32)
+    assert np.all(bits(y3) == want)
+    w.free()
+
+
 @pytest.mark.parametrize("case", [c for c in cases() if c["kind"] == "gemv_f32"], ids=lambda c: c["name"])
 def test_f32_golden_bit_exact(oracle, case):
     say("case", case["name"])

@@ -101,3 +101,34 @@ def test_write_gemma3_small(tmp_path, oracle):
                 want = G.bf16_bits(G.normals((5 << 32) + (i << 24), rows * cols, 0.0, 0.02))
                 assert np.array_equal(np.asarray(t.data).view(np.uint16), want), name
     os.remove(path)
+
+
+def _gemma_kv(**extra):
+    kv = {"gemma3.embedding_length": 1152, "gemma3.attention.head_count": 4, "gemma3.attention.head_count_kv": 1,
+          "gemma3.attention.key_length": 256, "gemma3.block_count": 12, "gemma3.feed_forward_length": 6912,
+          "gemma3.rope.freq_base": 1e6, "gemma3.attention.sliding_window": 512,
+          "tokenizer.ggml.tokens": ["a"] * 64}
+    kv.update({"gemma3." + k: v for k, v in extra.items()})
+    return kv
+
+
+def test_gemma3_hyperparameters_follow_the_loader():
+    # model/load.rs:486-493, 550-554, 1147-1165: the local RoPE base (stored
+    # or gemma3's 10000), the sliding pattern (every 6th layer global by
+    # default, a period or a per-layer array), no sliding layer when the
+    # window is 0, and the models these forwards cannot run are refused.
+    from nncpu_amd.gemma import gemma3_config_from_kv
+    c = gemma3_config_from_kv(_gemma_kv(), 256, 1)
+    assert (c.swa_period, c.window, c.rope_base, c.rope_base_swa) == (6, 512, 1e6, 10000.0)
+    c = gemma3_config_from_kv(_gemma_kv(**{"rope.freq_base_swa": 5e4, "attention.sliding_window_pattern": 4}), 256, 1)
+    assert (c.swa_period, c.rope_base_swa) == (4, 5e4)
+    pat = np.array([(i + 1) % 3 != 0 for i in range(12)], np.int32)
+    assert gemma3_config_from_kv(_gemma_kv(**{"attention.sliding_window_pattern": pat}), 256, 1).swa_period == 3
+    c = gemma3_config_from_kv(_gemma_kv(**{"attention.sliding_window": 0}), 256, 1)
+    assert c.swa_period == 0  # no layer slides: every layer keeps the global base
+    bad = [{"rope.scaling.type": "linear", "rope.scaling.factor": 8.0},
+           {"attention.sliding_window_pattern": np.array([1, 0] + [1] * 10, np.int32)},
+           {"attention.sliding_window_pattern": 0}]
+    for extra in bad:
+        with pytest.raises(ValueError):
+            gemma3_config_from_kv(_gemma_kv(**extra), 256, 1)

@@ -207,3 +207,39 @@ def test_i8_producer_quantization_matches_library_quantizer(N, case):
     assert np.array_equal(g0, t0) and np.array_equal(gk0, k0) and np.array_equal(gv0, v0)
     assert np.array_equal(g1, t0), (g1, t0)
     assert np.array_equal(gk1, k0) and np.array_equal(gv1, v0)
+
+
+def test_qwen25_7b_width_layer_prefill_512(N):
+    # One layer at Qwen2.5-7B's full width (d 3584, 28 query / 4 KV heads of
+    # 128 = 7 per KV head, FFN 18944, q/k/v biases, NeoX RoPE base 1e6), the
+    # 512-token prompt in one forward as the timed prefill runs it, then
+    # greedy tokens: hidden states and K/V cache identical to the CPU forward
+    # (forward.rs:197-439,719-841 restated), matmuls bit-exact in both.
+    from nncpu_amd.models import Model, qwen25_7b_config
+    cfg = qwen25_7b_config(n_ctx=520, n_layer=1)
+    cfg.n_vocab = 2048
+    model = Model.random(cfg, seed=0x7B7)
+    prompt = np.random.default_rng(9).integers(0, cfg.n_vocab, 512).astype(np.int32)
+    run_both(model, prompt, 4, batch=512)
+
+
+def test_qwen2_seven_query_heads_per_kv_head(N):
+    # Qwen2.5-7B's grouping, 7 query heads per KV head at head_dim 128 (4
+    # tokens per attention tile, 28 of its 32 query rows used), over more
+    # than one 256-key block, in 16-token prompt batches, one-token decodes
+    # and decode-graph replays.
+    import torch
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=896, n_head=7, n_kv=1, n_ff=1024, n_vocab=1024, n_ctx=300, head_dim=128)
+    model = Model.random(cfg, seed=0x77)
+    prompt = np.random.default_rng(10).integers(0, cfg.n_vocab, 270).astype(np.int32)
+    tc = run_both(model, prompt, 8)
+    _, _, kc, vc = model.cpu_generate(prompt, 8)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=16, stream=s.cuda_stream)
+    try:
+        tg, _, kg, vg = dev.generate_graph(prompt, 8, stream=s)
+    finally:
+        dev.free()
+    assert np.array_equal(tg, tc), (tg, tc)
+    assert np.array_equal(kg, kc) and np.array_equal(vg, vc)

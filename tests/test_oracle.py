@@ -9,6 +9,10 @@ fixes, chosen so a plausible restatement mistake fails one of them:
   * batch == single and thread-count invariance, bit for bit;
   * the scalar restatement == the AVX2-intrinsics restatement, bit for bit
     (two independent writings of the same reduction trees);
+  * known answers of the row kernels, the Q4 bias dot and block_sums whose
+    inputs tell the candidate reduction orders apart, derived by exact
+    rational arithmetic rounded per operation (tests/row_kats.py,
+    tests/f32_exact.py);
   * the committed golden vectors (tests/golden/).
 """
 import json
@@ -18,6 +22,9 @@ import numpy as np
 import pytest
 
 from conftest import bits, close
+from f32_exact import Lcg, bf16_value, block_sums_ref, dot_bf16_ref, f32_bits, row_candidates, row_ref
+from row_kats import (DOT_KATS, Q4_BIAS_DISCRIMINATED, Q4_KATS, Q8_KATS, dot_candidates, dot_inputs,
+                      q4_candidates, q4_inputs, q4_ref, q4_split, q8_inputs, q8_split)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -255,12 +262,74 @@ def test_argmax_ties_and_nan(oracle):
 # ---- dot_bf16_f32 (scalar.rs:334-347) ----------------------------------------------
 
 def test_dot_bf16_tail_is_unfused(oracle):
+    # Known answers (tests/row_kats.py): the 8-lane fused body, hsum8, then
+    # the tail s += a*b with the product rounded before the add. A fused
+    # tail, the tail folded into the lanes, another hsum8 tree or one chain
+    # each give other bits on these inputs, and the oracle gives these.
+    for seed, n, want in DOT_KATS:
+        a, b = dot_inputs(seed, n)
+        bv = [bf16_value(h) for h in a]
+        assert f32_bits(dot_bf16_ref(bv, b)) == want
+        for name, v in dot_candidates(a, b).items():
+            assert f32_bits(v) != want, (n, name)
+        got = oracle.dot_bf16_f32(np.array(a, np.uint16), np.array(b, np.float32))
+        assert f32_bits(got) == want, (n, hex(f32_bits(got)))
+    # And within 1e-5 of the f64 dot on random data.
     rng = oracle.Rng(0xD07)
     for n in (1, 7, 8, 9, 36, 37, 1025):
         a = np.array([oracle.f32_to_bf16(float(v)) for v in rng.vec(n, -1, 1)], np.uint16)
         b = rng.vec(n, -1, 1)
         want = (oracle.bf16_array_to_f32(a).astype(np.float64) * b).sum()
         assert abs(oracle.dot_bf16_f32(a, b) - want) <= 1e-5 * max(1.0, abs(want))
+
+
+# ---- q8_row / q4_row reduction order (scalar.rs:108-117, 626-742) -------------------
+
+def test_q8_row_known_answers(oracle):
+    # 32 fused chains (element e of every block into accumulator e // 8, lane
+    # e % 8), blocks in order, add8(add8(a0, a1), add8(a2, a3)), hsum8. The
+    # inputs make every other order give other bits; scalar and AVX2
+    # restatements, one row and a batch of three (q8_row3) give these.
+    for seed, nb, want in Q8_KATS:
+        q, s, x, w = q8_inputs(seed, nb)
+        assert f32_bits(row_ref(w, x, nb)) == want
+        for name, v in row_candidates(w, x, nb).items():
+            assert f32_bits(v) != want, (nb, name)
+        m = oracle.QMatrix(1, 1, 32 * nb, q8_split(q, s))
+        xv = np.array(x, np.float32)
+        for backend in ("scalar", "avx2"):
+            assert f32_bits(oracle.gemv_batch(m, xv, backend=backend)[0]) == want, backend
+            y3 = oracle.gemv_batch(m, np.tile(xv, 3), 3, backend=backend)
+            assert all(f32_bits(v) == want for v in y3), backend
+
+
+def test_q4_row_known_answers(oracle):
+    # As q8_row with byte i of a block giving element i (low nibble) and
+    # i + 16 (high), plus the bias term dot_bf16_f32(biases, block_sums(x))
+    # added once; ggml's interleaved nibbles and each wrong bias-dot form give
+    # other bits.
+    for seed, nb, want in Q4_KATS:
+        qb, s, bi, x = q4_inputs(seed, nb)
+        assert f32_bits(q4_ref(qb, s, bi, x, nb)) == want
+        for name, v in q4_candidates(qb, s, bi, x, nb).items():
+            if name.startswith("bias_") and nb not in Q4_BIAS_DISCRIMINATED:
+                continue
+            assert f32_bits(v) != want, (nb, name)
+        m = oracle.QMatrix(2, 1, 32 * nb, q4_split(qb, s, bi))
+        xv = np.array(x, np.float32)
+        for backend in ("scalar", "avx2"):
+            assert f32_bits(oracle.gemv_batch(m, xv, backend=backend)[0]) == want, backend
+            y3 = oracle.gemv_batch(m, np.tile(xv, 3), 3, backend=backend)
+            assert all(f32_bits(v) == want for v in y3), backend
+
+
+def test_block_sums_known_answer(oracle):
+    # block_sums' tree on full-mantissa inputs: oracle == exact-rounding restatement.
+    g = Lcg(0xB5)
+    x = [g.f32_wide(-10, 10) for _ in range(32 * 5)]
+    want = [f32_bits(v) for v in block_sums_ref(x)]
+    got = oracle.block_sums(np.array(x, np.float32))
+    assert [f32_bits(float(v)) for v in got] == want
 
 
 # ---- int8 path: exact block dots and the exact-sum reference -----------------------
