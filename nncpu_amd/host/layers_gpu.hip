@@ -21,6 +21,8 @@
 //               sum (scalar.rs:444-519)
 //   attn_merge  the partials merged in block order with glibc's expf, each
 //               head's output divided by its weight sum (scalar.rs:521-548)
+//   (one token: qkv_post's work runs inside the attention kernel, and when
+//   the grid is one 256-key block so does the merge: one launch for all three)
 //   r           = W_o attn
 //   resid_norm  x += post_attention_norm(r) (Gemma) or r; normed = ffn_norm(x)
 //   gu          = [W_gate; W_up] normed (fused, or gate and up into halves)
@@ -66,7 +68,7 @@ __device__ __forceinline__ float hsum8(const float* a) {
 // sum_sq (scalar.rs:232-250) of v[0..dim) (LDS), run by one wave: lanes
 // 0..7 each run FMA lane l over the whole 8-chunks in order, hsum8, then
 // the tail in f64. The result (a double) is returned to every lane.
-__device__ double row_sumsq(const float* v, int dim, int lane) {
+__device__ __forceinline__ double row_sumsq(const float* v, int dim, int lane) {
     const int body = dim & ~7;
     float a = 0.0f;
     if (lane < 8) {
@@ -764,6 +766,43 @@ struct V8 {
     }
 };
 
+// One token's q head `qh` (wave 0) and, when `own`, its key and value rows of
+// KV head `kvh` (waves 1 and 2), into rows[0..2][hd] (LDS): qkv_post_kernel's
+// operations in its order (bias, per-head RMSNorm, RoPE at position p0, the
+// value row with its bias only). Every wave of the workgroup calls it (it
+// holds barriers); wave 3 only waits.
+template <int HD>
+__device__ __forceinline__ void decode_qkv_rows(const QkvArgs& a, float* rows, int qh, int kvh, bool own, int p0,
+                                                int wave, int lane) {
+    const int kind = wave < 3 ? wave : 3;
+    const bool act = kind == 0 || (kind < 3 && own);
+    const int off = kind == 0 ? qh * HD : (kind == 1 ? a.H * HD + kvh * HD : a.H * HD + a.KV * HD + kvh * HD);
+    float* v = rows + (kind < 3 ? kind : 0) * HD;
+    if (act)
+        for (int i = lane; i < HD; i += 64) v[i] = a.bias ? __fadd_rn(a.qkv[off + i], a.bias[off + i]) : a.qkv[off + i];
+    __syncthreads();
+    const float* g = kind == 0 ? a.qn : a.kn;
+    if (act && kind < 2 && g) {
+        const float sc = rms_of_d(row_sumsq(v, HD, lane), HD, a.eps);
+        for (int i = lane; i < HD; i += 64) v[i] = __fmul_rn(__fmul_rn(v[i], sc), g[i]);
+    }
+    __syncthreads();
+    if (act && kind < 2) {
+        const int half = HD / 2;
+        const int stride = a.rope_mode == NNG_ROPE_NORM ? 2 : 1, partner = a.rope_mode == NNG_ROPE_NORM ? 1 : half;
+        const int pr = p0 < a.n_ctx ? p0 : a.n_ctx - 1;
+        const float* cs = a.cs + (size_t)pr * half;
+        const float* sn = a.sn + (size_t)pr * half;
+        for (int i = lane; i < half; i += 64) {
+            const int p = i * stride;
+            const float x0 = v[p], x1 = v[p + partner], c = cs[i], sv = sn[i];
+            v[p] = __fsub_rn(__fmul_rn(c, x0), __fmul_rn(sv, x1));
+            v[p + partner] = __fadd_rn(__fmul_rn(sv, x0), __fmul_rn(c, x1));
+        }
+    }
+    __syncthreads();
+}
+
 // One token's partial (decode) for query head x of KV head y over its block
 // b0 + z: attn_tile_kernel's arithmetic for a single row, spread over more
 // workgroups (one per head and block) for latency: the block's K and V rows
@@ -773,13 +812,28 @@ struct V8 {
 // as there, thread i the V chain of column i (from -0, so the first key's
 // FMA is w * v exactly). Its LDS (the staged rows) allows at most two
 // workgroups per CU, so the registers are budgeted for two waves per SIMD.
+//
+// qkv_post_kernel's work for the rows this workgroup reads is done here first, by the same operations
+// (so the same bits): wave 0 forms the query head (bias, q norm, RoPE) in
+// LDS, waves 1 and 2 the token's key and value rows when the token's
+// position lies in this workgroup's block (those rows then replace the
+// cache's row in the staged copy, and query head 0 of the KV head appends
+// them to the cache as BF16). With `direct` (the grid holds one block, so
+// every head's span is that block) the workgroup also finishes the head as
+// attn_merge_kernel does for a single partial (o times 1 / l) and writes the
+// attention output and its int8 row (qo) itself, so neither the
+// qkv_post nor the merge launch is needed.
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(AttnArgs a,
+                                                                                                     QkvArgs qa,
+                                                                                                     QOut qo,
+                                                                                                     int direct) {
     constexpr int KS = HD + 8, PR = HD / 8;
     extern __shared__ __align__(16) float lds[];
     float* sc = lds;                                   // [256]
     uint16_t* kv = (uint16_t*)(lds + ATTN_BLOCK + 4);  // [256][KS]
-    __shared__ float mh;
+    __shared__ float mh, lsh;
+    __shared__ __align__(16) float rows[3][HD];  // the token's q head, k and v rows
     const int hh = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.G, pw = HD + 2, KVD = a.KV * HD;
     int p0, n_seq, first, last;
@@ -796,13 +850,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int U = PR < 16 ? PR : 16, NB = PR / U;
     constexpr bool KV2 = HD <= 128;
     uint16_t* vv = KV2 ? kv + ATTN_BLOCK * KS : kv;
+    // The token's own key and value rows are this block's when its position
+    // is (a position past the context lies in no block).
+    const bool own = p0 >= k0 && p0 <= k1;
     if constexpr (KV2) {
+        decode_qkv_rows<HD>(qa, &rows[0][0], kvh * G + hh, kvh, own, p0, wave, lane);
         uint4 rk[U], rv[U];
         kv_load<HD, U>(rk, a.kc, k0, nk, KVD, kvh, tid, 0);
         kv_load<HD, U>(rv, a.vc, k0, nk, KVD, kvh, tid, 0);
         kv_store<HD, U>(rk, kv, tid, 0);
         kv_store<HD, U>(rv, vv, tid, 0);
     } else {
+        decode_qkv_rows<HD>(qa, &rows[0][0], kvh * G + hh, kvh, own, p0, wave, lane);
 #pragma unroll
         for (int bt = 0; bt < NB; ++bt) {
             uint4 r[U];
@@ -810,9 +869,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             kv_store<HD, U>(r, kv, tid, bt * U);
         }
     }
+    if (own) {
+        __syncthreads();  // every staged row is stored: the token's rows replace its stale one
+        uint16_t* kd = qa.kc + (size_t)p0 * KVD + kvh * HD;  // the same cache as a.kc, writable
+        uint16_t* vd = qa.vc + (size_t)p0 * KVD + kvh * HD;
+        for (int i = tid; i < HD; i += 256) {
+            const uint16_t kb = to_bf16(rows[1][i]), vb = to_bf16(rows[2][i]);
+            kv[(p0 - k0) * KS + i] = kb;
+            if (KV2) vv[(p0 - k0) * KS + i] = vb;
+            if (hh == 0) {
+                kd[i] = kb;
+                vd[i] = vb;
+            }
+        }
+    }
     __syncthreads();
     if (tid < nk) {
-        const float* __restrict__ qg = a.qkv + (size_t)__builtin_amdgcn_readfirstlane((kvh * G + hh) * HD);
+        const float* qg = &rows[0][0];
         const uint16_t* kr = kv + tid * KS;
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -852,6 +925,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             for (int j = body; j < nk; ++j) ls = __fadd_rn(ls, sc[j]);
             part[HD] = mh;
             part[HD + 1] = ls;
+            lsh = ls;
         }
     }
     if constexpr (!KV2) {
@@ -861,6 +935,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             uint4 r[U];
             kv_load<HD, U>(r, a.vc, k0, nk, KVD, kvh, tid, bt * U);
             kv_store<HD, U>(r, kv, tid, bt * U);
+        }
+        if (own) {
+            __syncthreads();
+            for (int i = tid; i < HD; i += 256) kv[(p0 - k0) * KS + i] = to_bf16(rows[2][i]);
         }
     }
     __syncthreads();
@@ -886,7 +964,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             }
         }
         for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(vv[j * KS + tid]), o);
-        part[tid] = o;
+        if (direct) {
+            // attn_merge_kernel with one partial: o * (1 / l).
+            const float al = lsh;
+            const float inv = al > 0.0f ? __fdiv_rn(1.0f, al) : 0.0f;
+            const float v = __fmul_rn(o, inv);
+            const int j = (kvh * G + hh) * HD + tid;
+            a.out[j] = v;
+            if (qo.q) q8_value(v, j, qo);
+        } else {
+            part[tid] = o;
+        }
     }
 }
 
@@ -1181,7 +1269,8 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     m->lds_dec = (size_t)(ATTN_BLOCK + 4) * 4 + (size_t)(hd <= 128 ? 2 : 1) * ATTN_BLOCK * (hd + 8) * 2;
     const void* dk = hd == 32 ? (const void*)attn_decode_kernel<32>
                      : hd == 64 ? (const void*)attn_decode_kernel<64>
-                     : hd == 128 ? (const void*)attn_decode_kernel<128> : (const void*)attn_decode_kernel<256>;
+                     : hd == 128 ? (const void*)attn_decode_kernel<128>
+                                 : (const void*)attn_decode_kernel<256>;
     NNGL_CHECK(hipFuncSetAttribute(dk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_dec));
     // The weights' layouts and the stream's scratch for this mode and batch
     // (and for one token), so no forward allocates and a forward can be
@@ -1286,20 +1375,24 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
                    c.rope_mode,
                    c.n_ctx,
                    c.rms_eps};
-        qkv_post_kernel<<<dim3(n, H + 2 * KV), 64, (size_t)hd * 4, st>>>(qa);
+        // One token: the attention kernel does qkv_post's work itself and,
+        // when the grid is one block, the merge too.
+        if (n != 1) qkv_post_kernel<<<dim3(n, H + 2 * KV), 64, (size_t)hd * 4, st>>>(qa);
         AttnArgs aa{m->qkv, kcl, vcl, m->parts, m->attn, m->expt, posp, KV, G, hd, QKV, m->nblk, (int)pos0,
                     n_seq, sliding ? c.window : 0, n, m->tq, c.n_ctx, c.attn_scale};
         const dim3 ag((n + m->tq - 1) / m->tq, KV, nblk);
+        const bool direct = n == 1 && nblk == 1;
         if (n == 1) {
             const dim3 dg(G, KV, nblk);
+            const int dr = direct ? 1 : 0;
             if (hd == 32)
-                attn_decode_kernel<32><<<dg, 256, m->lds_dec, st>>>(aa);
+                attn_decode_kernel<32><<<dg, 256, m->lds_dec, st>>>(aa, qa, oa, dr);
             else if (hd == 64)
-                attn_decode_kernel<64><<<dg, 256, m->lds_dec, st>>>(aa);
+                attn_decode_kernel<64><<<dg, 256, m->lds_dec, st>>>(aa, qa, oa, dr);
             else if (hd == 128)
-                attn_decode_kernel<128><<<dg, 256, m->lds_dec, st>>>(aa);
+                attn_decode_kernel<128><<<dg, 256, m->lds_dec, st>>>(aa, qa, oa, dr);
             else
-                attn_decode_kernel<256><<<dg, 256, m->lds_dec, st>>>(aa);
+                attn_decode_kernel<256><<<dg, 256, m->lds_dec, st>>>(aa, qa, oa, dr);
         } else if (hd == 32)
             attn_tile_kernel<32><<<ag, 256, m->lds_attn, st>>>(aa);
         else if (hd == 64)
@@ -1308,7 +1401,7 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
             attn_tile_kernel<128><<<ag, 256, m->lds_attn, st>>>(aa);
         else
             attn_tile_kernel<256><<<ag, 256, m->lds_attn, st>>>(aa);
-        attn_merge_kernel<<<dim3(KV, n), merge_threads, 0, st>>>(aa, oa);
+        if (!direct) attn_merge_kernel<<<dim3(KV, n), merge_threads, 0, st>>>(aa, oa);
         NNGL_CHECK(hipGetLastError());
         if (gemv_q(m, W[3], qt, m->attn, QD, m->r, E, n_tok)) return 1;
         launch_resid_norm(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed, nullptr, n, E, c.rms_eps, oe,
