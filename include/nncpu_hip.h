@@ -170,7 +170,7 @@ const void* nnh_weight_device_data(const nnh_weight* w);
  * blocks, and the Q4 biases as uploaded. For callers that fuse their own
  * work around that matmul, as the device-resident decode step does; no
  * counterpart in the reference, whose forward calls the matmul per weight.
- * NNH_E_INVALID when the weight is tall (16384 rows or more with x of at
+ * NNH_E_INVALID when the weight is tall (12288 rows or more with x of at
  * most 64 KB: those take the 8-lane layout instead). Read-only, valid until
  * nnh_free. */
 typedef struct {
@@ -205,9 +205,9 @@ int nnh_model_argmax(const nnh_weight* w, const float* x, size_t* out_row, int a
  * floats), logits (rows floats, written: W x) and work
  * (nnh_model_argmax_work_bytes(w) bytes) are device buffers, *out_row (a
  * device u64) receives the row; asynchronous on `stream`. For the matrices
- * of 16384 rows or more the first argmax stage runs inside the gemv (each
+ * of 12288 rows or more the first argmax stage runs inside the gemv (each
  * workgroup's best row), so only a one-workgroup reduction follows it.
- * Calls on different streams must not share `work`; a Q4 matrix under 16384
+ * Calls on different streams must not share `work`; a Q4 matrix under 12288
  * rows also uses the scratch of `stream` (as nnh_gemv_batch_dev). */
 size_t nnh_model_argmax_work_bytes(const nnh_weight* w);
 int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, void* work, uint64_t* out_row,

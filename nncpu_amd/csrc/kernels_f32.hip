@@ -45,6 +45,8 @@
 
 #include <algorithm>
 
+#include <type_traits>
+
 #include "common.h"
 #include "f32_m1.h"
 
@@ -879,20 +881,20 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
 
 // The 8-lane mapping (tall matrices).
 
-constexpr int V2_R = 4;  // rows per lane group: four rows share every x load
+constexpr int V2_R = 4;  // rows per lane group of the multi-vector form on tall matrices
 
-// One block for the lane group's V2_R rows: w[r][e] (exact weights) against
+// One block for the lane group's R rows: w[r][e] (exact weights) against
 // x[32b + 4j + e] of every token, read from the workgroup's LDS copy of x
 // (LDS reads wait on their own counter, so they never wait for the weight
 // loads in flight).
-template <int M>
-__device__ __forceinline__ void v2_block(float (&acc)[V2_R][M][4], const float (&w)[V2_R][4],
-                                         const float* xl, int cols, int e0) {
+template <int R, int M>
+__device__ __forceinline__ void v2_block(float (&acc)[R][M][4], const float (&w)[R][4], const float* xl, int cols,
+                                         int e0) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         const float4 xv = *(const float4*)(xl + m * cols + e0);
 #pragma unroll
-        for (int r = 0; r < V2_R; ++r) {
+        for (int r = 0; r < R; ++r) {
             acc[r][m][0] = __builtin_fmaf(w[r][0], xv.x, acc[r][m][0]);
             acc[r][m][1] = __builtin_fmaf(w[r][1], xv.y, acc[r][m][1]);
             acc[r][m][2] = __builtin_fmaf(w[r][2], xv.z, acc[r][m][2]);
@@ -901,70 +903,99 @@ __device__ __forceinline__ void v2_block(float (&acc)[V2_R][M][4], const float (
     }
 }
 
-template <int DT>
+// One group of the lane's rows in flight: the 16-byte quant pieces and the
+// group's BF16 scales (Q8: 4, in s.x and s.y; Q4: 8).
+template <int DT, int R>
 struct V2Group {
-    uint4 q[V2_R], s[V2_R];
+    uint4 q[R];
+    typename std::conditional<DT == 1, uint2, uint4>::type s[R];
 };
 
-template <int DT>
-__device__ __forceinline__ void v2_load(V2Group<DT>& gr, const uint4* const (&qrow)[V2_R],
-                                        const uint16_t* const (&srow)[V2_R], int g) {
+template <int DT, int R>
+__device__ __forceinline__ void v2_load(V2Group<DT, R>& gr, const uint4* const (&qrow)[R],
+                                        const uint16_t* const (&srow)[R], int g) {
 #pragma unroll
-    for (int r = 0; r < V2_R; ++r) {
+    for (int r = 0; r < R; ++r) {
         gr.q[r] = load_nt16u(qrow[r] + (size_t)g * 32 * 8);
-        if (DT == 1) {
-            const uint2 v = *(const uint2*)(srow[r] + 4 * g);
-            gr.s[r] = make_uint4(v.x, v.y, 0u, 0u);
-        } else {
+        if constexpr (DT == 1)
+            gr.s[r] = *(const uint2*)(srow[r] + 4 * g);
+        else
             gr.s[r] = *(const uint4*)(srow[r] + 8 * g);
+    }
+}
+
+__device__ __forceinline__ uint32_t half2_of(const uint2& v, int i) {
+    return ((i < 2 ? v.x : v.y) >> (16 * (i & 1))) & 0xffffu;
+}
+
+// The exact weights of block i of the group for the lane's R rows
+// (elements 4j..4j+3).
+template <int DT, int R>
+__device__ __forceinline__ void v2_weights(float (&w)[R][4], const V2Group<DT, R>& gr, int i) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if constexpr (DT == 1) {
+            const uint32_t qw = i == 0 ? gr.q[r].x : i == 1 ? gr.q[r].y : i == 2 ? gr.q[r].z : gr.q[r].w;
+            const float s = bf16f(half2_of(gr.s[r], i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[r][e] = (float)(int8_t)(qw >> (8 * e)) * s;  // exact
+        } else {
+            const int k = i >> 1, half = i & 1;
+            const uint32_t qw = k == 0 ? gr.q[r].x : k == 1 ? gr.q[r].y : k == 2 ? gr.q[r].z : gr.q[r].w;
+            uint32_t nib = (qw >> (4 * half)) & 0x0f0f0f0fu;
+            // Opaque to the compiler: it would fold the mask into a bit-field
+            // extract per element instead of converting the bytes directly.
+            asm volatile("" : "+v"(nib));
+            const float s = bf16f(half_of(gr.s[r], i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[r][e] = (float)((nib >> (8 * e)) & 0xffu) * s;  // exact
         }
     }
 }
 
-template <int DT, int M>
-__device__ __forceinline__ void v2_group(float (&acc)[V2_R][M][4], const V2Group<DT>& gr, int g, int nb,
+// Blocks G*g .. G*g + G - 1 (those below nb unless FULL). One vector: the
+// group's x pieces are read from LDS first, so one wait covers the group.
+template <int DT, int R, int M, bool FULL>
+__device__ __forceinline__ void v2_group(float (&acc)[R][M][4], const V2Group<DT, R>& gr, int g, int nb,
                                          const float* xl, int j) {
-    if (DT == 1) {
+    constexpr int G = DT == 1 ? 4 : 8;
+    if constexpr (M == 1) {
+        float4 xv[G];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = 4 * g + i;
-            if (b >= nb) break;
-            float w[V2_R][4];
+        for (int i = 0; i < G; ++i)
+            if (FULL || G * g + i < nb) xv[i] = *(const float4*)(xl + 32 * (G * g + i) + 4 * j);
 #pragma unroll
-            for (int r = 0; r < V2_R; ++r) {
-                const uint32_t qw = i == 0 ? gr.q[r].x : i == 1 ? gr.q[r].y : i == 2 ? gr.q[r].z : gr.q[r].w;
-                const float s = bf16f(half_of(gr.s[r], i));
+        for (int i = 0; i < G; ++i) {
+            if (!FULL && G * g + i >= nb) break;
+            float w[R][4];
+            v2_weights<DT, R>(w, gr, i);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[r][e] = (float)(int8_t)(qw >> (8 * e)) * s;  // exact
+            for (int r = 0; r < R; ++r) {
+                acc[r][0][0] = __builtin_fmaf(w[r][0], xv[i].x, acc[r][0][0]);
+                acc[r][0][1] = __builtin_fmaf(w[r][1], xv[i].y, acc[r][0][1]);
+                acc[r][0][2] = __builtin_fmaf(w[r][2], xv[i].z, acc[r][0][2]);
+                acc[r][0][3] = __builtin_fmaf(w[r][3], xv[i].w, acc[r][0][3]);
             }
-            v2_block<M>(acc, w, xl, nb * 32, 32 * b + 4 * j);
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int b = 8 * g + 2 * k + half;
-                if (b >= nb) break;
-                float w[V2_R][4];
-#pragma unroll
-                for (int r = 0; r < V2_R; ++r) {
-                    const uint32_t qw = k == 0 ? gr.q[r].x : k == 1 ? gr.q[r].y : k == 2 ? gr.q[r].z : gr.q[r].w;
-                    const uint32_t nib = (qw >> (4 * half)) & 0x0f0f0f0fu;
-                    const float s = bf16f(half_of(gr.s[r], 2 * k + half));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) w[r][e] = (float)((nib >> (8 * e)) & 0xffu) * s;  // exact
-                }
-                v2_block<M>(acc, w, xl, nb * 32, 32 * b + 4 * j);
-            }
+        for (int i = 0; i < G; ++i) {
+            const int b = G * g + i;
+            if (!FULL && b >= nb) break;
+            float w[R][4];
+            v2_weights<DT, R>(w, gr, i);
+            v2_block<R, M>(acc, w, xl, nb * 32, 32 * b + 4 * j);
         }
     }
 }
 
 // Workgroup: 4 waves = 32 lane groups; lane group lg of workgroup wg runs
-// rows (wg * V2_R + r) * 32 + lg for r < V2_R, one row from each of V2_R
-// consecutive 32-row tiles.
-template <int DT, int M>
+// rows (wg * R + r) * 32 + lg for r < R, one row from each of R consecutive
+// 32-row tiles (R rows share every x read; fewer rows per lane group give
+// more waves to a shorter matrix). PF groups of weights are in flight per
+// lane: group g in slot g % PF, each slot refilled with the group PF ahead
+// right after its arithmetic.
+template <int DT, int M, int R, int PF>
 __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restrict__ fq,
                                                           const uint16_t* __restrict__ fs,
                                                           const uint16_t* __restrict__ biases,
@@ -975,12 +1006,12 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
     constexpr int G = DT == 1 ? 4 : 8;
     const int j = threadIdx.x & 7, lg = threadIdx.x >> 3;
     const int ng = (nb + G - 1) / G;
-    int row[V2_R];
-    const uint4* qrow[V2_R];
-    const uint16_t* srow[V2_R];
+    int row[R];
+    const uint4* qrow[R];
+    const uint16_t* srow[R];
 #pragma unroll
-    for (int r = 0; r < V2_R; ++r) {
-        const int tile = blockIdx.x * V2_R + r;
+    for (int r = 0; r < R; ++r) {
+        const int tile = blockIdx.x * R + r;
         const int raw = tile * 32 + lg;
         row[r] = raw < rows ? raw : rows - 1;  // keep loads in bounds; stores are skipped
         const int t = row[r] / 32;
@@ -989,17 +1020,20 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
         srow[r] = fs + (size_t)row[r] * nbp;
     }
 
-    float acc[V2_R][M][4];
+    float acc[R][M][4];
 #pragma unroll
-    for (int r = 0; r < V2_R; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[r][m][e] = 0.0f;
 
-    // The first weight group is in flight while x is copied to LDS.
-    V2Group<DT> ga, gb;
-    v2_load<DT>(ga, qrow, srow, 0);
+    // The first PF weight groups are in flight while x is copied to LDS
+    // (indices clamped to the row's last group: a few repeated loads at the
+    // row's end are never used).
+    V2Group<DT, R> slot[PF];
+#pragma unroll
+    for (int d = 0; d < (PF == 2 ? 1 : PF); ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
     extern __shared__ float xl[];  // [M][cols]
     const int cols = nb * 32;
     for (int m = 0; m < M; ++m)
@@ -1007,19 +1041,38 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
             *(float4*)(xl + m * cols + i) = __builtin_bit_cast(float4, *(const f4u*)(x + (size_t)m * x_stride + i));
     __syncthreads();
 
-    // One group ahead: its quants and scales load while this one is used.
-    for (int g = 0; g < ng; g += 2) {
-        if (g + 1 < ng) v2_load<DT>(gb, qrow, srow, g + 1);
-        v2_group<DT, M>(acc, ga, g, nb, xl, j);
-        if (g + 1 >= ng) break;
-        if (g + 2 < ng) v2_load<DT>(ga, qrow, srow, g + 2);
-        v2_group<DT, M>(acc, gb, g + 1, nb, xl, j);
+    if constexpr (PF == 2) {
+        // Two slots: the next group's loads are issued before this group's
+        // arithmetic.
+        for (int g = 0; g < ng; g += 2) {
+            if (g + 1 < ng) v2_load<DT, R>(slot[1], qrow, srow, g + 1);
+            v2_group<DT, R, M, false>(acc, slot[0], g, nb, xl, j);
+            if (g + 1 >= ng) break;
+            if (g + 2 < ng) v2_load<DT, R>(slot[0], qrow, srow, g + 2);
+            v2_group<DT, R, M, false>(acc, slot[1], g + 1, nb, xl, j);
+        }
+    } else {
+        // Whole groups in rounds of PF, then the rest (the last group may
+        // be partial).
+        const int ngf = nb / G;
+        int g = 0;
+        for (; g + PF <= ngf; g += PF) {
+#pragma unroll
+            for (int d = 0; d < PF; ++d) {
+                v2_group<DT, R, M, true>(acc, slot[d], g + d, nb, xl, j);
+                const int gn = g + d + PF;
+                v2_load<DT, R>(slot[d], qrow, srow, gn < ng ? gn : ng - 1);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < PF; ++d)
+            if (g + d < ng) v2_group<DT, R, M, false>(acc, slot[d], g + d, nb, xl, j);
     }
 
     uint64_t key = 0;  // this lane's largest argmax key (M = 1, part != nullptr)
 #pragma unroll
-    for (int r = 0; r < V2_R; ++r) {
-        const bool valid = (blockIdx.x * V2_R + r) * 32 + lg < rows;
+    for (int r = 0; r < R; ++r) {
+        const bool valid = (blockIdx.x * R + r) * 32 + lg < rows;
         float bdot[M];
         if (DT == 2) {
             // dot_bf16_f32 (scalar.rs:334-347): lane j runs accumulator lane j
@@ -1080,16 +1133,38 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
     }
 }
 
+template <int DT, int M, int R, int PF>
+void launch_v2_rp(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, size_t xs,
+                  const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, uint64_t* part, hipStream_t st) {
+    const dim3 grid(ceil_div(rows, 32 * R)), block(256);
+    const size_t lds = (size_t)M * nb * 32 * sizeof(float);
+    gemv_f32_v2_kernel<DT, M, R, PF><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part);
+}
+
+// Rows per lane group: one vector takes one (the most waves; measured
+// faster than four at every height up to the vocabulary heads). Several
+// vectors take four, so that each x read serves four rows, when that still
+// leaves a workgroup per CU (two vectors: four per CU), else one; the
+// prefetch depth is four groups for one vector, two for several.
+template <int DT, int M>
+void launch_v2_m(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, size_t xs,
+                 const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, uint64_t* part, hipStream_t st) {
+    if constexpr (M == 1)
+        launch_v2_rp<DT, 1, 1, 4>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part, st);
+    else if (ceil_div(rows, 32 * V2_R) >= (M == 2 ? 4 : 1) * cu_count())
+        launch_v2_rp<DT, M, V2_R, 2>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part, st);
+    else
+        launch_v2_rp<DT, M, 1, 2>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part, st);
+}
+
 template <int DT>
 void launch_dt_v2(int M, const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const float* x, size_t xs,
                   const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, hipStream_t st) {
-    dim3 grid(ceil_div(rows, 32 * V2_R)), block(256);
-    const size_t lds = (size_t)M * nb * 32 * sizeof(float);
     switch (M) {
-        case 1: gemv_f32_v2_kernel<DT, 1><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
-        case 2: gemv_f32_v2_kernel<DT, 2><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
-        case 3: gemv_f32_v2_kernel<DT, 3><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
-        default: gemv_f32_v2_kernel<DT, 4><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr); break;
+        case 1: launch_v2_m<DT, 1>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr, st); break;
+        case 2: launch_v2_m<DT, 2>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr, st); break;
+        case 3: launch_v2_m<DT, 3>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr, st); break;
+        default: launch_v2_m<DT, 4>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, nullptr, st); break;
     }
 }
 
@@ -1141,20 +1216,16 @@ void launch_block_sums(const float* x, size_t x_stride, int nb, int n_tok, float
 
 // Tokens in chunks of up to four per launch: every token's chains are
 // independent, so the chunking never changes a bit.
-int f32_v2_parts(int rows) { return ceil_div(rows, 32 * V2_R); }
+int f32_v2_parts(int rows) { return ceil_div(rows, 32); }  // one vector: one row per lane group
 
 void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
                                const float* x, float* xsum, int rows, int nb, int nbp, float* y, uint64_t* part,
                                hipStream_t st) {
     if (dtype == 2) launch_block_sums(x, (size_t)nb * 32, nb, 1, xsum, st);
-    const dim3 grid(f32_v2_parts(rows)), block(256);
-    const size_t lds = (size_t)nb * 32 * sizeof(float);
     if (dtype == 1)
-        gemv_f32_v2_kernel<1, 1><<<grid, block, lds, st>>>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y,
-                                                           rows, part);
+        launch_v2_m<1, 1>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y, rows, part, st);
     else
-        gemv_f32_v2_kernel<2, 1><<<grid, block, lds, st>>>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y,
-                                                           rows, part);
+        launch_v2_m<2, 1>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y, rows, part, st);
 }
 
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,

@@ -61,13 +61,14 @@ def kat_cases():
     return [(1,) + k for k in Q8_KATS] + [(2,) + k for k in Q4_KATS]
 
 
-@pytest.mark.parametrize("rows", [4, 2048, 16384])
+@pytest.mark.parametrize("rows", [4, 2048, 16384, 32768])
 @pytest.mark.parametrize("kat", kat_cases(), ids=lambda k: f"{'Q8' if k[0] == 1 else 'Q4'}_nb{k[2]}")
 def test_f32_known_answers(kat, rows):
     # The hand-derived known answers whose inputs tell nncpu's reduction
     # order from every plausible other one: every kernel of the bit-exact
     # path (few rows, the streamed long-row kernels from 64 blocks, the
-    # 8-lane tall kernel from 16384 rows, 2-4 vectors) gives those bits.
+    # 8-lane tall kernel from 12288 rows with one or four rows per lane
+    # group, 2-4 vectors) gives those bits.
     dtype, seed, nb, want = kat
     say("kat", dtype, seed, nb, rows)
     w, x = kat_weight(dtype, seed, nb, rows)
@@ -196,12 +197,15 @@ def test_f32_batch_equals_single(oracle, dtype):
 
 
 @pytest.mark.parametrize("dtype", [1, 2])
-@pytest.mark.parametrize("rows,cols", [(16400, 96), (16390, 1056), (16384, 32), (16384, 544), (16384, 8192)])
+@pytest.mark.parametrize("rows,cols", [(16400, 96), (16390, 1056), (16384, 32), (16384, 544), (16384, 8192),
+                                       (12288, 544), (32800, 1056), (131100, 96)])
 def test_f32_tall_layout_bit_exact(oracle, dtype, rows, cols):
-    # Matrices of 16384 rows or more take the 8-lane layout; these shapes give
+    # Matrices of 12288 rows or more take the 8-lane layout; these shapes give
     # it partial groups (nb = 3, 33, 1, 17), a ragged last workgroup, strided
-    # batches, the Q4 bias tail, and (K = 8192) x too big for four tokens in
-    # LDS at once (two per launch).
+    # batches, the Q4 bias tail, (K = 8192) x too big for four tokens in LDS
+    # at once (two per launch), and both lane-group forms of several vectors:
+    # one row per lane group, and four (three or more vectors from 32768
+    # rows, two from 131072).
     say("tall", dtype, rows, cols)
     rng = oracle.Rng(0x7A11 + rows + cols + dtype)
     m = oracle.QMatrix.from_f32(dtype, rng.vec(rows * cols, -1.0, 1.0).reshape(rows, cols))
