@@ -644,45 +644,63 @@ __global__ __launch_bounds__(M1S_NT) void gemv_f32_m1s_kernel(F32Mat m, const fl
 // The streamed kernel (long rows, many of them): 32 lanes per row, lane j
 // running chain j alone (M1Wide's arithmetic on the same 16-lane layout),
 // every wave computing two rows; a workgroup takes NT / 32 consecutive rows.
-// x is staged once per workgroup, transposed (m1w_xpos: a lane's x values
-// for 4 consecutive blocks are one 16-byte LDS read), with the Q4 block sums
-// of x. Each lane streams its row's groups straight from global memory into
-// a ring of PF register slots (the quant piece and the group's BF16 scales,
-// the scale loads the same address across the row's 32 lanes), so PF
-// groups are always in flight behind the arithmetic; the staged kernel's
-// LDS copies of every row are not needed. The lane's byte (Q8) or nibble
-// (Q4) of each pair is brought to fixed positions once per group.
+// x is staged once per workgroup. Each lane streams its row's groups
+// straight from global memory into a ring of PF register slots (the quant
+// piece and the group's BF16 scales, the scale loads the same address
+// across the row's 32 lanes), so PF groups are always in flight behind the
+// arithmetic; the staged kernel's LDS copies of every row are not needed.
+// The lane's byte (Q8) or nibble (Q4) of each pair is brought to fixed
+// positions once per group.
 constexpr int M1R_MIN_ROWS = 2048;  // fills the GPU at 32 lanes per row
 
+// One group in flight: the quant piece, the group's BF16 scales and, for
+// Q4, the two biases that the lane's bias-dot lane (j mod 8) takes from the
+// group (blocks 16g + j mod 8 and 16g + 8 + j mod 8).
 template <int DT>
-struct M1rSlot {  // one group in flight
+struct M1xSlot {
     static constexpr int G = DT == 1 ? 8 : 16;
-    uint4 q;          // the lane's 16-byte piece of the group
-    uint4 s[G / 8];   // the group's BF16 scales
+    uint4 q;
+    uint4 s[G / 8];
+    uint32_t b0, b1;  // Q4 only
 };
 
-// One group of the lane's chain: blocks 0 .. nblk - 1 (all G when FULL) of
-// the slot, x from the transposed LDS copy (xg: the lane's x at the group's
-// first block). The lane's byte (Q8) / nibble (Q4) of each pair is brought
-// to fixed byte positions once per group.
+// Group g's quant piece and scales; Q4: the biases of group gb (g clamped
+// to the row's whole groups, so that those loads stay inside the row).
+template <int DT>
+__device__ __forceinline__ void m1x_load(M1xSlot<DT>& sl, const uint8_t* qrow, const uint16_t* srow,
+                                         const uint16_t* brow, int g, int gb) {
+    constexpr int G = DT == 1 ? 8 : 16;
+    sl.q = load_nt16u(qrow + (size_t)g * 256);
+#pragma unroll
+    for (int k = 0; k < G / 8; ++k) sl.s[k] = *(const uint4*)(srow + g * G + 8 * k);
+    if (DT == 2) {
+        sl.b0 = brow[16 * gb];
+        sl.b1 = brow[16 * gb + 8];
+    }
+}
+
+// One group of the lane's chain with x in its natural order in LDS (xb: x
+// at the group's first block plus the lane's element; block i's value 32
+// floats on). Q4 whole groups also take the group's two steps of the lane's
+// bias-dot accumulator (xsg: the block sums at the group's first block plus
+// j mod 8).
 template <int DT, bool FULL>
-__device__ __forceinline__ void m1r_group(const M1rSlot<DT>& sl, const float* xg, int h, int nblk, float& a) {
+__device__ __forceinline__ void m1x_group(const M1xSlot<DT>& sl, const float* xb, const float* xsg, int h, int nblk,
+                                          float& a, float& ab) {
     constexpr int G = DT == 1 ? 8 : 16;
     uint32_t qd[4] = {sl.q.x, sl.q.y, sl.q.z, sl.q.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         qd[k] = DT == 1 ? qd[k] >> (8 * h) : (qd[k] >> (4 * h)) & 0x0f0f0f0fu;
-        // Opaque to the compiler: it would fold the mask into a bit-field
-        // extract per block instead of converting the bytes directly.
         if (DT == 2) asm volatile("" : "+v"(qd[k]));
     }
     float xv[G];
 #pragma unroll
-    for (int i = 0; i < G; i += 4) {
-        if (FULL || i < nblk) {
-            const float4 v = *(const float4*)(xg + i);
-            xv[i] = v.x, xv[i + 1] = v.y, xv[i + 2] = v.z, xv[i + 3] = v.w;
-        }
+    for (int i = 0; i < G; ++i)
+        if (FULL || i < nblk) xv[i] = xb[32 * i];
+    if (DT == 2 && FULL) {
+        ab = __builtin_fmaf(bf16f(sl.b0), xsg[0], ab);
+        ab = __builtin_fmaf(bf16f(sl.b1), xsg[8], ab);
     }
 #pragma unroll
     for (int i = 0; i < G; ++i) {
@@ -698,101 +716,93 @@ __device__ __forceinline__ void m1r_group(const M1rSlot<DT>& sl, const float* xg
     }
 }
 
+// LDS of the streamed kernel: x (nb * 128 bytes, rounded up to
+// whole 1 KB copies), then the Q4 block sums of x (nb floats).
+__host__ __device__ inline size_t m1x_x_bytes(int nb) { return ((size_t)nb * 128 + 1023) & ~(size_t)1023; }
+inline size_t m1x_lds(int dt, int nb) { return m1x_x_bytes(nb) + (dt == 2 ? (size_t)nb * 4 : 0); }
+
+// x is copied to LDS as it lies in memory: every
+// wave issues its share of 1 KB direct-to-LDS copies of x before the first
+// PF groups of its row, so the staging is one round trip and holds no
+// registers. A lane reads block b's element j at 32 b + j (the 32 lanes of
+// a row read 128 contiguous bytes). Q4: the block sums of x are formed from
+// the LDS copy after the staging barrier, and the bias dot
+// (dot_bf16_f32, scalar.rs:334-347: lane j mod 8 of the accumulator over
+// whole groups of 8 blocks, hsum8, the unfused tail) runs alongside the
+// chains, its biases streamed with the weights.
 template <int DT, int NT, int M1R_PF>
-__global__ __launch_bounds__(NT) void gemv_f32_m1r_kernel(F32Mat m, const float* __restrict__ x,
+__global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float* __restrict__ x,
                                                          float* __restrict__ y) {
     constexpr int G = DT == 1 ? 8 : 16;
     constexpr int RPW = NT / 32;  // rows per workgroup
-    extern __shared__ __align__(16) float xw[];
-    const int tid = threadIdx.x, nb = m.nb, S = m1w_stride(nb);
+    constexpr int NW = NT / 64;
+    extern __shared__ __align__(1024) unsigned char m1x_smem[];
+    const int tid = threadIdx.x, nb = m.nb, wave = tid >> 6, lane = tid & 63;
     const int ngp = m1_groups(DT, nb), ng = nb / G;
-    float* xs = xw + 32 * S;
+    float* xw = (float*)m1x_smem;
+    float* xs = (float*)(m1x_smem + m1x_x_bytes(nb));
     const int row0 = blockIdx.x * RPW;
     const int rraw = row0 + (tid >> 5);
     const int row = rraw < m.rows ? rraw : m.rows - 1;
-    const int j = tid & 31, h = j >> 4;
+    const int j = tid & 31, h = j >> 4, j8 = j & 7;
 
-    // The first PF groups of the row first, so they are in flight while x
-    // is staged.
+    {
+        const size_t xl = (size_t)nb * 128;
+        for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(x, xl, c * 1024, m1x_smem + c * 1024, lane);
+    }
     const uint8_t* qrow = m.fq + (size_t)row * ngp * 256 + (j & 15) * 16;
     const uint16_t* srow = m.fs + (size_t)row * m.nbp;
-    M1rSlot<DT> slot[M1R_PF];
+    // Q4: block 16g + j8 of the row's biases; whole groups only, so the
+    // clamped prefetches past them read inside the row's first ng groups.
+    const uint16_t* brow = DT == 2 ? m.bi + (size_t)row * nb + j8 : nullptr;
+    const int ngb = ng > 0 ? ng : 1;  // bias prefetches stay in whole groups (or group 0)
+    M1xSlot<DT> slot[M1R_PF];
 #pragma unroll
     for (int d = 0; d < M1R_PF; ++d) {
         const int g = d < ngp ? d : ngp - 1;
-        slot[d].q = load_nt16u(qrow + (size_t)g * 256);
-#pragma unroll
-        for (int k = 0; k < G / 8; ++k) slot[d].s[k] = *(const uint4*)(srow + g * G + 8 * k);
+        m1x_load<DT>(slot[d], qrow, srow, brow, g, min(g, ngb - 1));
     }
-    // x in 16-byte pieces, four pieces' loads in flight per thread before
-    // their LDS stores (x is 16-byte aligned: checked by the launcher).
-    const float4* x4 = (const float4*)x;
-    const int nf = nb * 8;
-    for (int f0 = tid; f0 < nf; f0 += 4 * NT) {
-        float4 v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int f = f0 + k * NT;
-            v[k] = x4[f < nf ? f : nf - 1];
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int f = f0 + k * NT;
-            if (f < nf) {
-                const int b = f >> 3, c = 4 * (f & 7);
-                xw[m1w_xpos(b, c, S)] = v[k].x;
-                xw[m1w_xpos(b, c + 1, S)] = v[k].y;
-                xw[m1w_xpos(b, c + 2, S)] = v[k].z;
-                xw[m1w_xpos(b, c + 3, S)] = v[k].w;
-            }
-        }
-    }
-    if (DT == 2) {
-        for (int b = tid; b < nb; b += NT) {
-            float c[32];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float4 v = x4[8 * b + k];
-                c[4 * k] = v.x, c[4 * k + 1] = v.y, c[4 * k + 2] = v.z, c[4 * k + 3] = v.w;
-            }
-            xs[b] = m1_block_sum(c);
-        }
-    }
+    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
     __syncthreads();
+    if (DT == 2)
+        for (int b = tid; b < nb; b += NT) xs[b] = m1_block_sum(xw + 32 * b);
+    if (DT == 2) lds_barrier();
 
-    const float* xp = xw + j * S;
-    float a = 0.0f;
-    // Groups in order, group g in slot g % PF. Whole rounds of PF whole
-    // groups run straight-line, each slot refilled with the group PF ahead
-    // right after its arithmetic (clamped to the row's last group, so the
-    // refill needs no branch; a few repeated loads at the row's end are never
-    // used); the rest of the row follows from the slots as they are.
+    const float* xp = xw + j;
+    float a = 0.0f, ab = 0.0f;
     int g = 0;
     for (; g + M1R_PF <= ng; g += M1R_PF) {
 #pragma unroll
         for (int d = 0; d < M1R_PF; ++d) {
-            m1r_group<DT, true>(slot[d], xp + (g + d) * G, h, G, a);
+            m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
             const int gn = min(g + d + M1R_PF, ngp - 1);
-            slot[d].q = load_nt16u(qrow + (size_t)gn * 256);
-#pragma unroll
-            for (int k = 0; k < G / 8; ++k) slot[d].s[k] = *(const uint4*)(srow + gn * G + 8 * k);
+            m1x_load<DT>(slot[d], qrow, srow, brow, gn, min(gn, ngb - 1));
         }
     }
 #pragma unroll
     for (int d = 0; d < M1R_PF; ++d) {
         if (g + d < ng)
-            m1r_group<DT, true>(slot[d], xp + (g + d) * G, h, G, a);
+            m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
         else if (g + d == ng && ng < ngp)
-            m1r_group<DT, false>(slot[d], xp + (g + d) * G, h, nb - ng * G, a);
+            m1x_group<DT, false>(slot[d], xp + (g + d) * G * 32, xs, h, nb - ng * G, a, ab);
     }
-    // v[l] = (acc_l + acc_{8+l}) + (acc_{16+l} + acc_{24+l}) by xor-8, xor-16,
-    // then hsum8 by xor-4, xor-1, xor-2 (valid at lane 0 of the row).
     const float u = __fadd_rn(a, xor_get(a, 8));
     const float v = __fadd_rn(u, xor_get(u, 16));
     const float p = __fadd_rn(v, xor_get(v, 4));
     const float q = __fadd_rn(p, xor_get(p, 1));
     float res = __fadd_rn(q, xor_get(q, 2));
-    if (DT == 2) res = __fadd_rn(res, m1_bias_dot(m.bi + (size_t)row * nb, xs, nb, j));
+    if (DT == 2) {
+        // The bias dot's blocks past the whole groups: the rest of the
+        // 8-block body, hsum8, then the unfused tail.
+        const uint16_t* bfull = m.bi + (size_t)row * nb;
+        const int body = nb & ~7;
+        for (int i = G * ng + j8; i < body; i += 8) ab = __builtin_fmaf(bf16f(bfull[i]), xs[i], ab);
+        const float bp = __fadd_rn(ab, xor_get(ab, 4));
+        const float bq = __fadd_rn(bp, xor_get(bp, 1));
+        float bs = __fadd_rn(bq, xor_get(bq, 2));
+        for (int i = body; i < nb; ++i) bs = __fadd_rn(bs, __fmul_rn(bf16f(bfull[i]), xs[i]));
+        res = __fadd_rn(res, bs);
+    }
     if (rraw < m.rows && j == 0) y[rraw] = res;
 }
 
@@ -800,16 +810,16 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1r_kernel(F32Mat m, const float*
 // per row, x (staged whole in LDS) at most 64 KB and 16-byte aligned.
 // x staged whole: up to 150 KB of LDS (rows of about 37000 columns).
 constexpr size_t M1R_MAX_LDS = 150 * 1024;
-static size_t m1r_lds(int dt, int nb) { return (size_t)32 * m1w_stride_host(nb) * 4 + (dt == 2 ? (size_t)nb * 4 : 0); }
 static bool m1r_fits(int dt, int rows, int nb, const float* x) {
-    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && m1r_lds(dt, nb) <= M1R_MAX_LDS && ((uintptr_t)x & 15) == 0;
+    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && m1x_lds(dt, nb) <= M1R_MAX_LDS &&
+           ((uintptr_t)x & 15) == 0;
 }
 // The streamed kernel's instances may take more than the default 64 KB of
 // dynamic LDS (set once per instance).
 template <int DT, int NT, int PF>
-static void m1r_allow_lds() {
+static void m1x_allow_lds() {
     static const bool once = [] {
-        return hipFuncSetAttribute((const void*)gemv_f32_m1r_kernel<DT, NT, PF>,
+        return hipFuncSetAttribute((const void*)gemv_f32_m1x_kernel<DT, NT, PF>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)M1R_MAX_LDS) == hipSuccess;
     }();
     (void)once;
@@ -827,16 +837,17 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
     if (m1r_fits(DT, rows, nb, x)) {
         // Many long rows: the streamed kernel, 16 rows per workgroup (8
         // waves) when that still gives a workgroup per CU, else 8.
-        const size_t lds = m1r_lds(DT, nb);
         // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8,
-        // the fastest of 2..8 at Llama's shapes.
+        // the fastest of 2..8 at Llama's shapes (10 / 5 and 12 / 8 measured
+        // slower at Llama's and Qwen's).
         constexpr int PF = DT == 1 ? 6 : 3;
+        const size_t lds = m1x_lds(DT, nb);
         if (rows >= 16 * cu_count()) {
-            m1r_allow_lds<DT, 512, PF>();
-            gemv_f32_m1r_kernel<DT, 512, PF><<<dim3(ceil_div(rows, 16)), dim3(512), lds, st>>>(m, x, y);
+            m1x_allow_lds<DT, 512, PF>();
+            gemv_f32_m1x_kernel<DT, 512, PF><<<dim3(ceil_div(rows, 16)), dim3(512), lds, st>>>(m, x, y);
         } else {
-            m1r_allow_lds<DT, 256, PF>();
-            gemv_f32_m1r_kernel<DT, 256, PF><<<dim3(ceil_div(rows, 8)), dim3(256), lds, st>>>(m, x, y);
+            m1x_allow_lds<DT, 256, PF>();
+            gemv_f32_m1x_kernel<DT, 256, PF><<<dim3(ceil_div(rows, 8)), dim3(256), lds, st>>>(m, x, y);
         }
         return;
     }

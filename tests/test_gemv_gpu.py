@@ -136,18 +136,21 @@ def test_f32_baseline_shapes_bit_exact(oracle, dtype, rows, cols):
 @pytest.mark.parametrize("dtype", [1, 2])
 @pytest.mark.parametrize("rows,cols", [(5, 224), (3, 480), (33, 4512), (17, 8192), (17, 8224), (40, 2080),
                                        (300, 2048), (2100, 4096), (4100, 8192), (2050, 4128), (4099, 2080),
-                                       (2048, 16384), (2049, 8224), (2048, 18944), (2049, 36864)])
+                                       (2048, 16384), (2049, 8224), (2048, 18944), (2049, 36864), (2051, 2400),
+                                       (2048, 37888)])
 def test_f32_one_vector_ring_shapes(oracle, dtype, rows, cols):
     # One vector takes the one-vector kernels up to 8192 columns: rows without
     # a whole group (224 / 480 columns), every tail length class, the
     # 8192-column limit and the first width past it; from 2048 columns the
     # staged kernel with 1 to 8 rows per workgroup (ragged: 300 rows) and 1 to
     # 4 weight copies per wave; from 2048 rows the streamed kernel with 8 or
-    # 16 rows per workgroup (ragged: 2049 / 2050 / 2100 / 4099 / 4100 rows), a
-    # partial last group (4128 / 2080 columns), rows past 8192 columns (8224),
-    # x of 64 KB (16384), past it (18944: Qwen's down projection) and at the
-    # staging limit (36864: 144 KB, Q4's block sums then push it to the
-    # general kernel).
+    # 16 rows per workgroup (ragged: 2049 / 2050 / 2051 / 2100 / 4099 / 4100
+    # rows), a partial last group (4128 / 2080 columns; 2400: Q4's bias dot
+    # then has body blocks past the whole groups and a 3-block unfused tail),
+    # rows past 8192 columns (8224), x of 64 KB (16384), past it (18944:
+    # Qwen's down projection) and up to the staging limit of 150 KB (36864:
+    # x and Q4's block sums 148.5 KB; 37888: x alone 148 KB, so Q8 streams
+    # and Q4 takes the general kernel).
     say("ring", dtype, rows, cols)
     rng = oracle.Rng(0x0E1 + rows + cols + dtype)
     m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
