@@ -666,13 +666,14 @@ struct M1xSlot {
 
 // Group g's quant piece and scales; Q4: the biases of group gb (g clamped
 // to the row's whole groups, so that those loads stay inside the row).
-template <int DT>
+template <int DT, bool SL>
 __device__ __forceinline__ void m1x_load(M1xSlot<DT>& sl, const uint8_t* qrow, const uint16_t* srow,
                                          const uint16_t* brow, int g, int gb) {
     constexpr int G = DT == 1 ? 8 : 16;
     sl.q = load_nt16u(qrow + (size_t)g * 256);
+    if (!SL)
 #pragma unroll
-    for (int k = 0; k < G / 8; ++k) sl.s[k] = *(const uint4*)(srow + g * G + 8 * k);
+        for (int k = 0; k < G / 8; ++k) sl.s[k] = *(const uint4*)(srow + g * G + 8 * k);
     if (DT == 2) {
         sl.b0 = brow[16 * gb];
         sl.b1 = brow[16 * gb + 8];
@@ -717,20 +718,26 @@ __device__ __forceinline__ void m1x_group(const M1xSlot<DT>& sl, const float* xb
 }
 
 // LDS of the streamed kernel: x (nb * 128 bytes, rounded up to
-// whole 1 KB copies), then the Q4 block sums of x (nb floats).
+// whole 1 KB copies), the scale rows of the workgroup's rpw rows (rounded
+// up likewise), then the Q4 block sums of x (nb floats).
 __host__ __device__ inline size_t m1x_x_bytes(int nb) { return ((size_t)nb * 128 + 1023) & ~(size_t)1023; }
-inline size_t m1x_lds(int dt, int nb) { return m1x_x_bytes(nb) + (dt == 2 ? (size_t)nb * 4 : 0); }
+__host__ __device__ inline size_t m1x_s_bytes(int nbp, int rpw) {
+    return ((size_t)rpw * nbp * 2 + 1023) & ~(size_t)1023;
+}
+inline size_t m1x_lds(int dt, int nb, int nbp, int rpw) {
+    return m1x_x_bytes(nb) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
+}
 
-// x is copied to LDS as it lies in memory: every
-// wave issues its share of 1 KB direct-to-LDS copies of x before the first
-// PF groups of its row, so the staging is one round trip and holds no
-// registers. A lane reads block b's element j at 32 b + j (the 32 lanes of
-// a row read 128 contiguous bytes). Q4: the block sums of x are formed from
-// the LDS copy after the staging barrier, and the bias dot
-// (dot_bf16_f32, scalar.rs:334-347: lane j mod 8 of the accumulator over
-// whole groups of 8 blocks, hsum8, the unfused tail) runs alongside the
-// chains, its biases streamed with the weights.
-template <int DT, int NT, int M1R_PF>
+// x is copied to LDS as it lies in memory: every wave issues its share of
+// 1 KB direct-to-LDS copies of x (and, SL, of the workgroup's scale rows:
+// one contiguous span) before the first PF groups of its row, so the
+// staging is one round trip and holds no registers. A lane reads block b's
+// element j at 32 b + j (the 32 lanes of a row read 128 contiguous bytes).
+// Q4: the block sums of x are formed from the LDS copy after the staging
+// barrier, and the bias dot (dot_bf16_f32, scalar.rs:334-347: lane j mod 8
+// of the accumulator over whole groups of 8 blocks, hsum8, the unfused
+// tail) runs alongside the chains, its biases streamed with the weights.
+template <int DT, int NT, int M1R_PF, bool SL>
 __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float* __restrict__ x,
                                                          float* __restrict__ y) {
     constexpr int G = DT == 1 ? 8 : 16;
@@ -740,7 +747,8 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     const int tid = threadIdx.x, nb = m.nb, wave = tid >> 6, lane = tid & 63;
     const int ngp = m1_groups(DT, nb), ng = nb / G;
     float* xw = (float*)m1x_smem;
-    float* xs = (float*)(m1x_smem + m1x_x_bytes(nb));
+    const uint16_t* scl = (const uint16_t*)(m1x_smem + m1x_x_bytes(nb));
+    float* xs = (float*)(m1x_smem + m1x_x_bytes(nb) + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));
     const int row0 = blockIdx.x * RPW;
     const int rraw = row0 + (tid >> 5);
     const int row = rraw < m.rows ? rraw : m.rows - 1;
@@ -749,7 +757,15 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     {
         const size_t xl = (size_t)nb * 128;
         for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(x, xl, c * 1024, m1x_smem + c * 1024, lane);
+        if (SL) {
+            // The scale rows of the workgroup's rows: one contiguous span.
+            const size_t sl_len = (size_t)min(RPW, m.rows - row0) * m.nbp * 2;
+            const unsigned char* ssrc = (const unsigned char*)(m.fs + (size_t)row0 * m.nbp);
+            for (size_t c = wave; c * 1024 < sl_len; c += NW)
+                copy_1k(ssrc, sl_len, c * 1024, m1x_smem + m1x_x_bytes(nb) + c * 1024, lane);
+        }
     }
+    const uint4* srl = (const uint4*)(scl + (size_t)(row - row0) * m.nbp);  // the row's scales in LDS
     const uint8_t* qrow = m.fq + (size_t)row * ngp * 256 + (j & 15) * 16;
     const uint16_t* srow = m.fs + (size_t)row * m.nbp;
     // Q4: block 16g + j8 of the row's biases; whole groups only, so the
@@ -760,7 +776,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
 #pragma unroll
     for (int d = 0; d < M1R_PF; ++d) {
         const int g = d < ngp ? d : ngp - 1;
-        m1x_load<DT>(slot[d], qrow, srow, brow, g, min(g, ngb - 1));
+        m1x_load<DT, SL>(slot[d], qrow, srow, brow, g, min(g, ngb - 1));
     }
     __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
     __syncthreads();
@@ -774,13 +790,19 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     for (; g + M1R_PF <= ng; g += M1R_PF) {
 #pragma unroll
         for (int d = 0; d < M1R_PF; ++d) {
+            if (SL)
+#pragma unroll
+                for (int k = 0; k < G / 8; ++k) slot[d].s[k] = srl[(g + d) * (G / 8) + k];
             m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
             const int gn = min(g + d + M1R_PF, ngp - 1);
-            m1x_load<DT>(slot[d], qrow, srow, brow, gn, min(gn, ngb - 1));
+            m1x_load<DT, SL>(slot[d], qrow, srow, brow, gn, min(gn, ngb - 1));
         }
     }
 #pragma unroll
     for (int d = 0; d < M1R_PF; ++d) {
+        if (SL && g + d < ngp)
+#pragma unroll
+            for (int k = 0; k < G / 8; ++k) slot[d].s[k] = srl[(g + d) * (G / 8) + k];
         if (g + d < ng)
             m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
         else if (g + d == ng && ng < ngp)
@@ -810,16 +832,18 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
 // per row, x (staged whole in LDS) at most 64 KB and 16-byte aligned.
 // x staged whole: up to 150 KB of LDS (rows of about 37000 columns).
 constexpr size_t M1R_MAX_LDS = 150 * 1024;
+constexpr size_t CU_LDS_BYTES = 160 * 1024;  // LDS of one gfx950 CU
 static bool m1r_fits(int dt, int rows, int nb, const float* x) {
-    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && m1x_lds(dt, nb) <= M1R_MAX_LDS &&
+    const int nbp = dt == 1 ? (nb + 7) / 8 * 8 : (nb + 15) / 16 * 16;
+    return nb >= M1W_MIN_NB && rows >= M1R_MIN_ROWS && m1x_lds(dt, nb, nbp, 8) <= M1R_MAX_LDS &&
            ((uintptr_t)x & 15) == 0;
 }
 // The streamed kernel's instances may take more than the default 64 KB of
 // dynamic LDS (set once per instance).
-template <int DT, int NT, int PF>
+template <int DT, int NT, int PF, bool SL>
 static void m1x_allow_lds() {
     static const bool once = [] {
-        return hipFuncSetAttribute((const void*)gemv_f32_m1x_kernel<DT, NT, PF>,
+        return hipFuncSetAttribute((const void*)gemv_f32_m1x_kernel<DT, NT, PF, SL>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)M1R_MAX_LDS) == hipSuccess;
     }();
     (void)once;
@@ -840,14 +864,32 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
         // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8,
         // the fastest of 2..8 at Llama's shapes (10 / 5 and 12 / 8 measured
         // slower at Llama's and Qwen's).
+        // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8
+        // (deeper measured slower at Llama's and Qwen's shapes). The rows'
+        // scales are staged in LDS too unless that would leave fewer
+        // workgroups resident per CU than the launch needs (long rows: the
+        // copy of x alone takes half of a CU's LDS).
         constexpr int PF = DT == 1 ? 6 : 3;
-        const size_t lds = m1x_lds(DT, nb);
-        if (rows >= 16 * cu_count()) {
-            m1x_allow_lds<DT, 512, PF>();
-            gemv_f32_m1x_kernel<DT, 512, PF><<<dim3(ceil_div(rows, 16)), dim3(512), lds, st>>>(m, x, y);
+        const bool wide = rows >= 16 * cu_count() && m1x_lds(DT, nb, nbp, 16) <= M1R_MAX_LDS;
+        const int rpw = wide ? 16 : 8;
+        const int need = ceil_div(ceil_div(rows, rpw), cu_count());
+        const int fit_sl = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, rpw));
+        const int fit = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, 0));
+        const bool sl = fit_sl >= std::min(need, fit);
+        const size_t lds = m1x_lds(DT, nb, nbp, sl ? rpw : 0);
+        const dim3 grid(ceil_div(rows, rpw)), block(rpw * 32);
+        if (wide && sl) {
+            m1x_allow_lds<DT, 512, PF, true>();
+            gemv_f32_m1x_kernel<DT, 512, PF, true><<<grid, block, lds, st>>>(m, x, y);
+        } else if (wide) {
+            m1x_allow_lds<DT, 512, PF, false>();
+            gemv_f32_m1x_kernel<DT, 512, PF, false><<<grid, block, lds, st>>>(m, x, y);
+        } else if (sl) {
+            m1x_allow_lds<DT, 256, PF, true>();
+            gemv_f32_m1x_kernel<DT, 256, PF, true><<<grid, block, lds, st>>>(m, x, y);
         } else {
-            m1x_allow_lds<DT, 256, PF>();
-            gemv_f32_m1x_kernel<DT, 256, PF><<<dim3(ceil_div(rows, 8)), dim3(256), lds, st>>>(m, x, y);
+            m1x_allow_lds<DT, 256, PF, false>();
+            gemv_f32_m1x_kernel<DT, 256, PF, false><<<grid, block, lds, st>>>(m, x, y);
         }
         return;
     }
