@@ -511,7 +511,8 @@ def qwen_prefill(args, N, dtype: int, act: int, n_tok: int = 512, n_layer: int =
     return res
 
 
-def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128, n_layer: int = 28):
+def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128, n_layer: int = 28,
+                n_check: int = 16):
     """Batch-1 greedy decode of the Qwen2.5-7B shape (config 5's model) on the
     device forward: the prompt in 16-token batches, then one decode step per
     token (nngl_decode_step_dev + nngl_greedy_next_dev, captured once in a
@@ -520,7 +521,7 @@ def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128,
     beside the weight bytes a token streams and the matmul-only ceiling at
     the measured HBM read rate."""
     import torch
-    from nncpu_amd.models import DeviceForward, norm_stride, qwen25_7b_config
+    from nncpu_amd.models import DeviceForward, Model, norm_stride, qwen25_7b_config
     cfg = qwen25_7b_config(n_ctx=n_prompt + n_gen, n_layer=n_layer, wtype=2 if dtype == 2 else 1)
     d, ff, nkv, hd, vocab = cfg.n_embd, cfg.n_ff, cfg.n_kv, cfg.head_dim, cfg.n_vocab
     qkv = d + 2 * nkv * hd
@@ -534,15 +535,19 @@ def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128,
         del w
         return out
 
-    weights = []
+    layers = []
     for _ in range(n_layer):
-        weights += [weight(qkv, d), None, None, weight(d, d), weight(2 * ff, d), None, weight(d, ff)]
+        layers += [weight(d, d), weight(nkv * hd, d), weight(nkv * hd, d), weight(d, d), weight(ff, d), weight(ff, d),
+                   weight(d, ff)]
     lm_head = weight(vocab, d)
-    weights.append(lm_head)
     rng = np.random.default_rng(0xDEC0 + dtype)
     norms = (1.0 + 0.1 * rng.standard_normal(norm_stride(cfg) * n_layer + d)).astype(np.float32)
     biases = (0.02 * rng.standard_normal(n_layer * qkv)).astype(np.float32)
     prompt = rng.integers(0, vocab, n_prompt).astype(np.int32)
+    # The timed forward reads [q; k; v] and [gate; up] as one matrix each;
+    # the CPU forward that checks its tokens takes the seven matrices.
+    model = Model(cfg, layers + [lm_head], norms, biases, lm_head)
+    weights = model.fused_weights()
     wbytes = sum(w.split_bytes() for w in weights if w is not None)
     out = []
     for act in acts:
@@ -552,17 +557,25 @@ def qwen_decode(args, N, dtype: int, acts, n_prompt: int = 64, n_gen: int = 128,
         toks, secs, _, _ = fwd.generate_graph(prompt, n_gen, stream=s)
         fwd.free()
         tok_s = (n_gen - 1) / secs
+        # The first n_check tokens against the CPU forward (gemma3.cpp's
+        # restatement of forward.rs, matmuls through the same library in the
+        # same activation mode), outside the timed region.
+        t0 = time.perf_counter()
+        tc, _, _, _ = model.cpu_generate(prompt, n_check, batch=16, act=act)
+        cpu_s = time.perf_counter() - t0
         res = dict(case=f"{'Q8' if dtype == 1 else 'Q4'} Qwen2.5-7B-shaped decode, {n_layer} layers",
                    activations={N.ACT_F32: "f32 (bit-exact drop-in)", N.ACT_I8: "int8 blocks (nncpu Q8_0)",
                                 N.ACT_MXI8: "MX int8 blocks"}[act],
                    prompt=n_prompt, generated=n_gen, tok_s=round(tok_s, 1), ms_per_token=round(1e3 / tok_s, 3),
                    weight_bytes_per_token=wbytes, weights_gbs=round(wbytes * tok_s / 1e9, 1),
-                   timing="graph replays of one decode step per token, host clock around the replays")
+                   timing="graph replays of one decode step per token, host clock around the replays",
+                   tokens_identical=bool(np.array_equal(toks[:n_check], tc)), tokens_checked=n_check,
+                   check="the first tokens against the CPU forward with the library's matmuls, same mode")
         res["matmul_ceiling_tok_s"] = round(HBM_PEAK_GBS * 1e9 / wbytes, 1)
         res["frac_of_ceiling"] = round(tok_s / res["matmul_ceiling_tok_s"], 3)
-        log(f"qwen_decode: {res}")
+        log(f"qwen_decode: {res} (CPU check {cpu_s:.1f}s)")
         out.append(res)
-    for w in weights:
+    for w in weights + layers:
         if w is not None:
             w.free()
     return out
