@@ -225,6 +225,21 @@ int nnh_model_argmax_dev(const nnh_weight* w, const float* x, float* logits, voi
 int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
                        size_t n_tok, int act, void* stream);
 
+/* The residual add and RMSNorm of the reference's forward (forward.rs:
+ * 719-841, scalar.rs:232-292: v = x + r, then (v * scale) * gamma with
+ * scale = 1 / sqrt(sum_sq(v) / cols + eps) in nncpu's order and rounding)
+ * fused in front of one bit-exact f32 gemv: y = W ((v * scale) * gamma).
+ * No counterpart in the reference, whose forward runs the norm and the
+ * matmul as two calls; for a device-resident forward (one launch fewer per
+ * norm in a decode step). r may be NULL (v = x). x_out and rec (either may
+ * be NULL) receive v; neither may overlap x or r, which the call's
+ * workgroups read while one of them writes. `normed` (cols floats) is
+ * scratch the call may write the normed input to. All device pointers,
+ * asynchronous on `stream`; the same bits as the norm followed by
+ * nnh_gemv_batch_dev(..., NNH_ACT_F32). At most 16384 columns. */
+int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, const float* gamma, float eps,
+                         float* x_out, float* rec, float* normed, float* y, void* stream);
+
 /* Device-resident argmax of model_argmax (model/forward.rs:1003-1011) over
  * n logits at v (device): the first largest value, NaN never winning and a
  * NaN at index 0 keeping 0. Writes the index to *out_row (device, u64);

@@ -205,6 +205,14 @@ def gemv_batch_dev(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: i
     check(lib().nnh_gemv_batch_dev(w.handle, x_ptr, x_stride, y_ptr, y_stride, n_tok, act, stream or None))
 
 
+def gemv_rmsnorm_dev(w: Weight, x_ptr: int, r_ptr: int, gamma_ptr: int, eps: float, x_out_ptr: int, rec_ptr: int,
+                     normed_ptr: int, y_ptr: int, stream: int = 0) -> None:
+    """y = W ((v * rms(v)) * gamma), v = x + r (r_ptr 0: v = x), bit-exact f32;
+    v also to x_out / rec when non-zero (device pointers)."""
+    check(lib().nnh_gemv_rmsnorm_dev(w.handle, x_ptr, r_ptr or None, gamma_ptr, eps, x_out_ptr or None,
+                                     rec_ptr or None, normed_ptr, y_ptr, stream or None))
+
+
 def gemv_batch_dev_noalloc(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,
                            act: int = ACT_F32, stream: int = 0) -> None:
     """gemv_batch_dev with the library's fixed device scratch: allocates

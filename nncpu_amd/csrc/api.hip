@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "common.h"
+#include "f32_m1.h"
 #include "nncpu_hip.h"
 
 struct nnh_weight {
@@ -775,6 +776,34 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
     const size_t xs = n_tok > 1 ? x_stride : w->cols;
     const size_t ys = n_tok > 1 ? y_stride : w->rows;
     return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
+}
+
+int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, const float* gamma, float eps,
+                         float* x_out, float* rec, float* normed, float* y, void* stream) {
+    std::lock_guard<std::mutex> g(g_mu);
+    int rc = ensure_locked();
+    if (rc) return rc;
+    if ((rc = check_call(w, w ? w->cols : 0, w ? w->rows : 0, 1, NNH_ACT_F32))) return rc;
+    if (!x || !gamma || !normed || !y) return fail(NNH_E_INVALID, "gemv rmsnorm: null x, gamma, normed or y");
+    if (w->cols > 16384) return fail(NNH_E_INVALID, "gemv rmsnorm: more than 16384 columns");
+    const auto overlaps = [&](const float* a, const float* b) { return a && b && a < b + w->cols && b < a + w->cols; };
+    if (overlaps(x_out, x) || overlaps(x_out, r) || overlaps(rec, x) || overlaps(rec, r))
+        return fail(NNH_E_INVALID, "gemv rmsnorm: x_out / rec overlap x or r");
+    if ((rc = prepare_locked(w, layouts_for(w, NNH_ACT_F32, 1)))) return rc;
+    const hipStream_t st = (hipStream_t)stream;
+    const nnh::NormIn nrm{x, r, gamma, x_out, rec, eps};
+    if (w->dtype != NNH_BF16 &&
+        nnh::launch_gemv_f32_norm(w->dtype, w->fq, w->fs, w->bi, nrm, (int)w->rows, (int)w->nb, (int)w->nbp, y,
+                                  w->f32v2, st)) {
+        NNH_HIP(hipGetLastError());
+        return NNH_OK;
+    }
+    uint8_t* s = nullptr;
+    const size_t need = gemv_scratch_bytes(w, 1, NNH_ACT_F32);
+    if (need && (rc = scratch_locked(st, need, &s))) return rc;
+    nnh::launch_rmsnorm_vec(nrm, (int)w->cols, normed, st);
+    NNH_HIP(hipGetLastError());
+    return run_gemv(w, normed, w->cols, y, w->rows, 1, NNH_ACT_F32, s, st);
 }
 
 int nnh_gemv_batch_dev_noalloc(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,

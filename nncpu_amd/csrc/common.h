@@ -95,6 +95,14 @@ int f32_v2_parts(int rows);
 void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
                                const float* x, float* xsum, int rows, int nb, int nbp, float* y, uint64_t* part,
                                hipStream_t st);
+// One vector with the fused residual add and RMSNorm (f32_m1.h NormIn): the
+// streamed or tall kernel with the norm in its prologue; false (nothing
+// launched) when neither applies (the caller then runs launch_rmsnorm_vec,
+// at most 16384 columns, and the plain gemv).
+struct NormIn;
+bool launch_gemv_f32_norm(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
+                          const NormIn& nrm, int rows, int nb, int nbp, float* y, bool v2, hipStream_t st);
+void launch_rmsnorm_vec(const NormIn& nrm, int cols, float* out, hipStream_t st);
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,
                      size_t x_stride, float* xsum, int rows, int nb, int nbp, int n_tok, float* y,
                      size_t y_stride, bool v2, hipStream_t st);

@@ -49,6 +49,7 @@
 
 #include "common.h"
 #include "f32_m1.h"
+#include "rmsnorm_exact.h"
 
 namespace nnh {
 namespace {
@@ -724,8 +725,44 @@ __host__ __device__ inline size_t m1x_x_bytes(int nb) { return ((size_t)nb * 128
 __host__ __device__ inline size_t m1x_s_bytes(int nbp, int rpw) {
     return ((size_t)rpw * nbp * 2 + 1023) & ~(size_t)1023;
 }
-inline size_t m1x_lds(int dt, int nb, int nbp, int rpw) {
-    return m1x_x_bytes(nb) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
+inline size_t m1x_lds(int dt, int nb, int nbp, int rpw, bool norm = false) {
+    return m1x_x_bytes(nb) * (norm ? 3 : 1) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
+}
+
+// The fused residual add and RMSNorm (NormIn) on a vector of `cols` floats
+// staged in LDS at v, with r and gamma staged at rw and gw (r's copy unused
+// when n.r is NULL); NT threads. Afterwards v holds the gemv's input. The
+// operations and their order are the device forward's resid_norm_kernel's
+// (forward.rs:719-841: the add, sum_sq, the scale, (v * scale) * gamma).
+template <int NT, int B>
+__device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, const float* rw, const float* gw, int cols,
+                                              float* sc_lds) {
+    const int tid = threadIdx.x;
+    for (int i = 4 * tid; i < cols; i += 4 * NT) {
+        float4 a = *(const float4*)(v + i);
+        if (n.r) {
+            const float4 b = *(const float4*)(rw + i);
+            a = float4{__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w)};
+            *(float4*)(v + i) = a;
+        }
+        if (blockIdx.x == 0) {
+            if (n.x_out) *(float4*)(n.x_out + i) = a;
+            if (n.rec) *(float4*)(n.rec + i) = a;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const double ss = rms_sumsq<B>(v, cols, tid);
+        if (tid == 0) *sc_lds = rms_scale(ss, cols, n.eps);
+    }
+    __syncthreads();
+    const float sc = *sc_lds;
+    for (int i = 4 * tid; i < cols; i += 4 * NT) {
+        const float4 a = *(const float4*)(v + i), g = *(const float4*)(gw + i);
+        *(float4*)(v + i) = float4{__fmul_rn(__fmul_rn(a.x, sc), g.x), __fmul_rn(__fmul_rn(a.y, sc), g.y),
+                                   __fmul_rn(__fmul_rn(a.z, sc), g.z), __fmul_rn(__fmul_rn(a.w, sc), g.w)};
+    }
+    __syncthreads();
 }
 
 // x is copied to LDS as it lies in memory: every wave issues its share of
@@ -737,18 +774,20 @@ inline size_t m1x_lds(int dt, int nb, int nbp, int rpw) {
 // barrier, and the bias dot (dot_bf16_f32, scalar.rs:334-347: lane j mod 8
 // of the accumulator over whole groups of 8 blocks, hsum8, the unfused
 // tail) runs alongside the chains, its biases streamed with the weights.
-template <int DT, int NT, int M1R_PF, bool SL>
+template <int DT, int NT, int M1R_PF, bool SL, bool NORM>
 __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float* __restrict__ x,
-                                                         float* __restrict__ y) {
+                                                         float* __restrict__ y, NormIn nrm) {
     constexpr int G = DT == 1 ? 8 : 16;
     constexpr int RPW = NT / 32;  // rows per workgroup
     constexpr int NW = NT / 64;
     extern __shared__ __align__(1024) unsigned char m1x_smem[];
+    __shared__ float nsc;  // the norm's scale (NORM)
     const int tid = threadIdx.x, nb = m.nb, wave = tid >> 6, lane = tid & 63;
     const int ngp = m1_groups(DT, nb), ng = nb / G;
+    const size_t XB = m1x_x_bytes(nb), XR = NORM ? 3 * XB : XB;  // x (NORM: then r and gamma)
     float* xw = (float*)m1x_smem;
-    const uint16_t* scl = (const uint16_t*)(m1x_smem + m1x_x_bytes(nb));
-    float* xs = (float*)(m1x_smem + m1x_x_bytes(nb) + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));
+    const uint16_t* scl = (const uint16_t*)(m1x_smem + XR);
+    float* xs = (float*)(m1x_smem + XR + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));
     const int row0 = blockIdx.x * RPW;
     const int rraw = row0 + (tid >> 5);
     const int row = rraw < m.rows ? rraw : m.rows - 1;
@@ -756,13 +795,20 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
 
     {
         const size_t xl = (size_t)nb * 128;
-        for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(x, xl, c * 1024, m1x_smem + c * 1024, lane);
+        const float* src = NORM ? nrm.x : x;
+        for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(src, xl, c * 1024, m1x_smem + c * 1024, lane);
+        if (NORM) {
+            if (nrm.r)
+                for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(nrm.r, xl, c * 1024, m1x_smem + XB + c * 1024, lane);
+            for (size_t c = wave; c * 1024 < xl; c += NW)
+                copy_1k(nrm.gamma, xl, c * 1024, m1x_smem + 2 * XB + c * 1024, lane);
+        }
         if (SL) {
             // The scale rows of the workgroup's rows: one contiguous span.
             const size_t sl_len = (size_t)min(RPW, m.rows - row0) * m.nbp * 2;
             const unsigned char* ssrc = (const unsigned char*)(m.fs + (size_t)row0 * m.nbp);
             for (size_t c = wave; c * 1024 < sl_len; c += NW)
-                copy_1k(ssrc, sl_len, c * 1024, m1x_smem + m1x_x_bytes(nb) + c * 1024, lane);
+                copy_1k(ssrc, sl_len, c * 1024, m1x_smem + XR + c * 1024, lane);
         }
     }
     const uint4* srl = (const uint4*)(scl + (size_t)(row - row0) * m.nbp);  // the row's scales in LDS
@@ -780,6 +826,9 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     }
     __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
     __syncthreads();
+    if (NORM)
+        norm_prologue<NT, 32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
+                              &nsc);
     if (DT == 2)
         for (int b = tid; b < nb; b += NT) xs[b] = m1_block_sum(xw + 32 * b);
     if (DT == 2) lds_barrier();
@@ -840,13 +889,47 @@ static bool m1r_fits(int dt, int rows, int nb, const float* x) {
 }
 // The streamed kernel's instances may take more than the default 64 KB of
 // dynamic LDS (set once per instance).
-template <int DT, int NT, int PF, bool SL>
+template <int DT, int NT, int PF, bool SL, bool NORM>
 static void m1x_allow_lds() {
     static const bool once = [] {
-        return hipFuncSetAttribute((const void*)gemv_f32_m1x_kernel<DT, NT, PF, SL>,
+        return hipFuncSetAttribute((const void*)gemv_f32_m1x_kernel<DT, NT, PF, SL, NORM>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)M1R_MAX_LDS) == hipSuccess;
     }();
     (void)once;
+}
+
+// The streamed kernel: 16 rows per workgroup (8 waves) when that still
+// gives a workgroup per CU, else 8. Prefetch depth: 3 groups (48 blocks)
+// for Q4, 6 (48 blocks) for Q8 (deeper measured slower at Llama's and
+// Qwen's shapes). The rows' scales are staged in LDS too unless that would
+// leave fewer workgroups resident per CU than the launch needs (long rows:
+// the copy of x alone takes half of a CU's LDS). NORM: the fused residual
+// add and RMSNorm first (x unused; its input is nrm's).
+template <int DT, bool NORM>
+void launch_m1x(const F32Mat& m, const float* x, float* y, const NormIn& nrm, hipStream_t st) {
+    constexpr int PF = DT == 1 ? 6 : 3;
+    const int rows = m.rows, nb = m.nb, nbp = m.nbp;
+    const bool wide = rows >= 16 * cu_count() && m1x_lds(DT, nb, nbp, 16, NORM) <= M1R_MAX_LDS;
+    const int rpw = wide ? 16 : 8;
+    const int need = ceil_div(ceil_div(rows, rpw), cu_count());
+    const int fit_sl = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, rpw, NORM));
+    const int fit = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, 0, NORM));
+    const bool sl = fit_sl >= std::min(need, fit);
+    const size_t lds = m1x_lds(DT, nb, nbp, sl ? rpw : 0, NORM);
+    const dim3 grid(ceil_div(rows, rpw)), block(rpw * 32);
+    if (wide && sl) {
+        m1x_allow_lds<DT, 512, PF, true, NORM>();
+        gemv_f32_m1x_kernel<DT, 512, PF, true, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    } else if (wide) {
+        m1x_allow_lds<DT, 512, PF, false, NORM>();
+        gemv_f32_m1x_kernel<DT, 512, PF, false, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    } else if (sl) {
+        m1x_allow_lds<DT, 256, PF, true, NORM>();
+        gemv_f32_m1x_kernel<DT, 256, PF, true, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    } else {
+        m1x_allow_lds<DT, 256, PF, false, NORM>();
+        gemv_f32_m1x_kernel<DT, 256, PF, false, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    }
 }
 
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
@@ -859,38 +942,7 @@ void launch_m1(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const 
     const size_t q4 = DT == 2 ? (size_t)nb * 4 : 0;
     const dim3 block(256);
     if (m1r_fits(DT, rows, nb, x)) {
-        // Many long rows: the streamed kernel, 16 rows per workgroup (8
-        // waves) when that still gives a workgroup per CU, else 8.
-        // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8,
-        // the fastest of 2..8 at Llama's shapes (10 / 5 and 12 / 8 measured
-        // slower at Llama's and Qwen's).
-        // Prefetch depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8
-        // (deeper measured slower at Llama's and Qwen's shapes). The rows'
-        // scales are staged in LDS too unless that would leave fewer
-        // workgroups resident per CU than the launch needs (long rows: the
-        // copy of x alone takes half of a CU's LDS).
-        constexpr int PF = DT == 1 ? 6 : 3;
-        const bool wide = rows >= 16 * cu_count() && m1x_lds(DT, nb, nbp, 16) <= M1R_MAX_LDS;
-        const int rpw = wide ? 16 : 8;
-        const int need = ceil_div(ceil_div(rows, rpw), cu_count());
-        const int fit_sl = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, rpw));
-        const int fit = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, 0));
-        const bool sl = fit_sl >= std::min(need, fit);
-        const size_t lds = m1x_lds(DT, nb, nbp, sl ? rpw : 0);
-        const dim3 grid(ceil_div(rows, rpw)), block(rpw * 32);
-        if (wide && sl) {
-            m1x_allow_lds<DT, 512, PF, true>();
-            gemv_f32_m1x_kernel<DT, 512, PF, true><<<grid, block, lds, st>>>(m, x, y);
-        } else if (wide) {
-            m1x_allow_lds<DT, 512, PF, false>();
-            gemv_f32_m1x_kernel<DT, 512, PF, false><<<grid, block, lds, st>>>(m, x, y);
-        } else if (sl) {
-            m1x_allow_lds<DT, 256, PF, true>();
-            gemv_f32_m1x_kernel<DT, 256, PF, true><<<grid, block, lds, st>>>(m, x, y);
-        } else {
-            m1x_allow_lds<DT, 256, PF, false>();
-            gemv_f32_m1x_kernel<DT, 256, PF, false><<<grid, block, lds, st>>>(m, x, y);
-        }
+        launch_m1x<DT, false>(m, x, y, NormIn{}, st);
         return;
     }
     if (nb >= M1W_MIN_NB) {
@@ -1048,14 +1100,15 @@ __device__ __forceinline__ void v2_group(float (&acc)[R][M][4], const V2Group<DT
 // more waves to a shorter matrix). PF groups of weights are in flight per
 // lane: group g in slot g % PF, each slot refilled with the group PF ahead
 // right after its arithmetic.
-template <int DT, int M, int R, int PF>
+template <int DT, int M, int R, int PF, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restrict__ fq,
                                                           const uint16_t* __restrict__ fs,
                                                           const uint16_t* __restrict__ biases,
                                                           const float* __restrict__ x, size_t x_stride,
                                                           const float* __restrict__ xsum, int rows, int nb, int nbp,
                                                           float* __restrict__ y, size_t y_stride,
-                                                          uint64_t* __restrict__ part) {
+                                                          uint64_t* __restrict__ part, NormIn nrm) {
+    static_assert(!NORM || M == 1, "the fused norm takes one vector");
     constexpr int G = DT == 1 ? 4 : 8;
     const int j = threadIdx.x & 7, lg = threadIdx.x >> 3;
     const int ng = (nb + G - 1) / G;
@@ -1087,12 +1140,42 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
     V2Group<DT, R> slot[PF];
 #pragma unroll
     for (int d = 0; d < (PF == 2 ? 1 : PF); ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
-    extern __shared__ float xl[];  // [M][cols]
+    extern __shared__ __align__(16) float xl[];  // [M][cols] (NORM: then gamma), 16-byte aligned for float4
     const int cols = nb * 32;
-    for (int m = 0; m < M; ++m)
-        for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256)
-            *(float4*)(xl + m * cols + i) = __builtin_bit_cast(float4, *(const f4u*)(x + (size_t)m * x_stride + i));
-    __syncthreads();
+    if constexpr (NORM) {
+        // x (+ r) and gamma staged; norm_prologue then forms the gemv's input.
+        __shared__ float nsc;
+        float* gl = xl + cols;
+        for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256) {
+            *(float4*)(xl + i) = __builtin_bit_cast(float4, *(const f4u*)(nrm.x + i));
+            *(float4*)(gl + i) = __builtin_bit_cast(float4, *(const f4u*)(nrm.gamma + i));
+        }
+        if (nrm.r) {
+            // r added in place by each thread on its own pieces, before the barrier.
+            for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256) {
+                const float4 b = __builtin_bit_cast(float4, *(const f4u*)(nrm.r + i));
+                float4 a = *(float4*)(xl + i);
+                a = float4{__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w)};
+                *(float4*)(xl + i) = a;
+            }
+        }
+        __syncthreads();
+        NormIn n2 = nrm;
+        n2.r = nullptr;  // already added
+        norm_prologue<256, 16>(n2, xl, nullptr, gl, cols, &nsc);
+        if (DT == 2) {
+            // Q4: the block sums of the normed input (scalar.rs:355-359), in
+            // gamma's place, for the bias dot.
+            for (int b = threadIdx.x; b < nb; b += 256) gl[b] = m1_block_sum(xl + 32 * b);
+            __syncthreads();
+        }
+    } else {
+        for (int m = 0; m < M; ++m)
+            for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256)
+                *(float4*)(xl + m * cols + i) =
+                    __builtin_bit_cast(float4, *(const f4u*)(x + (size_t)m * x_stride + i));
+        __syncthreads();
+    }
 
     if constexpr (PF == 2) {
         // Two slots: the next group's loads are issued before this group's
@@ -1135,7 +1218,7 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
             const int body = nb & ~7;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float* xs = xsum + (size_t)m * nb;
+                const float* xs = NORM ? xl + cols : xsum + (size_t)m * nb;
                 float a = 0.0f;
                 for (int i = j; i < body; i += 8) a = __builtin_fmaf(bf16f(brow[i]), xs[i], a);
                 float p = __fadd_rn(a, xor_get(a, 4));
@@ -1191,7 +1274,24 @@ void launch_v2_rp(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, con
                   const float* xsum, int rows, int nb, int nbp, float* y, size_t ys, uint64_t* part, hipStream_t st) {
     const dim3 grid(ceil_div(rows, 32 * R)), block(256);
     const size_t lds = (size_t)M * nb * 32 * sizeof(float);
-    gemv_f32_v2_kernel<DT, M, R, PF><<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part);
+    gemv_f32_v2_kernel<DT, M, R, PF>
+        <<<grid, block, lds, st>>>(fq, fs, bi, x, xs, xsum, rows, nb, nbp, y, ys, part, NormIn{});
+}
+
+// One vector with the fused residual add and RMSNorm (x, r and gamma: 16-byte
+// aligned, x of at most 64 KB: twice that in LDS).
+template <int DT>
+void launch_v2_norm(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, const NormIn& nrm, int rows, int nb,
+                    int nbp, float* y, hipStream_t st) {
+    static const bool once = [] {
+        return hipFuncSetAttribute((const void*)gemv_f32_v2_kernel<DT, 1, 1, 4, true>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * F32_V2_MAX_LDS) == hipSuccess;
+    }();
+    (void)once;
+    const dim3 grid(ceil_div(rows, 32)), block(256);
+    const size_t lds = 2 * (size_t)nb * 32 * sizeof(float);
+    gemv_f32_v2_kernel<DT, 1, 1, 4, true>
+        <<<grid, block, lds, st>>>(fq, fs, bi, nullptr, 0, nullptr, rows, nb, nbp, y, rows, nullptr, nrm);
 }
 
 // Rows per lane group: one vector takes one (the most waves; measured
@@ -1279,6 +1379,62 @@ void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs,
         launch_v2_m<1, 1>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y, rows, part, st);
     else
         launch_v2_m<2, 1>(fq, fs, biases, x, (size_t)nb * 32, xsum, rows, nb, nbp, y, rows, part, st);
+}
+
+// The fused residual add and RMSNorm alone (when no fused gemv applies):
+// one workgroup, v in LDS (cols floats), the normed input to `out`.
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormIn n, int cols, float* __restrict__ out) {
+    extern __shared__ float v[];
+    __shared__ float sc;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < cols; i += 256) {
+        float a = n.x[i];
+        if (n.r) a = __fadd_rn(a, n.r[i]);
+        v[i] = a;
+        if (n.x_out) n.x_out[i] = a;
+        if (n.rec) n.rec[i] = a;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const double ss = rms_sumsq(v, cols, tid);
+        if (tid == 0) sc = rms_scale(ss, cols, n.eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < cols; i += 256) out[i] = __fmul_rn(__fmul_rn(v[i], sc), n.gamma[i]);
+}
+
+bool launch_gemv_f32_norm(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
+                          const NormIn& nrm, int rows, int nb, int nbp, float* y, bool v2, hipStream_t st) {
+    const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    const bool aligned = a16(nrm.x) && a16(nrm.gamma) && (!nrm.r || a16(nrm.r)) && (!nrm.x_out || a16(nrm.x_out)) &&
+                         (!nrm.rec || a16(nrm.rec));
+    if (!aligned) return false;
+    if (v2) {
+        if ((size_t)nb * 32 * 4 > (size_t)F32_V2_MAX_LDS) return false;
+        if (dtype == 1)
+            launch_v2_norm<1>(fq, fs, biases, nrm, rows, nb, nbp, y, st);
+        else
+            launch_v2_norm<2>(fq, fs, biases, nrm, rows, nb, nbp, y, st);
+        return true;
+    }
+    if (!m1r_fits(dtype, rows, nb, nrm.x)) return false;
+    const int nbpq = dtype == 1 ? (nb + 7) / 8 * 8 : (nb + 15) / 16 * 16;
+    if (m1x_lds(dtype, nb, nbpq, 8, true) > M1R_MAX_LDS) return false;
+    const F32Mat m{fq, fs, biases, rows, nb, nbp};
+    if (dtype == 1)
+        launch_m1x<1, true>(m, nullptr, y, nrm, st);
+    else
+        launch_m1x<2, true>(m, nullptr, y, nrm, st);
+    return true;
+}
+
+void launch_rmsnorm_vec(const NormIn& nrm, int cols, float* out, hipStream_t st) {
+    static const bool once = [] {
+        return hipFuncSetAttribute((const void*)rmsnorm_vec_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)(64 * 1024)) == hipSuccess;
+    }();
+    (void)once;
+    rmsnorm_vec_kernel<<<1, 256, (size_t)cols * 4, st>>>(nrm, cols, out);
 }
 
 void launch_gemv_f32(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases, const float* x,

@@ -46,6 +46,7 @@
 #include "nncpu_hip.h"
 #include "ops_dev.h"
 #include "q8_act.h"
+#include "rmsnorm_exact.h"
 
 namespace {
 
@@ -65,51 +66,9 @@ __device__ __forceinline__ float hsum8(const float* a) {
                      __fadd_rn(__fadd_rn(a[2], a[6]), __fadd_rn(a[3], a[7])));
 }
 
-// sum_sq (scalar.rs:232-250) of v[0..dim) (LDS), run by one wave: lanes
-// 0..7 each run FMA lane l over the whole 8-chunks in order, hsum8, then
-// the tail in f64. The result (a double) is returned to every lane.
-__device__ __forceinline__ double row_sumsq(const float* v, int dim, int lane) {
-    const int body = dim & ~7;
-    float a = 0.0f;
-    if (lane < 8) {
-        // The lane's values 32 at a time, each batch read while the previous
-        // batch's FMAs run (the chain itself is sequential); two named
-        // buffers in turn, so no register array is indexed at run time.
-        constexpr int B = 32;
-        int i = lane;
-        float ta[B], tb[B];
-        auto full = [&](int at) { return at + 8 * (B - 1) < body; };
-        if (full(i)) {
-#pragma unroll
-            for (int k = 0; k < B; ++k) ta[k] = v[i + 8 * k];
-            while (true) {
-                const bool nb = full(i + 8 * B);
-                if (nb) {
-#pragma unroll
-                    for (int k = 0; k < B; ++k) tb[k] = v[i + 8 * B + 8 * k];
-                }
-#pragma unroll
-                for (int k = 0; k < B; ++k) a = __fmaf_rn(ta[k], ta[k], a);
-                i += 8 * B;
-                if (!nb) break;
-                const bool na = full(i + 8 * B);
-                if (na) {
-#pragma unroll
-                    for (int k = 0; k < B; ++k) ta[k] = v[i + 8 * B + 8 * k];
-                }
-#pragma unroll
-                for (int k = 0; k < B; ++k) a = __fmaf_rn(tb[k], tb[k], a);
-                i += 8 * B;
-                if (!na) break;
-            }
-        }
-        for (; i < body; i += 8) a = __fmaf_rn(v[i], v[i], a);
-    }
-    const float h = hsum8_lanes(a);
-    double s = dim >= 8 ? (double)__shfl(h, 0, 64) : 0.0;
-    for (int i = body; i < dim; ++i) s = __dadd_rn(s, __dmul_rn((double)v[i], (double)v[i]));
-    return s;
-}
+// sum_sq (scalar.rs:232-250) of v[0..dim) (LDS), run by one wave
+// (rmsnorm_exact.h); the result is returned to every lane.
+__device__ __forceinline__ double row_sumsq(const float* v, int dim, int lane) { return nnh::rms_sumsq(v, dim, lane); }
 
 // A matmul's one-row input written by the kernel that produces it, in the
 // library's int8 activation layout (nnh_act_layout_ex, NNH_ACT_I8, one row):
@@ -1073,6 +1032,8 @@ struct nngl_model {
     uint8_t *qa_e = nullptr, *qa_a = nullptr, *qa_f = nullptr;
     size_t qo_e[2] = {}, qo_a[2] = {}, qo_f[2] = {};
     bool qfuse = true;    // nngl_set_fused_quant
+    bool nfuse = true;    // nngl_set_fused_norm
+    float* x2 = nullptr;  // the residual stream's second buffer (fused norms)
     bool q_last = false;  // the last forward left the lm_head input in qa_e
     std::string err;
 };
@@ -1083,7 +1044,7 @@ void nngl_free(nngl_model* m) {
     if (!m) return;
     void* bufs[] = {m->norms, m->bias, m->cs,    m->sn,     m->expt,   m->kc,     m->vc,   m->x,   m->normed,
                     m->r,     m->qkv,  m->attn, m->gu,     m->parts,  m->states, m->logits, m->tok, m->work, m->row,
-                    m->qa_e,  m->qa_a, m->qa_f};
+                    m->qa_e,  m->qa_a, m->qa_f, m->x2};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->tok_host) (void)hipHostFree(m->tok_host);
@@ -1236,6 +1197,7 @@ int nngl_create(const nng_config* cfg, const float* norms, const float* biases, 
     NNGL_CHECK(hipMemset(m->vc, 0, cache));
     const size_t nb = n_batch;
     NNGL_CHECK(hipMalloc(&m->x, nb * E * 4));
+    NNGL_CHECK(hipMalloc(&m->x2, (size_t)E * 4));
     NNGL_CHECK(hipMalloc(&m->normed, nb * E * 4));
     NNGL_CHECK(hipMalloc(&m->r, nb * E * 4));
     NNGL_CHECK(hipMalloc(&m->qkv, nb * QKV * 4));
@@ -1335,8 +1297,15 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
     uint8_t *qe = fq ? m->qa_e : nullptr, *qt = fq ? m->qa_a : nullptr, *qf = fq ? m->qa_f : nullptr;
     const QOut oe = qout(qe, m->qo_e), oa = qout(qt, m->qo_a), of = qout(qf, m->qo_f);
     m->q_last = false;
+    // One token in NNH_ACT_F32 with the fused matrices (Llama / Qwen: no
+    // post-norms): each residual add and RMSNorm runs in the prologue of the
+    // q / k / v or gate / up matmul (nnh_gemv_rmsnorm_dev), which writes the
+    // new residual stream to the other of two buffers; the last layer's
+    // final norm stays a kernel of its own.
+    const bool fn = m->nfuse && n == 1 && m->act == NNH_ACT_F32 && !gemma && m->fused_qkv && m->fused_gu;
+    float *xc = m->x, *xo = m->x2;  // the residual stream and the other buffer
     embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
-    launch_resid_norm(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E, c.rms_eps, oe, st);
+    if (!fn) launch_resid_norm(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E, c.rms_eps, oe, st);
     NNGL_CHECK(hipGetLastError());
     // One merged output per thread: G * head_dim threads (a multiple of 32)
     // up to 1024, else 1024 threads looping.
@@ -1349,7 +1318,19 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
                     *ffn_norm = nr + 2 * E + 2 * hd, *post_ffw = nr + 3 * E + 2 * hd;
         const bool sliding = c.swa_period > 0 && (li + 1) % c.swa_period != 0;  // load.rs:1156-1160
         nnh_weight* const* W = m->w.data() + 7 * li;
-        if (m->fused_qkv) {
+        if (fn) {
+            // Layer 0 normalises the embedding row; a later layer first adds
+            // the previous layer's FFN output and records that state.
+            const int rc = li == 0 ? nnh_gemv_rmsnorm_dev(W[0], xc, nullptr, nr, c.rms_eps, nullptr, nullptr,
+                                                           m->normed, m->qkv, st)
+                                   : nnh_gemv_rmsnorm_dev(W[0], xc, m->r, nr, c.rms_eps, xo,
+                                                           m->states + (size_t)(li - 1) * E, m->normed, m->qkv, st);
+            if (rc != NNH_OK) {
+                m->err = std::string("gemv rmsnorm: ") + nnh_last_error();
+                return 1;
+            }
+            if (li > 0) std::swap(xc, xo);
+        } else if (m->fused_qkv) {
             if (gemv_q(m, W[0], qe, m->normed, E, m->qkv, QKV, n_tok)) return 1;
         } else if (gemv_q(m, W[0], qe, m->normed, E, m->qkv, QKV, n_tok) ||
                    gemv_q(m, W[1], qe, m->normed, E, m->qkv + QD, QKV, n_tok) ||
@@ -1404,21 +1385,32 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
         if (!direct) attn_merge_kernel<<<dim3(KV, n), merge_threads, 0, st>>>(aa, oa);
         NNGL_CHECK(hipGetLastError());
         if (gemv_q(m, W[3], qt, m->attn, QD, m->r, E, n_tok)) return 1;
-        launch_resid_norm(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed, nullptr, n, E, c.rms_eps, oe,
-                          st);
-        if (m->fused_gu) {
-            if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok)) return 1;
-        } else if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok) ||
-                   gemv_q(m, W[5], qe, m->normed, E, m->gu + F, 2 * F, n_tok)) {
-            return 1;
+        if (fn) {
+            if (nnh_gemv_rmsnorm_dev(W[4], xc, m->r, ffn_norm, c.rms_eps, xo, nullptr, m->normed, m->gu, st) !=
+                NNH_OK) {
+                m->err = std::string("gemv rmsnorm: ") + nnh_last_error();
+                return 1;
+            }
+            std::swap(xc, xo);
+        } else {
+            launch_resid_norm(m->x, m->r, gemma ? post_attn : nullptr, ffn_norm, m->normed, nullptr, n, E, c.rms_eps,
+                              oe, st);
+            if (m->fused_gu) {
+                if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok)) return 1;
+            } else if (gemv_q(m, W[4], qe, m->normed, E, m->gu, 2 * F, n_tok) ||
+                       gemv_q(m, W[5], qe, m->normed, E, m->gu + F, 2 * F, n_tok)) {
+                return 1;
+            }
         }
         act_kernel<<<dim3((F + 1023) / 1024, n), 256, 0, st>>>(m->gu, F, gemma ? 1 : 0, of);
         NNGL_CHECK(hipGetLastError());
         if (gemv_q(m, W[6], qf, m->gu, 2 * F, m->r, E, n_tok)) return 1;
         const bool last = li + 1 == c.n_layer;
         const float* next = last ? m->norms + ns * c.n_layer : m->norms + ns * (li + 1);
-        launch_resid_norm(m->x, m->r, gemma ? post_ffw : nullptr, next, last ? m->x : m->normed,
-                          m->states + (size_t)li * E, n, E, c.rms_eps, oe, st);
+        // Fused: the next layer's q / k / v matmul runs this norm.
+        if (!fn || last)
+            launch_resid_norm(xc, m->r, gemma ? post_ffw : nullptr, next, last ? m->x : m->normed,
+                              m->states + (size_t)li * E, n, E, c.rms_eps, oe, st);
         NNGL_CHECK(hipGetLastError());
     }
     m->q_last = fq;
@@ -1545,6 +1537,15 @@ size_t nngl_pos(nngl_model* m) { return m->pos; }
 // 0: every matmul quantizes its f32 input itself.
 int nngl_set_fused_quant(nngl_model* m, int on) {
     m->qfuse = on != 0;
+    return 0;
+}
+
+// on != 0 (the default): one-token forwards in NNH_ACT_F32 with fused
+// q / k / v and gate / up matrices run each residual add and RMSNorm inside
+// the next matmul's prologue (nnh_gemv_rmsnorm_dev: the same bits, one
+// launch fewer per norm); 0: the norm kernel, then the matmul.
+int nngl_set_fused_norm(nngl_model* m, int on) {
+    m->nfuse = on != 0;
     return 0;
 }
 

@@ -12,6 +12,8 @@
 #include <cstdint>
 #include <cstring>
 
+#include "rmsnorm_exact.h"
+
 namespace {
 
 __device__ __forceinline__ float bf16f(uint32_t v) { return __uint_as_float(v << 16); }
@@ -59,10 +61,7 @@ __device__ __forceinline__ float sigmoid_lane(float g) {
 
 // (float)(1 / sqrt(ss / dim + eps)) in f64 (scalar.rs:232-292, gemma3.cpp
 // rmsnorm_gamma_multi), ss the sum of squares as a double.
-__device__ __forceinline__ float rms_of_d(double ss, int dim, float eps) {
-    const float inv_dim = __fdiv_rn(1.0f, (float)dim);
-    return (float)__ddiv_rn(1.0, __dsqrt_rn(__dadd_rn(__dmul_rn(ss, (double)inv_dim), (double)eps)));
-}
+__device__ __forceinline__ float rms_of_d(double ss, int dim, float eps) { return nnh::rms_scale(ss, dim, eps); }
 __device__ __forceinline__ float rms_of(float ss, int dim, float eps) { return rms_of_d((double)ss, dim, eps); }
 
 }  // namespace

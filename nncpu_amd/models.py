@@ -83,6 +83,7 @@ def _lib():
     L.nngl_decode_step_dev.argtypes, L.nngl_decode_step_dev.restype = [vp, vp, vp], i32
     L.nngl_greedy_next_dev.argtypes, L.nngl_greedy_next_dev.restype = [vp, vp, vp, vp, vp], i32
     L.nngl_set_fused_quant.argtypes, L.nngl_set_fused_quant.restype = [vp, i32], i32
+    L.nngl_set_fused_norm.argtypes, L.nngl_set_fused_norm.restype = [vp, i32], i32
     return L
 
 
@@ -263,6 +264,12 @@ class DeviceForward:
         """One-token int8 forwards: the kernels producing each matmul input
         write it quantized (default, same bits), or the matmuls quantize."""
         self._check(self._lib.nngl_set_fused_quant(self._h, int(bool(on))))
+
+    def set_fused_norm(self, on: bool) -> None:
+        """One-token f32 forwards with fused matrices: the residual add and
+        RMSNorm in the next matmul's prologue (the default) or as a kernel of
+        their own (False); the same bits either way."""
+        self._check(self._lib.nngl_set_fused_norm(self._h, int(bool(on))))
 
     def set_pos(self, pos: int) -> None:
         self._check(self._lib.nngl_set_pos(self._h, pos))

@@ -181,6 +181,77 @@ def test_f32_one_vector_unaligned_x(oracle, dtype, rows, cols):
         assert np.array_equal(bits(yd.cpu().numpy()), want), off
 
 
+def rmsnorm_ref(x, r, gamma, eps):
+    """nncpu's residual add and RMSNorm restated independently (exact-rounding
+    arithmetic of f32_exact.py): v = x + r; sum_sq (scalar.rs:232-250) with
+    eight FMA lanes over the whole 8-chunks, hsum8, the tail in f64; the scale
+    (float)(1 / sqrt(ss * (1 / dim) + eps)) in f64; (v * scale) * gamma."""
+    import math
+
+    from f32_exact import fma32, hsum8
+    v = x if r is None else (x + r).astype(np.float32)
+    dim = v.size
+    body = dim & ~7
+    acc = [0.0] * 8
+    for i in range(body):
+        acc[i % 8] = fma32(float(v[i]), float(v[i]), acc[i % 8])
+    ss = float(hsum8(acc)) if dim >= 8 else 0.0
+    for i in range(body, dim):
+        ss = ss + float(v[i]) * float(v[i])
+    inv_dim = float(np.float32(1.0) / np.float32(dim))
+    scale = np.float32(1.0 / math.sqrt(ss * inv_dim + float(np.float32(eps))))
+    return v, ((v * scale).astype(np.float32) * gamma).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(1, 4608, 3584), (2, 4608, 3584), (1, 2048, 3584), (2, 2050, 4128),
+                                             (1, 16384, 3584), (2, 16384, 3584), (2, 12300, 1024), (1, 256, 1152),
+                                             (2, 3000, 1056), (3, 512, 1024)])
+def test_gemv_rmsnorm_dev(oracle, dtype, rows, cols):
+    # The fused residual add and RMSNorm in front of the bit-exact gemv
+    # (nnh_gemv_rmsnorm_dev): the streamed kernel's prologue (2048+ rows of
+    # 64+ blocks; 4608 rows: 16 per workgroup), the tall kernel's (12288+
+    # rows), and the norm kernel before the plain gemv otherwise (few rows,
+    # short rows, BF16). y, x_out and rec bit-equal an independent
+    # restatement of the norm followed by the oracle's gemv; with and without r.
+    import torch
+    say("rmsnorm gemv", dtype, rows, cols)
+    rng = oracle.Rng(0x4E0 + rows + cols + dtype)
+    wf = rng.normals(rows * cols, 0.02).reshape(rows, cols)
+    if dtype == 3:
+        wb = oracle.f32_array_to_bf16(wf.ravel())
+        w = N.Weight.bf16(wb, rows, cols)
+        wdq = oracle.bf16_array_to_f32(wb).reshape(rows, cols).astype(np.float64)
+    else:
+        m = oracle.QMatrix.from_f32(dtype, wf)
+        w = upload(m)
+    x = rng.normals(cols, 1.0)
+    rr = rng.normals(cols, 0.5)
+    gamma = (1.0 + 0.1 * rng.normals(cols, 1.0)).astype(np.float32)
+    eps = 1e-6
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()  # noqa: E731
+    xd, rd, gd = dev(x), dev(rr), dev(gamma)
+    for use_r in (True, False):
+        v, normed = rmsnorm_ref(x, rr if use_r else None, gamma, eps)
+        if dtype == 3:
+            want = N.model_gemv(w, normed)  # the BF16 path on the normed input (its own parity is tested apart)
+        else:
+            want = oracle.gemv_batch(m, normed)
+        xo = torch.full((cols,), 7.0, device="cuda")
+        rec = torch.full((cols,), 7.0, device="cuda")
+        scratch = torch.zeros(cols, device="cuda")
+        y = torch.zeros(rows, device="cuda")
+        N.gemv_rmsnorm_dev(w, xd.data_ptr(), rd.data_ptr() if use_r else 0, gd.data_ptr(), eps, xo.data_ptr(),
+                           rec.data_ptr(), scratch.data_ptr(), y.data_ptr())
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y.cpu().numpy()), bits(want)), use_r
+        assert np.array_equal(bits(xo.cpu().numpy()), bits(v)) and np.array_equal(bits(rec.cpu().numpy()), bits(v))
+        assert np.array_equal(bits(xd.cpu().numpy()), bits(x))  # x itself untouched
+    with pytest.raises(N.InvalidArgument):
+        N.gemv_rmsnorm_dev(w, xd.data_ptr(), rd.data_ptr(), gd.data_ptr(), eps, xd.data_ptr(), 0,
+                           scratch.data_ptr(), y.data_ptr())
+    w.free()
+
+
 @pytest.mark.parametrize("dtype", [1, 2])
 def test_f32_batch_equals_single(oracle, dtype):
     # kernels/tests.rs:641-691: every vector of a batch gets the single-vector bits.

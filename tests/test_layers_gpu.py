@@ -111,6 +111,43 @@ def test_qwen2_q4_and_fused_matrices(N):
     assert np.array_equal(t, t2)
 
 
+@pytest.mark.parametrize("size", ["small", "wide"])
+def test_fused_norm_decode(N, size):
+    # One-token f32 forwards with fused q / k / v and gate / up: each
+    # residual add and RMSNorm runs in the next matmul's prologue
+    # (nnh_gemv_rmsnorm_dev; the residual stream alternates between two
+    # buffers). Tokens, per-layer states and K/V caches equal the CPU
+    # forward's, eagerly and from decode-graph replays, and the unfused
+    # run's. "wide": d 2048 and FFN 6144, so q / k / v takes the streamed
+    # kernel's prologue and gate / up (12288 rows) the tall kernel's;
+    # "small": the norm kernel before the plain gemv.
+    import torch
+    from nncpu_amd.models import Model, llama_config, qwen2_config
+    if size == "wide":
+        cfg = qwen2_config(n_layer=2, n_embd=2048, n_head=16, n_kv=2, n_ff=6144, n_vocab=1024, n_ctx=64,
+                           head_dim=128)
+        model = Model.random(cfg, seed=0x7E1)
+    else:
+        cfg = llama_config(n_layer=2, n_embd=384, n_head=6, n_kv=2, n_ff=1024, n_vocab=1024, n_ctx=64)
+        model = Model.random(cfg, seed=0x7E2, tied=False)
+    prompt = np.random.default_rng(11).integers(0, cfg.n_vocab, 21).astype(np.int32)
+    n_gen = 8
+    tc = run_both(model, prompt, n_gen, fused=True)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=16, stream=s.cuda_stream, fused=True)
+    try:
+        tg, _, kg, vg = dev.generate_graph(prompt, n_gen, stream=s)
+        dev.set_fused_norm(False)
+        tu, hu, ku, vu = dev.generate(prompt, n_gen)
+        dev.set_fused_norm(True)
+        tf, hf, kf, vf = dev.generate(prompt, n_gen)
+    finally:
+        dev.free()
+    assert np.array_equal(tg, tc) and np.array_equal(tu, tc) and np.array_equal(tf, tc)
+    assert np.array_equal(hf, hu), np.argwhere(hf != hu)[:5]
+    assert np.array_equal(kf, ku) and np.array_equal(vf, vu) and np.array_equal(kg, kf) and np.array_equal(vg, vf)
+
+
 def test_forward_dev_graph_replay(N):
     # nngl_forward_dev allocates nothing: one prefill captured in a HIP graph
     # and replayed (eager work between replays) gives the eager hidden states.
