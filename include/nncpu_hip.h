@@ -240,6 +240,17 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
 int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, const float* gamma, float eps,
                          float* x_out, float* rec, float* normed, float* y, void* stream);
 
+/* nnh_gemv_rmsnorm_dev with the activation mode named: NNH_ACT_F32 is that
+ * call; NNH_ACT_I8 quantizes the normed input with nncpu's Q8_0 encoder
+ * (quant.rs:31-60) and runs the int8 matmul on it, the same bits as the norm
+ * followed by nnh_gemv_batch_dev(..., NNH_ACT_I8). No counterpart in the
+ * reference (its forward quantizes inside each matmul call); for a
+ * device-resident forward in the int8 mode. Rows of 97 to 256 blocks (3104
+ * to 8192 columns) run the norm and the quantizer in the matmul's own
+ * launch; other shapes run a norm kernel into `normed`, then the matmul. */
+int nnh_gemv_rmsnorm_act_dev(const nnh_weight* w, int act, const float* x, const float* r, const float* gamma,
+                             float eps, float* x_out, float* rec, float* normed, float* y, void* stream);
+
 /* Device-resident argmax of model_argmax (model/forward.rs:1003-1011) over
  * n logits at v (device): the first largest value, NaN never winning and a
  * NaN at index 0 keeping 0. Writes the index to *out_row (device, u64);

@@ -206,11 +206,17 @@ def gemv_batch_dev(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: i
 
 
 def gemv_rmsnorm_dev(w: Weight, x_ptr: int, r_ptr: int, gamma_ptr: int, eps: float, x_out_ptr: int, rec_ptr: int,
-                     normed_ptr: int, y_ptr: int, stream: int = 0) -> None:
-    """y = W ((v * rms(v)) * gamma), v = x + r (r_ptr 0: v = x), bit-exact f32;
-    v also to x_out / rec when non-zero (device pointers)."""
-    check(lib().nnh_gemv_rmsnorm_dev(w.handle, x_ptr, r_ptr or None, gamma_ptr, eps, x_out_ptr or None,
-                                     rec_ptr or None, normed_ptr, y_ptr, stream or None))
+                     normed_ptr: int, y_ptr: int, stream: int = 0, act: int = ACT_F32) -> None:
+    """y = W ((v * rms(v)) * gamma), v = x + r (r_ptr 0: v = x), in the
+    activation mode `act` (ACT_F32 bit-exact, or ACT_I8: the normed input
+    quantized to Q8_0 blocks); v also to x_out / rec when non-zero (device
+    pointers)."""
+    if act == ACT_F32:
+        check(lib().nnh_gemv_rmsnorm_dev(w.handle, x_ptr, r_ptr or None, gamma_ptr, eps, x_out_ptr or None,
+                                         rec_ptr or None, normed_ptr, y_ptr, stream or None))
+    else:
+        check(lib().nnh_gemv_rmsnorm_act_dev(w.handle, act, x_ptr, r_ptr or None, gamma_ptr, eps, x_out_ptr or None,
+                                             rec_ptr or None, normed_ptr, y_ptr, stream or None))
 
 
 def gemv_batch_dev_noalloc(w: Weight, x_ptr: int, x_stride: int, y_ptr: int, y_stride: int, n_tok: int,

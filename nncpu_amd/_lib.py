@@ -86,6 +86,8 @@ def _declare(L):
     L.nnh_gemv_batch_dev.argtypes, L.nnh_gemv_batch_dev.restype = [vp, vp, sz, vp, sz, sz, i32, vp], i32
     L.nnh_gemv_rmsnorm_dev.argtypes = [vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, vp]
     L.nnh_gemv_rmsnorm_dev.restype = i32
+    L.nnh_gemv_rmsnorm_act_dev.argtypes = [vp, i32, vp, vp, vp, C.c_float, vp, vp, vp, vp, vp]
+    L.nnh_gemv_rmsnorm_act_dev.restype = i32
     L.nnh_gemv_batch_dev_noalloc.argtypes = [vp, vp, sz, vp, sz, sz, i32, vp]
     L.nnh_gemv_batch_dev_noalloc.restype = i32
     L.nnh_act_layout.argtypes, L.nnh_act_layout.restype = [sz, sz, P(sz), P(sz), P(sz)], i32

@@ -778,32 +778,44 @@ int nnh_gemv_batch_dev(const nnh_weight* w, const float* x, size_t x_stride, flo
     return run_gemv(w, x, xs, y, ys, n_tok, act, s, (hipStream_t)stream);
 }
 
-int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, const float* gamma, float eps,
-                         float* x_out, float* rec, float* normed, float* y, void* stream) {
+int nnh_gemv_rmsnorm_act_dev(const nnh_weight* w, int act, const float* x, const float* r, const float* gamma,
+                             float eps, float* x_out, float* rec, float* normed, float* y, void* stream) {
     std::lock_guard<std::mutex> g(g_mu);
     int rc = ensure_locked();
     if (rc) return rc;
-    if ((rc = check_call(w, w ? w->cols : 0, w ? w->rows : 0, 1, NNH_ACT_F32))) return rc;
+    if (act != NNH_ACT_F32 && act != NNH_ACT_I8)
+        return fail(NNH_E_INVALID, "gemv rmsnorm: activation mode is not NNH_ACT_F32 or NNH_ACT_I8");
+    if ((rc = check_call(w, w ? w->cols : 0, w ? w->rows : 0, 1, act))) return rc;
     if (!x || !gamma || !normed || !y) return fail(NNH_E_INVALID, "gemv rmsnorm: null x, gamma, normed or y");
     if (w->cols > 16384) return fail(NNH_E_INVALID, "gemv rmsnorm: more than 16384 columns");
     const auto overlaps = [&](const float* a, const float* b) { return a && b && a < b + w->cols && b < a + w->cols; };
     if (overlaps(x_out, x) || overlaps(x_out, r) || overlaps(rec, x) || overlaps(rec, r))
         return fail(NNH_E_INVALID, "gemv rmsnorm: x_out / rec overlap x or r");
-    if ((rc = prepare_locked(w, layouts_for(w, NNH_ACT_F32, 1)))) return rc;
+    if ((rc = prepare_locked(w, layouts_for(w, act, 1)))) return rc;
     const hipStream_t st = (hipStream_t)stream;
     const nnh::NormIn nrm{x, r, gamma, x_out, rec, eps};
-    if (w->dtype != NNH_BF16 &&
-        nnh::launch_gemv_f32_norm(w->dtype, w->fq, w->fs, w->bi, nrm, (int)w->rows, (int)w->nb, (int)w->nbp, y,
-                                  w->f32v2, st)) {
-        NNH_HIP(hipGetLastError());
-        return NNH_OK;
+    if (w->dtype != NNH_BF16) {
+        const bool fused =
+            act == NNH_ACT_F32
+                ? nnh::launch_gemv_f32_norm(w->dtype, w->fq, w->fs, w->bi, nrm, (int)w->rows, (int)w->nb,
+                                            (int)w->nbp, y, w->f32v2, st)
+                : nnh::launch_gemv_i8_norm(w->dtype, w->qs, w->sc, w->sb, nrm, (int)w->rows, (int)w->nb, y, st);
+        if (fused) {
+            NNH_HIP(hipGetLastError());
+            return NNH_OK;
+        }
     }
     uint8_t* s = nullptr;
-    const size_t need = gemv_scratch_bytes(w, 1, NNH_ACT_F32);
+    const size_t need = gemv_scratch_bytes(w, 1, act);
     if (need && (rc = scratch_locked(st, need, &s))) return rc;
     nnh::launch_rmsnorm_vec(nrm, (int)w->cols, normed, st);
     NNH_HIP(hipGetLastError());
-    return run_gemv(w, normed, w->cols, y, w->rows, 1, NNH_ACT_F32, s, st);
+    return run_gemv(w, normed, w->cols, y, w->rows, 1, act, s, st);
+}
+
+int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, const float* gamma, float eps,
+                         float* x_out, float* rec, float* normed, float* y, void* stream) {
+    return nnh_gemv_rmsnorm_act_dev(w, NNH_ACT_F32, x, r, gamma, eps, x_out, rec, normed, y, stream);
 }
 
 int nnh_gemv_batch_dev_noalloc(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,

@@ -70,6 +70,18 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
 #define NNH_LGKMCNT0 (0xF | (0x7 << 4) | (0x3 << 14))
 
+// s_waitcnt vmcnt(K) that is also a compiler memory barrier: every vector
+// memory load issued before the K issued last has completed (loads complete
+// in issue order), and no memory access moves across it. A kernel that
+// issues direct-to-LDS copies and then K register loads waits for the copies
+// alone with it; K must not exceed the number of load instructions issued
+// after the copies.
+template <int K>
+__device__ __forceinline__ void wait_vm_keep() {
+    static_assert(K >= 0 && K <= 63, "vmcnt holds 0..63");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(K) : "memory");
+}
+
 // Compute units of the current device (kernels_misc.hip).
 int cu_count();
 
@@ -95,11 +107,24 @@ int f32_v2_parts(int rows);
 void launch_gemv_f32_v2_argmax(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
                                const float* x, float* xsum, int rows, int nb, int nbp, float* y, uint64_t* part,
                                hipStream_t st);
-// One vector with the fused residual add and RMSNorm (f32_m1.h NormIn): the
-// streamed or tall kernel with the norm in its prologue; false (nothing
-// launched) when neither applies (the caller then runs launch_rmsnorm_vec,
-// at most 16384 columns, and the plain gemv).
-struct NormIn;
+// The residual add and RMSNorm that a one-vector gemv can run on its input
+// first (nnh_gemv_rmsnorm_dev, nnh_gemv_rmsnorm_act_dev): v = x + r (r NULL:
+// v = x), then the gemv's input is (v * rms(v)) * gamma. Workgroup 0 writes
+// v to x_out and rec (either may be NULL); x_out must not overlap x, which
+// other workgroups may still be reading.
+struct NormIn {
+    const float* x;
+    const float* r;
+    const float* gamma;
+    float* x_out;
+    float* rec;
+    float eps;
+};
+
+// One vector with the fused residual add and RMSNorm: the streamed or tall
+// kernel with the norm in its prologue; false (nothing launched) when
+// neither applies (the caller then runs launch_rmsnorm_vec, at most 16384
+// columns, and the plain gemv).
 bool launch_gemv_f32_norm(int dtype, const uint8_t* fq, const uint16_t* fs, const uint16_t* biases,
                           const NormIn& nrm, int rows, int nb, int nbp, float* y, bool v2, hipStream_t st);
 void launch_rmsnorm_vec(const NormIn& nrm, int cols, float* out, hipStream_t st);
@@ -114,6 +139,13 @@ void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
                     const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
                     hipStream_t st);
+// One vector with the residual add, RMSNorm and Q8_0 quantizer fused into
+// the int8 GEMV's prologue (same bits as launch_rmsnorm_vec, the quantizer
+// and launch_gemv_i8 in turn); false (nothing launched) when the shape or
+// alignment does not fit it (rows of 97 .. 256 blocks, 16-byte aligned
+// vectors, Q4 with its packed scale-and-bias words).
+bool launch_gemv_i8_norm(int dtype, const uint8_t* qs, const uint16_t* scales, const uint32_t* sb,
+                         const NormIn& nrm, int rows, int nb, float* y, hipStream_t st);
 // f32 -> Q8_0 / Q4 split layout on the device (kernels_encode.hip).
 void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* sc, uint16_t* bi, hipStream_t st);
 // BF16 weights (kernels_bf16.hip): the reference's kernel by shape.

@@ -48,20 +48,6 @@ struct F32Mat {
 
 __device__ __forceinline__ int m1_groups(int dt, int nb) { return dt == 1 ? (nb + 7) / 8 : (nb + 15) / 16; }
 
-// The residual add and RMSNorm that a one-vector gemv can run on its input
-// first (nnh_gemv_rmsnorm_dev): v = x + r (r NULL: v = x), then the gemv's
-// input is (v * rms(v)) * gamma. Workgroup 0 writes v to x_out and rec
-// (either may be NULL); x_out must not overlap x, which other workgroups
-// may still be reading.
-struct NormIn {
-    const float* x;
-    const float* r;
-    const float* gamma;
-    float* x_out;
-    float* rec;
-    float eps;
-};
-
 // The scale rows row0 .. row0 + nrows - 1 of a matrix, staged into LDS by a
 // workgroup of NT threads (MAXB: most bytes staged): load() issues the loads
 // (unconditional, clamped, so the caller's wait counts stay exact), store()

@@ -824,7 +824,10 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
         const int g = d < ngp ? d : ngp - 1;
         m1x_load<DT, SL>(slot[d], qrow, srow, brow, g, min(g, ngb - 1));
     }
-    __builtin_amdgcn_s_waitcnt(NNH_VMCNT(0));
+    // The copies have landed once at most the slots' loads are in flight
+    // (per slot: the quant piece, the scales unless staged, Q4's two
+    // biases); the norm and the block sums run while the slots fill.
+    wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>();
     __syncthreads();
     if (NORM)
         norm_prologue<NT, 32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
@@ -1134,42 +1137,71 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[r][m][e] = 0.0f;
 
-    // The first PF weight groups are in flight while x is copied to LDS
-    // (indices clamped to the row's last group: a few repeated loads at the
-    // row's end are never used).
     V2Group<DT, R> slot[PF];
-#pragma unroll
-    for (int d = 0; d < (PF == 2 ? 1 : PF); ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
-    extern __shared__ __align__(16) float xl[];  // [M][cols] (NORM: then gamma), 16-byte aligned for float4
+    constexpr int PF0 = PF == 2 ? 1 : PF;  // groups issued before the arithmetic
+    // [M][cols] (NORM: x, then r or gamma one 1 KB-rounded region on),
+    // 16-byte aligned for float4.
+    extern __shared__ __align__(16) float xl[];
     const int cols = nb * 32;
     if constexpr (NORM) {
-        // x (+ r) and gamma staged; norm_prologue then forms the gemv's input.
+        // x and r (else gamma) are copied to LDS, then the first weight
+        // groups issued: the add and the sum of squares run while those are
+        // in flight. With r, gamma is copied over r's region once the add
+        // is done, alongside the sum of squares.
         __shared__ float nsc;
-        float* gl = xl + cols;
-        for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256) {
-            *(float4*)(xl + i) = __builtin_bit_cast(float4, *(const f4u*)(nrm.x + i));
-            *(float4*)(gl + i) = __builtin_bit_cast(float4, *(const f4u*)(nrm.gamma + i));
-        }
-        if (nrm.r) {
-            // r added in place by each thread on its own pieces, before the barrier.
-            for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256) {
-                const float4 b = __builtin_bit_cast(float4, *(const f4u*)(nrm.r + i));
-                float4 a = *(float4*)(xl + i);
+        const size_t xlen = (size_t)cols * 4, xb = m1x_x_bytes(nb);
+        unsigned char* l8 = (unsigned char*)xl;
+        float* gl = (float*)(l8 + xb);
+        const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+        for (size_t c = wave; c * 1024 < xlen; c += 4) copy_1k(nrm.x, xlen, c * 1024, l8 + c * 1024, lane);
+        const float* second = nrm.r ? nrm.r : nrm.gamma;
+        for (size_t c = wave; c * 1024 < xlen; c += 4) copy_1k(second, xlen, c * 1024, l8 + xb + c * 1024, lane);
+#pragma unroll
+        for (int d = 0; d < PF0; ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
+        wait_vm_keep<PF0 * 2 * R>();  // per group and row: the quant piece and the scales
+        __syncthreads();
+        for (int i = 4 * tid; i < cols; i += 4 * 256) {
+            float4 a = *(const float4*)(xl + i);
+            if (nrm.r) {
+                const float4 b = *(const float4*)(gl + i);
                 a = float4{__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w)};
                 *(float4*)(xl + i) = a;
             }
+            if (blockIdx.x == 0) {
+                if (nrm.x_out) *(float4*)(nrm.x_out + i) = a;
+                if (nrm.rec) *(float4*)(nrm.rec + i) = a;
+            }
+        }
+        if (nrm.r) {
+            __syncthreads();
+            for (size_t c = wave; c * 1024 < xlen; c += 4)
+                copy_1k(nrm.gamma, xlen, c * 1024, l8 + xb + c * 1024, lane);
+        }
+        if (tid < 64) {
+            const double ss = rms_sumsq<16>(xl, cols, tid);
+            if (tid == 0) nsc = rms_scale(ss, cols, nrm.eps);
+        }
+        if (nrm.r) wait_vm_keep<0>();  // gamma's copies (the weight groups with them)
+        __syncthreads();
+        const float sc = nsc;
+        for (int i = 4 * tid; i < cols; i += 4 * 256) {
+            const float4 a = *(const float4*)(xl + i), g = *(const float4*)(gl + i);
+            *(float4*)(xl + i) = float4{__fmul_rn(__fmul_rn(a.x, sc), g.x), __fmul_rn(__fmul_rn(a.y, sc), g.y),
+                                        __fmul_rn(__fmul_rn(a.z, sc), g.z), __fmul_rn(__fmul_rn(a.w, sc), g.w)};
         }
         __syncthreads();
-        NormIn n2 = nrm;
-        n2.r = nullptr;  // already added
-        norm_prologue<256, 16>(n2, xl, nullptr, gl, cols, &nsc);
         if (DT == 2) {
             // Q4: the block sums of the normed input (scalar.rs:355-359), in
             // gamma's place, for the bias dot.
-            for (int b = threadIdx.x; b < nb; b += 256) gl[b] = m1_block_sum(xl + 32 * b);
+            for (int b = tid; b < nb; b += 256) gl[b] = m1_block_sum(xl + 32 * b);
             __syncthreads();
         }
     } else {
+        // The first weight groups are in flight while x is copied to LDS
+        // (indices clamped to the row's last group: a few repeated loads at
+        // the row's end are never used).
+#pragma unroll
+        for (int d = 0; d < PF0; ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
         for (int m = 0; m < M; ++m)
             for (int i = 4 * (int)threadIdx.x; i < cols; i += 4 * 256)
                 *(float4*)(xl + m * cols + i) =
@@ -1218,7 +1250,8 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
             const int body = nb & ~7;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float* xs = NORM ? xl + cols : xsum + (size_t)m * nb;
+                const float* xs =
+                    NORM ? (const float*)((const unsigned char*)xl + m1x_x_bytes(nb)) : xsum + (size_t)m * nb;
                 float a = 0.0f;
                 for (int i = j; i < body; i += 8) a = __builtin_fmaf(bf16f(brow[i]), xs[i], a);
                 float p = __fadd_rn(a, xor_get(a, 4));
@@ -1289,7 +1322,7 @@ void launch_v2_norm(const uint8_t* fq, const uint16_t* fs, const uint16_t* bi, c
     }();
     (void)once;
     const dim3 grid(ceil_div(rows, 32)), block(256);
-    const size_t lds = 2 * (size_t)nb * 32 * sizeof(float);
+    const size_t lds = 2 * m1x_x_bytes(nb);  // x, then r / gamma / Q4's block sums
     gemv_f32_v2_kernel<DT, 1, 1, 4, true>
         <<<grid, block, lds, st>>>(fq, fs, bi, nullptr, 0, nullptr, rows, nb, nbp, y, rows, nullptr, nrm);
 }

@@ -14,6 +14,7 @@
 
 #include "common.h"
 #include "q8_act.h"
+#include "rmsnorm_exact.h"
 
 namespace nnh {
 namespace {
@@ -445,6 +446,213 @@ bool launch_v2_m(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, cons
     return true;
 }
 
+
+// ---- int8 GEMV with the residual add, RMSNorm and quantizer fused -----------
+//
+// One vector, rows of 97 .. 256 blocks, where the plain GEMV runs 64 lanes
+// per row (lane l summing blocks l, l + 64, ... in that order) and reduces
+// the lanes with the xor tree (gemv_i8_kernel) or, for whole 64-block
+// rows, the DPP tree (gemv_i8_v2_kernel): the same per-lane order and tree
+// here (V2RED), so the results are the bits of the device forward's norm,
+// the quantizer and the plain GEMV run one after another. One workgroup of
+// 16 waves per CU forms the int8 input: its threads load their pieces of x,
+// r and gamma, then each wave requests its first weights, which are in
+// flight while wave 0 runs the sum of squares (the device forward's order,
+// rmsnorm_exact.h, from a chain-major copy in LDS) and the normed row is
+// quantized into LDS with the library quantizer's encoder (q8_act.h). Each
+// wave then takes row groups of R rows grid-stride, the next chunk's
+// weights in flight while the current one is summed.
+constexpr int I8N_T = 1024;  // threads per workgroup
+template <int DT, int R, int BPL, int K4, bool V2RED>
+__global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __restrict__ qs,
+                                                             const uint16_t* __restrict__ sc,
+                                                             const uint32_t* __restrict__ sb, int rows, int nb,
+                                                             float* __restrict__ y, NormIn nrm) {
+    constexpr int QV = DT == 1 ? 2 : 1;
+    constexpr int STEP = 64 * BPL;
+    constexpr int NW = I8N_T / 64;
+    extern __shared__ __align__(16) unsigned char i8n_smem[];
+    __shared__ float nsc;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int cols = nb * 32, n4 = cols / 4, ts = rms_t_stride(cols);
+    const size_t qrow_bytes = DT == 1 ? (size_t)cols : (size_t)cols / 2;
+    float* xt = (float*)i8n_smem;                                  // x (+ r), chain-major: [8][ts]
+    int8_t* xq = (int8_t*)(i8n_smem + (size_t)32 * ts);            // the quants
+    double2* xsx = (double2*)(i8n_smem + (size_t)32 * ts + cols);  // per block: scale, scale * sum of quants
+
+    // Piece k of this thread: values 4i .. 4i + 3, i = tid + I8N_T k.
+    float4 xv[K4], rv[K4], gv[K4];
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int i = tid + I8N_T * k;
+        if (i < n4) {
+            xv[k] = ((const float4*)nrm.x)[i];
+            gv[k] = ((const float4*)nrm.gamma)[i];
+            if (nrm.r) rv[k] = ((const float4*)nrm.r)[i];
+        }
+    }
+    // Every wave's piece loads are issued before any weight load (an
+    // execution barrier only: nothing waits for the loads here), so waiting
+    // for the pieces waits neither for this wave's weights (loads complete
+    // in issue order) nor behind other waves' in the CU's memory pipeline.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    struct Chunk {
+        int4 w[R][BPL][QV];
+        uint32_t s[R][BPL];
+    };
+    const int ng = (rows + R - 1) / R, gstep = gridDim.x * NW;
+    auto load = [&](Chunk& k, int g, int c0) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int braw = c0 + lane + 64 * i;
+            const size_t b = braw < nb ? braw : nb - 1;  // in bounds; skipped by run
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const size_t rw = g * R + r < rows ? g * R + r : rows - 1;
+                const int4* wp = (const int4*)(qs + rw * qrow_bytes + (DT == 1 ? 32 : 16) * b);
+#pragma unroll
+                for (int v = 0; v < QV; ++v) k.w[r][i][v] = load_nt16(wp + v);
+                k.s[r][i] = DT == 1 ? (uint32_t)sc[rw * nb + b] : sb[rw * nb + b];
+            }
+        }
+    };
+    double acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0;
+    // The block terms in gemv_i8_kernel's order: per block, per row, the
+    // scaled dot, then (Q4) the bias term.
+    auto run = [&](const Chunk& k, int c0) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = c0 + lane + 64 * i;
+            if (b >= nb) continue;
+            const int4 x0 = ((const int4*)(xq + 32 * b))[0], x1 = ((const int4*)(xq + 32 * b))[1];
+            const double2 sx = xsx[b];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const double sw = (double)bf16f(k.s[r][i] & 0xffffu);
+                const int P = DT == 1 ? dot_q8(k.w[r][i][0], k.w[r][i][QV - 1], x0, x1)
+                                      : dot_q4(k.w[r][i][0], x0, x1);
+                acc[r] = __builtin_fma(sw * sx.x, (double)P, acc[r]);
+                if (DT == 2) acc[r] = __builtin_fma((double)bf16f(k.s[r][i] >> 16), sx.y, acc[r]);
+            }
+        }
+    };
+    auto finish = [&](int g) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            double v = acc[r];
+            if (V2RED) {
+                v = group_sum_f64<64>(v);
+            } else {
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) v += xor_get(v, m);
+            }
+            if (lane == 0 && g * R + r < rows) y[g * R + r] = (float)v;
+            acc[r] = 0.0;
+        }
+    };
+
+    const int g0 = blockIdx.x * NW + (tid >> 6);
+    Chunk A, B;
+    // Unconditional (a wave past the last row group rereads it, unused), so
+    // the waits for the pieces below count these loads exactly.
+    load(A, g0 < ng ? g0 : ng - 1, 0);
+
+    // x + r into LDS chain-major (element e at (e mod 8) * ts + e / 8;
+    // workgroup 0 also writes it out), the sum of squares, then the normed
+    // pieces quantized into LDS.
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int i = tid + I8N_T * k;
+        if (i < n4) {
+            if (nrm.r)
+                xv[k] = float4{__fadd_rn(xv[k].x, rv[k].x), __fadd_rn(xv[k].y, rv[k].y),
+                               __fadd_rn(xv[k].z, rv[k].z), __fadd_rn(xv[k].w, rv[k].w)};
+            float* d = xt + (size_t)(4 * (i & 1)) * ts + (i >> 1);
+            d[0] = xv[k].x;
+            d[ts] = xv[k].y;
+            d[2 * ts] = xv[k].z;
+            d[3 * ts] = xv[k].w;
+            if (blockIdx.x == 0) {
+                if (nrm.x_out) ((float4*)nrm.x_out)[i] = xv[k];
+                if (nrm.rec) ((float4*)nrm.rec)[i] = xv[k];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const double ss = rms_sumsq_t(xt, cols, tid);
+        if (tid == 0) nsc = rms_scale(ss, cols, nrm.eps);
+    }
+    __syncthreads();
+    const float scl = nsc;
+    float4 o[K4];
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        o[k] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (tid + I8N_T * k < n4)
+            o[k] = float4{__fmul_rn(__fmul_rn(xv[k].x, scl), gv[k].x), __fmul_rn(__fmul_rn(xv[k].y, scl), gv[k].y),
+                          __fmul_rn(__fmul_rn(xv[k].z, scl), gv[k].z), __fmul_rn(__fmul_rn(xv[k].w, scl), gv[k].w)};
+    }
+    q8_pieces<K4>(o, tid, I8N_T, n4, [&](int i, uint32_t word, const Q8Scale& s, int qsum) {
+        ((uint32_t*)xq)[i] = word;
+        if ((i & 7) == 0) xsx[i >> 3] = double2{(double)s.scale, (double)s.scale * (double)qsum};
+    });
+    __syncthreads();
+
+    if (g0 >= ng) return;
+    // Items (row group, chunk) in order; A holds the current item's
+    // weights, B the next one's, then the roles swap.
+    int ga = g0, ca = 0;
+    while (true) {
+        int gb = ga, cb = ca + STEP;
+        if (cb >= nb) {
+            cb = 0;
+            gb += gstep;
+        }
+        const bool hb = gb < ng;
+        if (hb) load(B, gb, cb);
+        run(A, ca);
+        if (ca + STEP >= nb) finish(ga);
+        if (!hb) break;
+        int gc = gb, cc = cb + STEP;
+        if (cc >= nb) {
+            cc = 0;
+            gc += gstep;
+        }
+        const bool hc = gc < ng;
+        if (hc) load(A, gc, cc);
+        run(B, cb);
+        if (cb + STEP >= nb) finish(gb);
+        if (!hc) break;
+        ga = gc;
+        ca = cc;
+    }
+}
+
+template <int DT, int R, int BPL, int K4, bool V2RED>
+void launch_i8n(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const NormIn& nrm, int rows, int nb,
+                float* y, hipStream_t st) {
+    constexpr int NW = I8N_T / 64;
+    const int want = ceil_div(ceil_div(rows, R), NW), cap = cu_count();
+    const int grid = want < cap ? want : cap;
+    const size_t lds = (size_t)32 * rms_t_stride(nb * 32) + (size_t)nb * 32 + (size_t)nb * 16;
+    gemv_i8_norm_kernel<DT, R, BPL, K4, V2RED><<<grid, I8N_T, lds, st>>>(qs, sc, sb, rows, nb, y, nrm);
+}
+
+template <int DT, int K4, bool V2RED>
+void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const NormIn& nrm, int rows, int nb,
+                   float* y, hipStream_t st) {
+    if (nb <= 128)
+        launch_i8n<DT, DT == 1 ? 1 : 2, 2, K4, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+    else
+        launch_i8n<DT, DT == 1 ? 1 : 2, 4, K4, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+}
+
 }  // namespace
 
 void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st) {
@@ -478,6 +686,29 @@ void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const 
         }
 #undef NNH_L
     }
+}
+
+bool launch_gemv_i8_norm(int dtype, const uint8_t* qs, const uint16_t* scales, const uint32_t* sb,
+                         const NormIn& nrm, int rows, int nb, float* y, hipStream_t st) {
+    const auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (nb <= 96 || nb > 256 || (dtype == 2 && !sb)) return false;
+    if (!aligned(nrm.x) || !aligned(nrm.gamma) || !aligned(nrm.r) || !aligned(nrm.x_out) || !aligned(nrm.rec))
+        return false;
+    const bool v2red = nb % 64 == 0;  // the plain GEMV's kernel at this row length
+#define NNH_N(DT, K4)                                                            \
+    do {                                                                         \
+        if (v2red)                                                               \
+            launch_i8n_dt<DT, K4, true>(qs, scales, sb, nrm, rows, nb, y, st);   \
+        else                                                                     \
+            launch_i8n_dt<DT, K4, false>(qs, scales, sb, nrm, rows, nb, y, st);  \
+    } while (0)
+    if (dtype == 1) {
+        if (nb <= 128) NNH_N(1, 1); else NNH_N(1, 2);
+    } else {
+        if (nb <= 128) NNH_N(2, 1); else NNH_N(2, 2);
+    }
+#undef NNH_N
+    return true;
 }
 
 void launch_block_dots(int dtype, const uint8_t* qs, const int8_t* aq, int rows, int nb, int n_tok, int32_t* P,

@@ -63,6 +63,56 @@ __device__ __forceinline__ double rms_sumsq(const float* v, int dim, int lane) {
     return s;
 }
 
+// The same sum of squares from a chain-major copy: FMA lane l's values
+// (elements l, l + 8, ...) contiguous at vt + l * stride (rms_t_stride),
+// read 16 bytes at a time, B of those per batch, the next batch's reads in
+// flight while the current batch's FMAs run. dim a multiple of 32 (no tail).
+// Run by one wave; the result is returned to every lane.
+__host__ __device__ inline int rms_t_stride(int dim) { return dim / 8 + 4; }  // 16-byte rows, staggered banks
+template <int B = 8>
+__device__ __forceinline__ double rms_sumsq_t(const float* vt, int dim, int lane) {
+    const int nq = dim / 32;  // 16-byte reads per FMA lane
+    const int nfull = nq / B;
+    float a = 0.0f;
+    if (lane < 8) {
+        const float4* p = (const float4*)(vt + lane * rms_t_stride(dim));
+        float4 ta[B], tb[B];
+        auto fma4 = [&](const float4& v) {
+            a = __fmaf_rn(v.x, v.x, a);
+            a = __fmaf_rn(v.y, v.y, a);
+            a = __fmaf_rn(v.z, v.z, a);
+            a = __fmaf_rn(v.w, v.w, a);
+        };
+        if (nfull > 0) {
+#pragma unroll
+            for (int k = 0; k < B; ++k) ta[k] = p[k];
+            // Batch reads are clamped to the last whole batch (rereads past
+            // the end are never used), so the loop has no divergent loads.
+            // The scheduling barriers keep each batch's reads ahead of the
+            // previous batch's FMAs (the compiler would sink them).
+            for (int t = 0;; t += 2) {
+                const float4* q1 = p + B * min(t + 1, nfull - 1);
+#pragma unroll
+                for (int k = 0; k < B; ++k) tb[k] = q1[k];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k = 0; k < B; ++k) fma4(ta[k]);
+                if (t + 1 >= nfull) break;
+                const float4* q2 = p + B * min(t + 2, nfull - 1);
+#pragma unroll
+                for (int k = 0; k < B; ++k) ta[k] = q2[k];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k = 0; k < B; ++k) fma4(tb[k]);
+                if (t + 2 >= nfull) break;
+            }
+        }
+        for (int k = B * nfull; k < nq; ++k) fma4(p[k]);
+    }
+    const float h = rms_hsum8_lanes(a);
+    return (double)__shfl(h, 0, 64);
+}
+
 // (float)(1 / sqrt(ss / dim + eps)) with ss a double, in f64.
 __device__ __forceinline__ float rms_scale(double ss, int dim, float eps) {
     const float inv_dim = __fdiv_rn(1.0f, (float)dim);

@@ -82,67 +82,24 @@ struct QOut {
     double* sx;
 };
 
-// Lane exchanges by DPP (a VALU operand modifier, no LDS round trip): 0xB1
-// quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141 row_half_mirror (lane
-// i <-> 7 - i within 8), 0x140 row_mirror (i <-> 15 - i within 16). After
-// the first k of them every lane holds the max / sum over its aligned group
-// of 2, 4, 8, 16 lanes (max and integer sums do not depend on the order).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-__device__ __forceinline__ float max8(float a) {
-    a = fmaxf(a, dpp_f<0xB1>(a));
-    a = fmaxf(a, dpp_f<0x4E>(a));
-    return fmaxf(a, dpp_f<0x141>(a));
-}
-__device__ __forceinline__ int sum8(int a) {
-    a += dpp_i<0xB1>(a);
-    a += dpp_i<0x4E>(a);
-    return a + dpp_i<0x141>(a);
-}
+using nnh::dpp_f;
+using nnh::dpp_i;
+using nnh::max8;
+using nnh::sum8;
 
-// A thread's pieces k = 0 .. K-1, piece k being values 4i .. 4i+3 of the row
-// with i = i0 + k * stride (i0 & 7 == lane & 7, stride a multiple of 8), so a
-// block is one piece of each of 8 consecutive lanes. Every lane of the wave
-// calls it, pieces at i >= n4 holding zeros (a whole block is in range or
-// not); each step runs over all pieces before the next, so the pieces'
-// chains overlap, and only the stores are conditional.
+// A thread's pieces of the row into qo (nnh::q8_pieces: piece k is values
+// 4i .. 4i+3, i = i0 + k * stride; every lane of the wave calls it).
 template <int K>
 __device__ __forceinline__ void q8_pieces(const float4 (&p)[K], int i0, int stride, int n4, const QOut& qo) {
-    float a[K];
-    nnh::Q8Scale s[K];
-    int q[K][4], qs[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-        a[k] = max8(fmaxf(fmaxf(nnh::q8_abs(p[k].x), nnh::q8_abs(p[k].y)),
-                          fmaxf(nnh::q8_abs(p[k].z), nnh::q8_abs(p[k].w))));
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        s[k] = nnh::q8_scale(a[k]);
-        q[k][0] = nnh::q8_quant(p[k].x, s[k].inv);
-        q[k][1] = nnh::q8_quant(p[k].y, s[k].inv);
-        q[k][2] = nnh::q8_quant(p[k].z, s[k].inv);
-        q[k][3] = nnh::q8_quant(p[k].w, s[k].inv);
-        qs[k] = sum8(q[k][0] + q[k][1] + q[k][2] + q[k][3]);
-    }
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int i = i0 + k * stride;
-        if (i >= n4) continue;
-        ((uint32_t*)qo.q)[i] = (uint32_t)(q[k][0] & 255) | (uint32_t)(q[k][1] & 255) << 8 |
-                               (uint32_t)(q[k][2] & 255) << 16 | (uint32_t)(q[k][3] & 255) << 24;
+    nnh::q8_pieces<K>(p, i0, stride, n4, [&](int i, uint32_t word, const nnh::Q8Scale& s, int qs) {
+        ((uint32_t*)qo.q)[i] = word;
         if ((i & 7) == 0) {
             const int b = i >> 3;
-            qo.s[b] = (uint16_t)s[k].bits;
-            qo.sx[2 * b] = (double)s[k].scale;
-            qo.sx[2 * b + 1] = (double)s[k].scale * (double)qs[k];  // exact: s_x * sum(q_x)
+            qo.s[b] = (uint16_t)s.bits;
+            qo.sx[2 * b] = (double)s.scale;
+            qo.sx[2 * b + 1] = (double)s.scale * (double)qs;  // exact: s_x * sum(q_x)
         }
-    }
+    });
 }
 
 // Value j of the row, a block being one half-wave (j & 31 == lane & 31, all
@@ -1297,12 +1254,14 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
     uint8_t *qe = fq ? m->qa_e : nullptr, *qt = fq ? m->qa_a : nullptr, *qf = fq ? m->qa_f : nullptr;
     const QOut oe = qout(qe, m->qo_e), oa = qout(qt, m->qo_a), of = qout(qf, m->qo_f);
     m->q_last = false;
-    // One token in NNH_ACT_F32 with the fused matrices (Llama / Qwen: no
-    // post-norms): each residual add and RMSNorm runs in the prologue of the
-    // q / k / v or gate / up matmul (nnh_gemv_rmsnorm_dev), which writes the
-    // new residual stream to the other of two buffers; the last layer's
-    // final norm stays a kernel of its own.
-    const bool fn = m->nfuse && n == 1 && m->act == NNH_ACT_F32 && !gemma && m->fused_qkv && m->fused_gu;
+    // One token with the fused matrices (Llama / Qwen: no post-norms), in
+    // NNH_ACT_F32 or with the producers quantizing in NNH_ACT_I8: each
+    // residual add and RMSNorm (and in NNH_ACT_I8 the quantizer) runs in the
+    // prologue of the q / k / v or gate / up matmul
+    // (nnh_gemv_rmsnorm_act_dev), which writes the new residual stream to
+    // the other of two buffers; the last layer's final norm stays a kernel
+    // of its own.
+    const bool fn = m->nfuse && n == 1 && (m->act == NNH_ACT_F32 || fq) && !gemma && m->fused_qkv && m->fused_gu;
     float *xc = m->x, *xo = m->x2;  // the residual stream and the other buffer
     embed_kernel<<<n, 256, 0, st>>>(tokens_dev, m->table, c.wtype, c.n_vocab, E, embd_scale, m->x);
     if (!fn) launch_resid_norm(m->x, nullptr, nullptr, m->norms, m->normed, nullptr, n, E, c.rms_eps, oe, st);
@@ -1321,10 +1280,11 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
         if (fn) {
             // Layer 0 normalises the embedding row; a later layer first adds
             // the previous layer's FFN output and records that state.
-            const int rc = li == 0 ? nnh_gemv_rmsnorm_dev(W[0], xc, nullptr, nr, c.rms_eps, nullptr, nullptr,
-                                                           m->normed, m->qkv, st)
-                                   : nnh_gemv_rmsnorm_dev(W[0], xc, m->r, nr, c.rms_eps, xo,
-                                                           m->states + (size_t)(li - 1) * E, m->normed, m->qkv, st);
+            const int rc =
+                li == 0 ? nnh_gemv_rmsnorm_act_dev(W[0], m->act, xc, nullptr, nr, c.rms_eps, nullptr, nullptr,
+                                                   m->normed, m->qkv, st)
+                        : nnh_gemv_rmsnorm_act_dev(W[0], m->act, xc, m->r, nr, c.rms_eps, xo,
+                                                   m->states + (size_t)(li - 1) * E, m->normed, m->qkv, st);
             if (rc != NNH_OK) {
                 m->err = std::string("gemv rmsnorm: ") + nnh_last_error();
                 return 1;
@@ -1386,8 +1346,8 @@ static int forward_impl(nngl_model* m, const int32_t* tokens_dev, size_t n_tok, 
         NNGL_CHECK(hipGetLastError());
         if (gemv_q(m, W[3], qt, m->attn, QD, m->r, E, n_tok)) return 1;
         if (fn) {
-            if (nnh_gemv_rmsnorm_dev(W[4], xc, m->r, ffn_norm, c.rms_eps, xo, nullptr, m->normed, m->gu, st) !=
-                NNH_OK) {
+            if (nnh_gemv_rmsnorm_act_dev(W[4], m->act, xc, m->r, ffn_norm, c.rms_eps, xo, nullptr, m->normed, m->gu,
+                                         st) != NNH_OK) {
                 m->err = std::string("gemv rmsnorm: ") + nnh_last_error();
                 return 1;
             }
@@ -1540,10 +1500,11 @@ int nngl_set_fused_quant(nngl_model* m, int on) {
     return 0;
 }
 
-// on != 0 (the default): one-token forwards in NNH_ACT_F32 with fused
-// q / k / v and gate / up matrices run each residual add and RMSNorm inside
-// the next matmul's prologue (nnh_gemv_rmsnorm_dev: the same bits, one
-// launch fewer per norm); 0: the norm kernel, then the matmul.
+// on != 0 (the default): one-token forwards with fused q / k / v and
+// gate / up matrices, in NNH_ACT_F32 or in NNH_ACT_I8 with the producers
+// quantizing (nngl_set_fused_quant), run each residual add and RMSNorm
+// inside the next matmul's prologue (nnh_gemv_rmsnorm_act_dev: the same
+// bits, one launch fewer per norm); 0: the norm kernel, then the matmul.
 int nngl_set_fused_norm(nngl_model* m, int on) {
     m->nfuse = on != 0;
     return 0;

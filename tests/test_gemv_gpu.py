@@ -252,6 +252,52 @@ def test_gemv_rmsnorm_dev(oracle, dtype, rows, cols):
     w.free()
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(1, 4608, 3584), (2, 4608, 3584), (1, 4100, 4096), (2, 20000, 3584),
+                                             (2, 2050, 8192), (1, 1000, 6144), (1, 300, 3200), (2, 37, 4128),
+                                             (1, 512, 1024), (2, 96, 2048)])
+def test_gemv_rmsnorm_i8_dev(oracle, dtype, rows, cols):
+    # The int8 mode of the fused norm (nnh_gemv_rmsnorm_act_dev, NNH_ACT_I8):
+    # rows of 97..256 blocks run the norm and nncpu's Q8_0 quantizer in the
+    # int8 GEMV's prologue (112 blocks: the xor lane tree; 128 / 192 / 256:
+    # the DPP tree; row groups past four per CU and ragged last groups), other
+    # rows the norm kernel before the plain path (1024 and 2048 columns).
+    # y bit-equals the independent norm restatement followed by the plain
+    # int8 GEMV (nnh_gemv_batch_dev, NNH_ACT_I8) on the same device weight,
+    # whose own parity the int8 tests pin; x_out and rec bit-equal v.
+    import torch
+    say("rmsnorm gemv i8", dtype, rows, cols)
+    rng = oracle.Rng(0x18E0 + rows + cols + dtype)
+    dw = torch.from_numpy(rng.normals(rows * cols, 0.02)).cuda()
+    w = N.Weight.encode_dev(dtype, dw.data_ptr(), rows, cols)
+    del dw
+    x = rng.normals(cols, 1.0)
+    rr = rng.normals(cols, 0.5)
+    gamma = (1.0 + 0.1 * rng.normals(cols, 1.0)).astype(np.float32)
+    eps = 1e-6
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()  # noqa: E731
+    xd, rd, gd = dev(x), dev(rr), dev(gamma)
+    for use_r in (True, False):
+        v, normed = rmsnorm_ref(x, rr if use_r else None, gamma, eps)
+        want = torch.zeros(rows, device="cuda")
+        nd = dev(normed)
+        N.gemv_batch_dev(w, nd.data_ptr(), cols, want.data_ptr(), rows, 1, N.ACT_I8)
+        xo = torch.full((cols,), 7.0, device="cuda")
+        rec = torch.full((cols,), 7.0, device="cuda")
+        scratch = torch.zeros(cols, device="cuda")
+        y = torch.zeros(rows, device="cuda")
+        N.gemv_rmsnorm_dev(w, xd.data_ptr(), rd.data_ptr() if use_r else 0, gd.data_ptr(), eps, xo.data_ptr(),
+                           rec.data_ptr(), scratch.data_ptr(), y.data_ptr(), act=N.ACT_I8)
+        torch.cuda.synchronize()
+        got, exp = y.cpu().numpy(), want.cpu().numpy()
+        assert np.array_equal(bits(got), bits(exp)), (use_r, int(np.sum(bits(got) != bits(exp))))
+        assert np.array_equal(bits(xo.cpu().numpy()), bits(v)) and np.array_equal(bits(rec.cpu().numpy()), bits(v))
+        assert np.array_equal(bits(xd.cpu().numpy()), bits(x))
+    with pytest.raises(N.InvalidArgument):
+        N.gemv_rmsnorm_dev(w, xd.data_ptr(), rd.data_ptr(), gd.data_ptr(), eps, xd.data_ptr(), 0,
+                           scratch.data_ptr(), y.data_ptr(), act=N.ACT_I8)
+    w.free()
+
+
 @pytest.mark.parametrize("dtype", [1, 2])
 def test_f32_batch_equals_single(oracle, dtype):
     # kernels/tests.rs:641-691: every vector of a batch gets the single-vector bits.

@@ -148,6 +148,40 @@ def test_fused_norm_decode(N, size):
     assert np.array_equal(kf, ku) and np.array_equal(vf, vu) and np.array_equal(kg, kf) and np.array_equal(vg, vf)
 
 
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_fused_norm_decode_i8(N, dtype):
+    # One-token int8 forwards with fused q / k / v and gate / up at a width
+    # whose rows take the fused int8 kernel (d 3200: 100 blocks, the xor lane
+    # tree): each residual add, RMSNorm and Q8_0 quantizer runs in the next
+    # matmul's prologue (nnh_gemv_rmsnorm_act_dev). Tokens, per-layer states
+    # and K/V caches equal the run with the norm kernels, eagerly and from
+    # decode-graph replays, and the tokens and caches equal the CPU forward's
+    # in the int8 mode.
+    import torch
+    from nncpu_amd import ACT_I8, Q4S, Q8_0
+    from nncpu_amd.models import Model, qwen2_config
+    cfg = qwen2_config(n_layer=2, n_embd=3200, n_head=25, n_kv=5, n_ff=3200, n_vocab=1024, n_ctx=64, head_dim=128)
+    model = Model.random(cfg, seed=0x7E3 + dtype, dtype=Q8_0 if dtype == 1 else Q4S)
+    prompt = np.random.default_rng(12).integers(0, cfg.n_vocab, 21).astype(np.int32)
+    n_gen = 8
+    print(f"fused norm i8 dtype {dtype}", flush=True)
+    tc, _, kc, vc = model.cpu_generate(prompt, n_gen, act=ACT_I8)
+    s = torch.cuda.Stream()
+    dev = model.device(n_batch=16, act=ACT_I8, stream=s.cuda_stream, fused=True)
+    try:
+        tg, _, kg, vg = dev.generate_graph(prompt, n_gen, stream=s)
+        dev.set_fused_norm(False)
+        tu, hu, ku, vu = dev.generate(prompt, n_gen)
+        dev.set_fused_norm(True)
+        tf, hf, kf, vf = dev.generate(prompt, n_gen)
+    finally:
+        dev.free()
+    assert np.array_equal(tu, tc) and np.array_equal(tf, tc) and np.array_equal(tg, tc), (tf, tc)
+    assert np.array_equal(hf, hu), np.argwhere(hf != hu)[:5]
+    assert np.array_equal(kf, ku) and np.array_equal(vf, vu) and np.array_equal(kg, kf) and np.array_equal(vg, vf)
+    assert np.array_equal(kf, kc) and np.array_equal(vf, vc)
+
+
 def test_forward_dev_graph_replay(N):
     # nngl_forward_dev allocates nothing: one prefill captured in a HIP graph
     # and replayed (eager work between replays) gives the eager hidden states.
