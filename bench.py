@@ -782,6 +782,44 @@ def decode_leg(N, path, dtype, cpu: bool):
     return out
 
 
+def fused_norm(args, N):
+    """The residual add and RMSNorm fused into the next matmul's prologue
+    (nnh_gemv_rmsnorm_act_dev) at the Qwen2.5-7B decode's q / k / v and
+    gate / up shapes, per launch beside the plain matmul on an input formed
+    beforehand (f32: nnh_gemv_batch_dev; int8: nnh_gemv_act_dev on
+    activations quantized beforehand): the difference is what the norm
+    costs inside the matmul's launch."""
+    import torch
+    st = Stream()
+    out = []
+    for ci, (dtype, n, k) in enumerate((d, n, k) for d in (1, 2) for n, k in ((4608, 3584), (18944 * 2, 3584))):
+        for act in (N.ACT_F32, N.ACT_I8):
+            launch = rotating(N, st, dtype, n, k, 1, act, 0x5EED40 + 7 * ci + dtype)
+            ws, x, y, _ = launch.keep
+            r = torch.randn(k, device="cuda")
+            g = 1.0 + 0.1 * torch.randn(k, device="cuda")
+            xo = torch.zeros(k, device="cuda")
+            normed = torch.zeros(k, device="cuda")
+            state = {"i": 0}
+
+            def fused(ws=ws, x=x, y=y, r=r, g=g, xo=xo, normed=normed, act=act, state=state):
+                w = ws[state["i"] % len(ws)]
+                state["i"] += 1
+                N.gemv_rmsnorm_dev(w, x.data_ptr(), r.data_ptr(), g.data_ptr(), 1e-6, xo.data_ptr(), 0,
+                                   normed.data_ptr(), y.data_ptr(), st.handle, act=act)
+            fused.copies = launch.copies
+            torch.cuda.synchronize()
+            plain, _ = per_launch(st, launch, args.steps, args.warmup)
+            both, reps = per_launch(st, fused, args.steps, args.warmup)
+            e = dict(case=case_name(dtype, n, k, 1), act="f32" if act == N.ACT_F32 else "i8",
+                     plain_us=round(plain * 1e6, 3), fused_us=round(both * 1e6, 3), launches=reps)
+            log(f"fused_norm: {e}")
+            out.append(e)
+            del launch, fused
+            torch.cuda.synchronize()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -789,7 +827,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "qwen_decode", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "bf16", "peaks", "traffic", "all"])
+                             "bf16", "peaks", "traffic", "fused_norm", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -846,6 +884,8 @@ def main():
     if args.workload in ("decode_f32", "all"):
         extra["decode_f32_bit_exact"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in GEMMA_DECODE],
                                                       N.ACT_F32, "decode_f32")
+    if args.workload in ("fused_norm", "all"):
+        extra["fused_norm"] = fused_norm(args, N)
     if args.workload in ("bf16", "all"):
         extra["bf16_bit_exact"] = measure_cases(args, N, [(3, n, k, m) for n, k in BF16_SHAPES for m in (1, 4)],
                                                 N.ACT_F32, "bf16")
