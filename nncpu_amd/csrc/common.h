@@ -82,6 +82,19 @@ __device__ __forceinline__ void wait_vm_keep() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(K) : "memory");
 }
 
+// One 1 KB copy of the bytes [off, off + 1024) of a span of `len` bytes
+// (a multiple of 16) to dst (uniform); lanes past the end repeat the span's
+// last 16 bytes. Issued as asm: for the builtin the compiler cannot tell
+// the copy's LDS destination from any later LDS read and waits for every
+// copy before each read, which would undo the staging (the waits here are
+// explicit instead).
+__device__ __forceinline__ void copy_1k(const void* span, size_t len, size_t off, unsigned char* dst, int lane) {
+    const size_t o = min(off + lane * 16, len - 16);
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const unsigned char*)span + o),
+                 "{m0}"((uint32_t)(uintptr_t)dst)
+                 : "memory");
+}
+
 // Compute units of the current device (kernels_misc.hip).
 int cu_count();
 

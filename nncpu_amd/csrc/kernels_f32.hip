@@ -454,19 +454,6 @@ __device__ __forceinline__ void wait_vm_upto4(int n) {
         __builtin_amdgcn_s_waitcnt(NNH_VMCNT(4));
 }
 
-// One 1 KB copy of the bytes [off, off + 1024) of a span of `len` bytes
-// (a multiple of 16) to dst (uniform); lanes past the end repeat the span's
-// last 16 bytes. Issued as asm: for the builtin the compiler cannot tell
-// the copy's LDS destination from any later LDS read and waits for every
-// copy before each read, which would undo the staging (the waits here are
-// explicit instead).
-__device__ __forceinline__ void copy_1k(const void* span, size_t len, size_t off, unsigned char* dst, int lane) {
-    const size_t o = min(off + lane * 16, len - 16);
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((const unsigned char*)span + o),
-                 "{m0}"((uint32_t)(uintptr_t)dst)
-                 : "memory");
-}
-
 // One group of a lane's chain: the 16-byte piece, G values of x (row-major
 // x, element j: stride 32) and G f32 scales, all from LDS.
 template <int DT>

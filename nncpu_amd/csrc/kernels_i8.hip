@@ -585,7 +585,8 @@ __global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __re
     }
     __syncthreads();
     if (tid < 64) {
-        const double ss = rms_sumsq_t(xt, cols, tid);
+        // Shorter read batches where the chunk's registers are larger.
+        const double ss = rms_sumsq_t<BPL == 2 ? 8 : 4>(xt, cols, tid);
         if (tid == 0) nsc = rms_scale(ss, cols, nrm.eps);
     }
     __syncthreads();
@@ -644,13 +645,15 @@ void launch_i8n(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const
     gemv_i8_norm_kernel<DT, R, BPL, K4, V2RED><<<grid, I8N_T, lds, st>>>(qs, sc, sb, rows, nb, y, nrm);
 }
 
-template <int DT, int K4, bool V2RED>
+// A row is one chunk: 128 blocks (up to 128-block rows, one piece per
+// thread) or 256 blocks (two pieces, one row per group).
+template <int DT, bool V2RED>
 void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const NormIn& nrm, int rows, int nb,
                    float* y, hipStream_t st) {
     if (nb <= 128)
-        launch_i8n<DT, DT == 1 ? 1 : 2, 2, K4, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+        launch_i8n<DT, DT == 1 ? 1 : 2, 2, 1, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
     else
-        launch_i8n<DT, DT == 1 ? 1 : 2, 4, K4, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+        launch_i8n<DT, 1, 4, 2, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
 }
 
 }  // namespace
@@ -695,19 +698,13 @@ bool launch_gemv_i8_norm(int dtype, const uint8_t* qs, const uint16_t* scales, c
     if (!aligned(nrm.x) || !aligned(nrm.gamma) || !aligned(nrm.r) || !aligned(nrm.x_out) || !aligned(nrm.rec))
         return false;
     const bool v2red = nb % 64 == 0;  // the plain GEMV's kernel at this row length
-#define NNH_N(DT, K4)                                                            \
-    do {                                                                         \
-        if (v2red)                                                               \
-            launch_i8n_dt<DT, K4, true>(qs, scales, sb, nrm, rows, nb, y, st);   \
-        else                                                                     \
-            launch_i8n_dt<DT, K4, false>(qs, scales, sb, nrm, rows, nb, y, st);  \
-    } while (0)
     if (dtype == 1) {
-        if (nb <= 128) NNH_N(1, 1); else NNH_N(1, 2);
+        if (v2red) launch_i8n_dt<1, true>(qs, scales, sb, nrm, rows, nb, y, st);
+        else launch_i8n_dt<1, false>(qs, scales, sb, nrm, rows, nb, y, st);
     } else {
-        if (nb <= 128) NNH_N(2, 1); else NNH_N(2, 2);
+        if (v2red) launch_i8n_dt<2, true>(qs, scales, sb, nrm, rows, nb, y, st);
+        else launch_i8n_dt<2, false>(qs, scales, sb, nrm, rows, nb, y, st);
     }
-#undef NNH_N
     return true;
 }
 
