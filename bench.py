@@ -386,6 +386,8 @@ def peaks(args):
 
 QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
 VERIFY_SHAPES = [(6144, 1536), (1536, 6144), (2048, 1536), (1536, 1536)]
+I8_M1_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096), (4608, 3584), (3584, 3584),
+                (37888, 3584), (3584, 18944)]
 GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912), (262144, 1152)]
 # BF16 weights: the reference's own BF16 test shapes (Gemma E2B/E4B, kernels/tests.rs:435-447) and
 # Llama-3-8B projections.
@@ -827,7 +829,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "qwen_decode", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "bf16", "peaks", "traffic", "fused_norm", "all"])
+                             "bf16", "peaks", "traffic", "fused_norm", "i8_m1", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -886,6 +888,12 @@ def main():
                                                       N.ACT_F32, "decode_f32")
     if args.workload in ("fused_norm", "all"):
         extra["fused_norm"] = fused_norm(args, N)
+    if args.workload in ("i8_m1", "all"):
+        # The one-vector int8 GEMV at Llama-3-8B's and Qwen2.5-7B's matrices,
+        # both formats (the staged grid-stride kernel takes the Q8 4096- and
+        # 14336-column shapes and both 18944-column ones).
+        extra["i8_m1"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in I8_M1_SHAPES], N.ACT_I8,
+                                       "i8_m1")
     if args.workload in ("bf16", "all"):
         extra["bf16_bit_exact"] = measure_cases(args, N, [(3, n, k, m) for n, k in BF16_SHAPES for m in (1, 4)],
                                                 N.ACT_F32, "bf16")

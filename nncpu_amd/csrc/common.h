@@ -75,11 +75,15 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // in issue order), and no memory access moves across it. A kernel that
 // issues direct-to-LDS copies and then K register loads waits for the copies
 // alone with it; K must not exceed the number of load instructions issued
-// after the copies.
+// after the copies. The base pointers of those K loads are passed in (a, b,
+// c): loads through a __restrict__ argument are otherwise free to move
+// across a "memory" clobber, and sunk below the wait they would leave copies
+// in flight.
 template <int K>
-__device__ __forceinline__ void wait_vm_keep() {
+__device__ __forceinline__ void wait_vm_keep(const void* a = nullptr, const void* b = nullptr,
+                                             const void* c = nullptr) {
     static_assert(K >= 0 && K <= 63, "vmcnt holds 0..63");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(K) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(K), "s"(a), "s"(b), "s"(c) : "memory");
 }
 
 // One 1 KB copy of the bytes [off, off + 1024) of a span of `len` bytes

@@ -814,7 +814,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     // The copies have landed once at most the slots' loads are in flight
     // (per slot: the quant piece, the scales unless staged, Q4's two
     // biases); the norm and the block sums run while the slots fill.
-    wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>();
+    wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>(m.fq, m.fs, m.bi);
     __syncthreads();
     if (NORM)
         norm_prologue<NT, 32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
@@ -1145,7 +1145,7 @@ __global__ __launch_bounds__(256) void gemv_f32_v2_kernel(const uint8_t* __restr
         for (size_t c = wave; c * 1024 < xlen; c += 4) copy_1k(second, xlen, c * 1024, l8 + xb + c * 1024, lane);
 #pragma unroll
         for (int d = 0; d < PF0; ++d) v2_load<DT, R>(slot[d], qrow, srow, d < ng ? d : ng - 1);
-        wait_vm_keep<PF0 * 2 * R>();  // per group and row: the quant piece and the scales
+        wait_vm_keep<PF0 * 2 * R>(fq, fs);  // per group and row: the quant piece and the scales
         __syncthreads();
         for (int i = 4 * tid; i < cols; i += 4 * 256) {
             float4 a = *(const float4*)(xl + i);

@@ -656,6 +656,138 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
         launch_i8n<DT, 1, 4, 2, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
 }
 
+
+// ---- int8 GEMV, one vector, activations staged in LDS, grid-stride rows -----
+//
+// Rows of 64-lane groups where the plain launch shapes below are weakest:
+// Q8 rows of whole 64-block groups in tall matrices (8192+ rows) or of 256+
+// blocks, Q4 rows of 257+ blocks that are not whole groups (3584+ rows).
+// Measured against the plain path on one box, alternating (medians of 5):
+// Q8 14336x4096 18.0 -> 13.5 us, 4096x14336 13.7 -> 12.7, Q4 3584x18944
+// 11.9 -> 9.5; at Q8 4096-6144 rows of 128-192 blocks and Q8 3584x18944
+// the two were within 0.6 us either way, so those stay plain. Two
+// workgroups of 16 waves per CU; each copies the quantized activations
+// (the quants and the (scale, scale * sum) pairs) into LDS once, then each
+// wave takes rows grid-stride, chunks of 128 blocks with the next chunk's
+// weights in flight. A lane sums blocks l, l + 64, ... in order and the
+// lanes are reduced with the tree of the kernel the plain path would take
+// (V2RED), so the bits are the plain path's.
+constexpr int I8L_T = 1024;
+template <int DT, bool V2RED>
+__global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __restrict__ qs,
+                                                            const uint16_t* __restrict__ sc,
+                                                            const uint32_t* __restrict__ sb,
+                                                            const int8_t* __restrict__ aq,
+                                                            const double* __restrict__ asx, int rows, int nb,
+                                                            float* __restrict__ y) {
+    constexpr int QV = DT == 1 ? 2 : 1;
+    constexpr int BPL = 2, STEP = 64 * BPL, NW = I8L_T / 64;
+    extern __shared__ __align__(16) unsigned char i8l_smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t cols = (size_t)nb * 32, qrow_bytes = DT == 1 ? cols : cols / 2;
+    int8_t* xq = (int8_t*)i8l_smem;
+    double2* xsx = (double2*)(i8l_smem + ((cols + 1023) & ~(size_t)1023));
+    for (size_t c = wave; c * 1024 < cols; c += NW) copy_1k(aq, cols, c * 1024, (unsigned char*)xq + c * 1024, lane);
+    for (size_t c = wave; c * 1024 < (size_t)nb * 16; c += NW)
+        copy_1k(asx, (size_t)nb * 16, c * 1024, (unsigned char*)xsx + c * 1024, lane);
+
+    struct Chunk {
+        int4 w[BPL][QV];
+        uint32_t s[BPL];
+    };
+    const int gstep = gridDim.x * NW;
+    auto load = [&](Chunk& k, int row, int c0) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int braw = c0 + lane + 64 * i;
+            const size_t b = braw < nb ? braw : nb - 1;  // in bounds; skipped by run
+            const int4* wp = (const int4*)(qs + (size_t)row * qrow_bytes + (DT == 1 ? 32 : 16) * b);
+#pragma unroll
+            for (int v = 0; v < QV; ++v) k.w[i][v] = load_nt16(wp + v);
+            k.s[i] = DT == 1 ? (uint32_t)sc[(size_t)row * nb + b] : sb[(size_t)row * nb + b];
+        }
+    };
+    double acc = 0.0;
+    // gemv_i8_kernel's block term order: the scaled dot, then (Q4) the bias term.
+    auto run = [&](const Chunk& k, int c0) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = c0 + lane + 64 * i;
+            if (b >= nb) continue;
+            const int4 x0 = ((const int4*)(xq + 32 * b))[0], x1 = ((const int4*)(xq + 32 * b))[1];
+            const double2 sx = xsx[b];
+            const double sw = (double)bf16f(k.s[i] & 0xffffu);
+            const int P = DT == 1 ? dot_q8(k.w[i][0], k.w[i][QV - 1], x0, x1) : dot_q4(k.w[i][0], x0, x1);
+            acc = __builtin_fma(sw * sx.x, (double)P, acc);
+            if (DT == 2) acc = __builtin_fma((double)bf16f(k.s[i] >> 16), sx.y, acc);
+        }
+    };
+    auto finish = [&](int row) {
+        double v = acc;
+        if (V2RED) {
+            v = group_sum_f64<64>(v);
+        } else {
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v += xor_get(v, m);
+        }
+        if (lane == 0) y[row] = (float)v;
+        acc = 0.0;
+    };
+
+    const int r0 = blockIdx.x * NW + wave;
+    Chunk A, B;
+    // Unconditional (a wave past the last row rereads it, unused), so the
+    // wait below counts these loads exactly; the copies land first.
+    load(A, r0 < rows ? r0 : rows - 1, 0);
+    wait_vm_keep<BPL * (QV + 1)>(qs, DT == 1 ? (const void*)sc : (const void*)sb);
+    __syncthreads();
+    if (r0 >= rows) return;
+    // Items (row, chunk) in order; A holds the current item's weights, B
+    // the next one's, then the roles swap.
+    int ra = r0, ca = 0;
+    while (true) {
+        int rb = ra, cb = ca + STEP;
+        if (cb >= nb) {
+            cb = 0;
+            rb += gstep;
+        }
+        const bool hb = rb < rows;
+        if (hb) load(B, rb, cb);
+        run(A, ca);
+        if (ca + STEP >= nb) finish(ra);
+        if (!hb) break;
+        int rc = rb, cc = cb + STEP;
+        if (cc >= nb) {
+            cc = 0;
+            rc += gstep;
+        }
+        const bool hc = rc < rows;
+        if (hc) load(A, rc, cc);
+        run(B, cb);
+        if (cb + STEP >= nb) finish(rb);
+        if (!hc) break;
+        ra = rc;
+        ca = cc;
+    }
+}
+
+constexpr int I8L_WG_PER_CU = 2;
+
+// The shapes where the staged kernel measured faster (the plain path runs
+// 64 lanes per row at all of them, so the lane order is the same).
+bool i8_lds_shape(int dtype, int rows, int nb) {
+    if (dtype == 1) return nb % 64 == 0 && nb >= 128 && (rows >= 8192 || (nb >= 256 && rows >= 3584));
+    return nb > 256 && nb % 64 != 0 && rows >= 3584;
+}
+
+template <int DT, bool V2RED>
+void launch_i8_lds(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
+                   int rows, int nb, float* y, hipStream_t st) {
+    const int want = ceil_div(rows, I8L_T / 64), cap = I8L_WG_PER_CU * cu_count();
+    const int grid = want < cap ? want : cap;
+    const size_t lds = (((size_t)nb * 32 + 1023) & ~(size_t)1023) + (((size_t)nb * 16 + 1023) & ~(size_t)1023);
+    gemv_i8_lds_kernel<DT, V2RED><<<grid, I8L_T, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y);
+}
 }  // namespace
 
 void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st) {
@@ -671,6 +803,19 @@ void launch_quantize_act(const float* x, size_t x_stride, int cols, int n_tok, i
 void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const uint32_t* sb,
                     const int8_t* aq, const double* asx, int rows, int nb, int n_tok, float* y, size_t y_stride,
                     hipStream_t st) {
+    // One vector at the staged kernel's shapes (x and its pairs in LDS: up
+    // to 32768 columns).
+    if (n_tok == 1 && i8_lds_shape(dtype, rows, nb) && nb * 32 <= 32768 && (dtype == 1 || sb)) {
+        const bool v2red = nb % 64 == 0;  // the plain path's kernel at this row length: its lane tree
+        if (dtype == 1) {
+            if (v2red) launch_i8_lds<1, true>(qs, scales, sb, aq, asx, rows, nb, y, st);
+            else launch_i8_lds<1, false>(qs, scales, sb, aq, asx, rows, nb, y, st);
+        } else {
+            if (v2red) launch_i8_lds<2, true>(qs, scales, sb, aq, asx, rows, nb, y, st);
+            else launch_i8_lds<2, false>(qs, scales, sb, aq, asx, rows, nb, y, st);
+        }
+        return;
+    }
     const size_t cols = (size_t)nb * 32;
     for (int t0 = 0; t0 < n_tok; t0 += 4) {
         int m = n_tok - t0 < 4 ? n_tok - t0 : 4;

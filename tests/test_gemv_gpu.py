@@ -505,6 +505,36 @@ def test_i8_within_tolerance_of_reference(oracle, dtype, rows, cols, n_tok):
             assert np.all(np.abs(got - exact) <= np.spacing(np.abs(exact)))
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (1, 8200, 4096), (1, 8192, 6144), (1, 3600, 8192), (1, 4096, 14336), (1, 9000, 4096), (1, 3584, 10240),
+    (2, 3584, 9216), (2, 3584, 18944), (2, 5000, 8224),
+])
+def test_i8_staged_kernel_shapes(oracle, dtype, rows, cols):
+    # One vector at the shapes of the int8 kernel with the activations staged
+    # in LDS and rows taken grid-stride (Q8 rows of whole 64-block groups at
+    # 8192+ rows or of 256+ blocks; Q4 rows of 257+ blocks that are not whole
+    # groups; both lane trees, ragged grids and chunks): within
+    # one ulp of the oracle's exact sum of the exact block terms; against
+    # nncpu's kernel fed x', within 1e-5 except where nncpu's own f32 chains
+    # are farther from the exact sum than this kernel (as the config-5 test
+    # counts them: at K = 18944 nncpu is up to ~1.6e-5 from exact).
+    say("i8 staged", dtype, rows, cols)
+    rng = oracle.Rng(0x57A6 + rows + cols + dtype)
+    m = oracle.QMatrix.from_f32(dtype, rng.normals(rows * cols, 0.02).reshape(rows, cols))
+    w = upload(m)
+    x = rng.normals(cols, 1.0)
+    got = N.model_gemv(w, x, act=N.ACT_I8)
+    qx, sx = oracle.quantize_act(x)
+    exact = oracle.gemv_i8_exact(m, qx, sx)
+    assert np.all(np.abs(got - exact) <= np.spacing(np.abs(exact)))
+    ref = oracle.gemv_batch(m, oracle.dequant_act(qx, sx))
+    over = np.abs(got - ref) > 1e-5
+    print(f"above 1e-5 against nncpu: {int(over.sum())} of {rows}, max {np.abs(got - ref).max():.3g}")
+    assert np.all(np.abs(got - exact)[over] < np.abs(ref - exact)[over].astype(np.float64))
+    assert np.linalg.norm(got - ref) <= 1e-3 * np.linalg.norm(ref)
+    w.free()
+
+
 def i8_abs_terms(oracle, m, qx, sx):
     """sum_b |s_w s_x P_b| (+ |bias s_x sum q_x| for Q4) per row, in f64."""
     nb = m.cols // 32
