@@ -193,7 +193,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
 // The same computation with three changes for short launches: the chunk
 // loop has no tail (nb is a multiple of LPR*BPL, checked by the launcher),
 // Q4 scale and bias come as one packed 32-bit word per block (`sb`,
-// scale | bias << 16, built at upload), and the lane sum uses DPP.
+// scale | bias << 16, built at upload), and the lane sum uses DPP. One
+// vector in one chunk reads its activations from an LDS copy.
 template <int DT, int M, int R, int LPR, int BPL, bool PF>
 __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restrict__ qs,
                                                          const uint16_t* __restrict__ sc,
@@ -279,6 +280,50 @@ __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restri
             run(B);
         }
         if (c0 < nb) run(A);
+    } else if constexpr (M == 1) {
+        // One vector, one chunk (the launcher's shapes without PF): the
+        // activations are copied to LDS once per workgroup (direct-to-LDS
+        // loads, then the chunk's weight requests, then a wait for the
+        // copies alone), so the lanes' activation reads stay off the
+        // texture path that the weight stream uses.
+        extern __shared__ __align__(16) unsigned char v2_smem[];
+        const size_t xq_bytes = (cols + 1023) & ~(size_t)1023;
+        {
+            const int wave = threadIdx.x >> 6, ln = threadIdx.x & 63;
+            for (size_t c = wave; c * 1024 < cols; c += 4) copy_1k(aq, cols, c * 1024, v2_smem + c * 1024, ln);
+            for (size_t c = wave; c * 1024 < (size_t)nb * 16; c += 4)
+                copy_1k(asx, (size_t)nb * 16, c * 1024, v2_smem + xq_bytes + c * 1024, ln);
+        }
+        int4 w[R][BPL][QV];
+        uint32_t s[R][BPL];
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const size_t b = lane + i * LPR;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int4* wp = (const int4*)(qs + (size_t)rr[r] * qrow_bytes + (DT == 1 ? 32 : 16) * b);
+#pragma unroll
+                for (int v = 0; v < QV; ++v) w[r][i][v] = load_nt16(wp + v);
+                s[r][i] = DT == 1 ? (uint32_t)sc[(size_t)rr[r] * nb + b] : sb[(size_t)rr[r] * nb + b];
+            }
+        }
+        wait_vm_keep<R * BPL * (QV + 1)>(qs, DT == 1 ? (const void*)sc : (const void*)sb);
+        __syncthreads();
+        const int8_t* xq = (const int8_t*)v2_smem;
+        const double2* xsx = (const double2*)(v2_smem + xq_bytes);
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const size_t b = lane + i * LPR;
+            const int4 x0 = ((const int4*)(xq + 32 * b))[0], x1 = ((const int4*)(xq + 32 * b))[1];
+            const double2 sx = xsx[b];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const double sw = (double)bf16f(s[r][i] & 0xffffu);
+                const int P = DT == 1 ? dot_q8(w[r][i][0], w[r][i][QV - 1], x0, x1) : dot_q4(w[r][i][0], x0, x1);
+                acc[r][0] = __builtin_fma(sw * sx.x, (double)P, acc[r][0]);
+                if (DT == 2) acc[r][0] = __builtin_fma((double)bf16f(s[r][i] >> 16), sx.y, acc[r][0]);
+            }
+        }
     } else {
         for (int c0 = 0; c0 < nb; c0 += STEP) {
             int4 w[R][BPL][QV];
@@ -420,12 +465,16 @@ template <int DT, int M, int R, int LPR, int BPL>
 void launch_v2(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
                int rows, int nb, float* y, size_t ys, hipStream_t st) {
     constexpr int rows_per_wg = 4 * (64 / LPR) * R;
-    if (nb > LPR * BPL)
+    if (nb > LPR * BPL) {
         gemv_i8_v2_kernel<DT, M, R, LPR, BPL, true>
             <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
-    else
+    } else {
+        // One vector: the activation copy in LDS (quants, then the pairs).
+        const size_t lds = M == 1 ? (((size_t)nb * 32 + 1023) & ~(size_t)1023) + (((size_t)nb * 16 + 1023) & ~(size_t)1023)
+                                  : 0;
         gemv_i8_v2_kernel<DT, M, R, LPR, BPL, false>
-            <<<ceil_div(rows, rows_per_wg), 256, 0, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
+            <<<ceil_div(rows, rows_per_wg), 256, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, ys);
+    }
 }
 
 // Launch shape from the measured sweep (Llama-3-8B and vocab shapes): 64
