@@ -719,6 +719,70 @@ __device__ __forceinline__ void decode_qkv_rows(const QkvArgs& a, float* rows, i
     __syncthreads();
 }
 
+// decode_qkv_rows with its global reads issued first and consumed later, so
+// a caller can put further loads (the K/V rows) in flight between them: the
+// row's values with their bias and the RoPE coefficients at p0, loaded by
+// every lane of every wave unconditionally (a wave without a row rereads the
+// q head's; indices clamped), so the waits count them exactly.
+template <int HD>
+struct QkvRegs {
+    static constexpr int NV = (HD + 63) / 64, NR = (HD / 2 + 63) / 64;
+    float x[NV], b[NV], c[NR], s[NR];
+};
+template <int HD>
+__device__ __forceinline__ void decode_qkv_issue(const QkvArgs& a, QkvRegs<HD>& g, int qh, int kvh, int p0, int wave,
+                                                 int lane) {
+    const int kind = wave < 3 ? wave : 0;
+    const int off = kind == 0 ? qh * HD : (kind == 1 ? a.H * HD + kvh * HD : a.H * HD + a.KV * HD + kvh * HD);
+    const float* bsrc = a.bias ? a.bias : a.qkv;  // a dummy read without biases, unused
+#pragma unroll
+    for (int k = 0; k < QkvRegs<HD>::NV; ++k) {
+        const int i = lane + 64 * k < HD ? lane + 64 * k : HD - 1;
+        g.x[k] = a.qkv[off + i];
+        g.b[k] = bsrc[off + i];
+    }
+    const int half = HD / 2, pr = p0 < a.n_ctx ? p0 : a.n_ctx - 1;
+#pragma unroll
+    for (int k = 0; k < QkvRegs<HD>::NR; ++k) {
+        const int i = lane + 64 * k < half ? lane + 64 * k : half - 1;
+        g.c[k] = a.cs[(size_t)pr * half + i];
+        g.s[k] = a.sn[(size_t)pr * half + i];
+    }
+}
+template <int HD>
+__device__ __forceinline__ void decode_qkv_finish(const QkvArgs& a, const QkvRegs<HD>& g, float* rows, bool own,
+                                                  int wave, int lane) {
+    const int kind = wave < 3 ? wave : 3;
+    const bool act = kind == 0 || (kind < 3 && own);
+    float* v = rows + kind * HD;
+    // Stored by every wave (wave 3 into a row of its own, never read), so the
+    // loads' only use is not under a branch the compiler could sink them into.
+#pragma unroll
+    for (int k = 0; k < QkvRegs<HD>::NV; ++k)
+        if (lane + 64 * k < HD) v[lane + 64 * k] = a.bias ? __fadd_rn(g.x[k], g.b[k]) : g.x[k];
+    __syncthreads();
+    const float* gm = kind == 0 ? a.qn : a.kn;
+    if (act && kind < 2 && gm) {
+        const float sc = rms_of_d(row_sumsq(v, HD, lane), HD, a.eps);
+        for (int i = lane; i < HD; i += 64) v[i] = __fmul_rn(__fmul_rn(v[i], sc), gm[i]);
+    }
+    __syncthreads();
+    if (act && kind < 2) {
+        const int half = HD / 2;
+        const int stride = a.rope_mode == NNG_ROPE_NORM ? 2 : 1, partner = a.rope_mode == NNG_ROPE_NORM ? 1 : half;
+#pragma unroll
+        for (int k = 0; k < QkvRegs<HD>::NR; ++k) {
+            const int i = lane + 64 * k;
+            if (i >= half) continue;
+            const int p = i * stride;
+            const float x0 = v[p], x1 = v[p + partner], c = g.c[k], sv = g.s[k];
+            v[p] = __fsub_rn(__fmul_rn(c, x0), __fmul_rn(sv, x1));
+            v[p + partner] = __fadd_rn(__fmul_rn(sv, x0), __fmul_rn(c, x1));
+        }
+    }
+    __syncthreads();
+}
+
 // One token's partial (decode) for query head x of KV head y over its block
 // b0 + z: attn_tile_kernel's arithmetic for a single row, spread over more
 // workgroups (one per head and block) for latency: the block's K and V rows
@@ -749,7 +813,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     float* sc = lds;                                   // [256]
     uint16_t* kv = (uint16_t*)(lds + ATTN_BLOCK + 4);  // [256][KS]
     __shared__ float mh, lsh;
-    __shared__ __align__(16) float rows[3][HD];  // the token's q head, k and v rows
+    __shared__ __align__(16) float rows[4][HD];  // the token's q head, k and v rows (and a spare)
     const int hh = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.G, pw = HD + 2, KVD = a.KV * HD;
     int p0, n_seq, first, last;
@@ -770,12 +834,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     // is (a position past the context lies in no block).
     const bool own = p0 >= k0 && p0 <= k1;
     if constexpr (KV2) {
-        decode_qkv_rows<HD>(qa, &rows[0][0], kvh * G + hh, kvh, own, p0, wave, lane);
-        uint4 rk[U], rv[U];
-        kv_load<HD, U>(rk, a.kc, k0, nk, KVD, kvh, tid, 0);
-        kv_load<HD, U>(rv, a.vc, k0, nk, KVD, kvh, tid, 0);
-        kv_store<HD, U>(rk, kv, tid, 0);
-        kv_store<HD, U>(rv, vv, tid, 0);
+        // The q / k / v rows' reads, then the block's K and V rows', all in
+        // flight together (one round trip); the K / V rows are stored to LDS
+        // before the q / k / v rows are formed, so their registers are free
+        // again by then.
+        QkvRegs<HD> g;
+        decode_qkv_issue<HD>(qa, g, kvh * G + hh, kvh, p0, wave, lane);
+        {
+            uint4 rk[U], rv[U];
+            kv_load<HD, U>(rk, a.kc, k0, nk, KVD, kvh, tid, 0);
+            kv_load<HD, U>(rv, a.vc, k0, nk, KVD, kvh, tid, 0);
+            kv_store<HD, U>(rk, kv, tid, 0);
+            kv_store<HD, U>(rv, vv, tid, 0);
+        }
+        decode_qkv_finish<HD>(qa, g, &rows[0][0], own, wave, lane);
     } else {
         decode_qkv_rows<HD>(qa, &rows[0][0], kvh * G + hh, kvh, own, p0, wave, lane);
 #pragma unroll
@@ -831,11 +903,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     if (tid < nk) sc[tid] = exp_lane(__fsub_rn(sc[tid], mh));
     __syncthreads();
     float* part = a.parts + ((size_t)kvh * a.nblk + blockIdx.z) * G * pw + hh * pw;
-    if (wave == 0) {
+    // The weight sum (lanes 0..7 over the keys in order, hsum8, then the
+    // tail): before the V chain at head_dim 256, which takes every thread;
+    // up to 128 by wave 3 while waves 0-1 run the V chain.
+    auto weight_sum = [&]() {
         const int body = nk & ~7;
+        float t[ATTN_BLOCK / 8];
+        if (lane < 8) {
+#pragma unroll
+            for (int k = 0; k < ATTN_BLOCK / 8; ++k) t[k] = sc[lane + 8 * k < body ? lane + 8 * k : 0];
+        }
         float vs = 0.0f;
-        if (lane < 8)
-            for (int j = lane; j < body; j += 8) vs = __fadd_rn(vs, sc[j]);
+        if (lane < 8) {
+#pragma unroll
+            for (int k = 0; k < ATTN_BLOCK / 8; ++k)
+                if (lane + 8 * k < body) vs = __fadd_rn(vs, t[k]);
+        }
         float ls = hsum8_lanes(vs);
         if (lane == 0) {
             for (int j = body; j < nk; ++j) ls = __fadd_rn(ls, sc[j]);
@@ -843,7 +926,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             part[HD + 1] = ls;
             lsh = ls;
         }
-    }
+    };
+    if (!KV2 && wave == 0) weight_sum();
     if constexpr (!KV2) {
         // The K rows were last read before the barrier after the scores.
 #pragma unroll
@@ -856,38 +940,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             __syncthreads();
             for (int i = tid; i < HD; i += 256) kv[(p0 - k0) * KS + i] = to_bf16(rows[2][i]);
         }
+        __syncthreads();
     }
-    __syncthreads();
+    float o = -0.0f;
     if (tid < HD) {
         // Keys in order, 8 per step; the next step's LDS reads are issued
-        // before this step's FMAs (two named buffers, no copies).
-        float o = -0.0f;
+        // before this step's FMAs (two named buffers, no copies; the reads
+        // are unconditional, clamped to the last whole step, and kept ahead
+        // of the FMAs by scheduling barriers).
         const int body = nk & ~7;
         const uint16_t* vc = vv + tid;
         int j = 0;
         if (body) {
-            V8 a, b;
-            a.load<KS>(sc, vc, 0);
+            V8 va, vb;
+            va.load<KS>(sc, vc, 0);
             for (; j + 16 <= body; j += 16) {
-                b.load<KS>(sc, vc, j + 8);
-                o = a.fma(o);
-                if (j + 16 < body) a.load<KS>(sc, vc, j + 16);
-                o = b.fma(o);
+                vb.load<KS>(sc, vc, j + 8);
+                __builtin_amdgcn_sched_barrier(0);
+                o = va.fma(o);
+                va.load<KS>(sc, vc, j + 16 < body ? j + 16 : body - 8);
+                __builtin_amdgcn_sched_barrier(0);
+                o = vb.fma(o);
             }
             if (j < body) {
-                o = a.fma(o);
+                o = va.fma(o);
                 j += 8;
             }
         }
         for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(vv[j * KS + tid]), o);
+    } else if (KV2 && wave == 3) {
+        weight_sum();
+    }
+    if constexpr (KV2) __syncthreads();  // lsh
+    if (tid < HD) {
         if (direct) {
             // attn_merge_kernel with one partial: o * (1 / l).
             const float al = lsh;
             const float inv = al > 0.0f ? __fdiv_rn(1.0f, al) : 0.0f;
             const float v = __fmul_rn(o, inv);
-            const int j = (kvh * G + hh) * HD + tid;
-            a.out[j] = v;
-            if (qo.q) q8_value(v, j, qo);
+            const int jo = (kvh * G + hh) * HD + tid;
+            a.out[jo] = v;
+            if (qo.q) q8_value(v, jo, qo);
         } else {
             part[tid] = o;
         }
