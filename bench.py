@@ -822,6 +822,50 @@ def fused_norm(args, N):
     return out
 
 
+I8_PROLOGUE_SHAPES = [(4608, 3584), (3584, 3584), (1024, 4096), (14336, 4096), (4096, 8192), (3584, 9216),
+                      (4096, 14336), (37888, 3584), (3584, 18944)]
+
+
+def i8_prologue(args, N):
+    """One f32 vector through nnh_gemv_batch_dev(..., NNH_ACT_I8), which
+    quantizes x in the int8 GEMV's prologue at rows of 97..384 blocks (not
+    tall Q8 matrices of rows that are not whole 64-block groups), per launch
+    beside the two launches it replaces (the library quantizer, then
+    nnh_gemv_act_dev) and the GEMV alone on activations quantized
+    beforehand."""
+    import torch
+    st = Stream()
+    out = []
+    for ci, (dtype, n, k) in enumerate((d, n, k) for d in (1, 2) for n, k in I8_PROLOGUE_SHAPES):
+        launch = rotating(N, st, dtype, n, k, 1, N.ACT_I8, 0x5EED90 + 7 * ci + dtype)
+        ws, x, y, buf = launch.keep
+        state = {"i": 0}
+
+        def one(ws=ws, x=x, y=y, n=n, k=k, state=state):
+            w = ws[state["i"] % len(ws)]
+            state["i"] += 1
+            N.gemv_batch_dev(w, x.data_ptr(), k, y.data_ptr(), n, 1, N.ACT_I8, st.handle)
+
+        def two(ws=ws, x=x, y=y, buf=buf, n=n, k=k, state=state):
+            w = ws[state["i"] % len(ws)]
+            state["i"] += 1
+            N.quantize_act_dev(x.data_ptr(), k, k, 1, buf.data_ptr(), st.handle)
+            N.gemv_act_dev(w, N.ACT_I8, buf.data_ptr(), 1, y.data_ptr(), n, st.handle)
+        one.copies = two.copies = launch.copies
+        torch.cuda.synchronize()
+        pre, _ = per_launch(st, launch, args.steps, args.warmup)
+        t1, _ = per_launch(st, one, args.steps, args.warmup)
+        t2, reps = per_launch(st, two, args.steps, args.warmup)
+        e = dict(case=case_name(dtype, n, k, 1), prologue=(k // 32) <= 384 and not (dtype == 1 and n >= 16384 and (k // 32) % 64),
+                 gemv_batch_dev_us=round(t1 * 1e6, 3), quantizer_then_gemv_us=round(t2 * 1e6, 3),
+                 prequantized_gemv_us=round(pre * 1e6, 3), launches=reps)
+        log(f"i8_prologue: {e}")
+        out.append(e)
+        del launch, one, two
+        torch.cuda.synchronize()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -829,7 +873,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "qwen_decode", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "bf16", "peaks", "traffic", "fused_norm", "i8_m1", "all"])
+                             "bf16", "peaks", "traffic", "fused_norm", "i8_m1", "i8_prologue", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -894,6 +938,8 @@ def main():
         # 14336-column shapes and both 18944-column ones).
         extra["i8_m1"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in I8_M1_SHAPES], N.ACT_I8,
                                        "i8_m1")
+    if args.workload in ("i8_prologue", "all"):
+        extra["i8_prologue"] = i8_prologue(args, N)
     if args.workload in ("bf16", "all"):
         extra["bf16_bit_exact"] = measure_cases(args, N, [(3, n, k, m) for n, k in BF16_SHAPES for m in (1, 4)],
                                                 N.ACT_F32, "bf16")

@@ -240,7 +240,9 @@ int run_gemv(const nnh_weight* w, const float* x, size_t x_stride, float* y, siz
         float* xsum = w->dtype == NNH_Q4S ? (float*)scratch : nullptr;
         nnh::launch_gemv_f32(w->dtype, w->fq, w->fs, w->bi, x, x_stride, xsum, rows, nb, (int)w->nbp, (int)n_tok,
                              y, y_stride, w->f32v2, st);
-    } else {
+    } else if (!(act == NNH_ACT_I8 && n_tok == 1 &&
+                 nnh::launch_gemv_i8_qx(w->dtype, w->qs, w->sc, w->sb, x, rows, nb, y, st))) {
+        // (One vector at most rows: quantized in the GEMV's own prologue.)
         const ActLayout l = act_layout(w->cols, n_tok, act);
         launch_quantize(act, x, x_stride, w->cols, n_tok, scratch, st);
         launch_i8(w, act, scratch, n_tok, y, y_stride, scratch + l.bytes, st);
@@ -817,6 +819,7 @@ int nnh_gemv_rmsnorm_dev(const nnh_weight* w, const float* x, const float* r, co
                          float* x_out, float* rec, float* normed, float* y, void* stream) {
     return nnh_gemv_rmsnorm_act_dev(w, NNH_ACT_F32, x, r, gamma, eps, x_out, rec, normed, y, stream);
 }
+
 
 int nnh_gemv_batch_dev_noalloc(const nnh_weight* w, const float* x, size_t x_stride, float* y, size_t y_stride,
                                size_t n_tok, int act, void* stream) {

@@ -163,6 +163,14 @@ void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const 
 // vectors, Q4 with its packed scale-and-bias words).
 bool launch_gemv_i8_norm(int dtype, const uint8_t* qs, const uint16_t* scales, const uint32_t* sb,
                          const NormIn& nrm, int rows, int nb, float* y, hipStream_t st);
+// One f32 vector quantized with nncpu's Q8_0 encoder in the int8 GEMV's
+// prologue (same bits as the quantizer then launch_gemv_i8); false (nothing
+// launched) where it measured slower than the two launches or the shape or
+// alignment does not fit it (rows of 97 .. 384 blocks, except tall Q8
+// matrices of rows that are not whole 64-block groups; x 16-byte aligned;
+// Q4 with its packed scale-and-bias words).
+bool launch_gemv_i8_qx(int dtype, const uint8_t* qs, const uint16_t* scales, const uint32_t* sb, const float* x,
+                       int rows, int nb, float* y, hipStream_t st);
 // f32 -> Q8_0 / Q4 split layout on the device (kernels_encode.hip).
 void launch_encode(int dtype, const float* w, size_t n, uint8_t* qs, uint16_t* sc, uint16_t* bi, hipStream_t st);
 // BF16 weights (kernels_bf16.hip): the reference's kernel by shape.

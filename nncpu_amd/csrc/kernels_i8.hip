@@ -721,24 +721,48 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
 // weights in flight. A lane sums blocks l, l + 64, ... in order and the
 // lanes are reduced with the tree of the kernel the plain path would take
 // (V2RED), so the bits are the plain path's.
+//
+// K4 > 0: the vector arrives as f32 (xf) and the workgroup quantizes it
+// itself with the library quantizer's encoder (q8_act.h), no separate
+// quantizer launch: each thread loads its K4 pieces (values 4i .. 4i + 3,
+// i = tid + 1024 k; K4 * 1024 >= nb * 8) before any weight load, and
+// encodes them into LDS while its first weights are in flight.
 constexpr int I8L_T = 1024;
-template <int DT, bool V2RED>
+template <int DT, bool V2RED, int K4 = 0>
 __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __restrict__ qs,
                                                             const uint16_t* __restrict__ sc,
                                                             const uint32_t* __restrict__ sb,
                                                             const int8_t* __restrict__ aq,
                                                             const double* __restrict__ asx, int rows, int nb,
-                                                            float* __restrict__ y) {
+                                                            float* __restrict__ y, const float* __restrict__ xf) {
     constexpr int QV = DT == 1 ? 2 : 1;
     constexpr int BPL = 2, STEP = 64 * BPL, NW = I8L_T / 64;
+    constexpr bool QX = K4 > 0;
     extern __shared__ __align__(16) unsigned char i8l_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t cols = (size_t)nb * 32, qrow_bytes = DT == 1 ? cols : cols / 2;
     int8_t* xq = (int8_t*)i8l_smem;
     double2* xsx = (double2*)(i8l_smem + ((cols + 1023) & ~(size_t)1023));
-    for (size_t c = wave; c * 1024 < cols; c += NW) copy_1k(aq, cols, c * 1024, (unsigned char*)xq + c * 1024, lane);
-    for (size_t c = wave; c * 1024 < (size_t)nb * 16; c += NW)
-        copy_1k(asx, (size_t)nb * 16, c * 1024, (unsigned char*)xsx + c * 1024, lane);
+    const int n4 = nb * 8;
+    float4 xv[QX ? K4 : 1];
+    if constexpr (QX) {
+        // Unconditional (indices clamped; pieces past n4 are not encoded),
+        // and every wave's issued before any weight load (an execution
+        // barrier only), so waiting for them waits for no weights.
+#pragma unroll
+        for (int k = 0; k < K4; ++k) {
+            const int i = tid + I8L_T * k;
+            xv[k] = ((const float4*)xf)[i < n4 ? i : n4 - 1];
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    } else {
+        for (size_t c = wave; c * 1024 < cols; c += NW)
+            copy_1k(aq, cols, c * 1024, (unsigned char*)xq + c * 1024, lane);
+        for (size_t c = wave; c * 1024 < (size_t)nb * 16; c += NW)
+            copy_1k(asx, (size_t)nb * 16, c * 1024, (unsigned char*)xsx + c * 1024, lane);
+    }
 
     struct Chunk {
         int4 w[BPL][QV];
@@ -788,7 +812,14 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
     // Unconditional (a wave past the last row rereads it, unused), so the
     // wait below counts these loads exactly; the copies land first.
     load(A, r0 < rows ? r0 : rows - 1, 0);
-    wait_vm_keep<BPL * (QV + 1)>(qs, DT == 1 ? (const void*)sc : (const void*)sb);
+    if constexpr (QX) {
+        q8_pieces<K4>(xv, tid, I8L_T, n4, [&](int i, uint32_t word, const Q8Scale& s, int qsum) {
+            ((uint32_t*)xq)[i] = word;
+            if ((i & 7) == 0) xsx[i >> 3] = double2{(double)s.scale, (double)s.scale * (double)qsum};
+        });
+    } else {
+        wait_vm_keep<BPL * (QV + 1)>(qs, DT == 1 ? (const void*)sc : (const void*)sb);
+    }
     __syncthreads();
     if (r0 >= rows) return;
     // Items (row, chunk) in order; A holds the current item's weights, B
@@ -829,15 +860,66 @@ bool i8_lds_shape(int dtype, int rows, int nb) {
     return nb > 256 && nb % 64 != 0 && rows >= 3584;
 }
 
-template <int DT, bool V2RED>
+// Workgroups resident per CU (at most I8L_WG_PER_CU), from the instance's
+// registers and LDS: the grid is never larger than what runs at once.
+template <int DT, bool V2RED, int K4>
+int i8_lds_per_cu(size_t lds) {
+    static int n = -1;
+    if (n < 0) {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_i8_lds_kernel<DT, V2RED, K4>, I8L_T, lds) !=
+                hipSuccess ||
+            b < 1)
+            b = 1;
+        n = b < I8L_WG_PER_CU ? b : I8L_WG_PER_CU;
+    }
+    return n;
+}
+
+template <int DT, bool V2RED, int K4 = 0>
 void launch_i8_lds(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
-                   int rows, int nb, float* y, hipStream_t st) {
-    const int want = ceil_div(rows, I8L_T / 64), cap = I8L_WG_PER_CU * cu_count();
-    const int grid = want < cap ? want : cap;
+                   int rows, int nb, float* y, hipStream_t st, const float* xf = nullptr) {
     const size_t lds = (((size_t)nb * 32 + 1023) & ~(size_t)1023) + (((size_t)nb * 16 + 1023) & ~(size_t)1023);
-    gemv_i8_lds_kernel<DT, V2RED><<<grid, I8L_T, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y);
+    const int want = ceil_div(rows, I8L_T / 64), cap = i8_lds_per_cu<DT, V2RED, K4>(lds) * cu_count();
+    const int grid = want < cap ? want : cap;
+    gemv_i8_lds_kernel<DT, V2RED, K4><<<grid, I8L_T, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, xf);
+}
+
+// The quantizing prologue's pieces per thread: K4 * 1024 >= nb * 8.
+template <int DT, bool V2RED>
+void launch_i8_qx_k(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const float* x, int rows, int nb,
+                    float* y, hipStream_t st) {
+    if (nb <= 128) launch_i8_lds<DT, V2RED, 1>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (nb <= 256) launch_i8_lds<DT, V2RED, 2>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else launch_i8_lds<DT, V2RED, 3>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
 }
 }  // namespace
+
+// One vector, rows of 97+ blocks (the plain path's 64 lanes per row, so its
+// lane order and tree). Every workgroup encodes the whole vector, so the
+// encoding's VALU work per CU grows with the row: against the quantizer
+// launch followed by the GEMV (bench.py --workload i8_prologue: HIP graphs
+// of launches on rotating weights) the prologue is faster up to 288 blocks
+// (Q4 4608x3584 7.37 -> 5.13 us, 3584x3584 6.69 -> 3.76, 4096x8192 8.56 ->
+// 6.77, 3584x9216 8.85 -> 8.05; Q8 4608x3584 7.78 -> 7.02, 14336x4096
+// 15.80 -> 13.38, 3584x9216 11.46 -> 10.73); rows of 448 and 592 blocks
+// (14336 and 18944 columns) and tall Q8 matrices of rows that are not whole
+// 64-block groups (Q8 37888x3584) measured slower with it, so they keep the
+// two launches.
+bool launch_gemv_i8_qx(int dtype, const uint8_t* qs, const uint16_t* scales, const uint32_t* sb, const float* x,
+                       int rows, int nb, float* y, hipStream_t st) {
+    if (nb <= 96 || nb > 384 || (dtype == 2 && !sb) || ((uintptr_t)x & 15) != 0) return false;
+    if (dtype == 1 && rows >= 16384 && nb % 64 != 0) return false;
+    const bool v2red = nb % 64 == 0;  // the plain path's kernel at this row length: its lane tree
+    if (dtype == 1) {
+        if (v2red) launch_i8_qx_k<1, true>(qs, scales, sb, x, rows, nb, y, st);
+        else launch_i8_qx_k<1, false>(qs, scales, sb, x, rows, nb, y, st);
+    } else {
+        if (v2red) launch_i8_qx_k<2, true>(qs, scales, sb, x, rows, nb, y, st);
+        else launch_i8_qx_k<2, false>(qs, scales, sb, x, rows, nb, y, st);
+    }
+    return true;
+}
 
 void launch_pack_sb(const uint16_t* sc, const uint16_t* bi, uint32_t* sb, size_t n, hipStream_t st) {
     pack_sb_kernel<<<(int)((n + 255) / 256), 256, 0, st>>>(sc, bi, sb, n);

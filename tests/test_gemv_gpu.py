@@ -8,6 +8,7 @@ int32 block dots bit-exact, and the outputs within the north-star tolerance
 dequantized activations; also within one f32 ulp of the exact sum (up to 16
 vectors) or within the f32 rounding bound of the MFMA GEMM's epilogue.
 """
+import os
 import sys
 
 import numpy as np
@@ -402,6 +403,50 @@ def test_preconditions():
     y = np.full(2, 3.0, np.float32)
     N.gemv_batch(w, np.zeros(32, np.float32), 32, y, 2, 0)  # empty batch: a no-op
     assert np.all(y == 3.0)
+
+
+def gen_weight(dtype, rows, cols, seed):
+    """A device weight of 0.02 N(0, 1) values (torch's generator on the
+    GPU), re-encoded by the library's device encoder."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    dw = torch.randn(rows * cols, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+    w = N.Weight.encode_dev(dtype, dw.data_ptr(), rows, cols)
+    del dw
+    return w
+
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_i8_quantizing_prologue_bit_identity(oracle, dtype):
+    # One f32 vector through nnh_gemv_batch_dev(..., NNH_ACT_I8): rows of
+    # 97..384 blocks quantize x in the int8 GEMV's own prologue (each
+    # pieces-per-thread bound, 128 and 256 blocks, and one past it; the
+    # xor and DPP lane trees; ragged grids), except tall Q8 matrices of rows
+    # that are not whole 64-block groups; other rows run the quantizer
+    # kernel first (96, 385 and 592 blocks). y bit-equals the library
+    # quantizer followed by the int8 GEMV on the pre-quantized buffer
+    # (nnh_gemv_act_dev), whose parity the int8 tests above pin against the
+    # oracle.
+    import torch
+    for i, (rows, nb) in enumerate([(3584, 97), (1000, 128), (3584, 129), (300, 256), (4100, 257), (3584, 288),
+                                    (2000, 384), (777, 385), (3584, 592), (500, 96), (16384, 112), (16400, 128)]):
+        cols = nb * 32
+        say("i8 quantizing prologue", dtype, rows, cols)
+        w = gen_weight(dtype, rows, cols, 0x9A0 + i + dtype)
+        x = torch.from_numpy(oracle.Rng(0x9A1 + i).normals(cols, 1.0)).cuda()
+        y = torch.zeros(rows, device="cuda")
+        N.gemv_batch_dev(w, x.data_ptr(), cols, y.data_ptr(), rows, 1, N.ACT_I8)
+        _, _, nbytes = N.act_layout(cols, 1)
+        act = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        N.quantize_act_dev(x.data_ptr(), cols, cols, 1, act.data_ptr())
+        want = torch.zeros(rows, device="cuda")
+        N.gemv_act_dev(w, N.ACT_I8, act.data_ptr(), 1, want.data_ptr(), rows)
+        torch.cuda.synchronize()
+        got, exp = y.cpu().numpy(), want.cpu().numpy()
+        assert np.array_equal(bits(got), bits(exp)), (rows, nb, int(np.sum(bits(got) != bits(exp))))
+        w.free()
 
 
 # ---- int8 path ---------------------------------------------------------------------
