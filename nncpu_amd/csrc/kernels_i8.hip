@@ -714,8 +714,9 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
 // Measured against the plain path on one box, alternating (medians of 5):
 // Q8 14336x4096 18.0 -> 13.5 us, 4096x14336 13.7 -> 12.7, Q4 3584x18944
 // 11.9 -> 9.5; at Q8 4096-6144 rows of 128-192 blocks and Q8 3584x18944
-// the two were within 0.6 us either way, so those stay plain. Two
-// workgroups of 16 waves per CU; each copies the quantized activations
+// the two were within 0.6 us either way, so those stay plain. Up to two
+// workgroups of 16 waves per CU (below 16 rows per CU, one per CU of
+// ceil(rows / CUs) waves: i8_lds_waves); each copies the quantized activations
 // (the quants and the (scale, scale * sum) pairs) into LDS once, then each
 // wave takes rows grid-stride, chunks of 128 blocks with the next chunk's
 // weights in flight. A lane sums blocks l, l + 64, ... in order and the
@@ -725,8 +726,8 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
 // K4 > 0: the vector arrives as f32 (xf) and the workgroup quantizes it
 // itself with the library quantizer's encoder (q8_act.h), no separate
 // quantizer launch: each thread loads its K4 pieces (values 4i .. 4i + 3,
-// i = tid + 1024 k; K4 * 1024 >= nb * 8) before any weight load, and
-// encodes them into LDS while its first weights are in flight.
+// i = tid + T k for T threads; K4 * T >= nb * 8) before any weight load,
+// and encodes them into LDS while its first weights are in flight.
 constexpr int I8L_T = 1024;
 template <int DT, bool V2RED, int K4 = 0>
 __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __restrict__ qs,
@@ -736,8 +737,9 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
                                                             const double* __restrict__ asx, int rows, int nb,
                                                             float* __restrict__ y, const float* __restrict__ xf) {
     constexpr int QV = DT == 1 ? 2 : 1;
-    constexpr int BPL = 2, STEP = 64 * BPL, NW = I8L_T / 64;
+    constexpr int BPL = 2, STEP = 64 * BPL;
     constexpr bool QX = K4 > 0;
+    const int nt = blockDim.x, NW = nt >> 6;  // up to I8L_T threads
     extern __shared__ __align__(16) unsigned char i8l_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t cols = (size_t)nb * 32, qrow_bytes = DT == 1 ? cols : cols / 2;
@@ -751,7 +753,7 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
         // barrier only), so waiting for them waits for no weights.
 #pragma unroll
         for (int k = 0; k < K4; ++k) {
-            const int i = tid + I8L_T * k;
+            const int i = tid + nt * k;
             xv[k] = ((const float4*)xf)[i < n4 ? i : n4 - 1];
         }
         asm volatile("" ::: "memory");
@@ -813,7 +815,7 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
     // wait below counts these loads exactly; the copies land first.
     load(A, r0 < rows ? r0 : rows - 1, 0);
     if constexpr (QX) {
-        q8_pieces<K4>(xv, tid, I8L_T, n4, [&](int i, uint32_t word, const Q8Scale& s, int qsum) {
+        q8_pieces<K4>(xv, tid, nt, n4, [&](int i, uint32_t word, const Q8Scale& s, int qsum) {
             ((uint32_t*)xq)[i] = word;
             if ((i & 7) == 0) xsx[i >> 3] = double2{(double)s.scale, (double)s.scale * (double)qsum};
         });
@@ -876,22 +878,37 @@ int i8_lds_per_cu(size_t lds) {
     return n;
 }
 
+// Waves per workgroup: 16, except that below 16 rows per CU the rows are
+// spread over every CU (ceil(rows / CUs) waves, at least 8), so that no CU
+// sits idle while others take two rows per wave (3584 rows: 256 workgroups
+// of 14 waves, not 224 of 16).
+inline int i8_lds_waves(int rows) {
+    const int cus = cu_count();
+    if (rows >= 16 * cus) return 16;
+    const int w = ceil_div(rows, cus);
+    return w < 8 ? 8 : w;
+}
+
 template <int DT, bool V2RED, int K4 = 0>
 void launch_i8_lds(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
                    int rows, int nb, float* y, hipStream_t st, const float* xf = nullptr) {
     const size_t lds = (((size_t)nb * 32 + 1023) & ~(size_t)1023) + (((size_t)nb * 16 + 1023) & ~(size_t)1023);
-    const int want = ceil_div(rows, I8L_T / 64), cap = i8_lds_per_cu<DT, V2RED, K4>(lds) * cu_count();
+    const int waves = i8_lds_waves(rows);
+    const int want = ceil_div(rows, waves), cap = i8_lds_per_cu<DT, V2RED, K4>(lds) * cu_count();
     const int grid = want < cap ? want : cap;
-    gemv_i8_lds_kernel<DT, V2RED, K4><<<grid, I8L_T, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, xf);
+    gemv_i8_lds_kernel<DT, V2RED, K4><<<grid, 64 * waves, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, xf);
 }
 
-// The quantizing prologue's pieces per thread: K4 * 1024 >= nb * 8.
+// The quantizing prologue's pieces per thread: K4 * threads >= nb * 8.
 template <int DT, bool V2RED>
 void launch_i8_qx_k(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const float* x, int rows, int nb,
                     float* y, hipStream_t st) {
-    if (nb <= 128) launch_i8_lds<DT, V2RED, 1>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else if (nb <= 256) launch_i8_lds<DT, V2RED, 2>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else launch_i8_lds<DT, V2RED, 3>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    const int need = ceil_div(nb * 8, 64 * i8_lds_waves(rows));
+    if (need <= 1) launch_i8_lds<DT, V2RED, 1>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 2) launch_i8_lds<DT, V2RED, 2>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 3) launch_i8_lds<DT, V2RED, 3>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 4) launch_i8_lds<DT, V2RED, 4>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else launch_i8_lds<DT, V2RED, 6>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
 }
 }  // namespace
 
