@@ -718,14 +718,14 @@ inline size_t m1x_lds(int dt, int nb, int nbp, int rpw, bool norm = false) {
 
 // The fused residual add and RMSNorm (NormIn) on a vector of `cols` floats
 // staged in LDS at v, with r and gamma staged at rw and gw (r's copy unused
-// when n.r is NULL); NT threads. Afterwards v holds the gemv's input. The
+// when n.r is NULL); nt threads. Afterwards v holds the gemv's input. The
 // operations and their order are the device forward's resid_norm_kernel's
 // (forward.rs:719-841: the add, sum_sq, the scale, (v * scale) * gamma).
-template <int NT, int B>
+template <int B>
 __device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, const float* rw, const float* gw, int cols,
-                                              float* sc_lds) {
+                                              float* sc_lds, int nt) {
     const int tid = threadIdx.x;
-    for (int i = 4 * tid; i < cols; i += 4 * NT) {
+    for (int i = 4 * tid; i < cols; i += 4 * nt) {
         float4 a = *(const float4*)(v + i);
         if (n.r) {
             const float4 b = *(const float4*)(rw + i);
@@ -744,7 +744,7 @@ __device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, const f
     }
     __syncthreads();
     const float sc = *sc_lds;
-    for (int i = 4 * tid; i < cols; i += 4 * NT) {
+    for (int i = 4 * tid; i < cols; i += 4 * nt) {
         const float4 a = *(const float4*)(v + i), g = *(const float4*)(gw + i);
         *(float4*)(v + i) = float4{__fmul_rn(__fmul_rn(a.x, sc), g.x), __fmul_rn(__fmul_rn(a.y, sc), g.y),
                                    __fmul_rn(__fmul_rn(a.z, sc), g.z), __fmul_rn(__fmul_rn(a.w, sc), g.w)};
@@ -765,8 +765,9 @@ template <int DT, int NT, int M1R_PF, bool SL, bool NORM>
 __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float* __restrict__ x,
                                                          float* __restrict__ y, NormIn nrm) {
     constexpr int G = DT == 1 ? 8 : 16;
-    constexpr int RPW = NT / 32;  // rows per workgroup
-    constexpr int NW = NT / 64;
+    const int nt = blockDim.x;  // at most NT: 32 lanes per row
+    const int RPW = nt >> 5;    // rows per workgroup
+    const int NW = nt >> 6;
     extern __shared__ __align__(1024) unsigned char m1x_smem[];
     __shared__ float nsc;  // the norm's scale (NORM)
     const int tid = threadIdx.x, nb = m.nb, wave = tid >> 6, lane = tid & 63;
@@ -817,10 +818,10 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>(m.fq, m.fs, m.bi);
     __syncthreads();
     if (NORM)
-        norm_prologue<NT, 32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
-                              &nsc);
+        norm_prologue<32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
+                          &nsc, nt);
     if (DT == 2)
-        for (int b = tid; b < nb; b += NT) xs[b] = m1_block_sum(xw + 32 * b);
+        for (int b = tid; b < nb; b += nt) xs[b] = m1_block_sum(xw + 32 * b);
     if (DT == 2) lds_barrier();
 
     const float* xp = xw + j;
@@ -888,38 +889,57 @@ static void m1x_allow_lds() {
     (void)once;
 }
 
-// The streamed kernel: 16 rows per workgroup (8 waves) when that still
-// gives a workgroup per CU, else 8. Prefetch depth: 3 groups (48 blocks)
-// for Q4, 6 (48 blocks) for Q8 (deeper measured slower at Llama's and
-// Qwen's shapes). The rows' scales are staged in LDS too unless that would
-// leave fewer workgroups resident per CU than the launch needs (long rows:
-// the copy of x alone takes half of a CU's LDS). NORM: the fused residual
-// add and RMSNorm first (x unused; its input is nrm's).
+// The streamed kernel's rows per workgroup: every CU takes the same rows
+// where the matrix has at most 32 per CU (ceil(rows / CUs), even, at least
+// 8: 3584 rows as 256 workgroups of 14, 4608 as 256 of 18, where fixed
+// 8- or 16-row workgroups left some CUs a second one), else 16. Prefetch
+// depth: 3 groups (48 blocks) for Q4, 6 (48 blocks) for Q8 (deeper
+// measured slower at Llama's and Qwen's shapes). The rows' scales are
+// staged in LDS too unless that would leave fewer workgroups resident per
+// CU than the launch needs (long rows: the copy of x alone takes half of a
+// CU's LDS). NORM: the fused residual add and RMSNorm first (x unused; its
+// input is nrm's).
+template <int DT, int NT, bool NORM>
+void launch_m1x_nt(const F32Mat& m, const float* x, float* y, const NormIn& nrm, bool sl, int rpw, size_t lds,
+                   hipStream_t st) {
+    constexpr int PF = DT == 1 ? 6 : 3;
+    const dim3 grid(ceil_div(m.rows, rpw)), block(rpw * 32);
+    if (sl) {
+        m1x_allow_lds<DT, NT, PF, true, NORM>();
+        gemv_f32_m1x_kernel<DT, NT, PF, true, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    } else if constexpr (NT <= 512) {  // (1024 threads leave too few registers for the scales' loads)
+        m1x_allow_lds<DT, NT, PF, false, NORM>();
+        gemv_f32_m1x_kernel<DT, NT, PF, false, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    }
+}
+
 template <int DT, bool NORM>
 void launch_m1x(const F32Mat& m, const float* x, float* y, const NormIn& nrm, hipStream_t st) {
-    constexpr int PF = DT == 1 ? 6 : 3;
-    const int rows = m.rows, nb = m.nb, nbp = m.nbp;
-    const bool wide = rows >= 16 * cu_count() && m1x_lds(DT, nb, nbp, 16, NORM) <= M1R_MAX_LDS;
-    const int rpw = wide ? 16 : 8;
-    const int need = ceil_div(ceil_div(rows, rpw), cu_count());
-    const int fit_sl = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, rpw, NORM));
-    const int fit = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, 0, NORM));
-    const bool sl = fit_sl >= std::min(need, fit);
-    const size_t lds = m1x_lds(DT, nb, nbp, sl ? rpw : 0, NORM);
-    const dim3 grid(ceil_div(rows, rpw)), block(rpw * 32);
-    if (wide && sl) {
-        m1x_allow_lds<DT, 512, PF, true, NORM>();
-        gemv_f32_m1x_kernel<DT, 512, PF, true, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
-    } else if (wide) {
-        m1x_allow_lds<DT, 512, PF, false, NORM>();
-        gemv_f32_m1x_kernel<DT, 512, PF, false, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
-    } else if (sl) {
-        m1x_allow_lds<DT, 256, PF, true, NORM>();
-        gemv_f32_m1x_kernel<DT, 256, PF, true, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
-    } else {
-        m1x_allow_lds<DT, 256, PF, false, NORM>();
-        gemv_f32_m1x_kernel<DT, 256, PF, false, NORM><<<grid, block, lds, st>>>(m, x, y, nrm);
+    const int rows = m.rows, nb = m.nb, nbp = m.nbp, cus = cu_count();
+    int rpw = 16;
+    if (rows <= 32 * cus) {
+        rpw = ceil_div(rows, cus);
+        rpw += rpw & 1;
+        if (rpw < 8) rpw = 8;
     }
+    const auto staged = [&](int r) {
+        const int need = ceil_div(ceil_div(rows, r), cus);
+        const size_t lds_sl = m1x_lds(DT, nb, nbp, r, NORM);
+        const int fit = (int)(CU_LDS_BYTES / m1x_lds(DT, nb, nbp, 0, NORM));
+        return lds_sl <= M1R_MAX_LDS && (int)(CU_LDS_BYTES / lds_sl) >= std::min(need, fit);
+    };
+    bool sl = staged(rpw);
+    if (!sl && rpw > 16) {  // more than 16 rows only with the scales staged
+        rpw = 16;
+        sl = staged(rpw);
+    }
+    const size_t lds = m1x_lds(DT, nb, nbp, sl ? rpw : 0, NORM);
+    if (rpw <= 8)
+        launch_m1x_nt<DT, 256, NORM>(m, x, y, nrm, sl, rpw, lds, st);
+    else if (rpw <= 16)
+        launch_m1x_nt<DT, 512, NORM>(m, x, y, nrm, sl, rpw, lds, st);
+    else
+        launch_m1x_nt<DT, 1024, NORM>(m, x, y, nrm, sl, rpw, lds, st);
 }
 
 // Weight-load slots D >= the row's groups: 4 or 8 (Q4: 2 or 4) for the
