@@ -658,27 +658,24 @@ __device__ __forceinline__ void kv_store(const uint4 (&r)[U], uint16_t* kv, int 
     }
 }
 
-// Eight keys' weights and one V column's values (LDS rows of KS halves),
-// and their FMAs into a chain in key order.
+// Eight keys of a thread's V column (LDS rows of KS halves): the weights and
+// the raw BF16 values (converted in fma, so a load waits for nothing), and
+// their FMAs into the chain in key order.
 struct V8 {
     float4 w0, w1;
-    float v[8];
+    uint32_t v[8];
     template <int KS>
     __device__ __forceinline__ void load(const float* sc, const uint16_t* col, int j) {
         w0 = *(const float4*)(sc + j);
         w1 = *(const float4*)(sc + j + 4);
 #pragma unroll
-        for (int r = 0; r < 8; ++r) v[r] = bf16f(col[(j + r) * KS]);
+        for (int r = 0; r < 8; ++r) v[r] = col[(j + r) * KS];
     }
     __device__ __forceinline__ float fma(float o) const {
-        o = __fmaf_rn(w0.x, v[0], o);
-        o = __fmaf_rn(w0.y, v[1], o);
-        o = __fmaf_rn(w0.z, v[2], o);
-        o = __fmaf_rn(w0.w, v[3], o);
-        o = __fmaf_rn(w1.x, v[4], o);
-        o = __fmaf_rn(w1.y, v[5], o);
-        o = __fmaf_rn(w1.z, v[6], o);
-        return __fmaf_rn(w1.w, v[7], o);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) o = __fmaf_rn(w[r], bf16f(v[r]), o);
+        return o;
     }
 };
 
@@ -944,28 +941,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
     float o = -0.0f;
     if (tid < HD) {
-        // Keys in order, 8 per step; the next step's LDS reads are issued
-        // before this step's FMAs (two named buffers, no copies; the reads
-        // are unconditional, clamped to the last whole step, and kept ahead
-        // of the FMAs by scheduling barriers).
+        // Keys in order, 8 per step, the LDS reads of the next four steps in
+        // flight: a ring of four named buffers (no copies), each refilled
+        // right after its FMAs with the step four on; the reads are
+        // unconditional, clamped to the last whole step, and kept ahead of
+        // the FMAs by scheduling barriers.
+        constexpr int RING = 4;
         const int body = nk & ~7;
         const uint16_t* vc = vv + tid;
+        const auto step = [&](int s) { return s + 8 <= body ? s : body - 8; };
         int j = 0;
         if (body) {
-            V8 va, vb;
-            va.load<KS>(sc, vc, 0);
-            for (; j + 16 <= body; j += 16) {
-                vb.load<KS>(sc, vc, j + 8);
-                __builtin_amdgcn_sched_barrier(0);
-                o = va.fma(o);
-                va.load<KS>(sc, vc, j + 16 < body ? j + 16 : body - 8);
-                __builtin_amdgcn_sched_barrier(0);
-                o = vb.fma(o);
+            V8 r[RING];
+#pragma unroll
+            for (int k = 0; k < RING; ++k) r[k].load<KS>(sc, vc, step(8 * k));
+            for (; j + 8 * RING <= body; j += 8 * RING) {
+#pragma unroll
+                for (int k = 0; k < RING; ++k) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    o = r[k].fma(o);
+                    r[k].load<KS>(sc, vc, step(j + 8 * (RING + k)));
+                }
             }
-            if (j < body) {
-                o = va.fma(o);
-                j += 8;
-            }
+#pragma unroll
+            for (int k = 0; k < RING - 1; ++k)
+                if (j + 8 <= body) {
+                    o = r[k].fma(o);
+                    j += 8;
+                }
         }
         for (; j < nk; ++j) o = __fmaf_rn(sc[j], bf16f(vv[j * KS + tid]), o);
     } else if (KV2 && wave == 3) {
