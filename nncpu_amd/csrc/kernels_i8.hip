@@ -270,16 +270,28 @@ __global__ __launch_bounds__(256) void gemv_i8_v2_kernel(const uint8_t* __restri
     };
     constexpr int STEP = LPR * BPL;
     if (PF) {
+        // Every load in the loop is unconditional (the chunk after the pair
+        // exists), so the compiler's waits count the chunk in flight behind
+        // the one used: a load under a condition would make it wait for
+        // everything. The last one or two chunks after the loop. (Two
+        // chunks in flight, three buffers in turn, measured slower.)
+        const int n = nb / STEP;  // whole chunks (nb is a multiple of STEP), at least 2
         Chunk A, B;
         load(A, 0);
-        int c0 = 0;
-        for (; c0 + STEP < nb; c0 += 2 * STEP) {
-            load(B, c0 + STEP);
+        int c = 0;
+        for (; c + 2 < n; c += 2) {
+            load(B, (c + 1) * STEP);
             run(A);
-            if (c0 + 2 * STEP < nb) load(A, c0 + 2 * STEP);
+            load(A, (c + 2) * STEP);
             run(B);
         }
-        if (c0 < nb) run(A);
+        if (c + 1 < n) {
+            load(B, (c + 1) * STEP);
+            run(A);
+            run(B);
+        } else {
+            run(A);
+        }
     } else if constexpr (M == 1) {
         // One vector, one chunk (the launcher's shapes without PF): the
         // activations are copied to LDS once per workgroup (direct-to-LDS
