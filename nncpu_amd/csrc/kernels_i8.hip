@@ -668,7 +668,9 @@ __global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __re
 
     if (g0 >= ng) return;
     // Items (row group, chunk) in order; A holds the current item's
-    // weights, B the next one's, then the roles swap.
+    // weights, B the next one's, then the roles swap. (Unconditional loads,
+    // so that the compiler's waits count the item in flight, measured
+    // slower here at the decode's shapes but one.)
     int ga = g0, ca = 0;
     while (true) {
         int gb = ga, cb = ca + STEP;
@@ -837,7 +839,14 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
     __syncthreads();
     if (r0 >= rows) return;
     // Items (row, chunk) in order; A holds the current item's weights, B
-    // the next one's, then the roles swap.
+    // the next one's, then the roles swap. Q4: the loads are unconditional
+    // (past the wave's last item a reread of the current one, unused), so
+    // the compiler's waits count the item in flight (a load under a
+    // condition makes each item wait for everything): Q4 3584x18944 10.5
+    // -> 10.2 us, 3584x9216 6.65 -> 6.3. Q8 keeps the conditional loads:
+    // with its chunks (twice Q4's bytes) in flight as well, 14336x4096 went
+    // 14.7 -> 18.8 us and 3584x10240 10.0 -> 10.55.
+    constexpr bool EXACT = DT == 2;
     int ra = r0, ca = 0;
     while (true) {
         int rb = ra, cb = ca + STEP;
@@ -846,7 +855,10 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
             rb += gstep;
         }
         const bool hb = rb < rows;
-        if (hb) load(B, rb, cb);
+        if (EXACT)
+            load(B, hb ? rb : ra, hb ? cb : ca);
+        else if (hb)
+            load(B, rb, cb);
         run(A, ca);
         if (ca + STEP >= nb) finish(ra);
         if (!hb) break;
@@ -856,7 +868,10 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
             rc += gstep;
         }
         const bool hc = rc < rows;
-        if (hc) load(A, rc, cc);
+        if (EXACT)
+            load(A, hc ? rc : rb, hc ? cc : cb);
+        else if (hc)
+            load(A, rc, cc);
         run(B, cb);
         if (cb + STEP >= nb) finish(rb);
         if (!hc) break;
