@@ -52,7 +52,7 @@ FUSED_GATE_UP = (28672, 4096)
 # rocprofv3 --pmc FETCH_SIZE (scaled by 2.0, the factor a 64 MiB device copy
 # gives in the same run) + WRITE_SIZE readings of `bench.py --workload traffic`.
 TRAFFIC_SOURCE = "profiles/gemv_i8_q4_llama3_8b_sweep.md (rocprofv3 --pmc over bench.py --workload traffic)"
-Q4_SWEEP_TRAFFIC = [10_593_280, 2_704_384, 36_854_784, 36_943_872]
+Q4_SWEEP_TRAFFIC = [10_605_568, 2_716_672, 36_854_784, 36_948_992]
 Q8_VOCAB = [(262144, 1152), (151936, 3584)]
 
 
