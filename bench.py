@@ -386,6 +386,9 @@ def peaks(args):
 
 QWEN_PREFILL = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]  # q/o, k/v, gate/up, down
 VERIFY_SHAPES = [(6144, 1536), (1536, 6144), (2048, 1536), (1536, 1536)]
+# The bit-exact one-vector kernels' shapes: Qwen2.5-7B's down, q/k/v and o, Llama-3-8B's, and a
+# 2560-row case (the streamed kernel's rows-per-workgroup choice at each).
+F32_M1_SHAPES = [(3584, 18944), (4096, 14336), (4608, 3584), (4096, 4096), (3584, 3584), (2560, 8192)]
 I8_M1_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096), (4608, 3584), (3584, 3584),
                 (37888, 3584), (3584, 18944)]
 GEMMA_DECODE = [(1024, 1152), (256, 1152), (1152, 1024), (6912, 1152), (1152, 6912), (262144, 1152)]
@@ -873,7 +876,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="q4_sweep",
                     choices=["q4_sweep", "prefill", "qwen_prefill", "qwen_decode", "q8_vocab", "verify", "decode_f32", "gemma_decode",
-                             "bf16", "peaks", "traffic", "fused_norm", "i8_m1", "i8_prologue", "all"])
+                             "bf16", "peaks", "traffic", "fused_norm", "i8_m1", "i8_prologue", "f32_m1", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -938,6 +941,11 @@ def main():
         # 14336-column shapes and both 18944-column ones).
         extra["i8_m1"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in I8_M1_SHAPES], N.ACT_I8,
                                        "i8_m1")
+    if args.workload in ("f32_m1", "all"):
+        # The bit-exact one-vector GEMV (the drop-in mode) at the streamed
+        # kernel's shapes, both formats.
+        extra["f32_m1"] = measure_cases(args, N, [(d, n, k, 1) for d in (1, 2) for n, k in F32_M1_SHAPES],
+                                        N.ACT_F32, "f32_m1")
     if args.workload in ("i8_prologue", "all"):
         extra["i8_prologue"] = i8_prologue(args, N)
     if args.workload in ("bf16", "all"):
