@@ -713,7 +713,9 @@ __host__ __device__ inline size_t m1x_s_bytes(int nbp, int rpw) {
     return ((size_t)rpw * nbp * 2 + 1023) & ~(size_t)1023;
 }
 inline size_t m1x_lds(int dt, int nb, int nbp, int rpw, bool norm = false) {
-    return m1x_x_bytes(nb) * (norm ? 3 : 1) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
+    // NORM: x, then r (1 KB wider: it then holds the sum of squares'
+    // chain-major copy), then gamma.
+    return m1x_x_bytes(nb) * (norm ? 3 : 1) + (norm ? 1024 : 0) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
 }
 
 // The fused residual add and RMSNorm (NormIn) on a vector of `cols` floats
@@ -722,7 +724,7 @@ inline size_t m1x_lds(int dt, int nb, int nbp, int rpw, bool norm = false) {
 // operations and their order are the device forward's resid_norm_kernel's
 // (forward.rs:719-841: the add, sum_sq, the scale, (v * scale) * gamma).
 template <int B>
-__device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, const float* rw, const float* gw, int cols,
+__device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, float* rw, const float* gw, int cols,
                                               float* sc_lds, int nt) {
     const int tid = threadIdx.x;
     for (int i = 4 * tid; i < cols; i += 4 * nt) {
@@ -738,8 +740,21 @@ __device__ __forceinline__ void norm_prologue(const NormIn& n, float* v, const f
         }
     }
     __syncthreads();
+    // v chain-major over r's region (r is read by now): element e at
+    // (e mod 8) * ts + e / 8, so the chain's lanes read 16 bytes at a time.
+    const int ts = rms_t_stride(cols);
+    for (int i = 4 * tid; i < cols; i += 4 * nt) {
+        const float4 a = *(const float4*)(v + i);
+        const int p = i >> 2;
+        float* d = rw + (size_t)(4 * (p & 1)) * ts + (p >> 1);
+        d[0] = a.x;
+        d[ts] = a.y;
+        d[2 * ts] = a.z;
+        d[3 * ts] = a.w;
+    }
+    __syncthreads();
     if (tid < 64) {
-        const double ss = rms_sumsq<B>(v, cols, tid);
+        const double ss = rms_sumsq_t<B>(rw, cols, tid);
         if (tid == 0) *sc_lds = rms_scale(ss, cols, n.eps);
     }
     __syncthreads();
@@ -772,7 +787,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     __shared__ float nsc;  // the norm's scale (NORM)
     const int tid = threadIdx.x, nb = m.nb, wave = tid >> 6, lane = tid & 63;
     const int ngp = m1_groups(DT, nb), ng = nb / G;
-    const size_t XB = m1x_x_bytes(nb), XR = NORM ? 3 * XB : XB;  // x (NORM: then r and gamma)
+    const size_t XB = m1x_x_bytes(nb), XR = NORM ? 3 * XB + 1024 : XB;  // x (NORM: then r, 1 KB wider, and gamma)
     float* xw = (float*)m1x_smem;
     const uint16_t* scl = (const uint16_t*)(m1x_smem + XR);
     float* xs = (float*)(m1x_smem + XR + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));
@@ -789,7 +804,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
             if (nrm.r)
                 for (size_t c = wave; c * 1024 < xl; c += NW) copy_1k(nrm.r, xl, c * 1024, m1x_smem + XB + c * 1024, lane);
             for (size_t c = wave; c * 1024 < xl; c += NW)
-                copy_1k(nrm.gamma, xl, c * 1024, m1x_smem + 2 * XB + c * 1024, lane);
+                copy_1k(nrm.gamma, xl, c * 1024, m1x_smem + 2 * XB + 1024 + c * 1024, lane);
         }
         if (SL) {
             // The scale rows of the workgroup's rows: one contiguous span.
@@ -818,7 +833,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>(m.fq, m.fs, m.bi);
     __syncthreads();
     if (NORM)
-        norm_prologue<32>(nrm, xw, (const float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB), nb * 32,
+        norm_prologue<8>(nrm, xw, (float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB + 1024), nb * 32,
                           &nsc, nt);
     if (DT == 2)
         for (int b = tid; b < nb; b += nt) xs[b] = m1_block_sum(xw + 32 * b);
