@@ -649,7 +649,8 @@ struct M1xSlot {
     static constexpr int G = DT == 1 ? 8 : 16;
     uint4 q;
     uint4 s[G / 8];
-    uint32_t b0, b1;  // Q4 only
+    float4 sf[G / 4];  // the scales as f32 (staged rows)
+    uint32_t b0, b1;   // Q4 only
 };
 
 // Group g's quant piece and scales; Q4: the biases of group gb (g clamped
@@ -673,7 +674,8 @@ __device__ __forceinline__ void m1x_load(M1xSlot<DT>& sl, const uint8_t* qrow, c
 // floats on). Q4 whole groups also take the group's two steps of the lane's
 // bias-dot accumulator (xsg: the block sums at the group's first block plus
 // j mod 8).
-template <int DT, bool FULL>
+// SF: the group's scales are in sl.sf as f32, else in sl.s as BF16.
+template <int DT, bool FULL, bool SF = false>
 __device__ __forceinline__ void m1x_group(const M1xSlot<DT>& sl, const float* xb, const float* xsg, int h, int nblk,
                                           float& a, float& ab) {
     constexpr int G = DT == 1 ? 8 : 16;
@@ -694,7 +696,9 @@ __device__ __forceinline__ void m1x_group(const M1xSlot<DT>& sl, const float* xb
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         if (FULL || i < nblk) {
-            const float sb = bf16f(half_of(sl.s[i / 8], i % 8));
+            const float4 f4 = sl.sf[i / 4];
+            const float sb = SF ? (i % 4 == 0 ? f4.x : i % 4 == 1 ? f4.y : i % 4 == 2 ? f4.z : f4.w)
+                                : bf16f(half_of(sl.s[i / 8], i % 8));
             float w;
             if (DT == 1)
                 w = (float)(int8_t)((qd[i >> 1] >> (16 * (i & 1))) & 0xffu);
@@ -706,16 +710,21 @@ __device__ __forceinline__ void m1x_group(const M1xSlot<DT>& sl, const float* xb
 }
 
 // LDS of the streamed kernel: x (nb * 128 bytes, rounded up to
-// whole 1 KB copies), the scale rows of the workgroup's rpw rows (rounded
-// up likewise), then the Q4 block sums of x (nb floats).
+// whole 1 KB copies), the scale rows of the workgroup's rpw rows as copied
+// (BF16) and, Q4, as f32 (each rounded up likewise), then the Q4 block sums
+// of x (nb floats).
 __host__ __device__ inline size_t m1x_x_bytes(int nb) { return ((size_t)nb * 128 + 1023) & ~(size_t)1023; }
 __host__ __device__ inline size_t m1x_s_bytes(int nbp, int rpw) {
     return ((size_t)rpw * nbp * 2 + 1023) & ~(size_t)1023;
 }
+__host__ __device__ inline size_t m1x_sf_bytes(int nbp, int rpw) {
+    return ((size_t)rpw * nbp * 4 + 1023) & ~(size_t)1023;
+}
 inline size_t m1x_lds(int dt, int nb, int nbp, int rpw, bool norm = false) {
     // NORM: x, then r (1 KB wider: it then holds the sum of squares'
     // chain-major copy), then gamma.
-    return m1x_x_bytes(nb) * (norm ? 3 : 1) + (norm ? 1024 : 0) + m1x_s_bytes(nbp, rpw) + (dt == 2 ? (size_t)nb * 4 : 0);
+    return m1x_x_bytes(nb) * (norm ? 3 : 1) + (norm ? 1024 : 0) + m1x_s_bytes(nbp, rpw) +
+           (dt == 2 ? m1x_sf_bytes(nbp, rpw) + (size_t)nb * 4 : 0);
 }
 
 // The fused residual add and RMSNorm (NormIn) on a vector of `cols` floats
@@ -789,8 +798,14 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     const int ngp = m1_groups(DT, nb), ng = nb / G;
     const size_t XB = m1x_x_bytes(nb), XR = NORM ? 3 * XB + 1024 : XB;  // x (NORM: then r, 1 KB wider, and gamma)
     float* xw = (float*)m1x_smem;
+    // Q4 with the scale rows staged (SF): the chains read them as f32,
+    // converted once per workgroup (Q4 1-4 % faster at the measured
+    // shape; Q8, whose groups hold half the blocks, 5-12 % slower: twice the
+    // LDS reads of its scales), else each lane converts its BF16 scales.
+    constexpr bool SF = SL && DT == 2;
     const uint16_t* scl = (const uint16_t*)(m1x_smem + XR);
-    float* xs = (float*)(m1x_smem + XR + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));
+    float* sclf = (float*)(m1x_smem + XR + (SL ? m1x_s_bytes(m.nbp, RPW) : 0));  // the scale rows as f32 (SF)
+    float* xs = (float*)(m1x_smem + XR + (SL ? m1x_s_bytes(m.nbp, RPW) + (SF ? m1x_sf_bytes(m.nbp, RPW) : 0) : 0));
     const int row0 = blockIdx.x * RPW;
     const int rraw = row0 + (tid >> 5);
     const int row = rraw < m.rows ? rraw : m.rows - 1;
@@ -814,7 +829,8 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
                 copy_1k(ssrc, sl_len, c * 1024, m1x_smem + XR + c * 1024, lane);
         }
     }
-    const uint4* srl = (const uint4*)(scl + (size_t)(row - row0) * m.nbp);  // the row's scales in LDS
+    const uint4* srl = (const uint4*)(scl + (size_t)(row - row0) * m.nbp);       // the row's scales in LDS
+    const float4* srf = (const float4*)(sclf + (size_t)(row - row0) * m.nbp);  // as f32 (SF)
     const uint8_t* qrow = m.fq + (size_t)row * ngp * 256 + (j & 15) * 16;
     const uint16_t* srow = m.fs + (size_t)row * m.nbp;
     // Q4: block 16g + j8 of the row's biases; whole groups only, so the
@@ -832,6 +848,15 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     // biases); the norm and the block sums run while the slots fill.
     wait_vm_keep<M1R_PF * (1 + (SL ? 0 : G / 8) + (DT == 2 ? 2 : 0))>(m.fq, m.fs, m.bi);
     __syncthreads();
+    if (SF) {
+        // The staged scale rows to f32 once per workgroup, so the chains
+        // take each scale as it is instead of converting it per lane.
+        const int pairs = min(RPW, m.rows - row0) * m.nbp / 2;
+        for (int e = tid; e < pairs; e += nt) {
+            const uint32_t w = ((const uint32_t*)scl)[e];
+            ((float2*)sclf)[e] = float2{bf16f(w & 0xffffu), bf16f(w >> 16)};
+        }
+    }
     if (NORM)
         norm_prologue<8>(nrm, xw, (float*)(m1x_smem + XB), (const float*)(m1x_smem + 2 * XB + 1024), nb * 32,
                           &nsc, nt);
@@ -845,23 +870,29 @@ __global__ __launch_bounds__(NT) void gemv_f32_m1x_kernel(F32Mat m, const float*
     for (; g + M1R_PF <= ng; g += M1R_PF) {
 #pragma unroll
         for (int d = 0; d < M1R_PF; ++d) {
-            if (SL)
+            if (SF)
+#pragma unroll
+                for (int k = 0; k < G / 4; ++k) slot[d].sf[k] = srf[(g + d) * (G / 4) + k];
+            else if (SL)
 #pragma unroll
                 for (int k = 0; k < G / 8; ++k) slot[d].s[k] = srl[(g + d) * (G / 8) + k];
-            m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
+            m1x_group<DT, true, SF>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
             const int gn = min(g + d + M1R_PF, ngp - 1);
             m1x_load<DT, SL>(slot[d], qrow, srow, brow, gn, min(gn, ngb - 1));
         }
     }
 #pragma unroll
     for (int d = 0; d < M1R_PF; ++d) {
-        if (SL && g + d < ngp)
+        if (SF && g + d < ngp)
+#pragma unroll
+            for (int k = 0; k < G / 4; ++k) slot[d].sf[k] = srf[(g + d) * (G / 4) + k];
+        else if (SL && g + d < ngp)
 #pragma unroll
             for (int k = 0; k < G / 8; ++k) slot[d].s[k] = srl[(g + d) * (G / 8) + k];
         if (g + d < ng)
-            m1x_group<DT, true>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
+            m1x_group<DT, true, SF>(slot[d], xp + (g + d) * G * 32, xs + (g + d) * G + j8, h, G, a, ab);
         else if (g + d == ng && ng < ngp)
-            m1x_group<DT, false>(slot[d], xp + (g + d) * G * 32, xs, h, nb - ng * G, a, ab);
+            m1x_group<DT, false, SF>(slot[d], xp + (g + d) * G * 32, xs, h, nb - ng * G, a, ab);
     }
     const float u = __fadd_rn(a, xor_get(a, 8));
     const float v = __fadd_rn(u, xor_get(u, 16));
