@@ -99,7 +99,8 @@ __device__ __forceinline__ int dot_q4(const int4& w, const int4& x0, const int4&
 // are all issued before any is used, so a lane waits on memory once per
 // chunk rather than once per block. Per block and row: the int32 dot, then
 // acc += (s_w * s_x) * P (+ bias * s_x * sum q_x) in f64. The group's lanes
-// are summed with an xor tree in f64 and the sum is rounded once.
+// are summed in f64 (64 lanes: the DPP tree of every 64-lane int8 kernel;
+// 16 or 32: an xor tree) and the sum is rounded once.
 template <int DT, int M, int R, int LPR, int BPL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ sc,
                                                       const uint16_t* __restrict__ bi, const int8_t* __restrict__ aq,
@@ -177,8 +178,14 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             double v = acc[r][m];
+            // 64 lanes: the DPP tree of gemv_i8_v2_kernel (and of every
+            // 64-lane int8 kernel, so their bits agree); fewer: the xor tree.
+            if constexpr (LPR == 64) {
+                v = group_sum_f64<64>(v);
+            } else {
 #pragma unroll
-            for (int k = LPR / 2; k >= 1; k >>= 1) v += xor_get(v, k);
+                for (int k = LPR / 2; k >= 1; k >>= 1) v += xor_get(v, k);
+            }
             acc[r][m] = v;
         }
     if (lane == 0) {
@@ -512,9 +519,8 @@ bool launch_v2_m(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, cons
 //
 // One vector, rows of 97 .. 256 blocks, where the plain GEMV runs 64 lanes
 // per row (lane l summing blocks l, l + 64, ... in that order) and reduces
-// the lanes with the xor tree (gemv_i8_kernel) or, for whole 64-block
-// rows, the DPP tree (gemv_i8_v2_kernel): the same per-lane order and tree
-// here (V2RED), so the results are the bits of the device forward's norm,
+// the lanes with the DPP tree (group_sum_f64): the same per-lane order and
+// tree here, so the results are the bits of the device forward's norm,
 // the quantizer and the plain GEMV run one after another. One workgroup of
 // 16 waves per CU forms the int8 input: its threads load their pieces of x,
 // r and gamma, then each wave requests its first weights, which are in
@@ -524,7 +530,7 @@ bool launch_v2_m(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, cons
 // wave then takes row groups of R rows grid-stride, the next chunk's
 // weights in flight while the current one is summed.
 constexpr int I8N_T = 1024;  // threads per workgroup
-template <int DT, int R, int BPL, int K4, bool V2RED>
+template <int DT, int R, int BPL, int K4>
 __global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __restrict__ qs,
                                                              const uint16_t* __restrict__ sc,
                                                              const uint32_t* __restrict__ sb, int rows, int nb,
@@ -606,12 +612,7 @@ __global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __re
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             double v = acc[r];
-            if (V2RED) {
-                v = group_sum_f64<64>(v);
-            } else {
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) v += xor_get(v, m);
-            }
+            v = group_sum_f64<64>(v);
             if (lane == 0 && g * R + r < rows) y[g * R + r] = (float)v;
             acc[r] = 0.0;
         }
@@ -698,25 +699,25 @@ __global__ __launch_bounds__(I8N_T) void gemv_i8_norm_kernel(const uint8_t* __re
     }
 }
 
-template <int DT, int R, int BPL, int K4, bool V2RED>
+template <int DT, int R, int BPL, int K4>
 void launch_i8n(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const NormIn& nrm, int rows, int nb,
                 float* y, hipStream_t st) {
     constexpr int NW = I8N_T / 64;
     const int want = ceil_div(ceil_div(rows, R), NW), cap = cu_count();
     const int grid = want < cap ? want : cap;
     const size_t lds = (size_t)32 * rms_t_stride(nb * 32) + (size_t)nb * 32 + (size_t)nb * 16;
-    gemv_i8_norm_kernel<DT, R, BPL, K4, V2RED><<<grid, I8N_T, lds, st>>>(qs, sc, sb, rows, nb, y, nrm);
+    gemv_i8_norm_kernel<DT, R, BPL, K4><<<grid, I8N_T, lds, st>>>(qs, sc, sb, rows, nb, y, nrm);
 }
 
 // A row is one chunk: 128 blocks (up to 128-block rows, one piece per
 // thread) or 256 blocks (two pieces, one row per group).
-template <int DT, bool V2RED>
+template <int DT>
 void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const NormIn& nrm, int rows, int nb,
                    float* y, hipStream_t st) {
     if (nb <= 128)
-        launch_i8n<DT, DT == 1 ? 1 : 2, 2, 1, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+        launch_i8n<DT, DT == 1 ? 1 : 2, 2, 1>(qs, sc, sb, nrm, rows, nb, y, st);
     else
-        launch_i8n<DT, 1, 4, 2, V2RED>(qs, sc, sb, nrm, rows, nb, y, st);
+        launch_i8n<DT, 1, 4, 2>(qs, sc, sb, nrm, rows, nb, y, st);
 }
 
 
@@ -734,8 +735,8 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
 // (the quants and the (scale, scale * sum) pairs) into LDS once, then each
 // wave takes rows grid-stride, chunks of 128 blocks with the next chunk's
 // weights in flight. A lane sums blocks l, l + 64, ... in order and the
-// lanes are reduced with the tree of the kernel the plain path would take
-// (V2RED), so the bits are the plain path's.
+// lanes are reduced with the plain path's DPP tree, so the bits are the
+// plain path's.
 //
 // K4 > 0: the vector arrives as f32 (xf) and the workgroup quantizes it
 // itself with the library quantizer's encoder (q8_act.h), no separate
@@ -743,7 +744,7 @@ void launch_i8n_dt(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, co
 // i = tid + T k for T threads; K4 * T >= nb * 8) before any weight load,
 // and encodes them into LDS while its first weights are in flight.
 constexpr int I8L_T = 1024;
-template <int DT, bool V2RED, int K4 = 0>
+template <int DT, int K4 = 0>
 __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __restrict__ qs,
                                                             const uint16_t* __restrict__ sc,
                                                             const uint32_t* __restrict__ sb,
@@ -813,12 +814,7 @@ __global__ __launch_bounds__(I8L_T) void gemv_i8_lds_kernel(const uint8_t* __res
     };
     auto finish = [&](int row) {
         double v = acc;
-        if (V2RED) {
-            v = group_sum_f64<64>(v);
-        } else {
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) v += xor_get(v, m);
-        }
+        v = group_sum_f64<64>(v);
         if (lane == 0) y[row] = (float)v;
         acc = 0.0;
     };
@@ -891,12 +887,12 @@ bool i8_lds_shape(int dtype, int rows, int nb) {
 
 // Workgroups resident per CU (at most I8L_WG_PER_CU), from the instance's
 // registers and LDS: the grid is never larger than what runs at once.
-template <int DT, bool V2RED, int K4>
+template <int DT, int K4>
 int i8_lds_per_cu(size_t lds) {
     static int n = -1;
     if (n < 0) {
         int b = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_i8_lds_kernel<DT, V2RED, K4>, I8L_T, lds) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_i8_lds_kernel<DT, K4>, I8L_T, lds) !=
                 hipSuccess ||
             b < 1)
             b = 1;
@@ -916,26 +912,26 @@ inline int i8_lds_waves(int rows) {
     return w < 8 ? 8 : w;
 }
 
-template <int DT, bool V2RED, int K4 = 0>
+template <int DT, int K4 = 0>
 void launch_i8_lds(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const int8_t* aq, const double* asx,
                    int rows, int nb, float* y, hipStream_t st, const float* xf = nullptr) {
     const size_t lds = (((size_t)nb * 32 + 1023) & ~(size_t)1023) + (((size_t)nb * 16 + 1023) & ~(size_t)1023);
     const int waves = i8_lds_waves(rows);
-    const int want = ceil_div(rows, waves), cap = i8_lds_per_cu<DT, V2RED, K4>(lds) * cu_count();
+    const int want = ceil_div(rows, waves), cap = i8_lds_per_cu<DT, K4>(lds) * cu_count();
     const int grid = want < cap ? want : cap;
-    gemv_i8_lds_kernel<DT, V2RED, K4><<<grid, 64 * waves, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, xf);
+    gemv_i8_lds_kernel<DT, K4><<<grid, 64 * waves, lds, st>>>(qs, sc, sb, aq, asx, rows, nb, y, xf);
 }
 
 // The quantizing prologue's pieces per thread: K4 * threads >= nb * 8.
-template <int DT, bool V2RED>
+template <int DT>
 void launch_i8_qx_k(const uint8_t* qs, const uint16_t* sc, const uint32_t* sb, const float* x, int rows, int nb,
                     float* y, hipStream_t st) {
     const int need = ceil_div(nb * 8, 64 * i8_lds_waves(rows));
-    if (need <= 1) launch_i8_lds<DT, V2RED, 1>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else if (need <= 2) launch_i8_lds<DT, V2RED, 2>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else if (need <= 3) launch_i8_lds<DT, V2RED, 3>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else if (need <= 4) launch_i8_lds<DT, V2RED, 4>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
-    else launch_i8_lds<DT, V2RED, 6>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    if (need <= 1) launch_i8_lds<DT, 1>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 2) launch_i8_lds<DT, 2>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 3) launch_i8_lds<DT, 3>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else if (need <= 4) launch_i8_lds<DT, 4>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
+    else launch_i8_lds<DT, 6>(qs, sc, sb, nullptr, nullptr, rows, nb, y, st, x);
 }
 }  // namespace
 
@@ -954,14 +950,10 @@ bool launch_gemv_i8_qx(int dtype, const uint8_t* qs, const uint16_t* scales, con
                        int rows, int nb, float* y, hipStream_t st) {
     if (nb <= 96 || nb > 384 || (dtype == 2 && !sb) || ((uintptr_t)x & 15) != 0) return false;
     if (dtype == 1 && rows >= 16384 && nb % 64 != 0) return false;
-    const bool v2red = nb % 64 == 0;  // the plain path's kernel at this row length: its lane tree
-    if (dtype == 1) {
-        if (v2red) launch_i8_qx_k<1, true>(qs, scales, sb, x, rows, nb, y, st);
-        else launch_i8_qx_k<1, false>(qs, scales, sb, x, rows, nb, y, st);
-    } else {
-        if (v2red) launch_i8_qx_k<2, true>(qs, scales, sb, x, rows, nb, y, st);
-        else launch_i8_qx_k<2, false>(qs, scales, sb, x, rows, nb, y, st);
-    }
+    if (dtype == 1)
+        launch_i8_qx_k<1>(qs, scales, sb, x, rows, nb, y, st);
+    else
+        launch_i8_qx_k<2>(qs, scales, sb, x, rows, nb, y, st);
     return true;
 }
 
@@ -981,14 +973,10 @@ void launch_gemv_i8(int dtype, const uint8_t* qs, const uint16_t* scales, const 
     // One vector at the staged kernel's shapes (x and its pairs in LDS: up
     // to 32768 columns).
     if (n_tok == 1 && i8_lds_shape(dtype, rows, nb) && nb * 32 <= 32768 && (dtype == 1 || sb)) {
-        const bool v2red = nb % 64 == 0;  // the plain path's kernel at this row length: its lane tree
-        if (dtype == 1) {
-            if (v2red) launch_i8_lds<1, true>(qs, scales, sb, aq, asx, rows, nb, y, st);
-            else launch_i8_lds<1, false>(qs, scales, sb, aq, asx, rows, nb, y, st);
-        } else {
-            if (v2red) launch_i8_lds<2, true>(qs, scales, sb, aq, asx, rows, nb, y, st);
-            else launch_i8_lds<2, false>(qs, scales, sb, aq, asx, rows, nb, y, st);
-        }
+        if (dtype == 1)
+            launch_i8_lds<1>(qs, scales, sb, aq, asx, rows, nb, y, st);
+        else
+            launch_i8_lds<2>(qs, scales, sb, aq, asx, rows, nb, y, st);
         return;
     }
     const size_t cols = (size_t)nb * 32;
@@ -1017,14 +1005,10 @@ bool launch_gemv_i8_norm(int dtype, const uint8_t* qs, const uint16_t* scales, c
     if (nb <= 96 || nb > 256 || (dtype == 2 && !sb)) return false;
     if (!aligned(nrm.x) || !aligned(nrm.gamma) || !aligned(nrm.r) || !aligned(nrm.x_out) || !aligned(nrm.rec))
         return false;
-    const bool v2red = nb % 64 == 0;  // the plain GEMV's kernel at this row length
-    if (dtype == 1) {
-        if (v2red) launch_i8n_dt<1, true>(qs, scales, sb, nrm, rows, nb, y, st);
-        else launch_i8n_dt<1, false>(qs, scales, sb, nrm, rows, nb, y, st);
-    } else {
-        if (v2red) launch_i8n_dt<2, true>(qs, scales, sb, nrm, rows, nb, y, st);
-        else launch_i8n_dt<2, false>(qs, scales, sb, nrm, rows, nb, y, st);
-    }
+    if (dtype == 1)
+        launch_i8n_dt<1>(qs, scales, sb, nrm, rows, nb, y, st);
+    else
+        launch_i8n_dt<2>(qs, scales, sb, nrm, rows, nb, y, st);
     return true;
 }
 

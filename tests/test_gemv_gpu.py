@@ -259,8 +259,8 @@ def test_gemv_rmsnorm_dev(oracle, dtype, rows, cols):
 def test_gemv_rmsnorm_i8_dev(oracle, dtype, rows, cols):
     # The int8 mode of the fused norm (nnh_gemv_rmsnorm_act_dev, NNH_ACT_I8):
     # rows of 97..256 blocks run the norm and nncpu's Q8_0 quantizer in the
-    # int8 GEMV's prologue (112 blocks: the xor lane tree; 128 / 192 / 256:
-    # the DPP tree; row groups past four per CU and ragged last groups), other
+    # int8 GEMV's prologue (112, 128, 192 and 256 blocks; row groups past
+    # four per CU and ragged last groups), other
     # rows the norm kernel before the plain path (1024 and 2048 columns).
     # y bit-equals the independent norm restatement followed by the plain
     # int8 GEMV (nnh_gemv_batch_dev, NNH_ACT_I8) on the same device weight,
