@@ -99,8 +99,8 @@ __device__ __forceinline__ int dot_q4(const int4& w, const int4& x0, const int4&
 // are all issued before any is used, so a lane waits on memory once per
 // chunk rather than once per block. Per block and row: the int32 dot, then
 // acc += (s_w * s_x) * P (+ bias * s_x * sum q_x) in f64. The group's lanes
-// are summed in f64 (64 lanes: the DPP tree of every 64-lane int8 kernel;
-// 16 or 32: an xor tree) and the sum is rounded once.
+// are summed in f64 with the DPP tree (group_sum_f64) and the sum is rounded
+// once.
 template <int DT, int M, int R, int LPR, int BPL>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ sc,
                                                       const uint16_t* __restrict__ bi, const int8_t* __restrict__ aq,
@@ -178,14 +178,9 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             double v = acc[r][m];
-            // 64 lanes: the DPP tree of gemv_i8_v2_kernel (and of every
-            // 64-lane int8 kernel, so their bits agree); fewer: the xor tree.
-            if constexpr (LPR == 64) {
-                v = group_sum_f64<64>(v);
-            } else {
-#pragma unroll
-                for (int k = LPR / 2; k >= 1; k >>= 1) v += xor_get(v, k);
-            }
+            // The DPP tree over the row's LPR lanes (at 64 lanes that of
+            // every 64-lane int8 kernel, so their bits agree).
+            v = group_sum_f64<LPR>(v);
             acc[r][m] = v;
         }
     if (lane == 0) {
